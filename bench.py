@@ -1,0 +1,224 @@
+"""Benchmark of the MI355X DiT-block hot path.
+
+One step = one forward pass of the LTX-2-like video DiT block (9216 video
+tokens with 3D RoPE + 256 text tokens by cross-attention, D = 4096, 32 heads x 128, GELU MLP x4)
+over synthetic seeded inputs already resident in HBM. Prints ONE JSON line:
+
+  value        block throughput, algorithmic TFLOP/s (GEMM 2MNK + attention 4 H Tq Tk Dh)
+  ms_per_step  milliseconds per block
+  roofline     the dominant kernel's achieved TFLOP/s (its algorithmic FLOPs per launch over its
+               average launch time, measured with HIP events on the launch stream inside the
+               timed region) against the 2.5 PFLOP/s dense bf16 MFMA peak
+  cpu_baseline the FP32 numpy restatement of the config-1 block timed on this host's cores
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3|4|5] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from collections import defaultdict
+
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA (AMD published)
+PEAK_HBM_GBS = 8000.0
+
+
+def _kernel_flops(name: str, args: tuple) -> float:
+    """Algorithmic FLOPs of one launch from its C arguments (0 for memory-bound kernels)."""
+    if name == "kx_gemm_bf16":
+        m, n, k = args[7], args[8], args[9]
+        return 2.0 * m * n * k
+    if name == "kx_qgemm_affine_bf16":
+        m, n, k = args[8], args[9], args[10]
+        return 2.0 * m * n * k
+    if name == "kx_attention_fwd_bf16":
+        batch, tq, tk, heads, dh = args[8], args[9], args[10], args[11], args[12]
+        return 4.0 * batch * heads * tq * tk * dh
+    return 0.0
+
+
+def _kernel_label(name: str, args: tuple) -> str:
+    if name == "kx_gemm_bf16":
+        return f"gemm m{args[7]} n{args[8]} k{args[9]}"
+    if name == "kx_qgemm_affine_bf16":
+        return f"qgemm{args[12]} m{args[8]} n{args[9]} k{args[10]}"
+    if name == "kx_attention_fwd_bf16":
+        return f"attention tq{args[9]} tk{args[10]} h{args[11]} d{args[12]}"
+    return name.replace("kx_", "").replace("_bf16", "")
+
+
+def cpu_baseline(budget_s: float = 12.0) -> dict:
+    """Config-1 block (1024 + 128 tokens, D = 1024) through the FP32 numpy restatement on the
+    host cores: median of repeated runs within ``budget_s`` seconds."""
+    import numpy as np
+
+    import oracle
+    from kinomlx_amd import workloads
+
+    spec = workloads.CONFIGS[1]
+    p = workloads.flux_params(spec, 0)
+    inputs = workloads.flux_inputs(spec, 0)
+    op = {k: v.float().numpy() for k, v in p.items()}
+    image = inputs["image"][0].float().numpy()
+    text = inputs["text"][0].float().numpy()
+    cos, sin = (t.numpy() for t in workloads.flux_rope(spec))
+    flops = workloads.flop_count(spec)["total"]
+    times = []
+    start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - start < budget_s and len(times) < 50):
+        t0 = time.perf_counter()
+        oracle.config1_double_block(op, image, text, op["image_mod"], op["text_mod"], (cos, sin), heads=spec.heads)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {
+        "value": round(flops / med / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": len(os.sched_getaffinity(0)),
+        "kind": "port",
+        "sample": f"config-1 block (1024 image + 128 text tokens, D=1024, 16x64, GELU MLP), FP32 numpy "
+                  f"restatement, median of {len(times)} runs ({med * 1e3:.1f} ms/block); "
+                  f"CPU restatement (fp32), not reference code",
+        "ms_per_block": round(med * 1e3, 2),
+    }
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--config", type=int, default=3, choices=(3, 4, 5))
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--breakdown", action="store_true", help="print the per-kernel table to stderr")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from kinomlx_amd import _lib, workloads
+    from kinomlx_amd.ltx2.rope import precompute_freqs_cis
+    from kinomlx_amd.ltx2.transformer import TransformerArgs
+
+    device = torch.device("cuda:0")
+    spec = workloads.CONFIGS[args.config]
+    p = workloads.ltx_params(spec, 0)
+    if spec.bits:
+        p = workloads.quantize_ltx_params(p, spec.bits, spec.group_size)
+    inputs = workloads.ltx_inputs(spec, 0)
+    block = workloads.build_ltx_block(spec, p, device)
+    pe = precompute_freqs_cis(inputs["positions"].to(device), dim=spec.dim, theta=10000.0,
+                              max_pos=(20, 2048, 2048), use_middle_indices_grid=True,
+                              num_attention_heads=spec.heads)
+    video = TransformerArgs(x=inputs["x"].to(device), context=inputs["context"].to(device),
+                            timesteps=p["timesteps"].to(device), positional_embeddings=pe)
+    del p
+
+    def step():
+        return block(video)[0].x
+
+    for _ in range(args.warmup):
+        out = step()
+    torch.cuda.synchronize()
+    if not torch.isfinite(out).all():
+        print("non-finite block output", file=sys.stderr)
+        return 1
+
+    timer = _lib.LaunchTimer()
+    _lib.set_timer(timer)
+    begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    begin.record()
+    for _ in range(args.steps):
+        out = step()
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    _lib.set_timer(None)
+    ms_per_step = begin.elapsed_time(end) / args.steps
+
+    per_kernel: dict[str, list[float]] = defaultdict(list)
+    flops_of: dict[str, float] = {}
+    name_of: dict[str, str] = {}
+    for name, cargs, ms in timer.durations_ms():
+        label = _kernel_label(name, cargs)
+        per_kernel[label].append(ms)
+        flops_of[label] = _kernel_flops(name, cargs)
+        name_of[label] = name
+    kernel_ms_per_step = {k: sum(v) / args.steps for k, v in per_kernel.items()}
+    dominant = max(kernel_ms_per_step, key=kernel_ms_per_step.get)
+    dom_avg_ms = statistics.mean(per_kernel[dominant])
+    dom_tflops = flops_of[dominant] / (dom_avg_ms * 1e-3) / 1e12
+
+    flops = workloads.flop_count(spec)
+    attn_ms = sum(v for k, v in kernel_ms_per_step.items() if name_of[k] == "kx_attention_fwd_bf16")
+    gemm_ms = sum(v for k, v in kernel_ms_per_step.items() if name_of[k] in ("kx_gemm_bf16", "kx_qgemm_affine_bf16"))
+    other_ms = sum(kernel_ms_per_step.values()) - attn_ms - gemm_ms
+    attn_tflops = flops["attention"] / (attn_ms * 1e-3) / 1e12
+    gemm_tflops = flops["gemm"] / (gemm_ms * 1e-3) / 1e12
+    value = flops["total"] / (ms_per_step * 1e-3) / 1e12
+
+    if args.breakdown:
+        for label, ms in sorted(kernel_ms_per_step.items(), key=lambda kv: -kv[1]):
+            f = flops_of[label]
+            extra = f"  {f / (statistics.mean(per_kernel[label]) * 1e-3) / 1e12:7.1f} TFLOP/s" if f else ""
+            print(f"{ms:8.3f} ms/step  x{len(per_kernel[label]) // args.steps}  {label}{extra}", file=sys.stderr)
+
+    result = {
+        "metric": "DiT block ms + attention/GEMM TFLOP/s (% bf16 MFMA peak), 9216-token block",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,0.02) weights, N(0,1) activations; no checkpoint)",
+        "config": {
+            "workload": f"LTX2-like video DiT block, BASELINE config {args.config}",
+            "video_tokens": spec.tokens,
+            "latent_grid_thw": list(spec.grid),
+            "text_tokens": spec.text_tokens,
+            "dim": spec.dim,
+            "heads": spec.heads,
+            "head_dim": spec.head_dim,
+            "ff_mult": spec.ff_mult,
+            "weights": f"int{spec.bits} affine g{spec.group_size}" if spec.bits else "bf16",
+            "batch": 1,
+        },
+        "block_ms": round(ms_per_step, 4),
+        "attention": {"ms": round(attn_ms, 4), "tflops": round(attn_tflops, 1),
+                      "frac_of_peak": round(attn_tflops / PEAK_BF16_TFLOPS, 4)},
+        "gemm": {"ms": round(gemm_ms, 4), "tflops": round(gemm_tflops, 1),
+                 "frac_of_peak": round(gemm_tflops / PEAK_BF16_TFLOPS, 4)},
+        "memory_bound_ms": round(other_ms, 4),
+        "wall_s": round(wall, 3),
+        "roofline": {
+            "kernel": dominant,
+            "bound": "mfma",
+            "achieved": round(dom_tflops, 1),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(dom_tflops / PEAK_BF16_TFLOPS, 4),
+            "traffic": None,
+            "avg_launch_ms": round(dom_avg_ms, 4),
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

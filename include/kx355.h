@@ -1,0 +1,194 @@
+/*
+ * kx355 — C ABI of the MI355X (gfx950) DiT-block kernels.
+ *
+ * Conventions shared by every entry point:
+ *   - Pointers are device pointers. Activations are bf16 (raw 16-bit patterns), tables and
+ *     modulation vectors fp32, packed weights uint32. "ld*" arguments are row strides in
+ *     elements. Sizes are int64_t.
+ *   - Work is enqueued asynchronously on `stream` (a hipStream_t; NULL = the null stream).
+ *   - The library never allocates or frees device memory; the caller owns every buffer.
+ *   - Return value: 0 on success, a negative KX_ERR_* code otherwise; kx_last_error() gives the
+ *     message of the calling thread's last failure.
+ *   - Reference paths are relative to the dmlsrc/KinoMLX checkout.
+ */
+#ifndef KX355_H
+#define KX355_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* kx_stream_t; /* hipStream_t */
+
+enum {
+  KX_OK = 0,
+  KX_ERR_INVALID = -1,     /* bad argument: null pointer, size, stride or alignment */
+  KX_ERR_UNSUPPORTED = -2, /* valid request this build has no kernel for */
+  KX_ERR_LAUNCH = -3       /* the HIP launch reported an error */
+};
+
+/* Element type of tensors that may be fp32 or bf16. */
+enum { KX_F32 = 0, KX_BF16 = 1 };
+
+/* Norm kinds for kx_adaln_norm_bf16. */
+enum { KX_NORM_RMS = 0, KX_NORM_LAYER = 1 };
+
+/* RoPE kinds for kx_rmsnorm_rope_bf16. */
+enum { KX_ROPE_NONE = 0, KX_ROPE_SPLIT = 1, KX_ROPE_PAIR = 2 };
+
+/* GEMM / quantized-GEMM epilogue flags: bias, activation (bits 4-7), gated residual. */
+enum {
+  KX_EPI_BIAS = 1,
+  KX_EPI_ACT_GELU_TANH = 1 << 4,
+  KX_EPI_ACT_SILU = 2 << 4,
+  KX_EPI_ACT_SIGMOID2 = 3 << 4, /* 2 * sigmoid(.) — LTX gate logits */
+  KX_EPI_GATED_RESIDUAL = 1 << 8 /* c = resid + gate[col] * act(acc + bias) */
+};
+
+int kx_abi_version(void);
+const char* kx_last_error(void);
+
+/*
+ * Modulated norm: y = norm(x) * (1 + scale) + shift, fp32 opmath, one rounding.
+ *   KX_NORM_RMS  : norm = x * rsqrt(mean(x^2) + eps)
+ *     replaces transformer._adaln / _compiled_adaln
+ *     (kinomlx/models/ltx2/transformer/transformer.py:16-23,42) over
+ *     fused_ops.rms_norm(weight=None) (kinomlx/kernels/fused_ops.py:437-441).
+ *   KX_NORM_LAYER: norm = (x - mean) * rsqrt(var + eps)
+ *     replaces flux2 normalized (kinomlx/models/flux2/transformer.py:56-57).
+ * shift/scale are fp32 rows of `dim`; row r of x uses modulation row (r / mod_div) at
+ * mod_stride elements per row (mod_stride 0 broadcasts one row). shift == scale == NULL gives
+ * the plain norm (fused_ops.rms_norm(weight=None)).
+ */
+int kx_adaln_norm_bf16(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows,
+                       int64_t dim, const float* shift, const float* scale, int64_t mod_div,
+                       int64_t mod_stride, float eps, int kind, kx_stream_t stream);
+
+/*
+ * Weighted RMSNorm, optionally fused with RoPE on the normalized value:
+ *   n = x * rsqrt(mean(x^2 over each norm group) + eps) * (w + weight_offset)
+ *   then y = rope(n) (fp32 opmath, one rounding).
+ * norm_width == dim: one norm over the row (LTX q_norm/k_norm, full width,
+ *   kinomlx/models/ltx2/transformer/attention.py:121-133 -> fused_ops.rms_norm weighted,
+ *   kinomlx/kernels/fused_ops.py:141-193,412-457).
+ * norm_width == head_dim: per-head norm (FLUX QKNorm kinomlx/models/flux2/transformer.py:68-75,
+ *   Krea2RMSNorm kinomlx/models/krea2/transformer/model.py:29-46 with weight_offset 1).
+ * rope_kind KX_ROPE_SPLIT: split-half rotation (kinomlx/kernels/split_rope.py:35-56), tables
+ *   cos/sin[t * table_ld + h * table_hs + i], i < head_dim / 2.
+ * rope_kind KX_ROPE_PAIR: adjacent pairs (kinomlx/models/flux2/transformer.py:25-29), tables
+ *   cos/sin[t * table_ld + h * table_hs + d], d < head_dim.
+ * Token t of row r is r when table_batched, else r % tokens. w is fp32 or bf16 (w_dtype).
+ */
+int kx_rmsnorm_rope_bf16(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows,
+                         int64_t dim, int64_t norm_width, const void* w, int w_dtype, float eps,
+                         float weight_offset, int rope_kind, const float* cos, const float* sin,
+                         int64_t table_ld, int64_t table_hs, int64_t tokens, int table_batched,
+                         int64_t head_dim, kx_stream_t stream);
+
+/*
+ * Split-half RoPE, standalone: replaces split_rope.rotate (kinomlx/kernels/split_rope.py:144-163,
+ * arithmetic :35-56). x/y are (batch, tokens, heads * 2 * half) rows at stride ldx/ldy; tables
+ * token-major (table_batch, tokens, heads * half), table_batched selects per-batch tables.
+ * Each product is rounded in fp32 before the difference/sum, then one cast: bit-equal to the
+ * reference graph's fp32 arithmetic.
+ */
+int kx_rope_split_bf16(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t batch,
+                       int64_t tokens, int64_t heads, int64_t half, const float* cos,
+                       const float* sin, int table_batched, kx_stream_t stream);
+
+/*
+ * Adjacent-pair RoPE, standalone: replaces flux2.transformer.rotate
+ * (kinomlx/models/flux2/transformer.py:25-29) and krea2 apply_rotary_embedding
+ * (kinomlx/models/krea2/transformer/model.py:69-92). Rows r < rows of x/y hold heads * head_dim
+ * values; tables cos/sin[tok * table_ld + h * table_hs + d] with tok = r (table_batched) or
+ * r % tokens.
+ */
+int kx_rope_pair_bf16(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows,
+                      int64_t heads, int64_t head_dim, const float* cos, const float* sin,
+                      int64_t table_ld, int64_t table_hs, int64_t tokens, int table_batched,
+                      kx_stream_t stream);
+
+/*
+ * Non-causal flash attention on token-major flattened heads: replaces
+ * dense_attention.dense_attention (kinomlx/models/ltx2/kernels/dense_attention.py:106-153) and
+ * the unmasked SDPA calls (kinomlx/models/ltx2/transformer/attention.py:144-161,
+ * kinomlx/models/flux2/kv.py:48-54).
+ *   o[b, i, h*D:(h+1)*D] = softmax_j(q_i . k_j * scale) v_j   (fp32 scores and accumulation)
+ * q: (batch, tq) rows at ldq; k, v: (batch, tk) rows at ldk/ldv; o: (batch, tq) rows at ldo.
+ * gate (optional, bf16 (batch * tq, heads) at ld_gate) multiplies each head's output row before
+ * the one rounding (the LTX per-head gate, attention.py:360-366). head_dim is 64 or 128.
+ */
+int kx_attention_fwd_bf16(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v,
+                          int64_t ldv, void* o, int64_t ldo, int64_t batch, int64_t tq,
+                          int64_t tk, int64_t heads, int64_t head_dim, float scale,
+                          const void* gate, int64_t ld_gate, kx_stream_t stream);
+
+/*
+ * Dense bf16 linear on MFMA: c = epilogue(a · wᵀ) with fp32 accumulation and one rounding.
+ * Replaces mpp_linear.linear / mx.addmm(bias, x, Wᵀ) (kinomlx/kernels/mpp_linear.py:469-506,
+ * kinomlx/models/ltx2/transformer/attention.py:41-109, kinomlx/modeling/layers.py).
+ *   a: (m, k) at lda; w: (n, k) at ldw — the reference's (out, in) layout; c: (m, n) at ldc.
+ *   bias: bf16 (n) with KX_EPI_BIAS. Activations per KX_EPI_ACT_*.
+ *   KX_EPI_GATED_RESIDUAL: c = resid + gate * act(acc + bias), resid bf16 (m, n) at ldr, gate
+ *   fp32 row (r / gate_div) at gate_stride (0 broadcasts). c may alias resid.
+ * Requires k % 8 == 0, lda/ldw % 8 == 0 and 16-byte aligned a/w.
+ */
+int kx_gemm_bf16(const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias,
+                 void* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int epilogue,
+                 const void* resid, int64_t ldr, const float* gate, int64_t gate_div,
+                 int64_t gate_stride, kx_stream_t stream);
+
+/*
+ * Group-wise affine int4/int8 weight-quantized linear, dequantized inside the MFMA mainloop:
+ * replaces nn.QuantizedLinear / mx.quantized_matmul(x, wq, scales, biases, transpose=True,
+ * group_size, bits, mode="affine") + bias (kinomlx/models/ltx2/weights/quantization.py:28-44,
+ * kinomlx/_mlx_nn.py:20). wq: uint32 (n, k * bits / 32), element j of a word at bits
+ * [bits*j, bits*(j+1)); scales/biases: bf16 (n, k / group_size). The dequantized weight is
+ * bf16(fp32(scale) * q + fp32(bias)). Epilogue flags and residual/gate as kx_gemm_bf16.
+ * Requires bits in {4, 8}, group_size == 64, k % 64 == 0.
+ */
+int kx_qgemm_affine_bf16(const void* a, int64_t lda, const uint32_t* wq, const void* scales,
+                         const void* biases, const void* bias, void* c, int64_t ldc, int64_t m,
+                         int64_t n, int64_t k, int group_size, int bits, int epilogue,
+                         const void* resid, int64_t ldr, const float* gate, int64_t gate_div,
+                         int64_t gate_stride, kx_stream_t stream);
+
+/*
+ * Test hook and load-time helper: dequantize packed affine weights to bf16 (n, k), with the
+ * same arithmetic as kx_qgemm_affine_bf16's mainloop (the MLX dequantize semantics behind
+ * mx.quantized_matmul, called from kinomlx/models/ltx2/weights/quantization.py:32-41).
+ */
+int kx_dequant_affine_bf16(const uint32_t* wq, const void* scales, const void* biases, void* out,
+                           int64_t n, int64_t k, int group_size, int bits, kx_stream_t stream);
+
+/* tanh GELU in fp32, inner argument clamped to +-10: fused_ops.gelu_approx
+ * (kinomlx/kernels/fused_ops.py:27-35,327-350). */
+int kx_gelu_tanh_bf16(const void* x, void* y, int64_t count, kx_stream_t stream);
+
+/* x / (1 + exp(-x)) in fp32: fused_ops.silu (kinomlx/kernels/fused_ops.py:40-45,353-372). */
+int kx_silu_bf16(const void* x, void* y, int64_t count, kx_stream_t stream);
+
+/* SwiGLU: y[r, j] = silu(x[r, j]) * x[r, hidden + j], x (rows, 2 * hidden) at ldx:
+ * flux2 swiglu (kinomlx/models/flux2/transformer.py:63-65). */
+int kx_swiglu_bf16(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows,
+                   int64_t hidden, kx_stream_t stream);
+
+/* y = x * (1 + scale) + shift (modulation vectors fp32, rows as kx_adaln_norm_bf16):
+ * transformer._modulate (kinomlx/models/ltx2/transformer/transformer.py:33-34). */
+int kx_modulate_bf16(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows, int64_t dim,
+                     const float* shift, const float* scale, int64_t mod_div,
+                     int64_t mod_stride, kx_stream_t stream);
+
+/* y = x + r * gate (gate fp32 rows as kx_adaln_norm_bf16): transformer._gated_residual
+ * (transformer.py:26-30); with x == NULL, y = r * gate (transformer._gate, :37-38). */
+int kx_gated_residual_bf16(const void* x, int64_t ldx, const void* r, int64_t ldr, void* y,
+                           int64_t ldy, int64_t rows, int64_t dim, const float* gate,
+                           int64_t gate_div, int64_t gate_stride, kx_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KX355_H */

@@ -1,0 +1,343 @@
+"""ctypes binding of ``libkx355.so`` (the C ABI declared in ``include/kx355.h``).
+
+The library is loaded after ``torch`` so that its ``libamdhip64.so.7`` dependency resolves to the
+HIP runtime torch already holds: device pointers and streams are then shared. There is no CPU or
+PyTorch fallback anywhere behind these calls: a missing library raises.
+
+Each ``launch_*`` function takes torch tensors, checks what the kernel assumes (device, dtype,
+strides), and enqueues the kernel on the current torch stream.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch
+
+LIBRARY_PATH = Path(__file__).resolve().parent / "libkx355.so"
+
+KX_OK = 0
+KX_ERR_INVALID = -1
+KX_ERR_UNSUPPORTED = -2
+KX_ERR_LAUNCH = -3
+
+KX_F32 = 0
+KX_BF16 = 1
+KX_NORM_RMS = 0
+KX_NORM_LAYER = 1
+KX_ROPE_NONE = 0
+KX_ROPE_SPLIT = 1
+KX_ROPE_PAIR = 2
+EPI_BIAS = 1
+EPI_ACT_GELU_TANH = 1 << 4
+EPI_ACT_SILU = 2 << 4
+EPI_ACT_SIGMOID2 = 3 << 4
+EPI_GATED_RESIDUAL = 1 << 8
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I = ctypes.c_int
+_F = ctypes.c_float
+
+# Entry point -> argument types (every function returns int).
+SIGNATURES: dict[str, list] = {
+    "kx_adaln_norm_bf16": [_P, _I64, _P, _I64, _I64, _I64, _P, _P, _I64, _I64, _F, _I, _P],
+    "kx_rmsnorm_rope_bf16": [
+        _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I, _F, _F, _I, _P, _P, _I64, _I64, _I64, _I,
+        _I64, _P,
+    ],
+    "kx_rope_split_bf16": [_P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _I, _P],
+    "kx_rope_pair_bf16": [_P, _I64, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64, _I, _P],
+    "kx_attention_fwd_bf16": [
+        _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _I64, _P,
+    ],
+    "kx_gemm_bf16": [
+        _P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _I64, _P, _I64, _I64, _P,
+    ],
+    "kx_qgemm_affine_bf16": [
+        _P, _I64, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I, _I, _P, _I64, _P, _I64,
+        _I64, _P,
+    ],
+    "kx_dequant_affine_bf16": [_P, _P, _P, _P, _I64, _I64, _I, _I, _P],
+    "kx_gelu_tanh_bf16": [_P, _P, _I64, _P],
+    "kx_silu_bf16": [_P, _P, _I64, _P],
+    "kx_swiglu_bf16": [_P, _I64, _P, _I64, _I64, _I64, _P],
+    "kx_modulate_bf16": [_P, _I64, _P, _I64, _I64, _I64, _P, _P, _I64, _I64, _P],
+    "kx_gated_residual_bf16": [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _P],
+}
+
+_lib: ctypes.CDLL | None = None
+
+
+class KernelError(RuntimeError):
+    """A kx355 entry point returned an error code."""
+
+
+def load() -> ctypes.CDLL:
+    """Load ``libkx355.so`` once; raise if it was not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIBRARY_PATH.exists():
+        raise RuntimeError(
+            f"the kx355 HIP library is not built ({LIBRARY_PATH} missing); "
+            "run `python -m kinomlx_amd.csrc.build`"
+        )
+    lib = ctypes.CDLL(os.fspath(LIBRARY_PATH), mode=ctypes.RTLD_LOCAL)
+    for name, args in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = ctypes.c_int
+    lib.kx_abi_version.restype = ctypes.c_int
+    lib.kx_last_error.restype = ctypes.c_char_p
+    _lib = lib
+    return lib
+
+
+def available() -> bool:
+    """Whether the library is built and a GPU is visible to torch."""
+    return LIBRARY_PATH.exists() and torch.cuda.is_available()
+
+
+class LaunchTimer:
+    """Optional per-launch timing: while installed, each entry point call is bracketed by two
+    ``torch.cuda.Event`` records on the current stream (the stream the kernel runs on)."""
+
+    def __init__(self) -> None:
+        self.records: list[tuple[str, tuple, torch.cuda.Event, torch.cuda.Event]] = []
+
+    def durations_ms(self) -> list[tuple[str, tuple, float]]:
+        """(entry point, its C arguments, milliseconds) per recorded launch."""
+        torch.cuda.synchronize()
+        return [(name, args, start.elapsed_time(end)) for name, args, start, end in self.records]
+
+
+_timer: LaunchTimer | None = None
+
+
+def set_timer(timer: LaunchTimer | None) -> None:
+    """Install (or remove with None) a ``LaunchTimer``."""
+    global _timer
+    _timer = timer
+
+
+def _call(name: str, *args) -> None:
+    lib = load()
+    timer = _timer
+    if timer is not None:
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+    rc = getattr(lib, name)(*args)
+    if timer is not None:
+        end.record()
+        timer.records.append((name, args, start, end))
+    if rc != KX_OK:
+        message = lib.kx_last_error().decode(errors="replace")
+        raise KernelError(f"{name} failed ({rc}): {message}")
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _check_gpu(name: str, *tensors: torch.Tensor | None) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise ValueError(f"{name}: the MI355X kernels take GPU tensors, got one on {t.device}")
+
+
+def _rows(t: torch.Tensor, name: str) -> tuple[int, int, int]:
+    """(rows, width, row stride) of a tensor whose last axis is contiguous and whose leading
+    axes flatten into rows of one stride."""
+    if t.dim() < 1:
+        raise ValueError(f"{name}: needs at least one axis")
+    width = t.shape[-1]
+    if t.stride(-1) != 1 and width > 1:
+        raise ValueError(f"{name}: last axis must be contiguous")
+    if t.dim() == 1:
+        return 1, width, width
+    rows = t.numel() // width if width else 0
+    stride = t.stride(-2)
+    # leading axes must collapse into one stride
+    expected = stride
+    for axis in range(t.dim() - 2, -1, -1):
+        if t.shape[axis] != 1 and t.stride(axis) != expected:
+            raise ValueError(f"{name}: leading axes do not flatten into evenly strided rows")
+        expected *= t.shape[axis]
+    return rows, width, max(stride, width)
+
+
+def _mod_rows(vec: torch.Tensor, rows: int, width: int, name: str) -> tuple[int, int]:
+    """(mod_div, mod_stride) for an fp32 modulation tensor broadcast over ``rows`` rows: one
+    row ``(width,)``/``(1, .., width)``, one per batch ``(B, 1, width)``, or one per row."""
+    if vec.dtype != torch.float32 or vec.shape[-1] != width or vec.stride(-1) != 1:
+        raise ValueError(f"{name}: modulation must be fp32 with a contiguous last axis {width}")
+    count = vec.numel() // width
+    if count == 1:
+        return 1, 0
+    if rows % count:
+        raise ValueError(f"{name}: {count} modulation rows do not divide {rows} rows")
+    stride = vec.stride(-2) if vec.dim() >= 2 and vec.shape[-2] != 1 else vec.stride(0)
+    return rows // count, stride
+
+
+# ---- launches -----------------------------------------------------------------------------------
+
+
+def launch_adaln_norm(x, out, shift, scale, eps: float, kind: int) -> None:
+    _check_gpu("adaln_norm", x, out, shift, scale)
+    rows, dim, ldx = _rows(x, "adaln_norm x")
+    _, _, ldy = _rows(out, "adaln_norm out")
+    div, stride = (1, 0)
+    if shift is not None:
+        div, stride = _mod_rows(shift, rows, dim, "adaln_norm shift")
+        div2, stride2 = _mod_rows(scale, rows, dim, "adaln_norm scale")
+        if (div, stride) != (div2, stride2):
+            raise ValueError("adaln_norm: shift and scale must share one layout")
+    _call(
+        "kx_adaln_norm_bf16", _ptr(x), ldx, _ptr(out), ldy, rows, dim, _ptr(shift), _ptr(scale),
+        div, stride, eps, kind, _stream(),
+    )
+
+
+def launch_rmsnorm_rope(
+    x, out, weight, eps: float, weight_offset: float, *, norm_width: int, rope_kind: int = 0,
+    cos=None, sin=None, table_ld: int = 0, table_hs: int = 0, tokens: int = 0,
+    table_batched: bool = False, head_dim: int = 0,
+) -> None:
+    _check_gpu("rmsnorm_rope", x, out, weight, cos, sin)
+    rows, dim, ldx = _rows(x, "rmsnorm x")
+    _, _, ldy = _rows(out, "rmsnorm out")
+    if weight.dtype == torch.bfloat16:
+        w_dtype = KX_BF16
+    elif weight.dtype == torch.float32:
+        w_dtype = KX_F32
+    else:
+        raise ValueError("rms_norm weight must be float32 or bfloat16")
+    if not weight.is_contiguous():
+        raise ValueError("rms_norm weight must be contiguous")
+    _call(
+        "kx_rmsnorm_rope_bf16", _ptr(x), ldx, _ptr(out), ldy, rows, dim, norm_width, _ptr(weight),
+        w_dtype, eps, weight_offset, rope_kind, _ptr(cos), _ptr(sin), table_ld, table_hs, tokens,
+        int(table_batched), head_dim, _stream(),
+    )
+
+
+def launch_rope_split(x, out, cos_tm, sin_tm, *, batch, tokens, heads, half, table_batched) -> None:
+    _check_gpu("rope_split", x, out, cos_tm, sin_tm)
+    _, _, ldx = _rows(x, "rope x")
+    _, _, ldy = _rows(out, "rope out")
+    _call(
+        "kx_rope_split_bf16", _ptr(x), ldx, _ptr(out), ldy, batch, tokens, heads, half,
+        _ptr(cos_tm), _ptr(sin_tm), int(table_batched), _stream(),
+    )
+
+
+def launch_rope_pair(x, out, cos, sin, *, heads, head_dim, table_ld, table_hs, tokens, table_batched) -> None:
+    _check_gpu("rope_pair", x, out, cos, sin)
+    rows, _, ldx = _rows(x, "rope x")
+    _, _, ldy = _rows(out, "rope out")
+    _call(
+        "kx_rope_pair_bf16", _ptr(x), ldx, _ptr(out), ldy, rows, heads, head_dim, _ptr(cos),
+        _ptr(sin), table_ld, table_hs, tokens, int(table_batched), _stream(),
+    )
+
+
+def launch_attention(q, k, v, out, *, batch, tq, tk, heads, head_dim, scale, gate=None) -> None:
+    _check_gpu("attention", q, k, v, out, gate)
+    ld_gate = 0
+    if gate is not None:
+        _, _, ld_gate = _rows(gate, "attention gate")
+    _call(
+        "kx_attention_fwd_bf16", _ptr(q), q.stride(-2), _ptr(k), k.stride(-2), _ptr(v),
+        v.stride(-2), _ptr(out), out.stride(-2), batch, tq, tk, heads, head_dim, scale,
+        _ptr(gate), ld_gate, _stream(),
+    )
+
+
+def launch_gemm(a, w, out, *, bias=None, flags: int = 0, resid=None, gate=None) -> None:
+    _check_gpu("gemm", a, w, out, bias, resid, gate)
+    m, k, lda = _rows(a, "linear input")
+    n, kw, ldw = _rows(w, "linear weight")
+    if kw != k:
+        raise ValueError(f"linear: input width {k} does not match weight width {kw}")
+    _, _, ldc = _rows(out, "linear output")
+    ldr, div, stride = 0, 1, 0
+    if resid is not None:
+        _, _, ldr = _rows(resid, "linear residual")
+        div, stride = _mod_rows(gate, m, n, "linear gate")
+    _call(
+        "kx_gemm_bf16", _ptr(a), lda, _ptr(w), ldw, _ptr(bias), _ptr(out), ldc, m, n, k, flags,
+        _ptr(resid), ldr, _ptr(gate), div, stride, _stream(),
+    )
+
+
+def launch_qgemm(a, words, scales, biases, out, *, n, k, group_size, bits, bias=None,
+                 flags: int = 0, resid=None, gate=None) -> None:
+    _check_gpu("qgemm", a, words, scales, biases, out, bias, resid, gate)
+    m, ka, lda = _rows(a, "quantized linear input")
+    if ka != k:
+        raise ValueError(f"quantized linear: input width {ka} does not match {k}")
+    _, _, ldc = _rows(out, "quantized linear output")
+    ldr, div, stride = 0, 1, 0
+    if resid is not None:
+        _, _, ldr = _rows(resid, "quantized linear residual")
+        div, stride = _mod_rows(gate, m, n, "quantized linear gate")
+    _call(
+        "kx_qgemm_affine_bf16", _ptr(a), lda, _ptr(words), _ptr(scales), _ptr(biases), _ptr(bias),
+        _ptr(out), ldc, m, n, k, group_size, bits, flags, _ptr(resid), ldr, _ptr(gate), div,
+        stride, _stream(),
+    )
+
+
+def launch_dequant(words, scales, biases, out, *, n, k, group_size, bits) -> None:
+    _check_gpu("dequant", words, scales, biases, out)
+    _call(
+        "kx_dequant_affine_bf16", _ptr(words), _ptr(scales), _ptr(biases), _ptr(out), n, k,
+        group_size, bits, _stream(),
+    )
+
+
+def launch_unary(name: str, x, out) -> None:
+    _check_gpu(name, x, out)
+    if not (x.is_contiguous() and out.is_contiguous()):
+        raise ValueError(f"{name}: contiguous tensors required")
+    _call(name, _ptr(x), _ptr(out), x.numel(), _stream())
+
+
+def launch_swiglu(x, out) -> None:
+    _check_gpu("swiglu", x, out)
+    rows, width, ldx = _rows(x, "swiglu x")
+    _, _, ldy = _rows(out, "swiglu out")
+    _call("kx_swiglu_bf16", _ptr(x), ldx, _ptr(out), ldy, rows, width // 2, _stream())
+
+
+def launch_modulate(x, out, shift, scale) -> None:
+    _check_gpu("modulate", x, out, shift, scale)
+    rows, dim, ldx = _rows(x, "modulate x")
+    _, _, ldy = _rows(out, "modulate out")
+    div, stride = _mod_rows(shift, rows, dim, "modulate shift")
+    _call(
+        "kx_modulate_bf16", _ptr(x), ldx, _ptr(out), ldy, rows, dim, _ptr(shift), _ptr(scale),
+        div, stride, _stream(),
+    )
+
+
+def launch_gated_residual(x, r, out, gate) -> None:
+    _check_gpu("gated_residual", x, r, out, gate)
+    rows, dim, ldr = _rows(r, "gated_residual residual")
+    ldx = 0
+    if x is not None:
+        _, _, ldx = _rows(x, "gated_residual x")
+    _, _, ldy = _rows(out, "gated_residual out")
+    div, stride = _mod_rows(gate, rows, dim, "gated_residual gate")
+    _call(
+        "kx_gated_residual_bf16", _ptr(x), ldx, _ptr(r), ldr, _ptr(out), ldy, rows, dim, _ptr(gate),
+        div, stride, _stream(),
+    )

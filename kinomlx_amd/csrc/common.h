@@ -1,0 +1,95 @@
+// Shared device helpers and host-side argument checking for the kx355 kernels (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kx355.h"
+
+namespace kx {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+
+// ---- bf16 <-> fp32 -----------------------------------------------------------------------------
+// Widening is exact. Narrowing uses gfx950's v_cvt_pk_bf16_f32: round to nearest even.
+__device__ __forceinline__ float lo_f(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi_f(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+}
+
+__device__ __forceinline__ void unpack8(const uint4& w, float* v) {
+  v[0] = lo_f(w.x); v[1] = hi_f(w.x);
+  v[2] = lo_f(w.y); v[3] = hi_f(w.y);
+  v[4] = lo_f(w.z); v[5] = hi_f(w.z);
+  v[6] = lo_f(w.w); v[7] = hi_f(w.w);
+}
+__device__ __forceinline__ uint4 pack8(const float* v) {
+  uint4 w;
+  w.x = pack2(v[0], v[1]);
+  w.y = pack2(v[2], v[3]);
+  w.z = pack2(v[4], v[5]);
+  w.w = pack2(v[6], v[7]);
+  return w;
+}
+
+// ---- activations (fp32 opmath) -----------------------------------------------------------------
+// tanh GELU with the inner argument clamped to +-10 (kinomlx/kernels/fused_ops.py:27-35).
+__device__ __forceinline__ float gelu_tanh(float x) {
+  const float inner = 0.7978845608028654f * (x + 0.044715f * (x * x * x));
+  return 0.5f * x * (1.0f + tanhf(fminf(fmaxf(inner, -10.0f), 10.0f)));
+}
+// x / (1 + exp(-x)) (kinomlx/kernels/fused_ops.py:40-45).
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+
+// Call-free forms for epilogues that hold many live accumulators: a libm call there would force
+// every live register to be saved around it. exp via v_exp_f32 (exp2), tanh(u) = 1 - 2 / (e^2u + 1)
+// (saturates to +-1 for large |u|, no inf/inf).
+__device__ __forceinline__ float fast_exp(float x) {
+  return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
+}
+__device__ __forceinline__ float fast_gelu_tanh(float x) {
+  float inner = 0.7978845608028654f * (x + 0.044715f * (x * x * x));
+  inner = fminf(fmaxf(inner, -10.0f), 10.0f);
+  const float t = 1.0f - 2.0f / (fast_exp(2.0f * inner) + 1.0f);
+  return 0.5f * x * (1.0f + t);
+}
+__device__ __forceinline__ float fast_silu(float x) { return x / (1.0f + fast_exp(-x)); }
+__device__ __forceinline__ float fast_sigmoid2(float x) { return 2.0f / (1.0f + fast_exp(-x)); }
+
+// ---- wave reductions (wave64) -------------------------------------------------------------------
+template <int WIDTH>
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = WIDTH / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// ---- host side ----------------------------------------------------------------------------------
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
+
+// Maps a workgroup id to a logical tile id so that each of the 8 XCDs (which receive workgroups
+// round-robin) walks a contiguous range of logical tiles: neighbouring tiles then share the
+// same XCD's L2.
+__device__ __forceinline__ int xcd_remap(int bid, int total) {
+  const int per = total / 8, rem = total % 8;
+  const int xcd = bid % 8, local = bid / 8;
+  return (xcd < rem) ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+}
+
+}  // namespace kx
+
+#define KX_REQUIRE(cond, ...)                                  \
+  do {                                                         \
+    if (!(cond)) return ::kx::set_error(KX_ERR_INVALID, __VA_ARGS__); \
+  } while (0)

@@ -1,0 +1,439 @@
+// Dense bf16 and affine int4/int8 weight-quantized linear layers on gfx950 MFMA.
+//
+// c[m, n] = epilogue(sum_k a[m, k] * w[n, k]) — both operands K-contiguous (the reference's
+// (out, in) weight layout), fp32 accumulation in v_mfma_f32_32x32x16_bf16, one bf16 rounding.
+//
+// Tiling: a BM x BN output tile per workgroup of WM x WN waves; each wave owns a
+// (BM/WM) x (BN/WN) sub-tile as a grid of 32x32 MFMA blocks. K advances in stages of 64: the
+// next stage's global loads are issued into registers before the current stage's MFMAs and
+// written to the other half of a double-buffered LDS tile afterwards, so one barrier per stage
+// suffices. LDS rows are 128 bytes (64 bf16) with the 16-byte chunk index XOR-swizzled by the
+// row, so the 32-row fragment reads of an MFMA operand are bank-conflict free.
+//
+// The MFMA A operand is the weight tile and the B operand the activation tile, so that the
+// accumulator's lane holds one output row m and runs of 4 consecutive columns n: the epilogue
+// stores 8-byte vectors along the output row.
+//
+// Quantized weights: the stage's packed words and per-group bf16 scale/bias are loaded into
+// registers instead, and dequantized (bf16(fp32(scale) * q + fp32(bias))) on their way into LDS,
+// inside the mainloop; the MFMA loop is shared with the dense path.
+#include <stdlib.h>
+
+#include "common.h"
+
+namespace kx {
+namespace {
+
+constexpr int BK = 64;        // K per stage
+constexpr int ROWB = BK * 2;  // bytes per LDS tile row
+
+struct Epilogue {
+  const uint16_t* bias;
+  const uint16_t* resid;
+  int64_t ldr;
+  const float* gate;
+  int64_t gate_div;
+  int64_t gate_stride;
+  int flags;
+};
+
+struct QuantW {
+  const uint32_t* words;  // (n, k * bits / 32)
+  const uint16_t* scales;  // (n, k / 64)
+  const uint16_t* biases;  // (n, k / 64)
+};
+
+__device__ __forceinline__ int lds_off(int r, int c) { return r * ROWB + ((c ^ (r & 7)) << 4); }
+
+__device__ __forceinline__ float apply_act(float v, int act) {
+  switch (act) {
+    case 1: return fast_gelu_tanh(v);
+    case 2: return fast_silu(v);
+    case 3: return fast_sigmoid2(v);
+    default: return v;
+  }
+}
+
+template <int BITS>
+__device__ __forceinline__ uint4 dequant8(const uint32_t* wd, float s, float b) {
+  float v[8];
+  if (BITS == 4) {
+    const uint32_t w = wd[0];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = fmaf(s, (float)((w >> (4 * j)) & 15u), b);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[j] = fmaf(s, (float)((wd[0] >> (8 * j)) & 255u), b);
+      v[4 + j] = fmaf(s, (float)((wd[1] >> (8 * j)) & 255u), b);
+    }
+  }
+  return pack8(v);
+}
+
+// QB = 0: dense bf16 weights; QB = 4 / 8: affine quantized weights of that many bits.
+template <int BM, int BN, int WM, int WN, int QB>
+__global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(
+    const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ W, int64_t ldw,
+    QuantW qw, uint16_t* __restrict__ C, int64_t ldc, int M, int N, int K, Epilogue epi) {
+  constexpr int NT = WM * WN * 64;
+  constexpr int WT_M = BM / WM, WT_N = BN / WN;
+  constexpr int MB = WT_M / 32, NB = WT_N / 32;
+  constexpr int A_PER = BM * (BK / 8) / NT;
+  constexpr int W_PER = BN * (BK / 8) / NT;
+  constexpr int QWORDS = QB == 8 ? 2 : 1;
+  static_assert(A_PER * NT == BM * (BK / 8) && W_PER * NT == BN * (BK / 8), "tile/threads");
+  static_assert(MB >= 1 && NB >= 1, "wave tile");
+  constexpr int STAGE = (BM + BN) * ROWB;
+
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave % WM, wn = wave / WM;
+
+  // ---- tile coordinates: XCD-contiguous, then grouped by 8 tile rows for L2 reuse
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  const int t = xcd_remap(blockIdx.x, tiles_m * tiles_n);
+  constexpr int GM = 8;
+  const int group_width = GM * tiles_n;
+  const int first_m = (t / group_width) * GM;
+  const int gsz = min(tiles_m - first_m, GM);
+  const int tm = first_m + (t % group_width) % gsz;
+  const int tn = (t % group_width) / gsz;
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  // ---- global -> register prefetch
+  uint4 ra[A_PER];
+  uint4 rw[QB == 0 ? W_PER : 1];
+  uint32_t rq[QB == 0 ? 1 : W_PER][QWORDS];
+  float rs[QB == 0 ? 1 : W_PER], rb[QB == 0 ? 1 : W_PER];
+
+  auto load_stage = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < A_PER; ++i) {
+      const int q = tid + i * NT;
+      const int r = q >> 3, c = q & 7;
+      const int gm = min(m0 + r, M - 1);
+      const int gk = k0 + c * 8;
+      // Branch-free K tail: read a valid chunk, then zero it (K % 8 == 0, so K - 8 >= 0).
+      uint4 v = *reinterpret_cast<const uint4*>(A + (int64_t)gm * lda + min(gk, K - 8));
+      if (gk >= K) v = make_uint4(0, 0, 0, 0);
+      ra[i] = v;
+    }
+#pragma unroll
+    for (int i = 0; i < W_PER; ++i) {
+      const int q = tid + i * NT;
+      const int r = q >> 3, c = q & 7;
+      const int gn = min(n0 + r, N - 1);
+      const int gk = k0 + c * 8;
+      if (QB == 0) {
+        uint4 v = *reinterpret_cast<const uint4*>(W + (int64_t)gn * ldw + min(gk, K - 8));
+        if (gk >= K) v = make_uint4(0, 0, 0, 0);
+        rw[i] = v;
+      } else {
+        const int64_t wrow = (int64_t)gn * (K * QB / 32);
+#pragma unroll
+        for (int j = 0; j < QWORDS; ++j) rq[i][j] = qw.words[wrow + gk * QB / 32 + j];
+        const int64_t g = (int64_t)gn * (K / 64) + k0 / 64;
+        rs[i] = bf2f(qw.scales[g]);
+        rb[i] = bf2f(qw.biases[g]);
+      }
+    }
+  };
+
+  auto store_stage = [&](uint8_t* buf) {
+#pragma unroll
+    for (int i = 0; i < A_PER; ++i) {
+      const int q = tid + i * NT;
+      *reinterpret_cast<uint4*>(buf + lds_off(q >> 3, q & 7)) = ra[i];
+    }
+    uint8_t* wbuf = buf + BM * ROWB;
+#pragma unroll
+    for (int i = 0; i < W_PER; ++i) {
+      const int q = tid + i * NT;
+      uint4 v;
+      if (QB == 0)
+        v = rw[i];
+      else
+        v = dequant8<QB>(rq[i], rs[i], rb[i]);
+      *reinterpret_cast<uint4*>(wbuf + lds_off(q >> 3, q & 7)) = v;
+    }
+  };
+
+  f32x16 acc[NB][MB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i)
+#pragma unroll
+    for (int j = 0; j < MB; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  const int stages = (K + BK - 1) / BK;
+  load_stage(0);
+  store_stage(smem);
+  __syncthreads();
+
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  for (int kt = 0; kt < stages; ++kt) {
+    uint8_t* cur = smem + (kt & 1) * STAGE;
+    const bool more = kt + 1 < stages;
+    if (more) load_stage((kt + 1) * BK);
+    const uint8_t* tA = cur;
+    const uint8_t* tW = cur + BM * ROWB;
+#pragma unroll
+    for (int s = 0; s < BK / 16; ++s) {
+      const int c = 2 * s + lhalf;
+      bf16x8 af[MB], wf[NB];
+#pragma unroll
+      for (int j = 0; j < MB; ++j)
+        af[j] = *reinterpret_cast<const bf16x8*>(tA + lds_off(wm * WT_M + j * 32 + lrow, c));
+#pragma unroll
+      for (int i = 0; i < NB; ++i)
+        wf[i] = *reinterpret_cast<const bf16x8*>(tW + lds_off(wn * WT_N + i * 32 + lrow, c));
+#pragma unroll
+      for (int i = 0; i < NB; ++i)
+#pragma unroll
+        for (int j = 0; j < MB; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[i], af[j], acc[i][j], 0, 0, 0);
+    }
+    if (more) store_stage(smem + ((kt + 1) & 1) * STAGE);
+    __syncthreads();
+  }
+
+  // ---- epilogue, staged through LDS one 32-column block at a time. The unrolled part only
+  // moves accumulators (static indices, so they stay in registers); bias, activation and the
+  // gated residual run in a plain loop over rows with each lane on 4 consecutive columns.
+  constexpr int EP_LD = 36;  // padded fp32 row: 16-byte writes from 16 rows hit distinct banks
+  static_assert(WM * WN * WT_M * EP_LD * 4 <= 2 * STAGE, "epilogue staging must fit in LDS");
+  float* ep = reinterpret_cast<float*>(smem) + wave * (WT_M * EP_LD);
+  const int act = (epi.flags >> 4) & 15;
+  const bool has_bias = epi.flags & KX_EPI_BIAS;
+  const bool gated = epi.flags & KX_EPI_GATED_RESIDUAL;
+  const bool vec_store = (ldc % 4 == 0) && (!gated || epi.ldr % 4 == 0);
+  const int col4 = (lane & 7) * 4;
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+#pragma unroll
+    for (int j = 0; j < MB; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        float4 v;
+        v.x = acc[i][j][g * 4 + 0];
+        v.y = acc[i][j][g * 4 + 1];
+        v.z = acc[i][j][g * 4 + 2];
+        v.w = acc[i][j][g * 4 + 3];
+        *reinterpret_cast<float4*>(ep + (j * 32 + lrow) * EP_LD + g * 8 + lhalf * 4) = v;
+      }
+    __syncthreads();
+    const int n = n0 + wn * WT_N + i * 32 + col4;
+    float bias4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (has_bias) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bias4[e] = n + e < N ? bf2f(epi.bias[n + e]) : 0.0f;
+    }
+#pragma unroll 2
+    for (int r = lane >> 3; r < WT_M; r += 8) {
+      const int m = m0 + wm * WT_M + r;
+      if (m >= M || n >= N) continue;
+      const float4 a4 = *reinterpret_cast<const float4*>(ep + r * EP_LD + col4);
+      float v[4] = {a4.x + bias4[0], a4.y + bias4[1], a4.z + bias4[2], a4.w + bias4[3]};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = apply_act(v[e], act);
+      if (vec_store && n + 3 < N) {
+        if (gated) {
+          const float* grow = epi.gate + (m / epi.gate_div) * epi.gate_stride;
+          const uint2 rr = *reinterpret_cast<const uint2*>(epi.resid + (int64_t)m * epi.ldr + n);
+          const float4 gv = *reinterpret_cast<const float4*>(grow + n);
+          v[0] = lo_f(rr.x) + gv.x * v[0];
+          v[1] = hi_f(rr.x) + gv.y * v[1];
+          v[2] = lo_f(rr.y) + gv.z * v[2];
+          v[3] = hi_f(rr.y) + gv.w * v[3];
+        }
+        uint2 o;
+        o.x = pack2(v[0], v[1]);
+        o.y = pack2(v[2], v[3]);
+        *reinterpret_cast<uint2*>(C + (int64_t)m * ldc + n) = o;
+      } else {
+        for (int e = 0; e < 4 && n + e < N; ++e) {
+          float x = v[e];
+          if (gated)
+            x = bf2f(epi.resid[(int64_t)m * epi.ldr + n + e]) +
+                epi.gate[(m / epi.gate_div) * epi.gate_stride + n + e] * x;
+          C[(int64_t)m * ldc + n + e] = f2bf(x);
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+template <int BITS>
+__global__ __launch_bounds__(256) void dequant_kernel(const uint32_t* __restrict__ words,
+                                                      const uint16_t* __restrict__ scales,
+                                                      const uint16_t* __restrict__ biases,
+                                                      uint16_t* __restrict__ out, int64_t n,
+                                                      int64_t k, int group) {
+  const int64_t chunks_per_row = k / 8;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= n * chunks_per_row) return;
+  const int64_t r = idx / chunks_per_row, c = idx - r * chunks_per_row;
+  const int64_t kk = c * 8;
+  const int64_t g = r * (k / group) + kk / group;
+  const uint32_t* wd = words + r * (k * BITS / 32) + kk * BITS / 32;
+  uint32_t tmp[2] = {wd[0], BITS == 8 ? wd[1] : 0u};
+  *reinterpret_cast<uint4*>(out + r * k + kk) = dequant8<BITS>(tmp, bf2f(scales[g]), bf2f(biases[g]));
+}
+
+// ---- dispatch ---------------------------------------------------------------------------------
+
+enum TileCfg { T256x256 = 0, T256x128 = 1, T128x128 = 2, T64x64 = 3, T128x64 = 4 };
+
+template <int BM, int BN, int WM, int WN, int QB>
+int launch_cfg(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, QuantW qw,
+               uint16_t* c, int64_t ldc, int m, int n, int k, const Epilogue& epi,
+               hipStream_t s) {
+  const int tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+  gemm_kernel<BM, BN, WM, WN, QB><<<tiles, WM * WN * 64, 0, s>>>(a, lda, w, ldw, qw, c, ldc, m, n,
+                                                                k, epi);
+  return KX_OK;
+}
+
+int pick_cfg(int64_t m, int64_t n) {
+  const char* env = getenv("KX355_GEMM_TILE");
+  if (env && *env) {
+    const int v = atoi(env);
+    if (v >= 0 && v <= 4) return v;
+  }
+  if (m < 512 || n < 512) return (m * n >= 256 * 1024) ? T128x64 : T64x64;
+  // Prefer the largest tile whose last wave of workgroups keeps the 256 CUs mostly busy.
+  auto eff = [](int64_t tiles) {
+    const int64_t waves = (tiles + 255) / 256;
+    return (double)tiles / (double)(waves * 256);
+  };
+  const int64_t t256 = ((m + 255) / 256) * ((n + 255) / 256);
+  const int64_t t128 = ((m + 255) / 256) * ((n + 127) / 128);
+  if (eff(t256) >= 0.85) return T256x256;
+  if (eff(t128) >= 0.85 || t128 >= 1024) return T256x128;
+  return T128x128;
+}
+
+template <int QB>
+int dispatch(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, QuantW qw,
+             uint16_t* c, int64_t ldc, int64_t m, int64_t n, int64_t k, const Epilogue& epi,
+             hipStream_t s) {
+  switch (pick_cfg(m, n)) {
+    case T256x256:
+      return launch_cfg<256, 256, 2, 2, QB>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k,
+                                            epi, s);
+    case T256x128:
+      return launch_cfg<256, 128, 2, 2, QB>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k,
+                                            epi, s);
+    case T128x128:
+      return launch_cfg<128, 128, 2, 2, QB>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k,
+                                            epi, s);
+    case T128x64:
+      return launch_cfg<128, 64, 2, 2, QB>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k,
+                                           epi, s);
+    default:
+      return launch_cfg<64, 64, 2, 2, QB>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi,
+                                          s);
+  }
+}
+
+int check_epilogue(const char* name, int epilogue, const void* bias, const void* resid,
+                   int64_t ldr, int64_t n, const float* gate, int64_t gate_div,
+                   int64_t gate_stride) {
+  const int act = (epilogue >> 4) & 15;
+  KX_REQUIRE((epilogue & ~(KX_EPI_BIAS | (15 << 4) | KX_EPI_GATED_RESIDUAL)) == 0 && act <= 3,
+             "%s: bad epilogue flags %d", name, epilogue);
+  KX_REQUIRE(!(epilogue & KX_EPI_BIAS) || (bias && aligned8(bias)), "%s: bias missing or unaligned",
+             name);
+  if (epilogue & KX_EPI_GATED_RESIDUAL) {
+    KX_REQUIRE(resid && gate && ldr >= n && gate_div > 0 && gate_stride >= 0,
+               "%s: gated residual needs resid, ldr >= n and gate rows", name);
+    KX_REQUIRE(aligned8(resid) && aligned16(gate) && gate_stride % 4 == 0,
+               "%s: resid must be 8-byte and gate 16-byte aligned", name);
+  }
+  return KX_OK;
+}
+
+}  // namespace
+}  // namespace kx
+
+using namespace kx;
+
+extern "C" int kx_gemm_bf16(const void* a, int64_t lda, const void* w, int64_t ldw,
+                            const void* bias, void* c, int64_t ldc, int64_t m, int64_t n,
+                            int64_t k, int epilogue, const void* resid, int64_t ldr,
+                            const float* gate, int64_t gate_div, int64_t gate_stride,
+                            kx_stream_t stream) {
+  KX_REQUIRE(a && w && c, "kx_gemm_bf16: null tensor");
+  KX_REQUIRE(m >= 0 && n >= 0 && k > 0 && m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 30),
+             "kx_gemm_bf16: bad shape (%lld, %lld, %lld)", (long long)m, (long long)n,
+             (long long)k);
+  KX_REQUIRE(k % 8 == 0 && lda % 8 == 0 && ldw % 8 == 0 && lda >= k && ldw >= k && ldc >= n,
+             "kx_gemm_bf16: k, lda and ldw must be multiples of 8 (k=%lld lda=%lld ldw=%lld)",
+             (long long)k, (long long)lda, (long long)ldw);
+  KX_REQUIRE(aligned16(a) && aligned16(w) && aligned8(c), "kx_gemm_bf16: a/w must be 16-byte "
+             "and c 8-byte aligned");
+  const int rc = check_epilogue("kx_gemm_bf16", epilogue, bias, resid, ldr, n, gate, gate_div,
+                                gate_stride);
+  if (rc) return rc;
+  if (m == 0 || n == 0) return KX_OK;
+  const Epilogue epi{(const uint16_t*)bias, (const uint16_t*)resid, ldr, gate, gate_div,
+                     gate_stride, epilogue};
+  dispatch<0>((const uint16_t*)a, lda, (const uint16_t*)w, ldw, QuantW{}, (uint16_t*)c, ldc, m, n,
+              k, epi, (hipStream_t)stream);
+  return check_launch("kx_gemm_bf16");
+}
+
+extern "C" int kx_qgemm_affine_bf16(const void* a, int64_t lda, const uint32_t* wq,
+                                    const void* scales, const void* biases, const void* bias,
+                                    void* c, int64_t ldc, int64_t m, int64_t n, int64_t k,
+                                    int group_size, int bits, int epilogue, const void* resid,
+                                    int64_t ldr, const float* gate, int64_t gate_div,
+                                    int64_t gate_stride, kx_stream_t stream) {
+  KX_REQUIRE(a && wq && scales && biases && c, "kx_qgemm_affine_bf16: null tensor");
+  KX_REQUIRE(bits == 4 || bits == 8, "kx_qgemm_affine_bf16: bits must be 4 or 8, got %d", bits);
+  KX_REQUIRE(group_size == 64, "kx_qgemm_affine_bf16: group_size must be 64, got %d", group_size);
+  KX_REQUIRE(m >= 0 && n >= 0 && k > 0 && k % 64 == 0 && m < (1ll << 31) && n < (1ll << 31) &&
+                 k < (1ll << 30),
+             "kx_qgemm_affine_bf16: bad shape (k must be a multiple of 64)");
+  KX_REQUIRE(lda % 8 == 0 && lda >= k && ldc >= n && aligned16(a) && aligned8(c),
+             "kx_qgemm_affine_bf16: bad stride or alignment");
+  const int rc = check_epilogue("kx_qgemm_affine_bf16", epilogue, bias, resid, ldr, n, gate,
+                                gate_div, gate_stride);
+  if (rc) return rc;
+  if (m == 0 || n == 0) return KX_OK;
+  const Epilogue epi{(const uint16_t*)bias, (const uint16_t*)resid, ldr, gate, gate_div,
+                     gate_stride, epilogue};
+  const QuantW qw{wq, (const uint16_t*)scales, (const uint16_t*)biases};
+  if (bits == 4)
+    dispatch<4>((const uint16_t*)a, lda, nullptr, 0, qw, (uint16_t*)c, ldc, m, n, k, epi,
+                (hipStream_t)stream);
+  else
+    dispatch<8>((const uint16_t*)a, lda, nullptr, 0, qw, (uint16_t*)c, ldc, m, n, k, epi,
+                (hipStream_t)stream);
+  return check_launch("kx_qgemm_affine_bf16");
+}
+
+extern "C" int kx_dequant_affine_bf16(const uint32_t* wq, const void* scales, const void* biases,
+                                      void* out, int64_t n, int64_t k, int group_size, int bits,
+                                      kx_stream_t stream) {
+  KX_REQUIRE(wq && scales && biases && out, "kx_dequant_affine_bf16: null tensor");
+  KX_REQUIRE(bits == 4 || bits == 8, "kx_dequant_affine_bf16: bits must be 4 or 8");
+  KX_REQUIRE(group_size > 0 && group_size % 8 == 0 && n >= 0 && k > 0 && k % group_size == 0,
+             "kx_dequant_affine_bf16: k must be a multiple of group_size (a multiple of 8)");
+  KX_REQUIRE(aligned16(out), "kx_dequant_affine_bf16: out must be 16-byte aligned");
+  const int64_t total = n * (k / 8);
+  if (total == 0) return KX_OK;
+  const unsigned blocks = (unsigned)((total + 255) / 256);
+  if (bits == 4)
+    dequant_kernel<4><<<blocks, 256, 0, (hipStream_t)stream>>>(
+        wq, (const uint16_t*)scales, (const uint16_t*)biases, (uint16_t*)out, n, k, group_size);
+  else
+    dequant_kernel<8><<<blocks, 256, 0, (hipStream_t)stream>>>(
+        wq, (const uint16_t*)scales, (const uint16_t*)biases, (uint16_t*)out, n, k, group_size);
+  return check_launch("kx_dequant_affine_bf16");
+}

@@ -1,0 +1,479 @@
+// Row norms of the DiT block on gfx950: HBM-bound, one wavefront per row.
+//
+// Fast path: a row of DIM = 512 * VPL bf16 values is held in registers, VPL 16-byte vectors per
+// lane, lane l's vector i covering columns [(64 i + l) * 8, +8). Every load and store is a
+// 16-byte access and a wave's access of one vector index is 1 KiB contiguous. The reduction is
+// a wave64 butterfly; nothing goes through LDS. Generic path (any width or alignment): one wave
+// per row (or norm group) with a strided scalar loop.
+#include "common.h"
+
+namespace kx {
+namespace {
+
+constexpr int kWaves = 4;  // rows per 256-thread workgroup
+
+// ----------------------------------------------------------------------------------------------
+// Modulated RMSNorm / LayerNorm: y = norm(x) * (1 + scale) + shift.
+
+template <int VPL, int KIND, bool MOD>
+__global__ __launch_bounds__(256) void adaln_norm_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, uint16_t* __restrict__ y, int64_t ldy,
+    int64_t rows, const float* __restrict__ shift, const float* __restrict__ scale,
+    int64_t mod_div, int64_t mod_stride, float eps) {
+  constexpr int DIM = VPL * 512;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const uint16_t* xr = x + row * ldx;
+  float v[VPL][8];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const uint4 w = *reinterpret_cast<const uint4*>(xr + (i * 64 + lane) * 8);
+    unpack8(w, v[i]);
+  }
+  float mean = 0.0f;
+  if (KIND == KX_NORM_LAYER) {
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s += v[i][j];
+    mean = wave_sum<64>(s) * (1.0f / DIM);
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float d = v[i][j] - mean;
+      ss = fmaf(d, d, ss);
+    }
+  const float inv = rsqrtf(wave_sum<64>(ss) * (1.0f / DIM) + eps);
+  const int64_t mrow = MOD ? (row / mod_div) * mod_stride : 0;
+  uint16_t* yr = y + row * ldy;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int col = (i * 64 + lane) * 8;
+    float o[8];
+    if (MOD) {
+      const float4 sc0 = *reinterpret_cast<const float4*>(scale + mrow + col);
+      const float4 sc1 = *reinterpret_cast<const float4*>(scale + mrow + col + 4);
+      const float4 sh0 = *reinterpret_cast<const float4*>(shift + mrow + col);
+      const float4 sh1 = *reinterpret_cast<const float4*>(shift + mrow + col + 4);
+      const float sc[8] = {sc0.x, sc0.y, sc0.z, sc0.w, sc1.x, sc1.y, sc1.z, sc1.w};
+      const float sh[8] = {sh0.x, sh0.y, sh0.z, sh0.w, sh1.x, sh1.y, sh1.z, sh1.w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = (v[i][j] - mean) * inv * (1.0f + sc[j]) + sh[j];
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = (v[i][j] - mean) * inv;
+    }
+    *reinterpret_cast<uint4*>(yr + col) = pack8(o);
+  }
+}
+
+template <int KIND>
+__global__ __launch_bounds__(256) void adaln_norm_generic(
+    const uint16_t* __restrict__ x, int64_t ldx, uint16_t* __restrict__ y, int64_t ldy,
+    int64_t rows, int64_t dim, const float* __restrict__ shift, const float* __restrict__ scale,
+    int64_t mod_div, int64_t mod_stride, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const uint16_t* xr = x + row * ldx;
+  float mean = 0.0f;
+  if (KIND == KX_NORM_LAYER) {
+    float s = 0.0f;
+    for (int64_t c = lane; c < dim; c += 64) s += bf2f(xr[c]);
+    mean = wave_sum<64>(s) / (float)dim;
+  }
+  float ss = 0.0f;
+  for (int64_t c = lane; c < dim; c += 64) {
+    const float d = bf2f(xr[c]) - mean;
+    ss = fmaf(d, d, ss);
+  }
+  const float inv = rsqrtf(wave_sum<64>(ss) / (float)dim + eps);
+  const bool mod = shift != nullptr;
+  const int64_t mrow = mod ? (row / mod_div) * mod_stride : 0;
+  uint16_t* yr = y + row * ldy;
+  for (int64_t c = lane; c < dim; c += 64) {
+    float o = (bf2f(xr[c]) - mean) * inv;
+    if (mod) o = o * (1.0f + scale[mrow + c]) + shift[mrow + c];
+    yr[c] = f2bf(o);
+  }
+}
+
+// ----------------------------------------------------------------------------------------------
+// Weighted RMSNorm (+ optional RoPE on the normalized value).
+//
+// G == 0: one norm over the whole row. G > 0: norm groups of 8 * G columns (G lanes of one
+// vector), e.g. per-head norms of 128 columns with G = 16.
+// SPLIT RoPE pairs column d < half of a head with d + half, held by lane l ^ (half / 8).
+// PAIR RoPE pairs columns 2i and 2i + 1, both in the same lane.
+
+template <bool BF16W>
+__device__ __forceinline__ float load_w(const void* w, int64_t i) {
+  if (BF16W) return bf2f(reinterpret_cast<const uint16_t*>(w)[i]);
+  return reinterpret_cast<const float*>(w)[i];
+}
+
+template <int VPL, int G, int ROPE, bool BF16W>
+__global__ __launch_bounds__(256) void rmsnorm_rope_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, uint16_t* __restrict__ y, int64_t ldy,
+    int64_t rows, int norm_width, const void* __restrict__ w, float eps, float weight_offset,
+    const float* __restrict__ cosp, const float* __restrict__ sinp, int64_t table_ld,
+    int64_t table_hs, int64_t tokens, int table_batched, int head_dim) {
+  constexpr int DIM = VPL * 512;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const uint16_t* xr = x + row * ldx;
+  float v[VPL][8];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const uint4 q = *reinterpret_cast<const uint4*>(xr + (i * 64 + lane) * 8);
+    unpack8(q, v[i]);
+  }
+  float inv[VPL];
+  if (G == 0) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss = fmaf(v[i][j], v[i][j], ss);
+    const float r = rsqrtf(wave_sum<64>(ss) * (1.0f / DIM) + eps);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) inv[i] = r;
+  } else {
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss = fmaf(v[i][j], v[i][j], ss);
+      inv[i] = rsqrtf(wave_sum<G>(ss) * (1.0f / (8 * G)) + eps);
+    }
+  }
+  // normalized, weighted values (fp32, not rounded)
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int col = (i * 64 + lane) * 8;
+    const int wcol = (G == 0) ? col : (col % norm_width);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      v[i][j] = v[i][j] * inv[i] * (load_w<BF16W>(w, wcol + j) + weight_offset);
+  }
+  uint16_t* yr = y + row * ldy;
+  if (ROPE == KX_ROPE_NONE) {
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) *reinterpret_cast<uint4*>(yr + (i * 64 + lane) * 8) = pack8(v[i]);
+    return;
+  }
+  const int64_t tok = table_batched ? row : (row % tokens);
+  const float* ct = cosp + tok * table_ld;
+  const float* st = sinp + tok * table_ld;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int col = (i * 64 + lane) * 8;
+    const int h = col / head_dim;
+    const int d = col - h * head_dim;
+    float o[8];
+    if (ROPE == KX_ROPE_SPLIT) {
+      const int half = head_dim >> 1;
+      const int partner_mask = half >> 3;  // lanes between d and d + half
+      float p[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) p[j] = __shfl_xor(v[i][j], partner_mask, 64);
+      const bool first = d < half;
+      const int ti = first ? d : d - half;
+      const float* cr = ct + h * table_hs + ti;
+      const float* sr = st + h * table_hs + ti;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+#pragma clang fp contract(off)
+        const float c = cr[j], s = sr[j];
+        if (first) {
+          const float a = v[i][j] * c;  // first * c
+          const float b = p[j] * s;     // second * s
+          o[j] = a - b;
+        } else {
+          const float a = p[j] * s;     // first * s
+          const float b = v[i][j] * c;  // second * c
+          o[j] = a + b;
+        }
+      }
+    } else {  // PAIR
+      const float* cr = ct + h * table_hs + d;
+      const float* sr = st + h * table_hs + d;
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) {
+#pragma clang fp contract(off)
+        const float x0 = v[i][j], x1 = v[i][j + 1];
+        const float a0 = x0 * cr[j];
+        const float b0 = (-x1) * sr[j];
+        const float a1 = x1 * cr[j + 1];
+        const float b1 = x0 * sr[j + 1];
+        o[j] = a0 + b0;
+        o[j + 1] = a1 + b1;
+      }
+    }
+    *reinterpret_cast<uint4*>(yr + col) = pack8(o);
+  }
+}
+
+// One wave per norm group, any width; weighted RMSNorm only.
+template <bool BF16W>
+__global__ __launch_bounds__(256) void rmsnorm_generic(
+    const uint16_t* __restrict__ x, int64_t ldx, uint16_t* __restrict__ y, int64_t ldy,
+    int64_t rows, int64_t dim, int64_t norm_width, const void* __restrict__ w, float eps,
+    float weight_offset) {
+  const int lane = threadIdx.x & 63;
+  const int64_t groups_per_row = dim / norm_width;
+  const int64_t g = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (g >= rows * groups_per_row) return;
+  const int64_t row = g / groups_per_row;
+  const int64_t c0 = (g - row * groups_per_row) * norm_width;
+  const uint16_t* xr = x + row * ldx + c0;
+  float ss = 0.0f;
+  for (int64_t c = lane; c < norm_width; c += 64) {
+    const float a = bf2f(xr[c]);
+    ss = fmaf(a, a, ss);
+  }
+  const float inv = rsqrtf(wave_sum<64>(ss) / (float)norm_width + eps);
+  uint16_t* yr = y + row * ldy + c0;
+  for (int64_t c = lane; c < norm_width; c += 64)
+    yr[c] = f2bf(bf2f(xr[c]) * inv * (load_w<BF16W>(w, c) + weight_offset));
+}
+
+// ----------------------------------------------------------------------------------------------
+// Elementwise row ops with fp32 modulation rows.
+
+__global__ __launch_bounds__(256) void modulate_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, uint16_t* __restrict__ y, int64_t ldy,
+    int64_t rows, int64_t dim, const float* __restrict__ shift, const float* __restrict__ scale,
+    int64_t mod_div, int64_t mod_stride) {
+  const int64_t per_row = dim;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= rows * per_row) return;
+  const int64_t r = idx / per_row, c = idx - r * per_row;
+  const int64_t m = (r / mod_div) * mod_stride + c;
+  y[r * ldy + c] = f2bf(bf2f(x[r * ldx + c]) * (1.0f + scale[m]) + shift[m]);
+}
+
+__global__ __launch_bounds__(256) void gated_residual_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ r, int64_t ldr,
+    uint16_t* __restrict__ y, int64_t ldy, int64_t rows, int64_t dim,
+    const float* __restrict__ gate, int64_t gate_div, int64_t gate_stride) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= rows * dim) return;
+  const int64_t row = idx / dim, c = idx - row * dim;
+  const float g = gate[(row / gate_div) * gate_stride + c];
+  const float base = x ? bf2f(x[row * ldx + c]) : 0.0f;
+  y[row * ldy + c] = f2bf(base + bf2f(r[row * ldr + c]) * g);
+}
+
+template <int VPL, int KIND>
+int launch_adaln(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows,
+                 const float* shift, const float* scale, int64_t mod_div, int64_t mod_stride,
+                 float eps, hipStream_t s) {
+  const dim3 grid((unsigned)((rows + kWaves - 1) / kWaves));
+  if (shift)
+    adaln_norm_kernel<VPL, KIND, true><<<grid, 256, 0, s>>>(
+        (const uint16_t*)x, ldx, (uint16_t*)y, ldy, rows, shift, scale, mod_div, mod_stride, eps);
+  else
+    adaln_norm_kernel<VPL, KIND, false><<<grid, 256, 0, s>>>(
+        (const uint16_t*)x, ldx, (uint16_t*)y, ldy, rows, shift, scale, mod_div, mod_stride, eps);
+  return check_launch("kx_adaln_norm_bf16");
+}
+
+template <int VPL, int G, int ROPE>
+int launch_rmsnorm_rope(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows,
+                        int64_t norm_width, const void* w, int w_dtype, float eps, float off,
+                        const float* cosp, const float* sinp, int64_t table_ld, int64_t table_hs,
+                        int64_t tokens, int table_batched, int64_t head_dim, hipStream_t s) {
+  const dim3 grid((unsigned)((rows + kWaves - 1) / kWaves));
+  if (w_dtype == KX_BF16)
+    rmsnorm_rope_kernel<VPL, G, ROPE, true><<<grid, 256, 0, s>>>(
+        (const uint16_t*)x, ldx, (uint16_t*)y, ldy, rows, (int)norm_width, w, eps, off, cosp,
+        sinp, table_ld, table_hs, tokens, table_batched, (int)head_dim);
+  else
+    rmsnorm_rope_kernel<VPL, G, ROPE, false><<<grid, 256, 0, s>>>(
+        (const uint16_t*)x, ldx, (uint16_t*)y, ldy, rows, (int)norm_width, w, eps, off, cosp,
+        sinp, table_ld, table_hs, tokens, table_batched, (int)head_dim);
+  return check_launch("kx_rmsnorm_rope_bf16");
+}
+
+template <int VPL, int G>
+int dispatch_rope(int rope, const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows,
+                  int64_t nw, const void* w, int wd, float eps, float off, const float* c,
+                  const float* sn, int64_t tld, int64_t ths, int64_t tokens, int tb, int64_t hd,
+                  hipStream_t s) {
+  switch (rope) {
+    case KX_ROPE_NONE:
+      return launch_rmsnorm_rope<VPL, G, KX_ROPE_NONE>(x, ldx, y, ldy, rows, nw, w, wd, eps, off,
+                                                      c, sn, tld, ths, tokens, tb, hd, s);
+    case KX_ROPE_SPLIT:
+      return launch_rmsnorm_rope<VPL, G, KX_ROPE_SPLIT>(x, ldx, y, ldy, rows, nw, w, wd, eps,
+                                                       off, c, sn, tld, ths, tokens, tb, hd, s);
+    default:
+      return launch_rmsnorm_rope<VPL, G, KX_ROPE_PAIR>(x, ldx, y, ldy, rows, nw, w, wd, eps, off,
+                                                      c, sn, tld, ths, tokens, tb, hd, s);
+  }
+}
+
+template <int VPL>
+int dispatch_group(int64_t gw, int rope, const void* x, int64_t ldx, void* y, int64_t ldy,
+                   int64_t rows, int64_t nw, const void* w, int wd, float eps, float off,
+                   const float* c, const float* sn, int64_t tld, int64_t ths, int64_t tokens,
+                   int tb, int64_t hd, hipStream_t s) {
+  switch (gw) {
+    case 0:
+      return dispatch_rope<VPL, 0>(rope, x, ldx, y, ldy, rows, nw, w, wd, eps, off, c, sn, tld,
+                                   ths, tokens, tb, hd, s);
+    case 8:
+      return dispatch_rope<VPL, 8>(rope, x, ldx, y, ldy, rows, nw, w, wd, eps, off, c, sn, tld,
+                                   ths, tokens, tb, hd, s);
+    case 16:
+      return dispatch_rope<VPL, 16>(rope, x, ldx, y, ldy, rows, nw, w, wd, eps, off, c, sn, tld,
+                                    ths, tokens, tb, hd, s);
+    default:
+      return dispatch_rope<VPL, 32>(rope, x, ldx, y, ldy, rows, nw, w, wd, eps, off, c, sn, tld,
+                                    ths, tokens, tb, hd, s);
+  }
+}
+
+}  // namespace
+}  // namespace kx
+
+using namespace kx;
+
+extern "C" int kx_adaln_norm_bf16(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows,
+                                  int64_t dim, const float* shift, const float* scale,
+                                  int64_t mod_div, int64_t mod_stride, float eps, int kind,
+                                  kx_stream_t stream) {
+  KX_REQUIRE(x && y, "kx_adaln_norm_bf16: null tensor");
+  KX_REQUIRE(rows >= 0 && dim > 0 && ldx >= dim && ldy >= dim, "kx_adaln_norm_bf16: bad shape");
+  KX_REQUIRE((shift == nullptr) == (scale == nullptr),
+             "kx_adaln_norm_bf16: shift and scale must both be given or both be null");
+  KX_REQUIRE(!shift || (mod_div > 0 && mod_stride >= 0), "kx_adaln_norm_bf16: bad modulation");
+  KX_REQUIRE(kind == KX_NORM_RMS || kind == KX_NORM_LAYER, "kx_adaln_norm_bf16: bad kind");
+  if (rows == 0) return KX_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const bool vec = dim % 512 == 0 && ldx % 8 == 0 && ldy % 8 == 0 && aligned16(x) &&
+                   aligned16(y) &&
+                   (!shift || (aligned16(shift) && aligned16(scale) && mod_stride % 4 == 0));
+  const int64_t vpl = dim / 512;
+  if (vec && (vpl == 1 || vpl == 2 || vpl == 4 || vpl == 8)) {
+#define KX_ADALN(V)                                                                             \
+  return kind == KX_NORM_RMS                                                                    \
+             ? launch_adaln<V, KX_NORM_RMS>(x, ldx, y, ldy, rows, shift, scale, mod_div,       \
+                                            mod_stride, eps, s)                                 \
+             : launch_adaln<V, KX_NORM_LAYER>(x, ldx, y, ldy, rows, shift, scale, mod_div,     \
+                                              mod_stride, eps, s);
+    switch (vpl) {
+      case 1: KX_ADALN(1)
+      case 2: KX_ADALN(2)
+      case 4: KX_ADALN(4)
+      default: KX_ADALN(8)
+    }
+#undef KX_ADALN
+  }
+  const dim3 grid((unsigned)((rows + kWaves - 1) / kWaves));
+  if (kind == KX_NORM_RMS)
+    adaln_norm_generic<KX_NORM_RMS><<<grid, 256, 0, s>>>((const uint16_t*)x, ldx, (uint16_t*)y,
+                                                         ldy, rows, dim, shift, scale, mod_div,
+                                                         mod_stride, eps);
+  else
+    adaln_norm_generic<KX_NORM_LAYER><<<grid, 256, 0, s>>>((const uint16_t*)x, ldx,
+                                                           (uint16_t*)y, ldy, rows, dim, shift,
+                                                           scale, mod_div, mod_stride, eps);
+  return check_launch("kx_adaln_norm_bf16");
+}
+
+extern "C" int kx_rmsnorm_rope_bf16(const void* x, int64_t ldx, void* y, int64_t ldy,
+                                    int64_t rows, int64_t dim, int64_t norm_width, const void* w,
+                                    int w_dtype, float eps, float weight_offset, int rope_kind,
+                                    const float* cos, const float* sin, int64_t table_ld,
+                                    int64_t table_hs, int64_t tokens, int table_batched,
+                                    int64_t head_dim, kx_stream_t stream) {
+  KX_REQUIRE(x && y && w, "kx_rmsnorm_rope_bf16: null tensor");
+  KX_REQUIRE(rows >= 0 && dim > 0 && ldx >= dim && ldy >= dim, "kx_rmsnorm_rope_bf16: bad shape");
+  KX_REQUIRE(norm_width > 0 && dim % norm_width == 0, "kx_rmsnorm_rope_bf16: bad norm width");
+  KX_REQUIRE(w_dtype == KX_F32 || w_dtype == KX_BF16, "kx_rmsnorm_rope_bf16: bad weight dtype");
+  KX_REQUIRE(rope_kind >= KX_ROPE_NONE && rope_kind <= KX_ROPE_PAIR,
+             "kx_rmsnorm_rope_bf16: bad rope kind");
+  if (rope_kind != KX_ROPE_NONE) {
+    KX_REQUIRE(cos && sin, "kx_rmsnorm_rope_bf16: null table");
+    KX_REQUIRE(head_dim > 0 && head_dim % 2 == 0 && dim % head_dim == 0,
+               "kx_rmsnorm_rope_bf16: bad head_dim");
+    KX_REQUIRE(table_batched || tokens > 0, "kx_rmsnorm_rope_bf16: bad token count");
+  }
+  if (rows == 0) return KX_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t vpl = dim / 512;
+  const int64_t group_lanes = norm_width == dim ? 0 : norm_width / 8;
+  const bool shape_ok = dim % 512 == 0 && (vpl == 1 || vpl == 2 || vpl == 4 || vpl == 8) &&
+                        (norm_width == dim ||
+                         (norm_width % 8 == 0 &&
+                          (group_lanes == 8 || group_lanes == 16 || group_lanes == 32)));
+  bool rope_ok = true;
+  if (rope_kind == KX_ROPE_SPLIT)
+    rope_ok = head_dim >= 16 && 512 % head_dim == 0 && ((head_dim / 2) % 8 == 0);
+  else if (rope_kind == KX_ROPE_PAIR)
+    rope_ok = 512 % head_dim == 0 && head_dim >= 8;
+  const bool align_ok = ldx % 8 == 0 && ldy % 8 == 0 && aligned16(x) && aligned16(y);
+  if (shape_ok && rope_ok && align_ok) {
+#define KX_RR(V)                                                                               \
+  return dispatch_group<V>(group_lanes, rope_kind, x, ldx, y, ldy, rows, norm_width, w, w_dtype, \
+                           eps, weight_offset, cos, sin, table_ld, table_hs, tokens,            \
+                           table_batched, head_dim, s);
+    switch (vpl) {
+      case 1: KX_RR(1)
+      case 2: KX_RR(2)
+      case 4: KX_RR(4)
+      default: KX_RR(8)
+    }
+#undef KX_RR
+  }
+  if (rope_kind != KX_ROPE_NONE)
+    return set_error(KX_ERR_UNSUPPORTED,
+                     "kx_rmsnorm_rope_bf16: fused RoPE needs dim in {512,1024,2048,4096}, "
+                     "aligned rows and a head_dim dividing 512");
+  const int64_t groups = rows * (dim / norm_width);
+  const dim3 grid((unsigned)((groups + kWaves - 1) / kWaves));
+  if (w_dtype == KX_BF16)
+    rmsnorm_generic<true><<<grid, 256, 0, s>>>((const uint16_t*)x, ldx, (uint16_t*)y, ldy, rows,
+                                               dim, norm_width, w, eps, weight_offset);
+  else
+    rmsnorm_generic<false><<<grid, 256, 0, s>>>((const uint16_t*)x, ldx, (uint16_t*)y, ldy, rows,
+                                                dim, norm_width, w, eps, weight_offset);
+  return check_launch("kx_rmsnorm_rope_bf16");
+}
+
+extern "C" int kx_modulate_bf16(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows,
+                                int64_t dim, const float* shift, const float* scale,
+                                int64_t mod_div, int64_t mod_stride, kx_stream_t stream) {
+  KX_REQUIRE(x && y && shift && scale, "kx_modulate_bf16: null tensor");
+  KX_REQUIRE(rows >= 0 && dim > 0 && ldx >= dim && ldy >= dim && mod_div > 0 && mod_stride >= 0,
+             "kx_modulate_bf16: bad shape");
+  const int64_t total = rows * dim;
+  if (total == 0) return KX_OK;
+  modulate_kernel<<<(unsigned)((total + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+      (const uint16_t*)x, ldx, (uint16_t*)y, ldy, rows, dim, shift, scale, mod_div, mod_stride);
+  return check_launch("kx_modulate_bf16");
+}
+
+extern "C" int kx_gated_residual_bf16(const void* x, int64_t ldx, const void* r, int64_t ldr,
+                                      void* y, int64_t ldy, int64_t rows, int64_t dim,
+                                      const float* gate, int64_t gate_div, int64_t gate_stride,
+                                      kx_stream_t stream) {
+  KX_REQUIRE(r && y && gate, "kx_gated_residual_bf16: null tensor");
+  KX_REQUIRE(rows >= 0 && dim > 0 && ldr >= dim && ldy >= dim && (!x || ldx >= dim) &&
+                 gate_div > 0 && gate_stride >= 0,
+             "kx_gated_residual_bf16: bad shape");
+  const int64_t total = rows * dim;
+  if (total == 0) return KX_OK;
+  gated_residual_kernel<<<(unsigned)((total + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+      (const uint16_t*)x, ldx, (const uint16_t*)r, ldr, (uint16_t*)y, ldy, rows, dim, gate,
+      gate_div, gate_stride);
+  return check_launch("kx_gated_residual_bf16");
+}

@@ -1,0 +1,203 @@
+"""Group-wise affine int4/int8 weight-quantized linear layers on MI355X.
+
+Replaces ``nn.QuantizedLinear`` / ``mx.quantized_matmul(..., mode="affine")`` as the LTX-2 loader
+installs them (``kinomlx/models/ltx2/weights/quantization.py:17-44``, ``:221-274``; defaults
+``kinomlx/models/ltx2/weights/tensors.py:185-203``: affine -> group 64, 4 bits; quantizer call
+``kinomlx/models/ltx2/preparation.py:139-157``).
+
+Format: ``weight`` uint32 words ``(out, in * bits / 32)`` (stored in an int32 tensor), element
+``j`` of a word at bits ``[bits*j, bits*(j+1))``; ``scales`` and ``biases`` bf16 ``(out, in /
+group_size)``; ``w = scale * q + bias``. The kernel dequantizes inside its MFMA mainloop with
+``bf16(fp32(scale) * q + fp32(bias))`` — exact product, one FP32 add, one round-to-nearest-even.
+
+``quantize`` is this build's deterministic quantizer (MLX's own scale/bias selection is not
+reproduced): per group ``scale = bf16((max - min) / (2^bits - 1))``, ``bias = bf16(min)``,
+``q = clip(round((w - bias) / scale), 0, 2^bits - 1)``.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from .mpp_linear import ACTIVATIONS
+
+DEFAULT_GROUP_SIZE = 64
+DEFAULT_BITS = 4
+_MODES = ("affine",)
+
+
+def quant_defaults(mode: str, group_size: int | None, bits: int | None) -> tuple[int, int]:
+    """(group_size, bits) with the affine defaults (``weights/tensors.py:185-203``)."""
+    if mode not in _MODES:
+        raise ValueError(f"Unsupported quantization mode on MI355X: {mode}")
+    g = DEFAULT_GROUP_SIZE if group_size is None else group_size
+    b = DEFAULT_BITS if bits is None else bits
+    if g <= 0 or b <= 0:
+        raise ValueError("quantization group size and bits must be positive")
+    return g, b
+
+
+def _check_format(group_size: int, bits: int) -> None:
+    if bits not in (4, 8):
+        raise ValueError(f"affine quantization on MI355X takes 4 or 8 bits, got {bits}")
+    if group_size != 64:
+        raise ValueError(f"affine quantization on MI355X takes group size 64, got {group_size}")
+
+
+def pack(codes: torch.Tensor, bits: int) -> torch.Tensor:
+    """``(N, K)`` integer codes -> ``(N, K * bits / 32)`` little-endian words (int32 storage)."""
+    per_word = 32 // bits
+    n, k = codes.shape
+    c = codes.to(torch.int64).reshape(n, k // per_word, per_word)
+    shifts = torch.arange(per_word, device=codes.device, dtype=torch.int64) * bits
+    words = (c << shifts).sum(dim=-1)  # disjoint bit fields: the sum is the bitwise or
+    words = torch.where(words >= 2**31, words - 2**32, words)
+    return words.to(torch.int32)
+
+
+def unpack(words: torch.Tensor, bits: int) -> torch.Tensor:
+    """``(N, W)`` words -> ``(N, W * 32 / bits)`` codes (int64)."""
+    per_word = 32 // bits
+    w = words.to(torch.int64) & 0xFFFFFFFF
+    shifts = torch.arange(per_word, device=words.device, dtype=torch.int64) * bits
+    return ((w[..., None] >> shifts) & ((1 << bits) - 1)).reshape(words.shape[0], -1)
+
+
+def quantize(weight: torch.Tensor, group_size: int = DEFAULT_GROUP_SIZE, bits: int = DEFAULT_BITS,
+             mode: str = "affine") -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """``(out, in)`` weight -> ``(words, scales, biases)`` in the packed affine format."""
+    quant_defaults(mode, group_size, bits)
+    _check_format(group_size, bits)
+    w = weight.float()
+    n, k = w.shape
+    if k % group_size:
+        raise ValueError("the input width must be a multiple of the group size")
+    levels = (1 << bits) - 1
+    groups = w.reshape(n, k // group_size, group_size)
+    lo = groups.amin(dim=-1)
+    hi = groups.amax(dim=-1)
+    scale = (hi - lo) / levels
+    scale = torch.where(scale > 0, scale, torch.ones_like(scale))
+    scale_bf = scale.to(torch.bfloat16)
+    scale_bf = torch.where(scale_bf > 0, scale_bf, torch.ones_like(scale_bf))
+    bias_bf = lo.to(torch.bfloat16)
+    codes = torch.round((groups - bias_bf.float()[..., None]) / scale_bf.float()[..., None])
+    codes = codes.clamp(0, levels).to(torch.int64).reshape(n, k)
+    return pack(codes, bits), scale_bf.contiguous(), bias_bf.contiguous()
+
+
+def dequantize(words: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, *,
+               group_size: int = DEFAULT_GROUP_SIZE, bits: int = DEFAULT_BITS) -> torch.Tensor:
+    """Packed affine weight -> bf16 ``(out, in)`` through the kernel's own dequantization."""
+    _check_format(group_size, bits)
+    n = int(words.shape[0])
+    k = int(words.shape[1]) * 32 // bits
+    out = torch.empty((n, k), dtype=torch.bfloat16, device=words.device)
+    _lib.launch_dequant(words.contiguous(), scales.contiguous(), biases.contiguous(), out, n=n, k=k,
+                        group_size=group_size, bits=bits)
+    return out
+
+
+def quantized_matmul(
+    value: torch.Tensor,
+    weight: torch.Tensor,
+    scales: torch.Tensor,
+    biases: torch.Tensor,
+    *,
+    transpose: bool = True,
+    group_size: int = DEFAULT_GROUP_SIZE,
+    bits: int = DEFAULT_BITS,
+    mode: str = "affine",
+    bias: torch.Tensor | None = None,
+    activation: str | None = None,
+    residual: torch.Tensor | None = None,
+    gate: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """``value @ dequant(weight)^T (+ bias)`` with dequantization inside the MFMA mainloop;
+    ``activation``/``residual``/``gate`` as ``mpp_linear.fused_linear``."""
+    if not transpose:
+        raise ValueError("the MI355X quantized linear takes the (out, in) packing (transpose=True)")
+    quant_defaults(mode, group_size, bits)
+    _check_format(group_size, bits)
+    if value.dtype != torch.bfloat16:
+        raise ValueError(f"quantized_matmul takes bfloat16 activations on MI355X, got {value.dtype}")
+    n = int(weight.shape[0])
+    k = int(weight.shape[1]) * 32 // bits
+    if int(value.shape[-1]) != k:
+        raise ValueError(f"input width {value.shape[-1]} does not match the packed width {k}")
+    if scales.shape != (n, k // group_size) or biases.shape != scales.shape:
+        raise ValueError("scales and biases must be (out, in / group_size)")
+    a = value.reshape(-1, k)
+    if a.stride(-1) != 1 or a.data_ptr() % 16 or a.stride(0) % 8:
+        a = a.contiguous()
+    out = torch.empty((*value.shape[:-1], n), dtype=value.dtype, device=value.device)
+    if a.shape[0] == 0:
+        return out
+    flags = ACTIVATIONS[activation]
+    if bias is not None:
+        flags |= _lib.EPI_BIAS
+        bias = bias.to(torch.bfloat16).contiguous()
+    resid2 = gate32 = None
+    if residual is not None:
+        flags |= _lib.EPI_GATED_RESIDUAL
+        resid2 = residual.reshape(-1, n)
+        gate32 = gate.float()
+        if gate32.stride(-1) != 1 or gate32.data_ptr() % 16:
+            gate32 = gate32.contiguous()
+    _lib.launch_qgemm(
+        a, weight, scales, biases, out.reshape(-1, n), n=n, k=k, group_size=group_size, bits=bits,
+        bias=bias, flags=flags, resid=resid2, gate=gate32,
+    )
+    return out
+
+
+class QuantizedLinear:
+    """``nn.QuantizedLinear`` counterpart: packed affine weight, bf16 scales/biases, optional
+    bf16 bias; ``layer(x) = quantized_matmul(x, ...) + bias`` (bias fused in the epilogue)."""
+
+    def __init__(self, weight: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+                 bias: torch.Tensor | None = None, *, group_size: int = DEFAULT_GROUP_SIZE,
+                 bits: int = DEFAULT_BITS, mode: str = "affine") -> None:
+        quant_defaults(mode, group_size, bits)
+        _check_format(group_size, bits)
+        self.weight = weight
+        self.scales = scales
+        self.biases = biases
+        self.bias = bias
+        self.group_size = group_size
+        self.bits = bits
+        self.mode = mode
+
+    @classmethod
+    def from_linear(cls, weight: torch.Tensor, bias: torch.Tensor | None = None, *,
+                    group_size: int = DEFAULT_GROUP_SIZE, bits: int = DEFAULT_BITS) -> "QuantizedLinear":
+        words, scales, biases = quantize(weight, group_size, bits)
+        return cls(words, scales, biases, bias, group_size=group_size, bits=bits)
+
+    @property
+    def out_features(self) -> int:
+        return int(self.weight.shape[0])
+
+    @property
+    def in_features(self) -> int:
+        return int(self.weight.shape[1]) * 32 // self.bits
+
+    def __call__(self, value: torch.Tensor, *, activation: str | None = None,
+                 residual: torch.Tensor | None = None, gate: torch.Tensor | None = None) -> torch.Tensor:
+        return quantized_matmul(
+            value, self.weight, self.scales, self.biases, group_size=self.group_size,
+            bits=self.bits, mode=self.mode, bias=self.bias, activation=activation,
+            residual=residual, gate=gate,
+        )
+
+
+__all__ = [
+    "QuantizedLinear",
+    "dequantize",
+    "pack",
+    "quant_defaults",
+    "quantize",
+    "quantized_matmul",
+    "unpack",
+]

@@ -1,0 +1,261 @@
+"""LTX-2 attention on MI355X: gated multi-head attention with full-width Q/K RMSNorm and split
+RoPE.
+
+Mirror of ``kinomlx/models/ltx2/transformer/attention.py`` (``Attention``, ``RMSNorm``,
+``rms_norm``, ``scaled_dot_product_attention``, ``dense_kernel_attention``). The call sequence of
+``Attention.__call__`` (``:291-371``) is kept; the MI355X schedule fuses it into:
+
+* one MFMA GEMM for Q, K and V when the projections are fused (``fuse_projections``: one
+  ``(3 * inner, in)`` weight whose row blocks back ``to_q``/``to_k``/``to_v``), writing one
+  ``(T, 3 * inner)`` buffer whose column slices feed the next kernels without copies;
+* the gate logits GEMM with ``2 * sigmoid`` in its epilogue;
+* one pass per Q and K for the weighted RMSNorm and the split RoPE (FP32 throughout);
+* the flash-attention kernel with the per-head gate applied before its one rounding;
+* the output GEMM, optionally with the block's gated residual in its epilogue.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from ..kernels import fused_ops, mpp_linear, split_rope
+from ..kernels.quantized import QuantizedLinear
+from . import dense_attention as _dense
+from .rope import LTXRopeType
+
+
+class Linear:
+    """``nn.Linear`` counterpart: ``(out, in)`` bf16 weight and optional bias;
+    ``layer(x) = addmm(bias, x, W^T)`` through the MFMA kernel, with the kernel's epilogues."""
+
+    def __init__(self, weight: torch.Tensor, bias: torch.Tensor | None = None) -> None:
+        self.weight = weight
+        self.bias = bias
+
+    @property
+    def out_features(self) -> int:
+        return int(self.weight.shape[0])
+
+    @property
+    def in_features(self) -> int:
+        return int(self.weight.shape[1])
+
+    def __call__(self, value: torch.Tensor, *, activation: str | None = None,
+                 residual: torch.Tensor | None = None, gate: torch.Tensor | None = None,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+        return mpp_linear.fused_linear(value, self.weight, self.bias, activation=activation,
+                                       residual=residual, gate=gate, out=out)
+
+
+def rms_norm(value: torch.Tensor, weight: torch.Tensor | None = None, eps: float = 1e-6) -> torch.Tensor:
+    """Central RMSNorm precision policy (``attention.py:112-118``)."""
+    return fused_ops.rms_norm(value, weight, eps)
+
+
+class RMSNorm:
+    """RMS normalization with a checkpoint-backed scale vector (``attention.py:121-133``)."""
+
+    def __init__(self, dims: int, *, eps: float = 1e-6, weight: torch.Tensor | None = None) -> None:
+        self.dims = dims
+        self.eps = eps
+        self.weight = weight
+
+    def __call__(self, value: torch.Tensor) -> torch.Tensor:
+        if value.shape[-1] != self.dims:
+            raise ValueError(f"RMSNorm expects width {self.dims}, got {value.shape[-1]}")
+        return rms_norm(value, self.weight, self.eps)
+
+
+def _fused_norm_rope_ok(dim: int, head_dim: int) -> bool:
+    return dim % 512 == 0 and dim // 512 in (1, 2, 4, 8) and head_dim >= 16 and 512 % head_dim == 0
+
+
+def norm_rope(value: torch.Tensor, norm: RMSNorm, pe: tuple[torch.Tensor, torch.Tensor] | None,
+              heads: int) -> torch.Tensor:
+    """Weighted RMSNorm over the full width, then split RoPE on the normalized value; one pass
+    when the shape allows (``attention.py:353-359`` then ``rope.py:18-61``)."""
+    batch, tokens, dim = value.shape
+    head_dim = dim // heads
+    out = torch.empty((batch, tokens, dim), dtype=value.dtype, device=value.device)
+    if out.numel() == 0:
+        return out
+    if pe is None:
+        _lib.launch_rmsnorm_rope(value, out, norm.weight, norm.eps, 0.0, norm_width=dim)
+        return out
+    cos, sin = pe
+    if not (cos.dim() == 4 and cos.shape[1] == heads and cos.shape[2] == tokens and cos.shape[3] * 2 == head_dim
+            and cos.shape[0] in (1, batch) and cos.dtype == torch.float32 and cos.shape == sin.shape):
+        raise ValueError("RoPE tables must be fp32 (1 or batch, heads, tokens, head_dim / 2)")
+    if _fused_norm_rope_ok(dim, head_dim):
+        cos_tm, sin_tm = split_rope.token_major(cos), split_rope.token_major(sin)
+        _lib.launch_rmsnorm_rope(
+            value, out, norm.weight, norm.eps, 0.0, norm_width=dim, rope_kind=_lib.KX_ROPE_SPLIT,
+            cos=cos_tm, sin=sin_tm, table_ld=heads * head_dim // 2, table_hs=head_dim // 2,
+            tokens=tokens, table_batched=cos.shape[0] > 1, head_dim=head_dim,
+        )
+        return out
+    _lib.launch_rmsnorm_rope(value, out, norm.weight, norm.eps, 0.0, norm_width=dim)
+    return split_rope.rotate(out, cos, sin)
+
+
+def dense_kernel_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, *, heads: int,
+                           gate: torch.Tensor | None = None) -> torch.Tensor:
+    """The flash-attention kernel on flattened-head ``(batch, tokens, heads * dim)`` inputs;
+    keys and values may have their own token count (``attention.py:192-206``)."""
+    return _dense.batched_attention(query, key, value, heads=heads, gate=gate)
+
+
+def scaled_dot_product_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, *, heads: int,
+                                 dim_head: int, mask: torch.Tensor | None = None,
+                                 compile_attention: bool = True) -> torch.Tensor:
+    """Unmasked attention on flattened-head inputs (``attention.py:224-246``). Masked attention
+    is not built for MI355X and raises."""
+    del compile_attention
+    if mask is not None:
+        raise ValueError("masked attention is not built for MI355X")
+    if query.shape[-1] != heads * dim_head:
+        raise ValueError("query width must be heads * dim_head")
+    return _dense.batched_attention(query, key, value, heads=heads)
+
+
+def _cat_layers(layers):
+    """One fused layer whose output row blocks are ``layers`` in order, and views back into it."""
+    if all(isinstance(layer, Linear) for layer in layers):
+        weight = torch.cat([layer.weight for layer in layers], dim=0).contiguous()
+        has_bias = [layer.bias is not None for layer in layers]
+        bias = None
+        if any(has_bias):
+            bias = torch.cat([
+                layer.bias if layer.bias is not None else torch.zeros(layer.out_features, dtype=weight.dtype,
+                                                                      device=weight.device)
+                for layer in layers
+            ]).contiguous()
+        fused = Linear(weight, bias)
+        start = 0
+        for layer in layers:
+            stop = start + layer.out_features
+            layer.weight = weight[start:stop]
+            if layer.bias is not None:
+                layer.bias = bias[start:stop]
+            start = stop
+        return fused
+    if all(isinstance(layer, QuantizedLinear) for layer in layers):
+        first = layers[0]
+        if any((layer.bits, layer.group_size) != (first.bits, first.group_size) for layer in layers):
+            return None
+        words = torch.cat([layer.weight for layer in layers], dim=0).contiguous()
+        scales = torch.cat([layer.scales for layer in layers], dim=0).contiguous()
+        biases = torch.cat([layer.biases for layer in layers], dim=0).contiguous()
+        bias = None
+        if any(layer.bias is not None for layer in layers):
+            bias = torch.cat([
+                layer.bias.to(torch.bfloat16) if layer.bias is not None else
+                torch.zeros(layer.out_features, dtype=torch.bfloat16, device=words.device)
+                for layer in layers
+            ]).contiguous()
+        return QuantizedLinear(words, scales, biases, bias, group_size=first.group_size, bits=first.bits)
+    return None
+
+
+class Attention:
+    """Multi-head attention with Q/K RMSNorm, split RoPE and per-head gates
+    (``attention.py:249-371``). Weights are assigned after construction, as the reference's
+    loader does: ``to_q``/``to_k``/``to_v``/``to_out``/``to_gate_logits`` hold ``Linear`` or
+    ``QuantizedLinear`` layers and ``q_norm.weight``/``k_norm.weight`` the norm scales."""
+
+    def __init__(
+        self,
+        query_dim: int,
+        *,
+        heads: int = 8,
+        dim_head: int = 64,
+        context_dim: int | None = None,
+        rope_type: LTXRopeType = LTXRopeType.SPLIT,
+        norm_eps: float = 1e-6,
+        apply_gated_attention: bool = False,
+        compile_attention: bool = True,
+        dense_kernel: bool = True,
+    ) -> None:
+        if heads <= 0 or dim_head <= 0:
+            raise ValueError("attention heads and head dimension must be positive")
+        self.heads = heads
+        self.dim_head = dim_head
+        self.query_dim = query_dim
+        self.context_dim = query_dim if context_dim is None else context_dim
+        self.rope_type = rope_type
+        self.compile_attention = compile_attention
+        self.dense_kernel = dense_kernel
+        self.apply_gated_attention = apply_gated_attention
+        inner = heads * dim_head
+        self.q_norm = RMSNorm(inner, eps=norm_eps)
+        self.k_norm = RMSNorm(inner, eps=norm_eps)
+        self.to_q = self.to_k = self.to_v = self.to_out = None
+        self.to_gate_logits = None
+        self._qkv = None
+        self._kv = None
+
+    def fuse_projections(self, *, self_attention: bool = True) -> None:
+        """Concatenate Q/K/V (self-attention) or K/V (cross-attention on a context) into one
+        weight; the per-projection layers become views into it (no extra memory for dense
+        weights)."""
+        if self_attention:
+            self._qkv = _cat_layers([self.to_q, self.to_k, self.to_v])
+        else:
+            self._kv = _cat_layers([self.to_k, self.to_v])
+
+    def project(self, value: torch.Tensor, *, context: torch.Tensor | None = None,
+                pe=None, k_pe=None):
+        """Gate, normalized/rotated Q and K, and V, as the kernel reads them."""
+        if value.shape[-1] != self.query_dim:
+            raise ValueError(f"attention query expects width {self.query_dim}, got {value.shape[-1]}")
+        gate = None
+        if self.to_gate_logits is not None:
+            gate = self.to_gate_logits(value, activation="sigmoid2")
+        source = value if context is None else context
+        if source.shape[-1] != self.context_dim:
+            raise ValueError(f"attention context expects width {self.context_dim}, got {source.shape[-1]}")
+        inner = self.heads * self.dim_head
+        if context is None and self._qkv is not None:
+            qkv = self._qkv(value)
+            q_raw, k_raw, v = qkv[..., :inner], qkv[..., inner:2 * inner], qkv[..., 2 * inner:]
+        else:
+            q_raw = self.to_q(value)
+            if self._kv is not None:
+                kv = self._kv(source)
+                k_raw, v = kv[..., :inner], kv[..., inner:]
+            else:
+                k_raw, v = self.to_k(source), self.to_v(source)
+        q = norm_rope(q_raw, self.q_norm, pe, self.heads)
+        k = norm_rope(k_raw, self.k_norm, pe if k_pe is None else k_pe, self.heads) if pe is not None else \
+            norm_rope(k_raw, self.k_norm, None, self.heads)
+        return gate, q, k, v
+
+    def attend(self, value: torch.Tensor, *, context: torch.Tensor | None = None,
+               mask: torch.Tensor | None = None, pe=None, k_pe=None) -> torch.Tensor:
+        """Everything before the output projection (gated attention output ``(B, T, inner)``)."""
+        if mask is not None:
+            raise ValueError("masked attention is not built for MI355X")
+        gate, q, k, v = self.project(value, context=context, pe=pe, k_pe=k_pe)
+        return _dense.batched_attention(q, k, v, heads=self.heads, gate=gate)
+
+    def __call__(self, value: torch.Tensor, *, context: torch.Tensor | None = None,
+                 mask: torch.Tensor | None = None, pe=None, k_pe=None, sparse=None,
+                 residual: torch.Tensor | None = None, gate: torch.Tensor | None = None) -> torch.Tensor:
+        """``to_out(attention)``; with ``residual``/``gate`` the block's gated residual
+        ``residual + gate * to_out(attention)`` is formed in the output GEMM's epilogue."""
+        if sparse is not None:
+            raise ValueError("sparse (Sol-Attn) attention is not built for MI355X")
+        attended = self.attend(value, context=context, mask=mask, pe=pe, k_pe=k_pe)
+        return self.to_out(attended, residual=residual, gate=gate)
+
+
+__all__ = [
+    "Attention",
+    "Linear",
+    "RMSNorm",
+    "dense_kernel_attention",
+    "norm_rope",
+    "rms_norm",
+    "scaled_dot_product_attention",
+]

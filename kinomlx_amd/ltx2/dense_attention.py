@@ -1,0 +1,111 @@
+"""Dense (non-causal) flash attention for unmasked attention calls, on gfx950 MFMA.
+
+Mirror of ``kinomlx/models/ltx2/kernels/dense_attention.py`` (``HEAD_DIMS``, ``applies``,
+``dense_attention``). Queries are token-major ``(query_tokens, heads * dim)`` and keys/values
+``(key_tokens, heads * dim)`` — the layout of the projections, so neither side needs a head
+transpose and self- and cross-attention are the same call. Scores and accumulation are FP32
+(bf16 MFMA inputs); the output has the queries' shape and dtype.
+
+Differences from the M1 kernel, by design: inputs stay bf16 (no FP16 saturation step: MI355X
+multiplies bf16 natively), and 64-wide heads take the kernel at any token count (the
+reference's 512-token floor was an M1 speed heuristic against MLX's SDPA).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+
+HEAD_DIMS = (64, 128)
+_SUPPORTED_DTYPES = (torch.bfloat16,)
+
+
+def applies(query: torch.Tensor, key: torch.Tensor, *, heads: int) -> bool:
+    """Whether flattened-head ``(batch, tokens, heads * dim)`` queries and keys take the kernel
+    (contract of ``dense_attention.py:87-104``)."""
+    return (
+        query.dim() == 3
+        and key.dim() == 3
+        and query.dtype in _SUPPORTED_DTYPES
+        and key.dtype == query.dtype
+        and query.shape[0] == key.shape[0]
+        and query.shape[-1] == key.shape[-1]
+        and heads > 0
+        and query.shape[-1] in tuple(heads * d for d in HEAD_DIMS)
+        and query.shape[1] > 0
+        and key.shape[1] > 0
+        and query.is_cuda
+        and _lib.available()
+    )
+
+
+def _attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, heads: int, batch: int,
+               tq: int, tk: int, dim: int, gate: torch.Tensor | None, scale: float | None) -> torch.Tensor:
+    out = torch.empty((batch, tq, heads * dim), dtype=q.dtype, device=q.device)
+    if gate is not None:
+        if gate.dtype != torch.bfloat16 or tuple(gate.shape[-1:]) != (heads,):
+            raise ValueError(f"attention gate must be bf16 (..., {heads})")
+        gate = gate.reshape(batch * tq, heads)
+    _lib.launch_attention(
+        q, k, v, out, batch=batch, tq=tq, tk=tk, heads=heads, head_dim=dim,
+        scale=dim ** -0.5 if scale is None else scale, gate=gate,
+    )
+    return out
+
+
+def _check(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, heads: int, width: int) -> int:
+    if q.dtype not in (torch.float16, torch.bfloat16) or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError(
+            f"dense attention needs float16 or bfloat16 q, k and v, got {q.dtype}, {k.dtype}, {v.dtype}"
+        )
+    if q.dtype not in _SUPPORTED_DTYPES:
+        raise ValueError("dense attention on MI355X computes bfloat16 q, k and v, got float16")
+    dim = width // heads if heads > 0 and width % heads == 0 else 0
+    return dim
+
+
+def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, heads: int,
+                    gate: torch.Tensor | None = None) -> torch.Tensor:
+    """Dense attention of ``(query_tokens, heads * dim)`` queries over ``(key_tokens, ...)``
+    (``dense_attention.py:106-153``). ``dim`` is 64 or 128. ``gate`` (optional, bf16
+    ``(query_tokens, heads)``) multiplies each head's output before the one rounding."""
+    width = q.shape[1] if q.dim() == 2 else 0
+    dim = _check(q, k, v, heads, width)
+    if (
+        dim not in HEAD_DIMS
+        or k.dim() != 2
+        or k.shape[1] != width
+        or v.shape != k.shape
+        or q.shape[0] == 0
+        or k.shape[0] == 0
+    ):
+        raise ValueError(
+            f"dense attention needs (query_tokens, {heads} * 64 or 128) queries and matching "
+            f"(key_tokens, width) keys and values, got {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}"
+        )
+    out = _attention(q, k, v, heads=heads, batch=1, tq=q.shape[0], tk=k.shape[0], dim=dim,
+                     gate=gate, scale=None)
+    return out[0]
+
+
+def batched_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, heads: int,
+                      gate: torch.Tensor | None = None, scale: float | None = None) -> torch.Tensor:
+    """``(batch, tokens, heads * dim)`` form of ``dense_attention``; q/k/v may be strided row
+    views (e.g. column slices of a fused QKV projection)."""
+    if q.dim() != 3 or k.dim() != 3 or v.shape != k.shape or q.shape[0] != k.shape[0]:
+        raise ValueError("batched attention needs (batch, tokens, heads * dim) q, k and v")
+    width = q.shape[-1]
+    dim = _check(q, k, v, heads, width)
+    if dim not in HEAD_DIMS or k.shape[-1] != width:
+        raise ValueError(f"attention head width must be 64 or 128, got {width} / {heads}")
+    batch, tq, tk = q.shape[0], q.shape[1], k.shape[1]
+    if tk == 0:
+        raise ValueError("attention needs at least one key")
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if t.stride(-1) != 1 or (batch > 1 and t.stride(0) != t.shape[1] * t.stride(1)):
+            raise ValueError(f"attention {name} must have contiguous rows, evenly strided over the batch")
+    return _attention(q, k, v, heads=heads, batch=batch, tq=tq, tk=tk, dim=dim, gate=gate, scale=scale)
+
+
+__all__ = ["HEAD_DIMS", "applies", "batched_attention", "dense_attention"]

@@ -1,0 +1,202 @@
+"""The LTX-2 DiT block's video branch on MI355X.
+
+Mirror of ``kinomlx/models/ltx2/transformer/transformer.py``: the modulation helpers
+(``adaln``, ``gated_residual``, ``modulate``, ``gate``; the reference's private ``_adaln`` ...
+and their ``mx.compile``d forms, ``:16-45``), ``TransformerConfig``, ``TransformerArgs`` and
+``BasicAVTransformerBlock`` with its video branch (``:225-276,373-392``) and text cross-attention
+(``:201-223``).
+
+Kernel schedule of one block (B=1, T video tokens, Tc text tokens):
+  AdaLN(x) -> [QKV GEMM, gate GEMM (2*sigmoid)] -> Q/K norm+RoPE -> flash attention (gated)
+  -> out GEMM (+ x + g0 * .) ; AdaLN(x), modulate(ctx) -> [Q GEMM, gate GEMM, KV GEMM] -> Q/K norm
+  -> attention -> out GEMM (+ x + g8 * .) ; AdaLN(x) -> up GEMM (GELU) -> down GEMM (+ x + g5 * .)
+Every residual add rides in a GEMM epilogue; every intermediate is bf16, every reduction and
+epilogue FP32. The audio stream, A/V cross-attention, masks and sparse attention are not built.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, replace
+
+import torch
+
+from .. import _lib
+from .attention import Attention, rms_norm
+from .feed_forward import FeedForward
+from .rope import LTXRopeType
+
+
+def _mod32(value: torch.Tensor) -> torch.Tensor:
+    v = value.float()
+    return v if (v.stride(-1) == 1 and v.data_ptr() % 16 == 0) else v.contiguous()
+
+
+def adaln(value: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor, eps: float) -> torch.Tensor:
+    """``rms_norm(x) * (1 + scale) + shift`` in one FP32 pass (``transformer.py:16-23``).
+    ``scale``/``shift`` broadcast as ``(D,)``, ``(B, 1, D)`` or ``(B, T, D)``."""
+    if value.dtype != torch.bfloat16:
+        raise ValueError(f"adaln takes bfloat16 activations on MI355X, got {value.dtype}")
+    out = torch.empty(value.shape, dtype=value.dtype, device=value.device)
+    if value.numel():
+        _lib.launch_adaln_norm(value, out, _mod32(shift), _mod32(scale), eps, _lib.KX_NORM_RMS)
+    return out
+
+
+def layer_norm_modulate(value: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor,
+                        eps: float = 1e-6) -> torch.Tensor:
+    """``layer_norm(x) * (1 + scale) + shift`` in one FP32 pass (FLUX.2 ``normalized``,
+    ``kinomlx/models/flux2/transformer.py:56-57``)."""
+    if value.dtype != torch.bfloat16:
+        raise ValueError(f"layer_norm_modulate takes bfloat16 activations on MI355X, got {value.dtype}")
+    out = torch.empty(value.shape, dtype=value.dtype, device=value.device)
+    if value.numel():
+        _lib.launch_adaln_norm(value, out, _mod32(shift), _mod32(scale), eps, _lib.KX_NORM_LAYER)
+    return out
+
+
+def gated_residual(value: torch.Tensor, residual: torch.Tensor, gate_value: torch.Tensor) -> torch.Tensor:
+    """``x + r * gate`` (``transformer.py:26-30``)."""
+    out = torch.empty(value.shape, dtype=value.dtype, device=value.device)
+    if value.numel():
+        _lib.launch_gated_residual(value, residual, out, _mod32(gate_value))
+    return out
+
+
+def modulate(value: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor) -> torch.Tensor:
+    """``x * (1 + scale) + shift`` (``transformer.py:33-34``)."""
+    out = torch.empty(value.shape, dtype=value.dtype, device=value.device)
+    if value.numel():
+        _lib.launch_modulate(value, out, _mod32(shift), _mod32(scale))
+    return out
+
+
+def gate(value: torch.Tensor, gate_value: torch.Tensor) -> torch.Tensor:
+    """``x * gate`` (``transformer.py:37-38``)."""
+    out = torch.empty(value.shape, dtype=value.dtype, device=value.device)
+    if value.numel():
+        _lib.launch_gated_residual(None, value, out, _mod32(gate_value))
+    return out
+
+
+# The reference's private names and their compiled forms map to the same fused kernels.
+_adaln = _compiled_adaln = adaln
+_gated_residual = _compiled_gated_residual = gated_residual
+_modulate = _compiled_modulate = modulate
+_gate = _compiled_gate = gate
+
+
+@dataclass(frozen=True)
+class TransformerConfig:
+    """Shape and feature selection for one transformer stream (``transformer.py:52-63``)."""
+
+    dim: int
+    heads: int
+    head_dim: int
+    context_dim: int
+    ff_bias: bool = True
+    apply_gated_attention: bool = True
+    compile_attention: bool = True
+    dense_attention_kernel: bool = True
+
+
+@dataclass(frozen=True)
+class TransformerArgs:
+    """Prepared inputs carried through every block (``transformer.py:66-82``)."""
+
+    x: torch.Tensor
+    context: torch.Tensor
+    timesteps: torch.Tensor
+    positional_embeddings: tuple[torch.Tensor, torch.Tensor]
+    context_mask: torch.Tensor | None = None
+    self_attention_mask: torch.Tensor | None = None
+    embedded_timestep: torch.Tensor | None = None
+    prompt_timestep: torch.Tensor | None = None
+    cross_positional_embeddings: tuple[torch.Tensor, torch.Tensor] | None = None
+    cross_scale_shift_timestep: torch.Tensor | None = None
+    cross_gate_timestep: torch.Tensor | None = None
+    enabled: bool = True
+    sparse_attention: object | None = None
+
+
+class BasicAVTransformerBlock:
+    """One LTX-2 block, video branch (``transformer.py:85-421``). Weights are assigned after
+    construction: ``attn1``/``attn2`` (``Attention``), ``ff`` (``FeedForward``),
+    ``scale_shift_table`` ``(9, D)`` and ``prompt_scale_shift_table`` ``(2, D)``."""
+
+    def __init__(self, idx: int, *, video_config: TransformerConfig, audio_config: TransformerConfig | None = None,
+                 rope_type: LTXRopeType = LTXRopeType.SPLIT, norm_eps: float = 1e-6) -> None:
+        self.idx = idx
+        self.norm_eps = norm_eps
+        self.video_config = video_config
+        self.audio_config = audio_config
+        backend = {
+            "compile_attention": video_config.compile_attention,
+            "dense_kernel": video_config.dense_attention_kernel,
+        }
+        self.attn1 = Attention(video_config.dim, heads=video_config.heads, dim_head=video_config.head_dim,
+                               norm_eps=norm_eps, rope_type=rope_type,
+                               apply_gated_attention=video_config.apply_gated_attention, **backend)
+        self.attn2 = Attention(video_config.dim, context_dim=video_config.context_dim, heads=video_config.heads,
+                               dim_head=video_config.head_dim, norm_eps=norm_eps, rope_type=rope_type,
+                               apply_gated_attention=video_config.apply_gated_attention, **backend)
+        self.ff = FeedForward(video_config.dim, bias=video_config.ff_bias)
+        self.scale_shift_table: torch.Tensor | None = None
+        self.prompt_scale_shift_table: torch.Tensor | None = None
+
+    def fuse_projections(self) -> None:
+        """Fuse Q/K/V of the self-attention and K/V of the text cross-attention."""
+        self.attn1.fuse_projections(self_attention=True)
+        self.attn2.fuse_projections(self_attention=False)
+
+    @staticmethod
+    def _ada_values(table: torch.Tensor, timestep: torch.Tensor, start: int, stop: int) -> tuple[torch.Tensor, ...]:
+        """``table[start:stop] + timestep[:, :, start:stop]`` split per row (``:179-186``)."""
+        values = (table[start:stop][None, None].float() + timestep[:, :, start:stop, :].float()).contiguous()
+        return tuple(values[:, :, i, :] for i in range(stop - start))
+
+    def _text_cross_attention(self, value: torch.Tensor, args: TransformerArgs, ada: torch.Tensor) -> torch.Tensor:
+        """``x + gate(attn2(adaln(x), modulate(context)))`` with the residual in the output
+        GEMM (``transformer.py:201-223`` and ``:266-276``)."""
+        prompt = self.prompt_scale_shift_table[None, None].float()
+        if args.prompt_timestep is not None:
+            prompt = prompt + args.prompt_timestep.float()
+        prompt = prompt.contiguous()
+        query = adaln(value, ada[:, :, 7], ada[:, :, 6], self.norm_eps)
+        context = modulate(args.context, prompt[:, :, 1], prompt[:, :, 0])
+        if args.context_mask is not None:
+            raise ValueError("masked text cross-attention is not built for MI355X")
+        return self.attn2(query, context=context, residual=value, gate=ada[:, :, 8])
+
+    def __call__(self, video: TransformerArgs | None, audio: TransformerArgs | None = None):
+        if audio is not None:
+            raise ValueError("the audio stream and A/V attention are not built for MI355X")
+        if video is None or not video.enabled or video.x.numel() == 0:
+            return video, audio
+        if video.self_attention_mask is not None:
+            raise ValueError("masked self-attention is not built for MI355X")
+        if video.sparse_attention is not None:
+            raise ValueError("sparse (Sol-Attn) attention is not built for MI355X")
+        x = video.x
+        ada = (self.scale_shift_table[None, None].float() + video.timesteps.float()).contiguous()
+
+        normalized = adaln(x, ada[:, :, 1], ada[:, :, 0], self.norm_eps)
+        x = self.attn1(normalized, pe=video.positional_embeddings, residual=x, gate=ada[:, :, 2])
+
+        x = self._text_cross_attention(x, video, ada)
+
+        normalized = adaln(x, ada[:, :, 4], ada[:, :, 3], self.norm_eps)
+        x = self.ff(normalized, residual=x, gate=ada[:, :, 5])
+        return replace(video, x=x), audio
+
+
+__all__ = [
+    "BasicAVTransformerBlock",
+    "TransformerArgs",
+    "TransformerConfig",
+    "adaln",
+    "gate",
+    "gated_residual",
+    "layer_norm_modulate",
+    "modulate",
+    "rms_norm",
+]

@@ -1,0 +1,309 @@
+"""Seeded synthetic DiT-block workloads for the five benchmark configurations.
+
+Every tensor is drawn from its own ``torch.Generator`` seeded by (seed, name), in float32 on the
+CPU, then rounded once to bf16 where the block stores it in bf16. Weights ~ N(0, 0.02); hidden
+states, context and the conditioning vector ~ N(0, 1). Modulation follows the reference's AdaLN
+path: a seeded N(0, 0.02) linear layer maps a 1024-d conditioning vector to the modulation rows
+(LTX ``AdaLayerNormSingle`` output ``(1, 1, 9, D)`` in bf16 plus an fp32 ``scale_shift_table``,
+``kinomlx/models/ltx2/transformer/transformer.py:179-186``; FLUX ``Modulation``,
+``kinomlx/models/flux2/transformer.py:223-229``). There are no checkpoints: the numbers measure
+kernels, not a trained model.
+
+``params`` dicts map parameter names to CPU tensors; ``build_*`` functions turn them into the
+MI355X block objects on a device.
+"""
+
+from __future__ import annotations
+
+import hashlib
+from dataclasses import dataclass
+
+import torch
+
+COND_DIM = 1024
+
+
+@dataclass(frozen=True)
+class LTXSpec:
+    """LTX-2-like video block: ``grid`` = (t, h, w) latent tokens, text via cross-attention."""
+
+    grid: tuple[int, int, int]
+    text_tokens: int
+    dim: int = 4096
+    heads: int = 32
+    head_dim: int = 128
+    ff_mult: int = 4
+    bits: int | None = None  # affine-quantized linears (4 or 8) when set
+    group_size: int = 64
+
+    @property
+    def tokens(self) -> int:
+        return self.grid[0] * self.grid[1] * self.grid[2]
+
+
+@dataclass(frozen=True)
+class FluxSpec:
+    """FLUX.2-like (or config-1) image block: ``grid`` = (h, w) image tokens joined with text."""
+
+    grid: tuple[int, int]
+    text_tokens: int
+    dim: int
+    heads: int
+    head_dim: int
+    ff_hidden: int
+    ff: str  # "swiglu" (FLUX.2) or "gelu" (config 1, LTX FeedForward with biases)
+    single: bool = False  # also run one single-stream block (config 2)
+
+    @property
+    def image_tokens(self) -> int:
+        return self.grid[0] * self.grid[1]
+
+
+CONFIGS = {
+    1: FluxSpec(grid=(32, 32), text_tokens=128, dim=1024, heads=16, head_dim=64, ff_hidden=4096, ff="gelu"),
+    2: FluxSpec(grid=(64, 64), text_tokens=512, dim=4096, heads=32, head_dim=128, ff_hidden=12288, ff="swiglu",
+                single=True),
+    3: LTXSpec(grid=(16, 18, 32), text_tokens=256),
+    4: LTXSpec(grid=(16, 18, 32), text_tokens=256, bits=4),
+    5: LTXSpec(grid=(31, 22, 40), text_tokens=256, bits=4),
+}
+
+
+def _generator(seed: int, name: str) -> torch.Generator:
+    digest = hashlib.sha256(f"{seed}:{name}".encode()).digest()
+    return torch.Generator().manual_seed(int.from_bytes(digest[:8], "little") & ((1 << 63) - 1))
+
+
+def normal(seed: int, name: str, shape, std: float = 1.0, mean: float = 0.0) -> torch.Tensor:
+    """float32 N(mean, std^2) of ``shape`` from the (seed, name) stream."""
+    return torch.randn(tuple(shape), generator=_generator(seed, name), dtype=torch.float32) * std + mean
+
+
+def bf16(t: torch.Tensor) -> torch.Tensor:
+    return t.to(torch.bfloat16)
+
+
+# ---- LTX-2 -------------------------------------------------------------------------------------
+
+
+def ltx_positions(grid: tuple[int, int, int]) -> torch.Tensor:
+    """``(1, 3, T, 2)`` integer latent-grid bounds ``[i, i + 1]`` per axis, t-major token order."""
+    t, h, w = grid
+    tt, hh, ww = torch.meshgrid(torch.arange(t), torch.arange(h), torch.arange(w), indexing="ij")
+    start = torch.stack([tt.reshape(-1), hh.reshape(-1), ww.reshape(-1)]).float()
+    return torch.stack([start, start + 1.0], dim=-1)[None]
+
+
+def _ltx_attention_params(p: dict, seed: int, prefix: str, dim: int, heads: int) -> None:
+    for name in ("to_q", "to_k", "to_v", "to_out"):
+        p[f"{prefix}.{name}.weight"] = bf16(normal(seed, f"{prefix}.{name}.weight", (dim, dim), 0.02))
+        p[f"{prefix}.{name}.bias"] = bf16(normal(seed, f"{prefix}.{name}.bias", (dim,), 0.02))
+    p[f"{prefix}.to_gate_logits.weight"] = bf16(normal(seed, f"{prefix}.to_gate_logits.weight", (heads, dim), 0.02))
+    p[f"{prefix}.to_gate_logits.bias"] = bf16(normal(seed, f"{prefix}.to_gate_logits.bias", (heads,), 0.02))
+    for name in ("q_norm", "k_norm"):
+        p[f"{prefix}.{name}.weight"] = bf16(normal(seed, f"{prefix}.{name}.weight", (dim,), 0.02, 1.0))
+
+
+def ltx_params(spec: LTXSpec, seed: int = 0) -> dict[str, torch.Tensor]:
+    """Dense bf16 parameters of one LTX video block plus its per-step modulation rows."""
+    d = spec.dim
+    p: dict[str, torch.Tensor] = {}
+    _ltx_attention_params(p, seed, "attn1", d, spec.heads)
+    _ltx_attention_params(p, seed, "attn2", d, spec.heads)
+    f = d * spec.ff_mult
+    p["ff.proj_in.weight"] = bf16(normal(seed, "ff.proj_in.weight", (f, d), 0.02))
+    p["ff.proj_in.bias"] = bf16(normal(seed, "ff.proj_in.bias", (f,), 0.02))
+    p["ff.proj_out.weight"] = bf16(normal(seed, "ff.proj_out.weight", (d, f), 0.02))
+    p["ff.proj_out.bias"] = bf16(normal(seed, "ff.proj_out.bias", (d,), 0.02))
+    p["scale_shift_table"] = normal(seed, "scale_shift_table", (9, d), 0.02)
+    p["prompt_scale_shift_table"] = normal(seed, "prompt_scale_shift_table", (2, d), 0.02)
+    cond = normal(seed, "cond", (1, COND_DIM))
+    w_mod = bf16(normal(seed, "adaln.linear.weight", (9 * d, COND_DIM), 0.02)).float()
+    p["timesteps"] = bf16((cond @ w_mod.T).reshape(1, 1, 9, d))
+    return p
+
+
+QUANTIZED_LTX_LINEARS = tuple(
+    f"{a}.{n}" for a in ("attn1", "attn2") for n in ("to_q", "to_k", "to_v", "to_out", "to_gate_logits")
+) + ("ff.proj_in", "ff.proj_out")
+
+
+def quantize_ltx_params(p: dict[str, torch.Tensor], bits: int, group_size: int = 64) -> dict[str, torch.Tensor]:
+    """Replace every block linear's weight by its packed affine form (``.wq/.scales/.biases``)."""
+    from .kernels.quantized import quantize
+
+    q = dict(p)
+    for name in QUANTIZED_LTX_LINEARS:
+        words, scales, biases = quantize(q.pop(f"{name}.weight"), group_size, bits)
+        q[f"{name}.wq"] = words
+        q[f"{name}.scales"] = scales
+        q[f"{name}.biases"] = biases
+        q[f"{name}.group_size"] = torch.tensor(group_size)
+        q[f"{name}.bits"] = torch.tensor(bits)
+    return q
+
+
+def ltx_inputs(spec: LTXSpec, seed: int = 0) -> dict[str, torch.Tensor]:
+    """Hidden states ``(1, T, D)``, context ``(1, Tc, D)`` (bf16) and RoPE positions."""
+    return {
+        "x": bf16(normal(seed, "x", (1, spec.tokens, spec.dim))),
+        "context": bf16(normal(seed, "context", (1, spec.text_tokens, spec.dim))),
+        "positions": ltx_positions(spec.grid),
+    }
+
+
+def _layer(p: dict, name: str, device):
+    from .kernels.quantized import QuantizedLinear
+    from .ltx2.attention import Linear
+
+    bias = p.get(f"{name}.bias")
+    bias = None if bias is None else bias.to(device)
+    if f"{name}.wq" in p:
+        return QuantizedLinear(
+            p[f"{name}.wq"].to(device), p[f"{name}.scales"].to(device), p[f"{name}.biases"].to(device), bias,
+            group_size=int(p[f"{name}.group_size"]), bits=int(p[f"{name}.bits"]),
+        )
+    return Linear(p[f"{name}.weight"].to(device), bias)
+
+
+def build_ltx_block(spec: LTXSpec, p: dict[str, torch.Tensor], device, *, fuse: bool = True):
+    """The MI355X ``BasicAVTransformerBlock`` holding ``p``'s weights on ``device``."""
+    from .ltx2.transformer import BasicAVTransformerBlock, TransformerConfig
+
+    cfg = TransformerConfig(dim=spec.dim, heads=spec.heads, head_dim=spec.head_dim, context_dim=spec.dim)
+    block = BasicAVTransformerBlock(0, video_config=cfg)
+    for a in ("attn1", "attn2"):
+        attn = getattr(block, a)
+        for n in ("to_q", "to_k", "to_v", "to_out", "to_gate_logits"):
+            setattr(attn, n, _layer(p, f"{a}.{n}", device))
+        attn.q_norm.weight = p[f"{a}.q_norm.weight"].to(device)
+        attn.k_norm.weight = p[f"{a}.k_norm.weight"].to(device)
+    block.ff.project_in.proj = _layer(p, "ff.proj_in", device)
+    block.ff.project_out = _layer(p, "ff.proj_out", device)
+    block.scale_shift_table = p["scale_shift_table"].to(device)
+    block.prompt_scale_shift_table = p["prompt_scale_shift_table"].to(device)
+    if fuse:
+        block.fuse_projections()
+    return block
+
+
+# ---- FLUX.2 / config 1 ---------------------------------------------------------------------------
+
+
+def flux_ids(spec: FluxSpec) -> torch.Tensor:
+    """``(1, Tt + Ti, 4)`` FLUX.2 ids: text ``(0, 0, 0, l)`` then image ``(0, h, w, 0)``."""
+    h, w = spec.grid
+    text = torch.zeros(spec.text_tokens, 4)
+    text[:, 3] = torch.arange(spec.text_tokens, dtype=torch.float32)
+    hh, ww = torch.meshgrid(torch.arange(h), torch.arange(w), indexing="ij")
+    image = torch.zeros(h * w, 4)
+    image[:, 1] = hh.reshape(-1).float()
+    image[:, 2] = ww.reshape(-1).float()
+    return torch.cat([text, image])[None]
+
+
+def config1_positions(spec: FluxSpec) -> torch.Tensor:
+    """``(1, Tt + Ti, 2)`` (h, w) positions: text at (0, 0), image on its grid."""
+    h, w = spec.grid
+    hh, ww = torch.meshgrid(torch.arange(h), torch.arange(w), indexing="ij")
+    image = torch.stack([hh.reshape(-1), ww.reshape(-1)], dim=-1).float()
+    return torch.cat([torch.zeros(spec.text_tokens, 2), image])[None]
+
+
+def axis_rope_tables(positions: torch.Tensor, *, theta: float, axes_dims: tuple[int, ...]):
+    """Per-axis adjacent-pair tables ``(B, T, Dh)`` (Krea ``Krea2RotaryEmbedding``,
+    ``kinomlx/models/krea2/transformer/model.py:49-66``), computed in float32 on the CPU."""
+    parts = []
+    for axis, dims in enumerate(axes_dims):
+        freqs = 1.0 / (torch.tensor(theta, dtype=torch.float32) ** (torch.arange(0, dims, 2, dtype=torch.float32) / dims))
+        angles = positions[..., axis, None].float() * freqs
+        parts.append(torch.repeat_interleave(angles, 2, dim=-1))
+    combined = torch.cat(parts, dim=-1)
+    return torch.cos(combined), torch.sin(combined)
+
+
+def flux_params(spec: FluxSpec, seed: int = 0) -> dict[str, torch.Tensor]:
+    d, dh = spec.dim, spec.head_dim
+    p: dict[str, torch.Tensor] = {}
+    for name in ("to_q", "to_k", "to_v", "add_q_proj", "add_k_proj", "add_v_proj", "to_out", "to_add_out"):
+        p[f"attn.{name}.weight"] = bf16(normal(seed, f"attn.{name}.weight", (d, d), 0.02))
+    for name in ("norm_q", "norm_k", "norm_added_q", "norm_added_k"):
+        p[f"attn.{name}.weight"] = bf16(normal(seed, f"attn.{name}.weight", (dh,), 0.02, 1.0))
+    f = spec.ff_hidden
+    for prefix in ("ff", "ff_context"):
+        if spec.ff == "swiglu":
+            p[f"{prefix}.linear_in.weight"] = bf16(normal(seed, f"{prefix}.linear_in.weight", (2 * f, d), 0.02))
+            p[f"{prefix}.linear_out.weight"] = bf16(normal(seed, f"{prefix}.linear_out.weight", (d, f), 0.02))
+        else:
+            p[f"{prefix}.proj_in.weight"] = bf16(normal(seed, f"{prefix}.proj_in.weight", (f, d), 0.02))
+            p[f"{prefix}.proj_in.bias"] = bf16(normal(seed, f"{prefix}.proj_in.bias", (f,), 0.02))
+            p[f"{prefix}.proj_out.weight"] = bf16(normal(seed, f"{prefix}.proj_out.weight", (d, f), 0.02))
+            p[f"{prefix}.proj_out.bias"] = bf16(normal(seed, f"{prefix}.proj_out.bias", (d,), 0.02))
+    cond = normal(seed, "cond", (1, COND_DIM))
+    for stream in ("image_mod", "text_mod"):
+        w = bf16(normal(seed, f"{stream}.linear.weight", (6 * d, COND_DIM), 0.02)).float()
+        p[stream] = bf16((cond @ w.T).reshape(6, d))
+    if spec.single:
+        p["single.attn.to_qkv_mlp_proj.weight"] = bf16(
+            normal(seed, "single.attn.to_qkv_mlp_proj.weight", (3 * d + 2 * f, d), 0.02))
+        p["single.attn.to_out.weight"] = bf16(normal(seed, "single.attn.to_out.weight", (d, d + f), 0.02))
+        for name in ("norm_q", "norm_k"):
+            p[f"single.attn.{name}.weight"] = bf16(normal(seed, f"single.attn.{name}.weight", (dh,), 0.02, 1.0))
+        w = bf16(normal(seed, "single_mod.linear.weight", (3 * d, COND_DIM), 0.02)).float()
+        p["single_mod"] = bf16((cond @ w.T).reshape(3, d))
+    return p
+
+
+def flux_inputs(spec: FluxSpec, seed: int = 0) -> dict[str, torch.Tensor]:
+    return {
+        "image": bf16(normal(seed, "image", (1, spec.image_tokens, spec.dim))),
+        "text": bf16(normal(seed, "text", (1, spec.text_tokens, spec.dim))),
+    }
+
+
+def flux_rope(spec: FluxSpec) -> tuple[torch.Tensor, torch.Tensor]:
+    """``(T, Dh)`` fp32 adjacent-pair tables for the joint [text, image] sequence."""
+    if spec.ff == "swiglu":
+        ids = flux_ids(spec)
+        frequency = 2000.0 ** (-torch.arange(0, 32, 2, dtype=torch.float32) / 32)
+        angles = (ids[..., None] * frequency).reshape(*ids.shape[:-1], 64)
+        angles = torch.repeat_interleave(angles, 2, dim=-1)
+        return torch.cos(angles)[0], torch.sin(angles)[0]
+    half = spec.head_dim // 2
+    cos, sin = axis_rope_tables(config1_positions(spec), theta=10000.0, axes_dims=(half, half))
+    return cos[0], sin[0]
+
+
+def flop_count(spec) -> dict[str, float]:
+    """Algorithmic work of one block: GEMM ``2MNK``, attention ``4 H Tq Tk Dh``."""
+    if isinstance(spec, LTXSpec):
+        t, tc, d, h, dh, f = spec.tokens, spec.text_tokens, spec.dim, spec.heads, spec.head_dim, spec.dim * spec.ff_mult
+        gemm = 2.0 * t * d * (4 * d + h) + 2.0 * t * d * (2 * d + h) + 2.0 * tc * d * 2 * d + 2.0 * 2 * t * d * f
+        attn = 4.0 * h * dh * (t * t + t * tc)
+        return {"gemm": gemm, "attention": attn, "total": gemm + attn}
+    ti, tt, d, h, dh, f = spec.image_tokens, spec.text_tokens, spec.dim, spec.heads, spec.head_dim, spec.ff_hidden
+    ff_in = 2 * f if spec.ff == "swiglu" else f
+    gemm = 2.0 * (ti + tt) * d * (4 * d) + 2.0 * (ti + tt) * d * (ff_in + f)
+    t = ti + tt
+    attn = 4.0 * h * dh * t * t
+    if spec.single:
+        gemm += 2.0 * t * d * (3 * d + 2 * f) + 2.0 * t * (d + f) * d
+        attn *= 2
+    return {"gemm": gemm, "attention": attn, "total": gemm + attn}
+
+
+__all__ = [
+    "CONFIGS",
+    "FluxSpec",
+    "LTXSpec",
+    "build_ltx_block",
+    "flop_count",
+    "flux_inputs",
+    "flux_params",
+    "flux_rope",
+    "ltx_inputs",
+    "ltx_params",
+    "ltx_positions",
+    "normal",
+    "quantize_ltx_params",
+]

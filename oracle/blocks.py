@@ -1,0 +1,202 @@
+"""Block-level CPU restatements (test infrastructure only): the LTX-2 video block, the FLUX.2
+double/single blocks and this build's config-1 double-stream block, all in FP32.
+
+Parameters are dicts of float32 numpy arrays whose values bf16 represents exactly (the same
+values the GPU path receives as bf16). Batch is 1 and tokens are the leading axis.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from .ops import (
+    F32,
+    adaln,
+    attention,
+    gate,
+    gated_residual,
+    gelu_approx,
+    linear,
+    modulate,
+    normalized,
+    pair_rope,
+    quantized_linear,
+    rms_norm,
+    split_rope,
+    swiglu,
+)
+
+__all__ = [
+    "config1_double_block",
+    "flux_double_block",
+    "flux_single_block",
+    "ltx_attention",
+    "ltx_feed_forward",
+    "ltx_video_block",
+    "sigmoid",
+]
+
+
+def sigmoid(value) -> np.ndarray:
+    x = np.asarray(value, dtype=F32)
+    with np.errstate(over="ignore"):
+        return (F32(1.0) / (F32(1.0) + np.exp(-x))).astype(F32)
+
+
+def _lin(params: dict, name: str, value: np.ndarray) -> np.ndarray:
+    """One linear layer, dense or affine-quantized, by the parameter names present."""
+    bias = params.get(f"{name}.bias")
+    if f"{name}.wq" in params:
+        return quantized_linear(
+            value,
+            params[f"{name}.wq"],
+            params[f"{name}.scales"],
+            params[f"{name}.biases"],
+            bias,
+            group_size=int(params[f"{name}.group_size"]),
+            bits=int(params[f"{name}.bits"]),
+        )
+    return linear(value, params[f"{name}.weight"], bias)
+
+
+def ltx_attention(params: dict, prefix: str, value, *, heads: int, context=None, pe=None, eps=1e-6):
+    """LTX ``Attention.__call__`` without mask or sparse routing
+    (``kinomlx/models/ltx2/transformer/attention.py:291-371``): gate logits ``2*sigmoid``,
+    full-width weighted RMSNorm on Q and K, split RoPE, SDPA, per-head gate, output projection."""
+    x = np.asarray(value, dtype=F32)
+    source = x if context is None else np.asarray(context, dtype=F32)
+    head_gate = None
+    if f"{prefix}.to_gate_logits.weight" in params or f"{prefix}.to_gate_logits.wq" in params:
+        head_gate = F32(2.0) * sigmoid(_lin(params, f"{prefix}.to_gate_logits", x))
+    v = _lin(params, f"{prefix}.to_v", source)
+    q = rms_norm(_lin(params, f"{prefix}.to_q", x), params[f"{prefix}.q_norm.weight"], eps)
+    k = rms_norm(_lin(params, f"{prefix}.to_k", source), params[f"{prefix}.k_norm.weight"], eps)
+    if pe is not None:
+        cos, sin = pe
+        q = split_rope(q[None], cos, sin)[0]
+        k = split_rope(k[None], cos, sin)[0]
+    out = attention(q, k, v, heads=heads)
+    if head_gate is not None:
+        tokens, width = out.shape
+        out = (out.reshape(tokens, heads, width // heads) * head_gate[:, :, None]).reshape(tokens, width)
+    return _lin(params, f"{prefix}.to_out", out)
+
+
+def ltx_feed_forward(params: dict, prefix: str, value) -> np.ndarray:
+    """``project_out(gelu_approx(project_in(x)))``
+    (``kinomlx/models/ltx2/transformer/feed_forward.py:80-97``)."""
+    hidden = gelu_approx(_lin(params, f"{prefix}.proj_in", value))
+    return _lin(params, f"{prefix}.proj_out", hidden)
+
+
+def ltx_video_block(params: dict, x, context, pe, *, heads: int, eps: float = 1e-6) -> np.ndarray:
+    """Video branch of ``BasicAVTransformerBlock.__call__``
+    (``kinomlx/models/ltx2/transformer/transformer.py:225-276,373-392``) with the text
+    cross-attention of ``:201-223``.
+
+    ``params["ada"]`` is ``scale_shift_table + timesteps`` as ``(9, D)`` (``:179-186``): rows
+    0-2 attention (shift, scale, gate), 3-5 feed-forward, 6-8 text query. ``params["prompt"]``
+    is the ``(2, D)`` context (shift, scale) (``:209-219``).
+    """
+    ada = np.asarray(params["ada"], dtype=F32)
+    prompt = np.asarray(params["prompt"], dtype=F32)
+    value = np.asarray(x, dtype=F32)
+
+    normalized_x = adaln(value, ada[1], ada[0], eps)
+    attended = ltx_attention(params, "attn1", normalized_x, heads=heads, pe=pe, eps=eps)
+    value = gated_residual(value, attended, ada[2])
+
+    query = adaln(value, ada[7], ada[6], eps)
+    ctx = modulate(context, prompt[1], prompt[0])
+    cross = ltx_attention(params, "attn2", query, heads=heads, context=ctx, eps=eps)
+    value = (value + gate(cross, ada[8])).astype(F32)
+
+    normalized_x = adaln(value, ada[4], ada[3], eps)
+    return gated_residual(value, ltx_feed_forward(params, "ff", normalized_x), ada[5])
+
+
+def _heads_norm(value, weight, heads: int, eps: float = 1e-6) -> np.ndarray:
+    tokens, width = value.shape
+    return rms_norm(value.reshape(tokens, heads, width // heads), weight, eps).reshape(tokens, width)
+
+
+def _heads_rope(value, cos, sin, heads: int) -> np.ndarray:
+    tokens, width = value.shape
+    rotated = pair_rope(value.reshape(tokens, heads, width // heads), cos[:, None, :], sin[:, None, :])
+    return rotated.reshape(tokens, width)
+
+
+def _joint_attention(q_parts, k_parts, v_parts, rope, heads: int) -> np.ndarray:
+    """Concatenate [text, image] streams, rotate Q/K by adjacent pairs, attend
+    (``kinomlx/models/flux2/transformer.py:35-53``; ``kv.py:48-54``)."""
+    q = np.concatenate(q_parts, axis=0)
+    k = np.concatenate(k_parts, axis=0)
+    v = np.concatenate(v_parts, axis=0)
+    cos, sin = rope
+    q = _heads_rope(q, cos, sin, heads)
+    k = _heads_rope(k, cos, sin, heads)
+    return attention(q, k, v, heads=heads)
+
+
+def flux_double_block(params: dict, image, text, image_mod, text_mod, rope, *, heads: int, ff: str = "swiglu"):
+    """FLUX.2 ``DoubleBlock.__call__`` (``kinomlx/models/flux2/transformer.py:136-167``) with
+    ``DoubleAttention`` (``:88-133``): LayerNorm modulation, per-head QKNorm, joint [text, image]
+    attention with adjacent-pair RoPE, gated residuals.
+
+    ``image_mod``/``text_mod`` are ``(6, D)``: shift, scale, gate, ff_shift, ff_scale, ff_gate.
+    ``rope`` is ``(cos, sin)`` of shape ``(T_text + T_image, Dh)``. ``ff`` selects the
+    feed-forward: ``"swiglu"`` (FLUX, ``:63-85``) or ``"gelu"`` (LTX ``FeedForward``, config 1).
+    """
+    image = np.asarray(image, dtype=F32)
+    text = np.asarray(text, dtype=F32)
+    im = np.asarray(image_mod, dtype=F32)
+    tm = np.asarray(text_mod, dtype=F32)
+    img_n = normalized(image, im[0], im[1])
+    txt_n = normalized(text, tm[0], tm[1])
+    q = [
+        _heads_norm(_lin(params, "attn.add_q_proj", txt_n), params["attn.norm_added_q.weight"], heads),
+        _heads_norm(_lin(params, "attn.to_q", img_n), params["attn.norm_q.weight"], heads),
+    ]
+    k = [
+        _heads_norm(_lin(params, "attn.add_k_proj", txt_n), params["attn.norm_added_k.weight"], heads),
+        _heads_norm(_lin(params, "attn.to_k", img_n), params["attn.norm_k.weight"], heads),
+    ]
+    v = [_lin(params, "attn.add_v_proj", txt_n), _lin(params, "attn.to_v", img_n)]
+    result = _joint_attention(q, k, v, rope, heads)
+    t_text = text.shape[0]
+    ai = _lin(params, "attn.to_out", result[t_text:])
+    at = _lin(params, "attn.to_add_out", result[:t_text])
+    image = (image + im[2] * ai).astype(F32)
+    text = (text + tm[2] * at).astype(F32)
+
+    def feed_forward(prefix: str, value):
+        if ff == "swiglu":
+            return _lin(params, f"{prefix}.linear_out", swiglu(_lin(params, f"{prefix}.linear_in", value)))
+        return ltx_feed_forward(params, prefix, value)
+
+    image = (image + im[5] * feed_forward("ff", normalized(image, im[3], im[4]))).astype(F32)
+    text = (text + tm[5] * feed_forward("ff_context", normalized(text, tm[3], tm[4]))).astype(F32)
+    return image, text
+
+
+def flux_single_block(params: dict, value, modulation, rope, *, heads: int, width: int):
+    """FLUX.2 ``SingleBlock.__call__`` (``kinomlx/models/flux2/transformer.py:201-220``) with
+    ``SingleAttention`` (``:170-198``): one fused projection split [D, 2D, 3D], per-head QKNorm,
+    adjacent-pair RoPE, ``to_out(concat[attention, swiglu(mlp)])``, gated residual.
+    ``modulation`` is ``(3, D)``: shift, scale, gate."""
+    x = np.asarray(value, dtype=F32)
+    mod = np.asarray(modulation, dtype=F32)
+    n = normalized(x, mod[0], mod[1])
+    fused = _lin(params, "attn.to_qkv_mlp_proj", n)
+    q, k, v, mlp = fused[:, :width], fused[:, width : 2 * width], fused[:, 2 * width : 3 * width], fused[:, 3 * width :]
+    q = _heads_norm(q, params["attn.norm_q.weight"], heads)
+    k = _heads_norm(k, params["attn.norm_k.weight"], heads)
+    attn = _joint_attention([q], [k], [v], rope, heads)
+    out = _lin(params, "attn.to_out", np.concatenate([attn, swiglu(mlp)], axis=-1))
+    return (x + mod[2] * out).astype(F32)
+
+
+def config1_double_block(params: dict, image, text, image_mod, text_mod, rope, *, heads: int):
+    """This build's config-1 block: the FLUX.2 double-stream structure with LTX's GELU-tanh
+    feed-forward (biases on the feed-forward only) and Krea-style per-axis RoPE tables."""
+    return flux_double_block(params, image, text, image_mod, text_mod, rope, heads=heads, ff="gelu")

@@ -1,0 +1,432 @@
+"""Operator-level CPU restatement of the reference's DiT-block math (test infrastructure only).
+
+Each function names the reference file:line whose MLX arithmetic it restates. Arrays are numpy
+float32 unless stated; bfloat16 data is carried as float32 values that bf16 represents exactly.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+F32 = np.float32
+
+__all__ = [
+    "adaln",
+    "attention",
+    "bf16_bits",
+    "dequantize_affine",
+    "flux_rotary_positions",
+    "fractional_positions",
+    "frequency_grid",
+    "from_bf16_bits",
+    "gate",
+    "gated_residual",
+    "gelu_approx",
+    "krea_apply_rotary",
+    "krea_rms_norm",
+    "krea_rotary",
+    "layer_norm",
+    "linear",
+    "modulate",
+    "normalized",
+    "pack_affine",
+    "pair_rope",
+    "precompute_freqs_cis",
+    "quantize_affine",
+    "quantized_linear",
+    "rms_norm",
+    "silu",
+    "split_rope",
+    "swiglu",
+    "to_bf16",
+    "unpack_affine",
+]
+
+
+# ---------------------------------------------------------------------------------------------
+# bfloat16 helpers (round-to-nearest-even, the rounding of every bf16 store on both sides)
+
+
+def bf16_bits(value: np.ndarray) -> np.ndarray:
+    """float32 -> bf16 bit patterns (uint16), round to nearest even; NaNs stay quiet NaNs."""
+    u = np.ascontiguousarray(value, dtype=F32).view(np.uint32).astype(np.uint64)
+    rounded = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    quiet = ((u >> 16) | 0x40) & 0xFFFF
+    return np.where(nan, quiet, rounded).astype(np.uint16)
+
+
+def from_bf16_bits(bits: np.ndarray) -> np.ndarray:
+    """bf16 bit patterns (uint16) -> float32 values."""
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(F32)
+
+
+def to_bf16(value: np.ndarray) -> np.ndarray:
+    """Round float32 values to the nearest bf16 value (returned as float32)."""
+    return from_bf16_bits(bf16_bits(value))
+
+
+def _f32(value) -> np.ndarray:
+    return np.asarray(value, dtype=F32)
+
+
+# ---------------------------------------------------------------------------------------------
+# Norms and modulation
+
+
+def rms_norm(value, weight=None, eps: float = 1e-6, *, weight_offset: float = 0.0) -> np.ndarray:
+    """RMSNorm over the last axis with FP32 opmath.
+
+    Weighted form: ``x * rsqrt(mean(x^2) + eps) * (w + weight_offset)``
+    (``kinomlx/kernels/fused_ops.py:141-193`` reduction and affine order, ``:412-457`` policy).
+    Unweighted form: ``mx.fast.rms_norm(x, None, eps)`` (``fused_ops.py:437-441``).
+    """
+    x = _f32(value)
+    mean_square = np.mean(x * x, axis=-1, keepdims=True, dtype=F32)
+    inverse = F32(1.0) / np.sqrt(mean_square + F32(eps))
+    out = x * inverse
+    if weight is not None:
+        out = out * (_f32(weight) + F32(weight_offset))
+    return out.astype(F32)
+
+
+def layer_norm(value, eps: float = 1e-6) -> np.ndarray:
+    """Non-affine LayerNorm, ``mx.fast.layer_norm(x, None, None, eps)``
+    (``kinomlx/models/flux2/transformer.py:56-57``)."""
+    x = _f32(value)
+    mean = np.mean(x, axis=-1, keepdims=True, dtype=F32)
+    centred = x - mean
+    variance = np.mean(centred * centred, axis=-1, keepdims=True, dtype=F32)
+    return (centred / np.sqrt(variance + F32(eps))).astype(F32)
+
+
+def adaln(value, scale, shift, eps: float = 1e-6) -> np.ndarray:
+    """LTX AdaLN: ``rms_norm(x) * (1 + scale) + shift``
+    (``kinomlx/models/ltx2/transformer/transformer.py:16-23``)."""
+    return (rms_norm(value, eps=eps) * (F32(1.0) + _f32(scale)) + _f32(shift)).astype(F32)
+
+
+def modulate(value, scale, shift) -> np.ndarray:
+    """``x * (1 + scale) + shift`` (``transformer.py:33-34``)."""
+    return (_f32(value) * (F32(1.0) + _f32(scale)) + _f32(shift)).astype(F32)
+
+
+def gated_residual(value, residual, gate_value) -> np.ndarray:
+    """``x + r * gate`` (``transformer.py:26-30``)."""
+    return (_f32(value) + _f32(residual) * _f32(gate_value)).astype(F32)
+
+
+def gate(value, gate_value) -> np.ndarray:
+    """``x * gate`` (``transformer.py:37-38``)."""
+    return (_f32(value) * _f32(gate_value)).astype(F32)
+
+
+def normalized(value, shift, scale, eps: float = 1e-6) -> np.ndarray:
+    """FLUX.2 modulation: ``layer_norm(x) * (1 + scale) + shift``
+    (``kinomlx/models/flux2/transformer.py:56-57``)."""
+    return (layer_norm(value, eps) * (F32(1.0) + _f32(scale)) + _f32(shift)).astype(F32)
+
+
+def krea_rms_norm(value, weight, eps: float) -> np.ndarray:
+    """Zero-centred RMSNorm ``x * rsqrt(mean(x^2) + eps) * (w + 1)``
+    (``kinomlx/models/krea2/transformer/model.py:29-46``)."""
+    return rms_norm(value, weight, eps, weight_offset=1.0)
+
+
+# ---------------------------------------------------------------------------------------------
+# Activations
+
+
+def gelu_approx(value) -> np.ndarray:
+    """tanh GELU with the inner argument clamped to +-10, FP32
+    (``kinomlx/kernels/fused_ops.py:27-35``)."""
+    x = _f32(value)
+    inner = F32(0.7978845608028654) * (x + F32(0.044715) * (x * x * x))
+    inner = np.clip(inner, F32(-10.0), F32(10.0))
+    return (F32(0.5) * x * (F32(1.0) + np.tanh(inner))).astype(F32)
+
+
+def silu(value) -> np.ndarray:
+    """``x / (1 + exp(-x))`` in FP32 (``kinomlx/kernels/fused_ops.py:40-45``)."""
+    x = _f32(value)
+    with np.errstate(over="ignore"):
+        return (x / (F32(1.0) + np.exp(-x))).astype(F32)
+
+
+def swiglu(value) -> np.ndarray:
+    """``silu(gate) * content`` over the two halves of the last axis
+    (``kinomlx/models/flux2/transformer.py:63-65``)."""
+    x = _f32(value)
+    half = x.shape[-1] // 2
+    return (silu(x[..., :half]) * x[..., half:]).astype(F32)
+
+
+# ---------------------------------------------------------------------------------------------
+# Rotary embeddings
+
+
+def split_rope(value, cos, sin) -> np.ndarray:
+    """Split-half rotation of flattened-head activations by head-major FP32 tables.
+
+    ``value`` is ``(B, T, H * 2 * half)``; ``cos``/``sin`` are ``(B or 1, H, T, half)``. For each
+    head and ``i < half``: ``o[i] = x[i]c - x[i+half]s`` and ``o[i+half] = x[i]s + x[i+half]c``
+    with each product rounded in FP32 before the difference/sum
+    (``kinomlx/kernels/split_rope.py:35-56``; graph ``kinomlx/models/ltx2/transformer/rope.py:18-61``).
+    """
+    x = _f32(value)
+    c = _f32(cos)
+    s = _f32(sin)
+    batch, tokens, width = x.shape
+    _, heads, t2, half = c.shape
+    if t2 != tokens or width != heads * 2 * half:
+        raise ValueError("split RoPE shape mismatch")
+    xh = x.reshape(batch, tokens, heads, 2 * half).transpose(0, 2, 1, 3)
+    first = xh[..., :half]
+    second = xh[..., half:]
+    first_c = first * c
+    second_s = second * s
+    first_s = first * s
+    second_c = second * c
+    out = np.concatenate([first_c - second_s, first_s + second_c], axis=-1)
+    return out.transpose(0, 2, 1, 3).reshape(batch, tokens, width).astype(F32)
+
+
+def frequency_grid(theta: float, position_dims: int, inner_dim: int) -> np.ndarray:
+    """``theta ** (j / (n - 1)) * pi / 2`` for ``j < n = inner_dim // (2 * position_dims)``, in host
+    double precision, then narrowed to FP32 (``kinomlx/models/ltx2/transformer/rope.py:75-92``)."""
+    count = inner_dim // (2 * position_dims)
+    if count <= 0:
+        raise ValueError("RoPE dimension is too small for its position axes")
+    exponents = (0.0,) if count == 1 else tuple(j / (count - 1) for j in range(count))
+    return np.array([math.pow(theta, e) * math.pi / 2 for e in exponents], dtype=np.float64).astype(
+        F32
+    )
+
+
+def fractional_positions(positions, max_pos, *, use_middle_indices_grid: bool) -> np.ndarray:
+    """Positions ``(B, axes, T[, 2])`` -> ``(B, T, axes)`` fractions of ``max_pos``
+    (``kinomlx/models/ltx2/transformer/rope.py:95-112``)."""
+    p = np.asarray(positions)
+    if p.shape[1] != len(max_pos):
+        raise ValueError("position axes must match max_pos")
+    if use_middle_indices_grid:
+        if p.ndim != 4 or p.shape[-1] != 2:
+            raise ValueError("middle-position RoPE expects (B, axes, T, 2) bounds")
+        p = (_f32(p[..., 0]) + _f32(p[..., 1])) / F32(2.0)
+    elif p.ndim == 4:
+        p = p[..., 0]
+    scale = np.asarray(max_pos, dtype=F32)[None, :, None]
+    return (_f32(p) / scale).transpose(0, 2, 1)
+
+
+def precompute_freqs_cis(
+    indices_grid,
+    *,
+    dim: int,
+    theta: float = 10000.0,
+    max_pos=(20, 2048, 2048),
+    use_middle_indices_grid: bool = False,
+    num_attention_heads: int = 32,
+) -> tuple[np.ndarray, np.ndarray]:
+    """Split-RoPE cosine/sine tables ``(B, H, T, dim / (2H))`` in FP32
+    (``kinomlx/models/ltx2/transformer/rope.py:115-176``).
+
+    ``scaled = 2 * fraction - 1``; ``freq[b, t, j * axes + a] = scaled[b, t, a] * grid[j]``
+    (frequency-major, axis-minor); front-padded with ``cos = 1``, ``sin = 0`` up to ``dim / 2``.
+    """
+    if dim % num_attention_heads:
+        raise ValueError("RoPE dimension must divide evenly across attention heads")
+    grid_in = np.asarray(indices_grid)
+    fractional = fractional_positions(grid_in, tuple(max_pos), use_middle_indices_grid=use_middle_indices_grid)
+    grid = frequency_grid(theta, grid_in.shape[1], dim)
+    scaled = fractional * F32(2.0) - F32(1.0)
+    frequencies = scaled[..., None] * grid[None, None, None, :]  # (B, T, axes, n)
+    frequencies = frequencies.transpose(0, 1, 3, 2).reshape(frequencies.shape[0], frequencies.shape[1], -1)
+    expected = dim // 2
+    padding = expected - frequencies.shape[-1]
+    if padding < 0:
+        raise ValueError("RoPE frequency grid exceeds half the model dimension")
+    cos = np.cos(frequencies).astype(F32)
+    sin = np.sin(frequencies).astype(F32)
+    if padding:
+        cos = np.concatenate([np.ones((*cos.shape[:-1], padding), F32), cos], axis=-1)
+        sin = np.concatenate([np.zeros((*sin.shape[:-1], padding), F32), sin], axis=-1)
+    batch, tokens, _ = cos.shape
+    cos = cos.reshape(batch, tokens, num_attention_heads, -1).transpose(0, 2, 1, 3)
+    sin = sin.reshape(batch, tokens, num_attention_heads, -1).transpose(0, 2, 1, 3)
+    return np.ascontiguousarray(cos), np.ascontiguousarray(sin)
+
+
+def pair_rope(value, cos, sin) -> np.ndarray:
+    """Adjacent-pair rotation ``(x0, x1) -> (x0 c0 - x1 s0, x1 c1 + x0 s1)`` in FP32, cast back
+    (``kinomlx/models/flux2/transformer.py:25-29``; Krea ``model.py:69-92``).
+
+    ``value`` is ``(..., Dh)``; ``cos``/``sin`` broadcast against it.
+    """
+    x = _f32(value)
+    pairs = x.reshape(*x.shape[:-1], -1, 2)
+    perpendicular = np.stack([-pairs[..., 1], pairs[..., 0]], axis=-1).reshape(x.shape)
+    return (x * _f32(cos) + perpendicular * _f32(sin)).astype(F32)
+
+
+def flux_rotary_positions(ids) -> tuple[np.ndarray, np.ndarray]:
+    """FLUX.2 tables from ``(B, T, 4)`` ids: ``freq_i = 2000^(-2i/32)``, ``i < 16`` per axis,
+    angles repeated pairwise to ``(B, T, 1, 128)`` (``kinomlx/models/flux2/transformer.py:17-22``)."""
+    frequency = (F32(2000.0) ** (-np.arange(0, 32, 2, dtype=F32) / F32(32))).astype(F32)
+    ids = _f32(ids)
+    angles = (ids[..., None] * frequency).reshape(*ids.shape[:-1], 64)
+    angles = np.repeat(angles, 2, axis=-1)
+    return np.cos(angles)[:, :, None].astype(F32), np.sin(angles)[:, :, None].astype(F32)
+
+
+def krea_rotary(position_ids, *, theta: float, axes_dims) -> tuple[np.ndarray, np.ndarray]:
+    """Per-axis ``1 / theta^(2i/d_axis)`` frequencies, adjacent-pair repetition, axes concatenated
+    in declared order (``kinomlx/models/krea2/transformer/model.py:49-66``)."""
+    positions = _f32(position_ids)
+    if positions.ndim != 3 or positions.shape[-1] != len(axes_dims):
+        raise ValueError("position_ids must have shape [batch, sequence, position_axes]")
+    parts = []
+    for axis, dims in enumerate(axes_dims):
+        frequencies = (F32(1.0) / (F32(theta) ** (np.arange(0, dims, 2, dtype=F32) / F32(dims)))).astype(F32)
+        angles = positions[..., axis, None] * frequencies
+        parts.append(np.repeat(angles, 2, axis=-1))
+    combined = np.concatenate(parts, axis=-1)
+    return np.cos(combined).astype(F32), np.sin(combined).astype(F32)
+
+
+def krea_apply_rotary(queries, keys, cos, sin) -> tuple[np.ndarray, np.ndarray]:
+    """Krea adjacent-pair RoPE on head-major ``(B, H, T, Dh)`` with ``(B, T, Dh)`` tables
+    (``kinomlx/models/krea2/transformer/model.py:69-92``)."""
+    c = _f32(cos)[:, None, :, :]
+    s = _f32(sin)[:, None, :, :]
+    return pair_rope(queries, c, s), pair_rope(keys, c, s)
+
+
+# ---------------------------------------------------------------------------------------------
+# Attention and linear products
+
+
+def attention(q, k, v, *, heads: int, scale: float | None = None) -> np.ndarray:
+    """Non-causal softmax attention on token-major flattened heads.
+
+    ``q`` is ``(Tq, H * Dh)``, ``k``/``v`` are ``(Tk, H * Dh)``; output ``(Tq, H * Dh)``.
+    ``softmax(q k^T * Dh^-0.5) v`` per head, FP32 scores and accumulation (contract of
+    ``kinomlx/models/ltx2/kernels/dense_attention.py:87-153``; SDPA fallback
+    ``kinomlx/models/ltx2/transformer/attention.py:144-161``).
+    """
+    q = _f32(q)
+    k = _f32(k)
+    v = _f32(v)
+    tq, width = q.shape
+    tk = k.shape[0]
+    dh = width // heads
+    sc = F32(dh ** -0.5 if scale is None else scale)
+    out = np.empty((tq, width), F32)
+    for h in range(heads):
+        sl = slice(h * dh, (h + 1) * dh)
+        qh = q[:, sl]
+        kh = k[:, sl]
+        vh = v[:, sl]
+        for start in range(0, tq, 2048):
+            stop = min(tq, start + 2048)
+            scores = (qh[start:stop] @ kh.T) * sc
+            scores -= scores.max(axis=-1, keepdims=True)
+            np.exp(scores, out=scores)
+            denom = scores.sum(axis=-1, keepdims=True, dtype=F32)
+            out[start:stop, sl] = (scores @ vh) / denom
+    return out
+
+
+def linear(value, weight, bias=None) -> np.ndarray:
+    """``addmm(bias, x, W^T)`` for an ``(out, in)`` weight: FP32 products and sums, bias added in
+    FP32 (``kinomlx/kernels/mpp_linear.py:1-6``, ``:469-506``; ``kinomlx/modeling/layers.py``)."""
+    x = _f32(value)
+    out = x @ _f32(weight).T
+    if bias is not None:
+        out = out + _f32(bias)
+    return out.astype(F32)
+
+
+# ---------------------------------------------------------------------------------------------
+# Group-wise affine int4 / int8 weights
+#
+# The arithmetic of ``mx.quantize`` / ``mx.quantized_matmul`` lives in MLX (mlx>=0.32.4,
+# ``pyproject.toml:28``), not in the reference tree. Call sites: ``kinomlx/models/ltx2/
+# preparation.py:152`` and ``kinomlx/models/ltx2/weights/quantization.py:28-44``; defaults
+# ``kinomlx/models/ltx2/weights/tensors.py:185-203`` (affine -> group 64, 4 bits). The packed
+# format restated here: ``(N, K * bits / 32)`` uint32 words, element ``j`` of a word at bits
+# ``[bits*j, bits*(j+1))`` (little-endian nibble/byte order), bf16 scale and bias per group of
+# ``group_size`` along K, ``w = scale * q + bias``.
+
+
+def pack_affine(codes: np.ndarray, bits: int) -> np.ndarray:
+    """``(N, K)`` integer codes -> ``(N, K * bits / 32)`` little-endian uint32 words."""
+    if bits not in (4, 8):
+        raise ValueError("bits must be 4 or 8")
+    per_word = 32 // bits
+    c = np.asarray(codes, dtype=np.uint32)
+    n, k = c.shape
+    if k % per_word:
+        raise ValueError("K must fill whole words")
+    c = c.reshape(n, k // per_word, per_word)
+    shifts = (np.arange(per_word, dtype=np.uint32) * bits)[None, None, :]
+    return np.bitwise_or.reduce(c << shifts, axis=-1).astype(np.uint32)
+
+
+def unpack_affine(words: np.ndarray, bits: int) -> np.ndarray:
+    """``(N, W)`` uint32 words -> ``(N, W * 32 / bits)`` integer codes (uint32)."""
+    if bits not in (4, 8):
+        raise ValueError("bits must be 4 or 8")
+    per_word = 32 // bits
+    w = np.asarray(words, dtype=np.uint32)
+    shifts = (np.arange(per_word, dtype=np.uint32) * bits)[None, None, :]
+    mask = np.uint32((1 << bits) - 1)
+    return ((w[..., None] >> shifts) & mask).reshape(w.shape[0], -1)
+
+
+def quantize_affine(weight, group_size: int = 64, bits: int = 4):
+    """This build's deterministic affine quantizer (stands in for ``mx.quantize``).
+
+    Per group: ``scale = bf16((max - min) / (2^bits - 1))`` (1 for a constant group),
+    ``bias = bf16(min)``, ``q = clip(rint((w - bias) / scale), 0, 2^bits - 1)``. Returns
+    ``(words uint32 (N, K*bits/32), scales float32 (N, K/group), biases float32 (N, K/group))``
+    with scales and biases holding bf16 values.
+    """
+    w = _f32(weight)
+    n, k = w.shape
+    if k % group_size:
+        raise ValueError("K must be a multiple of the group size")
+    levels = (1 << bits) - 1
+    groups = w.reshape(n, k // group_size, group_size)
+    lo = groups.min(axis=-1)
+    hi = groups.max(axis=-1)
+    scale = (hi - lo) / F32(levels)
+    scale = np.where(scale > 0, scale, F32(1.0)).astype(F32)
+    scale_bf = to_bf16(scale)
+    scale_bf = np.where(scale_bf > 0, scale_bf, F32(1.0)).astype(F32)
+    bias_bf = to_bf16(lo)
+    codes = np.rint((groups - bias_bf[..., None]) / scale_bf[..., None])
+    codes = np.clip(codes, 0, levels).astype(np.uint32).reshape(n, k)
+    return pack_affine(codes, bits), scale_bf, bias_bf
+
+
+def dequantize_affine(words, scales, biases, *, group_size: int = 64, bits: int = 4) -> np.ndarray:
+    """Bit-exact dequantisation ``bf16(fp32(scale) * q + fp32(bias))`` -> ``(N, K)`` float32.
+
+    A bf16 scale (8 significant bits) times ``q < 256`` is exact in FP32, so the only roundings
+    are the FP32 add and the final round-to-nearest-even into bf16.
+    """
+    codes = unpack_affine(words, bits).astype(F32)
+    n, k = codes.shape
+    s = np.repeat(_f32(scales), group_size, axis=1)[:, :k]
+    b = np.repeat(_f32(biases), group_size, axis=1)[:, :k]
+    return to_bf16(s * codes + b)
+
+
+def quantized_linear(value, words, scales, biases, bias=None, *, group_size: int = 64, bits: int = 4):
+    """``quantized_matmul(x, w, scales, biases, transpose=True) + bias`` with the bit-exact bf16
+    dequantised weight and FP32 accumulation (``kinomlx/models/ltx2/weights/quantization.py:28-44``)."""
+    weight = dequantize_affine(words, scales, biases, group_size=group_size, bits=bits)
+    return linear(value, weight, bias)

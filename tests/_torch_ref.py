@@ -1,0 +1,69 @@
+"""FP32 PyTorch evaluation of the LTX-2 video block (test infrastructure).
+
+The same composition as ``oracle.ltx_video_block`` written with torch operations, so that the
+full-size (9216-token) block can be evaluated in FP32 on the GPU in seconds, where the numpy
+oracle would take minutes. ``tests/test_blocks_cpu.py`` pins it against the numpy oracle.
+"""
+
+import torch
+
+
+def _lin(p, name, x):
+    out = x @ p[f"{name}.weight"].T
+    bias = p.get(f"{name}.bias")
+    return out if bias is None else out + bias
+
+
+def _rms(x, w=None, eps=1e-6):
+    y = x * torch.rsqrt((x * x).mean(-1, keepdim=True) + eps)
+    return y if w is None else y * w
+
+
+def _split_rope(x, cos, sin):
+    t, width = x.shape
+    heads, half = cos.shape[1], cos.shape[3]
+    xh = x.reshape(t, heads, 2 * half).transpose(0, 1)
+    c, s = cos[0], sin[0]
+    first, second = xh[..., :half], xh[..., half:]
+    out = torch.cat([first * c - second * s, first * s + second * c], -1)
+    return out.transpose(0, 1).reshape(t, width)
+
+
+def _attention(q, k, v, heads):
+    t, width = q.shape
+    dh = width // heads
+    qh = q.reshape(t, heads, dh).transpose(0, 1)
+    kh = k.reshape(k.shape[0], heads, dh).transpose(0, 1)
+    vh = v.reshape(v.shape[0], heads, dh).transpose(0, 1)
+    out = torch.empty_like(qh)
+    for start in range(0, t, 2048):
+        sc = qh[:, start:start + 2048] @ kh.transpose(1, 2) * dh ** -0.5
+        out[:, start:start + 2048] = torch.softmax(sc, -1) @ vh
+    return out.transpose(0, 1).reshape(t, width)
+
+
+def _ltx_attention(p, prefix, x, heads, context=None, pe=None):
+    source = x if context is None else context
+    gate = 2 * torch.sigmoid(_lin(p, f"{prefix}.to_gate_logits", x))
+    v = _lin(p, f"{prefix}.to_v", source)
+    q = _rms(_lin(p, f"{prefix}.to_q", x), p[f"{prefix}.q_norm.weight"])
+    k = _rms(_lin(p, f"{prefix}.to_k", source), p[f"{prefix}.k_norm.weight"])
+    if pe is not None:
+        q, k = _split_rope(q, *pe), _split_rope(k, *pe)
+    o = _attention(q, k, v, heads)
+    t, width = o.shape
+    o = (o.reshape(t, heads, width // heads) * gate[:, :, None]).reshape(t, width)
+    return _lin(p, f"{prefix}.to_out", o)
+
+
+def ltx_video_block(p, x, context, pe, heads):
+    """``p``: fp32 tensors named as in ``oracle.ltx_video_block`` (dense weights)."""
+    ada, prompt = p["ada"], p["prompt"]
+    n = _rms(x) * (1 + ada[1]) + ada[0]
+    x = x + _ltx_attention(p, "attn1", n, heads, pe=pe) * ada[2]
+    q = _rms(x) * (1 + ada[7]) + ada[6]
+    ctx = context * (1 + prompt[1]) + prompt[0]
+    x = x + _ltx_attention(p, "attn2", q, heads, context=ctx) * ada[8]
+    n = _rms(x) * (1 + ada[4]) + ada[3]
+    h = torch.nn.functional.gelu(_lin(p, "ff.proj_in", n), approximate="tanh")
+    return x + _lin(p, "ff.proj_out", h) * ada[5]

@@ -1,0 +1,110 @@
+"""Host-side logic of the operator surface: contracts, error messages and routing predicates
+that hold before any kernel runs, plus the product's CPU-side helpers (quantizer, RoPE tables,
+workload FLOP counts) against the oracle. CPU only."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from kinomlx_amd import workloads
+from kinomlx_amd.kernels import mpp_linear, quantized, split_rope
+from kinomlx_amd.ltx2 import dense_attention, rope
+
+
+def _zeros(tokens, width, dtype=torch.bfloat16):
+    return torch.zeros((1, tokens, width), dtype=dtype)
+
+
+def test_dense_attention_refuses_inputs_outside_the_contract():
+    """Messages of kinomlx/models/ltx2/kernels/dense_attention.py:112-130 (test_dense_attention.py:86-99)."""
+    q = torch.zeros(32, 256, dtype=torch.bfloat16)
+    k = torch.zeros(20, 256, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="float16 or bfloat16"):
+        dense_attention.dense_attention(q.float(), k.float(), k.float(), heads=2)
+    with pytest.raises(ValueError, match="float16 or bfloat16"):
+        dense_attention.dense_attention(q, k, k.float(), heads=2)
+    with pytest.raises(ValueError, match="64 or 128"):
+        dense_attention.dense_attention(q, k, k, heads=3)
+    with pytest.raises(ValueError, match="64 or 128"):
+        dense_attention.dense_attention(q, k, k, heads=8)
+    with pytest.raises(ValueError, match="64 or 128"):
+        dense_attention.dense_attention(q, k[:, :128], k[:, :128], heads=2)
+    with pytest.raises(ValueError, match="64 or 128"):
+        dense_attention.dense_attention(q, k, k[:-1], heads=2)
+
+
+def test_dense_attention_applies_only_to_gpu_bf16_64_or_128_wide_heads():
+    # CPU tensors never take the kernel
+    assert not dense_attention.applies(_zeros(5, 256), _zeros(9, 256), heads=2)
+    assert not dense_attention.applies(_zeros(5, 256, torch.float32), _zeros(5, 256, torch.float32), heads=2)
+    assert not dense_attention.applies(_zeros(5, 96), _zeros(5, 96), heads=2)
+    assert not dense_attention.applies(_zeros(0, 256), _zeros(5, 256), heads=2)
+    assert dense_attention.HEAD_DIMS == (64, 128)
+
+
+def test_split_rope_contract_on_the_host():
+    value = torch.zeros(1, 13, 4 * 48, dtype=torch.bfloat16)
+    cos = torch.zeros(1, 4, 13, 24)
+    assert not split_rope.applies(value, cos, cos)  # CPU tensors
+    assert not split_rope.applies(value, cos[:, :3], cos[:, :3])
+    with pytest.raises(ValueError, match="does not apply"):
+        split_rope.rotate(value, cos, cos)
+    split_rope.set_enabled(False)
+    try:
+        assert not split_rope.enabled()
+    finally:
+        split_rope.set_enabled(True)
+    with pytest.raises(ValueError, match="matching shapes"):
+        rope.apply_split_rotary_emb(value, cos, cos[:, :, :5])
+
+
+def test_linear_supports_and_applies():
+    assert mpp_linear.supports(1056, 1024, 1040, transposed=True, dtype=torch.bfloat16)
+    assert not mpp_linear.supports(10, 12, 16, transposed=True, dtype=torch.bfloat16)
+    assert not mpp_linear.supports(10, 16, 16, transposed=True, dtype=torch.float32)
+    w = torch.zeros(16, 32, dtype=torch.bfloat16)
+    assert mpp_linear.prepare(w).peak is None
+    assert mpp_linear.prepare(w.t(), transposed=False).values.shape == (16, 32)
+    assert mpp_linear.restore(mpp_linear.prepare(w)) is not None
+    assert not mpp_linear.applies(torch.zeros(4, 32, dtype=torch.bfloat16), w, None, transposed=True) or torch.cuda.is_available()
+
+
+def test_quant_defaults_follow_the_reference():
+    assert quantized.quant_defaults("affine", None, None) == (64, 4)
+    assert quantized.quant_defaults("affine", None, 8) == (64, 8)
+    with pytest.raises(ValueError, match="mode"):
+        quantized.quant_defaults("mxfp4", None, None)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_product_quantizer_is_bit_identical_to_the_oracle(bits):
+    w = workloads.normal(3, "q", (96, 256), 0.02).to(torch.bfloat16)
+    words, scales, biases = quantized.quantize(w, 64, bits)
+    o_words, o_scales, o_biases = oracle.quantize_affine(w.float().numpy(), 64, bits)
+    assert np.array_equal(words.numpy().view(np.uint32), o_words)
+    assert np.array_equal(scales.float().numpy(), o_scales)
+    assert np.array_equal(biases.float().numpy(), o_biases)
+    assert np.array_equal(quantized.unpack(words, bits).numpy(), oracle.unpack_affine(o_words, bits).astype(np.int64))
+
+
+def test_product_rope_tables_match_the_oracle():
+    pos = workloads.ltx_positions((3, 4, 5))
+    cos, sin = rope.precompute_freqs_cis(pos, dim=1024, max_pos=(20, 2048, 2048), use_middle_indices_grid=True,
+                                         num_attention_heads=8)
+    o_cos, o_sin = oracle.precompute_freqs_cis(pos.numpy(), dim=1024, max_pos=(20, 2048, 2048),
+                                               use_middle_indices_grid=True, num_attention_heads=8)
+    assert cos.shape == (1, 8, 60, 64)
+    assert cos.transpose(1, 2).is_contiguous()  # token-major storage, head-major view
+    assert np.allclose(cos.numpy(), o_cos, atol=1e-6) and np.allclose(sin.numpy(), o_sin, atol=1e-6)
+
+
+def test_workload_flops_match_baseline():
+    f3 = workloads.flop_count(workloads.CONFIGS[3])
+    assert f3["gemm"] / 1e9 == pytest.approx(4351.4, abs=0.2)
+    assert f3["attention"] / 1e9 == pytest.approx(1430.2, abs=0.1)
+    assert workloads.flop_count(workloads.CONFIGS[1])["total"] / 1e9 == pytest.approx(34.4, abs=0.1)
+    assert workloads.flop_count(workloads.CONFIGS[2])["total"] / 1e9 == pytest.approx(4715.9, abs=0.2)
+    f5 = workloads.flop_count(workloads.CONFIGS[5])
+    assert f5["gemm"] / 1e9 == pytest.approx(12846.6, abs=0.2)
+    assert workloads.CONFIGS[3].tokens == 9216 and workloads.CONFIGS[5].tokens == 27280

@@ -1,0 +1,404 @@
+"""Kernel parity on the GPU: each HIP kernel (through the C ABI via the operator surface) against
+the CPU oracle on the same seeded inputs.
+
+Bars: bit-exact for the split/pair RoPE standalone kernels and the int4/int8 dequantization;
+elsewhere the tolerance is written in each test (bf16 output vs the FP32 oracle).
+"""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from kinomlx_amd import _lib
+from kinomlx_amd.kernels import fused_ops, mpp_linear, quantized, split_rope
+from kinomlx_amd.ltx2 import attention as ltx_attention
+from kinomlx_amd.ltx2 import dense_attention, transformer
+from tests.conftest import cosine, max_abs, rel_l2
+
+pytestmark = pytest.mark.gpu
+F32 = np.float32
+
+
+def _bf(a, device):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=F32)).to(device).to(torch.bfloat16)
+
+
+def _f32(a, device):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=F32)).to(device)
+
+
+def _np(t):
+    return t.float().cpu().numpy()
+
+
+def _rng(seed):
+    return np.random.default_rng(seed)
+
+
+def _within_one_ulp(got, ref):
+    """|got - ref| within one bf16 ulp of ref (2^-7 relative, plus a tiny absolute floor)."""
+    return np.all(np.abs(got - ref) <= np.abs(ref) * 2.0**-7 + 1e-6)
+
+
+# ---- norms ---------------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dim", [512, 1024, 4096, 1000])
+@pytest.mark.parametrize("kind", ["rms", "layer"])
+def test_modulated_norm_matches_oracle(device, dim, kind):
+    r = _rng(dim)
+    x = oracle.to_bf16((r.standard_normal((37, dim)) * 2 + 0.5).astype(F32))
+    scale = (r.standard_normal(dim) * 0.5).astype(F32)
+    shift = (r.standard_normal(dim) * 0.5).astype(F32)
+    if kind == "rms":
+        got = transformer.adaln(_bf(x, device), _f32(scale, device), _f32(shift, device), 1e-6)
+        ref = oracle.adaln(x, scale, shift)
+    else:
+        got = transformer.layer_norm_modulate(_bf(x, device), _f32(shift, device), _f32(scale, device))
+        ref = oracle.normalized(x, shift, scale)
+    # one rounding of an FP32 result: within one bf16 ulp (reduction order may differ)
+    assert _within_one_ulp(_np(got), ref)
+
+
+def test_modulated_norm_per_token_and_per_batch_rows(device):
+    r = _rng(11)
+    b, t, d = 2, 9, 1024
+    x = oracle.to_bf16(r.standard_normal((b, t, d)).astype(F32))
+    per_batch = (r.standard_normal((b, 1, d)) * 0.3).astype(F32)
+    per_token = (r.standard_normal((b, t, d)) * 0.3).astype(F32)
+    got = transformer.adaln(_bf(x, device), _f32(per_batch, device), _f32(per_token, device), 1e-6)
+    assert _within_one_ulp(_np(got), oracle.adaln(x, per_batch, per_token))
+
+
+@pytest.mark.parametrize(("dim", "wdtype", "offset"), [(4096, "bf16", 0.0), (256, "f32", 0.0), (3840, "bf16", 1.0)])
+def test_weighted_rms_norm_matches_oracle(device, dim, wdtype, offset):
+    """Relative L2 <= 5e-5 before the bf16 store is the reference's bar
+    (tests/kernels/test_fused_ops.py:68-84); after one bf16 rounding we bound each element by
+    one ulp."""
+    r = _rng(dim + 1)
+    x = oracle.to_bf16((r.standard_normal((2, 5, dim)) * 4).astype(F32))
+    w = (r.standard_normal(dim) * (0.02 if offset else 0.1) + (0.0 if offset else 1.0)).astype(F32)
+    w = oracle.to_bf16(w) if wdtype == "bf16" else w
+    wt = _bf(w, device) if wdtype == "bf16" else _f32(w, device)
+    got = fused_ops.rms_norm(_bf(x, device), wt, 1e-6, weight_offset=offset)
+    assert _within_one_ulp(_np(got), oracle.rms_norm(x, w, 1e-6, weight_offset=offset))
+
+
+@pytest.mark.parametrize(("dim", "heads"), [(4096, 32), (1024, 16)])
+def test_fused_norm_and_split_rope_matches_oracle(device, dim, heads):
+    r = _rng(dim + heads)
+    t = 41
+    dh = dim // heads
+    x = oracle.to_bf16((r.standard_normal((1, t, dim)) * 3).astype(F32))
+    w = oracle.to_bf16((r.standard_normal(dim) * 0.05 + 1).astype(F32))
+    pos = np.zeros((1, 3, t, 2), F32)
+    pos[0, 0, :, 0] = np.arange(t) // 7
+    pos[0, 1, :, 0] = np.arange(t) % 7
+    pos[0, 2, :, 0] = np.arange(t) % 5
+    pos[..., 1] = pos[..., 0] + 1
+    cos, sin = oracle.precompute_freqs_cis(pos, dim=dim, use_middle_indices_grid=True, num_attention_heads=heads)
+    norm = ltx_attention.RMSNorm(dim, weight=_bf(w, device))
+    # token-major storage viewed head-major, as precompute_freqs_cis returns it
+    cos_d = _f32(cos.transpose(0, 2, 1, 3), device).transpose(1, 2)
+    sin_d = _f32(sin.transpose(0, 2, 1, 3), device).transpose(1, 2)
+    got = _np(ltx_attention.norm_rope(_bf(x, device), norm, (cos_d, sin_d), heads))
+    ref = oracle.split_rope(oracle.rms_norm(x, w, 1e-6), cos, sin)
+    assert rel_l2(got, ref) < 4e-3 and max_abs(got, ref) < 2e-2 * max(1.0, np.abs(ref).max() / 4)
+    assert dh in (64, 128)
+
+
+@pytest.mark.parametrize(("norm_width", "rope_kind"), [(128, "pair"), (64, "pair"), (128, "none")])
+def test_per_head_norm_and_pair_rope_matches_oracle(device, norm_width, rope_kind):
+    r = _rng(norm_width)
+    t, heads = 23, 4096 // norm_width if norm_width == 128 else 16
+    dim = heads * norm_width
+    x = oracle.to_bf16((r.standard_normal((t, dim)) * 2).astype(F32))
+    w = oracle.to_bf16((r.standard_normal(norm_width) * 0.05 + 1).astype(F32))
+    ang = np.repeat(r.uniform(-3, 3, (t, norm_width // 2)), 2, axis=-1).astype(F32)
+    cos, sin = np.cos(ang).astype(F32), np.sin(ang).astype(F32)
+    out = torch.empty((t, dim), dtype=torch.bfloat16, device=device)
+    kind = _lib.KX_ROPE_PAIR if rope_kind == "pair" else _lib.KX_ROPE_NONE
+    _lib.launch_rmsnorm_rope(
+        _bf(x, device), out, _bf(w, device), 1e-6, 0.0, norm_width=norm_width, rope_kind=kind,
+        cos=_f32(cos, device), sin=_f32(sin, device), table_ld=norm_width, table_hs=0, tokens=t, head_dim=norm_width,
+    )
+    normed = oracle.rms_norm(x.reshape(t, heads, norm_width), w, 1e-6)
+    ref = oracle.pair_rope(normed, cos[:, None], sin[:, None]) if rope_kind == "pair" else normed
+    got = _np(out).reshape(t, heads, norm_width)
+    assert rel_l2(got, ref) < 4e-3 and cosine(got, ref) > 0.99999
+
+
+# ---- RoPE (bit-exact) -------------------------------------------------------------------------
+
+
+def _tables(batch, heads, tokens, half, token_major, seed=0):
+    count = batch * tokens * heads * half
+    angles = np.arange(count, dtype=F32) * F32(0.2718281)
+    if token_major:
+        angles = angles.reshape(batch, tokens, heads, half).transpose(0, 2, 1, 3)
+    else:
+        angles = angles.reshape(batch, heads, tokens, half)
+    return np.cos(angles).astype(F32), np.sin(angles).astype(F32)
+
+
+@pytest.mark.parametrize(("batch", "table_batch", "token_major"), [(1, 1, True), (2, 1, True), (2, 2, False)])
+@pytest.mark.parametrize("half", [24, 5])
+def test_split_rope_is_bit_exact(device, batch, table_batch, token_major, half):
+    """tests/kernels/test_split_rope.py:31-50 shapes (H=4, T=13, half=24) and the ragged
+    self-test case (half=5), against the oracle's exact FP32 op order."""
+    heads, tokens = 4, 13
+    r = _rng(611 + half)
+    x = oracle.to_bf16((r.standard_normal((batch, tokens, heads * 2 * half)) * 3).astype(F32))
+    cos, sin = _tables(table_batch, heads, tokens, half, token_major)
+    cos_d, sin_d = _f32(cos, device), _f32(sin, device)
+    value = _bf(x, device)
+    assert split_rope.applies(value, cos_d, sin_d)
+    got = _np(split_rope.rotate(value, cos_d, sin_d))
+    ref = oracle.to_bf16(oracle.split_rope(x, cos, sin))  # tables broadcast over the batch when shared
+    assert np.array_equal(got, ref)
+
+
+def test_pair_rope_is_bit_exact(device):
+    r = _rng(5)
+    t, heads, dh = 19, 3, 64
+    x = oracle.to_bf16((r.standard_normal((t, heads * dh)) * 3).astype(F32))
+    ang = np.repeat(r.uniform(-3, 3, (t, dh // 2)), 2, axis=-1).astype(F32)
+    cos, sin = np.cos(ang).astype(F32), np.sin(ang).astype(F32)
+    out = torch.empty((t, heads * dh), dtype=torch.bfloat16, device=device)
+    _lib.launch_rope_pair(_bf(x, device), out, _f32(cos, device), _f32(sin, device), heads=heads, head_dim=dh,
+                          table_ld=dh, table_hs=0, tokens=t, table_batched=False)
+    ref = oracle.to_bf16(oracle.pair_rope(x.reshape(t, heads, dh), cos[:, None], sin[:, None]).reshape(t, -1))
+    assert np.array_equal(_np(out), ref)
+
+
+# ---- activations ---------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("op", ["gelu", "silu"])
+def test_activations_round_the_fp32_result_once(device, op):
+    """linspace(-8, 8, 65536) as in tests/kernels/test_fused_ops.py:18-65. The device tanh/exp
+    and numpy's differ by an ulp or two in FP32, which can move a bf16 rounding: every element
+    is within one bf16 ulp and at least 99.9% are bit-equal."""
+    x = oracle.to_bf16(np.linspace(-8, 8, 65536, dtype=F32))
+    fn, ref_fn = (fused_ops.gelu_approx, oracle.gelu_approx) if op == "gelu" else (fused_ops.silu, oracle.silu)
+    got = _np(fn(_bf(x, device)))
+    ref = oracle.to_bf16(ref_fn(x))
+    assert _within_one_ulp(got, ref_fn(x))
+    assert np.mean(got == ref) >= 0.999
+
+
+def test_gelu_saturates_without_nan(device):
+    x = oracle.to_bf16(np.linspace(-128, 128, 65536, dtype=F32))
+    got = _np(fused_ops.gelu_approx(_bf(x, device)))
+    assert np.all(np.isfinite(got))
+    assert np.allclose(got, oracle.gelu_approx(x), rtol=1e-2, atol=1.3e-4)
+
+
+def test_swiglu_matches_oracle(device):
+    r = _rng(9)
+    x = oracle.to_bf16((r.standard_normal((33, 2 * 96)) * 3).astype(F32))
+    got = _np(fused_ops.swiglu(_bf(x, device)))
+    assert _within_one_ulp(got, oracle.swiglu(x))
+
+
+def test_modulate_gate_and_gated_residual(device):
+    r = _rng(10)
+    x = oracle.to_bf16(r.standard_normal((2, 7, 96)).astype(F32))
+    y = oracle.to_bf16(r.standard_normal((2, 7, 96)).astype(F32))
+    g = r.standard_normal((2, 1, 96)).astype(F32)
+    s = r.standard_normal(96).astype(F32)
+    xd, yd = _bf(x, device), _bf(y, device)
+    assert _within_one_ulp(_np(transformer.gated_residual(xd, yd, _f32(g, device))), oracle.gated_residual(x, y, g))
+    assert _within_one_ulp(_np(transformer.modulate(xd, _f32(s, device), _f32(g, device))), oracle.modulate(x, s, g))
+    assert _within_one_ulp(_np(transformer.gate(yd, _f32(g, device))), oracle.gate(y, g))
+
+
+# ---- linear ----------------------------------------------------------------------------------------
+
+
+def _linear_case(m, n, k, seed, device, scale=1.0):
+    r = _rng(seed)
+    x = oracle.to_bf16((r.standard_normal((m, k)) * 0.5 * scale).astype(F32))
+    w = oracle.to_bf16((r.standard_normal((n, k)) * k ** -0.5).astype(F32))
+    b = oracle.to_bf16((r.standard_normal(n) * 0.5).astype(F32))
+    return x, w, b
+
+
+def _gemm_close(got, ref):
+    """FP32 accumulation in another order, then one bf16 rounding: within one ulp of the value
+    plus the FP32 sum's own rounding noise."""
+    tol = np.abs(ref) * 2.0**-7 + 1e-4 * np.abs(ref).max()
+    return np.all(np.abs(got - ref) <= tol)
+
+
+@pytest.mark.parametrize("tile", ["auto", "0", "1", "2", "3", "4"])
+@pytest.mark.parametrize(("m", "n", "k"), [(1056, 1040, 1024), (300, 96, 64), (7, 32, 200)])
+def test_linear_matches_oracle_for_every_tile(device, monkeypatch, tile, m, n, k):
+    """Ragged against every tile shape (tests/kernels/test_mpp_linear.py:8-43 shape)."""
+    if tile != "auto":
+        monkeypatch.setenv("KX355_GEMM_TILE", tile)
+    x, w, b = _linear_case(m, n, k, m + n + k, device)
+    got = _np(mpp_linear.linear(_bf(x, device), _bf(w, device), _bf(b, device), transposed=True))
+    assert _gemm_close(got, oracle.linear(x, w, b))
+    got_nb = _np(mpp_linear.linear(_bf(x, device), _bf(w, device), None, transposed=True))
+    assert _gemm_close(got_nb, oracle.linear(x, w))
+
+
+def test_linear_takes_in_out_weights(device):
+    x, w, b = _linear_case(64, 48, 32, 3, device)
+    got = _np(mpp_linear.linear(_bf(x, device), _bf(w.T, device), _bf(b, device), transposed=False))
+    assert _gemm_close(got, oracle.linear(x, w, b))
+
+
+@pytest.mark.parametrize("act", ["gelu_tanh", "silu", "sigmoid2"])
+def test_linear_activation_epilogues(device, act):
+    x, w, b = _linear_case(130, 200, 256, 4, device, scale=4.0)
+    got = _np(mpp_linear.fused_linear(_bf(x, device), _bf(w, device), _bf(b, device), activation=act))
+    lin = oracle.linear(x, w, b)
+    ref = {"gelu_tanh": oracle.gelu_approx, "silu": oracle.silu,
+           "sigmoid2": lambda v: 2.0 / (1.0 + np.exp(-v))}[act](lin)
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0**-7 + 2e-4 * np.abs(ref).max() + 1e-6)
+
+
+def test_linear_gated_residual_epilogue(device):
+    x, w, b = _linear_case(2 * 70, 96, 128, 5, device)
+    r = _rng(6)
+    resid = oracle.to_bf16(r.standard_normal((2, 70, 96)).astype(F32))
+    gate = r.standard_normal((2, 1, 96)).astype(F32)
+    got = _np(mpp_linear.fused_linear(_bf(x.reshape(2, 70, 128), device), _bf(w, device), _bf(b, device),
+                                      residual=_bf(resid, device), gate=_f32(gate, device)))
+    ref = oracle.gated_residual(resid, oracle.linear(x, w, b).reshape(2, 70, 96), gate)
+    assert _gemm_close(got, ref)
+
+
+@pytest.mark.parametrize("bad", [float("nan"), float("inf")])
+def test_linear_non_finite_inputs_stay_non_finite(device, bad):
+    """tests/kernels/test_mpp_linear.py:76-85."""
+    x, w, b = _linear_case(64, 64, 64, 7, device)
+    x[0] = bad
+    got = _np(mpp_linear.linear(_bf(x, device), _bf(w, device), _bf(b, device), transposed=True))
+    assert not np.any(np.isfinite(got[0]))
+    assert np.all(np.isfinite(got[1:]))
+
+
+def test_linear_rows_adds_the_residual_after_the_product(device):
+    x, w, b = _linear_case(70, 96, 64, 8, device)
+    resid = oracle.to_bf16(_rng(8).standard_normal((70, 96)).astype(F32))
+    got = _np(mpp_linear.linear_rows(_bf(x, device), _bf(w, device), _bf(b, device), residual=_bf(resid, device)))
+    ref = resid + oracle.to_bf16(oracle.linear(x, w, b))
+    assert _gemm_close(got, ref)
+
+
+# ---- attention -----------------------------------------------------------------------------------
+
+
+def _attn_inputs(tq, tk, dim, heads, seed):
+    r = _rng(seed)
+    return tuple(oracle.to_bf16(r.standard_normal((t, heads * dim)).astype(F32)) for t in (tq, tk, tk))
+
+
+@pytest.mark.parametrize("dim", [64, 128])
+@pytest.mark.parametrize(("tq", "tk"), [(7, 7), (16, 16), (33, 33), (517, 517), (300, 1024), (1, 300), (517, 33), (40, 5)])
+def test_attention_matches_oracle_across_tile_edges(device, dim, tq, tk):
+    """tests/models/ltx2/test_dense_attention.py:49-64: relative L2 < 6e-3 for bf16."""
+    q, k, v = _attn_inputs(tq, tk, dim, 2, tq + tk + dim)
+    got = dense_attention.dense_attention(_bf(q, device), _bf(k, device), _bf(v, device), heads=2)
+    assert got.dtype == torch.bfloat16 and tuple(got.shape) == q.shape
+    assert rel_l2(_np(got), oracle.attention(q, k, v, heads=2)) < 6e-3
+
+
+def test_keys_past_a_partial_tile_take_no_weight(device):
+    """tests/models/ltx2/test_dense_attention.py:67-76: a sentinel key one past the end."""
+    q, k, v = _attn_inputs(9, 17, 128, 2, 3)
+    kp = np.concatenate([k, np.full((1, k.shape[1]), 8.0, F32)])
+    vp = np.concatenate([v, np.full((1, v.shape[1]), 1000.0, F32)])
+    kd, vd = _bf(kp, device), _bf(vp, device)
+    got = dense_attention.dense_attention(_bf(q, device), kd[:17], vd[:17], heads=2)
+    assert rel_l2(_np(got), oracle.attention(q, k, v, heads=2)) < 6e-3
+
+
+def test_attention_large_values_stay_finite(device):
+    """bf16 values beyond fp16's range (test_dense_attention.py:79-83) need no saturation here."""
+    q, k, v = _attn_inputs(64, 64, 128, 2, 4)
+    v[0] = 1e5
+    got = _np(dense_attention.dense_attention(_bf(q, device), _bf(k, device), _bf(v, device), heads=2))
+    assert np.all(np.isfinite(got))
+    assert rel_l2(got, oracle.attention(q, k, oracle.to_bf16(v), heads=2)) < 6e-3
+
+
+def test_attention_gate_batch_and_strided_inputs(device):
+    r = _rng(12)
+    b, t, tk, heads, dim = 2, 70, 45, 4, 128
+    width = heads * dim
+    qkv = oracle.to_bf16(r.standard_normal((b, t, 3 * width)).astype(F32))
+    kv = oracle.to_bf16(r.standard_normal((b, tk, 2 * width)).astype(F32))
+    gate = oracle.to_bf16(r.uniform(0, 2, (b, t, heads)).astype(F32))
+    qkv_d, kv_d = _bf(qkv, device), _bf(kv, device)
+    got = dense_attention.batched_attention(qkv_d[..., :width], kv_d[..., :width], kv_d[..., width:], heads=heads,
+                                            gate=_bf(gate, device))
+    for i in range(b):
+        ref = oracle.attention(qkv[i, :, :width], kv[i, :, :width], kv[i, :, width:], heads=heads)
+        ref = (ref.reshape(t, heads, dim) * gate[i][:, :, None]).reshape(t, width)
+        assert rel_l2(_np(got[i]), ref) < 6e-3
+
+
+def test_attention_self_attention_at_ltx_width(device):
+    q, k, v = _attn_inputs(1100, 1100, 128, 32, 13)
+    got = dense_attention.dense_attention(_bf(q, device), _bf(k, device), _bf(v, device), heads=32)
+    ref = oracle.attention(q, k, v, heads=32)
+    assert rel_l2(_np(got), ref) < 6e-3 and cosine(_np(got), ref) > 0.9999
+
+
+# ---- affine int4 / int8 ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_dequant_is_bit_exact(device, bits):
+    r = _rng(20 + bits)
+    n, k = 96, 512
+    codes = r.integers(0, 1 << bits, (n, k))
+    words = oracle.pack_affine(codes, bits)
+    scales = oracle.to_bf16((np.abs(r.standard_normal((n, k // 64))) * 0.003 + 1e-5).astype(F32))
+    biases = oracle.to_bf16((r.standard_normal((n, k // 64)) * 0.05).astype(F32))
+    wq = torch.from_numpy(words.view(np.int32)).to(device)
+    got = quantized.dequantize(wq, _bf(scales, device), _bf(biases, device), group_size=64, bits=bits)
+    ref = oracle.dequantize_affine(words, scales, biases, group_size=64, bits=bits)
+    assert np.array_equal(_np(got), ref)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_gpu_quantizer_is_bit_identical_to_the_oracle(device, bits):
+    w = oracle.to_bf16((_rng(30).standard_normal((128, 1024)) * 0.02).astype(F32))
+    words, scales, biases = quantized.quantize(_bf(w, device), 64, bits)
+    o_words, o_scales, o_biases = oracle.quantize_affine(w, 64, bits)
+    assert np.array_equal(words.cpu().numpy().view(np.uint32), o_words)
+    assert np.array_equal(_np(scales), o_scales) and np.array_equal(_np(biases), o_biases)
+
+
+@pytest.mark.parametrize("tile", ["auto", "0", "2", "3"])
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize(("m", "n", "k"), [(300, 520, 1024), (9, 64, 256)])
+def test_quantized_linear_matches_oracle(device, monkeypatch, tile, bits, m, n, k):
+    if tile != "auto":
+        monkeypatch.setenv("KX355_GEMM_TILE", tile)
+    r = _rng(m + n + bits)
+    x = oracle.to_bf16((r.standard_normal((m, k)) * 0.5).astype(F32))
+    w = oracle.to_bf16((r.standard_normal((n, k)) * 0.02).astype(F32))
+    b = oracle.to_bf16((r.standard_normal(n) * 0.02).astype(F32))
+    words, scales, biases = oracle.quantize_affine(w, 64, bits)
+    layer = quantized.QuantizedLinear(torch.from_numpy(words.view(np.int32)).to(device), _bf(scales, device),
+                                      _bf(biases, device), _bf(b, device), group_size=64, bits=bits)
+    got = _np(layer(_bf(x, device)))
+    ref = oracle.quantized_linear(x, words, scales, biases, b, group_size=64, bits=bits)
+    assert _gemm_close(got, ref)
+    # the dequantized weight through the dense kernel gives the same product
+    dense = _np(mpp_linear.linear(_bf(x, device), quantized.dequantize(layer.weight, layer.scales, layer.biases,
+                                                                       bits=bits), _bf(b, device), transposed=True))
+    assert max_abs(got, dense) <= 2.0**-7 * np.abs(dense).max()
+
+
+def test_env_tile_override_is_restored():
+    assert os.environ.get("KX355_GEMM_TILE") in (None, "")
