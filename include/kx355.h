@@ -32,8 +32,8 @@ enum {
 /* Element type of tensors that may be fp32 or bf16. */
 enum { KX_F32 = 0, KX_BF16 = 1 };
 
-/* Norm kinds for kx_adaln_norm_bf16. */
-enum { KX_NORM_RMS = 0, KX_NORM_LAYER = 1 };
+/* Norm kinds for kx_adaln_norm_bf16; KX_NORM_IN_F32 may be or-ed in for an fp32 input. */
+enum { KX_NORM_RMS = 0, KX_NORM_LAYER = 1, KX_NORM_IN_F32 = 1 << 4 };
 
 /* RoPE kinds for kx_rmsnorm_rope_bf16. */
 enum { KX_ROPE_NONE = 0, KX_ROPE_SPLIT = 1, KX_ROPE_PAIR = 2 };
@@ -44,7 +44,9 @@ enum {
   KX_EPI_ACT_GELU_TANH = 1 << 4,
   KX_EPI_ACT_SILU = 2 << 4,
   KX_EPI_ACT_SIGMOID2 = 3 << 4, /* 2 * sigmoid(.) — LTX gate logits */
-  KX_EPI_GATED_RESIDUAL = 1 << 8 /* c = resid + gate[col] * act(acc + bias) */
+  KX_EPI_GATED_RESIDUAL = 1 << 8, /* c = resid + gate[col] * act(acc + bias) */
+  KX_EPI_RESID_F32 = 1 << 9,      /* resid is fp32 (a residual stream carried in fp32) */
+  KX_EPI_OUT_F32 = 1 << 10        /* c is fp32 */
 };
 
 int kx_abi_version(void);
@@ -60,7 +62,8 @@ const char* kx_last_error(void);
  *     replaces flux2 normalized (kinomlx/models/flux2/transformer.py:56-57).
  * shift/scale are fp32 rows of `dim`; row r of x uses modulation row (r / mod_div) at
  * mod_stride elements per row (mod_stride 0 broadcasts one row). shift == scale == NULL gives
- * the plain norm (fused_ops.rms_norm(weight=None)).
+ * the plain norm (fused_ops.rms_norm(weight=None)). With KX_NORM_IN_F32 in `kind`, x is fp32
+ * (the block's residual stream); y is always bf16.
  */
 int kx_adaln_norm_bf16(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows,
                        int64_t dim, const float* shift, const float* scale, int64_t mod_div,
@@ -131,8 +134,10 @@ int kx_attention_fwd_bf16(const void* q, int64_t ldq, const void* k, int64_t ldk
  * kinomlx/models/ltx2/transformer/attention.py:41-109, kinomlx/modeling/layers.py).
  *   a: (m, k) at lda; w: (n, k) at ldw — the reference's (out, in) layout; c: (m, n) at ldc.
  *   bias: bf16 (n) with KX_EPI_BIAS. Activations per KX_EPI_ACT_*.
- *   KX_EPI_GATED_RESIDUAL: c = resid + gate * act(acc + bias), resid bf16 (m, n) at ldr, gate
- *   fp32 row (r / gate_div) at gate_stride (0 broadcasts). c may alias resid.
+ *   KX_EPI_GATED_RESIDUAL: c = resid + gate * act(acc + bias), resid (m, n) at ldr, gate
+ *   fp32 row (r / gate_div) at gate_stride (0 broadcasts). c may alias resid when both have
+ *   the same element type. resid is bf16, or fp32 with KX_EPI_RESID_F32; c is bf16, or fp32
+ *   with KX_EPI_OUT_F32 (fp32 operands need 16-byte aligned rows).
  * Requires k % 8 == 0, lda/ldw % 8 == 0 and 16-byte aligned a/w.
  */
 int kx_gemm_bf16(const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias,

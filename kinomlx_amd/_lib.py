@@ -27,6 +27,7 @@ KX_F32 = 0
 KX_BF16 = 1
 KX_NORM_RMS = 0
 KX_NORM_LAYER = 1
+KX_NORM_IN_F32 = 1 << 4
 KX_ROPE_NONE = 0
 KX_ROPE_SPLIT = 1
 KX_ROPE_PAIR = 2
@@ -35,6 +36,8 @@ EPI_ACT_GELU_TANH = 1 << 4
 EPI_ACT_SILU = 2 << 4
 EPI_ACT_SIGMOID2 = 3 << 4
 EPI_GATED_RESIDUAL = 1 << 8
+EPI_RESID_F32 = 1 << 9
+EPI_OUT_F32 = 1 << 10
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -190,16 +193,29 @@ def _mod_rows(vec: torch.Tensor, rows: int, width: int, name: str) -> tuple[int,
 # ---- launches -----------------------------------------------------------------------------------
 
 
+def _shared_mod_rows(shift, scale, rows: int, width: int, name: str) -> tuple[int, int]:
+    """The one (mod_div, mod_stride) layout that ``shift`` and ``scale`` must share: the
+    kernels index both with it."""
+    layout = _mod_rows(shift, rows, width, f"{name} shift")
+    if _mod_rows(scale, rows, width, f"{name} scale") != layout:
+        raise ValueError(f"{name}: shift and scale must share one layout")
+    return layout
+
+
 def launch_adaln_norm(x, out, shift, scale, eps: float, kind: int) -> None:
+    """``x`` is bf16 or fp32 (a residual stream carried in fp32); ``out`` is bf16."""
     _check_gpu("adaln_norm", x, out, shift, scale)
+    if x.dtype == torch.float32:
+        kind |= KX_NORM_IN_F32
+    elif x.dtype != torch.bfloat16:
+        raise ValueError(f"adaln_norm: x must be bfloat16 or float32, got {x.dtype}")
+    if out.dtype != torch.bfloat16:
+        raise ValueError("adaln_norm: the output is bfloat16")
     rows, dim, ldx = _rows(x, "adaln_norm x")
     _, _, ldy = _rows(out, "adaln_norm out")
     div, stride = (1, 0)
     if shift is not None:
-        div, stride = _mod_rows(shift, rows, dim, "adaln_norm shift")
-        div2, stride2 = _mod_rows(scale, rows, dim, "adaln_norm scale")
-        if (div, stride) != (div2, stride2):
-            raise ValueError("adaln_norm: shift and scale must share one layout")
+        div, stride = _shared_mod_rows(shift, scale, rows, dim, "adaln_norm")
     _call(
         "kx_adaln_norm_bf16", _ptr(x), ldx, _ptr(out), ldy, rows, dim, _ptr(shift), _ptr(scale),
         div, stride, eps, kind, _stream(),
@@ -261,8 +277,24 @@ def launch_attention(q, k, v, out, *, batch, tq, tk, heads, head_dim, scale, gat
     )
 
 
+def _dtype_flags(out, resid, name: str) -> int:
+    """Epilogue flags for an fp32 output and an fp32 residual (bf16 otherwise)."""
+    flags = 0
+    if out.dtype == torch.float32:
+        flags |= EPI_OUT_F32
+    elif out.dtype != torch.bfloat16:
+        raise ValueError(f"{name}: the output must be bfloat16 or float32, got {out.dtype}")
+    if resid is not None:
+        if resid.dtype == torch.float32:
+            flags |= EPI_RESID_F32
+        elif resid.dtype != torch.bfloat16:
+            raise ValueError(f"{name}: the residual must be bfloat16 or float32, got {resid.dtype}")
+    return flags
+
+
 def launch_gemm(a, w, out, *, bias=None, flags: int = 0, resid=None, gate=None) -> None:
     _check_gpu("gemm", a, w, out, bias, resid, gate)
+    flags |= _dtype_flags(out, resid, "linear")
     m, k, lda = _rows(a, "linear input")
     n, kw, ldw = _rows(w, "linear weight")
     if kw != k:
@@ -281,6 +313,7 @@ def launch_gemm(a, w, out, *, bias=None, flags: int = 0, resid=None, gate=None) 
 def launch_qgemm(a, words, scales, biases, out, *, n, k, group_size, bits, bias=None,
                  flags: int = 0, resid=None, gate=None) -> None:
     _check_gpu("qgemm", a, words, scales, biases, out, bias, resid, gate)
+    flags |= _dtype_flags(out, resid, "quantized linear")
     m, ka, lda = _rows(a, "quantized linear input")
     if ka != k:
         raise ValueError(f"quantized linear: input width {ka} does not match {k}")
@@ -322,7 +355,7 @@ def launch_modulate(x, out, shift, scale) -> None:
     _check_gpu("modulate", x, out, shift, scale)
     rows, dim, ldx = _rows(x, "modulate x")
     _, _, ldy = _rows(out, "modulate out")
-    div, stride = _mod_rows(shift, rows, dim, "modulate shift")
+    div, stride = _shared_mod_rows(shift, scale, rows, dim, "modulate")
     _call(
         "kx_modulate_bf16", _ptr(x), ldx, _ptr(out), ldy, rows, dim, _ptr(shift), _ptr(scale),
         div, stride, _stream(),

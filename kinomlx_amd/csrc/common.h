@@ -40,28 +40,32 @@ __device__ __forceinline__ uint4 pack8(const float* v) {
 }
 
 // ---- activations (fp32 opmath) -----------------------------------------------------------------
-// tanh GELU with the inner argument clamped to +-10 (kinomlx/kernels/fused_ops.py:27-35).
-__device__ __forceinline__ float gelu_tanh(float x) {
+// tanh GELU with the inner argument clamped to +-10 (kinomlx/kernels/fused_ops.py:27-35), through
+// the identity 0.5 x (1 + tanh(u)) = x * sigmoid(2u) = x / (1 + e^(-2u)). The tanh form cancels in
+// 1 + tanh(u) for negative u (at x = -3 an ulp of tanh is ~70 ulps of the result, so last-bit
+// differences between tanh implementations flip bf16 roundings); the sigmoid form has no
+// cancellation and stays within a few fp32 ulps of the exact function everywhere.
+__device__ __forceinline__ float gelu_inner(float x) {
   const float inner = 0.7978845608028654f * (x + 0.044715f * (x * x * x));
-  return 0.5f * x * (1.0f + tanhf(fminf(fmaxf(inner, -10.0f), 10.0f)));
+  return fminf(fmaxf(inner, -10.0f), 10.0f);
+}
+__device__ __forceinline__ float gelu_tanh(float x) {
+  return x / (1.0f + expf(-2.0f * gelu_inner(x)));
 }
 // x / (1 + exp(-x)) (kinomlx/kernels/fused_ops.py:40-45).
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
 
 // Call-free forms for epilogues that hold many live accumulators: a libm call there would force
-// every live register to be saved around it. exp via v_exp_f32 (exp2), tanh(u) = 1 - 2 / (e^2u + 1)
-// (saturates to +-1 for large |u|, no inf/inf).
+// every live register to be saved around it. exp via v_exp_f32 (exp2), division via v_rcp_f32.
 __device__ __forceinline__ float fast_exp(float x) {
   return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
 }
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 __device__ __forceinline__ float fast_gelu_tanh(float x) {
-  float inner = 0.7978845608028654f * (x + 0.044715f * (x * x * x));
-  inner = fminf(fmaxf(inner, -10.0f), 10.0f);
-  const float t = 1.0f - 2.0f / (fast_exp(2.0f * inner) + 1.0f);
-  return 0.5f * x * (1.0f + t);
+  return x * fast_rcp(1.0f + fast_exp(-2.0f * gelu_inner(x)));
 }
-__device__ __forceinline__ float fast_silu(float x) { return x / (1.0f + fast_exp(-x)); }
-__device__ __forceinline__ float fast_sigmoid2(float x) { return 2.0f / (1.0f + fast_exp(-x)); }
+__device__ __forceinline__ float fast_silu(float x) { return x * fast_rcp(1.0f + fast_exp(-x)); }
+__device__ __forceinline__ float fast_sigmoid2(float x) { return 2.0f * fast_rcp(1.0f + fast_exp(-x)); }
 
 // ---- wave reductions (wave64) -------------------------------------------------------------------
 template <int WIDTH>

@@ -29,7 +29,7 @@ constexpr int ROWB = BK * 2;  // bytes per LDS tile row
 
 struct Epilogue {
   const uint16_t* bias;
-  const uint16_t* resid;
+  const void* resid;  // bf16, or fp32 with KX_EPI_RESID_F32
   int64_t ldr;
   const float* gate;
   int64_t gate_div;
@@ -75,7 +75,7 @@ __device__ __forceinline__ uint4 dequant8(const uint32_t* wd, float s, float b) 
 template <int BM, int BN, int WM, int WN, int QB>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ W, int64_t ldw,
-    QuantW qw, uint16_t* __restrict__ C, int64_t ldc, int M, int N, int K, Epilogue epi) {
+    QuantW qw, void* __restrict__ C, int64_t ldc, int M, int N, int K, Epilogue epi) {
   constexpr int NT = WM * WN * 64;
   constexpr int WT_M = BM / WM, WT_N = BN / WN;
   constexpr int MB = WT_M / 32, NB = WT_N / 32;
@@ -210,6 +210,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(
   const int act = (epi.flags >> 4) & 15;
   const bool has_bias = epi.flags & KX_EPI_BIAS;
   const bool gated = epi.flags & KX_EPI_GATED_RESIDUAL;
+  const bool resid_f32 = epi.flags & KX_EPI_RESID_F32;
+  const bool out_f32 = epi.flags & KX_EPI_OUT_F32;
   const bool vec_store = (ldc % 4 == 0) && (!gated || epi.ldr % 4 == 0);
   const int col4 = (lane & 7) * 4;
 #pragma unroll
@@ -240,27 +242,45 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(
       float v[4] = {a4.x + bias4[0], a4.y + bias4[1], a4.z + bias4[2], a4.w + bias4[3]};
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] = apply_act(v[e], act);
+      const int64_t ro = (int64_t)m * epi.ldr + n;
+      const int64_t co = (int64_t)m * ldc + n;
       if (vec_store && n + 3 < N) {
         if (gated) {
           const float* grow = epi.gate + (m / epi.gate_div) * epi.gate_stride;
-          const uint2 rr = *reinterpret_cast<const uint2*>(epi.resid + (int64_t)m * epi.ldr + n);
           const float4 gv = *reinterpret_cast<const float4*>(grow + n);
-          v[0] = lo_f(rr.x) + gv.x * v[0];
-          v[1] = hi_f(rr.x) + gv.y * v[1];
-          v[2] = lo_f(rr.y) + gv.z * v[2];
-          v[3] = hi_f(rr.y) + gv.w * v[3];
+          float rv[4];
+          if (resid_f32) {
+            const float4 rr = *reinterpret_cast<const float4*>(static_cast<const float*>(epi.resid) + ro);
+            rv[0] = rr.x; rv[1] = rr.y; rv[2] = rr.z; rv[3] = rr.w;
+          } else {
+            const uint2 rr = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(epi.resid) + ro);
+            rv[0] = lo_f(rr.x); rv[1] = hi_f(rr.x); rv[2] = lo_f(rr.y); rv[3] = hi_f(rr.y);
+          }
+          v[0] = rv[0] + gv.x * v[0];
+          v[1] = rv[1] + gv.y * v[1];
+          v[2] = rv[2] + gv.z * v[2];
+          v[3] = rv[3] + gv.w * v[3];
         }
-        uint2 o;
-        o.x = pack2(v[0], v[1]);
-        o.y = pack2(v[2], v[3]);
-        *reinterpret_cast<uint2*>(C + (int64_t)m * ldc + n) = o;
+        if (out_f32) {
+          *reinterpret_cast<float4*>(static_cast<float*>(C) + co) = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+          uint2 o;
+          o.x = pack2(v[0], v[1]);
+          o.y = pack2(v[2], v[3]);
+          *reinterpret_cast<uint2*>(static_cast<uint16_t*>(C) + co) = o;
+        }
       } else {
         for (int e = 0; e < 4 && n + e < N; ++e) {
           float x = v[e];
-          if (gated)
-            x = bf2f(epi.resid[(int64_t)m * epi.ldr + n + e]) +
-                epi.gate[(m / epi.gate_div) * epi.gate_stride + n + e] * x;
-          C[(int64_t)m * ldc + n + e] = f2bf(x);
+          if (gated) {
+            const float rv = resid_f32 ? static_cast<const float*>(epi.resid)[ro + e]
+                                       : bf2f(static_cast<const uint16_t*>(epi.resid)[ro + e]);
+            x = rv + epi.gate[(m / epi.gate_div) * epi.gate_stride + n + e] * x;
+          }
+          if (out_f32)
+            static_cast<float*>(C)[co + e] = x;
+          else
+            static_cast<uint16_t*>(C)[co + e] = f2bf(x);
         }
       }
     }
@@ -291,7 +311,7 @@ enum TileCfg { T256x256 = 0, T256x128 = 1, T128x128 = 2, T64x64 = 3, T128x64 = 4
 
 template <int BM, int BN, int WM, int WN, int QB>
 int launch_cfg(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, QuantW qw,
-               uint16_t* c, int64_t ldc, int m, int n, int k, const Epilogue& epi,
+               void* c, int64_t ldc, int m, int n, int k, const Epilogue& epi,
                hipStream_t s) {
   const int tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
   gemm_kernel<BM, BN, WM, WN, QB><<<tiles, WM * WN * 64, 0, s>>>(a, lda, w, ldw, qw, c, ldc, m, n,
@@ -320,7 +340,7 @@ int pick_cfg(int64_t m, int64_t n) {
 
 template <int QB>
 int dispatch(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, QuantW qw,
-             uint16_t* c, int64_t ldc, int64_t m, int64_t n, int64_t k, const Epilogue& epi,
+             void* c, int64_t ldc, int64_t m, int64_t n, int64_t k, const Epilogue& epi,
              hipStream_t s) {
   switch (pick_cfg(m, n)) {
     case T256x256:
@@ -341,19 +361,28 @@ int dispatch(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, Qua
   }
 }
 
-int check_epilogue(const char* name, int epilogue, const void* bias, const void* resid,
-                   int64_t ldr, int64_t n, const float* gate, int64_t gate_div,
-                   int64_t gate_stride) {
+int check_epilogue(const char* name, int epilogue, const void* bias, const void* c,
+                   int64_t ldc, const void* resid, int64_t ldr, int64_t n, const float* gate,
+                   int64_t gate_div, int64_t gate_stride) {
   const int act = (epilogue >> 4) & 15;
-  KX_REQUIRE((epilogue & ~(KX_EPI_BIAS | (15 << 4) | KX_EPI_GATED_RESIDUAL)) == 0 && act <= 3,
-             "%s: bad epilogue flags %d", name, epilogue);
+  const int known = KX_EPI_BIAS | (15 << 4) | KX_EPI_GATED_RESIDUAL | KX_EPI_RESID_F32 |
+                    KX_EPI_OUT_F32;
+  KX_REQUIRE((epilogue & ~known) == 0 && act <= 3, "%s: bad epilogue flags %d", name, epilogue);
   KX_REQUIRE(!(epilogue & KX_EPI_BIAS) || (bias && aligned8(bias)), "%s: bias missing or unaligned",
              name);
+  KX_REQUIRE(!(epilogue & KX_EPI_OUT_F32) || (aligned16(c) && ldc % 4 == 0),
+             "%s: an fp32 output needs 16-byte aligned rows", name);
+  KX_REQUIRE(!(epilogue & KX_EPI_RESID_F32) || (epilogue & KX_EPI_GATED_RESIDUAL),
+             "%s: KX_EPI_RESID_F32 without a gated residual", name);
   if (epilogue & KX_EPI_GATED_RESIDUAL) {
     KX_REQUIRE(resid && gate && ldr >= n && gate_div > 0 && gate_stride >= 0,
                "%s: gated residual needs resid, ldr >= n and gate rows", name);
-    KX_REQUIRE(aligned8(resid) && aligned16(gate) && gate_stride % 4 == 0,
-               "%s: resid must be 8-byte and gate 16-byte aligned", name);
+    KX_REQUIRE(aligned16(gate) && gate_stride % 4 == 0, "%s: gate must be 16-byte aligned", name);
+    if (epilogue & KX_EPI_RESID_F32)
+      KX_REQUIRE(aligned16(resid) && ldr % 4 == 0, "%s: an fp32 residual needs 16-byte aligned rows",
+                 name);
+    else
+      KX_REQUIRE(aligned8(resid), "%s: resid must be 8-byte aligned", name);
   }
   return KX_OK;
 }
@@ -377,14 +406,13 @@ extern "C" int kx_gemm_bf16(const void* a, int64_t lda, const void* w, int64_t l
              (long long)k, (long long)lda, (long long)ldw);
   KX_REQUIRE(aligned16(a) && aligned16(w) && aligned8(c), "kx_gemm_bf16: a/w must be 16-byte "
              "and c 8-byte aligned");
-  const int rc = check_epilogue("kx_gemm_bf16", epilogue, bias, resid, ldr, n, gate, gate_div,
-                                gate_stride);
+  const int rc = check_epilogue("kx_gemm_bf16", epilogue, bias, c, ldc, resid, ldr, n, gate,
+                                gate_div, gate_stride);
   if (rc) return rc;
   if (m == 0 || n == 0) return KX_OK;
-  const Epilogue epi{(const uint16_t*)bias, (const uint16_t*)resid, ldr, gate, gate_div,
-                     gate_stride, epilogue};
-  dispatch<0>((const uint16_t*)a, lda, (const uint16_t*)w, ldw, QuantW{}, (uint16_t*)c, ldc, m, n,
-              k, epi, (hipStream_t)stream);
+  const Epilogue epi{(const uint16_t*)bias, resid, ldr, gate, gate_div, gate_stride, epilogue};
+  dispatch<0>((const uint16_t*)a, lda, (const uint16_t*)w, ldw, QuantW{}, c, ldc, m, n, k, epi,
+              (hipStream_t)stream);
   return check_launch("kx_gemm_bf16");
 }
 
@@ -402,19 +430,16 @@ extern "C" int kx_qgemm_affine_bf16(const void* a, int64_t lda, const uint32_t* 
              "kx_qgemm_affine_bf16: bad shape (k must be a multiple of 64)");
   KX_REQUIRE(lda % 8 == 0 && lda >= k && ldc >= n && aligned16(a) && aligned8(c),
              "kx_qgemm_affine_bf16: bad stride or alignment");
-  const int rc = check_epilogue("kx_qgemm_affine_bf16", epilogue, bias, resid, ldr, n, gate,
-                                gate_div, gate_stride);
+  const int rc = check_epilogue("kx_qgemm_affine_bf16", epilogue, bias, c, ldc, resid, ldr, n,
+                                gate, gate_div, gate_stride);
   if (rc) return rc;
   if (m == 0 || n == 0) return KX_OK;
-  const Epilogue epi{(const uint16_t*)bias, (const uint16_t*)resid, ldr, gate, gate_div,
-                     gate_stride, epilogue};
+  const Epilogue epi{(const uint16_t*)bias, resid, ldr, gate, gate_div, gate_stride, epilogue};
   const QuantW qw{wq, (const uint16_t*)scales, (const uint16_t*)biases};
   if (bits == 4)
-    dispatch<4>((const uint16_t*)a, lda, nullptr, 0, qw, (uint16_t*)c, ldc, m, n, k, epi,
-                (hipStream_t)stream);
+    dispatch<4>((const uint16_t*)a, lda, nullptr, 0, qw, c, ldc, m, n, k, epi, (hipStream_t)stream);
   else
-    dispatch<8>((const uint16_t*)a, lda, nullptr, 0, qw, (uint16_t*)c, ldc, m, n, k, epi,
-                (hipStream_t)stream);
+    dispatch<8>((const uint16_t*)a, lda, nullptr, 0, qw, c, ldc, m, n, k, epi, (hipStream_t)stream);
   return check_launch("kx_qgemm_affine_bf16");
 }
 

@@ -15,22 +15,39 @@ constexpr int kWaves = 4;  // rows per 256-thread workgroup
 // ----------------------------------------------------------------------------------------------
 // Modulated RMSNorm / LayerNorm: y = norm(x) * (1 + scale) + shift.
 
-template <int VPL, int KIND, bool MOD>
+// Loads 8 consecutive elements of a bf16 or fp32 row (16-byte aligned) as fp32.
+template <bool XF32>
+__device__ __forceinline__ void load8(const void* row, int64_t col, float* v) {
+  if (XF32) {
+    const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(row) + col);
+    const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(row) + col + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+    unpack8(*reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(row) + col), v);
+  }
+}
+
+template <bool XF32>
+__device__ __forceinline__ float load1(const void* row, int64_t col) {
+  return XF32 ? static_cast<const float*>(row)[col] : bf2f(static_cast<const uint16_t*>(row)[col]);
+}
+
+// XF32: x is fp32 (a residual stream carried in fp32); y is always bf16.
+template <int VPL, int KIND, bool MOD, bool XF32>
 __global__ __launch_bounds__(256) void adaln_norm_kernel(
-    const uint16_t* __restrict__ x, int64_t ldx, uint16_t* __restrict__ y, int64_t ldy,
+    const void* __restrict__ x, int64_t ldx, uint16_t* __restrict__ y, int64_t ldy,
     int64_t rows, const float* __restrict__ shift, const float* __restrict__ scale,
     int64_t mod_div, int64_t mod_stride, float eps) {
   constexpr int DIM = VPL * 512;
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const uint16_t* xr = x + row * ldx;
+  const void* xr = XF32 ? (const void*)(static_cast<const float*>(x) + row * ldx)
+                        : (const void*)(static_cast<const uint16_t*>(x) + row * ldx);
   float v[VPL][8];
 #pragma unroll
-  for (int i = 0; i < VPL; ++i) {
-    const uint4 w = *reinterpret_cast<const uint4*>(xr + (i * 64 + lane) * 8);
-    unpack8(w, v[i]);
-  }
+  for (int i = 0; i < VPL; ++i) load8<XF32>(xr, (i * 64 + lane) * 8, v[i]);
   float mean = 0.0f;
   if (KIND == KX_NORM_LAYER) {
     float s = 0.0f;
@@ -72,24 +89,25 @@ __global__ __launch_bounds__(256) void adaln_norm_kernel(
   }
 }
 
-template <int KIND>
+template <int KIND, bool XF32>
 __global__ __launch_bounds__(256) void adaln_norm_generic(
-    const uint16_t* __restrict__ x, int64_t ldx, uint16_t* __restrict__ y, int64_t ldy,
+    const void* __restrict__ x, int64_t ldx, uint16_t* __restrict__ y, int64_t ldy,
     int64_t rows, int64_t dim, const float* __restrict__ shift, const float* __restrict__ scale,
     int64_t mod_div, int64_t mod_stride, float eps) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const uint16_t* xr = x + row * ldx;
+  const void* xr = XF32 ? (const void*)(static_cast<const float*>(x) + row * ldx)
+                        : (const void*)(static_cast<const uint16_t*>(x) + row * ldx);
   float mean = 0.0f;
   if (KIND == KX_NORM_LAYER) {
     float s = 0.0f;
-    for (int64_t c = lane; c < dim; c += 64) s += bf2f(xr[c]);
+    for (int64_t c = lane; c < dim; c += 64) s += load1<XF32>(xr, c);
     mean = wave_sum<64>(s) / (float)dim;
   }
   float ss = 0.0f;
   for (int64_t c = lane; c < dim; c += 64) {
-    const float d = bf2f(xr[c]) - mean;
+    const float d = load1<XF32>(xr, c) - mean;
     ss = fmaf(d, d, ss);
   }
   const float inv = rsqrtf(wave_sum<64>(ss) / (float)dim + eps);
@@ -97,7 +115,7 @@ __global__ __launch_bounds__(256) void adaln_norm_generic(
   const int64_t mrow = mod ? (row / mod_div) * mod_stride : 0;
   uint16_t* yr = y + row * ldy;
   for (int64_t c = lane; c < dim; c += 64) {
-    float o = (bf2f(xr[c]) - mean) * inv;
+    float o = (load1<XF32>(xr, c) - mean) * inv;
     if (mod) o = o * (1.0f + scale[mrow + c]) + shift[mrow + c];
     yr[c] = f2bf(o);
   }
@@ -271,17 +289,35 @@ __global__ __launch_bounds__(256) void gated_residual_kernel(
   y[row * ldy + c] = f2bf(base + bf2f(r[row * ldr + c]) * g);
 }
 
-template <int VPL, int KIND>
+template <int VPL, int KIND, bool XF32>
 int launch_adaln(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows,
                  const float* shift, const float* scale, int64_t mod_div, int64_t mod_stride,
                  float eps, hipStream_t s) {
   const dim3 grid((unsigned)((rows + kWaves - 1) / kWaves));
   if (shift)
-    adaln_norm_kernel<VPL, KIND, true><<<grid, 256, 0, s>>>(
-        (const uint16_t*)x, ldx, (uint16_t*)y, ldy, rows, shift, scale, mod_div, mod_stride, eps);
+    adaln_norm_kernel<VPL, KIND, true, XF32><<<grid, 256, 0, s>>>(
+        x, ldx, (uint16_t*)y, ldy, rows, shift, scale, mod_div, mod_stride, eps);
   else
-    adaln_norm_kernel<VPL, KIND, false><<<grid, 256, 0, s>>>(
-        (const uint16_t*)x, ldx, (uint16_t*)y, ldy, rows, shift, scale, mod_div, mod_stride, eps);
+    adaln_norm_kernel<VPL, KIND, false, XF32><<<grid, 256, 0, s>>>(
+        x, ldx, (uint16_t*)y, ldy, rows, shift, scale, mod_div, mod_stride, eps);
+  return check_launch("kx_adaln_norm_bf16");
+}
+
+template <int KIND, bool XF32>
+int dispatch_adaln(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows, int64_t dim,
+                   const float* shift, const float* scale, int64_t mod_div, int64_t mod_stride,
+                   float eps, bool vec, hipStream_t s) {
+  if (vec) {
+    switch (dim / 512) {
+      case 1: return launch_adaln<1, KIND, XF32>(x, ldx, y, ldy, rows, shift, scale, mod_div, mod_stride, eps, s);
+      case 2: return launch_adaln<2, KIND, XF32>(x, ldx, y, ldy, rows, shift, scale, mod_div, mod_stride, eps, s);
+      case 4: return launch_adaln<4, KIND, XF32>(x, ldx, y, ldy, rows, shift, scale, mod_div, mod_stride, eps, s);
+      default: return launch_adaln<8, KIND, XF32>(x, ldx, y, ldy, rows, shift, scale, mod_div, mod_stride, eps, s);
+    }
+  }
+  const dim3 grid((unsigned)((rows + kWaves - 1) / kWaves));
+  adaln_norm_generic<KIND, XF32><<<grid, 256, 0, s>>>(x, ldx, (uint16_t*)y, ldy, rows, dim, shift,
+                                                      scale, mod_div, mod_stride, eps);
   return check_launch("kx_adaln_norm_bf16");
 }
 
@@ -355,38 +391,26 @@ extern "C" int kx_adaln_norm_bf16(const void* x, int64_t ldx, void* y, int64_t l
   KX_REQUIRE((shift == nullptr) == (scale == nullptr),
              "kx_adaln_norm_bf16: shift and scale must both be given or both be null");
   KX_REQUIRE(!shift || (mod_div > 0 && mod_stride >= 0), "kx_adaln_norm_bf16: bad modulation");
+  const bool xf32 = kind & KX_NORM_IN_F32;
+  kind &= ~KX_NORM_IN_F32;
   KX_REQUIRE(kind == KX_NORM_RMS || kind == KX_NORM_LAYER, "kx_adaln_norm_bf16: bad kind");
   if (rows == 0) return KX_OK;
   hipStream_t s = (hipStream_t)stream;
-  const bool vec = dim % 512 == 0 && ldx % 8 == 0 && ldy % 8 == 0 && aligned16(x) &&
-                   aligned16(y) &&
-                   (!shift || (aligned16(shift) && aligned16(scale) && mod_stride % 4 == 0));
   const int64_t vpl = dim / 512;
-  if (vec && (vpl == 1 || vpl == 2 || vpl == 4 || vpl == 8)) {
-#define KX_ADALN(V)                                                                             \
-  return kind == KX_NORM_RMS                                                                    \
-             ? launch_adaln<V, KX_NORM_RMS>(x, ldx, y, ldy, rows, shift, scale, mod_div,       \
-                                            mod_stride, eps, s)                                 \
-             : launch_adaln<V, KX_NORM_LAYER>(x, ldx, y, ldy, rows, shift, scale, mod_div,     \
-                                              mod_stride, eps, s);
-    switch (vpl) {
-      case 1: KX_ADALN(1)
-      case 2: KX_ADALN(2)
-      case 4: KX_ADALN(4)
-      default: KX_ADALN(8)
-    }
-#undef KX_ADALN
-  }
-  const dim3 grid((unsigned)((rows + kWaves - 1) / kWaves));
-  if (kind == KX_NORM_RMS)
-    adaln_norm_generic<KX_NORM_RMS><<<grid, 256, 0, s>>>((const uint16_t*)x, ldx, (uint16_t*)y,
-                                                         ldy, rows, dim, shift, scale, mod_div,
-                                                         mod_stride, eps);
-  else
-    adaln_norm_generic<KX_NORM_LAYER><<<grid, 256, 0, s>>>((const uint16_t*)x, ldx,
-                                                           (uint16_t*)y, ldy, rows, dim, shift,
-                                                           scale, mod_div, mod_stride, eps);
-  return check_launch("kx_adaln_norm_bf16");
+  const bool vec = dim % 512 == 0 && (vpl == 1 || vpl == 2 || vpl == 4 || vpl == 8) &&
+                   ldx % 8 == 0 && ldy % 8 == 0 && aligned16(x) && aligned16(y) &&
+                   (!shift || (aligned16(shift) && aligned16(scale) && mod_stride % 4 == 0));
+  if (xf32)
+    return kind == KX_NORM_RMS
+               ? dispatch_adaln<KX_NORM_RMS, true>(x, ldx, y, ldy, rows, dim, shift, scale,
+                                                   mod_div, mod_stride, eps, vec, s)
+               : dispatch_adaln<KX_NORM_LAYER, true>(x, ldx, y, ldy, rows, dim, shift, scale,
+                                                     mod_div, mod_stride, eps, vec, s);
+  return kind == KX_NORM_RMS
+             ? dispatch_adaln<KX_NORM_RMS, false>(x, ldx, y, ldy, rows, dim, shift, scale,
+                                                  mod_div, mod_stride, eps, vec, s)
+             : dispatch_adaln<KX_NORM_LAYER, false>(x, ldx, y, ldy, rows, dim, shift, scale,
+                                                    mod_div, mod_stride, eps, vec, s);
 }
 
 extern "C" int kx_rmsnorm_rope_bf16(const void* x, int64_t ldx, void* y, int64_t ldy,

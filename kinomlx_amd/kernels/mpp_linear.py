@@ -137,11 +137,14 @@ def fused_linear(
     residual: torch.Tensor | None = None,
     gate: torch.Tensor | None = None,
     out: torch.Tensor | None = None,
+    out_dtype: torch.dtype | None = None,
 ) -> torch.Tensor:
     """``residual + gate * act(value @ W^T + bias)`` in one MFMA pass (``(out, in)`` weight).
 
     ``gate`` is an fp32 row vector ``(n,)``, one per batch ``(B, 1, n)`` or per row; without
-    ``residual`` the epilogue stops after the activation.
+    ``residual`` the epilogue stops after the activation. ``residual`` may be bf16 or fp32 and
+    the output (``out_dtype``, default the input dtype) bf16 or fp32: a residual stream can be
+    carried in fp32 between blocks' branches so that it is rounded once, not once per add.
     """
     w = _as_out_in(weight, True)
     dtype = value.dtype
@@ -152,7 +155,7 @@ def fused_linear(
         raise ValueError(f"linear input width {value.shape[-1]} does not match weight width {k}")
     a = _rows_view(value)
     if out is None:
-        out = torch.empty((*value.shape[:-1], n), dtype=dtype, device=value.device)
+        out = torch.empty((*value.shape[:-1], n), dtype=out_dtype or dtype, device=value.device)
     if a.shape[0] == 0:
         return out
     flags = ACTIVATIONS[activation]

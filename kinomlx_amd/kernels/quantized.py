@@ -113,9 +113,10 @@ def quantized_matmul(
     activation: str | None = None,
     residual: torch.Tensor | None = None,
     gate: torch.Tensor | None = None,
+    out_dtype: torch.dtype | None = None,
 ) -> torch.Tensor:
     """``value @ dequant(weight)^T (+ bias)`` with dequantization inside the MFMA mainloop;
-    ``activation``/``residual``/``gate`` as ``mpp_linear.fused_linear``."""
+    ``activation``/``residual``/``gate``/``out_dtype`` as ``mpp_linear.fused_linear``."""
     if not transpose:
         raise ValueError("the MI355X quantized linear takes the (out, in) packing (transpose=True)")
     quant_defaults(mode, group_size, bits)
@@ -131,7 +132,7 @@ def quantized_matmul(
     a = value.reshape(-1, k)
     if a.stride(-1) != 1 or a.data_ptr() % 16 or a.stride(0) % 8:
         a = a.contiguous()
-    out = torch.empty((*value.shape[:-1], n), dtype=value.dtype, device=value.device)
+    out = torch.empty((*value.shape[:-1], n), dtype=out_dtype or value.dtype, device=value.device)
     if a.shape[0] == 0:
         return out
     flags = ACTIVATIONS[activation]
@@ -184,11 +185,12 @@ class QuantizedLinear:
         return int(self.weight.shape[1]) * 32 // self.bits
 
     def __call__(self, value: torch.Tensor, *, activation: str | None = None,
-                 residual: torch.Tensor | None = None, gate: torch.Tensor | None = None) -> torch.Tensor:
+                 residual: torch.Tensor | None = None, gate: torch.Tensor | None = None,
+                 out_dtype: torch.dtype | None = None) -> torch.Tensor:
         return quantized_matmul(
             value, self.weight, self.scales, self.biases, group_size=self.group_size,
             bits=self.bits, mode=self.mode, bias=self.bias, activation=activation,
-            residual=residual, gate=gate,
+            residual=residual, gate=gate, out_dtype=out_dtype,
         )
 
 

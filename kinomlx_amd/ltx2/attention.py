@@ -43,9 +43,9 @@ class Linear:
 
     def __call__(self, value: torch.Tensor, *, activation: str | None = None,
                  residual: torch.Tensor | None = None, gate: torch.Tensor | None = None,
-                 out: torch.Tensor | None = None) -> torch.Tensor:
+                 out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None) -> torch.Tensor:
         return mpp_linear.fused_linear(value, self.weight, self.bias, activation=activation,
-                                       residual=residual, gate=gate, out=out)
+                                       residual=residual, gate=gate, out=out, out_dtype=out_dtype)
 
 
 def rms_norm(value: torch.Tensor, weight: torch.Tensor | None = None, eps: float = 1e-6) -> torch.Tensor:
@@ -241,13 +241,15 @@ class Attention:
 
     def __call__(self, value: torch.Tensor, *, context: torch.Tensor | None = None,
                  mask: torch.Tensor | None = None, pe=None, k_pe=None, sparse=None,
-                 residual: torch.Tensor | None = None, gate: torch.Tensor | None = None) -> torch.Tensor:
+                 residual: torch.Tensor | None = None, gate: torch.Tensor | None = None,
+                 out_dtype: torch.dtype | None = None) -> torch.Tensor:
         """``to_out(attention)``; with ``residual``/``gate`` the block's gated residual
-        ``residual + gate * to_out(attention)`` is formed in the output GEMM's epilogue."""
+        ``residual + gate * to_out(attention)`` is formed in the output GEMM's epilogue, written
+        as ``out_dtype`` (default the input dtype; fp32 carries the residual stream unrounded)."""
         if sparse is not None:
             raise ValueError("sparse (Sol-Attn) attention is not built for MI355X")
         attended = self.attend(value, context=context, mask=mask, pe=pe, k_pe=k_pe)
-        return self.to_out(attended, residual=residual, gate=gate)
+        return self.to_out(attended, residual=residual, gate=gate, out_dtype=out_dtype)
 
 
 __all__ = [

@@ -44,13 +44,13 @@ class FeedForward:
         self.project_out: Linear | None = None
 
     def __call__(self, value: torch.Tensor, *, residual: torch.Tensor | None = None,
-                 gate: torch.Tensor | None = None) -> torch.Tensor:
+                 gate: torch.Tensor | None = None, out_dtype: torch.dtype | None = None) -> torch.Tensor:
         """``project_out(gelu(project_in(x)))``; with ``residual``/``gate`` the block's gated
-        residual is formed in the down-projection's epilogue."""
+        residual is formed in the down-projection's epilogue (``out_dtype`` as ``Attention``)."""
         if value.shape[-1] != self.dim:
             raise ValueError(f"feed-forward expects width {self.dim}, got {value.shape[-1]}")
         hidden = self.project_in(value)
-        out = self.project_out(hidden, residual=residual, gate=gate)
+        out = self.project_out(hidden, residual=residual, gate=gate, out_dtype=out_dtype)
         if out.shape[-1] != self.output_dim:
             raise ValueError(f"feed-forward produced width {out.shape[-1]}, expected {self.output_dim}")
         return out

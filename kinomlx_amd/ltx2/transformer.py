@@ -10,8 +10,13 @@ Kernel schedule of one block (B=1, T video tokens, Tc text tokens):
   AdaLN(x) -> [QKV GEMM, gate GEMM (2*sigmoid)] -> Q/K norm+RoPE -> flash attention (gated)
   -> out GEMM (+ x + g0 * .) ; AdaLN(x), modulate(ctx) -> [Q GEMM, gate GEMM, KV GEMM] -> Q/K norm
   -> attention -> out GEMM (+ x + g8 * .) ; AdaLN(x) -> up GEMM (GELU) -> down GEMM (+ x + g5 * .)
-Every residual add rides in a GEMM epilogue; every intermediate is bf16, every reduction and
-epilogue FP32. The audio stream, A/V cross-attention, masks and sparse attention are not built.
+Every residual add rides in a GEMM epilogue; every reduction and epilogue is FP32. Between the
+block's three branches the residual stream is carried in FP32 (written by the out-projection
+epilogues, read by the next AdaLN and epilogue) and rounded to bf16 once, by the last epilogue;
+every other intermediate is bf16. The reference rounds the stream after each branch
+(``transformer.py:26-30`` casts to ``value.dtype``); carrying it costs 2 x T x D x 2 extra bytes
+per branch and removes two of the block's output roundings. The audio stream, A/V
+cross-attention, masks and sparse attention are not built.
 """
 
 from __future__ import annotations
@@ -31,14 +36,29 @@ def _mod32(value: torch.Tensor) -> torch.Tensor:
     return v if (v.stride(-1) == 1 and v.data_ptr() % 16 == 0) else v.contiguous()
 
 
+def _mod_pair(shift: torch.Tensor, scale: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """fp32 ``shift`` and ``scale`` in one row layout (the kernels index both rows with one
+    divisor and stride): when they broadcast differently, both are expanded to their common
+    shape first."""
+    shift32, scale32 = _mod32(shift), _mod32(scale)
+    if shift32.shape != scale32.shape or shift32.stride() != scale32.stride():
+        shape = torch.broadcast_shapes(shift32.shape, scale32.shape)
+        shift32 = shift32.expand(shape).contiguous()
+        scale32 = scale32.expand(shape).contiguous()
+    return shift32, scale32
+
+
 def adaln(value: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor, eps: float) -> torch.Tensor:
     """``rms_norm(x) * (1 + scale) + shift`` in one FP32 pass (``transformer.py:16-23``).
-    ``scale``/``shift`` broadcast as ``(D,)``, ``(B, 1, D)`` or ``(B, T, D)``."""
-    if value.dtype != torch.bfloat16:
-        raise ValueError(f"adaln takes bfloat16 activations on MI355X, got {value.dtype}")
-    out = torch.empty(value.shape, dtype=value.dtype, device=value.device)
+    ``scale``/``shift`` broadcast as ``(D,)``, ``(B, 1, D)`` or ``(B, T, D)``. ``value`` is bf16,
+    or an FP32 residual stream; the result is bf16, the dtype the next GEMM reads (the
+    reference returns ``value.dtype``)."""
+    if value.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"adaln takes bfloat16 (or an fp32 residual stream) on MI355X, got {value.dtype}")
+    out = torch.empty(value.shape, dtype=torch.bfloat16, device=value.device)
     if value.numel():
-        _lib.launch_adaln_norm(value, out, _mod32(shift), _mod32(scale), eps, _lib.KX_NORM_RMS)
+        shift32, scale32 = _mod_pair(shift, scale)
+        _lib.launch_adaln_norm(value, out, shift32, scale32, eps, _lib.KX_NORM_RMS)
     return out
 
 
@@ -50,7 +70,8 @@ def layer_norm_modulate(value: torch.Tensor, shift: torch.Tensor, scale: torch.T
         raise ValueError(f"layer_norm_modulate takes bfloat16 activations on MI355X, got {value.dtype}")
     out = torch.empty(value.shape, dtype=value.dtype, device=value.device)
     if value.numel():
-        _lib.launch_adaln_norm(value, out, _mod32(shift), _mod32(scale), eps, _lib.KX_NORM_LAYER)
+        shift32, scale32 = _mod_pair(shift, scale)
+        _lib.launch_adaln_norm(value, out, shift32, scale32, eps, _lib.KX_NORM_LAYER)
     return out
 
 
@@ -66,7 +87,8 @@ def modulate(value: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor) -> t
     """``x * (1 + scale) + shift`` (``transformer.py:33-34``)."""
     out = torch.empty(value.shape, dtype=value.dtype, device=value.device)
     if value.numel():
-        _lib.launch_modulate(value, out, _mod32(shift), _mod32(scale))
+        shift32, scale32 = _mod_pair(shift, scale)
+        _lib.launch_modulate(value, out, shift32, scale32)
     return out
 
 
@@ -165,7 +187,7 @@ class BasicAVTransformerBlock:
         context = modulate(args.context, prompt[:, :, 1], prompt[:, :, 0])
         if args.context_mask is not None:
             raise ValueError("masked text cross-attention is not built for MI355X")
-        return self.attn2(query, context=context, residual=value, gate=ada[:, :, 8])
+        return self.attn2(query, context=context, residual=value, gate=ada[:, :, 8], out_dtype=torch.float32)
 
     def __call__(self, video: TransformerArgs | None, audio: TransformerArgs | None = None):
         if audio is not None:
@@ -179,14 +201,16 @@ class BasicAVTransformerBlock:
         x = video.x
         ada = (self.scale_shift_table[None, None].float() + video.timesteps.float()).contiguous()
 
+        # x1, x2: the residual stream in FP32 between the branches; one rounding at the end.
         normalized = adaln(x, ada[:, :, 1], ada[:, :, 0], self.norm_eps)
-        x = self.attn1(normalized, pe=video.positional_embeddings, residual=x, gate=ada[:, :, 2])
+        x1 = self.attn1(normalized, pe=video.positional_embeddings, residual=x, gate=ada[:, :, 2],
+                        out_dtype=torch.float32)
 
-        x = self._text_cross_attention(x, video, ada)
+        x2 = self._text_cross_attention(x1, video, ada)
 
-        normalized = adaln(x, ada[:, :, 4], ada[:, :, 3], self.norm_eps)
-        x = self.ff(normalized, residual=x, gate=ada[:, :, 5])
-        return replace(video, x=x), audio
+        normalized = adaln(x2, ada[:, :, 4], ada[:, :, 3], self.norm_eps)
+        out = self.ff(normalized, residual=x2, gate=ada[:, :, 5], out_dtype=x.dtype)
+        return replace(video, x=out), audio
 
 
 __all__ = [

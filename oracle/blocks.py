@@ -24,6 +24,7 @@ from .ops import (
     rms_norm,
     split_rope,
     swiglu,
+    to_bf16,
 )
 
 __all__ = [
@@ -59,37 +60,44 @@ def _lin(params: dict, name: str, value: np.ndarray) -> np.ndarray:
     return linear(value, params[f"{name}.weight"], bias)
 
 
-def ltx_attention(params: dict, prefix: str, value, *, heads: int, context=None, pe=None, eps=1e-6):
+def _keep(value: np.ndarray) -> np.ndarray:
+    return value
+
+
+def ltx_attention(params: dict, prefix: str, value, *, heads: int, context=None, pe=None, eps=1e-6,
+                  store=_keep):
     """LTX ``Attention.__call__`` without mask or sparse routing
     (``kinomlx/models/ltx2/transformer/attention.py:291-371``): gate logits ``2*sigmoid``,
-    full-width weighted RMSNorm on Q and K, split RoPE, SDPA, per-head gate, output projection."""
+    full-width weighted RMSNorm on Q and K, split RoPE, SDPA, per-head gate, output projection.
+    ``store`` is applied to every array the reference materialises (see ``ltx_video_block``)."""
     x = np.asarray(value, dtype=F32)
     source = x if context is None else np.asarray(context, dtype=F32)
     head_gate = None
     if f"{prefix}.to_gate_logits.weight" in params or f"{prefix}.to_gate_logits.wq" in params:
-        head_gate = F32(2.0) * sigmoid(_lin(params, f"{prefix}.to_gate_logits", x))
-    v = _lin(params, f"{prefix}.to_v", source)
-    q = rms_norm(_lin(params, f"{prefix}.to_q", x), params[f"{prefix}.q_norm.weight"], eps)
-    k = rms_norm(_lin(params, f"{prefix}.to_k", source), params[f"{prefix}.k_norm.weight"], eps)
+        head_gate = store(F32(2.0) * store(sigmoid(store(_lin(params, f"{prefix}.to_gate_logits", x)))))
+    v = store(_lin(params, f"{prefix}.to_v", source))
+    q = store(rms_norm(store(_lin(params, f"{prefix}.to_q", x)), params[f"{prefix}.q_norm.weight"], eps))
+    k = store(rms_norm(store(_lin(params, f"{prefix}.to_k", source)), params[f"{prefix}.k_norm.weight"], eps))
     if pe is not None:
         cos, sin = pe
-        q = split_rope(q[None], cos, sin)[0]
-        k = split_rope(k[None], cos, sin)[0]
-    out = attention(q, k, v, heads=heads)
+        q = store(split_rope(q[None], cos, sin)[0])
+        k = store(split_rope(k[None], cos, sin)[0])
+    out = store(attention(q, k, v, heads=heads))
     if head_gate is not None:
         tokens, width = out.shape
-        out = (out.reshape(tokens, heads, width // heads) * head_gate[:, :, None]).reshape(tokens, width)
-    return _lin(params, f"{prefix}.to_out", out)
+        out = store((out.reshape(tokens, heads, width // heads) * head_gate[:, :, None]).reshape(tokens, width))
+    return store(_lin(params, f"{prefix}.to_out", out))
 
 
-def ltx_feed_forward(params: dict, prefix: str, value) -> np.ndarray:
+def ltx_feed_forward(params: dict, prefix: str, value, store=_keep) -> np.ndarray:
     """``project_out(gelu_approx(project_in(x)))``
     (``kinomlx/models/ltx2/transformer/feed_forward.py:80-97``)."""
-    hidden = gelu_approx(_lin(params, f"{prefix}.proj_in", value))
-    return _lin(params, f"{prefix}.proj_out", hidden)
+    hidden = store(gelu_approx(store(_lin(params, f"{prefix}.proj_in", value))))
+    return store(_lin(params, f"{prefix}.proj_out", hidden))
 
 
-def ltx_video_block(params: dict, x, context, pe, *, heads: int, eps: float = 1e-6) -> np.ndarray:
+def ltx_video_block(params: dict, x, context, pe, *, heads: int, eps: float = 1e-6,
+                    bf16_graph: bool = False) -> np.ndarray:
     """Video branch of ``BasicAVTransformerBlock.__call__``
     (``kinomlx/models/ltx2/transformer/transformer.py:225-276,373-392``) with the text
     cross-attention of ``:201-223``.
@@ -97,22 +105,35 @@ def ltx_video_block(params: dict, x, context, pe, *, heads: int, eps: float = 1e
     ``params["ada"]`` is ``scale_shift_table + timesteps`` as ``(9, D)`` (``:179-186``): rows
     0-2 attention (shift, scale, gate), 3-5 feed-forward, 6-8 text query. ``params["prompt"]``
     is the ``(2, D)`` context (shift, scale) (``:209-219``).
+
+    ``bf16_graph=False`` (default) is the FP32 evaluation. ``bf16_graph=True`` restates the
+    reference's own bf16 execution: FP32 opmath inside each op, and every array the MLX graph
+    materialises in the activation dtype rounded to bf16 — each linear output, the stock
+    ``rms_norm`` output before modulation and the modulated value (``transformer.py:16-23``),
+    sigmoid and the doubled gate (``attention.py:319-325``), Q/K norms, RoPE, attention, the
+    per-head gate product, the gated residual (``transformer.py:26-30``), ``_gate`` and the
+    cross-attention sum (``:266-276``), GELU (``feed_forward.py:80-97``). It measures the error
+    the reference itself carries against the FP32 evaluation.
     """
+    store = to_bf16 if bf16_graph else _keep
     ada = np.asarray(params["ada"], dtype=F32)
     prompt = np.asarray(params["prompt"], dtype=F32)
     value = np.asarray(x, dtype=F32)
 
-    normalized_x = adaln(value, ada[1], ada[0], eps)
-    attended = ltx_attention(params, "attn1", normalized_x, heads=heads, pe=pe, eps=eps)
-    value = gated_residual(value, attended, ada[2])
+    def _adaln(v, scale, shift):
+        return store((store(rms_norm(v, eps=eps)) * (F32(1.0) + scale) + shift).astype(F32))
 
-    query = adaln(value, ada[7], ada[6], eps)
-    ctx = modulate(context, prompt[1], prompt[0])
-    cross = ltx_attention(params, "attn2", query, heads=heads, context=ctx, eps=eps)
-    value = (value + gate(cross, ada[8])).astype(F32)
+    normalized_x = _adaln(value, ada[1], ada[0])
+    attended = ltx_attention(params, "attn1", normalized_x, heads=heads, pe=pe, eps=eps, store=store)
+    value = store(gated_residual(value, attended, ada[2]))
 
-    normalized_x = adaln(value, ada[4], ada[3], eps)
-    return gated_residual(value, ltx_feed_forward(params, "ff", normalized_x), ada[5])
+    query = _adaln(value, ada[7], ada[6])
+    ctx = store(modulate(context, prompt[1], prompt[0]))
+    cross = ltx_attention(params, "attn2", query, heads=heads, context=ctx, eps=eps, store=store)
+    value = store((value + store(gate(cross, ada[8]))).astype(F32))
+
+    normalized_x = _adaln(value, ada[4], ada[3])
+    return store(gated_residual(value, ltx_feed_forward(params, "ff", normalized_x, store), ada[5]))
 
 
 def _heads_norm(value, weight, heads: int, eps: float = 1e-6) -> np.ndarray:

@@ -8,6 +8,15 @@ oracle would take minutes. ``tests/test_blocks_cpu.py`` pins it against the nump
 import torch
 
 
+def _keep(x):
+    return x
+
+
+def bf16_store(x):
+    """Round an FP32 tensor to bf16 values (kept in FP32): the reference's materialised arrays."""
+    return x.to(torch.bfloat16).float()
+
+
 def _lin(p, name, x):
     out = x @ p[f"{name}.weight"].T
     bias = p.get(f"{name}.bias")
@@ -36,34 +45,37 @@ def _attention(q, k, v, heads):
     kh = k.reshape(k.shape[0], heads, dh).transpose(0, 1)
     vh = v.reshape(v.shape[0], heads, dh).transpose(0, 1)
     out = torch.empty_like(qh)
+    kt = kh.transpose(1, 2).contiguous()
     for start in range(0, t, 2048):
-        sc = qh[:, start:start + 2048] @ kh.transpose(1, 2) * dh ** -0.5
+        sc = qh[:, start:start + 2048] @ kt * dh ** -0.5
         out[:, start:start + 2048] = torch.softmax(sc, -1) @ vh
     return out.transpose(0, 1).reshape(t, width)
 
 
-def _ltx_attention(p, prefix, x, heads, context=None, pe=None):
+def _ltx_attention(p, prefix, x, heads, context=None, pe=None, st=_keep):
     source = x if context is None else context
-    gate = 2 * torch.sigmoid(_lin(p, f"{prefix}.to_gate_logits", x))
-    v = _lin(p, f"{prefix}.to_v", source)
-    q = _rms(_lin(p, f"{prefix}.to_q", x), p[f"{prefix}.q_norm.weight"])
-    k = _rms(_lin(p, f"{prefix}.to_k", source), p[f"{prefix}.k_norm.weight"])
+    gate = st(2 * st(torch.sigmoid(st(_lin(p, f"{prefix}.to_gate_logits", x)))))
+    v = st(_lin(p, f"{prefix}.to_v", source))
+    q = st(_rms(st(_lin(p, f"{prefix}.to_q", x)), p[f"{prefix}.q_norm.weight"]))
+    k = st(_rms(st(_lin(p, f"{prefix}.to_k", source)), p[f"{prefix}.k_norm.weight"]))
     if pe is not None:
-        q, k = _split_rope(q, *pe), _split_rope(k, *pe)
-    o = _attention(q, k, v, heads)
+        q, k = st(_split_rope(q, *pe)), st(_split_rope(k, *pe))
+    o = st(_attention(q, k, v, heads))
     t, width = o.shape
-    o = (o.reshape(t, heads, width // heads) * gate[:, :, None]).reshape(t, width)
-    return _lin(p, f"{prefix}.to_out", o)
+    o = st((o.reshape(t, heads, width // heads) * gate[:, :, None]).reshape(t, width))
+    return st(_lin(p, f"{prefix}.to_out", o))
 
 
-def ltx_video_block(p, x, context, pe, heads):
-    """``p``: fp32 tensors named as in ``oracle.ltx_video_block`` (dense weights)."""
+def ltx_video_block(p, x, context, pe, heads, bf16_graph=False):
+    """``p``: fp32 tensors named as in ``oracle.ltx_video_block`` (dense weights);
+    ``bf16_graph`` rounds at the same points as the oracle's ``bf16_graph`` mode."""
+    st = bf16_store if bf16_graph else _keep
     ada, prompt = p["ada"], p["prompt"]
-    n = _rms(x) * (1 + ada[1]) + ada[0]
-    x = x + _ltx_attention(p, "attn1", n, heads, pe=pe) * ada[2]
-    q = _rms(x) * (1 + ada[7]) + ada[6]
-    ctx = context * (1 + prompt[1]) + prompt[0]
-    x = x + _ltx_attention(p, "attn2", q, heads, context=ctx) * ada[8]
-    n = _rms(x) * (1 + ada[4]) + ada[3]
-    h = torch.nn.functional.gelu(_lin(p, "ff.proj_in", n), approximate="tanh")
-    return x + _lin(p, "ff.proj_out", h) * ada[5]
+    n = st(st(_rms(x)) * (1 + ada[1]) + ada[0])
+    x = st(x + _ltx_attention(p, "attn1", n, heads, pe=pe, st=st) * ada[2])
+    q = st(st(_rms(x)) * (1 + ada[7]) + ada[6])
+    ctx = st(context * (1 + prompt[1]) + prompt[0])
+    x = st(x + st(_ltx_attention(p, "attn2", q, heads, context=ctx, st=st) * ada[8]))
+    n = st(st(_rms(x)) * (1 + ada[4]) + ada[3])
+    h = st(torch.nn.functional.gelu(st(_lin(p, "ff.proj_in", n)), approximate="tanh"))
+    return st(x + st(_lin(p, "ff.proj_out", h)) * ada[5])
