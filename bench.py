@@ -95,7 +95,20 @@ def main() -> int:
     parser.add_argument("--config", type=int, default=3, choices=(3, 4, 5))
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--breakdown", action="store_true", help="print the per-kernel table to stderr")
+    parser.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                        help="only run 5 device-to-device copies of MIB MiB (the known-size kernel that "
+                             "scales the FETCH_SIZE / WRITE_SIZE counters) and exit")
     args = parser.parse_args()
+    if args.calibrate_copy:
+        import torch
+
+        src = torch.ones(args.calibrate_copy << 19, dtype=torch.bfloat16, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": src.numel() * 2}))
+        return 0
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
         return 2
