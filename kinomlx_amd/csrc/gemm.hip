@@ -305,6 +305,241 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint32_t* __restrict
   *reinterpret_cast<uint4*>(out + r * k + kk) = dequant8<BITS>(tmp, bf2f(scales[g]), bf2f(biases[g]));
 }
 
+// ---- direct-to-LDS pipelined kernel (K % 64 == 0) -----------------------------------------------
+//
+// Operand tiles go from global memory straight into LDS with global_load_lds_dwordx4 (no VGPR
+// staging): a wave instruction fills 8 rows of 128 B. Two LDS stages of BK = 64: the loads for
+// stage kt+1 are issued when stage kt starts; in the last k16 step of stage kt each wave waits
+// for them, the workgroup meets at one barrier, and the first fragments of stage kt+1 are read
+// while that step's MFMAs run. Fragments are double-buffered in registers across k16 steps, and
+// the schedule interleaves one fragment read per MFMA. The 16-byte slot of row r holds chunk
+// c ^ ((r ^ (r >> 3)) & 7): conflict-free for the 32-row fragment reads with 64 banks (and 32).
+//
+// Epilogue: each wave stages half of its fp32 tile in LDS at a time and writes it back in rows,
+// 4 columns per lane, so bias / gate / residual loads and the stores are contiguous runs.
+
+__device__ __forceinline__ int swz8(int r) { return (r ^ (r >> 3)) & 7; }
+#define KX_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+
+// bias + activation + gated residual on 4 consecutive columns n..n+3 of row m, then the store.
+__device__ __forceinline__ void epilogue_store4(float v[4], int m, int n, int N, const Epilogue& epi,
+                                                void* __restrict__ C, int64_t ldc, bool vec_ok) {
+  const int act = (epi.flags >> 4) & 15;
+  const bool gated = epi.flags & KX_EPI_GATED_RESIDUAL;
+  const bool resid_f32 = epi.flags & KX_EPI_RESID_F32;
+  const bool out_f32 = epi.flags & KX_EPI_OUT_F32;
+  const int64_t ro = (int64_t)m * epi.ldr + n;
+  const int64_t co = (int64_t)m * ldc + n;
+  if (vec_ok && n + 3 < N) {
+    if (epi.flags & KX_EPI_BIAS) {
+      const uint2 bb = *reinterpret_cast<const uint2*>(epi.bias + n);
+      v[0] += lo_f(bb.x); v[1] += hi_f(bb.x); v[2] += lo_f(bb.y); v[3] += hi_f(bb.y);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = apply_act(v[e], act);
+    if (gated) {
+      const float4 gv = *reinterpret_cast<const float4*>(epi.gate + (m / epi.gate_div) * epi.gate_stride + n);
+      float rv[4];
+      if (resid_f32) {
+        const float4 rr = *reinterpret_cast<const float4*>(static_cast<const float*>(epi.resid) + ro);
+        rv[0] = rr.x; rv[1] = rr.y; rv[2] = rr.z; rv[3] = rr.w;
+      } else {
+        const uint2 rr = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(epi.resid) + ro);
+        rv[0] = lo_f(rr.x); rv[1] = hi_f(rr.x); rv[2] = lo_f(rr.y); rv[3] = hi_f(rr.y);
+      }
+      v[0] = rv[0] + gv.x * v[0];
+      v[1] = rv[1] + gv.y * v[1];
+      v[2] = rv[2] + gv.z * v[2];
+      v[3] = rv[3] + gv.w * v[3];
+    }
+    if (out_f32) {
+      *reinterpret_cast<float4*>(static_cast<float*>(C) + co) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+      uint2 o;
+      o.x = pack2(v[0], v[1]);
+      o.y = pack2(v[2], v[3]);
+      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(C) + co) = o;
+    }
+    return;
+  }
+  for (int e = 0; e < 4 && n + e < N; ++e) {
+    float x = v[e];
+    if (epi.flags & KX_EPI_BIAS) x += bf2f(epi.bias[n + e]);
+    x = apply_act(x, act);
+    if (gated) {
+      const float rv = resid_f32 ? static_cast<const float*>(epi.resid)[ro + e]
+                                 : bf2f(static_cast<const uint16_t*>(epi.resid)[ro + e]);
+      x = rv + epi.gate[(m / epi.gate_div) * epi.gate_stride + n + e] * x;
+    }
+    if (out_f32)
+      static_cast<float*>(C)[co + e] = x;
+    else
+      static_cast<uint16_t*>(C)[co + e] = f2bf(x);
+  }
+}
+
+template <int BM, int BN>
+__global__ __launch_bounds__(256) void gemm_lds_kernel(
+    const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ W, int64_t ldw,
+    void* __restrict__ C, int64_t ldc, int M, int N, int K, Epilogue epi) {
+  constexpr int RPI = 8;  // rows one DMA instruction fills (64 lanes x 16 B over 128-B rows)
+  constexpr int A_INST = BM / RPI / 4, W_INST = BN / RPI / 4;
+  constexpr int STAGE = (BM + BN) * ROWB;
+  constexpr int WT_M = BM / 2, WT_N = BN / 2;
+  constexpr int MB = WT_M / 32, NB = WT_N / 32;
+  constexpr int KS = BK / 16;
+  constexpr int PITCH = WT_N / 2 + 4;  // staged epilogue row, floats
+  constexpr int EP_BYTES = 4 * WT_M * PITCH * 4;
+  constexpr int SMEM = 2 * STAGE > EP_BYTES ? 2 * STAGE : EP_BYTES;
+  static_assert(A_INST * RPI * 4 == BM && W_INST * RPI * 4 == BN && MB >= 1 && NB >= 2, "tile");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int lrow = lane & 31, lhalf = lane >> 5;
+
+  // tile coordinates: XCD-contiguous, then grouped by 8 tile rows for L2 reuse
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  const int t = xcd_remap(blockIdx.x, tiles_m * tiles_n);
+  constexpr int GM = 8;
+  const int group_width = GM * tiles_n;
+  const int first_m = (t / group_width) * GM;
+  const int gsz = min(tiles_m - first_m, GM);
+  const int m0 = (first_m + (t % group_width) % gsz) * BM;
+  const int n0 = ((t % group_width) / gsz) * BN;
+
+  // per-lane DMA sources: lane -> row lane / 8 of the instruction's 8 rows, slot lane % 8
+  const int r_in = lane >> 3, slot = lane & 7;
+  const uint16_t* a_src[A_INST];
+  const uint16_t* w_src[W_INST];
+#pragma unroll
+  for (int i = 0; i < A_INST; ++i) {
+    const int r = (wave * A_INST + i) * RPI + r_in;
+    a_src[i] = A + (int64_t)min(m0 + r, M - 1) * lda + (slot ^ swz8(r)) * 8;
+  }
+#pragma unroll
+  for (int i = 0; i < W_INST; ++i) {
+    const int r = (wave * W_INST + i) * RPI + r_in;
+    w_src[i] = W + (int64_t)min(n0 + r, N - 1) * ldw + (slot ^ swz8(r)) * 8;
+  }
+  auto issue = [&](uint8_t* buf, int k0) {
+#pragma unroll
+    for (int i = 0; i < A_INST; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(a_src[i] + k0),
+                                       KX_LDS(buf + (wave * A_INST + i) * RPI * ROWB), 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < W_INST; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(w_src[i] + k0),
+                                       KX_LDS(buf + (BM + (wave * W_INST + i) * RPI) * ROWB), 16, 0, 0);
+  };
+
+  // fragment byte offsets within a stage, per k16 step (the MFMA A operand is the weight tile)
+  int a_off[KS][MB], w_off[KS][NB];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    const int c = 2 * s + lhalf;
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+      const int r = wm * WT_M + j * 32 + lrow;
+      a_off[s][j] = r * ROWB + ((c ^ swz8(r)) << 4);
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int r = BM + wn * WT_N + i * 32 + lrow;
+      w_off[s][i] = r * ROWB + ((c ^ swz8(r)) << 4);
+    }
+  }
+  auto load_frags = [&](const uint8_t* buf, int s, bf16x8* af, bf16x8* wf) {
+#pragma unroll
+    for (int j = 0; j < MB; ++j) af[j] = *reinterpret_cast<const bf16x8*>(buf + a_off[s][j]);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) wf[i] = *reinterpret_cast<const bf16x8*>(buf + w_off[s][i]);
+  };
+
+  f32x16 acc[NB][MB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i)
+#pragma unroll
+    for (int j = 0; j < MB; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  const int stages = K / BK;
+  issue(smem, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+
+  bf16x8 fa[2][MB], fw[2][NB];
+  load_frags(smem, 0, fa[0], fw[0]);
+  for (int kt = 0; kt < stages; ++kt) {
+    const uint8_t* cur = smem + (kt & 1) * STAGE;
+    uint8_t* nxt = smem + ((kt + 1) & 1) * STAGE;
+    // the last iteration re-loads the last stage into the idle buffer: the loop stays branch-free
+    issue(nxt, min(kt + 1, stages - 1) * BK);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const int b = s & 1;
+      if (s + 1 < KS) {
+        load_frags(cur, s + 1, fa[b ^ 1], fw[b ^ 1]);
+      } else {
+        // stage kt+1 has landed for this wave and its reads of cur are done; after the barrier
+        // it has landed for every wave, and nobody reads cur again before it is refilled.
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        load_frags(nxt, 0, fa[b ^ 1], fw[b ^ 1]);
+      }
+#pragma unroll
+      for (int i = 0; i < NB; ++i)
+#pragma unroll
+        for (int j = 0; j < MB; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fw[b][i], fa[b][j], acc[i][j], 0, 0, 0);
+      // one fragment read between consecutive MFMAs, then the rest of the MFMAs
+#pragma unroll
+      for (int q = 0; q < MB + NB; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, NB * MB - (MB + NB), 0);
+    }
+  }
+
+  // ---- epilogue: the accumulator lane holds row m = j*32 + lrow and columns 8g + 4 lhalf + e of
+  // block i; staged per half of the wave's columns into a private LDS region.
+  const bool vec_ok = (ldc % 4 == 0) && (!(epi.flags & KX_EPI_GATED_RESIDUAL) || epi.ldr % 4 == 0);
+  float* ep = reinterpret_cast<float*>(smem) + wave * (WT_M * PITCH);
+  constexpr int HALF_N = WT_N / 2;
+  constexpr int LPR = HALF_N / 4;  // lanes per staged row
+  constexpr int RPI_EP = 64 / LPR;   // rows per read-back iteration
+  const int q = lane % LPR, rr = lane / LPR;
+  __builtin_amdgcn_s_barrier();  // every wave is done with the main loop's LDS
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int ii = 0; ii < NB / 2; ++ii) {
+      const int i = h * (NB / 2) + ii;
+#pragma unroll
+      for (int j = 0; j < MB; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<float4*>(ep + (j * 32 + lrow) * PITCH + ii * 32 + 8 * g + 4 * lhalf) =
+              make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                          acc[i][j][4 * g + 3]);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const int n = n0 + wn * WT_N + h * HALF_N + 4 * q;
+#pragma unroll 2
+    for (int r = rr; r < WT_M; r += RPI_EP) {
+      const int m = m0 + wm * WT_M + r;
+      const float4 a4 = *reinterpret_cast<const float4*>(ep + r * PITCH + 4 * q);
+      if (m < M && n < N) {
+        float v[4] = {a4.x, a4.y, a4.z, a4.w};
+        epilogue_store4(v, m, n, N, epi, C, ldc, vec_ok);
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  }
+}
+
 // ---- dispatch ---------------------------------------------------------------------------------
 
 enum TileCfg { T256x256 = 0, T256x128 = 1, T128x128 = 2, T64x64 = 3, T128x64 = 4 };
@@ -338,10 +573,50 @@ int pick_cfg(int64_t m, int64_t n) {
   return T128x128;
 }
 
+template <int BM, int BN>
+int launch_lds(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, void* c, int64_t ldc,
+               int m, int n, int k, const Epilogue& epi, hipStream_t s) {
+  const int tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+  gemm_lds_kernel<BM, BN><<<tiles, 256, 0, s>>>(a, lda, w, ldw, c, ldc, m, n, k, epi);
+  return KX_OK;
+}
+
+// Tile for the direct-to-LDS kernel: the fewest rounds of 256 workgroups, weighted by the
+// tile's relative speed (a bigger tile reuses each LDS byte more). 0: 256x256, 1: 192x256,
+// 2: 128x128.
+int pick_lds_cfg(int64_t m, int64_t n) {
+  const char* env = getenv("KX355_GEMM_LDS_TILE");
+  if (env && *env) {
+    const int v = atoi(env);
+    if (v >= 0 && v <= 2) return v;
+  }
+  const int64_t bm[3] = {256, 192, 128}, bn[3] = {256, 256, 128};
+  const double speed[3] = {1.0, 0.97, 0.8};
+  int best = 0;
+  double best_cost = 0.0;
+  for (int i = 0; i < 3; ++i) {
+    const int64_t tiles = ((m + bm[i] - 1) / bm[i]) * ((n + bn[i] - 1) / bn[i]);
+    const double cost = (double)((tiles + 255) / 256) * (double)(bm[i] * bn[i]) / speed[i];
+    if (i == 0 || cost < best_cost) {
+      best = i;
+      best_cost = cost;
+    }
+  }
+  return best;
+}
+
 template <int QB>
 int dispatch(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, QuantW qw,
              void* c, int64_t ldc, int64_t m, int64_t n, int64_t k, const Epilogue& epi,
              hipStream_t s) {
+  const char* legacy = getenv("KX355_GEMM_TILE");
+  if (QB == 0 && k % BK == 0 && !(legacy && *legacy)) {
+    switch (pick_lds_cfg(m, n)) {
+      case 0: return launch_lds<256, 256>(a, lda, w, ldw, c, ldc, (int)m, (int)n, (int)k, epi, s);
+      case 1: return launch_lds<192, 256>(a, lda, w, ldw, c, ldc, (int)m, (int)n, (int)k, epi, s);
+      default: return launch_lds<128, 128>(a, lda, w, ldw, c, ldc, (int)m, (int)n, (int)k, epi, s);
+    }
+  }
   switch (pick_cfg(m, n)) {
     case T256x256:
       return launch_cfg<256, 256, 2, 2, QB>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k,

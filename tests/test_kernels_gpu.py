@@ -265,6 +265,32 @@ def test_linear_matches_oracle_for_every_tile(device, monkeypatch, tile, m, n, k
     assert _gemm_close(got_nb, oracle.linear(x, w))
 
 
+@pytest.mark.parametrize("tile", ["0", "1", "2"])
+@pytest.mark.parametrize(("m", "n", "k"), [(1056, 1040, 1024), (300, 96, 64), (513, 520, 192), (9, 8, 64)])
+@pytest.mark.parametrize("epilogue", ["bias", "gelu_tanh", "gated_f32"])
+def test_direct_to_lds_linear_every_tile_and_epilogue(device, monkeypatch, tile, m, n, k, epilogue):
+    """The K % 64 == 0 direct-to-LDS kernel at each of its tiles (256x256, 192x256, 128x128) on
+    ragged M and N (partial tiles, clamped loads, masked stores) with each epilogue family."""
+    monkeypatch.setenv("KX355_GEMM_LDS_TILE", tile)
+    x, w, b = _linear_case(m, n, k, m + n + k + 1, device)
+    lin = oracle.linear(x, w, b)
+    if epilogue == "bias":
+        got = _np(mpp_linear.linear(_bf(x, device), _bf(w, device), _bf(b, device), transposed=True))
+        assert _gemm_close(got, lin)
+    elif epilogue == "gelu_tanh":
+        got = _np(mpp_linear.fused_linear(_bf(x, device), _bf(w, device), _bf(b, device), activation="gelu_tanh"))
+        ref = oracle.gelu_approx(lin)
+        assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0**-7 + 2e-4 * np.abs(ref).max() + 1e-6)
+    else:
+        r = _rng(m + n)
+        resid = r.standard_normal((m, n)).astype(F32)
+        gate = r.standard_normal(n).astype(F32)
+        out = mpp_linear.fused_linear(_bf(x, device), _bf(w, device), _bf(b, device), residual=_f32(resid, device),
+                                      gate=_f32(gate, device), out_dtype=torch.float32)
+        ref = resid + gate * lin
+        assert np.all(np.abs(_np(out) - ref) <= 1e-5 * np.abs(ref) + 2e-5 * np.abs(ref).max())
+
+
 def test_linear_takes_in_out_weights(device):
     x, w, b = _linear_case(64, 48, 32, 3, device)
     got = _np(mpp_linear.linear(_bf(x, device), _bf(w.T, device), _bf(b, device), transposed=False))
@@ -472,3 +498,4 @@ def test_quantized_linear_matches_oracle(device, monkeypatch, tile, bits, m, n, 
 
 def test_env_tile_override_is_restored():
     assert os.environ.get("KX355_GEMM_TILE") in (None, "")
+    assert os.environ.get("KX355_GEMM_LDS_TILE") in (None, "")
