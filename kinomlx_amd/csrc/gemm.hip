@@ -305,21 +305,41 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint32_t* __restrict
   *reinterpret_cast<uint4*>(out + r * k + kk) = dequant8<BITS>(tmp, bf2f(scales[g]), bf2f(biases[g]));
 }
 
-// ---- direct-to-LDS pipelined kernel (K % 64 == 0) -----------------------------------------------
+// ---- direct-to-LDS pipelined kernel (K % 32 == 0) -----------------------------------------------
 //
 // Operand tiles go from global memory straight into LDS with global_load_lds_dwordx4 (no VGPR
-// staging): a wave instruction fills 8 rows of 128 B. Two LDS stages of BK = 64: the loads for
-// stage kt+1 are issued when stage kt starts; in the last k16 step of stage kt each wave waits
-// for them, the workgroup meets at one barrier, and the first fragments of stage kt+1 are read
-// while that step's MFMAs run. Fragments are double-buffered in registers across k16 steps, and
-// the schedule interleaves one fragment read per MFMA. The 16-byte slot of row r holds chunk
-// c ^ ((r ^ (r >> 3)) & 7): conflict-free for the 32-row fragment reads with 64 banks (and 32).
+// staging): one wave instruction fills 64 lanes x 16 B = RPI rows of BKT bf16. NS LDS stages of
+// BKT = 32 along K form a ring: while stage kt is consumed, stages kt+1 .. kt+NS-1 are in flight.
+// Each wave issues its DMA instructions for stage kt+NS-1 between the MFMAs of the first k16
+// steps, from a scalar tile base plus a loop-invariant 32-bit lane offset. Every k16 step is
+// one scheduling region: wait for this step's fragments (read one step earlier), issue the
+// fragment reads of the next step, then the step's MFMAs — so LDS latency hides under a full
+// step of MFMAs and never more than MB + NB reads are outstanding (lgkmcnt counts to 15). The
+// last step of a stage holds the stage's only workgroup barrier. The 16-byte slot of a row is
+// XOR-swizzled so that both the DMA writes and the 32-row fragment reads are bank-conflict free.
 //
 // Epilogue: each wave stages half of its fp32 tile in LDS at a time and writes it back in rows,
-// 4 columns per lane, so bias / gate / residual loads and the stores are contiguous runs.
+// 4 columns per lane, so bias / gate / residual loads and the stores are contiguous runs. Full,
+// aligned tiles take a compile-time specialisation per residual mode (GMODE 0: none, 1: bf16
+// residual, 2: fp32 residual) and output type; edge tiles take the generic masked path.
 
-__device__ __forceinline__ int swz8(int r) { return (r ^ (r >> 3)) & 7; }
+constexpr int DBK = 32;                // K per LDS stage
+constexpr int DROW = DBK * 2;          // bytes per LDS row
+constexpr int DCPR = DBK / 8;          // 16-byte chunks per row
+constexpr int DRPI = 64 / DCPR;        // rows one DMA instruction fills
+constexpr int DNS = 4;                 // stages in the ring
+__device__ __forceinline__ int dswz(int r) { return (r >> 2) & 3; }
 #define KX_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+// A workgroup barrier that the compiler may not move memory accesses across.
+#define KX_BARRIER() asm volatile("s_barrier" ::: "memory")
+
+// gfx9 s_waitcnt immediate that waits for vmcnt <= N only.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
 // bias + activation + gated residual on 4 consecutive columns n..n+3 of row m, then the store.
 __device__ __forceinline__ void epilogue_store4(float v[4], int m, int n, int N, const Epilogue& epi,
@@ -378,23 +398,29 @@ __device__ __forceinline__ void epilogue_store4(float v[4], int m, int n, int N,
   }
 }
 
-template <int BM, int BN>
+template <int BM, int BN, int GMODE, bool OUTF32>
 __global__ __launch_bounds__(256) void gemm_lds_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ W, int64_t ldw,
     void* __restrict__ C, int64_t ldc, int M, int N, int K, Epilogue epi) {
-  constexpr int RPI = 8;  // rows one DMA instruction fills (64 lanes x 16 B over 128-B rows)
-  constexpr int A_INST = BM / RPI / 4, W_INST = BN / RPI / 4;
-  constexpr int STAGE = (BM + BN) * ROWB;
+  constexpr int A_INST = BM / DRPI / 4, W_INST = BN / DRPI / 4;
+  constexpr int PER = A_INST + W_INST;  // DMA instructions per wave per stage
+  constexpr int STAGE = (BM + BN) * DROW;
   constexpr int WT_M = BM / 2, WT_N = BN / 2;
   constexpr int MB = WT_M / 32, NB = WT_N / 32;
-  constexpr int KS = BK / 16;
+  constexpr int KS = DBK / 16;
+  constexpr int DPS = (PER + KS - 1) / KS;  // DMA instructions per k16 step
+  // At the wait in the last k16 step, stages kt+2 .. kt+NS-2 and the DMA of this iteration's
+  // earlier steps may stay in flight: stage kt+1 is then complete.
+  constexpr int WAITN = (DNS - 3) * PER + ((KS - 1) * DPS < PER ? (KS - 1) * DPS : PER);
   constexpr int PITCH = WT_N / 2 + 4;  // staged epilogue row, floats
   constexpr int EP_BYTES = 4 * WT_M * PITCH * 4;
-  constexpr int SMEM = 2 * STAGE > EP_BYTES ? 2 * STAGE : EP_BYTES;
-  static_assert(A_INST * RPI * 4 == BM && W_INST * RPI * 4 == BN && MB >= 1 && NB >= 2, "tile");
+  constexpr int SMEM = DNS * STAGE > EP_BYTES ? DNS * STAGE : EP_BYTES;
+  static_assert(A_INST * DRPI * 4 == BM && W_INST * DRPI * 4 == BN && MB >= 1 && NB >= 2, "tile");
+  static_assert(MB + NB <= 15 && WAITN >= 0, "pipeline");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave & 1, wn = wave >> 1;
   const int lrow = lane & 31, lhalf = lane >> 5;
 
@@ -408,29 +434,29 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
   const int m0 = (first_m + (t % group_width) % gsz) * BM;
   const int n0 = ((t % group_width) / gsz) * BN;
 
-  // per-lane DMA sources: lane -> row lane / 8 of the instruction's 8 rows, slot lane % 8
-  const int r_in = lane >> 3, slot = lane & 7;
-  const uint16_t* a_src[A_INST];
-  const uint16_t* w_src[W_INST];
+  // per-lane DMA sources: lane -> row lane / DCPR of the instruction's rows, slot lane % DCPR;
+  // rows past the end re-read the last row (in bounds; their results are never stored)
+  const int r_in = lane / DCPR, slot = lane % DCPR;
+  uint32_t vo[PER];
 #pragma unroll
   for (int i = 0; i < A_INST; ++i) {
-    const int r = (wave * A_INST + i) * RPI + r_in;
-    a_src[i] = A + (int64_t)min(m0 + r, M - 1) * lda + (slot ^ swz8(r)) * 8;
+    const int r = (wave * A_INST + i) * DRPI + r_in;
+    vo[i] = (uint32_t)(((int64_t)(min(m0 + r, M - 1) - m0) * lda + (slot ^ dswz(r)) * 8) * 2);
   }
 #pragma unroll
   for (int i = 0; i < W_INST; ++i) {
-    const int r = (wave * W_INST + i) * RPI + r_in;
-    w_src[i] = W + (int64_t)min(n0 + r, N - 1) * ldw + (slot ^ swz8(r)) * 8;
+    const int r = (wave * W_INST + i) * DRPI + r_in;
+    vo[A_INST + i] = (uint32_t)(((int64_t)(min(n0 + r, N - 1) - n0) * ldw + (slot ^ dswz(r)) * 8) * 2);
   }
-  auto issue = [&](uint8_t* buf, int k0) {
-#pragma unroll
-    for (int i = 0; i < A_INST; ++i)
-      __builtin_amdgcn_global_load_lds((const void*)(a_src[i] + k0),
-                                       KX_LDS(buf + (wave * A_INST + i) * RPI * ROWB), 16, 0, 0);
-#pragma unroll
-    for (int i = 0; i < W_INST; ++i)
-      __builtin_amdgcn_global_load_lds((const void*)(w_src[i] + k0),
-                                       KX_LDS(buf + (BM + (wave * W_INST + i) * RPI) * ROWB), 16, 0, 0);
+  const char* a_base = reinterpret_cast<const char*>(A + (int64_t)m0 * lda);
+  const char* w_base = reinterpret_cast<const char*>(W + (int64_t)n0 * ldw);
+  auto dma = [&](int i, uint8_t* buf, int k0) {
+    if (i < A_INST)
+      __builtin_amdgcn_global_load_lds((const void*)(a_base + (int64_t)k0 * 2 + vo[i]),
+                                       KX_LDS(buf + (wave * A_INST + i) * DRPI * DROW), 16, 0, 0);
+    else
+      __builtin_amdgcn_global_load_lds((const void*)(w_base + (int64_t)k0 * 2 + vo[i]),
+                                       KX_LDS(buf + (BM + (wave * W_INST + i - A_INST) * DRPI) * DROW), 16, 0, 0);
   };
 
   // fragment byte offsets within a stage, per k16 step (the MFMA A operand is the weight tile)
@@ -441,12 +467,12 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
 #pragma unroll
     for (int j = 0; j < MB; ++j) {
       const int r = wm * WT_M + j * 32 + lrow;
-      a_off[s][j] = r * ROWB + ((c ^ swz8(r)) << 4);
+      a_off[s][j] = r * DROW + ((c ^ dswz(r)) << 4);
     }
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
       const int r = BM + wn * WT_N + i * 32 + lrow;
-      w_off[s][i] = r * ROWB + ((c ^ swz8(r)) << 4);
+      w_off[s][i] = r * DROW + ((c ^ dswz(r)) << 4);
     }
   }
   auto load_frags = [&](const uint8_t* buf, int s, bf16x8* af, bf16x8* wf) {
@@ -464,54 +490,73 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  const int stages = K / BK;
-  issue(smem, 0);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-
+  const int stages = K / DBK;
+#pragma unroll
+  for (int p = 0; p < DNS - 1; ++p)
+#pragma unroll
+    for (int i = 0; i < PER; ++i) dma(i, smem + p * STAGE, min(p, stages - 1) * DBK);
+  wait_vmcnt<(DNS - 2) * PER>();
+  KX_BARRIER();
   bf16x8 fa[2][MB], fw[2][NB];
   load_frags(smem, 0, fa[0], fw[0]);
+  int cur_i = 0;
   for (int kt = 0; kt < stages; ++kt) {
-    const uint8_t* cur = smem + (kt & 1) * STAGE;
-    uint8_t* nxt = smem + ((kt + 1) & 1) * STAGE;
-    // the last iteration re-loads the last stage into the idle buffer: the loop stays branch-free
-    issue(nxt, min(kt + 1, stages - 1) * BK);
+    const uint8_t* cur = smem + cur_i * STAGE;
+    const int nxt_i = cur_i + 1 == DNS ? 0 : cur_i + 1;
+    // stage kt+NS-1 goes into the buffer stage kt-1 used; past the end the last stage is
+    // re-read into it, which keeps the loop free of branches and the vmcnt arithmetic uniform
+    uint8_t* iss = smem + (cur_i == 0 ? DNS - 1 : cur_i - 1) * STAGE;
+    const int k_iss = min(kt + DNS - 1, stages - 1) * DBK;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const int b = s & 1;
+      __builtin_amdgcn_sched_barrier(0);
+      wait_lgkmcnt0();
+      __builtin_amdgcn_sched_barrier(0);
       if (s + 1 < KS) {
         load_frags(cur, s + 1, fa[b ^ 1], fw[b ^ 1]);
       } else {
         // stage kt+1 has landed for this wave and its reads of cur are done; after the barrier
-        // it has landed for every wave, and nobody reads cur again before it is refilled.
-        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        load_frags(nxt, 0, fa[b ^ 1], fw[b ^ 1]);
+        // it has landed for every wave, and nobody reads cur again before it is refilled
+        wait_vmcnt<WAITN>();
+        KX_BARRIER();
+        load_frags(smem + nxt_i * STAGE, 0, fa[b ^ 1], fw[b ^ 1]);
       }
+#pragma unroll
+      for (int d = 0; d < DPS; ++d)
+        if (s * DPS + d < PER) dma(s * DPS + d, iss, k_iss);
 #pragma unroll
       for (int i = 0; i < NB; ++i)
 #pragma unroll
         for (int j = 0; j < MB; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fw[b][i], fa[b][j], acc[i][j], 0, 0, 0);
-      // one fragment read between consecutive MFMAs, then the rest of the MFMAs
+      // the fragment reads for the next step first, then MFMAs with the DMA issues between them
+      __builtin_amdgcn_sched_group_barrier(0x100, MB + NB, 0);
 #pragma unroll
-      for (int q = 0; q < MB + NB; ++q) {
+      for (int q = 0; q < DPS; ++q) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
       }
-      __builtin_amdgcn_sched_group_barrier(0x008, NB * MB - (MB + NB), 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, NB * MB - DPS, 0);
     }
+    cur_i = nxt_i;
   }
+  wait_vmcnt<0>();
 
   // ---- epilogue: the accumulator lane holds row m = j*32 + lrow and columns 8g + 4 lhalf + e of
   // block i; staged per half of the wave's columns into a private LDS region.
   const bool vec_ok = (ldc % 4 == 0) && (!(epi.flags & KX_EPI_GATED_RESIDUAL) || epi.ldr % 4 == 0);
+  const bool full = vec_ok && m0 + BM <= M && n0 + BN <= N;
   float* ep = reinterpret_cast<float*>(smem) + wave * (WT_M * PITCH);
   constexpr int HALF_N = WT_N / 2;
   constexpr int LPR = HALF_N / 4;  // lanes per staged row
   constexpr int RPI_EP = 64 / LPR;   // rows per read-back iteration
   const int q = lane % LPR, rr = lane / LPR;
-  __builtin_amdgcn_s_barrier();  // every wave is done with the main loop's LDS
+  const int act = (epi.flags >> 4) & 15;
+  const bool has_bias = epi.flags & KX_EPI_BIAS;
+  const int mrow0 = m0 + wm * WT_M;
+  KX_BARRIER();  // every wave is done with the main loop's LDS
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
 #pragma unroll
@@ -527,13 +572,65 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     const int n = n0 + wn * WT_N + h * HALF_N + 4 * q;
+    if (full) {
+      // column data is fixed per lane: bias, and the gate when one gate row covers the rows
+      float b4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (has_bias) {
+        const uint2 bb = *reinterpret_cast<const uint2*>(epi.bias + n);
+        b4[0] = lo_f(bb.x); b4[1] = hi_f(bb.x); b4[2] = lo_f(bb.y); b4[3] = hi_f(bb.y);
+      }
+      const int64_t gstride = epi.gate_stride, gdiv = epi.gate_div;
+      const bool gate_const = GMODE == 0 || gstride == 0 || (mrow0 / gdiv) == ((mrow0 + WT_M - 1) / gdiv);
+      float4 g4c = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (GMODE != 0 && gate_const) g4c = *reinterpret_cast<const float4*>(epi.gate + (mrow0 / gdiv) * gstride + n);
+      char* cbase = reinterpret_cast<char*>(C) + ((int64_t)mrow0 * ldc + n) * (OUTF32 ? 4 : 2);
+      const char* rbase = GMODE == 0 ? nullptr
+          : reinterpret_cast<const char*>(epi.resid) + ((int64_t)mrow0 * epi.ldr + n) * (GMODE == 2 ? 4 : 2);
+#pragma unroll 4
+      for (int r = rr; r < WT_M; r += RPI_EP) {
+        const float4 a4 = *reinterpret_cast<const float4*>(ep + r * PITCH + 4 * q);
+        float v[4] = {a4.x + b4[0], a4.y + b4[1], a4.z + b4[2], a4.w + b4[3]};
+        if (act) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = apply_act(v[e], act);
+        }
+        if (GMODE != 0) {
+          float4 gv = g4c;
+          if (!gate_const) {
+            const int64_t grow = gdiv == 1 ? (int64_t)(mrow0 + r) : (int64_t)(mrow0 + r) / gdiv;
+            gv = *reinterpret_cast<const float4*>(epi.gate + grow * gstride + n);
+          }
+          float rv[4];
+          if (GMODE == 2) {
+            const float4 x = *reinterpret_cast<const float4*>(rbase + (int64_t)r * epi.ldr * 4);
+            rv[0] = x.x; rv[1] = x.y; rv[2] = x.z; rv[3] = x.w;
+          } else {
+            const uint2 x = *reinterpret_cast<const uint2*>(rbase + (int64_t)r * epi.ldr * 2);
+            rv[0] = lo_f(x.x); rv[1] = hi_f(x.x); rv[2] = lo_f(x.y); rv[3] = hi_f(x.y);
+          }
+          v[0] = rv[0] + gv.x * v[0];
+          v[1] = rv[1] + gv.y * v[1];
+          v[2] = rv[2] + gv.z * v[2];
+          v[3] = rv[3] + gv.w * v[3];
+        }
+        if (OUTF32) {
+          *reinterpret_cast<float4*>(cbase + (int64_t)r * ldc * 4) = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+          uint2 o;
+          o.x = pack2(v[0], v[1]);
+          o.y = pack2(v[2], v[3]);
+          *reinterpret_cast<uint2*>(cbase + (int64_t)r * ldc * 2) = o;
+        }
+      }
+    } else {
 #pragma unroll 2
-    for (int r = rr; r < WT_M; r += RPI_EP) {
-      const int m = m0 + wm * WT_M + r;
-      const float4 a4 = *reinterpret_cast<const float4*>(ep + r * PITCH + 4 * q);
-      if (m < M && n < N) {
-        float v[4] = {a4.x, a4.y, a4.z, a4.w};
-        epilogue_store4(v, m, n, N, epi, C, ldc, vec_ok);
+      for (int r = rr; r < WT_M; r += RPI_EP) {
+        const int m = mrow0 + r;
+        const float4 a4 = *reinterpret_cast<const float4*>(ep + r * PITCH + 4 * q);
+        if (m < M && n < N) {
+          float v[4] = {a4.x, a4.y, a4.z, a4.w};
+          epilogue_store4(v, m, n, N, epi, C, ldc, vec_ok);
+        }
       }
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -573,12 +670,28 @@ int pick_cfg(int64_t m, int64_t n) {
   return T128x128;
 }
 
+template <int BM, int BN, int GMODE, bool OUTF32>
+int launch_lds_t(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, void* c, int64_t ldc,
+                 int m, int n, int k, const Epilogue& epi, hipStream_t s) {
+  const int tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+  gemm_lds_kernel<BM, BN, GMODE, OUTF32><<<tiles, 256, 0, s>>>(a, lda, w, ldw, c, ldc, m, n, k, epi);
+  return KX_OK;
+}
+
+// Residual mode (none / bf16 / fp32) and output type select the epilogue specialisation.
 template <int BM, int BN>
 int launch_lds(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, void* c, int64_t ldc,
                int m, int n, int k, const Epilogue& epi, hipStream_t s) {
-  const int tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
-  gemm_lds_kernel<BM, BN><<<tiles, 256, 0, s>>>(a, lda, w, ldw, c, ldc, m, n, k, epi);
-  return KX_OK;
+  const int gmode = (epi.flags & KX_EPI_GATED_RESIDUAL) ? ((epi.flags & KX_EPI_RESID_F32) ? 2 : 1) : 0;
+  const bool out32 = epi.flags & KX_EPI_OUT_F32;
+  switch (gmode * 2 + (out32 ? 1 : 0)) {
+    case 0: return launch_lds_t<BM, BN, 0, false>(a, lda, w, ldw, c, ldc, m, n, k, epi, s);
+    case 1: return launch_lds_t<BM, BN, 0, true>(a, lda, w, ldw, c, ldc, m, n, k, epi, s);
+    case 2: return launch_lds_t<BM, BN, 1, false>(a, lda, w, ldw, c, ldc, m, n, k, epi, s);
+    case 3: return launch_lds_t<BM, BN, 1, true>(a, lda, w, ldw, c, ldc, m, n, k, epi, s);
+    case 4: return launch_lds_t<BM, BN, 2, false>(a, lda, w, ldw, c, ldc, m, n, k, epi, s);
+    default: return launch_lds_t<BM, BN, 2, true>(a, lda, w, ldw, c, ldc, m, n, k, epi, s);
+  }
 }
 
 // Tile for the direct-to-LDS kernel: the fewest rounds of 256 workgroups, weighted by the
@@ -610,7 +723,8 @@ int dispatch(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, Qua
              void* c, int64_t ldc, int64_t m, int64_t n, int64_t k, const Epilogue& epi,
              hipStream_t s) {
   const char* legacy = getenv("KX355_GEMM_TILE");
-  if (QB == 0 && k % BK == 0 && !(legacy && *legacy)) {
+  // the direct-to-LDS kernel keeps per-lane 32-bit byte offsets within a 256-row tile
+  if (QB == 0 && k % DBK == 0 && lda <= (1 << 22) && ldw <= (1 << 22) && !(legacy && *legacy)) {
     switch (pick_lds_cfg(m, n)) {
       case 0: return launch_lds<256, 256>(a, lda, w, ldw, c, ldc, (int)m, (int)n, (int)k, epi, s);
       case 1: return launch_lds<192, 256>(a, lda, w, ldw, c, ldc, (int)m, (int)n, (int)k, epi, s);

@@ -266,11 +266,13 @@ def test_linear_matches_oracle_for_every_tile(device, monkeypatch, tile, m, n, k
 
 
 @pytest.mark.parametrize("tile", ["0", "1", "2"])
-@pytest.mark.parametrize(("m", "n", "k"), [(1056, 1040, 1024), (300, 96, 64), (513, 520, 192), (9, 8, 64)])
-@pytest.mark.parametrize("epilogue", ["bias", "gelu_tanh", "gated_f32"])
+@pytest.mark.parametrize(("m", "n", "k"), [(1056, 1040, 1024), (512, 512, 256), (300, 96, 64), (513, 520, 192), (9, 8, 64)])
+@pytest.mark.parametrize("epilogue", ["bias", "gelu_tanh", "gated_f32", "gated_bf16", "gated_f32_to_bf16", "gated_rows"])
 def test_direct_to_lds_linear_every_tile_and_epilogue(device, monkeypatch, tile, m, n, k, epilogue):
-    """The K % 64 == 0 direct-to-LDS kernel at each of its tiles (256x256, 192x256, 128x128) on
-    ragged M and N (partial tiles, clamped loads, masked stores) with each epilogue family."""
+    """The K % 32 == 0 direct-to-LDS kernel at each of its tiles (256x256, 192x256, 128x128) on
+    full tiles (the compile-time epilogue) and ragged M and N (partial tiles, clamped loads,
+    masked stores) with each epilogue family: residual fp32 or bf16, output fp32 or bf16, one
+    broadcast gate row or one gate row per output row."""
     monkeypatch.setenv("KX355_GEMM_LDS_TILE", tile)
     x, w, b = _linear_case(m, n, k, m + n + k + 1, device)
     lin = oracle.linear(x, w, b)
@@ -284,11 +286,21 @@ def test_direct_to_lds_linear_every_tile_and_epilogue(device, monkeypatch, tile,
     else:
         r = _rng(m + n)
         resid = r.standard_normal((m, n)).astype(F32)
-        gate = r.standard_normal(n).astype(F32)
-        out = mpp_linear.fused_linear(_bf(x, device), _bf(w, device), _bf(b, device), residual=_f32(resid, device),
-                                      gate=_f32(gate, device), out_dtype=torch.float32)
+        gate = r.standard_normal((m, n) if epilogue == "gated_rows" else n).astype(F32)
+        if epilogue == "gated_bf16":
+            resid = oracle.to_bf16(resid)
+            resid_t, out_dtype = _bf(resid, device), torch.float32
+        elif epilogue == "gated_f32_to_bf16":
+            resid_t, out_dtype = _f32(resid, device), torch.bfloat16
+        else:
+            resid_t, out_dtype = _f32(resid, device), torch.float32
+        out = mpp_linear.fused_linear(_bf(x, device), _bf(w, device), _bf(b, device), residual=resid_t,
+                                      gate=_f32(gate, device), out_dtype=out_dtype)
         ref = resid + gate * lin
-        assert np.all(np.abs(_np(out) - ref) <= 1e-5 * np.abs(ref) + 2e-5 * np.abs(ref).max())
+        tol = 1e-5 * np.abs(ref) + 2e-5 * np.abs(ref).max()
+        if out_dtype == torch.bfloat16:
+            tol = tol + np.abs(ref) * 2.0**-8
+        assert np.all(np.abs(_np(out) - ref) <= tol)
 
 
 def test_linear_takes_in_out_weights(device):
