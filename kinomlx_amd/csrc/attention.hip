@@ -1,24 +1,30 @@
 // Non-causal flash attention on gfx950 MFMA for token-major flattened heads.
 //
-// One workgroup = 4 waves = 128 queries of one head; each wave owns 32 queries. K and V advance
-// in tiles of 64 keys through a double-buffered LDS stage (global loads for tile i+1 are issued
-// before tile i's MFMAs and written to the other buffer afterwards; one barrier per tile).
+// One workgroup = 8 waves = 256 queries of one head; each wave owns 32 queries and keeps them in
+// registers as the MFMA B operand for the whole key loop. Waves w and w + 4 share a SIMD.
 //
-// Layout trick: scores are computed transposed, S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (A =
-// 32 keys from LDS, B = the wave's 32 queries held in registers for the whole loop). The
-// accumulator's lane then holds one query (lane % 32) and 16 of the 32 keys, so the softmax row
-// max / sum is an in-lane reduction plus one exchange with lane ^ 32. The output is accumulated
-// transposed too, O^T += V^T P^T: P^T comes straight out of the S^T accumulator (converted to
-// bf16) as the B operand, and V^T is the A operand read from an LDS tile that the loader writes
-// transposed (rows = head dims, 64 keys per row), with keys permuted inside each 16-key group as
-// {0-3, 8-11 | 4-7, 12-15} so that one 16-byte LDS read gives a lane exactly the 8 keys its P^T
-// operand covers.
+// K and V tiles of 64 keys go from global memory straight into LDS with global_load_lds_dwordx4
+// (no VGPR staging) through a ring of 4 stages: while tile i is consumed, tiles i+1 .. i+3 are in
+// flight. Each wave issues 1/8 of a stage's DMA instructions; one workgroup barrier per tile makes
+// tile i visible and frees the buffer of tile i-1 for tile i+3.
 //
-// Softmax: scores scaled into the exp2 domain (scale * log2 e folded into one multiply), running
-// max per query, the O^T rescale skipped when no query's max moved in a tile, fp32 sums. Keys
-// past the end are masked to -inf; queries past the end are computed on a clamped row and not
-// stored. An optional per-(query, head) gate multiplies the output before the single bf16
-// rounding.
+// Scores are computed transposed, S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (A = 32 keys read from
+// LDS, B = the wave's 32 queries): the accumulator lane holds one query (lane % 32) and 16 of the
+// 32 keys, so the row max is an in-lane reduction plus one exchange with lane ^ 32. The output
+// is accumulated transposed too, O^T += V^T P^T: P^T comes straight out of the S^T accumulator
+// (converted to bf16) as the B operand, with the 16 keys of an MFMA step taken in the order
+// {0-3, 8-11 | 4-7, 12-15} that the accumulator layout gives; V^T is the A operand, read from the
+// V tile kept in its natural key-major layout by the transposing ds_read_b64_tr_b16: a read of 16
+// lanes, each addressing 4 dims of one key, hands lane i dim i of 4 consecutive keys.
+//
+// LDS rows are 2 * D bytes with their 16-byte chunks XOR-swizzled per row: for K so that the 32-row
+// fragment reads hit distinct banks, for V so that each transposing read (4 keys x 4 chunks) does.
+//
+// Softmax: fp32, in the exp2 domain with the scale * log2 e folded into one FMA per score. The
+// running max is lazy: it moves (and O, l are rescaled) only when a score exceeds it by more than
+// 2^8 in the exp2 domain, so p stays below 256 (exact in fp32 and bf16) and rescales are rare.
+// Keys past the end are masked to -inf; queries past the end run on a clamped row and are not
+// stored. An optional per-(query, head) gate multiplies the output before the single bf16 rounding.
 #include <math.h>
 
 #include "common.h"
@@ -26,48 +32,65 @@
 namespace kx {
 namespace {
 
-constexpr int BQ = 128;  // queries per workgroup (4 waves x 32)
-constexpr int BKV = 64;  // keys per LDS tile
+constexpr int NWAVE = 8;           // waves per workgroup
+constexpr int BQ = 32 * NWAVE;     // queries per workgroup
+constexpr int BKV = 64;            // keys per LDS tile
+constexpr int NSTAGE = 4;          // tiles in the LDS ring
+constexpr float LAZY_TH = 8.0f;    // exp2-domain slack of the running max
 
-__device__ __forceinline__ uint32_t half16(const uint4& v, int j) {
-  const uint32_t w = (j >> 1) == 0 ? v.x : (j >> 1) == 1 ? v.y : (j >> 1) == 2 ? v.z : v.w;
-  return (j & 1) ? (w >> 16) : (w & 0xffffu);
+#define KX_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+// A workgroup barrier that the compiler may not move memory accesses across.
+#define KX_BARRIER() asm volatile("s_barrier" ::: "memory")
+typedef short v4s __attribute__((ext_vector_type(4)));
+
+// gfx9 s_waitcnt immediate that waits for vmcnt <= N only.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Swizzle of 16-byte chunks in a 128-byte V^T row: distinct for 8 consecutive rows (fragment
-// reads) and for rows 8 apart (the transposing writes).
-__device__ __forceinline__ int vt_swz(int d) { return (d ^ (d >> 3)) & 7; }
+// K rows: 16 consecutive keys hit 16 distinct 16-byte slots (and the swizzle depends on the key
+// modulo 16 only, so key block 1 is key block 0 plus 32 rows). V rows: the 4 keys x 4 chunks of a
+// transposing read hit distinct slots.
+template <int D> __device__ __forceinline__ int swz_k(int r) { return D == 128 ? (r & 15) : ((r >> 1) & 7); }
+template <int D> __device__ __forceinline__ int swz_v(int r) { return D == 128 ? 4 * (r & 3) : 4 * ((r >> 1) & 1); }
+
+__device__ __forceinline__ bf16x8 read_vt(const uint8_t* p, int second) {
+  const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(p));
+  const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(p + second));
+  // whole-word casts: the operand is the two 8-byte results back to back
+  const uint2 lo2 = __builtin_bit_cast(uint2, lo), hi2 = __builtin_bit_cast(uint2, hi);
+  return __builtin_bit_cast(bf16x8, make_uint4(lo2.x, lo2.y, hi2.x, hi2.y));
+}
 
 template <int D>
-__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(
+__global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
     const uint16_t* __restrict__ Q, int64_t ldq, const uint16_t* __restrict__ K, int64_t ldk,
     const uint16_t* __restrict__ V, int64_t ldv, uint16_t* __restrict__ O, int64_t ldo, int tq,
     int tk, int heads, float scale_log2, const uint16_t* __restrict__ gate, int64_t ld_gate,
     int qtiles) {
-  constexpr int DC = D / 8;           // 16-byte chunks per K row
-  constexpr int KROWB = D * 2;        // bytes per K row in LDS
-  constexpr int KT_BYTES = BKV * KROWB;
-  constexpr int VROWB = BKV * 2;      // bytes per V^T row (64 keys)
-  constexpr int STAGE = KT_BYTES + D * VROWB;
-  constexpr int QS = D / 16;          // k16 steps of Q K^T
-  constexpr int DB = D / 32;          // 32-row blocks of O^T
-  constexpr int K_PER = BKV * DC / 256;
-  constexpr int VBLK = (BKV / 4) * DC;  // (4-key, 8-dim) transpose blocks per tile
-  static_assert(K_PER >= 1 && VBLK <= 256, "tile shape");
+  constexpr int ROWB = D * 2;             // bytes per K / V row
+  constexpr int CPR = ROWB / 16;          // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;           // rows per DMA instruction
+  constexpr int TILE = BKV * ROWB;        // one K (or V) tile
+  constexpr int STAGE = 2 * TILE;
+  constexpr int INST = 2 * BKV / RPI;     // DMA instructions per stage (K then V)
+  constexpr int PER = INST / NWAVE;       // per wave
+  static_assert(PER * NWAVE == INST, "DMA split");
+  constexpr int QS = D / 16, DB = D / 32;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[NSTAGE * STAGE];
 
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * STAGE];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lrow = lane & 31, lhalf = lane >> 5;
-
-  // Work order: XCD-contiguous so the workgroups of one XCD share few heads' K/V in its L2.
+  // work order: XCD-contiguous so the workgroups of one XCD share few heads' K/V in its L2
   const int t = xcd_remap(blockIdx.x, gridDim.x);
-  const int qt = t % qtiles;
-  const int bh = t / qtiles;
+  const int qt = t % qtiles, bh = t / qtiles;
   const int h = bh % heads, b = bh / heads;
   const uint16_t* Qb = Q + (int64_t)b * tq * ldq + (int64_t)h * D;
-  const uint16_t* Kb = K + (int64_t)b * tk * ldk + (int64_t)h * D;
-  const uint16_t* Vb = V + (int64_t)b * tk * ldv + (int64_t)h * D;
+  const char* Kb = reinterpret_cast<const char*>(K + (int64_t)b * tk * ldk + (int64_t)h * D);
+  const char* Vb = reinterpret_cast<const char*>(V + (int64_t)b * tk * ldv + (int64_t)h * D);
 
   const int q0 = qt * BQ + wave * 32;
   const int qrow = min(q0 + lrow, tq - 1);
@@ -76,67 +99,67 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(
   for (int s = 0; s < QS; ++s)
     qf[s] = *reinterpret_cast<const bf16x8*>(Qb + (int64_t)qrow * ldq + (2 * s + lhalf) * 8);
 
-  uint4 rk[K_PER];
-  uint4 rv[4];
-  const int v_do = tid % DC, v_kq = tid / DC;
-
-  auto load_kv = [&](int j0) {
+  // DMA: instruction g = wave * PER + i of a stage fills RPI rows of the K tile (g < INST / 2) or
+  // the V tile; lane -> row lane / CPR, slot lane % CPR, which holds chunk slot ^ swz(row). Keys
+  // past the end re-read the last key (in bounds; masked below).
+  const int r_in = lane / CPR, slot = lane % CPR;
+  int dma_row[PER];
+  uint32_t dma_col[PER];
+  bool dma_isv[PER];
 #pragma unroll
-    for (int i = 0; i < K_PER; ++i) {
-      const int q = tid + 256 * i;
-      const int key = q / DC, c = q % DC;
-      const int gk = min(j0 + key, tk - 1);
-      rk[i] = *reinterpret_cast<const uint4*>(Kb + (int64_t)gk * ldk + c * 8);
-    }
-    if (tid < VBLK) {
+  for (int i = 0; i < PER; ++i) {
+    const int g = wave * PER + i;
+    const bool isv = g >= INST / 2;
+    const int r = (isv ? g - INST / 2 : g) * RPI + r_in;
+    dma_isv[i] = isv;
+    dma_row[i] = r;
+    dma_col[i] = (uint32_t)((slot ^ (isv ? swz_v<D>(r) : swz_k<D>(r))) * 16);
+  }
+  auto issue = [&](uint8_t* buf, int j0) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int gk = min(j0 + 4 * v_kq + r, tk - 1);
-        rv[r] = *reinterpret_cast<const uint4*>(Vb + (int64_t)gk * ldv + v_do * 8);
-      }
-    }
-  };
-
-  auto store_kv = [&](uint8_t* buf) {
-#pragma unroll
-    for (int i = 0; i < K_PER; ++i) {
-      const int q = tid + 256 * i;
-      const int key = q / DC, c = q % DC;
-      *reinterpret_cast<uint4*>(buf + key * KROWB + ((c ^ (key & 7)) << 4)) = rk[i];
-    }
-    if (tid < VBLK) {
-      const int grp = v_kq >> 2, q4 = v_kq & 3;
-      const int ch = 2 * grp + (q4 & 1);
-      const int off = (q4 >> 1) * 8;
-      uint8_t* vt = buf + KT_BYTES;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int d = v_do * 8 + j;
-        uint2 w;
-        w.x = half16(rv[0], j) | (half16(rv[1], j) << 16);
-        w.y = half16(rv[2], j) | (half16(rv[3], j) << 16);
-        *reinterpret_cast<uint2*>(vt + d * VROWB + ((ch ^ vt_swz(d)) << 4) + off) = w;
-      }
+    for (int i = 0; i < PER; ++i) {
+      const int key = min(j0 + dma_row[i], tk - 1);
+      const char* src = (dma_isv[i] ? Vb + (int64_t)key * ldv * 2 : Kb + (int64_t)key * ldk * 2) + dma_col[i];
+      __builtin_amdgcn_global_load_lds((const void*)src, KX_LDS(buf + (wave * PER + i) * 1024), 16, 0, 0);
     }
   };
+
+  // fragment offsets: one per K step (key block kb adds 32 rows) and one per V dim block (the key
+  // step adds whole rows); the rest are immediate offsets of the LDS reads
+  int koff[QS];
+#pragma unroll
+  for (int st = 0; st < QS; ++st) koff[st] = lrow * ROWB + (((2 * st + lhalf) ^ swz_k<D>(lrow)) << 4);
+  // transposing read q of key step ts: lane group g16 = lane / 16, r16 = lane % 16 addresses key
+  // 16 ts + 8 q + 4 (g16 >> 1) + (r16 >> 2), dims 32 db + 16 (g16 & 1) + 4 (r16 & 3) .. +3
+  const int g16 = lane >> 4, r16 = lane & 15;
+  const int vkey = 4 * (g16 >> 1) + (r16 >> 2);
+  int voff[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+    const int dim = 32 * db + 16 * (g16 & 1) + 4 * (r16 & 3);
+    voff[db] = TILE + vkey * ROWB + (((dim >> 3) ^ swz_v<D>(vkey)) << 4) + ((dim >> 2) & 1) * 8;
+  }
 
   f32x16 o[DB];
 #pragma unroll
   for (int i = 0; i < DB; ++i)
 #pragma unroll
     for (int e = 0; e < 16; ++e) o[i][e] = 0.0f;
-  float m_run = -INFINITY;  // running max, exp2 domain
+  float m_run = -INFINITY;  // running max of the raw scores (the exp2 domain is m_run * scale_log2)
   float l_run = 0.0f;       // this lane's partial row sum
 
   const int ntiles = (tk + BKV - 1) / BKV;
-  load_kv(0);
-  store_kv(smem);
-  __syncthreads();
-
+#pragma unroll
+  for (int p = 0; p < NSTAGE - 1; ++p) issue(smem + p * STAGE, min(p, ntiles - 1) * BKV);
+  int cur_i = 0;
   for (int it = 0; it < ntiles; ++it) {
-    const uint8_t* cur = smem + (it & 1) * STAGE;
-    const bool more = it + 1 < ntiles;
-    if (more) load_kv((it + 1) * BKV);
+    // tile it has landed for this wave; after the barrier for every wave, and every wave is done
+    // with tile it-1, whose buffer takes tile it+3 (past the end the last tile is re-read, which
+    // keeps the vmcnt arithmetic uniform)
+    wait_vmcnt<(NSTAGE - 2) * PER>();
+    KX_BARRIER();
+    const uint8_t* cur = smem + cur_i * STAGE;
+    issue(smem + (cur_i == 0 ? NSTAGE - 1 : cur_i - 1) * STAGE, min(it + NSTAGE - 1, ntiles - 1) * BKV);
 
     // S^T = K Q^T for two 32-key blocks
     f32x16 s[2];
@@ -144,35 +167,31 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) s[kb][e] = 0.0f;
-      const int krow = kb * 32 + lrow;
 #pragma unroll
       for (int st = 0; st < QS; ++st) {
-        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(
-            cur + krow * KROWB + (((2 * st + lhalf) ^ (krow & 7)) << 4));
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(cur + koff[st] + kb * 32 * ROWB);
         s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], s[kb], 0, 0, 0);
       }
     }
-
-    // scale into the exp2 domain, mask keys past the end
     const int j0 = it * BKV;
-    const bool tail = j0 + BKV > tk;
-    float tmax = -INFINITY;
+    if (j0 + BKV > tk) {
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        float x = s[kb][e] * scale_log2;
-        if (tail) {
+        for (int e = 0; e < 16; ++e) {
           const int key = j0 + kb * 32 + 8 * (e >> 2) + 4 * lhalf + (e & 3);
-          if (key >= tk) x = -INFINITY;
+          if (key >= tk) s[kb][e] = -INFINITY;
         }
-        s[kb][e] = x;
-        tmax = fmaxf(tmax, x);
-      }
+    }
+    float tmax = s[0][0];
+#pragma unroll
+    for (int e = 1; e < 16; ++e) tmax = fmaxf(tmax, s[0][e]);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, s[1][e]);
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float m_new = fmaxf(m_run, tmax);
-    if (__any(m_new != m_run)) {
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    if (__any(tmax * scale_log2 > m_run * scale_log2 + LAZY_TH || m_run == -INFINITY)) {
+      const float m_new = fmaxf(m_run, tmax);
+      const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
       l_run *= alpha;
 #pragma unroll
       for (int i = 0; i < DB; ++i)
@@ -182,6 +201,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(
     }
 
     // P^T in bf16 as the B operand: elements 8hf .. 8hf+7 of block kb
+    const float mc = m_run * scale_log2;
     bf16x8 pb[2][2];
     float psum = 0.0f;
 #pragma unroll
@@ -190,31 +210,23 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(
       for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float p = __builtin_amdgcn_exp2f(s[kb][8 * hf + e] - m_run);
+          const float p = __builtin_amdgcn_exp2f(fmaf(s[kb][8 * hf + e], scale_log2, -mc));
           psum += p;
           pb[kb][hf][e] = (__bf16)p;
         }
     l_run += psum;
 
-    // O^T += V^T P^T
-    const uint8_t* vt = cur + KT_BYTES;
+    // O^T += V^T P^T, 16 keys per step; step ts = 2 kb + hf uses P^T block pb[kb][hf]
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      const int d = db * 32 + lrow;
+    for (int ts = 0; ts < 4; ++ts)
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-          const int ch = 2 * (2 * kb + hf) + lhalf;
-          const bf16x8 vf =
-              *reinterpret_cast<const bf16x8*>(vt + d * VROWB + ((ch ^ vt_swz(d)) << 4));
-          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb[kb][hf], o[db], 0, 0, 0);
-        }
-    }
-
-    if (more) store_kv(smem + ((it + 1) & 1) * STAGE);
-    __syncthreads();
+      for (int db = 0; db < DB; ++db) {
+        const bf16x8 vf = read_vt(cur + voff[db] + 16 * ts * ROWB, 8 * ROWB);
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb[ts >> 1][ts & 1], o[db], 0, 0, 0);
+      }
+    cur_i = cur_i + 1 == NSTAGE ? 0 : cur_i + 1;
   }
+  wait_vmcnt<0>();  // the re-read tiles past the end have landed before the workgroup ends
 
   // normalise, gate, store: lane holds query q0 + lrow, dims db*32 + 8g + 4*lhalf + (0..3)
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
@@ -240,7 +252,7 @@ int launch_attn(const void* q, int64_t ldq, const void* k, int64_t ldk, const vo
                 float scale, const void* gate, int64_t ld_gate, hipStream_t s) {
   const int qtiles = (int)((tq + BQ - 1) / BQ);
   const int64_t blocks = (int64_t)qtiles * heads * batch;
-  attn_fwd_kernel<D><<<(unsigned)blocks, 256, 0, s>>>(
+  attn_fwd_kernel<D><<<(unsigned)blocks, NWAVE * 64, 0, s>>>(
       (const uint16_t*)q, ldq, (const uint16_t*)k, ldk, (const uint16_t*)v, ldv, (uint16_t*)o,
       ldo, (int)tq, (int)tk, (int)heads, scale * 1.4426950408889634f, (const uint16_t*)gate,
       ld_gate, qtiles);
