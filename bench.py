@@ -36,6 +36,9 @@ def _kernel_flops(name: str, args: tuple) -> float:
     if name == "kx_qgemm_affine_bf16":
         m, n, k = args[8], args[9], args[10]
         return 2.0 * m * n * k
+    if name == "kx_qgemm_affine_tiled_bf16":
+        m, n, k = args[7], args[8], args[9]
+        return 2.0 * m * n * k
     if name == "kx_attention_fwd_bf16":
         batch, tq, tk, heads, dh = args[8], args[9], args[10], args[11], args[12]
         return 4.0 * batch * heads * tq * tk * dh
@@ -47,6 +50,8 @@ def _kernel_label(name: str, args: tuple) -> str:
         return f"gemm m{args[7]} n{args[8]} k{args[9]}"
     if name == "kx_qgemm_affine_bf16":
         return f"qgemm{args[12]} m{args[8]} n{args[9]} k{args[10]}"
+    if name == "kx_qgemm_affine_tiled_bf16":
+        return f"qgemm{args[10]} tiled m{args[7]} n{args[8]} k{args[9]}"
     if name == "kx_attention_fwd_bf16":
         return f"attention tq{args[9]} tk{args[10]} h{args[11]} d{args[12]}"
     return name.replace("kx_", "").replace("_bf16", "")
@@ -172,7 +177,7 @@ def main() -> int:
 
     flops = workloads.flop_count(spec)
     attn_ms = sum(v for k, v in kernel_ms_per_step.items() if name_of[k] == "kx_attention_fwd_bf16")
-    gemm_ms = sum(v for k, v in kernel_ms_per_step.items() if name_of[k] in ("kx_gemm_bf16", "kx_qgemm_affine_bf16"))
+    gemm_ms = sum(v for k, v in kernel_ms_per_step.items() if name_of[k] in ("kx_gemm_bf16", "kx_qgemm_affine_bf16", "kx_qgemm_affine_tiled_bf16"))
     other_ms = sum(kernel_ms_per_step.values()) - attn_ms - gemm_ms
     attn_tflops = flops["attention"] / (attn_ms * 1e-3) / 1e12
     gemm_tflops = flops["gemm"] / (gemm_ms * 1e-3) / 1e12

@@ -168,6 +168,34 @@ int kx_qgemm_affine_bf16(const void* a, int64_t lda, const uint32_t* wq, const v
 int kx_dequant_affine_bf16(const uint32_t* wq, const void* scales, const void* biases, void* out,
                            int64_t n, int64_t k, int group_size, int bits, kx_stream_t stream);
 
+/*
+ * Load-time layout for kx_qgemm_affine_tiled_bf16 (no counterpart in the reference: its
+ * quantized weights stay in the packed layout above; this is the same data regrouped so that
+ * each 256-row weight tile and 32-wide K stage is one contiguous block). With npad = n rounded
+ * up to 256 (rows past n repeat row n - 1):
+ *   wt : npad * k * bits / 8 bytes; block (nb, kb) at ((nb * k/32 + kb) * 256 + r) * (4 * bits)
+ *        holds row nb*256 + r's packed bytes of k = 32 kb .. 32 kb + 31;
+ *   sbt: npad * (k / 128) * 8 bytes; block (nb, p) at ((nb * k/128 + p) * 256 + r) * 8 holds
+ *        bf16 scale[2p], scale[2p+1], bias[2p], bias[2p+1] of row nb*256 + r.
+ * Requires k % 128 == 0, group_size 64, bits 4 or 8.
+ */
+int kx_qweight_tile_affine(const uint32_t* wq, const void* scales, const void* biases, void* wt,
+                           void* sbt, int64_t n, int64_t k, int group_size, int bits,
+                           kx_stream_t stream);
+
+/*
+ * kx_qgemm_affine_bf16 on the tiled layout of kx_qweight_tile_affine: the same result
+ * (bit-exact dequantization, fp32 accumulation, one rounding), with each stage's packed weights
+ * and scale / bias pairs read as contiguous blocks. Replaces the same reference call
+ * (kinomlx/models/ltx2/weights/quantization.py:28-44); QuantizedLinear prepares the layout once.
+ * Requires k % 128 == 0 and lda <= 2^22.
+ */
+int kx_qgemm_affine_tiled_bf16(const void* a, int64_t lda, const void* wt, const void* sbt,
+                               const void* bias, void* c, int64_t ldc, int64_t m, int64_t n,
+                               int64_t k, int bits, int epilogue, const void* resid, int64_t ldr,
+                               const float* gate, int64_t gate_div, int64_t gate_stride,
+                               kx_stream_t stream);
+
 /* tanh GELU in fp32, inner argument clamped to +-10: fused_ops.gelu_approx
  * (kinomlx/kernels/fused_ops.py:27-35,327-350). */
 int kx_gelu_tanh_bf16(const void* x, void* y, int64_t count, kx_stream_t stream);

@@ -64,6 +64,10 @@ SIGNATURES: dict[str, list] = {
         _I64, _P,
     ],
     "kx_dequant_affine_bf16": [_P, _P, _P, _P, _I64, _I64, _I, _I, _P],
+    "kx_qweight_tile_affine": [_P, _P, _P, _P, _P, _I64, _I64, _I, _I, _P],
+    "kx_qgemm_affine_tiled_bf16": [
+        _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I, _P, _I64, _P, _I64, _I64, _P,
+    ],
     "kx_gelu_tanh_bf16": [_P, _P, _I64, _P],
     "kx_silu_bf16": [_P, _P, _I64, _P],
     "kx_swiglu_bf16": [_P, _I64, _P, _I64, _I64, _I64, _P],
@@ -326,6 +330,32 @@ def launch_qgemm(a, words, scales, biases, out, *, n, k, group_size, bits, bias=
         "kx_qgemm_affine_bf16", _ptr(a), lda, _ptr(words), _ptr(scales), _ptr(biases), _ptr(bias),
         _ptr(out), ldc, m, n, k, group_size, bits, flags, _ptr(resid), ldr, _ptr(gate), div,
         stride, _stream(),
+    )
+
+
+def launch_tile_weights(words, scales, biases, wt, sbt, *, n, k, group_size, bits) -> None:
+    _check_gpu("tile_weights", words, scales, biases, wt, sbt)
+    _call(
+        "kx_qweight_tile_affine", _ptr(words), _ptr(scales), _ptr(biases), _ptr(wt), _ptr(sbt), n, k,
+        group_size, bits, _stream(),
+    )
+
+
+def launch_qgemm_tiled(a, wt, sbt, out, *, n, k, bits, bias=None, flags: int = 0, resid=None,
+                       gate=None) -> None:
+    _check_gpu("qgemm_tiled", a, wt, sbt, out, bias, resid, gate)
+    flags |= _dtype_flags(out, resid, "quantized linear")
+    m, ka, lda = _rows(a, "quantized linear input")
+    if ka != k:
+        raise ValueError(f"quantized linear: input width {ka} does not match {k}")
+    _, _, ldc = _rows(out, "quantized linear output")
+    ldr, div, stride = 0, 1, 0
+    if resid is not None:
+        _, _, ldr = _rows(resid, "quantized linear residual")
+        div, stride = _mod_rows(gate, m, n, "quantized linear gate")
+    _call(
+        "kx_qgemm_affine_tiled_bf16", _ptr(a), lda, _ptr(wt), _ptr(sbt), _ptr(bias), _ptr(out), ldc, m,
+        n, k, bits, flags, _ptr(resid), ldr, _ptr(gate), div, stride, _stream(),
     )
 
 

@@ -398,24 +398,105 @@ __device__ __forceinline__ void epilogue_store4(float v[4], int m, int n, int N,
   }
 }
 
-template <int BM, int BN, int GMODE, bool OUTF32>
+// Dequantization of one stage's packed rows into the bf16 tile the MFMA loop reads: thread t owns
+// weight row t of the tile (32 k values). The packed words and the scale / bias pairs are read
+// from LDS one k16 step before the arithmetic, so their latency hides under MFMAs. The weight is
+// bf16(fp32(scale) * q + fp32(bias)): scale * q is exact in fp32 (8-bit scale significand times
+// q < 256), so the fma rounds once, like the separate multiply and add.
+template <int QB>
+struct DqIn {
+  uint32_t words[DBK * QB / 32];
+  uint32_t sw, bw;  // scale and bias pairs of the stage's two-group window
+};
+// TL: scale / bias pairs interleaved per row (s0 s1 b0 b1, the tiled layout); otherwise the
+// scale pairs of all rows then the bias pairs.
+template <int QB, bool TL>
+__device__ __forceinline__ void dequant_load(const uint8_t* wq, const uint8_t* sb, int bn, int r, DqIn<QB>& in) {
+  constexpr int QROW = DBK * QB / 8;  // packed bytes per row per stage
+#pragma unroll
+  for (int c = 0; c < QROW / 16; ++c) {
+    const uint4 v = *reinterpret_cast<const uint4*>(wq + r * QROW + 16 * c);
+    in.words[4 * c] = v.x; in.words[4 * c + 1] = v.y; in.words[4 * c + 2] = v.z; in.words[4 * c + 3] = v.w;
+  }
+  if (TL) {
+    const uint2 p = *reinterpret_cast<const uint2*>(sb + 8 * r);
+    in.sw = p.x;
+    in.bw = p.y;
+  } else {
+    in.sw = *reinterpret_cast<const uint32_t*>(sb + 4 * r);
+    in.bw = *reinterpret_cast<const uint32_t*>(sb + 4 * bn + 4 * r);
+  }
+}
+// Half a 16-byte chunk of the dequantized row (h = 2c + half: k = 8c + 4 half .. +3); the caller
+// spreads the eight pieces between MFMAs. `out` collects the chunk; piece 2c+1 stores it.
+template <int QB>
+__device__ __forceinline__ void dequant_piece(const DqIn<QB>& in, int h, float sc, float bi, uint32_t (&out)[2],
+                                              int r, uint8_t* wd) {
+  const int c = h >> 1, hf = h & 1;
+  float v[4];
+  if (QB == 4) {
+    // nibbles 4hf .. 4hf+3 of word c: even ones in the low nibbles of bytes 2hf, 2hf+1
+    const uint32_t lo = in.words[c] & 0x0F0F0F0Fu, hi = (in.words[c] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      v[2 * j] = fmaf(sc, (float)((lo >> (8 * (2 * hf + j))) & 255u), bi);
+      v[2 * j + 1] = fmaf(sc, (float)((hi >> (8 * (2 * hf + j))) & 255u), bi);
+    }
+  } else {
+    const uint32_t w = in.words[2 * c + hf];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = fmaf(sc, (float)((w >> (8 * j)) & 255u), bi);
+  }
+  const uint32_t p0 = pack2(v[0], v[1]), p1 = pack2(v[2], v[3]);
+  if (hf == 0) {
+    out[0] = p0;
+    out[1] = p1;
+  } else {
+    *reinterpret_cast<uint4*>(wd + r * DROW + ((c ^ dswz(r)) << 4)) = make_uint4(out[0], out[1], p0, p1);
+  }
+}
+template <int QB>
+__device__ __forceinline__ void dequant_store(const DqIn<QB>& in, int r, int half, uint8_t* wd) {
+  const float sc = half ? hi_f(in.sw) : lo_f(in.sw);
+  const float bi = half ? hi_f(in.bw) : lo_f(in.bw);
+  uint32_t out[2];
+#pragma unroll
+  for (int h = 0; h < 2 * DCPR; ++h) dequant_piece<QB>(in, h, sc, bi, out, r, wd);
+}
+
+// QB = 0: bf16 weights, DMA'd like the activations. QB = 4 / 8: affine quantized weights; each
+// stage DMAs the packed words and the scale / bias pairs of its 64-wide group, and the workgroup
+// dequantizes stage kt+1 into one of two bf16 tiles while the MFMAs consume stage kt. TL: the
+// weights are in the tiled layout (one contiguous block per 256-row tile and stage, see
+// kx_qweight_tile_affine), else in the reference layout (one 16- or 4-byte piece per row).
+template <int BM, int BN, int QB, bool TL, int GMODE, bool OUTF32>
 __global__ __launch_bounds__(256) void gemm_lds_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ W, int64_t ldw,
-    void* __restrict__ C, int64_t ldc, int M, int N, int K, Epilogue epi) {
-  constexpr int A_INST = BM / DRPI / 4, W_INST = BN / DRPI / 4;
+    QuantW qw, void* __restrict__ C, int64_t ldc, int M, int N, int K, Epilogue epi) {
+  constexpr int A_INST = BM / DRPI / 4;
+  constexpr int QROW = DBK * QB / 8;                                  // packed bytes per row
+  constexpr int WQ_INST = QB ? BN * QROW / 1024 / 4 : 0;              // packed words, per wave
+  constexpr int SB_INST = QB ? 2 * BN / 64 / 4 : 0;                   // scale and bias pairs
+  constexpr int W_INST = QB ? WQ_INST + SB_INST : BN / DRPI / 4;
   constexpr int PER = A_INST + W_INST;  // DMA instructions per wave per stage
-  constexpr int STAGE = (BM + BN) * DROW;
+  constexpr int W_BYTES = QB ? BN * QROW + BN * 8 : BN * DROW;
+  constexpr int STAGE = BM * DROW + W_BYTES;
+  constexpr int WD_OFF = DNS * STAGE;    // two dequantized bf16 weight tiles follow the ring
+  constexpr int RING = QB ? WD_OFF + 2 * BN * DROW : DNS * STAGE;
   constexpr int WT_M = BM / 2, WT_N = BN / 2;
   constexpr int MB = WT_M / 32, NB = WT_N / 32;
   constexpr int KS = DBK / 16;
   constexpr int DPS = (PER + KS - 1) / KS;  // DMA instructions per k16 step
   // At the wait in the last k16 step, stages kt+2 .. kt+NS-2 and the DMA of this iteration's
-  // earlier steps may stay in flight: stage kt+1 is then complete.
-  constexpr int WAITN = (DNS - 3) * PER + ((KS - 1) * DPS < PER ? (KS - 1) * DPS : PER);
+  // earlier steps may stay in flight: stage kt+1 is then complete. The quantized path dequantizes
+  // one stage ahead, so there stage kt+2 must be complete too.
+  constexpr int NBEFORE = (KS - 1) * DPS < PER ? (KS - 1) * DPS : PER;
+  constexpr int WAITN = (DNS - (QB ? 4 : 3)) * PER + NBEFORE;
   constexpr int PITCH = WT_N / 2 + 4;  // staged epilogue row, floats
   constexpr int EP_BYTES = 4 * WT_M * PITCH * 4;
-  constexpr int SMEM = DNS * STAGE > EP_BYTES ? DNS * STAGE : EP_BYTES;
-  static_assert(A_INST * DRPI * 4 == BM && W_INST * DRPI * 4 == BN && MB >= 1 && NB >= 2, "tile");
+  constexpr int SMEM = RING > EP_BYTES ? RING : EP_BYTES;
+  static_assert(A_INST * DRPI * 4 == BM && MB >= 1 && NB >= 2, "tile");
+  static_assert(QB == 0 ? (BN / DRPI / 4) * DRPI * 4 == BN : (BN == 256 && WQ_INST >= 1), "weight tile");
   static_assert(MB + NB <= 15 && WAITN >= 0, "pipeline");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
 
@@ -443,23 +524,74 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
     const int r = (wave * A_INST + i) * DRPI + r_in;
     vo[i] = (uint32_t)(((int64_t)(min(m0 + r, M - 1) - m0) * lda + (slot ^ dswz(r)) * 8) * 2);
   }
-#pragma unroll
-  for (int i = 0; i < W_INST; ++i) {
-    const int r = (wave * W_INST + i) * DRPI + r_in;
-    vo[A_INST + i] = (uint32_t)(((int64_t)(min(n0 + r, N - 1) - n0) * ldw + (slot ^ dswz(r)) * 8) * 2);
-  }
   const char* a_base = reinterpret_cast<const char*>(A + (int64_t)m0 * lda);
-  const char* w_base = reinterpret_cast<const char*>(W + (int64_t)n0 * ldw);
+  const char* w_base;   // bf16 weights, or the packed words
+  const char* s_base = nullptr;  // scale pairs (bias pairs follow at b_base)
+  const char* b_base = nullptr;
+  const int64_t qrow_bytes = (int64_t)K * QB / 8, groups = K / 64;
+  if constexpr (QB == 0) {
+#pragma unroll
+    for (int i = 0; i < W_INST; ++i) {
+      const int r = (wave * W_INST + i) * DRPI + r_in;
+      vo[A_INST + i] = (uint32_t)(((int64_t)(min(n0 + r, N - 1) - n0) * ldw + (slot ^ dswz(r)) * 8) * 2);
+    }
+    w_base = reinterpret_cast<const char*>(W + (int64_t)n0 * ldw);
+  } else if constexpr (TL) {
+    // tiled: the stage's packed words (BN * QROW bytes) and scale / bias pairs (BN * 8 bytes of
+    // its 128-wide window) are contiguous blocks
+#pragma unroll
+    for (int i = 0; i < WQ_INST; ++i) vo[A_INST + i] = (uint32_t)((wave * WQ_INST + i) * 1024 + lane * 16);
+#pragma unroll
+    for (int i = 0; i < SB_INST; ++i) vo[A_INST + WQ_INST + i] = (uint32_t)((wave * SB_INST + i) * 256 + lane * 4);
+    const int64_t nb = n0 / BN;
+    w_base = reinterpret_cast<const char*>(qw.words) + nb * (K / DBK) * (int64_t)(BN * QROW);
+    s_base = reinterpret_cast<const char*>(qw.scales) + nb * (K / 128) * (int64_t)(BN * 8);
+  } else {
+    // packed words: RPW rows per instruction, QROW / 16 chunks per row
+    constexpr int RPW = 1024 / QROW;
+#pragma unroll
+    for (int i = 0; i < WQ_INST; ++i) {
+      const int r = (wave * WQ_INST + i) * RPW + lane / (QROW / 16);
+      vo[A_INST + i] = (uint32_t)((int64_t)(min(n0 + r, N - 1) - n0) * qrow_bytes + (lane % (QROW / 16)) * 16);
+    }
+    // scale / bias pairs: 64 rows x 4 bytes per instruction
+#pragma unroll
+    for (int i = 0; i < SB_INST; ++i) {
+      const int g = wave * SB_INST + i;
+      const int r = (g % (BN / 64)) * 64 + lane;
+      vo[A_INST + WQ_INST + i] = (uint32_t)((int64_t)(min(n0 + r, N - 1) - n0) * groups * 2);
+    }
+    w_base = reinterpret_cast<const char*>(qw.words) + (int64_t)n0 * qrow_bytes;
+    s_base = reinterpret_cast<const char*>(qw.scales) + (int64_t)n0 * groups * 2;
+    b_base = reinterpret_cast<const char*>(qw.biases) + (int64_t)n0 * groups * 2;
+  }
   auto dma = [&](int i, uint8_t* buf, int k0) {
-    if (i < A_INST)
+    if (i < A_INST) {
       __builtin_amdgcn_global_load_lds((const void*)(a_base + (int64_t)k0 * 2 + vo[i]),
                                        KX_LDS(buf + (wave * A_INST + i) * DRPI * DROW), 16, 0, 0);
-    else
+    } else if constexpr (QB == 0) {
       __builtin_amdgcn_global_load_lds((const void*)(w_base + (int64_t)k0 * 2 + vo[i]),
                                        KX_LDS(buf + (BM + (wave * W_INST + i - A_INST) * DRPI) * DROW), 16, 0, 0);
+    } else if (TL && i < A_INST + WQ_INST) {
+      __builtin_amdgcn_global_load_lds((const void*)(w_base + (int64_t)(k0 / DBK) * (BN * QROW) + vo[i]),
+                                       KX_LDS(buf + BM * DROW + (wave * WQ_INST + i - A_INST) * 1024), 16, 0, 0);
+    } else if (TL) {
+      const int g = wave * SB_INST + (i - A_INST - WQ_INST);
+      __builtin_amdgcn_global_load_lds((const void*)(s_base + (int64_t)(k0 / 128) * (BN * 8) + vo[i]),
+                                       KX_LDS(buf + BM * DROW + BN * QROW + g * 256), 4, 0, 0);
+    } else if (i < A_INST + WQ_INST) {
+      __builtin_amdgcn_global_load_lds((const void*)(w_base + (int64_t)k0 * QB / 8 + vo[i]),
+                                       KX_LDS(buf + BM * DROW + (wave * WQ_INST + i - A_INST) * 1024), 16, 0, 0);
+    } else {
+      // the pair of groups holding group k0 / 64 (k0 / 64 rounded down to even)
+      const int g = wave * SB_INST + (i - A_INST - WQ_INST);
+      const char* src = (g < BN / 64 ? s_base : b_base) + (int64_t)((k0 >> 6) & ~1) * 2 + vo[i];
+      __builtin_amdgcn_global_load_lds((const void*)src, KX_LDS(buf + BM * DROW + BN * QROW + g * 256), 4, 0, 0);
+    }
   };
 
-  // fragment byte offsets within a stage, per k16 step (the MFMA A operand is the weight tile)
+  // fragment byte offsets, per k16 step (the MFMA A operand is the weight tile): activation rows
+  // within a stage; weight rows within the stage (bf16) or within a dequantized tile
   int a_off[KS][MB], w_off[KS][NB];
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
@@ -471,15 +603,28 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
     }
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
-      const int r = BM + wn * WT_N + i * 32 + lrow;
-      w_off[s][i] = r * DROW + ((c ^ dswz(r)) << 4);
+      const int r = wn * WT_N + i * 32 + lrow;
+      w_off[s][i] = (QB ? 0 : BM * DROW) + r * DROW + ((c ^ dswz(r)) << 4);
     }
   }
-  auto load_frags = [&](const uint8_t* buf, int s, bf16x8* af, bf16x8* wf) {
+  auto load_frags = [&](const uint8_t* abuf, const uint8_t* wbuf, int s, bf16x8* af, bf16x8* wf) {
 #pragma unroll
-    for (int j = 0; j < MB; ++j) af[j] = *reinterpret_cast<const bf16x8*>(buf + a_off[s][j]);
+    for (int j = 0; j < MB; ++j) af[j] = *reinterpret_cast<const bf16x8*>(abuf + a_off[s][j]);
 #pragma unroll
-    for (int i = 0; i < NB; ++i) wf[i] = *reinterpret_cast<const bf16x8*>(buf + w_off[s][i]);
+    for (int i = 0; i < NB; ++i) wf[i] = *reinterpret_cast<const bf16x8*>(wbuf + w_off[s][i]);
+  };
+  auto wtile = [&](const uint8_t* stage_buf, int kt) -> const uint8_t* {
+    return QB ? smem + WD_OFF + (kt & 1) * BN * DROW : stage_buf;
+  };
+  DqIn<QB ? QB : 4> dq;
+  auto dequant_in = [&](int stage_i) {  // packed inputs of a stage into registers
+    if constexpr (QB != 0) {
+      const uint8_t* buf = smem + stage_i * STAGE + BM * DROW;
+      dequant_load<QB, TL>(buf, buf + BN * QROW, BN, tid, dq);
+    }
+  };
+  auto dequant_out = [&](int kt) {  // stage kt's bf16 weights into its tile
+    if constexpr (QB != 0) dequant_store<QB>(dq, tid, (kt >> 1) & 1, smem + WD_OFF + (kt & 1) * BN * DROW);
   };
 
   f32x16 acc[NB][MB];
@@ -495,10 +640,21 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
   for (int p = 0; p < DNS - 1; ++p)
 #pragma unroll
     for (int i = 0; i < PER; ++i) dma(i, smem + p * STAGE, min(p, stages - 1) * DBK);
-  wait_vmcnt<(DNS - 2) * PER>();
-  KX_BARRIER();
+  if constexpr (QB == 0) {
+    wait_vmcnt<(DNS - 2) * PER>();
+    KX_BARRIER();
+  } else {
+    // stages 0 and 1 landed; stage 0 dequantized and visible
+    wait_vmcnt<(DNS - 3) * PER>();
+    KX_BARRIER();
+    dequant_in(0);
+    dequant_out(0);
+    dequant_in(1);
+    wait_lgkmcnt0();
+    KX_BARRIER();
+  }
   bf16x8 fa[2][MB], fw[2][NB];
-  load_frags(smem, 0, fa[0], fw[0]);
+  load_frags(smem, wtile(smem, 0), 0, fa[0], fw[0]);
   int cur_i = 0;
   for (int kt = 0; kt < stages; ++kt) {
     const uint8_t* cur = smem + cur_i * STAGE;
@@ -513,14 +669,48 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
       __builtin_amdgcn_sched_barrier(0);
       wait_lgkmcnt0();
       __builtin_amdgcn_sched_barrier(0);
+      if (QB != 0 && s == 0) {
+        // quantized first step, in a fixed order: the next step's fragment reads and this step's
+        // DMA, then the MFMAs with one piece of the next stage's dequantization after every
+        // other MFMA (the pieces' arithmetic runs while the MFMAs execute)
+        load_frags(cur, wtile(cur, kt), 1, fa[1], fw[1]);
+#pragma unroll
+        for (int d = 0; d < DPS; ++d)
+          if (d < PER) dma(d, iss, k_iss);
+        const int kq = kt + 1;
+        const float sc = ((kq >> 1) & 1) ? hi_f(dq.sw) : lo_f(dq.sw);
+        const float bi = ((kq >> 1) & 1) ? hi_f(dq.bw) : lo_f(dq.bw);
+        uint8_t* wd = smem + WD_OFF + (kq & 1) * BN * DROW;
+        uint32_t piece[2];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 0; q < NB * MB; ++q) {
+          const int i = q / MB, j = q % MB;
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fw[0][i], fa[0][j], acc[i][j], 0, 0, 0);
+          if constexpr (QB != 0) {
+            // pieces [q P / Q, (q + 1) P / Q): all P = 2 * DCPR pieces over the Q MFMAs
+            constexpr int P = 2 * DCPR, Q = NB * MB;
+#pragma unroll
+            for (int h = q * P / Q; h < (q + 1) * P / Q; ++h) dequant_piece<QB>(dq, h, sc, bi, piece, tid, wd);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        continue;
+      }
       if (s + 1 < KS) {
-        load_frags(cur, s + 1, fa[b ^ 1], fw[b ^ 1]);
+        load_frags(cur, wtile(cur, kt), s + 1, fa[b ^ 1], fw[b ^ 1]);
       } else {
-        // stage kt+1 has landed for this wave and its reads of cur are done; after the barrier
-        // it has landed for every wave, and nobody reads cur again before it is refilled
+        // stage kt+1 (kt+2 when quantized) has landed for this wave and its reads of cur are
+        // done; after the barrier this holds for every wave, and nobody reads cur again before
+        // it is refilled
         wait_vmcnt<WAITN>();
         KX_BARRIER();
-        load_frags(smem + nxt_i * STAGE, 0, fa[b ^ 1], fw[b ^ 1]);
+        load_frags(smem + nxt_i * STAGE, wtile(smem + nxt_i * STAGE, kt + 1), 0, fa[b ^ 1], fw[b ^ 1]);
+        // packed inputs of stage kt+2 (landed before this barrier; its buffer is refilled only
+        // after stage kt+2 has been dequantized)
+        int i2 = nxt_i + 1;
+        i2 = i2 == DNS ? 0 : i2;
+        dequant_in(i2);
       }
 #pragma unroll
       for (int d = 0; d < DPS; ++d)
@@ -670,27 +860,27 @@ int pick_cfg(int64_t m, int64_t n) {
   return T128x128;
 }
 
-template <int BM, int BN, int GMODE, bool OUTF32>
-int launch_lds_t(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, void* c, int64_t ldc,
-                 int m, int n, int k, const Epilogue& epi, hipStream_t s) {
+template <int BM, int BN, int QB, bool TL, int GMODE, bool OUTF32>
+int launch_lds_t(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, QuantW qw, void* c,
+                 int64_t ldc, int m, int n, int k, const Epilogue& epi, hipStream_t s) {
   const int tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
-  gemm_lds_kernel<BM, BN, GMODE, OUTF32><<<tiles, 256, 0, s>>>(a, lda, w, ldw, c, ldc, m, n, k, epi);
+  gemm_lds_kernel<BM, BN, QB, TL, GMODE, OUTF32><<<tiles, 256, 0, s>>>(a, lda, w, ldw, qw, c, ldc, m, n, k, epi);
   return KX_OK;
 }
 
 // Residual mode (none / bf16 / fp32) and output type select the epilogue specialisation.
-template <int BM, int BN>
-int launch_lds(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, void* c, int64_t ldc,
-               int m, int n, int k, const Epilogue& epi, hipStream_t s) {
+template <int BM, int BN, int QB, bool TL = false>
+int launch_lds(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, QuantW qw, void* c,
+               int64_t ldc, int m, int n, int k, const Epilogue& epi, hipStream_t s) {
   const int gmode = (epi.flags & KX_EPI_GATED_RESIDUAL) ? ((epi.flags & KX_EPI_RESID_F32) ? 2 : 1) : 0;
   const bool out32 = epi.flags & KX_EPI_OUT_F32;
   switch (gmode * 2 + (out32 ? 1 : 0)) {
-    case 0: return launch_lds_t<BM, BN, 0, false>(a, lda, w, ldw, c, ldc, m, n, k, epi, s);
-    case 1: return launch_lds_t<BM, BN, 0, true>(a, lda, w, ldw, c, ldc, m, n, k, epi, s);
-    case 2: return launch_lds_t<BM, BN, 1, false>(a, lda, w, ldw, c, ldc, m, n, k, epi, s);
-    case 3: return launch_lds_t<BM, BN, 1, true>(a, lda, w, ldw, c, ldc, m, n, k, epi, s);
-    case 4: return launch_lds_t<BM, BN, 2, false>(a, lda, w, ldw, c, ldc, m, n, k, epi, s);
-    default: return launch_lds_t<BM, BN, 2, true>(a, lda, w, ldw, c, ldc, m, n, k, epi, s);
+    case 0: return launch_lds_t<BM, BN, QB, TL, 0, false>(a, lda, w, ldw, qw, c, ldc, m, n, k, epi, s);
+    case 1: return launch_lds_t<BM, BN, QB, TL, 0, true>(a, lda, w, ldw, qw, c, ldc, m, n, k, epi, s);
+    case 2: return launch_lds_t<BM, BN, QB, TL, 1, false>(a, lda, w, ldw, qw, c, ldc, m, n, k, epi, s);
+    case 3: return launch_lds_t<BM, BN, QB, TL, 1, true>(a, lda, w, ldw, qw, c, ldc, m, n, k, epi, s);
+    case 4: return launch_lds_t<BM, BN, QB, TL, 2, false>(a, lda, w, ldw, qw, c, ldc, m, n, k, epi, s);
+    default: return launch_lds_t<BM, BN, QB, TL, 2, true>(a, lda, w, ldw, qw, c, ldc, m, n, k, epi, s);
   }
 }
 
@@ -723,12 +913,27 @@ int dispatch(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, Qua
              void* c, int64_t ldc, int64_t m, int64_t n, int64_t k, const Epilogue& epi,
              hipStream_t s) {
   const char* legacy = getenv("KX355_GEMM_TILE");
+  const bool use_legacy = legacy && *legacy;
   // the direct-to-LDS kernel keeps per-lane 32-bit byte offsets within a 256-row tile
-  if (QB == 0 && k % DBK == 0 && lda <= (1 << 22) && ldw <= (1 << 22) && !(legacy && *legacy)) {
+  if (QB == 0 && k % DBK == 0 && lda <= (1 << 22) && ldw <= (1 << 22) && !use_legacy) {
     switch (pick_lds_cfg(m, n)) {
-      case 0: return launch_lds<256, 256>(a, lda, w, ldw, c, ldc, (int)m, (int)n, (int)k, epi, s);
-      case 1: return launch_lds<192, 256>(a, lda, w, ldw, c, ldc, (int)m, (int)n, (int)k, epi, s);
-      default: return launch_lds<128, 128>(a, lda, w, ldw, c, ldc, (int)m, (int)n, (int)k, epi, s);
+      case 0: return launch_lds<256, 256, 0>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi, s);
+      case 1: return launch_lds<192, 256, 0>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi, s);
+      default: return launch_lds<128, 128, 0>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi, s);
+    }
+  }
+  // quantized weights: the direct-to-LDS kernel with in-LDS dequantization needs whole 128-wide
+  // K blocks (scale / bias pairs of two groups), 16-byte aligned packed rows and 4-byte aligned
+  // scale / bias rows; tile 2 (or a narrow N) selects the register-staged kernel
+  if (QB != 0 && k % 128 == 0 && lda <= (1 << 22) && n >= 128 && !use_legacy &&
+      aligned16(qw.words) && (reinterpret_cast<uintptr_t>(qw.scales) & 3) == 0 &&
+      (reinterpret_cast<uintptr_t>(qw.biases) & 3) == 0) {
+    const int cfg = pick_lds_cfg(m, n);
+    const int64_t t256 = ((m + 255) / 256) * ((n + 255) / 256), t192 = ((m + 191) / 192) * ((n + 255) / 256);
+    const bool tall = cfg == 0 || (cfg != 1 && (t256 + 255) / 256 * 256 <= (t192 + 255) / 256 * 192);
+    if (cfg != 2 || !getenv("KX355_GEMM_LDS_TILE")) {
+      if (tall) return launch_lds<256, 256, QB>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi, s);
+      return launch_lds<192, 256, QB>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi, s);
     }
   }
   switch (pick_cfg(m, n)) {
@@ -747,6 +952,41 @@ int dispatch(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, Qua
     default:
       return launch_cfg<64, 64, 2, 2, QB>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi,
                                           s);
+  }
+}
+
+// Tiled affine weights: for 256-row tile nb and 32-wide K stage kb, the rows' packed bytes of the
+// stage are one block of 256 * (32 * bits / 8) bytes; for the 128-wide window p, the rows'
+// (scale 2p, scale 2p+1, bias 2p, bias 2p+1) are one block of 256 * 8 bytes. Rows past n repeat
+// row n - 1 (their products are never stored).
+template <int BITS>
+__global__ __launch_bounds__(256) void tile_weights_kernel(const uint32_t* __restrict__ words,
+                                                           const uint16_t* __restrict__ scales,
+                                                           const uint16_t* __restrict__ biases,
+                                                           uint8_t* __restrict__ wt, uint8_t* __restrict__ sbt,
+                                                           int64_t n, int64_t k) {
+  constexpr int QROW = 32 * BITS / 8;
+  const int64_t npad = (n + 255) / 256 * 256;
+  const int64_t kb_count = k / 32, p_count = k / 128;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t rows_x_kb = npad * kb_count;
+  if (idx < rows_x_kb) {
+    const int64_t r = idx % npad, kb = idx / npad;  // consecutive threads: consecutive rows
+    const int64_t src_row = r < n ? r : n - 1;
+    const uint32_t* src = words + src_row * (k * BITS / 32) + kb * (QROW / 4);
+    uint32_t* dst = reinterpret_cast<uint32_t*>(wt + (((r / 256) * kb_count + kb) * 256 + (r % 256)) * QROW);
+#pragma unroll
+    for (int j = 0; j < QROW / 4; ++j) dst[j] = src[j];
+  }
+  if (idx < npad * p_count) {
+    const int64_t r = idx % npad, p = idx / npad;
+    const int64_t src_row = r < n ? r : n - 1;
+    const int64_t g = src_row * (k / 64) + 2 * p;
+    uint16_t* dst = reinterpret_cast<uint16_t*>(sbt + (((r / 256) * p_count + p) * 256 + (r % 256)) * 8);
+    dst[0] = scales[g];
+    dst[1] = scales[g + 1];
+    dst[2] = biases[g];
+    dst[3] = biases[g + 1];
   }
 }
 
@@ -850,4 +1090,58 @@ extern "C" int kx_dequant_affine_bf16(const uint32_t* wq, const void* scales, co
     dequant_kernel<8><<<blocks, 256, 0, (hipStream_t)stream>>>(
         wq, (const uint16_t*)scales, (const uint16_t*)biases, (uint16_t*)out, n, k, group_size);
   return check_launch("kx_dequant_affine_bf16");
+}
+
+extern "C" int kx_qweight_tile_affine(const uint32_t* wq, const void* scales, const void* biases,
+                                      void* wt, void* sbt, int64_t n, int64_t k, int group_size,
+                                      int bits, kx_stream_t stream) {
+  KX_REQUIRE(wq && scales && biases && wt && sbt, "kx_qweight_tile_affine: null tensor");
+  KX_REQUIRE(bits == 4 || bits == 8, "kx_qweight_tile_affine: bits must be 4 or 8, got %d", bits);
+  KX_REQUIRE(group_size == 64, "kx_qweight_tile_affine: group_size must be 64, got %d", group_size);
+  KX_REQUIRE(n > 0 && k > 0 && k % 128 == 0 && n < (1ll << 31) && k < (1ll << 30),
+             "kx_qweight_tile_affine: k must be a positive multiple of 128");
+  KX_REQUIRE(aligned16(wt) && aligned8(sbt), "kx_qweight_tile_affine: wt must be 16-byte and sbt 8-byte aligned");
+  const int64_t npad = (n + 255) / 256 * 256;
+  const int64_t work = npad * (k / 32);
+  const unsigned blocks = (unsigned)((work + 255) / 256);
+  if (bits == 4)
+    tile_weights_kernel<4><<<blocks, 256, 0, (hipStream_t)stream>>>(
+        wq, (const uint16_t*)scales, (const uint16_t*)biases, (uint8_t*)wt, (uint8_t*)sbt, n, k);
+  else
+    tile_weights_kernel<8><<<blocks, 256, 0, (hipStream_t)stream>>>(
+        wq, (const uint16_t*)scales, (const uint16_t*)biases, (uint8_t*)wt, (uint8_t*)sbt, n, k);
+  return check_launch("kx_qweight_tile_affine");
+}
+
+extern "C" int kx_qgemm_affine_tiled_bf16(const void* a, int64_t lda, const void* wt, const void* sbt,
+                                          const void* bias, void* c, int64_t ldc, int64_t m, int64_t n,
+                                          int64_t k, int bits, int epilogue, const void* resid,
+                                          int64_t ldr, const float* gate, int64_t gate_div,
+                                          int64_t gate_stride, kx_stream_t stream) {
+  KX_REQUIRE(a && wt && sbt && c, "kx_qgemm_affine_tiled_bf16: null tensor");
+  KX_REQUIRE(bits == 4 || bits == 8, "kx_qgemm_affine_tiled_bf16: bits must be 4 or 8, got %d", bits);
+  KX_REQUIRE(m >= 0 && n > 0 && k > 0 && k % 128 == 0 && m < (1ll << 31) && n < (1ll << 31) &&
+                 k < (1ll << 30),
+             "kx_qgemm_affine_tiled_bf16: bad shape (k must be a multiple of 128)");
+  KX_REQUIRE(lda % 8 == 0 && lda >= k && lda <= (1 << 22) && ldc >= n && aligned16(a) && aligned8(c) &&
+                 aligned16(wt) && aligned8(sbt),
+             "kx_qgemm_affine_tiled_bf16: bad stride or alignment");
+  const int rc = check_epilogue("kx_qgemm_affine_tiled_bf16", epilogue, bias, c, ldc, resid, ldr, n,
+                                gate, gate_div, gate_stride);
+  if (rc) return rc;
+  if (m == 0) return KX_OK;
+  const Epilogue epi{(const uint16_t*)bias, resid, ldr, gate, gate_div, gate_stride, epilogue};
+  const QuantW qw{(const uint32_t*)wt, (const uint16_t*)sbt, nullptr};
+  const int64_t t256 = ((m + 255) / 256) * ((n + 255) / 256), t192 = ((m + 191) / 192) * ((n + 255) / 256);
+  const char* env = getenv("KX355_GEMM_LDS_TILE");
+  const bool tall = (env && *env) ? atoi(env) == 0 : (t256 + 255) / 256 * 256 <= (t192 + 255) / 256 * 192;
+  hipStream_t s = (hipStream_t)stream;
+  if (bits == 4) {
+    if (tall) launch_lds<256, 256, 4, true>((const uint16_t*)a, lda, nullptr, 0, qw, c, ldc, (int)m, (int)n, (int)k, epi, s);
+    else launch_lds<192, 256, 4, true>((const uint16_t*)a, lda, nullptr, 0, qw, c, ldc, (int)m, (int)n, (int)k, epi, s);
+  } else {
+    if (tall) launch_lds<256, 256, 8, true>((const uint16_t*)a, lda, nullptr, 0, qw, c, ldc, (int)m, (int)n, (int)k, epi, s);
+    else launch_lds<192, 256, 8, true>((const uint16_t*)a, lda, nullptr, 0, qw, c, ldc, (int)m, (int)n, (int)k, epi, s);
+  }
+  return check_launch("kx_qgemm_affine_tiled_bf16");
 }

@@ -10,6 +10,10 @@ Format: ``weight`` uint32 words ``(out, in * bits / 32)`` (stored in an int32 te
 group_size)``; ``w = scale * q + bias``. The kernel dequantizes inside its MFMA mainloop with
 ``bf16(fp32(scale) * q + fp32(bias))`` — exact product, one FP32 add, one round-to-nearest-even.
 
+``QuantizedLinear`` also keeps a copy of its weights in the kernel's tiled layout
+(``kx_qweight_tile_affine``: each 256-row tile's packed words and scale / bias pairs of one K
+stage in one contiguous block), prepared once on construction and used by every call.
+
 ``quantize`` is this build's deterministic quantizer (MLX's own scale/bias selection is not
 reproduced): per group ``scale = bf16((max - min) / (2^bits - 1))``, ``bias = bf16(min)``,
 ``q = clip(round((w - bias) / scale), 0, 2^bits - 1)``.
@@ -99,6 +103,46 @@ def dequantize(words: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, 
     return out
 
 
+def tile_weights(words: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, *,
+                 bits: int = DEFAULT_BITS, group_size: int = DEFAULT_GROUP_SIZE) -> tuple[torch.Tensor, torch.Tensor]:
+    """Packed affine weights -> the kernel's tiled layout ``(wt, sbt)`` (uint8 tensors)."""
+    _check_format(group_size, bits)
+    n = int(words.shape[0])
+    k = int(words.shape[1]) * 32 // bits
+    if k % 128:
+        raise ValueError("the tiled quantized layout needs an input width that is a multiple of 128")
+    npad = (n + 255) // 256 * 256
+    wt = torch.empty(npad * k * bits // 8, dtype=torch.uint8, device=words.device)
+    sbt = torch.empty(npad * (k // 128) * 8, dtype=torch.uint8, device=words.device)
+    _lib.launch_tile_weights(words.contiguous(), scales.contiguous(), biases.contiguous(), wt, sbt, n=n, k=k,
+                             group_size=group_size, bits=bits)
+    return wt, sbt
+
+
+def _prepare_call(value, n, k, bias, activation, residual, gate, out_dtype):
+    """Shared argument handling of the reference-layout and tiled-layout products."""
+    if value.dtype != torch.bfloat16:
+        raise ValueError(f"quantized_matmul takes bfloat16 activations on MI355X, got {value.dtype}")
+    if int(value.shape[-1]) != k:
+        raise ValueError(f"input width {value.shape[-1]} does not match the packed width {k}")
+    a = value.reshape(-1, k)
+    if a.stride(-1) != 1 or a.data_ptr() % 16 or a.stride(0) % 8:
+        a = a.contiguous()
+    out = torch.empty((*value.shape[:-1], n), dtype=out_dtype or value.dtype, device=value.device)
+    flags = ACTIVATIONS[activation]
+    if bias is not None:
+        flags |= _lib.EPI_BIAS
+        bias = bias.to(torch.bfloat16).contiguous()
+    resid2 = gate32 = None
+    if residual is not None:
+        flags |= _lib.EPI_GATED_RESIDUAL
+        resid2 = residual.reshape(-1, n)
+        gate32 = gate.float()
+        if gate32.stride(-1) != 1 or gate32.data_ptr() % 16:
+            gate32 = gate32.contiguous()
+    return a, out, flags, bias, resid2, gate32
+
+
 def quantized_matmul(
     value: torch.Tensor,
     weight: torch.Tensor,
@@ -121,31 +165,13 @@ def quantized_matmul(
         raise ValueError("the MI355X quantized linear takes the (out, in) packing (transpose=True)")
     quant_defaults(mode, group_size, bits)
     _check_format(group_size, bits)
-    if value.dtype != torch.bfloat16:
-        raise ValueError(f"quantized_matmul takes bfloat16 activations on MI355X, got {value.dtype}")
     n = int(weight.shape[0])
     k = int(weight.shape[1]) * 32 // bits
-    if int(value.shape[-1]) != k:
-        raise ValueError(f"input width {value.shape[-1]} does not match the packed width {k}")
     if scales.shape != (n, k // group_size) or biases.shape != scales.shape:
         raise ValueError("scales and biases must be (out, in / group_size)")
-    a = value.reshape(-1, k)
-    if a.stride(-1) != 1 or a.data_ptr() % 16 or a.stride(0) % 8:
-        a = a.contiguous()
-    out = torch.empty((*value.shape[:-1], n), dtype=out_dtype or value.dtype, device=value.device)
+    a, out, flags, bias, resid2, gate32 = _prepare_call(value, n, k, bias, activation, residual, gate, out_dtype)
     if a.shape[0] == 0:
         return out
-    flags = ACTIVATIONS[activation]
-    if bias is not None:
-        flags |= _lib.EPI_BIAS
-        bias = bias.to(torch.bfloat16).contiguous()
-    resid2 = gate32 = None
-    if residual is not None:
-        flags |= _lib.EPI_GATED_RESIDUAL
-        resid2 = residual.reshape(-1, n)
-        gate32 = gate.float()
-        if gate32.stride(-1) != 1 or gate32.data_ptr() % 16:
-            gate32 = gate32.contiguous()
     _lib.launch_qgemm(
         a, weight, scales, biases, out.reshape(-1, n), n=n, k=k, group_size=group_size, bits=bits,
         bias=bias, flags=flags, resid=resid2, gate=gate32,
@@ -169,6 +195,11 @@ class QuantizedLinear:
         self.group_size = group_size
         self.bits = bits
         self.mode = mode
+        # the tiled copy the kernel reads (an input width that is a multiple of 128 on the GPU)
+        self._tiled = None
+        k = int(weight.shape[1]) * 32 // bits
+        if weight.is_cuda and k % 128 == 0 and int(weight.shape[0]) >= 128:
+            self._tiled = tile_weights(weight, scales, biases, bits=bits, group_size=group_size)
 
     @classmethod
     def from_linear(cls, weight: torch.Tensor, bias: torch.Tensor | None = None, *,
@@ -187,6 +218,14 @@ class QuantizedLinear:
     def __call__(self, value: torch.Tensor, *, activation: str | None = None,
                  residual: torch.Tensor | None = None, gate: torch.Tensor | None = None,
                  out_dtype: torch.dtype | None = None) -> torch.Tensor:
+        if self._tiled is not None:
+            n, k = self.out_features, self.in_features
+            a, out, flags, bias, resid2, gate32 = _prepare_call(value, n, k, self.bias, activation, residual,
+                                                                gate, out_dtype)
+            if a.shape[0]:
+                _lib.launch_qgemm_tiled(a, self._tiled[0], self._tiled[1], out.reshape(-1, n), n=n, k=k,
+                                        bits=self.bits, bias=bias, flags=flags, resid=resid2, gate=gate32)
+            return out
         return quantized_matmul(
             value, self.weight, self.scales, self.biases, group_size=self.group_size,
             bits=self.bits, mode=self.mode, bias=self.bias, activation=activation,
@@ -201,5 +240,6 @@ __all__ = [
     "quant_defaults",
     "quantize",
     "quantized_matmul",
+    "tile_weights",
     "unpack",
 ]

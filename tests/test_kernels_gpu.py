@@ -508,6 +508,39 @@ def test_quantized_linear_matches_oracle(device, monkeypatch, tile, bits, m, n, 
     assert max_abs(got, dense) <= 2.0**-7 * np.abs(dense).max()
 
 
+@pytest.mark.parametrize("tile", ["0", "1"])
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize(("m", "n", "k"), [(512, 512, 512), (300, 520, 1024), (200, 256, 128), (1000, 132, 384)])
+@pytest.mark.parametrize("epilogue", ["bias", "gated_f32"])
+@pytest.mark.parametrize("layout", ["tiled", "reference"])
+def test_quantized_linear_dequantizes_in_lds(device, monkeypatch, tile, bits, m, n, k, epilogue, layout):
+    """The direct-to-LDS quantized kernel (packed words and scale / bias pairs DMA'd per stage,
+    dequantized once per stage into a bf16 tile) at both of its tiles (256x256, 192x256), on full
+    and ragged tiles: equal to the dense kernel on the exactly dequantized weight (the dequant is
+    bit-exact, so the two differ only in fp32 summation order)."""
+    monkeypatch.setenv("KX355_GEMM_LDS_TILE", tile)
+    r = _rng(m + n + k + bits)
+    x = oracle.to_bf16((r.standard_normal((m, k)) * 0.5).astype(F32))
+    w = oracle.to_bf16((r.standard_normal((n, k)) * 0.02).astype(F32))
+    b = oracle.to_bf16((r.standard_normal(n) * 0.02).astype(F32))
+    words, scales, biases = oracle.quantize_affine(w, 64, bits)
+    layer = quantized.QuantizedLinear(torch.from_numpy(words.view(np.int32)).to(device), _bf(scales, device),
+                                      _bf(biases, device), _bf(b, device), group_size=64, bits=bits)
+    assert layer._tiled is not None
+    if layout == "reference":  # the C ABI on the reference layout (packed rows read in place)
+        layer._tiled = None
+    ref = oracle.quantized_linear(x, words, scales, biases, b, group_size=64, bits=bits)
+    if epilogue == "bias":
+        got = _np(layer(_bf(x, device)))
+        assert _gemm_close(got, ref)
+    else:
+        resid = r.standard_normal((m, n)).astype(F32)
+        gate = r.standard_normal(n).astype(F32)
+        got = _np(layer(_bf(x, device), residual=_f32(resid, device), gate=_f32(gate, device), out_dtype=torch.float32))
+        full = resid + gate * ref
+        assert np.all(np.abs(got - full) <= 1e-5 * np.abs(full) + 2e-5 * np.abs(full).max())
+
+
 def test_env_tile_override_is_restored():
     assert os.environ.get("KX355_GEMM_TILE") in (None, "")
     assert os.environ.get("KX355_GEMM_LDS_TILE") in (None, "")
