@@ -175,6 +175,16 @@ def main() -> int:
     dom_avg_ms = statistics.mean(per_kernel[dominant])
     dom_tflops = flops_of[dominant] / (dom_avg_ms * 1e-3) / 1e12
 
+    # HBM bytes per launch of the dominant kernel, from the committed rocprofv3 FETCH_SIZE /
+    # WRITE_SIZE summary of the same workload (None when no summary covers the kernel)
+    traffic = None
+    traffic_file = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "roofline_traffic.json")
+    if os.path.exists(traffic_file):
+        with open(traffic_file) as fh:
+            entry = json.load(fh).get(dominant)
+        if entry:
+            traffic = entry["fetch_bytes"] + entry["write_bytes"]
+
     flops = workloads.flop_count(spec)
     attn_ms = sum(v for k, v in kernel_ms_per_step.items() if name_of[k] == "kx_attention_fwd_bf16")
     gemm_ms = sum(v for k, v in kernel_ms_per_step.items() if name_of[k] in ("kx_gemm_bf16", "kx_qgemm_affine_bf16", "kx_qgemm_affine_tiled_bf16"))
@@ -228,7 +238,7 @@ def main() -> int:
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(dom_tflops / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": traffic,
             "avg_launch_ms": round(dom_avg_ms, 4),
         },
     }
