@@ -238,6 +238,67 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_kernel(
   }
 }
 
+// Full-width weighted RMSNorm with split-half RoPE for 128-wide heads (the LTX q/k path): each
+// lane owns matching 8-value chunks of both halves of a head (dims d .. d+7 and d+64 .. d+71), so
+// the rotation needs no lane exchange and every cos / sin table value is read once. All loads
+// (row, both tables) are issued before the row reduction. Rounding as rmsnorm_rope_kernel: the
+// normalized value stays fp32, each RoPE product is rounded before the difference / sum.
+template <int VPL, bool BF16W>
+__global__ __launch_bounds__(256) void rmsnorm_rope_split128_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, uint16_t* __restrict__ y, int64_t ldy,
+    int64_t rows, const void* __restrict__ w, float eps, float weight_offset,
+    const float* __restrict__ cosp, const float* __restrict__ sinp, int64_t table_ld,
+    int64_t table_hs, int64_t tokens, int table_batched) {
+  constexpr int DIM = VPL * 512;
+  constexpr int NP = VPL / 2;  // head-half pairs of chunks per lane
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const uint16_t* xr = x + row * ldx;
+  const int64_t tok = table_batched ? row : (row % tokens);
+  float a[NP][8], b[NP][8], c[NP][8], sn[NP][8];
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const int p = i * 64 + lane, h = p >> 3, k = p & 7;
+    const int col = h * 128 + k * 8;
+    unpack8(*reinterpret_cast<const uint4*>(xr + col), a[i]);
+    unpack8(*reinterpret_cast<const uint4*>(xr + col + 64), b[i]);
+    const float* cr = cosp + tok * table_ld + h * table_hs + k * 8;
+    const float* sr = sinp + tok * table_ld + h * table_hs + k * 8;
+    const float4 c0 = *reinterpret_cast<const float4*>(cr), c1 = *reinterpret_cast<const float4*>(cr + 4);
+    const float4 s0 = *reinterpret_cast<const float4*>(sr), s1 = *reinterpret_cast<const float4*>(sr + 4);
+    c[i][0] = c0.x; c[i][1] = c0.y; c[i][2] = c0.z; c[i][3] = c0.w;
+    c[i][4] = c1.x; c[i][5] = c1.y; c[i][6] = c1.z; c[i][7] = c1.w;
+    sn[i][0] = s0.x; sn[i][1] = s0.y; sn[i][2] = s0.z; sn[i][3] = s0.w;
+    sn[i][4] = s1.x; sn[i][5] = s1.y; sn[i][6] = s1.z; sn[i][7] = s1.w;
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NP; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss = fmaf(b[i][j], b[i][j], fmaf(a[i][j], a[i][j], ss));
+  const float r = rsqrtf(wave_sum<64>(ss) * (1.0f / DIM) + eps);
+  uint16_t* yr = y + row * ldy;
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const int p = i * 64 + lane, h = p >> 3, k = p & 7;
+    const int col = h * 128 + k * 8;
+    float o0[8], o1[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+#pragma clang fp contract(off)
+      const float n0 = a[i][j] * r * (load_w<BF16W>(w, col + j) + weight_offset);
+      const float n1 = b[i][j] * r * (load_w<BF16W>(w, col + 64 + j) + weight_offset);
+      const float fc = n0 * c[i][j], ss2 = n1 * sn[i][j];  // first * c, second * s
+      const float fs = n0 * sn[i][j], sc = n1 * c[i][j];   // first * s, second * c
+      o0[j] = fc - ss2;
+      o1[j] = fs + sc;
+    }
+    *reinterpret_cast<uint4*>(yr + col) = pack8(o0);
+    *reinterpret_cast<uint4*>(yr + col + 64) = pack8(o1);
+  }
+}
+
 // One wave per norm group, any width; weighted RMSNorm only.
 template <bool BF16W>
 __global__ __launch_bounds__(256) void rmsnorm_generic(
@@ -445,6 +506,24 @@ extern "C" int kx_rmsnorm_rope_bf16(const void* x, int64_t ldx, void* y, int64_t
   else if (rope_kind == KX_ROPE_PAIR)
     rope_ok = 512 % head_dim == 0 && head_dim >= 8;
   const bool align_ok = ldx % 8 == 0 && ldy % 8 == 0 && aligned16(x) && aligned16(y);
+  if (shape_ok && align_ok && rope_kind == KX_ROPE_SPLIT && norm_width == dim && head_dim == 128 &&
+      vpl >= 2 && table_ld % 4 == 0 && table_hs % 4 == 0 && aligned16(cos) && aligned16(sin)) {
+    const dim3 grid((unsigned)((rows + kWaves - 1) / kWaves));
+#define KX_RS(V)                                                                                   \
+  if (w_dtype == KX_BF16)                                                                          \
+    rmsnorm_rope_split128_kernel<V, true><<<grid, 256, 0, s>>>((const uint16_t*)x, ldx, (uint16_t*)y, \
+        ldy, rows, w, eps, weight_offset, cos, sin, table_ld, table_hs, tokens, table_batched);     \
+  else                                                                                             \
+    rmsnorm_rope_split128_kernel<V, false><<<grid, 256, 0, s>>>((const uint16_t*)x, ldx, (uint16_t*)y, \
+        ldy, rows, w, eps, weight_offset, cos, sin, table_ld, table_hs, tokens, table_batched);     \
+  return check_launch("kx_rmsnorm_rope_bf16");
+    switch (vpl) {
+      case 2: KX_RS(2)
+      case 4: KX_RS(4)
+      default: KX_RS(8)
+    }
+#undef KX_RS
+  }
   if (shape_ok && rope_ok && align_ok) {
 #define KX_RR(V)                                                                               \
   return dispatch_group<V>(group_lanes, rope_kind, x, ldx, y, ldy, rows, norm_width, w, w_dtype, \

@@ -87,20 +87,25 @@ def test_weighted_rms_norm_matches_oracle(device, dim, wdtype, offset):
     assert _within_one_ulp(_np(got), oracle.rms_norm(x, w, 1e-6, weight_offset=offset))
 
 
-@pytest.mark.parametrize(("dim", "heads"), [(4096, 32), (1024, 16)])
-def test_fused_norm_and_split_rope_matches_oracle(device, dim, heads):
+@pytest.mark.parametrize(("dim", "heads"), [(4096, 32), (1024, 16), (2048, 16), (1024, 8)])
+@pytest.mark.parametrize("wdtype", ["bf16", "f32"])
+def test_fused_norm_and_split_rope_matches_oracle(device, dim, heads, wdtype):
+    """Full-width RMSNorm + split RoPE: 128-wide heads take the kernel whose lanes own both halves
+    of a head, 64-wide heads the lane-exchange kernel; bf16 and fp32 norm weights."""
     r = _rng(dim + heads)
     t = 41
     dh = dim // heads
     x = oracle.to_bf16((r.standard_normal((1, t, dim)) * 3).astype(F32))
-    w = oracle.to_bf16((r.standard_normal(dim) * 0.05 + 1).astype(F32))
+    w = (r.standard_normal(dim) * 0.05 + 1).astype(F32)
+    if wdtype == "bf16":
+        w = oracle.to_bf16(w)
     pos = np.zeros((1, 3, t, 2), F32)
     pos[0, 0, :, 0] = np.arange(t) // 7
     pos[0, 1, :, 0] = np.arange(t) % 7
     pos[0, 2, :, 0] = np.arange(t) % 5
     pos[..., 1] = pos[..., 0] + 1
     cos, sin = oracle.precompute_freqs_cis(pos, dim=dim, use_middle_indices_grid=True, num_attention_heads=heads)
-    norm = ltx_attention.RMSNorm(dim, weight=_bf(w, device))
+    norm = ltx_attention.RMSNorm(dim, weight=_bf(w, device) if wdtype == "bf16" else _f32(w, device))
     # token-major storage viewed head-major, as precompute_freqs_cis returns it
     cos_d = _f32(cos.transpose(0, 2, 1, 3), device).transpose(1, 2)
     sin_d = _f32(sin.transpose(0, 2, 1, 3), device).transpose(1, 2)
