@@ -827,6 +827,61 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
   }
 }
 
+// ---- skinny kernel (N <= 64: the gate-logit projections) ------------------------------------
+//
+// One workgroup per 32 rows x 32 columns; its 4 waves split K into quarters and read both MFMA
+// operands straight from global memory (the weight is a few hundred KB and stays in L2, each
+// activation row is read once), then add their partial tiles through LDS. Quantized weights are
+// dequantized in registers with the arithmetic of the other kernels.
+template <int QB>
+__global__ __launch_bounds__(256) void gemm_skinny_kernel(
+    const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ W, int64_t ldw,
+    QuantW qw, void* __restrict__ C, int64_t ldc, int M, int N, int K, Epilogue epi) {
+  __shared__ __attribute__((aligned(16))) float part[4][16][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  const int m0 = blockIdx.x * 32, n0 = blockIdx.y * 32;
+  const int m = min(m0 + lrow, M - 1), n = min(n0 + lrow, N - 1);
+  const int kq = K / 4, kbeg = wave * kq;
+  const uint16_t* arow = A + (int64_t)m * lda + 8 * lhalf;
+  f32x16 acc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+  auto wfrag = [&](int k) -> bf16x8 {  // k: this lane's 8 values start at k (k % 8 == 0)
+    if constexpr (QB == 0) {
+      return *reinterpret_cast<const bf16x8*>(W + (int64_t)n * ldw + k);
+    } else {
+      const int64_t g = (int64_t)n * (K / 64) + k / 64;
+      const float sc = bf2f(qw.scales[g]), bi = bf2f(qw.biases[g]);
+      const uint32_t* wd = qw.words + (int64_t)n * (K * QB / 32) + k * QB / 32;
+      uint32_t tmp[2] = {wd[0], QB == 8 ? wd[1] : 0u};
+      return __builtin_bit_cast(bf16x8, dequant8<QB>(tmp, sc, bi));
+    }
+  };
+#pragma unroll 8
+  for (int k = kbeg; k < kbeg + kq; k += 16) {
+    const bf16x8 wf = wfrag(k + 8 * lhalf);
+    const bf16x8 xf = *reinterpret_cast<const bf16x8*>(arow + k);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, xf, acc, 0, 0, 0);
+  }
+#pragma unroll
+  for (int e = 0; e < 16; ++e) part[wave][e][lane] = acc[e];
+  __syncthreads();
+  // wave w finishes accumulator elements 4w .. 4w+3 (4 consecutive columns of one row)
+  const int row = m0 + lrow;
+  const int col = n0 + 8 * wave + 4 * lhalf;
+  float v[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    v[e] = part[0][4 * wave + e][lane] + part[1][4 * wave + e][lane] + part[2][4 * wave + e][lane] +
+           part[3][4 * wave + e][lane];
+  if (row < M && col < N) {
+    const bool vec_ok = (ldc % 4 == 0) && (!(epi.flags & KX_EPI_GATED_RESIDUAL) || epi.ldr % 4 == 0);
+    epilogue_store4(v, row, col, N, epi, C, ldc, vec_ok);
+  }
+}
+
 // ---- dispatch ---------------------------------------------------------------------------------
 
 enum TileCfg { T256x256 = 0, T256x128 = 1, T128x128 = 2, T64x64 = 3, T128x64 = 4 };
@@ -914,6 +969,11 @@ int dispatch(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, Qua
              hipStream_t s) {
   const char* legacy = getenv("KX355_GEMM_TILE");
   const bool use_legacy = legacy && *legacy;
+  if (n <= 64 && k % 64 == 0 && !use_legacy) {
+    const dim3 grid((unsigned)((m + 31) / 32), (unsigned)((n + 31) / 32));
+    gemm_skinny_kernel<QB><<<grid, 256, 0, s>>>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi);
+    return KX_OK;
+  }
   // the direct-to-LDS kernel keeps per-lane 32-bit byte offsets within a 256-row tile
   if (QB == 0 && k % DBK == 0 && lda <= (1 << 22) && ldw <= (1 << 22) && !use_legacy) {
     switch (pick_lds_cfg(m, n)) {

@@ -546,6 +546,37 @@ def test_quantized_linear_dequantizes_in_lds(device, monkeypatch, tile, bits, m,
         assert np.all(np.abs(got - full) <= 1e-5 * np.abs(full) + 2e-5 * np.abs(full).max())
 
 
+@pytest.mark.parametrize(("m", "n", "k"), [(1000, 32, 1024), (37, 64, 256), (300, 40, 512)])
+@pytest.mark.parametrize("bits", [None, 4, 8])
+@pytest.mark.parametrize("epilogue", ["sigmoid2", "gated_f32"])
+def test_skinny_linear_matches_oracle(device, m, n, k, bits, epilogue):
+    """N <= 64 (the gate-logit projections) takes the split-K skinny kernel, dense and quantized."""
+    r = _rng(m + n + k)
+    x = oracle.to_bf16((r.standard_normal((m, k)) * 0.5).astype(F32))
+    w = oracle.to_bf16((r.standard_normal((n, k)) * k ** -0.5).astype(F32))
+    b = oracle.to_bf16((r.standard_normal(n) * 0.5).astype(F32))
+    if bits is None:
+        weight = w
+        call = lambda **kw: mpp_linear.fused_linear(_bf(x, device), _bf(w, device), _bf(b, device), **kw)  # noqa: E731
+    else:
+        words, scales, biases = oracle.quantize_affine(w, 64, bits)
+        weight = oracle.dequantize_affine(words, scales, biases, group_size=64, bits=bits)
+        layer = quantized.QuantizedLinear(torch.from_numpy(words.view(np.int32)).to(device), _bf(scales, device),
+                                          _bf(biases, device), _bf(b, device), group_size=64, bits=bits)
+        call = lambda **kw: layer(_bf(x, device), **kw)  # noqa: E731
+    lin = oracle.linear(x, weight, b)
+    if epilogue == "sigmoid2":
+        got = _np(call(activation="sigmoid2"))
+        ref = 2.0 / (1.0 + np.exp(-lin.astype(np.float64)))
+        assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0**-7 + 1e-5)
+    else:
+        resid = r.standard_normal((m, n)).astype(F32)
+        gate = r.standard_normal(n).astype(F32)
+        got = _np(call(residual=_f32(resid, device), gate=_f32(gate, device), out_dtype=torch.float32))
+        ref = resid + gate * lin
+        assert np.all(np.abs(got - ref) <= 1e-5 * np.abs(ref) + 2e-5 * np.abs(ref).max())
+
+
 def test_env_tile_override_is_restored():
     assert os.environ.get("KX355_GEMM_TILE") in (None, "")
     assert os.environ.get("KX355_GEMM_LDS_TILE") in (None, "")
