@@ -174,7 +174,7 @@ def fused_linear(
         gate32 = gate.float()
         if gate32.stride(-1) != 1 or gate32.data_ptr() % 16:
             gate32 = gate32.contiguous()
-    out2 = out.reshape(-1, n)
+    out2 = out.view(-1, n)  # a view: a strided `out` is written in place, never via a copy
     _lib.launch_gemm(a, w, out2, bias=bias, flags=flags, resid=resid2, gate=gate32)
     return out
 

@@ -119,7 +119,7 @@ def tile_weights(words: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor
     return wt, sbt
 
 
-def _prepare_call(value, n, k, bias, activation, residual, gate, out_dtype):
+def _prepare_call(value, n, k, bias, activation, residual, gate, out_dtype, out=None):
     """Shared argument handling of the reference-layout and tiled-layout products."""
     if value.dtype != torch.bfloat16:
         raise ValueError(f"quantized_matmul takes bfloat16 activations on MI355X, got {value.dtype}")
@@ -128,7 +128,10 @@ def _prepare_call(value, n, k, bias, activation, residual, gate, out_dtype):
     a = value.reshape(-1, k)
     if a.stride(-1) != 1 or a.data_ptr() % 16 or a.stride(0) % 8:
         a = a.contiguous()
-    out = torch.empty((*value.shape[:-1], n), dtype=out_dtype or value.dtype, device=value.device)
+    if out is None:
+        out = torch.empty((*value.shape[:-1], n), dtype=out_dtype or value.dtype, device=value.device)
+    elif out.shape[-1] != n or out.numel() != a.shape[0] * n:
+        raise ValueError(f"out must hold {a.shape[0]} rows of width {n}")
     flags = ACTIVATIONS[activation]
     if bias is not None:
         flags |= _lib.EPI_BIAS
@@ -157,10 +160,11 @@ def quantized_matmul(
     activation: str | None = None,
     residual: torch.Tensor | None = None,
     gate: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
     out_dtype: torch.dtype | None = None,
 ) -> torch.Tensor:
     """``value @ dequant(weight)^T (+ bias)`` with dequantization inside the MFMA mainloop;
-    ``activation``/``residual``/``gate``/``out_dtype`` as ``mpp_linear.fused_linear``."""
+    ``activation``/``residual``/``gate``/``out``/``out_dtype`` as ``mpp_linear.fused_linear``."""
     if not transpose:
         raise ValueError("the MI355X quantized linear takes the (out, in) packing (transpose=True)")
     quant_defaults(mode, group_size, bits)
@@ -169,11 +173,12 @@ def quantized_matmul(
     k = int(weight.shape[1]) * 32 // bits
     if scales.shape != (n, k // group_size) or biases.shape != scales.shape:
         raise ValueError("scales and biases must be (out, in / group_size)")
-    a, out, flags, bias, resid2, gate32 = _prepare_call(value, n, k, bias, activation, residual, gate, out_dtype)
+    a, out, flags, bias, resid2, gate32 = _prepare_call(value, n, k, bias, activation, residual, gate, out_dtype,
+                                                        out)
     if a.shape[0] == 0:
         return out
     _lib.launch_qgemm(
-        a, weight, scales, biases, out.reshape(-1, n), n=n, k=k, group_size=group_size, bits=bits,
+        a, weight, scales, biases, out.view(-1, n), n=n, k=k, group_size=group_size, bits=bits,
         bias=bias, flags=flags, resid=resid2, gate=gate32,
     )
     return out
@@ -217,19 +222,19 @@ class QuantizedLinear:
 
     def __call__(self, value: torch.Tensor, *, activation: str | None = None,
                  residual: torch.Tensor | None = None, gate: torch.Tensor | None = None,
-                 out_dtype: torch.dtype | None = None) -> torch.Tensor:
+                 out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None) -> torch.Tensor:
         if self._tiled is not None:
             n, k = self.out_features, self.in_features
             a, out, flags, bias, resid2, gate32 = _prepare_call(value, n, k, self.bias, activation, residual,
-                                                                gate, out_dtype)
+                                                                gate, out_dtype, out)
             if a.shape[0]:
-                _lib.launch_qgemm_tiled(a, self._tiled[0], self._tiled[1], out.reshape(-1, n), n=n, k=k,
+                _lib.launch_qgemm_tiled(a, self._tiled[0], self._tiled[1], out.view(-1, n), n=n, k=k,
                                         bits=self.bits, bias=bias, flags=flags, resid=resid2, gate=gate32)
             return out
         return quantized_matmul(
             value, self.weight, self.scales, self.biases, group_size=self.group_size,
             bits=self.bits, mode=self.mode, bias=self.bias, activation=activation,
-            residual=residual, gate=gate, out_dtype=out_dtype,
+            residual=residual, gate=gate, out=out, out_dtype=out_dtype,
         )
 
 

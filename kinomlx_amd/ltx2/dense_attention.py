@@ -41,8 +41,13 @@ def applies(query: torch.Tensor, key: torch.Tensor, *, heads: int) -> bool:
 
 
 def _attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, heads: int, batch: int,
-               tq: int, tk: int, dim: int, gate: torch.Tensor | None, scale: float | None) -> torch.Tensor:
-    out = torch.empty((batch, tq, heads * dim), dtype=q.dtype, device=q.device)
+               tq: int, tk: int, dim: int, gate: torch.Tensor | None, scale: float | None,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    if out is None:
+        out = torch.empty((batch, tq, heads * dim), dtype=q.dtype, device=q.device)
+    elif (out.dtype != q.dtype or tuple(out.shape) != (batch, tq, heads * dim) or out.stride(-1) != 1
+          or (batch > 1 and out.stride(0) != tq * out.stride(1))):
+        raise ValueError(f"attention out must be {q.dtype} ({batch}, {tq}, {heads * dim}) with contiguous rows")
     if gate is not None:
         if gate.dtype != torch.bfloat16 or tuple(gate.shape[-1:]) != (heads,):
             raise ValueError(f"attention gate must be bf16 (..., {heads})")
@@ -90,9 +95,11 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, heads:
 
 
 def batched_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, heads: int,
-                      gate: torch.Tensor | None = None, scale: float | None = None) -> torch.Tensor:
-    """``(batch, tokens, heads * dim)`` form of ``dense_attention``; q/k/v may be strided row
-    views (e.g. column slices of a fused QKV projection)."""
+                      gate: torch.Tensor | None = None, scale: float | None = None,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+    """``(batch, tokens, heads * dim)`` form of ``dense_attention``; q/k/v (and ``out``, when
+    given) may be strided row views, e.g. column slices of a fused QKV projection or of the
+    buffer the next projection reads."""
     if q.dim() != 3 or k.dim() != 3 or v.shape != k.shape or q.shape[0] != k.shape[0]:
         raise ValueError("batched attention needs (batch, tokens, heads * dim) q, k and v")
     width = q.shape[-1]
@@ -105,7 +112,7 @@ def batched_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, head
     for name, t in (("q", q), ("k", k), ("v", v)):
         if t.stride(-1) != 1 or (batch > 1 and t.stride(0) != t.shape[1] * t.stride(1)):
             raise ValueError(f"attention {name} must have contiguous rows, evenly strided over the batch")
-    return _attention(q, k, v, heads=heads, batch=batch, tq=tq, tk=tk, dim=dim, gate=gate, scale=scale)
+    return _attention(q, k, v, heads=heads, batch=batch, tq=tq, tk=tk, dim=dim, gate=gate, scale=scale, out=out)
 
 
 __all__ = ["HEAD_DIMS", "applies", "batched_attention", "dense_attention"]

@@ -65,10 +65,11 @@ def adaln(value: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor, eps: fl
 def layer_norm_modulate(value: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor,
                         eps: float = 1e-6) -> torch.Tensor:
     """``layer_norm(x) * (1 + scale) + shift`` in one FP32 pass (FLUX.2 ``normalized``,
-    ``kinomlx/models/flux2/transformer.py:56-57``)."""
-    if value.dtype != torch.bfloat16:
-        raise ValueError(f"layer_norm_modulate takes bfloat16 activations on MI355X, got {value.dtype}")
-    out = torch.empty(value.shape, dtype=value.dtype, device=value.device)
+    ``kinomlx/models/flux2/transformer.py:56-57``). ``value`` is bf16 or an FP32 residual
+    stream; the result is bf16."""
+    if value.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"layer_norm_modulate takes bfloat16 (or an fp32 residual stream) on MI355X, got {value.dtype}")
+    out = torch.empty(value.shape, dtype=torch.bfloat16, device=value.device)
     if value.numel():
         shift32, scale32 = _mod_pair(shift, scale)
         _lib.launch_adaln_norm(value, out, shift32, scale32, eps, _lib.KX_NORM_LAYER)

@@ -274,6 +274,52 @@ def flux_rope(spec: FluxSpec) -> tuple[torch.Tensor, torch.Tensor]:
     return cos[0], sin[0]
 
 
+def build_flux_double_block(spec: FluxSpec, p: dict[str, torch.Tensor], device, *, fuse: bool = True):
+    """The MI355X FLUX.2 ``DoubleBlock`` holding ``p``'s weights on ``device``. Config 1 (``ff ==
+    "gelu"``) takes LTX's GELU ``FeedForward`` (biased ``proj_in``/``proj_out``) per stream."""
+    from .flux2.transformer import DoubleBlock
+    from .ltx2.feed_forward import FeedForward as GeluFeedForward
+
+    block = DoubleBlock(heads=spec.heads, head_dim=spec.head_dim)
+    attn = block.attn
+    for n in ("to_q", "to_k", "to_v", "add_q_proj", "add_k_proj", "add_v_proj", "to_add_out"):
+        setattr(attn, n, _layer(p, f"attn.{n}", device))
+    attn.to_out = [_layer(p, "attn.to_out", device)]
+    for n in ("norm_q", "norm_k", "norm_added_q", "norm_added_k"):
+        getattr(attn, n).weight = p[f"attn.{n}.weight"].to(device)
+    for prefix in ("ff", "ff_context"):
+        if spec.ff == "swiglu":
+            ff = getattr(block, prefix)
+            ff.linear_in = _layer(p, f"{prefix}.linear_in", device)
+            ff.linear_out = _layer(p, f"{prefix}.linear_out", device)
+        else:
+            ff = GeluFeedForward(spec.dim, mult=spec.ff_hidden // spec.dim)
+            ff.project_in.proj = _layer(p, f"{prefix}.proj_in", device)
+            ff.project_out = _layer(p, f"{prefix}.proj_out", device)
+            setattr(block, prefix, ff)
+    if fuse:
+        block.fuse_projections()
+    return block
+
+
+def build_flux_single_block(spec: FluxSpec, p: dict[str, torch.Tensor], device):
+    """The MI355X FLUX.2 ``SingleBlock`` holding ``p``'s ``single.*`` weights on ``device``."""
+    from .flux2.transformer import SingleBlock
+
+    block = SingleBlock(heads=spec.heads, head_dim=spec.head_dim)
+    block.attn.to_qkv_mlp_proj = _layer(p, "single.attn.to_qkv_mlp_proj", device)
+    block.attn.to_out = _layer(p, "single.attn.to_out", device)
+    block.attn.norm_q.weight = p["single.attn.norm_q.weight"].to(device)
+    block.attn.norm_k.weight = p["single.attn.norm_k.weight"].to(device)
+    return block
+
+
+def flux_tables(spec: FluxSpec, device) -> tuple[torch.Tensor, torch.Tensor]:
+    """``(1, T, 1, Dh)`` fp32 rotary tables for the joint [text, image] sequence on ``device``."""
+    cos, sin = flux_rope(spec)
+    return cos[None, :, None].contiguous().to(device), sin[None, :, None].contiguous().to(device)
+
+
 def flop_count(spec) -> dict[str, float]:
     """Algorithmic work of one block: GEMM ``2MNK``, attention ``4 H Tq Tk Dh``."""
     if isinstance(spec, LTXSpec):
@@ -296,7 +342,10 @@ __all__ = [
     "CONFIGS",
     "FluxSpec",
     "LTXSpec",
+    "build_flux_double_block",
+    "build_flux_single_block",
     "build_ltx_block",
+    "flux_tables",
     "flop_count",
     "flux_inputs",
     "flux_params",

@@ -16,12 +16,14 @@ from .ops import (
     gate,
     gated_residual,
     gelu_approx,
+    layer_norm,
     linear,
     modulate,
     normalized,
     pair_rope,
     quantized_linear,
     rms_norm,
+    silu,
     split_rope,
     swiglu,
     to_bf16,
@@ -147,19 +149,42 @@ def _heads_rope(value, cos, sin, heads: int) -> np.ndarray:
     return rotated.reshape(tokens, width)
 
 
-def _joint_attention(q_parts, k_parts, v_parts, rope, heads: int) -> np.ndarray:
+def _joint_attention(q_parts, k_parts, v_parts, rope, heads: int, store=_keep) -> np.ndarray:
     """Concatenate [text, image] streams, rotate Q/K by adjacent pairs, attend
     (``kinomlx/models/flux2/transformer.py:35-53``; ``kv.py:48-54``)."""
     q = np.concatenate(q_parts, axis=0)
     k = np.concatenate(k_parts, axis=0)
     v = np.concatenate(v_parts, axis=0)
     cos, sin = rope
-    q = _heads_rope(q, cos, sin, heads)
-    k = _heads_rope(k, cos, sin, heads)
-    return attention(q, k, v, heads=heads)
+    q = store(_heads_rope(q, cos, sin, heads))
+    k = store(_heads_rope(k, cos, sin, heads))
+    return store(attention(q, k, v, heads=heads))
 
 
-def flux_double_block(params: dict, image, text, image_mod, text_mod, rope, *, heads: int, ff: str = "swiglu"):
+def _flux_normalized(store):
+    """``normalized`` as the reference's graph evaluates it: ``mx.fast.layer_norm`` returns the
+    activation dtype, then the compiled modulation (``flux2/transformer.py:56-60``)."""
+
+    def run(value, shift, scale):
+        n = store(layer_norm(value))
+        return store((n * (F32(1.0) + scale) + shift).astype(F32))
+
+    return run
+
+
+def _flux_swiglu(store):
+    """``silu(gate) * content`` with ``fused_ops.silu`` returning the activation dtype
+    (``flux2/transformer.py:63-65``)."""
+
+    def run(value):
+        half = value.shape[-1] // 2
+        return store((store(silu(value[..., :half])) * value[..., half:]).astype(F32))
+
+    return run
+
+
+def flux_double_block(params: dict, image, text, image_mod, text_mod, rope, *, heads: int, ff: str = "swiglu",
+                      bf16_graph: bool = False):
     """FLUX.2 ``DoubleBlock.__call__`` (``kinomlx/models/flux2/transformer.py:136-167``) with
     ``DoubleAttention`` (``:88-133``): LayerNorm modulation, per-head QKNorm, joint [text, image]
     attention with adjacent-pair RoPE, gated residuals.
@@ -167,57 +192,69 @@ def flux_double_block(params: dict, image, text, image_mod, text_mod, rope, *, h
     ``image_mod``/``text_mod`` are ``(6, D)``: shift, scale, gate, ff_shift, ff_scale, ff_gate.
     ``rope`` is ``(cos, sin)`` of shape ``(T_text + T_image, Dh)``. ``ff`` selects the
     feed-forward: ``"swiglu"`` (FLUX, ``:63-85``) or ``"gelu"`` (LTX ``FeedForward``, config 1).
+
+    ``bf16_graph=True`` restates the reference's own bf16 execution: every array the MLX graph
+    materialises in the activation dtype is rounded to bf16 — the layer norm and the modulated
+    value, each projection, the QK norms, each rotation, the attention output, the gate
+    products and the residual sums (``:155-166``), SiLU and the SwiGLU product.
     """
+    store = to_bf16 if bf16_graph else _keep
+    norm = _flux_normalized(store)
+    glu = _flux_swiglu(store)
     image = np.asarray(image, dtype=F32)
     text = np.asarray(text, dtype=F32)
     im = np.asarray(image_mod, dtype=F32)
     tm = np.asarray(text_mod, dtype=F32)
-    img_n = normalized(image, im[0], im[1])
-    txt_n = normalized(text, tm[0], tm[1])
-    q = [
-        _heads_norm(_lin(params, "attn.add_q_proj", txt_n), params["attn.norm_added_q.weight"], heads),
-        _heads_norm(_lin(params, "attn.to_q", img_n), params["attn.norm_q.weight"], heads),
-    ]
-    k = [
-        _heads_norm(_lin(params, "attn.add_k_proj", txt_n), params["attn.norm_added_k.weight"], heads),
-        _heads_norm(_lin(params, "attn.to_k", img_n), params["attn.norm_k.weight"], heads),
-    ]
-    v = [_lin(params, "attn.add_v_proj", txt_n), _lin(params, "attn.to_v", img_n)]
-    result = _joint_attention(q, k, v, rope, heads)
+
+    def lin(name, value):
+        return store(_lin(params, name, value))
+
+    def qk(name, norm_name, value):
+        return store(_heads_norm(lin(name, value), params[norm_name], heads))
+
+    img_n = norm(image, im[0], im[1])
+    txt_n = norm(text, tm[0], tm[1])
+    q = [qk("attn.add_q_proj", "attn.norm_added_q.weight", txt_n), qk("attn.to_q", "attn.norm_q.weight", img_n)]
+    k = [qk("attn.add_k_proj", "attn.norm_added_k.weight", txt_n), qk("attn.to_k", "attn.norm_k.weight", img_n)]
+    v = [lin("attn.add_v_proj", txt_n), lin("attn.to_v", img_n)]
+    result = _joint_attention(q, k, v, rope, heads, store)
     t_text = text.shape[0]
-    ai = _lin(params, "attn.to_out", result[t_text:])
-    at = _lin(params, "attn.to_add_out", result[:t_text])
-    image = (image + im[2] * ai).astype(F32)
-    text = (text + tm[2] * at).astype(F32)
+    ai = lin("attn.to_out", result[t_text:])
+    at = lin("attn.to_add_out", result[:t_text])
+    image = store((image + store(im[2] * ai)).astype(F32))
+    text = store((text + store(tm[2] * at)).astype(F32))
 
     def feed_forward(prefix: str, value):
         if ff == "swiglu":
-            return _lin(params, f"{prefix}.linear_out", swiglu(_lin(params, f"{prefix}.linear_in", value)))
-        return ltx_feed_forward(params, prefix, value)
+            return lin(f"{prefix}.linear_out", glu(lin(f"{prefix}.linear_in", value)))
+        return ltx_feed_forward(params, prefix, value, store)
 
-    image = (image + im[5] * feed_forward("ff", normalized(image, im[3], im[4]))).astype(F32)
-    text = (text + tm[5] * feed_forward("ff_context", normalized(text, tm[3], tm[4]))).astype(F32)
+    image = store((image + store(im[5] * feed_forward("ff", norm(image, im[3], im[4])))).astype(F32))
+    text = store((text + store(tm[5] * feed_forward("ff_context", norm(text, tm[3], tm[4])))).astype(F32))
     return image, text
 
 
-def flux_single_block(params: dict, value, modulation, rope, *, heads: int, width: int):
+def flux_single_block(params: dict, value, modulation, rope, *, heads: int, width: int, bf16_graph: bool = False):
     """FLUX.2 ``SingleBlock.__call__`` (``kinomlx/models/flux2/transformer.py:201-220``) with
     ``SingleAttention`` (``:170-198``): one fused projection split [D, 2D, 3D], per-head QKNorm,
     adjacent-pair RoPE, ``to_out(concat[attention, swiglu(mlp)])``, gated residual.
-    ``modulation`` is ``(3, D)``: shift, scale, gate."""
+    ``modulation`` is ``(3, D)``: shift, scale, gate. ``bf16_graph`` as ``flux_double_block``."""
+    store = to_bf16 if bf16_graph else _keep
     x = np.asarray(value, dtype=F32)
     mod = np.asarray(modulation, dtype=F32)
-    n = normalized(x, mod[0], mod[1])
-    fused = _lin(params, "attn.to_qkv_mlp_proj", n)
+    n = _flux_normalized(store)(x, mod[0], mod[1])
+    fused = store(_lin(params, "attn.to_qkv_mlp_proj", n))
     q, k, v, mlp = fused[:, :width], fused[:, width : 2 * width], fused[:, 2 * width : 3 * width], fused[:, 3 * width :]
-    q = _heads_norm(q, params["attn.norm_q.weight"], heads)
-    k = _heads_norm(k, params["attn.norm_k.weight"], heads)
-    attn = _joint_attention([q], [k], [v], rope, heads)
-    out = _lin(params, "attn.to_out", np.concatenate([attn, swiglu(mlp)], axis=-1))
-    return (x + mod[2] * out).astype(F32)
+    q = store(_heads_norm(q, params["attn.norm_q.weight"], heads))
+    k = store(_heads_norm(k, params["attn.norm_k.weight"], heads))
+    attn = _joint_attention([q], [k], [v], rope, heads, store)
+    out = store(_lin(params, "attn.to_out", np.concatenate([attn, _flux_swiglu(store)(mlp)], axis=-1)))
+    return store((x + store(mod[2] * out)).astype(F32))
 
 
-def config1_double_block(params: dict, image, text, image_mod, text_mod, rope, *, heads: int):
+def config1_double_block(params: dict, image, text, image_mod, text_mod, rope, *, heads: int,
+                         bf16_graph: bool = False):
     """This build's config-1 block: the FLUX.2 double-stream structure with LTX's GELU-tanh
     feed-forward (biases on the feed-forward only) and Krea-style per-axis RoPE tables."""
-    return flux_double_block(params, image, text, image_mod, text_mod, rope, heads=heads, ff="gelu")
+    return flux_double_block(params, image, text, image_mod, text_mod, rope, heads=heads, ff="gelu",
+                             bf16_graph=bf16_graph)

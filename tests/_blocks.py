@@ -43,3 +43,14 @@ def device_tables(pe, device):
     cos_d = torch.from_numpy(np.ascontiguousarray(cos.transpose(0, 2, 1, 3))).to(device).transpose(1, 2)
     sin_d = torch.from_numpy(np.ascontiguousarray(sin.transpose(0, 2, 1, 3))).to(device).transpose(1, 2)
     return cos_d, sin_d
+
+
+def flux_case(spec, seed=0):
+    """(params, oracle double-block params, oracle single-block params, inputs, (cos, sin) numpy
+    ``(T, Dh)`` tables) for a FLUX.2 / config-1 spec."""
+    p = workloads.flux_params(spec, seed)
+    inputs = workloads.flux_inputs(spec, seed)
+    cos, sin = workloads.flux_rope(spec)
+    op = {k: v.float().numpy() for k, v in p.items()}
+    single = {k[len("single."):]: v for k, v in op.items() if k.startswith("single.")}
+    return p, op, single, inputs, (cos.numpy(), sin.numpy())

@@ -1,4 +1,4 @@
-"""FP32 PyTorch evaluation of the LTX-2 video block (test infrastructure).
+"""FP32 PyTorch evaluation of the LTX-2 video block and the FLUX.2 blocks (test infrastructure).
 
 The same composition as ``oracle.ltx_video_block`` written with torch operations, so that the
 full-size (9216-token) block can be evaluated in FP32 on the GPU in seconds, where the numpy
@@ -79,3 +79,78 @@ def ltx_video_block(p, x, context, pe, heads, bf16_graph=False):
     n = st(st(_rms(x)) * (1 + ada[4]) + ada[3])
     h = st(torch.nn.functional.gelu(st(_lin(p, "ff.proj_in", n)), approximate="tanh"))
     return st(x + st(_lin(p, "ff.proj_out", h)) * ada[5])
+
+
+def _layer_norm(x, eps=1e-6):
+    mean = x.mean(-1, keepdim=True)
+    c = x - mean
+    return c * torch.rsqrt((c * c).mean(-1, keepdim=True) + eps)
+
+
+def _pair_rope(x, cos, sin, heads):
+    """Adjacent-pair rotation of ``(T, H * Dh)`` rows by ``(T, Dh)`` tables."""
+    t, width = x.shape
+    xh = x.reshape(t, heads, width // (2 * heads), 2)
+    c = cos.reshape(t, 1, -1, 2)[..., 0]
+    s = sin.reshape(t, 1, -1, 2)[..., 0]
+    x0, x1 = xh[..., 0], xh[..., 1]
+    return torch.stack([x0 * c - x1 * s, x1 * c + x0 * s], -1).reshape(t, width)
+
+
+def _heads_rms(x, w, heads):
+    t, width = x.shape
+    return _rms(x.reshape(t, heads, width // heads), w).reshape(t, width)
+
+
+def _swiglu(x, st):
+    half = x.shape[-1] // 2
+    return st(st(torch.nn.functional.silu(x[..., :half])) * x[..., half:])
+
+
+def flux_double_block(p, image, text, im, tm, rope, heads, ff="swiglu", bf16_graph=False):
+    """Torch form of ``oracle.flux_double_block`` (same names, same rounding points)."""
+    st = bf16_store if bf16_graph else _keep
+
+    def norm(x, shift, scale):
+        return st(st(_layer_norm(x)) * (1 + scale) + shift)
+
+    def lin(name, x):
+        return st(_lin(p, name, x))
+
+    def qk(name, norm_name, x):
+        return st(_heads_rms(lin(name, x), p[norm_name], heads))
+
+    img_n, txt_n = norm(image, im[0], im[1]), norm(text, tm[0], tm[1])
+    q = torch.cat([qk("attn.add_q_proj", "attn.norm_added_q.weight", txt_n),
+                   qk("attn.to_q", "attn.norm_q.weight", img_n)])
+    k = torch.cat([qk("attn.add_k_proj", "attn.norm_added_k.weight", txt_n),
+                   qk("attn.to_k", "attn.norm_k.weight", img_n)])
+    v = torch.cat([lin("attn.add_v_proj", txt_n), lin("attn.to_v", img_n)])
+    q, k = st(_pair_rope(q, *rope, heads)), st(_pair_rope(k, *rope, heads))
+    result = st(_attention(q, k, v, heads))
+    tt = text.shape[0]
+    image = st(image + st(im[2] * lin("attn.to_out", result[tt:])))
+    text = st(text + st(tm[2] * lin("attn.to_add_out", result[:tt])))
+
+    def feed_forward(prefix, x):
+        if ff == "swiglu":
+            return lin(f"{prefix}.linear_out", _swiglu(lin(f"{prefix}.linear_in", x), st))
+        h = st(torch.nn.functional.gelu(lin(f"{prefix}.proj_in", x), approximate="tanh"))
+        return lin(f"{prefix}.proj_out", h)
+
+    image = st(image + st(im[5] * feed_forward("ff", norm(image, im[3], im[4]))))
+    text = st(text + st(tm[5] * feed_forward("ff_context", norm(text, tm[3], tm[4]))))
+    return image, text
+
+
+def flux_single_block(p, x, mod, rope, heads, width, bf16_graph=False):
+    """Torch form of ``oracle.flux_single_block``."""
+    st = bf16_store if bf16_graph else _keep
+    n = st(st(_layer_norm(x)) * (1 + mod[1]) + mod[0])
+    fused = st(_lin(p, "attn.to_qkv_mlp_proj", n))
+    q = st(_heads_rms(fused[:, :width], p["attn.norm_q.weight"], heads))
+    k = st(_heads_rms(fused[:, width:2 * width], p["attn.norm_k.weight"], heads))
+    q, k = st(_pair_rope(q, *rope, heads)), st(_pair_rope(k, *rope, heads))
+    attn = st(_attention(q, k, fused[:, 2 * width:3 * width], heads))
+    out = st(_lin(p, "attn.to_out", torch.cat([attn, _swiglu(fused[:, 3 * width:], st)], -1)))
+    return st(x + st(mod[2] * out))

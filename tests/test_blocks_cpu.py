@@ -52,3 +52,39 @@ def test_bf16_graph_rounds_every_output_and_stays_close_to_fp32():
     cos = float(graph.ravel() @ fp32.ravel() / np.linalg.norm(graph) / np.linalg.norm(fp32))
     assert cos > 0.9999
     assert 0 < max_abs(graph, fp32) < 0.1
+
+
+def _flux_small(ff):
+    from tests._blocks import flux_case
+
+    spec = workloads.FluxSpec(grid=(3, 4), text_tokens=5, dim=256, heads=2, head_dim=128, ff_hidden=384, ff=ff,
+                              single=ff == "swiglu")
+    return spec, flux_case(spec)
+
+
+def test_torch_reference_matches_oracle_flux_double_and_config1_blocks():
+    for ff in ("swiglu", "gelu"):
+        spec, (p, op, _, inputs, rope) = _flux_small(ff)
+        image, text = inputs["image"][0].float().numpy(), inputs["text"][0].float().numpy()
+        rope_t = tuple(torch.from_numpy(t) for t in rope)
+        tp = {k: torch.from_numpy(np.asarray(v)) for k, v in op.items()}
+        for graph in (False, True):
+            ri, rt = oracle.flux_double_block(op, image, text, op["image_mod"], op["text_mod"], rope,
+                                              heads=spec.heads, ff=ff, bf16_graph=graph)
+            gi, gt = _torch_ref.flux_double_block(tp, torch.from_numpy(image), torch.from_numpy(text),
+                                                  tp["image_mod"], tp["text_mod"], rope_t, spec.heads, ff=ff,
+                                                  bf16_graph=graph)
+            if graph:  # rare one-ulp flips between the two restatements
+                assert np.mean(gi.numpy() == ri) > 0.95 and np.mean(gt.numpy() == rt) > 0.95
+            else:
+                assert max_abs(gi.numpy(), ri) < 1e-4 and max_abs(gt.numpy(), rt) < 1e-4
+
+
+def test_torch_reference_matches_oracle_flux_single_block():
+    spec, (p, op, single, inputs, rope) = _flux_small("swiglu")
+    x = np.concatenate([inputs["text"][0].float().numpy(), inputs["image"][0].float().numpy()])
+    ref = oracle.flux_single_block(single, x, op["single_mod"], rope, heads=spec.heads, width=spec.dim)
+    tp = {k: torch.from_numpy(np.asarray(v)) for k, v in single.items()}
+    got = _torch_ref.flux_single_block(tp, torch.from_numpy(x), torch.from_numpy(op["single_mod"]),
+                                       tuple(torch.from_numpy(t) for t in rope), spec.heads, spec.dim).numpy()
+    assert max_abs(got, ref) < 1e-4
