@@ -44,6 +44,7 @@ enum {
   KX_EPI_ACT_GELU_TANH = 1 << 4,
   KX_EPI_ACT_SILU = 2 << 4,
   KX_EPI_ACT_SIGMOID2 = 3 << 4, /* 2 * sigmoid(.) — LTX gate logits */
+  KX_EPI_ACT_SIGMOID = 4 << 4,  /* sigmoid(.) — Krea 2 output gate */
   KX_EPI_GATED_RESIDUAL = 1 << 8, /* c = resid + gate[col] * act(acc + bias) */
   KX_EPI_RESID_F32 = 1 << 9,      /* resid is fp32 (a residual stream carried in fp32) */
   KX_EPI_OUT_F32 = 1 << 10        /* c is fp32 */
@@ -127,6 +128,20 @@ int kx_attention_fwd_bf16(const void* q, int64_t ldq, const void* k, int64_t ldk
                           int64_t ldv, void* o, int64_t ldo, int64_t batch, int64_t tq,
                           int64_t tk, int64_t heads, int64_t head_dim, float scale,
                           const void* gate, int64_t ld_gate, kx_stream_t stream);
+
+/*
+ * Grouped-query form of kx_attention_fwd_bf16: k and v hold kv_heads heads ((batch * tk,
+ * kv_heads * head_dim) rows at ldk/ldv) and query head h reads key/value head
+ * h / (heads / kv_heads); heads % kv_heads == 0. Replaces the SDPA call of Krea2Attention
+ * (kinomlx/models/krea2/transformer/model.py:134-185, num_kv_heads <= num_heads), whose K/V
+ * are not repeated per query head here. kx_attention_fwd_bf16 is this call with
+ * kv_heads == heads.
+ */
+int kx_attention_gqa_fwd_bf16(const void* q, int64_t ldq, const void* k, int64_t ldk,
+                              const void* v, int64_t ldv, void* o, int64_t ldo, int64_t batch,
+                              int64_t tq, int64_t tk, int64_t heads, int64_t kv_heads,
+                              int64_t head_dim, float scale, const void* gate, int64_t ld_gate,
+                              kx_stream_t stream);
 
 /*
  * Dense bf16 linear on MFMA: c = epilogue(a · wᵀ) with fp32 accumulation and one rounding.

@@ -35,6 +35,7 @@ EPI_BIAS = 1
 EPI_ACT_GELU_TANH = 1 << 4
 EPI_ACT_SILU = 2 << 4
 EPI_ACT_SIGMOID2 = 3 << 4
+EPI_ACT_SIGMOID = 4 << 4
 EPI_GATED_RESIDUAL = 1 << 8
 EPI_RESID_F32 = 1 << 9
 EPI_OUT_F32 = 1 << 10
@@ -55,6 +56,9 @@ SIGNATURES: dict[str, list] = {
     "kx_rope_pair_bf16": [_P, _I64, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64, _I, _P],
     "kx_attention_fwd_bf16": [
         _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _I64, _P,
+    ],
+    "kx_attention_gqa_fwd_bf16": [
+        _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _I64, _P,
     ],
     "kx_gemm_bf16": [
         _P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _I64, _P, _I64, _I64, _P,
@@ -269,11 +273,18 @@ def launch_rope_pair(x, out, cos, sin, *, heads, head_dim, table_ld, table_hs, t
     )
 
 
-def launch_attention(q, k, v, out, *, batch, tq, tk, heads, head_dim, scale, gate=None) -> None:
+def launch_attention(q, k, v, out, *, batch, tq, tk, heads, head_dim, scale, gate=None, kv_heads=None) -> None:
     _check_gpu("attention", q, k, v, out, gate)
     ld_gate = 0
     if gate is not None:
         _, _, ld_gate = _rows(gate, "attention gate")
+    if kv_heads is not None and kv_heads != heads:
+        _call(
+            "kx_attention_gqa_fwd_bf16", _ptr(q), q.stride(-2), _ptr(k), k.stride(-2), _ptr(v),
+            v.stride(-2), _ptr(out), out.stride(-2), batch, tq, tk, heads, kv_heads, head_dim, scale,
+            _ptr(gate), ld_gate, _stream(),
+        )
+        return
     _call(
         "kx_attention_fwd_bf16", _ptr(q), q.stride(-2), _ptr(k), k.stride(-2), _ptr(v),
         v.stride(-2), _ptr(out), out.stride(-2), batch, tq, tk, heads, head_dim, scale,

@@ -68,8 +68,8 @@ template <int D>
 __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
     const uint16_t* __restrict__ Q, int64_t ldq, const uint16_t* __restrict__ K, int64_t ldk,
     const uint16_t* __restrict__ V, int64_t ldv, uint16_t* __restrict__ O, int64_t ldo, int tq,
-    int tk, int heads, float scale_log2, const uint16_t* __restrict__ gate, int64_t ld_gate,
-    int qtiles) {
+    int tk, int heads, int kv_group, float scale_log2, const uint16_t* __restrict__ gate,
+    int64_t ld_gate, int qtiles) {
   constexpr int ROWB = D * 2;             // bytes per K / V row
   constexpr int CPR = ROWB / 16;          // 16-byte chunks per row
   constexpr int RPI = 64 / CPR;           // rows per DMA instruction
@@ -89,8 +89,9 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
   const int qt = t % qtiles, bh = t / qtiles;
   const int h = bh % heads, b = bh / heads;
   const uint16_t* Qb = Q + (int64_t)b * tq * ldq + (int64_t)h * D;
-  const char* Kb = reinterpret_cast<const char*>(K + (int64_t)b * tk * ldk + (int64_t)h * D);
-  const char* Vb = reinterpret_cast<const char*>(V + (int64_t)b * tk * ldv + (int64_t)h * D);
+  const int hk = h / kv_group;  // grouped-query attention: kv_group query heads share a K/V head
+  const char* Kb = reinterpret_cast<const char*>(K + (int64_t)b * tk * ldk + (int64_t)hk * D);
+  const char* Vb = reinterpret_cast<const char*>(V + (int64_t)b * tk * ldv + (int64_t)hk * D);
 
   const int q0 = qt * BQ + wave * 32;
   const int qrow = min(q0 + lrow, tq - 1);
@@ -249,13 +250,13 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
 template <int D>
 int launch_attn(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
                 void* o, int64_t ldo, int64_t batch, int64_t tq, int64_t tk, int64_t heads,
-                float scale, const void* gate, int64_t ld_gate, hipStream_t s) {
+                int64_t kv_heads, float scale, const void* gate, int64_t ld_gate, hipStream_t s) {
   const int qtiles = (int)((tq + BQ - 1) / BQ);
   const int64_t blocks = (int64_t)qtiles * heads * batch;
   attn_fwd_kernel<D><<<(unsigned)blocks, NWAVE * 64, 0, s>>>(
       (const uint16_t*)q, ldq, (const uint16_t*)k, ldk, (const uint16_t*)v, ldv, (uint16_t*)o,
-      ldo, (int)tq, (int)tk, (int)heads, scale * 1.4426950408889634f, (const uint16_t*)gate,
-      ld_gate, qtiles);
+      ldo, (int)tq, (int)tk, (int)heads, (int)(heads / kv_heads), scale * 1.4426950408889634f,
+      (const uint16_t*)gate, ld_gate, qtiles);
   return check_launch("kx_attention_fwd_bf16");
 }
 
@@ -264,30 +265,52 @@ int launch_attn(const void* q, int64_t ldq, const void* k, int64_t ldk, const vo
 
 using namespace kx;
 
+namespace {
+int attention_entry(const char* name, const void* q, int64_t ldq, const void* k, int64_t ldk,
+                    const void* v, int64_t ldv, void* o, int64_t ldo, int64_t batch, int64_t tq,
+                    int64_t tk, int64_t heads, int64_t kv_heads, int64_t head_dim, float scale,
+                    const void* gate, int64_t ld_gate, kx_stream_t stream) {
+  KX_REQUIRE(q && k && v && o, "%s: null tensor", name);
+  KX_REQUIRE(head_dim == 64 || head_dim == 128, "%s: head_dim must be 64 or 128, got %lld", name,
+             (long long)head_dim);
+  KX_REQUIRE(batch >= 0 && tq >= 0 && tk > 0 && heads > 0 && tq < (1ll << 30) &&
+                 tk < (1ll << 30),
+             "%s: bad shape", name);
+  KX_REQUIRE(kv_heads > 0 && heads % kv_heads == 0,
+             "%s: %lld query heads do not group over %lld key/value heads", name, (long long)heads,
+             (long long)kv_heads);
+  const int64_t width = heads * head_dim, kv_width = kv_heads * head_dim;
+  KX_REQUIRE(ldq >= width && ldk >= kv_width && ldv >= kv_width && ldo >= width,
+             "%s: row strides must cover heads * head_dim", name);
+  KX_REQUIRE(ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 && ldo % 4 == 0 && aligned16(q) &&
+                 aligned16(k) && aligned16(v) && aligned8(o),
+             "%s: q/k/v rows must be 16-byte and o rows 8-byte aligned", name);
+  KX_REQUIRE(!gate || ld_gate >= heads, "%s: gate stride must cover heads", name);
+  KX_REQUIRE((int64_t)((tq + BQ - 1) / BQ) * heads * batch < (1ll << 31), "%s: too many tiles",
+             name);
+  if (tq == 0 || batch == 0) return KX_OK;
+  if (head_dim == 128)
+    return launch_attn<128>(q, ldq, k, ldk, v, ldv, o, ldo, batch, tq, tk, heads, kv_heads, scale,
+                            gate, ld_gate, (hipStream_t)stream);
+  return launch_attn<64>(q, ldq, k, ldk, v, ldv, o, ldo, batch, tq, tk, heads, kv_heads, scale,
+                         gate, ld_gate, (hipStream_t)stream);
+}
+}  // namespace
+
+extern "C" int kx_attention_gqa_fwd_bf16(const void* q, int64_t ldq, const void* k, int64_t ldk,
+                                         const void* v, int64_t ldv, void* o, int64_t ldo,
+                                         int64_t batch, int64_t tq, int64_t tk, int64_t heads,
+                                         int64_t kv_heads, int64_t head_dim, float scale,
+                                         const void* gate, int64_t ld_gate, kx_stream_t stream) {
+  return attention_entry("kx_attention_gqa_fwd_bf16", q, ldq, k, ldk, v, ldv, o, ldo, batch, tq,
+                         tk, heads, kv_heads, head_dim, scale, gate, ld_gate, stream);
+}
+
 extern "C" int kx_attention_fwd_bf16(const void* q, int64_t ldq, const void* k, int64_t ldk,
                                      const void* v, int64_t ldv, void* o, int64_t ldo,
                                      int64_t batch, int64_t tq, int64_t tk, int64_t heads,
                                      int64_t head_dim, float scale, const void* gate,
                                      int64_t ld_gate, kx_stream_t stream) {
-  KX_REQUIRE(q && k && v && o, "kx_attention_fwd_bf16: null tensor");
-  KX_REQUIRE(head_dim == 64 || head_dim == 128,
-             "kx_attention_fwd_bf16: head_dim must be 64 or 128, got %lld", (long long)head_dim);
-  KX_REQUIRE(batch >= 0 && tq >= 0 && tk > 0 && heads > 0 && tq < (1ll << 30) &&
-                 tk < (1ll << 30),
-             "kx_attention_fwd_bf16: bad shape");
-  const int64_t width = heads * head_dim;
-  KX_REQUIRE(ldq >= width && ldk >= width && ldv >= width && ldo >= width,
-             "kx_attention_fwd_bf16: row strides must cover heads * head_dim");
-  KX_REQUIRE(ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 && ldo % 4 == 0 && aligned16(q) &&
-                 aligned16(k) && aligned16(v) && aligned8(o),
-             "kx_attention_fwd_bf16: q/k/v rows must be 16-byte and o rows 8-byte aligned");
-  KX_REQUIRE(!gate || ld_gate >= heads, "kx_attention_fwd_bf16: gate stride must cover heads");
-  KX_REQUIRE((int64_t)((tq + BQ - 1) / BQ) * heads * batch < (1ll << 31),
-             "kx_attention_fwd_bf16: too many tiles");
-  if (tq == 0 || batch == 0) return KX_OK;
-  if (head_dim == 128)
-    return launch_attn<128>(q, ldq, k, ldk, v, ldv, o, ldo, batch, tq, tk, heads, scale, gate,
-                            ld_gate, (hipStream_t)stream);
-  return launch_attn<64>(q, ldq, k, ldk, v, ldv, o, ldo, batch, tq, tk, heads, scale, gate,
-                         ld_gate, (hipStream_t)stream);
+  return attention_entry("kx_attention_fwd_bf16", q, ldq, k, ldk, v, ldv, o, ldo, batch, tq, tk,
+                         heads, heads, head_dim, scale, gate, ld_gate, stream);
 }

@@ -69,6 +69,7 @@ __device__ __forceinline__ float fast_gelu_tanh(float x) {
 }
 __device__ __forceinline__ float fast_silu(float x) { return x * fast_rcp(1.0f + fast_exp(-x)); }
 __device__ __forceinline__ float fast_sigmoid2(float x) { return 2.0f * fast_rcp(1.0f + fast_exp(-x)); }
+__device__ __forceinline__ float fast_sigmoid(float x) { return fast_rcp(1.0f + fast_exp(-x)); }
 
 // ---- wave reductions (wave64) -------------------------------------------------------------------
 template <int WIDTH>

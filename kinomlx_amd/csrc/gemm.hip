@@ -50,6 +50,7 @@ __device__ __forceinline__ float apply_act(float v, int act) {
     case 1: return fast_gelu_tanh(v);
     case 2: return fast_silu(v);
     case 3: return fast_sigmoid2(v);
+    case 4: return fast_sigmoid(v);
     default: return v;
   }
 }
@@ -1056,7 +1057,7 @@ int check_epilogue(const char* name, int epilogue, const void* bias, const void*
   const int act = (epilogue >> 4) & 15;
   const int known = KX_EPI_BIAS | (15 << 4) | KX_EPI_GATED_RESIDUAL | KX_EPI_RESID_F32 |
                     KX_EPI_OUT_F32;
-  KX_REQUIRE((epilogue & ~known) == 0 && act <= 3, "%s: bad epilogue flags %d", name, epilogue);
+  KX_REQUIRE((epilogue & ~known) == 0 && act <= 4, "%s: bad epilogue flags %d", name, epilogue);
   KX_REQUIRE(!(epilogue & KX_EPI_BIAS) || (bias && aligned8(bias)), "%s: bias missing or unaligned",
              name);
   KX_REQUIRE(!(epilogue & KX_EPI_OUT_F32) || (aligned16(c) && ldc % 4 == 0),

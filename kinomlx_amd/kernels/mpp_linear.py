@@ -33,6 +33,7 @@ ACTIVATIONS = {
     "gelu_tanh": _lib.EPI_ACT_GELU_TANH,
     "silu": _lib.EPI_ACT_SILU,
     "sigmoid2": _lib.EPI_ACT_SIGMOID2,
+    "sigmoid": _lib.EPI_ACT_SIGMOID,
 }
 
 

@@ -42,7 +42,7 @@ def applies(query: torch.Tensor, key: torch.Tensor, *, heads: int) -> bool:
 
 def _attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, heads: int, batch: int,
                tq: int, tk: int, dim: int, gate: torch.Tensor | None, scale: float | None,
-               out: torch.Tensor | None = None) -> torch.Tensor:
+               out: torch.Tensor | None = None, kv_heads: int | None = None) -> torch.Tensor:
     if out is None:
         out = torch.empty((batch, tq, heads * dim), dtype=q.dtype, device=q.device)
     elif (out.dtype != q.dtype or tuple(out.shape) != (batch, tq, heads * dim) or out.stride(-1) != 1
@@ -54,7 +54,7 @@ def _attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, heads: int,
         gate = gate.reshape(batch * tq, heads)
     _lib.launch_attention(
         q, k, v, out, batch=batch, tq=tq, tk=tk, heads=heads, head_dim=dim,
-        scale=dim ** -0.5 if scale is None else scale, gate=gate,
+        scale=dim ** -0.5 if scale is None else scale, gate=gate, kv_heads=kv_heads,
     )
     return out
 
@@ -96,15 +96,20 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, heads:
 
 def batched_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, heads: int,
                       gate: torch.Tensor | None = None, scale: float | None = None,
-                      out: torch.Tensor | None = None) -> torch.Tensor:
+                      out: torch.Tensor | None = None, kv_heads: int | None = None) -> torch.Tensor:
     """``(batch, tokens, heads * dim)`` form of ``dense_attention``; q/k/v (and ``out``, when
     given) may be strided row views, e.g. column slices of a fused QKV projection or of the
-    buffer the next projection reads."""
+    buffer the next projection reads. With ``kv_heads`` (grouped-query attention) k and v hold
+    ``kv_heads * dim`` columns and query head ``h`` reads key/value head
+    ``h // (heads // kv_heads)``."""
     if q.dim() != 3 or k.dim() != 3 or v.shape != k.shape or q.shape[0] != k.shape[0]:
         raise ValueError("batched attention needs (batch, tokens, heads * dim) q, k and v")
     width = q.shape[-1]
     dim = _check(q, k, v, heads, width)
-    if dim not in HEAD_DIMS or k.shape[-1] != width:
+    groups = heads if kv_heads is None else kv_heads
+    if groups <= 0 or heads % groups:
+        raise ValueError(f"{heads} query heads do not group over {groups} key/value heads")
+    if dim not in HEAD_DIMS or k.shape[-1] != groups * dim:
         raise ValueError(f"attention head width must be 64 or 128, got {width} / {heads}")
     batch, tq, tk = q.shape[0], q.shape[1], k.shape[1]
     if tk == 0:
@@ -112,7 +117,8 @@ def batched_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, head
     for name, t in (("q", q), ("k", k), ("v", v)):
         if t.stride(-1) != 1 or (batch > 1 and t.stride(0) != t.shape[1] * t.stride(1)):
             raise ValueError(f"attention {name} must have contiguous rows, evenly strided over the batch")
-    return _attention(q, k, v, heads=heads, batch=batch, tq=tq, tk=tk, dim=dim, gate=gate, scale=scale, out=out)
+    return _attention(q, k, v, heads=heads, batch=batch, tq=tq, tk=tk, dim=dim, gate=gate, scale=scale, out=out,
+                      kv_heads=kv_heads)
 
 
 __all__ = ["HEAD_DIMS", "applies", "batched_attention", "dense_attention"]

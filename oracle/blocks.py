@@ -33,6 +33,8 @@ __all__ = [
     "config1_double_block",
     "flux_double_block",
     "flux_single_block",
+    "krea_attention",
+    "krea_block",
     "ltx_attention",
     "ltx_feed_forward",
     "ltx_video_block",
@@ -258,3 +260,58 @@ def config1_double_block(params: dict, image, text, image_mod, text_mod, rope, *
     feed-forward (biases on the feed-forward only) and Krea-style per-axis RoPE tables."""
     return flux_double_block(params, image, text, image_mod, text_mod, rope, heads=heads, ff="gelu",
                              bf16_graph=bf16_graph)
+
+
+def krea_attention(params: dict, prefix: str, value, *, heads: int, kv_heads: int, eps: float, rotary=None,
+                   store=_keep) -> np.ndarray:
+    """``Krea2Attention.__call__`` without a mask (``kinomlx/models/krea2/transformer/model.py:134-196``):
+    Q/K/V/gate projections, zero-centred per-head RMSNorm on Q and K, adjacent-pair RoPE with
+    ``(T, Dh)`` tables, grouped-query SDPA (query head ``h`` reads K/V head ``h // (H / Hkv)``,
+    scale ``Dh ** -0.5``), ``attended * sigmoid(gate)`` over the full width, ``to_out``."""
+    x = np.asarray(value, dtype=F32)
+    tokens, hidden = x.shape
+    dh = hidden // heads
+    q = store(_lin(params, f"{prefix}.to_q", x)).reshape(tokens, heads, dh)
+    k = store(_lin(params, f"{prefix}.to_k", x)).reshape(tokens, kv_heads, dh)
+    v = store(_lin(params, f"{prefix}.to_v", x)).reshape(tokens, kv_heads, dh)
+    g = store(_lin(params, f"{prefix}.to_gate", x))
+    q = store(rms_norm(q, params[f"{prefix}.norm_q.weight"], eps, weight_offset=1.0))
+    k = store(rms_norm(k, params[f"{prefix}.norm_k.weight"], eps, weight_offset=1.0))
+    if rotary is not None:
+        cos, sin = rotary
+        q = store(pair_rope(q, cos[:, None, :], sin[:, None, :]))
+        k = store(pair_rope(k, cos[:, None, :], sin[:, None, :]))
+    group = heads // kv_heads
+    k_full = np.repeat(k, group, axis=1).reshape(tokens, hidden)
+    v_full = np.repeat(v, group, axis=1).reshape(tokens, hidden)
+    out = store(attention(q.reshape(tokens, hidden), k_full, v_full, heads=heads))
+    out = store(out * store(sigmoid(g)))
+    return store(_lin(params, f"{prefix}.to_out", out))
+
+
+def krea_block(params: dict, value, modulation, rotary, *, heads: int, kv_heads: int, eps: float = 1e-6,
+               bf16_graph: bool = False) -> np.ndarray:
+    """``Krea2TransformerBlock.__call__`` (``kinomlx/models/krea2/transformer/model.py:310-348``).
+
+    ``modulation`` is the ``(6, D)`` sum ``time_modulation + scale_shift_table`` in the official
+    chunk order (prescale, preshift, pregate, postscale, postshift, postgate; ``:288-307``).
+    ``norm1``/``norm2`` are zero-centred RMSNorms with weights (``:29-46``); the feed-forward is
+    ``down(silu(gate(x)) * up(x))`` (``:199-214``). ``bf16_graph=True`` rounds every array the
+    MLX graph materialises to bf16, as ``ltx_video_block`` does."""
+    store = to_bf16 if bf16_graph else _keep
+    x = np.asarray(value, dtype=F32)
+    mod = np.asarray(modulation, dtype=F32)
+    pre_s, pre_sh, pre_g, post_s, post_sh, post_g = mod
+    one = F32(1.0)
+
+    def modulated(v, norm_name, scale, shift):
+        n = store(rms_norm(v, params[norm_name], eps, weight_offset=1.0))
+        return store((store(store(one + scale) * n) + shift).astype(F32))
+
+    attn = krea_attention(params, "attn", modulated(x, "norm1.weight", pre_s, pre_sh), heads=heads,
+                          kv_heads=kv_heads, eps=eps, rotary=rotary, store=store)
+    x = store((x + store(pre_g * attn)).astype(F32))
+    f = modulated(x, "norm2.weight", post_s, post_sh)
+    hidden = store(store(silu(store(_lin(params, "ff.gate", f)))) * store(_lin(params, "ff.up", f)))
+    ff = store(_lin(params, "ff.down", hidden))
+    return store((x + store(post_g * ff)).astype(F32))

@@ -54,3 +54,48 @@ def flux_case(spec, seed=0):
     op = {k: v.float().numpy() for k, v in p.items()}
     single = {k[len("single."):]: v for k, v in op.items() if k.startswith("single.")}
     return p, op, single, inputs, (cos.numpy(), sin.numpy())
+
+
+def krea_case(hidden, heads, kv_heads, tokens, ff_hidden, seed=0, batch=1):
+    """Seeded Krea 2 block: (device-agnostic CPU params, oracle params, x (B, T, D) bf16,
+    time_modulation (B, 6D) bf16, position ids (B, T, 3))."""
+    dh = hidden // heads
+    p = {}
+    for name, rows in (("to_q", hidden), ("to_k", kv_heads * dh), ("to_v", kv_heads * dh), ("to_gate", hidden),
+                       ("to_out", hidden)):
+        p[f"attn.{name}.weight"] = workloads.bf16(workloads.normal(seed, f"krea.attn.{name}", (rows, hidden), 0.02))
+    for name in ("norm_q", "norm_k"):
+        p[f"attn.{name}.weight"] = workloads.normal(seed, f"krea.attn.{name}", (dh,), 0.1)
+    for name in ("norm1", "norm2"):
+        p[f"{name}.weight"] = workloads.normal(seed, f"krea.{name}", (hidden,), 0.1)
+    p["ff.gate.weight"] = workloads.bf16(workloads.normal(seed, "krea.ff.gate", (ff_hidden, hidden), 0.02))
+    p["ff.up.weight"] = workloads.bf16(workloads.normal(seed, "krea.ff.up", (ff_hidden, hidden), 0.02))
+    p["ff.down.weight"] = workloads.bf16(workloads.normal(seed, "krea.ff.down", (hidden, ff_hidden), 0.02))
+    p["scale_shift_table"] = workloads.normal(seed, "krea.table", (6, hidden), 0.1)
+    x = workloads.bf16(workloads.normal(seed, "krea.x", (batch, tokens, hidden)))
+    tmod = workloads.bf16(workloads.normal(seed, "krea.tmod", (batch, 6 * hidden), 0.3))
+    g = torch.Generator().manual_seed(seed)
+    ids = torch.randint(0, 40, (batch, tokens, 3), generator=g).float()
+    op = {k: v.float().numpy() for k, v in p.items()}
+    return p, op, x, tmod, ids
+
+
+def build_krea_block(p, hidden, heads, kv_heads, device, *, fuse=True):
+    from kinomlx_amd.krea2.transformer import Krea2BlockConfig, Krea2TransformerBlock
+    from kinomlx_amd.ltx2.attention import Linear
+
+    cfg = Krea2BlockConfig(attention_head_dim=hidden // heads, num_attention_heads=heads,
+                           num_key_value_heads=kv_heads)
+    block = Krea2TransformerBlock(cfg)
+    for name in ("to_q", "to_k", "to_v", "to_gate", "to_out"):
+        setattr(block.attn, name, Linear(p[f"attn.{name}.weight"].to(device)))
+    block.attn.norm_q.weight = p["attn.norm_q.weight"].to(device)
+    block.attn.norm_k.weight = p["attn.norm_k.weight"].to(device)
+    block.norm1.weight = p["norm1.weight"].to(device)
+    block.norm2.weight = p["norm2.weight"].to(device)
+    for name in ("gate", "up", "down"):
+        setattr(block.ff, name, Linear(p[f"ff.{name}.weight"].to(device)))
+    block.scale_shift_table = p["scale_shift_table"].to(device)
+    if fuse:
+        block.fuse_projections()
+    return block

@@ -424,3 +424,68 @@ def test_flux_double_block_gates_and_stream_order():
     tm_ff[[3, 4, 5]] += 1.0  # text feed-forward modulation only
     i2, t2 = oracle.flux_double_block(p, image, text, im, tm_ff, rope, heads=heads)
     assert np.array_equal(i1, i2) and not np.array_equal(t2, _)
+
+
+def _krea_params(r, hidden, heads, kv_heads, ff=48):
+    dh = hidden // heads
+    p = {}
+    for name, rows in (("to_q", hidden), ("to_k", kv_heads * dh), ("to_v", kv_heads * dh), ("to_gate", hidden),
+                       ("to_out", hidden)):
+        p[f"attn.{name}.weight"] = (r.standard_normal((rows, hidden)) * 0.2).astype(F32)
+    p["attn.norm_q.weight"] = (r.standard_normal(dh) * 0.1).astype(F32)
+    p["attn.norm_k.weight"] = (r.standard_normal(dh) * 0.1).astype(F32)
+    p["norm1.weight"] = (r.standard_normal(hidden) * 0.1).astype(F32)
+    p["norm2.weight"] = (r.standard_normal(hidden) * 0.1).astype(F32)
+    p["ff.gate.weight"] = (r.standard_normal((ff, hidden)) * 0.2).astype(F32)
+    p["ff.up.weight"] = (r.standard_normal((ff, hidden)) * 0.2).astype(F32)
+    p["ff.down.weight"] = (r.standard_normal((hidden, ff)) * 0.2).astype(F32)
+    return p
+
+
+def test_krea_grouped_query_attention_reads_kv_head_h_over_group():
+    """Grouped-query attention equals full multi-head attention whose K/V weights repeat each
+    K/V head's rows for its group of query heads ``h // (H / Hkv)`` (MLX SDPA GQA semantics):
+    an ``h % Hkv`` mapping or a transposed head order fails this."""
+    r = _rng(401)
+    hidden, heads, kv_heads, t = 32, 4, 2, 6
+    dh = hidden // heads
+    p = _krea_params(r, hidden, heads, kv_heads)
+    x = r.standard_normal((t, hidden)).astype(F32)
+    ang = r.uniform(-2, 2, (t, dh // 2)).astype(F32)
+    rot = (np.repeat(np.cos(ang), 2, -1), np.repeat(np.sin(ang), 2, -1))
+    got = oracle.krea_attention(p, "attn", x, heads=heads, kv_heads=kv_heads, eps=1e-6, rotary=rot)
+    full = dict(p)
+    for name in ("to_k", "to_v"):
+        w = p[f"attn.{name}.weight"].reshape(kv_heads, dh, hidden)
+        full[f"attn.{name}.weight"] = np.repeat(w, heads // kv_heads, axis=0).reshape(hidden, hidden)
+    want = oracle.krea_attention(full, "attn", x, heads=heads, kv_heads=heads, eps=1e-6, rotary=rot)
+    assert max_abs(got, want) < 1e-6
+    swapped = dict(full)
+    for name in ("to_k", "to_v"):  # the other head order really changes the result
+        w = p[f"attn.{name}.weight"].reshape(kv_heads, dh, hidden)
+        swapped[f"attn.{name}.weight"] = np.tile(w, (heads // kv_heads, 1, 1)).reshape(hidden, hidden)
+    other = oracle.krea_attention(swapped, "attn", x, heads=heads, kv_heads=heads, eps=1e-6, rotary=rot)
+    assert max_abs(got, other) > 1e-3
+
+
+def test_krea_block_gates_and_modulation_order():
+    """Zero pre/post gates (chunks 2 and 5 of the official order) leave x unchanged; the output
+    gate is sigmoid over the full width (a zero to_gate weight halves the attention output)."""
+    r = _rng(402)
+    hidden, heads, kv_heads, t = 32, 4, 2, 5
+    p = _krea_params(r, hidden, heads, kv_heads)
+    x = r.standard_normal((t, hidden)).astype(F32)
+    mod = (r.standard_normal((6, hidden)) * 0.3).astype(F32)
+    mod0 = mod.copy()
+    mod0[[2, 5]] = 0
+    assert np.array_equal(oracle.krea_block(p, x, mod0, None, heads=heads, kv_heads=kv_heads), x)
+    only_attn = mod.copy()
+    only_attn[5] = 0
+    pz = dict(p)
+    pz["attn.to_gate.weight"] = np.zeros_like(p["attn.to_gate.weight"])
+    half = oracle.krea_block(pz, x, only_attn, None, heads=heads, kv_heads=kv_heads) - x
+    p_out = dict(pz)
+    p_out["attn.to_out.weight"] = p["attn.to_out.weight"] * F32(2.0)
+    full = oracle.krea_block(p_out, x, only_attn, None, heads=heads, kv_heads=kv_heads) - x
+    assert max_abs(2 * half, full) < 1e-5
+    assert max_abs(half, 0) > 1e-3
