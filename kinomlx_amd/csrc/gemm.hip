@@ -19,6 +19,8 @@
 // inside the mainloop; the MFMA loop is shared with the dense path.
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace kx {
@@ -470,6 +472,38 @@ __device__ __forceinline__ void dequant_store(const DqIn<QB>& in, int r, int hal
 // dequantizes stage kt+1 into one of two bf16 tiles while the MFMAs consume stage kt. TL: the
 // weights are in the tiled layout (one contiguous block per 256-row tile and stage, see
 // kx_qweight_tile_affine), else in the reference layout (one 16- or 4-byte piece per row).
+// One full-tile epilogue row piece: bias + activation (+ gated residual), then the store of 4
+// consecutive columns. Values by value so that nothing of the caller's frame is addressed.
+template <int GMODE, bool OUTF32, typename ResidT>
+__device__ __forceinline__ void epi_row4(float4 a4, ResidT res, float b0, float b1, float b2, float b3,
+                                         int act, float4 gv, char* dst) {
+  float v[4] = {a4.x + b0, a4.y + b1, a4.z + b2, a4.w + b3};
+  if (act) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = apply_act(v[e], act);
+  }
+  if constexpr (GMODE != 0) {
+    float rv[4];
+    if constexpr (GMODE == 2) {
+      rv[0] = res.x; rv[1] = res.y; rv[2] = res.z; rv[3] = res.w;
+    } else {
+      rv[0] = lo_f(res.x); rv[1] = hi_f(res.x); rv[2] = lo_f(res.y); rv[3] = hi_f(res.y);
+    }
+    v[0] = rv[0] + gv.x * v[0];
+    v[1] = rv[1] + gv.y * v[1];
+    v[2] = rv[2] + gv.z * v[2];
+    v[3] = rv[3] + gv.w * v[3];
+  }
+  if constexpr (OUTF32) {
+    *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+    uint2 o;
+    o.x = pack2(v[0], v[1]);
+    o.y = pack2(v[2], v[3]);
+    *reinterpret_cast<uint2*>(dst) = o;
+  }
+}
+
 template <int BM, int BN, int QB, bool TL, int GMODE, bool OUTF32>
 __global__ __launch_bounds__(256) void gemm_lds_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ W, int64_t ldw,
@@ -747,20 +781,50 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
   const int act = (epi.flags >> 4) & 15;
   const bool has_bias = epi.flags & KX_EPI_BIAS;
   const int mrow0 = m0 + wm * WT_M;
+  // Full tiles read the residual of all of a lane's rows of a half before any compute or store:
+  // the loads are in flight together (C may alias the residual, so loads issued after a store
+  // would wait for it), and the half's LDS staging and barrier run under their latency.
+  constexpr int NROW = WT_M / RPI_EP;  // rows per lane per half
+  static_assert(NROW * RPI_EP == WT_M, "epilogue rows");
+  // residual rows are prefetched in chunks of PF rows. 256-row tiles hold all 256 accumulator
+  // registers through the epilogue and have no room for the prefetch: they read the residual
+  // row by row (PREF false).
+  constexpr bool PREF = GMODE != 0 && BM <= 192;
+  constexpr int PF = NROW > 24 ? NROW / 2 : NROW;
+  constexpr int NCH = NROW / PF;
+  static_assert(NCH * PF == NROW && PF % 4 == 0, "epilogue chunks");
+  using ResidT = typename std::conditional<GMODE == 2, float4, uint2>::type;
+  ResidT rpre[PREF ? PF : 1];
+  const int64_t resid_es = GMODE == 2 ? 4 : 2;
+  const char* rbase = GMODE == 0 ? nullptr
+      : reinterpret_cast<const char*>(epi.resid) + ((int64_t)mrow0 * epi.ldr + n0 + wn * WT_N + 4 * q) * resid_es;
+#define KX_PREFETCH_RESID(h, c)                                                                    \
+  _Pragma("unroll") for (int k = 0; k < PF; ++k) rpre[k] = *reinterpret_cast<const ResidT*>(       \
+      rbase + ((int64_t)(rr + ((c) * PF + k) * RPI_EP) * epi.ldr + (h) * HALF_N) * resid_es);
+  if constexpr (PREF) {
+    if (full) { KX_PREFETCH_RESID(0, 0) }
+  }
   KX_BARRIER();  // every wave is done with the main loop's LDS
-#pragma unroll
+  // The half loop is not unrolled (its body is large); each half stages its accumulator blocks
+  // under its own branch so that every accumulator index stays a compile-time constant.
+#define KX_STAGE_BLOCK(ii, i)                                                                     \
+  _Pragma("unroll") for (int j = 0; j < MB; ++j)                                                  \
+  _Pragma("unroll") for (int g = 0; g < 4; ++g)                                                   \
+      *reinterpret_cast<float4*>(ep + (j * 32 + lrow) * PITCH + (ii) * 32 + 8 * g + 4 * lhalf) =  \
+          make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+#pragma unroll 1
   for (int h = 0; h < 2; ++h) {
-#pragma unroll
-    for (int ii = 0; ii < NB / 2; ++ii) {
-      const int i = h * (NB / 2) + ii;
-#pragma unroll
-      for (int j = 0; j < MB; ++j)
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-          *reinterpret_cast<float4*>(ep + (j * 32 + lrow) * PITCH + ii * 32 + 8 * g + 4 * lhalf) =
-              make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
-                          acc[i][j][4 * g + 3]);
+    if constexpr (PREF) {
+      if (h == 1 && full) { KX_PREFETCH_RESID(1, 0) }
     }
+    if (h == 0) {
+#pragma unroll
+      for (int ii = 0; ii < NB / 2; ++ii) { KX_STAGE_BLOCK(ii, ii) }
+    } else {
+#pragma unroll
+      for (int ii = 0; ii < NB / 2; ++ii) { KX_STAGE_BLOCK(ii, NB / 2 + ii) }
+    }
+#undef KX_STAGE_BLOCK
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     const int n = n0 + wn * WT_N + h * HALF_N + 4 * q;
     if (full) {
@@ -775,42 +839,47 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
       float4 g4c = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       if (GMODE != 0 && gate_const) g4c = *reinterpret_cast<const float4*>(epi.gate + (mrow0 / gdiv) * gstride + n);
       char* cbase = reinterpret_cast<char*>(C) + ((int64_t)mrow0 * ldc + n) * (OUTF32 ? 4 : 2);
-      const char* rbase = GMODE == 0 ? nullptr
-          : reinterpret_cast<const char*>(epi.resid) + ((int64_t)mrow0 * epi.ldr + n) * (GMODE == 2 ? 4 : 2);
+      if constexpr (!PREF) {
 #pragma unroll 4
-      for (int r = rr; r < WT_M; r += RPI_EP) {
-        const float4 a4 = *reinterpret_cast<const float4*>(ep + r * PITCH + 4 * q);
-        float v[4] = {a4.x + b4[0], a4.y + b4[1], a4.z + b4[2], a4.w + b4[3]};
-        if (act) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = apply_act(v[e], act);
-        }
-        if (GMODE != 0) {
+        for (int r = rr; r < WT_M; r += RPI_EP) {
+          ResidT res{};
           float4 gv = g4c;
-          if (!gate_const) {
-            const int64_t grow = gdiv == 1 ? (int64_t)(mrow0 + r) : (int64_t)(mrow0 + r) / gdiv;
-            gv = *reinterpret_cast<const float4*>(epi.gate + grow * gstride + n);
+          if constexpr (GMODE != 0) {
+            res = *reinterpret_cast<const ResidT*>(rbase + ((int64_t)r * epi.ldr + h * HALF_N) * resid_es);
+            if (!gate_const) {
+              const int64_t grow = gdiv == 1 ? (int64_t)(mrow0 + r) : (int64_t)(mrow0 + r) / gdiv;
+              gv = *reinterpret_cast<const float4*>(epi.gate + grow * gstride + n);
+            }
           }
-          float rv[4];
-          if (GMODE == 2) {
-            const float4 x = *reinterpret_cast<const float4*>(rbase + (int64_t)r * epi.ldr * 4);
-            rv[0] = x.x; rv[1] = x.y; rv[2] = x.z; rv[3] = x.w;
-          } else {
-            const uint2 x = *reinterpret_cast<const uint2*>(rbase + (int64_t)r * epi.ldr * 2);
-            rv[0] = lo_f(x.x); rv[1] = hi_f(x.x); rv[2] = lo_f(x.y); rv[3] = hi_f(x.y);
-          }
-          v[0] = rv[0] + gv.x * v[0];
-          v[1] = rv[1] + gv.y * v[1];
-          v[2] = rv[2] + gv.z * v[2];
-          v[3] = rv[3] + gv.w * v[3];
+          epi_row4<GMODE, OUTF32>(*reinterpret_cast<const float4*>(ep + r * PITCH + 4 * q), res, b4[0], b4[1],
+                                  b4[2], b4[3], act, gv, cbase + (int64_t)r * ldc * (OUTF32 ? 4 : 2));
         }
-        if (OUTF32) {
-          *reinterpret_cast<float4*>(cbase + (int64_t)r * ldc * 4) = make_float4(v[0], v[1], v[2], v[3]);
-        } else {
-          uint2 o;
-          o.x = pack2(v[0], v[1]);
-          o.y = pack2(v[2], v[3]);
-          *reinterpret_cast<uint2*>(cbase + (int64_t)r * ldc * 2) = o;
+      } else {
+        // groups of 4 rows: their staged reads together, then their stores (bounded registers:
+        // the prefetched residual stays live, the staged values of one group at a time)
+        constexpr int GR = 4;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+          if (c > 0) { KX_PREFETCH_RESID(h, c) }
+#pragma unroll
+          for (int k0 = 0; k0 < PF; k0 += GR) {
+            float4 a4[GR];
+#pragma unroll
+            for (int k = 0; k < GR; ++k)
+              a4[k] = *reinterpret_cast<const float4*>(ep + (rr + (c * PF + k0 + k) * RPI_EP) * PITCH + 4 * q);
+#pragma unroll
+            for (int k = 0; k < GR; ++k) {
+              const int r = rr + (c * PF + k0 + k) * RPI_EP;
+              float4 gv = g4c;
+              if (!gate_const) {
+                const int64_t grow = gdiv == 1 ? (int64_t)(mrow0 + r) : (int64_t)(mrow0 + r) / gdiv;
+                gv = *reinterpret_cast<const float4*>(epi.gate + grow * gstride + n);
+              }
+              epi_row4<GMODE, OUTF32>(a4[k], rpre[k0 + k], b4[0], b4[1], b4[2], b4[3], act, gv,
+                                      cbase + (int64_t)r * ldc * (OUTF32 ? 4 : 2));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          }
         }
       }
     } else {
@@ -826,6 +895,7 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   }
+#undef KX_PREFETCH_RESID
 }
 
 // ---- skinny kernel (N <= 64: the gate-logit projections) ------------------------------------
