@@ -144,6 +144,24 @@ int kx_attention_gqa_fwd_bf16(const void* q, int64_t ldq, const void* k, int64_t
                               kx_stream_t stream);
 
 /*
+ * Self-attention q_norm / k_norm + split RoPE of the same tokens in one pass: Q rows at xq / ldq
+ * and K rows at xk / ldk (column slices of one fused projection are fine), each normalized over
+ * its full width dim with its own weight (wq, wk: w_dtype, plus weight_offset), then rotated by
+ * the same split-half tables (cos / sin as kx_rmsnorm_rope_bf16 with KX_ROPE_SPLIT, 128-wide
+ * heads), written to yq / yk. Each row's arithmetic is that of kx_rmsnorm_rope_bf16; the tables
+ * are read once for both. Replaces the q_norm / k_norm + apply_rotary_emb pair of
+ * Attention.__call__ (kinomlx/models/ltx2/transformer/attention.py:353-359, rope.py:18-61) when
+ * q and k share the positional embedding. Returns KX_ERR_UNSUPPORTED (no work done) unless dim
+ * is 1024, 2048 or 4096 with 16-byte aligned rows and tables.
+ */
+int kx_qk_rmsnorm_rope_bf16(const void* xq, int64_t ldq, const void* xk, int64_t ldk, void* yq,
+                            int64_t ldyq, void* yk, int64_t ldyk, int64_t rows, int64_t dim,
+                            const void* wq, const void* wk, int w_dtype, float eps,
+                            float weight_offset, const float* cos, const float* sin,
+                            int64_t table_ld, int64_t table_hs, int64_t tokens, int table_batched,
+                            kx_stream_t stream);
+
+/*
  * Dense bf16 linear on MFMA: c = epilogue(a · wᵀ) with fp32 accumulation and one rounding.
  * Replaces mpp_linear.linear / mx.addmm(bias, x, Wᵀ) (kinomlx/kernels/mpp_linear.py:469-506,
  * kinomlx/models/ltx2/transformer/attention.py:41-109, kinomlx/modeling/layers.py).

@@ -52,6 +52,10 @@ SIGNATURES: dict[str, list] = {
         _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I, _F, _F, _I, _P, _P, _I64, _I64, _I64, _I,
         _I64, _P,
     ],
+    "kx_qk_rmsnorm_rope_bf16": [
+        _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _P, _I, _F, _F, _P, _P, _I64, _I64, _I64, _I,
+        _P,
+    ],
     "kx_rope_split_bf16": [_P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _I, _P],
     "kx_rope_pair_bf16": [_P, _I64, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64, _I, _P],
     "kx_attention_fwd_bf16": [
@@ -134,7 +138,9 @@ def set_timer(timer: LaunchTimer | None) -> None:
     _timer = timer
 
 
-def _call(name: str, *args) -> None:
+def _call(name: str, *args, unsupported_ok: bool = False) -> int:
+    """Run one entry point (timed when a LaunchTimer is set); raise on an error code, except
+    KX_ERR_UNSUPPORTED when ``unsupported_ok`` (then the code is returned and nothing ran)."""
     lib = load()
     timer = _timer
     if timer is not None:
@@ -144,9 +150,14 @@ def _call(name: str, *args) -> None:
     if timer is not None:
         end.record()
         timer.records.append((name, args, start, end))
+    if rc == KX_ERR_UNSUPPORTED and unsupported_ok:
+        if timer is not None:
+            timer.records.pop()
+        return rc
     if rc != KX_OK:
         message = lib.kx_last_error().decode(errors="replace")
         raise KernelError(f"{name} failed ({rc}): {message}")
+    return rc
 
 
 def _stream() -> int:
@@ -251,6 +262,31 @@ def launch_rmsnorm_rope(
         w_dtype, eps, weight_offset, rope_kind, _ptr(cos), _ptr(sin), table_ld, table_hs, tokens,
         int(table_batched), head_dim, _stream(),
     )
+
+
+def launch_qk_rmsnorm_rope(xq, xk, yq, yk, wq, wk, eps: float, *, cos, sin, table_ld: int, table_hs: int,
+                           tokens: int, table_batched: bool) -> bool:
+    """One pass for the Q and K rows of the same tokens; False (nothing launched) when the shape
+    or alignment is outside the fused kernel's contract."""
+    _check_gpu("qk_rmsnorm_rope", xq, xk, yq, yk, wq, wk, cos, sin)
+    rows, dim, ldq = _rows(xq, "qk_rmsnorm_rope q")
+    rows_k, dim_k, ldk = _rows(xk, "qk_rmsnorm_rope k")
+    _, _, ldyq = _rows(yq, "qk_rmsnorm_rope q out")
+    _, _, ldyk = _rows(yk, "qk_rmsnorm_rope k out")
+    if (rows_k, dim_k) != (rows, dim) or wq.dtype != wk.dtype:
+        raise ValueError("qk_rmsnorm_rope: q and k must have one shape and one weight dtype")
+    if wq.dtype == torch.bfloat16:
+        w_dtype = KX_BF16
+    elif wq.dtype == torch.float32:
+        w_dtype = KX_F32
+    else:
+        raise ValueError("rms_norm weight must be float32 or bfloat16")
+    code = _call(
+        "kx_qk_rmsnorm_rope_bf16", _ptr(xq), ldq, _ptr(xk), ldk, _ptr(yq), ldyq, _ptr(yk), ldyk, rows, dim,
+        _ptr(wq), _ptr(wk), w_dtype, eps, 0.0, _ptr(cos), _ptr(sin), table_ld, table_hs, tokens,
+        int(table_batched), _stream(), unsupported_ok=True,
+    )
+    return code == KX_OK
 
 
 def launch_rope_split(x, out, cos_tm, sin_tm, *, batch, tokens, heads, half, table_batched) -> None:

@@ -900,21 +900,22 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
 
 // ---- skinny kernel (N <= 64: the gate-logit projections) ------------------------------------
 //
-// One workgroup per 32 rows x 32 columns; its 4 waves split K into quarters and read both MFMA
-// operands straight from global memory (the weight is a few hundred KB and stays in L2, each
-// activation row is read once), then add their partial tiles through LDS. Quantized weights are
-// dequantized in registers with the arithmetic of the other kernels.
-template <int QB>
-__global__ __launch_bounds__(256) void gemm_skinny_kernel(
+// One workgroup per 32 rows x 32 columns; its NWK waves split K into NWK slices and read both
+// MFMA operands straight from global memory (the weight is a few hundred KB and stays in L2, each
+// activation row is read once), then add their partial tiles through LDS. (Splitting K over 8 or
+// 16 waves measured slower at 9216 x 32 x 4096: fewer workgroups fit a CU.)
+// Quantized weights are dequantized in registers with the arithmetic of the other kernels.
+template <int QB, int NWK>
+__global__ __launch_bounds__(NWK * 64) void gemm_skinny_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ W, int64_t ldw,
     QuantW qw, void* __restrict__ C, int64_t ldc, int M, int N, int K, Epilogue epi) {
-  __shared__ __attribute__((aligned(16))) float part[4][16][64];
+  __shared__ __attribute__((aligned(16))) float part[NWK][16][64];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lrow = lane & 31, lhalf = lane >> 5;
   const int m0 = blockIdx.x * 32, n0 = blockIdx.y * 32;
   const int m = min(m0 + lrow, M - 1), n = min(n0 + lrow, N - 1);
-  const int kq = K / 4, kbeg = wave * kq;
+  const int kq = K / NWK, kbeg = wave * kq;
   const uint16_t* arow = A + (int64_t)m * lda + 8 * lhalf;
   f32x16 acc;
 #pragma unroll
@@ -939,14 +940,15 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(
 #pragma unroll
   for (int e = 0; e < 16; ++e) part[wave][e][lane] = acc[e];
   __syncthreads();
-  // wave w finishes accumulator elements 4w .. 4w+3 (4 consecutive columns of one row)
+  if (wave >= 4) return;
+  // wave w < 4 finishes accumulator elements 4w .. 4w+3 (4 consecutive columns of one row)
   const int row = m0 + lrow;
   const int col = n0 + 8 * wave + 4 * lhalf;
-  float v[4];
+  float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-  for (int e = 0; e < 4; ++e)
-    v[e] = part[0][4 * wave + e][lane] + part[1][4 * wave + e][lane] + part[2][4 * wave + e][lane] +
-           part[3][4 * wave + e][lane];
+  for (int p = 0; p < NWK; ++p)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] += part[p][4 * wave + e][lane];
   if (row < M && col < N) {
     const bool vec_ok = (ldc % 4 == 0) && (!(epi.flags & KX_EPI_GATED_RESIDUAL) || epi.ldr % 4 == 0);
     epilogue_store4(v, row, col, N, epi, C, ldc, vec_ok);
@@ -1017,13 +1019,15 @@ int pick_lds_cfg(int64_t m, int64_t n) {
   const char* env = getenv("KX355_GEMM_LDS_TILE");
   if (env && *env) {
     const int v = atoi(env);
-    if (v >= 0 && v <= 2) return v;
+    if (v >= 0 && v <= 3) return v;
   }
-  const int64_t bm[3] = {256, 192, 128}, bn[3] = {256, 256, 128};
-  const double speed[3] = {1.0, 0.97, 0.8};
+  // tiles 256x256, 192x256, 128x128 and (for a few hundred rows, e.g. the text K/V projection)
+  // 64x128, which fills the CUs where 128x128 leaves half of them idle
+  const int64_t bm[4] = {256, 192, 128, 64}, bn[4] = {256, 256, 128, 128};
+  const double speed[4] = {1.0, 0.97, 0.8, 0.6};
   int best = 0;
   double best_cost = 0.0;
-  for (int i = 0; i < 3; ++i) {
+  for (int i = 0; i < 4; ++i) {
     const int64_t tiles = ((m + bm[i] - 1) / bm[i]) * ((n + bn[i] - 1) / bn[i]);
     const double cost = (double)((tiles + 255) / 256) * (double)(bm[i] * bn[i]) / speed[i];
     if (i == 0 || cost < best_cost) {
@@ -1042,7 +1046,7 @@ int dispatch(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, Qua
   const bool use_legacy = legacy && *legacy;
   if (n <= 64 && k % 64 == 0 && !use_legacy) {
     const dim3 grid((unsigned)((m + 31) / 32), (unsigned)((n + 31) / 32));
-    gemm_skinny_kernel<QB><<<grid, 256, 0, s>>>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi);
+    gemm_skinny_kernel<QB, 4><<<grid, 256, 0, s>>>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi);
     return KX_OK;
   }
   // the direct-to-LDS kernel keeps per-lane 32-bit byte offsets within a 256-row tile
@@ -1050,7 +1054,8 @@ int dispatch(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, Qua
     switch (pick_lds_cfg(m, n)) {
       case 0: return launch_lds<256, 256, 0>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi, s);
       case 1: return launch_lds<192, 256, 0>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi, s);
-      default: return launch_lds<128, 128, 0>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi, s);
+      case 2: return launch_lds<128, 128, 0>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi, s);
+      default: return launch_lds<64, 128, 0>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi, s);
     }
   }
   // quantized weights: the direct-to-LDS kernel with in-LDS dequantization needs whole 128-wide

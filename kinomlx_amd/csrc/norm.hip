@@ -299,6 +299,83 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_split128_kernel(
   }
 }
 
+// Q and K of the same tokens in one pass (self-attention q_norm / k_norm + split RoPE): a wave
+// handles one token's Q row and K row with their own weights and shares the token's cos / sin
+// table values between them, so the tables (as large as Q and K together at D = 4096, fp32) are
+// read once instead of twice. Per row the arithmetic is exactly rmsnorm_rope_split128_kernel's.
+template <int VPL, bool BF16W>
+__global__ __launch_bounds__(256) void qk_rmsnorm_rope_split128_kernel(
+    const uint16_t* __restrict__ xq, int64_t ldq, const uint16_t* __restrict__ xk, int64_t ldk,
+    uint16_t* __restrict__ yq, int64_t ldyq, uint16_t* __restrict__ yk, int64_t ldyk, int64_t rows,
+    const void* __restrict__ wq, const void* __restrict__ wk, float eps, float weight_offset,
+    const float* __restrict__ cosp, const float* __restrict__ sinp, int64_t table_ld,
+    int64_t table_hs, int64_t tokens, int table_batched) {
+  constexpr int DIM = VPL * 512;
+  constexpr int NP = VPL / 2;  // head-half pairs of chunks per lane
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t tok = table_batched ? row : (row % tokens);
+  uint4 qa[NP], qb[NP], ka[NP], kb[NP];
+  float c[NP][8], sn[NP][8];
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const int p = i * 64 + lane, h = p >> 3, k = p & 7;
+    const int col = h * 128 + k * 8;
+    qa[i] = *reinterpret_cast<const uint4*>(xq + row * ldq + col);
+    qb[i] = *reinterpret_cast<const uint4*>(xq + row * ldq + col + 64);
+    ka[i] = *reinterpret_cast<const uint4*>(xk + row * ldk + col);
+    kb[i] = *reinterpret_cast<const uint4*>(xk + row * ldk + col + 64);
+    const float* cr = cosp + tok * table_ld + h * table_hs + k * 8;
+    const float* sr = sinp + tok * table_ld + h * table_hs + k * 8;
+    const float4 c0 = *reinterpret_cast<const float4*>(cr), c1 = *reinterpret_cast<const float4*>(cr + 4);
+    const float4 s0 = *reinterpret_cast<const float4*>(sr), s1 = *reinterpret_cast<const float4*>(sr + 4);
+    c[i][0] = c0.x; c[i][1] = c0.y; c[i][2] = c0.z; c[i][3] = c0.w;
+    c[i][4] = c1.x; c[i][5] = c1.y; c[i][6] = c1.z; c[i][7] = c1.w;
+    sn[i][0] = s0.x; sn[i][1] = s0.y; sn[i][2] = s0.z; sn[i][3] = s0.w;
+    sn[i][4] = s1.x; sn[i][5] = s1.y; sn[i][6] = s1.z; sn[i][7] = s1.w;
+  }
+  float ssq = 0.0f, ssk = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    float a[8], b[8];
+    unpack8(qa[i], a);
+    unpack8(qb[i], b);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ssq = fmaf(b[j], b[j], fmaf(a[j], a[j], ssq));
+    unpack8(ka[i], a);
+    unpack8(kb[i], b);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ssk = fmaf(b[j], b[j], fmaf(a[j], a[j], ssk));
+  }
+  const float rq = rsqrtf(wave_sum<64>(ssq) * (1.0f / DIM) + eps);
+  const float rk = rsqrtf(wave_sum<64>(ssk) * (1.0f / DIM) + eps);
+  auto finish = [&](const uint4* xa, const uint4* xb, float r, const void* w, uint16_t* yr) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const int p = i * 64 + lane, h = p >> 3, k = p & 7;
+      const int col = h * 128 + k * 8;
+      float a[8], b[8], o0[8], o1[8];
+      unpack8(xa[i], a);
+      unpack8(xb[i], b);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+#pragma clang fp contract(off)
+        const float n0 = a[j] * r * (load_w<BF16W>(w, col + j) + weight_offset);
+        const float n1 = b[j] * r * (load_w<BF16W>(w, col + 64 + j) + weight_offset);
+        const float fc = n0 * c[i][j], ss2 = n1 * sn[i][j];  // first * c, second * s
+        const float fs = n0 * sn[i][j], sc = n1 * c[i][j];   // first * s, second * c
+        o0[j] = fc - ss2;
+        o1[j] = fs + sc;
+      }
+      *reinterpret_cast<uint4*>(yr + col) = pack8(o0);
+      *reinterpret_cast<uint4*>(yr + col + 64) = pack8(o1);
+    }
+  };
+  finish(qa, qb, rq, wq, yq + row * ldyq);
+  finish(ka, kb, rk, wk, yk + row * ldyk);
+}
+
 // One wave per norm group, any width; weighted RMSNorm only.
 template <bool BF16W>
 __global__ __launch_bounds__(256) void rmsnorm_generic(
@@ -550,6 +627,46 @@ extern "C" int kx_rmsnorm_rope_bf16(const void* x, int64_t ldx, void* y, int64_t
     rmsnorm_generic<false><<<grid, 256, 0, s>>>((const uint16_t*)x, ldx, (uint16_t*)y, ldy, rows,
                                                 dim, norm_width, w, eps, weight_offset);
   return check_launch("kx_rmsnorm_rope_bf16");
+}
+
+extern "C" int kx_qk_rmsnorm_rope_bf16(const void* xq, int64_t ldq, const void* xk, int64_t ldk,
+                                       void* yq, int64_t ldyq, void* yk, int64_t ldyk, int64_t rows,
+                                       int64_t dim, const void* wq, const void* wk, int w_dtype,
+                                       float eps, float weight_offset, const float* cos,
+                                       const float* sin, int64_t table_ld, int64_t table_hs,
+                                       int64_t tokens, int table_batched, kx_stream_t stream) {
+  KX_REQUIRE(xq && xk && yq && yk && wq && wk && cos && sin, "kx_qk_rmsnorm_rope_bf16: null tensor");
+  KX_REQUIRE(rows >= 0 && dim > 0 && ldq >= dim && ldk >= dim && ldyq >= dim && ldyk >= dim,
+             "kx_qk_rmsnorm_rope_bf16: bad shape");
+  KX_REQUIRE(w_dtype == KX_F32 || w_dtype == KX_BF16, "kx_qk_rmsnorm_rope_bf16: bad weight dtype");
+  KX_REQUIRE(table_batched || tokens > 0, "kx_qk_rmsnorm_rope_bf16: bad token count");
+  const int64_t vpl = dim / 512;
+  const bool ok = dim % 512 == 0 && (vpl == 2 || vpl == 4 || vpl == 8) && ldq % 8 == 0 && ldk % 8 == 0 &&
+                  ldyq % 8 == 0 && ldyk % 8 == 0 && aligned16(xq) && aligned16(xk) && aligned16(yq) &&
+                  aligned16(yk) && table_ld % 4 == 0 && table_hs % 4 == 0 && aligned16(cos) && aligned16(sin);
+  if (!ok)
+    return set_error(KX_ERR_UNSUPPORTED,
+                     "kx_qk_rmsnorm_rope_bf16: needs dim in {1024, 2048, 4096}, 128-wide heads and "
+                     "16-byte aligned rows and tables");
+  if (rows == 0) return KX_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)((rows + kWaves - 1) / kWaves));
+#define KX_QK(V)                                                                                  \
+  if (w_dtype == KX_BF16)                                                                         \
+    qk_rmsnorm_rope_split128_kernel<V, true><<<grid, 256, 0, s>>>(                                \
+        (const uint16_t*)xq, ldq, (const uint16_t*)xk, ldk, (uint16_t*)yq, ldyq, (uint16_t*)yk, ldyk, \
+        rows, wq, wk, eps, weight_offset, cos, sin, table_ld, table_hs, tokens, table_batched);    \
+  else                                                                                            \
+    qk_rmsnorm_rope_split128_kernel<V, false><<<grid, 256, 0, s>>>(                               \
+        (const uint16_t*)xq, ldq, (const uint16_t*)xk, ldk, (uint16_t*)yq, ldyq, (uint16_t*)yk, ldyk, \
+        rows, wq, wk, eps, weight_offset, cos, sin, table_ld, table_hs, tokens, table_batched);    \
+  return check_launch("kx_qk_rmsnorm_rope_bf16");
+  switch (vpl) {
+    case 2: KX_QK(2)
+    case 4: KX_QK(4)
+    default: KX_QK(8)
+  }
+#undef KX_QK
 }
 
 extern "C" int kx_modulate_bf16(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows,

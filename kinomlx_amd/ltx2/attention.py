@@ -9,7 +9,8 @@ Mirror of ``kinomlx/models/ltx2/transformer/attention.py`` (``Attention``, ``RMS
   ``(3 * inner, in)`` weight whose row blocks back ``to_q``/``to_k``/``to_v``), writing one
   ``(T, 3 * inner)`` buffer whose column slices feed the next kernels without copies;
 * the gate logits GEMM with ``2 * sigmoid`` in its epilogue;
-* one pass per Q and K for the weighted RMSNorm and the split RoPE (FP32 throughout);
+* one pass over Q and K together for the weighted RMSNorms and the split RoPE (FP32 throughout;
+  the fp32 RoPE tables, as large as Q and K together, are read once);
 * the flash-attention kernel with the per-head gate applied before its one rounding;
 * the output GEMM, optionally with the block's gated residual in its epilogue.
 """
@@ -97,6 +98,30 @@ def norm_rope(value: torch.Tensor, norm: RMSNorm, pe: tuple[torch.Tensor, torch.
         return out
     _lib.launch_rmsnorm_rope(value, out, norm.weight, norm.eps, 0.0, norm_width=dim)
     return split_rope.rotate(out, cos, sin)
+
+
+def norm_rope_qk(q_raw: torch.Tensor, k_raw: torch.Tensor, q_norm: RMSNorm, k_norm: RMSNorm,
+                 pe: tuple[torch.Tensor, torch.Tensor], heads: int):
+    """``(norm_rope(q), norm_rope(k))`` for Q and K of the same tokens and tables in one pass
+    (the tables are read once); None when the fused kernel does not take the shape."""
+    batch, tokens, dim = q_raw.shape
+    head_dim = dim // heads
+    cos, sin = pe
+    if (head_dim != 128 or q_norm.weight is None or k_norm.weight is None or q_norm.eps != k_norm.eps
+            or q_norm.weight.dtype != k_norm.weight.dtype or not (cos.dim() == 4 and cos.shape[1] == heads
+            and cos.shape[2] == tokens and cos.shape[3] * 2 == head_dim and cos.shape[0] in (1, batch)
+            and cos.dtype == torch.float32 and cos.shape == sin.shape)):
+        return None
+    q = torch.empty((batch, tokens, dim), dtype=q_raw.dtype, device=q_raw.device)
+    k = torch.empty_like(q)
+    if q.numel() == 0:
+        return q, k
+    cos_tm, sin_tm = split_rope.token_major(cos), split_rope.token_major(sin)
+    if not _lib.launch_qk_rmsnorm_rope(q_raw, k_raw, q, k, q_norm.weight, k_norm.weight, q_norm.eps, cos=cos_tm,
+                                       sin=sin_tm, table_ld=heads * head_dim // 2, table_hs=head_dim // 2,
+                                       tokens=tokens, table_batched=cos.shape[0] > 1):
+        return None
+    return q, k
 
 
 def dense_kernel_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, *, heads: int,
@@ -226,6 +251,10 @@ class Attention:
                 k_raw, v = kv[..., :inner], kv[..., inner:]
             else:
                 k_raw, v = self.to_k(source), self.to_v(source)
+        if pe is not None and k_pe is None and k_raw.shape == q_raw.shape:
+            qk = norm_rope_qk(q_raw, k_raw, self.q_norm, self.k_norm, pe, self.heads)
+            if qk is not None:
+                return gate, qk[0], qk[1], v
         q = norm_rope(q_raw, self.q_norm, pe, self.heads)
         k = norm_rope(k_raw, self.k_norm, pe if k_pe is None else k_pe, self.heads) if pe is not None else \
             norm_rope(k_raw, self.k_norm, None, self.heads)
@@ -258,6 +287,7 @@ __all__ = [
     "RMSNorm",
     "dense_kernel_attention",
     "norm_rope",
+    "norm_rope_qk",
     "rms_norm",
     "scaled_dot_product_attention",
 ]

@@ -115,6 +115,27 @@ def test_fused_norm_and_split_rope_matches_oracle(device, dim, heads, wdtype):
     assert dh in (64, 128)
 
 
+@pytest.mark.parametrize(("dim", "batch", "table_batch", "wdtype"),
+                         [(4096, 1, 1, torch.bfloat16), (1024, 2, 2, torch.float32), (2048, 2, 1, torch.bfloat16)])
+def test_fused_qk_norm_rope_is_bit_identical_to_two_passes(device, dim, batch, table_batch, wdtype):
+    """kx_qk_rmsnorm_rope_bf16 (Q and K rows of one fused projection, tables read once) against
+    two kx_rmsnorm_rope_bf16 passes: the same arithmetic per row, so the same bits."""
+    heads, t = dim // 128, 37
+    r = _rng(dim + batch)
+    qkv = torch.from_numpy((r.standard_normal((batch, t, 3 * dim)) * 2).astype(F32)).to(device).to(torch.bfloat16)
+    wq = torch.from_numpy((r.standard_normal(dim) * 0.05 + 1).astype(F32)).to(device).to(wdtype)
+    wk = torch.from_numpy((r.standard_normal(dim) * 0.05 + 1).astype(F32)).to(device).to(wdtype)
+    qn, kn = ltx_attention.RMSNorm(dim, weight=wq), ltx_attention.RMSNorm(dim, weight=wk)
+    ang = r.uniform(-3, 3, (table_batch, heads, t, 64)).astype(F32)
+    cos = torch.from_numpy(np.ascontiguousarray(np.cos(ang).transpose(0, 2, 1, 3))).to(device).transpose(1, 2)
+    sin = torch.from_numpy(np.ascontiguousarray(np.sin(ang).transpose(0, 2, 1, 3))).to(device).transpose(1, 2)
+    q_raw, k_raw = qkv[..., :dim], qkv[..., dim:2 * dim]
+    fused = ltx_attention.norm_rope_qk(q_raw, k_raw, qn, kn, (cos, sin), heads)
+    assert fused is not None
+    assert torch.equal(fused[0], ltx_attention.norm_rope(q_raw, qn, (cos, sin), heads))
+    assert torch.equal(fused[1], ltx_attention.norm_rope(k_raw, kn, (cos, sin), heads))
+
+
 @pytest.mark.parametrize(("norm_width", "rope_kind"), [(128, "pair"), (64, "pair"), (128, "none")])
 def test_per_head_norm_and_pair_rope_matches_oracle(device, norm_width, rope_kind):
     r = _rng(norm_width)
@@ -270,11 +291,11 @@ def test_linear_matches_oracle_for_every_tile(device, monkeypatch, tile, m, n, k
     assert _gemm_close(got_nb, oracle.linear(x, w))
 
 
-@pytest.mark.parametrize("tile", ["0", "1", "2"])
+@pytest.mark.parametrize("tile", ["0", "1", "2", "3"])
 @pytest.mark.parametrize(("m", "n", "k"), [(1056, 1040, 1024), (512, 512, 256), (300, 96, 64), (513, 520, 192), (9, 8, 64)])
 @pytest.mark.parametrize("epilogue", ["bias", "gelu_tanh", "gated_f32", "gated_bf16", "gated_f32_to_bf16", "gated_rows"])
 def test_direct_to_lds_linear_every_tile_and_epilogue(device, monkeypatch, tile, m, n, k, epilogue):
-    """The K % 32 == 0 direct-to-LDS kernel at each of its tiles (256x256, 192x256, 128x128) on
+    """The K % 32 == 0 direct-to-LDS kernel at each of its tiles (256x256, 192x256, 128x128, 64x128) on
     full tiles (the compile-time epilogue) and ragged M and N (partial tiles, clamped loads,
     masked stores) with each epilogue family: residual fp32 or bf16, output fp32 or bf16, one
     broadcast gate row or one gate row per output row."""
