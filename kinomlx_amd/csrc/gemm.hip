@@ -1061,7 +1061,9 @@ int dispatch(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, Qua
   // quantized weights: the direct-to-LDS kernel with in-LDS dequantization needs whole 128-wide
   // K blocks (scale / bias pairs of two groups), 16-byte aligned packed rows and 4-byte aligned
   // scale / bias rows; tile 2 (or a narrow N) selects the register-staged kernel
-  if (QB != 0 && k % 128 == 0 && lda <= (1 << 22) && n >= 128 && !use_legacy &&
+  // (a few hundred rows leave most CUs idle with its 192 / 256-row tiles: they take the
+  // register-staged kernel's small tiles instead)
+  if (QB != 0 && k % 128 == 0 && lda <= (1 << 22) && n >= 128 && m >= 512 && !use_legacy &&
       aligned16(qw.words) && (reinterpret_cast<uintptr_t>(qw.scales) & 3) == 0 &&
       (reinterpret_cast<uintptr_t>(qw.biases) & 3) == 0) {
     const int cfg = pick_lds_cfg(m, n);

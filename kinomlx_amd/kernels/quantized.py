@@ -202,8 +202,14 @@ class QuantizedLinear:
         self.mode = mode
         # the tiled copy the kernel reads (an input width that is a multiple of 128 on the GPU)
         self._tiled = None
+        # layers of at most 64 outputs (the gate logits) keep their weight dequantized once, by the
+        # bit-exact dequantization kernel, and run the memory-bound dense GEMV: per-lane
+        # dequantization from global memory made that GEMV latency-bound
+        self._dense = None
         k = int(weight.shape[1]) * 32 // bits
-        if weight.is_cuda and k % 128 == 0 and int(weight.shape[0]) >= 128:
+        if weight.is_cuda and int(weight.shape[0]) <= 64:
+            self._dense = dequantize(weight, scales, biases, group_size=group_size, bits=bits)
+        elif weight.is_cuda and k % 128 == 0 and int(weight.shape[0]) >= 128:
             self._tiled = tile_weights(weight, scales, biases, bits=bits, group_size=group_size)
 
     @classmethod
@@ -223,7 +229,14 @@ class QuantizedLinear:
     def __call__(self, value: torch.Tensor, *, activation: str | None = None,
                  residual: torch.Tensor | None = None, gate: torch.Tensor | None = None,
                  out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None) -> torch.Tensor:
-        if self._tiled is not None:
+        if self._dense is not None:
+            from .mpp_linear import fused_linear
+
+            bias = None if self.bias is None else self.bias.to(torch.bfloat16)
+            return fused_linear(value, self._dense, bias, activation=activation, residual=residual, gate=gate,
+                                out=out, out_dtype=out_dtype)
+        rows = value.numel() // max(int(value.shape[-1]), 1)
+        if self._tiled is not None and rows >= 512:
             n, k = self.out_features, self.in_features
             a, out, flags, bias, resid2, gate32 = _prepare_call(value, n, k, self.bias, activation, residual,
                                                                 gate, out_dtype, out)
