@@ -1,12 +1,15 @@
 // Non-causal flash attention on gfx950 MFMA for token-major flattened heads.
 //
-// One workgroup = 8 waves = 256 queries of one head; each wave owns 32 queries and keeps them in
-// registers as the MFMA B operand for the whole key loop. Waves w and w + 4 share a SIMD.
+// One workgroup = 12 waves = 384 queries of one head; each wave owns 32 queries and keeps them in
+// registers as the MFMA B operand for the whole key loop. Three waves share each SIMD (at most 168
+// VGPRs each). At 9216 tokens x 32 heads that is 768 workgroups, three full rounds of one per CU (with 8
+// waves the 1152 workgroups took 4.5 rounds: 1.59 -> 1.44 ms), and each LDS K/V tile serves 384
+// queries.
 //
 // K and V tiles of 64 keys go from global memory straight into LDS with global_load_lds_dwordx4
 // (no VGPR staging) through a ring of 4 stages: while tile i is consumed, tiles i+1 .. i+3 are in
-// flight. Each wave issues 1/8 of a stage's DMA instructions; one workgroup barrier per tile makes
-// tile i visible and frees the buffer of tile i-1 for tile i+3.
+// flight. Waves 0-7 each issue 1/8 of a stage's DMA instructions; one workgroup barrier per tile
+// makes tile i visible and frees the buffer of tile i-1 for tile i+3.
 //
 // Scores are computed transposed, S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (A = 32 keys read from
 // LDS, B = the wave's 32 queries): the accumulator lane holds one query (lane % 32) and 16 of the
@@ -32,7 +35,8 @@
 namespace kx {
 namespace {
 
-constexpr int NWAVE = 8;           // waves per workgroup
+constexpr int NWAVE = 12;          // waves per workgroup (three per SIMD)
+constexpr int NDMA = 8;            // waves that issue the K/V DMA
 constexpr int BQ = 32 * NWAVE;     // queries per workgroup
 constexpr int BKV = 64;            // keys per LDS tile
 constexpr int NSTAGE = 4;          // tiles in the LDS ring
@@ -76,8 +80,9 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
   constexpr int TILE = BKV * ROWB;        // one K (or V) tile
   constexpr int STAGE = 2 * TILE;
   constexpr int INST = 2 * BKV / RPI;     // DMA instructions per stage (K then V)
-  constexpr int PER = INST / NWAVE;       // per wave
-  static_assert(PER * NWAVE == INST, "DMA split");
+  constexpr int PER = INST / NDMA;        // per DMA wave
+  static_assert(PER * NDMA == INST, "DMA split");
+  const bool dma_wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) < NDMA;
   constexpr int QS = D / 16, DB = D / 32;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[NSTAGE * STAGE];
 
@@ -117,6 +122,7 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
     dma_col[i] = (uint32_t)((slot ^ (isv ? swz_v<D>(r) : swz_k<D>(r))) * 16);
   }
   auto issue = [&](uint8_t* buf, int j0) {
+    if (!dma_wave) return;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int key = min(j0 + dma_row[i], tk - 1);
