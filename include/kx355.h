@@ -253,6 +253,55 @@ int kx_gated_residual_bf16(const void* x, int64_t ldx, const void* r, int64_t ld
                            int64_t ldy, int64_t rows, int64_t dim, const float* gate,
                            int64_t gate_div, int64_t gate_stride, kx_stream_t stream);
 
+/* LTX split-RoPE tables: cos, sin (batch, tokens, half) fp32, token-major (the head-major
+ * (B, H, T, half/H) views precompute_freqs_cis returns share this storage). positions fp32
+ * (batch, axes, tokens, pos_stride) contiguous; with middle the position is the mean of elements
+ * 0 and 1, else element 0. With pad = half - axes * n, columns j < pad hold (1, 0) and column
+ * pad + f * axes + a the angle ((p / max_pos[a]) * 2 - 1) * grid[f], grid (n,) fp32 from
+ * _frequency_grid. precompute_freqs_cis (kinomlx/models/ltx2/transformer/rope.py:95-176). */
+int kx_ltx_rope_tables(const float* positions, int64_t pos_stride, int middle, const float* max_pos,
+                       const float* grid, float* cos, float* sin, int64_t batch, int64_t axes,
+                       int64_t tokens, int64_t n, int64_t half, kx_stream_t stream);
+
+/* ---- the steps either side of the blocks (element-wise, contiguous tensors) ------------------ */
+
+/* Sinusoidal timestep features, out (n, dim) in out_dtype (KX_F32 or KX_BF16): with half = dim/2,
+ * s_i = t[i] * time_scale and f_j = exp((neg_log_period * j) / half) in fp32, out[i, j] =
+ * cos(s_i f_j) for j < half, sin(s_i f_(j-half)) for j < 2 half, 0 in a last odd column;
+ * neg_log_period = -ln(max_period). get_timestep_embedding
+ * (kinomlx/models/ltx2/transformer/timestep.py:13-28) of the preprocessor's scaled timesteps
+ * (preprocessing.py:66-75, time_scale 1 for the plain function); the bf16 output is its
+ * `.astype(hidden_dtype)` in TimestepEmbedding (timestep.py:40-41). */
+int kx_timestep_embedding(const float* t, void* out, int64_t n, int64_t dim, int out_dtype,
+                          float time_scale, float neg_log_period, kx_stream_t stream);
+
+/* out = sample + dtype(delta * velocity), fp32 multiply, sample and velocity of one dtype:
+ * euler_velocity_step (kinomlx/samplers/steps.py:8-32), delta = sigma_next - sigma. */
+int kx_euler_velocity_step(const void* sample, const void* velocity, void* out, int64_t n,
+                           int dtype, float delta, kx_stream_t stream);
+
+/* out = denoised + ratio * (sample - denoised) in fp32, rounded once to sample_dtype:
+ * euler_step (kinomlx/samplers/steps.py:35-72), ratio = sigma_next / sigma. */
+int kx_euler_step(const void* sample, int sample_dtype, const void* denoised, int denoised_dtype,
+                  void* out, int64_t n, float ratio, kx_stream_t stream);
+
+/* X0 conversion: out[r, c] = latent[r, c] - timesteps[r / ts_div] * velocity[r, c] in fp32,
+ * rounded once to latent_dtype; (rows, dim) = (B*T, C), ts_div = T for per-batch timesteps, 1 for
+ * per-token ones. _to_denoised (kinomlx/models/ltx2/transformer/wrappers.py:48-66). */
+int kx_to_denoised(const void* latent, int latent_dtype, const void* velocity, int velocity_dtype,
+                   const float* timesteps, void* out, int64_t rows, int64_t dim, int64_t ts_div,
+                   kx_stream_t stream);
+
+/* Conditioning composite: out[r, c] = denoised[r, c] * mask[r] + clean[r, c] * (1 - mask[r]) in
+ * fp32, rounded once to denoised_dtype: post_process_latent (kinomlx/models/ltx2/state.py:70-83). */
+int kx_mask_composite(const void* denoised, int denoised_dtype, const void* clean, int clean_dtype,
+                      const float* mask, void* out, int64_t rows, int64_t dim, kx_stream_t stream);
+
+/* *flag = 1 if every one of the n elements of x is finite, else 0 (flag: one device int, written
+ * on the stream; x may be NULL when n == 0): the per-step check mx.all(mx.isfinite(latent))
+ * (kinomlx/models/ltx2/denoise.py:244-258). */
+int kx_all_finite(const void* x, int64_t n, int dtype, int* flag, kx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -81,6 +81,13 @@ SIGNATURES: dict[str, list] = {
     "kx_swiglu_bf16": [_P, _I64, _P, _I64, _I64, _I64, _P],
     "kx_modulate_bf16": [_P, _I64, _P, _I64, _I64, _I64, _P, _P, _I64, _I64, _P],
     "kx_gated_residual_bf16": [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _P],
+    "kx_timestep_embedding": [_P, _P, _I64, _I64, _I, _F, _F, _P],
+    "kx_ltx_rope_tables": [_P, _I64, _I, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P],
+    "kx_euler_velocity_step": [_P, _P, _P, _I64, _I, _F, _P],
+    "kx_euler_step": [_P, _I, _P, _I, _P, _I64, _F, _P],
+    "kx_to_denoised": [_P, _I, _P, _I, _P, _P, _I64, _I64, _I64, _P],
+    "kx_mask_composite": [_P, _I, _P, _I, _P, _P, _I64, _I64, _P],
+    "kx_all_finite": [_P, _I64, _I, _P, _P],
 }
 
 _lib: ctypes.CDLL | None = None
@@ -451,3 +458,83 @@ def launch_gated_residual(x, r, out, gate) -> None:
         "kx_gated_residual_bf16", _ptr(x), ldx, _ptr(r), ldr, _ptr(out), ldy, rows, dim, _ptr(gate),
         div, stride, _stream(),
     )
+
+
+def _dtype_code(t, name: str) -> int:
+    if t.dtype == torch.float32:
+        return KX_F32
+    if t.dtype == torch.bfloat16:
+        return KX_BF16
+    raise ValueError(f"{name}: tensors must be bfloat16 or float32, got {t.dtype}")
+
+
+def _dense(name: str, *tensors) -> None:
+    _check_gpu(name, *tensors)
+    for t in tensors:
+        if t is not None and not t.is_contiguous():
+            raise ValueError(f"{name}: tensors must be contiguous")
+
+
+def launch_timestep_embedding(t, out, neg_log_period: float, time_scale: float = 1.0) -> None:
+    """out (n, dim) fp32 or bf16 <- sinusoidal features of the fp32 timesteps t (n,) * time_scale."""
+    _dense("timestep_embedding", t, out)
+    if t.dtype != torch.float32 or t.dim() != 1 or out.dim() != 2 or out.shape[0] != t.shape[0]:
+        raise ValueError("timestep_embedding: t must be fp32 (n,) and out (n, dim)")
+    _call("kx_timestep_embedding", _ptr(t), _ptr(out), t.shape[0], out.shape[1],
+          _dtype_code(out, "timestep_embedding"), time_scale, neg_log_period, _stream())
+
+
+def launch_ltx_rope_tables(positions, max_pos, grid, cos, sin, *, middle: bool) -> None:
+    """cos, sin (B, T, half) fp32 <- LTX split-RoPE angles of fp32 positions (B, axes, T[, 2])."""
+    _dense("ltx_rope_tables", positions, max_pos, grid, cos, sin)
+    if any(t.dtype != torch.float32 for t in (positions, max_pos, grid, cos, sin)):
+        raise ValueError("ltx_rope_tables: every tensor is float32")
+    batch, axes, tokens = (int(s) for s in positions.shape[:3])
+    stride = int(positions.shape[3]) if positions.dim() == 4 else 1
+    half = int(cos.shape[-1])
+    if cos.shape != (batch, tokens, half) or sin.shape != cos.shape or max_pos.numel() != axes:
+        raise ValueError("ltx_rope_tables: table or max_pos shape does not match the positions")
+    _call("kx_ltx_rope_tables", _ptr(positions), stride, int(middle), _ptr(max_pos), _ptr(grid), _ptr(cos),
+          _ptr(sin), batch, axes, tokens, grid.numel(), half, _stream())
+
+
+def launch_euler_velocity_step(sample, velocity, out, delta: float) -> None:
+    _dense("euler_velocity_step", sample, velocity, out)
+    if not (sample.shape == velocity.shape == out.shape) or not (sample.dtype == velocity.dtype == out.dtype):
+        raise ValueError("euler_velocity_step: sample, velocity and out must share shape and dtype")
+    _call("kx_euler_velocity_step", _ptr(sample), _ptr(velocity), _ptr(out), sample.numel(),
+          _dtype_code(sample, "euler_velocity_step"), delta, _stream())
+
+
+def launch_euler_step(sample, denoised, out, ratio: float) -> None:
+    _dense("euler_step", sample, denoised, out)
+    if not (sample.shape == denoised.shape == out.shape) or out.dtype != sample.dtype:
+        raise ValueError("euler_step: shapes must match and out must have the sample dtype")
+    _call("kx_euler_step", _ptr(sample), _dtype_code(sample, "euler_step"), _ptr(denoised),
+          _dtype_code(denoised, "euler_step"), _ptr(out), sample.numel(), ratio, _stream())
+
+
+def launch_to_denoised(latent, velocity, timesteps, out, *, rows: int, dim: int, ts_div: int) -> None:
+    _dense("to_denoised", latent, velocity, timesteps, out)
+    if timesteps.dtype != torch.float32 or latent.numel() != rows * dim or velocity.numel() != rows * dim \
+            or out.numel() != rows * dim or out.dtype != latent.dtype or timesteps.numel() * ts_div != rows:
+        raise ValueError("to_denoised: shapes or dtypes do not match")
+    _call("kx_to_denoised", _ptr(latent), _dtype_code(latent, "to_denoised"), _ptr(velocity),
+          _dtype_code(velocity, "to_denoised"), _ptr(timesteps), _ptr(out), rows, dim, ts_div, _stream())
+
+
+def launch_mask_composite(denoised, clean, mask, out, *, rows: int, dim: int) -> None:
+    _dense("mask_composite", denoised, clean, mask, out)
+    if mask.dtype != torch.float32 or mask.numel() != rows or denoised.numel() != rows * dim \
+            or clean.numel() != rows * dim or out.numel() != rows * dim or out.dtype != denoised.dtype:
+        raise ValueError("mask_composite: shapes or dtypes do not match")
+    _call("kx_mask_composite", _ptr(denoised), _dtype_code(denoised, "mask_composite"), _ptr(clean),
+          _dtype_code(clean, "mask_composite"), _ptr(mask), _ptr(out), rows, dim, _stream())
+
+
+def launch_all_finite(x, flag) -> None:
+    """flag (one int32 on the device) <- 1 when every element of x is finite, else 0."""
+    _dense("all_finite", x, flag)
+    if flag.dtype != torch.int32 or flag.numel() < 1:
+        raise ValueError("all_finite: flag must be an int32 device tensor")
+    _call("kx_all_finite", _ptr(x), x.numel(), _dtype_code(x, "all_finite"), _ptr(flag), _stream())

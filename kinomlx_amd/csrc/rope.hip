@@ -100,6 +100,35 @@ __global__ __launch_bounds__(256) void rope_pair_scalar(
   y[row * ldy + off + 1] = f2bf(a1 + b1);
 }
 
+// LTX split-RoPE tables (kinomlx/models/ltx2/transformer/rope.py:95-176): for token t of batch b
+// and table column j < half, with pad = half - axes * n leading columns of (cos 1, sin 0), column
+// pad + f * axes + a holds the angle ((p / max_pos[a]) * 2 - 1) * grid[f] of axis a, where p is
+// the position (the mean of the two bounds with `middle`). Every step is one fp32 op rounded on
+// its own, as the reference's array ops are.
+__global__ __launch_bounds__(256) void ltx_rope_tables_kernel(
+    const float* __restrict__ pos, int64_t pstride, int middle, const float* __restrict__ max_pos,
+    const float* __restrict__ grid, float* __restrict__ cos_out, float* __restrict__ sin_out,
+    int64_t total, int64_t tokens, int axes, int n, int half) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int64_t bt = idx / half;
+  const int j = (int)(idx - bt * half);
+  const int pad = half - axes * n;
+  float c = 1.0f, s = 0.0f;
+  if (j >= pad) {
+    const int jj = j - pad;
+    const int f = jj / axes, a = jj - f * axes;
+    const int64_t b = bt / tokens, t = bt - b * tokens;
+    const float* p = pos + ((b * axes + a) * tokens + t) * pstride;
+    const float v = middle ? (p[0] + p[1]) / 2.0f : p[0];
+    const float frac = v / max_pos[a];
+    const float scaled = frac * 2.0f - 1.0f;
+    sincosf(scaled * grid[f], &s, &c);
+  }
+  cos_out[idx] = c;
+  sin_out[idx] = s;
+}
+
 }  // namespace
 }  // namespace kx
 
@@ -146,4 +175,23 @@ extern "C" int kx_rope_pair_bf16(const void* x, int64_t ldx, void* y, int64_t ld
       (const uint16_t*)x, ldx, (uint16_t*)y, ldy, rows, (int)heads, (int)head_dim, cos, sin,
       table_ld, table_hs, tokens, table_batched);
   return check_launch("kx_rope_pair_bf16");
+}
+
+extern "C" int kx_ltx_rope_tables(const float* positions, int64_t pos_stride, int middle,
+                                  const float* max_pos, const float* grid, float* cos, float* sin,
+                                  int64_t batch, int64_t axes, int64_t tokens, int64_t n,
+                                  int64_t half, kx_stream_t stream) {
+  KX_REQUIRE(positions && max_pos && grid && cos && sin, "kx_ltx_rope_tables: null tensor");
+  KX_REQUIRE(batch >= 0 && tokens >= 0 && axes > 0 && axes <= 16 && n > 0 && half > 0 &&
+                 axes * n <= half && half < (1 << 24),
+             "kx_ltx_rope_tables: bad shape (axes=%lld n=%lld half=%lld)", (long long)axes,
+             (long long)n, (long long)half);
+  KX_REQUIRE(pos_stride >= (middle ? 2 : 1), "kx_ltx_rope_tables: bad position stride");
+  const int64_t total = batch * tokens * half;
+  KX_REQUIRE(total / 256 < (1ll << 31), "kx_ltx_rope_tables: too many elements");
+  if (total == 0) return KX_OK;
+  ltx_rope_tables_kernel<<<(unsigned)((total + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+      positions, pos_stride, middle, max_pos, grid, cos, sin, total, tokens, (int)axes, (int)n,
+      (int)half);
+  return check_launch("kx_ltx_rope_tables");
 }

@@ -1,0 +1,100 @@
+"""One LTX-2 denoising step on MI355X: the X0 transformer call, the Euler update and the finite
+check.
+
+Mirror of the deterministic-Euler path of ``kinomlx/models/ltx2/denoise.py``
+(``LTX2DenoiseError`` ``:11-12``, ``_advance_sample`` ``:60-85``, ``_advance_state``
+``:100-120``, ``modality_from_state`` ``:123-156``, ``denoise_step`` ``:159-258``) for the video
+stream. The finite check is one reduction kernel over the new latent; its one-int flag is the
+step's only device-to-host read, as ``mx.stack([...]).tolist()`` is the reference's.
+"""
+
+from __future__ import annotations
+
+from dataclasses import replace
+from typing import Literal
+
+import torch
+
+from .. import _lib
+from ..samplers.steps import euler_step
+from .state import LatentState, post_process_latent
+from .wrappers import Modality
+
+DenoiseStepKind = Literal["deterministic-euler", "ancestral-rf"]
+
+
+class LTX2DenoiseError(RuntimeError):
+    """A completed denoise step produced nonfinite active latents."""
+
+
+def all_finite(value: torch.Tensor) -> bool:
+    """``mx.all(mx.isfinite(value))`` through the finite-check kernel (one host read)."""
+    flag = torch.empty(1, dtype=torch.int32, device=value.device)
+    _lib.launch_all_finite(value.contiguous(), flag)
+    return bool(flag.item())
+
+
+def modality_from_state(state: LatentState, context: torch.Tensor, sigma: float, *, enabled: bool = True,
+                        context_mask: torch.Tensor | None = None, keyframes_mask: torch.Tensor | None = None,
+                        sparse_attention: object | None = None) -> Modality:
+    """Scalar-timestep fast path: ``(B,)`` timesteps of ``sigma`` for a uniform mask, else
+    ``mask * sigma`` per token (``denoise.py:123-156``)."""
+    sigma_tensor = torch.full((state.latent.shape[0],), sigma, dtype=torch.float32, device=state.latent.device)
+    if state.uniform_mask:
+        timesteps = sigma_tensor
+    else:
+        mask = state.denoise_mask
+        if mask.dim() == 3 and mask.shape[-1] == 1:
+            mask = mask[..., 0]
+        timesteps = mask.float() * sigma
+    return Modality(latent=state.latent, context=context, timesteps=timesteps, sigma=sigma_tensor,
+                    positions=state.positions, enabled=enabled, context_mask=context_mask,
+                    keyframes_mask=keyframes_mask, sparse_attention=sparse_attention)
+
+
+def _advance_sample(sample: torch.Tensor, denoised: torch.Tensor, *, sigma: float, sigma_next: float,
+                    step_kind: DenoiseStepKind, noise: torch.Tensor | None) -> torch.Tensor:
+    if step_kind == "deterministic-euler":
+        if noise is not None:
+            raise ValueError("deterministic Euler must not receive transition noise")
+        return euler_step(sample, denoised, sigma, sigma_next)
+    if step_kind == "ancestral-rf":
+        raise ValueError("the ancestral RF step is not built for MI355X")
+    raise ValueError(f"unknown denoise step kind {step_kind!r}")
+
+
+def denoise_step(video_state: LatentState, audio_state: LatentState | None = None, *, sigma: float,
+                 sigma_next: float, transformer, video_context: torch.Tensor,
+                 audio_context: torch.Tensor | None = None, video_context_mask: torch.Tensor | None = None,
+                 video_keyframes_mask: torch.Tensor | None = None, video_enabled: bool = True,
+                 step_kind: DenoiseStepKind = "deterministic-euler", video_noise: torch.Tensor | None = None,
+                 video_sparse_attention: object | None = None) -> tuple[LatentState, LatentState | None]:
+    """Run one X0 transformer call and the Euler update of the video stream, then check the
+    new latent is finite (``denoise.py:159-258``). ``transformer`` is an ``X0Model``."""
+    if audio_state is not None or audio_context is not None:
+        raise ValueError("the audio stream is not built for MI355X")
+    video_modality = modality_from_state(video_state, video_context, sigma, enabled=video_enabled,
+                                         context_mask=video_context_mask, keyframes_mask=video_keyframes_mask,
+                                         sparse_attention=video_sparse_attention)
+    video_denoised, _ = transformer(video_modality, None)
+    if video_enabled:
+        if video_denoised is None:
+            raise RuntimeError("transformer returned no video prediction")
+        prediction = post_process_latent(video_denoised, video_state)
+        latent = _advance_sample(video_state.latent, prediction, sigma=sigma, sigma_next=sigma_next,
+                                 step_kind=step_kind, noise=video_noise)
+        video_state = replace(video_state, latent=latent)
+        if not all_finite(video_state.latent):
+            raise LTX2DenoiseError(
+                f"LTX-2 denoising produced a nonfinite video latent in {video_state.latent.dtype}."
+            )
+    return video_state, None
+
+
+__all__ = [
+    "DenoiseStepKind",
+    "LTX2DenoiseError",
+    "all_finite",
+    "denoise_step",
+    "modality_from_state",
+]

@@ -2,7 +2,7 @@
 
 Mirror of ``kinomlx/models/ltx2/transformer/rope.py``: ``LTXRopeType``,
 ``apply_split_rotary_emb``, ``apply_rotary_emb``, ``precompute_freqs_cis``. Tables are built on
-the positions' device in FP32 token-major storage and returned as head-major
+the GPU by one HIP kernel in FP32 token-major storage and returned as head-major
 ``(B, H, T, dim / (2H))`` views, the layout the split-RoPE kernel reads without a copy.
 """
 
@@ -14,6 +14,7 @@ from functools import lru_cache
 
 import torch
 
+from .. import _lib
 from ..kernels import split_rope
 
 
@@ -62,21 +63,18 @@ def _frequency_grid(theta: float, position_dims: int, inner_dim: int, double_pre
     return tuple(math.pow(theta, e) * math.pi / 2 for e in exponents)
 
 
-def _fractional_positions(positions: torch.Tensor, max_pos: tuple[int, ...], *,
-                          use_middle_indices_grid: bool) -> torch.Tensor:
-    """``(B, axes, T[, 2])`` positions -> ``(B, T, axes)`` FP32 fractions (``rope.py:95-112``)."""
+def _position_tensor(positions: torch.Tensor, max_pos: tuple[int, ...], *,
+                     use_middle_indices_grid: bool) -> tuple[torch.Tensor, bool]:
+    """fp32 contiguous positions for the table kernel and whether it averages the two bounds
+    (the argument checks of ``_fractional_positions``, ``rope.py:95-112``)."""
     if positions.shape[1] != len(max_pos):
         raise ValueError("position axes must match max_pos")
     if use_middle_indices_grid:
         if positions.dim() != 4 or positions.shape[-1] != 2:
             raise ValueError("middle-position RoPE expects (B, axes, T, 2) bounds")
-        positions = (positions[..., 0].float() + positions[..., 1].float()) / 2.0
-    elif positions.dim() == 4:
-        positions = positions[..., 0]
-    elif positions.dim() != 3:
+    elif positions.dim() not in (3, 4):
         raise ValueError("RoPE positions must have three or four dimensions")
-    scale = torch.tensor(max_pos, dtype=torch.float32, device=positions.device)[None, :, None]
-    return (positions.float() / scale).transpose(1, 2)
+    return positions.float().contiguous(), use_middle_indices_grid
 
 
 def precompute_freqs_cis(
@@ -91,31 +89,30 @@ def precompute_freqs_cis(
     rope_type: LTXRopeType = LTXRopeType.SPLIT,
     use_double_precision: bool = False,
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """Split-RoPE cosine/sine tables for one token grid (``rope.py:115-176``)."""
+    """Split-RoPE cosine/sine tables for one token grid (``rope.py:115-176``), built by one HIP
+    kernel: ``(B, H, T, dim / 2H)`` head-major views of token-major ``(B, T, dim / 2)`` fp32
+    storage (the layout the norm + RoPE kernels read)."""
     if rope_type is not LTXRopeType.SPLIT:
         raise ValueError(f"unsupported RoPE type: {rope_type}")
     if dim % num_attention_heads:
         raise ValueError("RoPE dimension must divide evenly across attention heads")
     resolved = tuple(max_pos)
-    fractional = _fractional_positions(indices_grid, resolved, use_middle_indices_grid=use_middle_indices_grid)
-    grid = torch.tensor(
-        _frequency_grid(theta, indices_grid.shape[1], dim, use_double_precision),
-        dtype=torch.float32, device=indices_grid.device,
-    )
-    scaled = fractional * 2.0 - 1.0
-    frequencies = scaled[..., None] * grid[None, None, None, :]  # (B, T, axes, n)
-    batch, tokens = frequencies.shape[0], frequencies.shape[1]
-    frequencies = frequencies.transpose(2, 3).reshape(batch, tokens, -1)
-    padding = dim // 2 - frequencies.shape[-1]
-    if padding < 0:
+    positions, middle = _position_tensor(indices_grid, resolved, use_middle_indices_grid=use_middle_indices_grid)
+    grid_values = _frequency_grid(theta, indices_grid.shape[1], dim, use_double_precision)
+    half = dim // 2
+    if half < len(grid_values) * len(resolved):
         raise ValueError("RoPE frequency grid exceeds half the model dimension")
-    cos = torch.cos(frequencies)
-    sin = torch.sin(frequencies)
-    if padding:
-        cos = torch.cat([torch.ones((batch, tokens, padding), dtype=cos.dtype, device=cos.device), cos], dim=-1)
-        sin = torch.cat([torch.zeros((batch, tokens, padding), dtype=sin.dtype, device=sin.device), sin], dim=-1)
-    cos = cos.reshape(batch, tokens, num_attention_heads, -1).to(out_dtype).contiguous()
-    sin = sin.reshape(batch, tokens, num_attention_heads, -1).to(out_dtype).contiguous()
+    device = positions.device
+    grid = torch.tensor(grid_values, dtype=torch.float32, device=device)
+    scale = torch.tensor(resolved, dtype=torch.float32, device=device)
+    batch, tokens = int(positions.shape[0]), int(positions.shape[2])
+    cos = torch.empty((batch, tokens, half), dtype=torch.float32, device=device)
+    sin = torch.empty_like(cos)
+    _lib.launch_ltx_rope_tables(positions, scale, grid, cos, sin, middle=middle)
+    if out_dtype != torch.float32:
+        cos, sin = cos.to(out_dtype), sin.to(out_dtype)
+    cos = cos.view(batch, tokens, num_attention_heads, -1)
+    sin = sin.view(batch, tokens, num_attention_heads, -1)
     return cos.transpose(1, 2), sin.transpose(1, 2)
 
 

@@ -187,6 +187,65 @@ def build_ltx_block(spec: LTXSpec, p: dict[str, torch.Tensor], device, *, fuse: 
     return block
 
 
+def ltx_model_params(spec: LTXSpec, num_blocks: int, *, in_channels: int = 128, out_channels: int = 128,
+                     seed: int = 0) -> dict:
+    """Dense bf16 parameters of an LTX video transformer: ``blocks`` (one ``ltx_params`` dict per
+    block, without the per-step ``timesteps``), ``patchify_proj``, ``adaln_single`` (9 rows),
+    ``prompt_adaln_single`` (2 rows), the output ``scale_shift_table`` ``(2, D)`` and ``proj_out``.
+    Weights N(0, 0.02), biases N(0, 0.02), tables N(0, 0.02)."""
+    d = spec.dim
+    p: dict = {"blocks": []}
+    for index in range(num_blocks):
+        block = ltx_params(spec, seed * 1000 + index)
+        block.pop("timesteps")
+        p["blocks"].append(block)
+
+    def lin(name: str, n: int, k: int) -> None:
+        p[f"{name}.weight"] = bf16(normal(seed, f"model.{name}.weight", (n, k), 0.02))
+        p[f"{name}.bias"] = bf16(normal(seed, f"model.{name}.bias", (n,), 0.02))
+
+    lin("patchify_proj", d, in_channels)
+    for prefix, rows in (("adaln_single", 9), ("prompt_adaln_single", 2)):
+        lin(f"{prefix}.emb.timestep_embedder.linear_1", d, 256)
+        lin(f"{prefix}.emb.timestep_embedder.linear_2", d, d)
+        lin(f"{prefix}.linear", rows * d, d)
+    p["scale_shift_table"] = bf16(normal(seed, "model.scale_shift_table", (2, d), 0.02))
+    lin("proj_out", out_channels, d)
+    return p
+
+
+def ltx_model_inputs(spec: LTXSpec, *, in_channels: int = 128, seed: int = 0) -> dict[str, torch.Tensor]:
+    """Latent ``(1, T, C)`` N(0, 1) bf16, context ``(1, Tc, D)`` bf16 and RoPE positions."""
+    return {
+        "latent": bf16(normal(seed, "latent", (1, spec.tokens, in_channels))),
+        "context": bf16(normal(seed, "context", (1, spec.text_tokens, spec.dim))),
+        "positions": ltx_positions(spec.grid),
+    }
+
+
+def _assign_adaln(adaln, p: dict, prefix: str, device) -> None:
+    embedder = adaln.emb.timestep_embedder
+    embedder.linear_1 = _layer(p, f"{prefix}.emb.timestep_embedder.linear_1", device)
+    embedder.linear_2 = _layer(p, f"{prefix}.emb.timestep_embedder.linear_2", device)
+    adaln.linear = _layer(p, f"{prefix}.linear", device)
+
+
+def build_ltx_model(spec: LTXSpec, p: dict, device, *, in_channels: int = 128, out_channels: int = 128,
+                    fuse: bool = True):
+    """The MI355X ``LTXAVModel`` (video stream) holding ``p``'s weights on ``device``."""
+    from .ltx2.model import LTXAVModel
+
+    model = LTXAVModel(num_layers=len(p["blocks"]), video_heads=spec.heads, video_head_dim=spec.head_dim,
+                       video_in_channels=in_channels, video_out_channels=out_channels, video_context_dim=spec.dim)
+    model.transformer_blocks = [build_ltx_block(spec, block, device, fuse=fuse) for block in p["blocks"]]
+    model.patchify_proj = _layer(p, "patchify_proj", device)
+    _assign_adaln(model.adaln_single, p, "adaln_single", device)
+    _assign_adaln(model.prompt_adaln_single, p, "prompt_adaln_single", device)
+    model.scale_shift_table = p["scale_shift_table"].to(device)
+    model.proj_out = _layer(p, "proj_out", device)
+    return model
+
+
 # ---- FLUX.2 / config 1 ---------------------------------------------------------------------------
 
 
@@ -345,12 +404,15 @@ __all__ = [
     "build_flux_double_block",
     "build_flux_single_block",
     "build_ltx_block",
+    "build_ltx_model",
     "flux_tables",
     "flop_count",
     "flux_inputs",
     "flux_params",
     "flux_rope",
     "ltx_inputs",
+    "ltx_model_inputs",
+    "ltx_model_params",
     "ltx_params",
     "ltx_positions",
     "normal",

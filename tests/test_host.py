@@ -88,15 +88,12 @@ def test_product_quantizer_is_bit_identical_to_the_oracle(bits):
     assert np.array_equal(quantized.unpack(words, bits).numpy(), oracle.unpack_affine(o_words, bits).astype(np.int64))
 
 
-def test_product_rope_tables_match_the_oracle():
+def test_product_rope_tables_take_gpu_tensors_only():
+    """The tables come from a HIP kernel: CPU positions are refused, not computed on the host."""
     pos = workloads.ltx_positions((3, 4, 5))
-    cos, sin = rope.precompute_freqs_cis(pos, dim=1024, max_pos=(20, 2048, 2048), use_middle_indices_grid=True,
-                                         num_attention_heads=8)
-    o_cos, o_sin = oracle.precompute_freqs_cis(pos.numpy(), dim=1024, max_pos=(20, 2048, 2048),
-                                               use_middle_indices_grid=True, num_attention_heads=8)
-    assert cos.shape == (1, 8, 60, 64)
-    assert cos.transpose(1, 2).is_contiguous()  # token-major storage, head-major view
-    assert np.allclose(cos.numpy(), o_cos, atol=1e-6) and np.allclose(sin.numpy(), o_sin, atol=1e-6)
+    with pytest.raises(ValueError, match="GPU tensors"):
+        rope.precompute_freqs_cis(pos, dim=1024, max_pos=(20, 2048, 2048), use_middle_indices_grid=True,
+                                  num_attention_heads=8)
 
 
 def test_workload_flops_match_baseline():
