@@ -12,6 +12,11 @@ over synthetic seeded inputs already resident in HBM. Prints ONE JSON line:
   cpu_baseline the FP32 numpy restatement of the config-1 block timed on this host's cores
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3|4|5] [--no-cpu-baseline]
+
+With --denoise-step the step is instead one whole LTX-2 video denoising step (patchify, the
+timestep / AdaLN producers, the RoPE tables, --blocks blocks, the output head, the X0
+conversion, the Euler update and the finite check) at the config's shape, or at --grid T,H,W
+latent tokens; value is then milliseconds per denoising step.
 """
 
 from __future__ import annotations
@@ -100,6 +105,10 @@ def main() -> int:
     parser.add_argument("--config", type=int, default=3, choices=(3, 4, 5))
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--breakdown", action="store_true", help="print the per-kernel table to stderr")
+    parser.add_argument("--denoise-step", action="store_true",
+                        help="time one whole denoising step of the video transformer instead of one block")
+    parser.add_argument("--blocks", type=int, default=48, help="blocks of the --denoise-step transformer")
+    parser.add_argument("--grid", type=str, default="", help="T,H,W latent grid for --denoise-step")
     parser.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                         help="only run 5 device-to-device copies of MIB MiB (the known-size kernel that "
                              "scales the FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -117,6 +126,8 @@ def main() -> int:
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
         return 2
+    if args.denoise_step:
+        return denoise_main(args)
 
     import torch
 
@@ -244,6 +255,99 @@ def main() -> int:
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result))
+    return 0
+
+
+def denoise_main(args) -> int:
+    """One LTX-2 video denoising step: ``denoise_step`` over ``X0Model(LTXAVModel)``."""
+    import dataclasses
+
+    import torch
+
+    from kinomlx_amd import _lib, workloads
+    from kinomlx_amd.ltx2.denoise import denoise_step
+    from kinomlx_amd.ltx2.state import LatentState
+    from kinomlx_amd.ltx2.wrappers import X0Model
+
+    device = torch.device("cuda:0")
+    spec = workloads.CONFIGS[args.config]
+    if args.grid:
+        spec = dataclasses.replace(spec, grid=tuple(int(v) for v in args.grid.split(",")))
+    build0 = time.perf_counter()
+    model = X0Model(workloads.random_ltx_model(spec, args.blocks, device))
+    torch.cuda.synchronize()
+    build_s = time.perf_counter() - build0
+    gen = torch.Generator(device=device).manual_seed(1)
+    latent = torch.randn((1, spec.tokens, 128), generator=gen, device=device).to(torch.bfloat16)
+    context = torch.randn((1, spec.text_tokens, spec.dim), generator=gen, device=device).to(torch.bfloat16)
+    positions = workloads.ltx_positions(spec.grid).to(device)
+    state = LatentState(latent=latent, denoise_mask=torch.ones((1, spec.tokens, 1), device=device),
+                        positions=positions, clean_latent=latent)
+    sigmas = (0.909375, 0.725, 0.421875)
+
+    def step(s):
+        return denoise_step(s, sigma=sigmas[0], sigma_next=sigmas[1], transformer=model, video_context=context)[0]
+
+    for _ in range(args.warmup):
+        step(state)
+    timer = _lib.LaunchTimer()
+    _lib.set_timer(timer)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    for _ in range(args.steps):
+        out = step(state)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    _lib.set_timer(None)
+    ms_per_step = wall * 1e3 / args.steps
+
+    per_kernel: dict[str, list[float]] = defaultdict(list)
+    name_of: dict[str, str] = {}
+    for name, cargs, ms in timer.durations_ms():
+        label = _kernel_label(name, cargs)
+        per_kernel[label].append(ms)
+        name_of[label] = name
+    kernel_ms = {k: sum(v) / args.steps for k, v in per_kernel.items()}
+    block_flops = workloads.flop_count(spec)["total"] * args.blocks
+    attn_ms = sum(v for k, v in kernel_ms.items() if name_of[k] == "kx_attention_fwd_bf16")
+    gemm_ms = sum(v for k, v in kernel_ms.items() if name_of[k].startswith(("kx_gemm", "kx_qgemm")))
+    outside = ("kx_timestep_embedding", "kx_ltx_rope_tables", "kx_to_denoised", "kx_euler_step", "kx_all_finite",
+               "kx_mask_composite", "kx_silu_bf16")
+    if args.breakdown:
+        for label, ms in sorted(kernel_ms.items(), key=lambda kv: -kv[1]):
+            print(f"{ms:9.3f} ms/step  x{len(per_kernel[label]) // args.steps}  {label}", file=sys.stderr)
+    result = {
+        "metric": "LTX-2 video denoising step ms (X0 transformer + Euler update + finite check)",
+        "value": round(ms_per_step, 2),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 2),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (N(0,0.02) weights drawn on the device, N(0,1) latent and context; no checkpoint)",
+        "config": {
+            "workload": f"LTX2-like video transformer, {args.blocks} blocks, BASELINE config {args.config} block shape",
+            "video_tokens": spec.tokens,
+            "latent_grid_thw": list(spec.grid),
+            "text_tokens": spec.text_tokens,
+            "dim": spec.dim,
+            "latent_channels": 128,
+            "weights": f"int{spec.bits} affine g{spec.group_size}" if spec.bits else "bf16",
+            "batch": 1,
+        },
+        "block_tflops": round(block_flops / (ms_per_step * 1e-3) / 1e12, 1),
+        "attention_ms": round(attn_ms, 2),
+        "gemm_ms": round(gemm_ms, 2),
+        "outside_block_kernels_ms": round(sum(v for k, v in kernel_ms.items() if name_of[k] in outside), 3),
+        "kernel_sum_ms": round(sum(kernel_ms.values()), 2),
+        "build_s": round(build_s, 1),
+        "finite": bool(torch.isfinite(out.latent.float()).all()),
+    }
     print(json.dumps(result))
     return 0
 

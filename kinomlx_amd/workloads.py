@@ -235,7 +235,7 @@ def build_ltx_model(spec: LTXSpec, p: dict, device, *, in_channels: int = 128, o
     """The MI355X ``LTXAVModel`` (video stream) holding ``p``'s weights on ``device``."""
     from .ltx2.model import LTXAVModel
 
-    model = LTXAVModel(num_layers=len(p["blocks"]), video_heads=spec.heads, video_head_dim=spec.head_dim,
+    model = LTXAVModel(num_layers=max(1, len(p["blocks"])), video_heads=spec.heads, video_head_dim=spec.head_dim,
                        video_in_channels=in_channels, video_out_channels=out_channels, video_context_dim=spec.dim)
     model.transformer_blocks = [build_ltx_block(spec, block, device, fuse=fuse) for block in p["blocks"]]
     model.patchify_proj = _layer(p, "patchify_proj", device)
@@ -243,6 +243,55 @@ def build_ltx_model(spec: LTXSpec, p: dict, device, *, in_channels: int = 128, o
     _assign_adaln(model.prompt_adaln_single, p, "prompt_adaln_single", device)
     model.scale_shift_table = p["scale_shift_table"].to(device)
     model.proj_out = _layer(p, "proj_out", device)
+    return model
+
+
+def random_ltx_model(spec: LTXSpec, num_blocks: int, device, *, in_channels: int = 128, out_channels: int = 128,
+                     seed: int = 0):
+    """An ``LTXAVModel`` of ``num_blocks`` blocks with N(0, 0.02) weights drawn directly on
+    ``device`` (one seeded device generator; for timing runs, where host-side generation of
+    tens of GB of weights would dominate). Every block has its own weights; with ``spec.bits``
+    the block linears are quantized on the device into the packed affine layout."""
+    gen = torch.Generator(device=device).manual_seed(seed)
+
+    def rnd(shape, std=0.02, mean=0.0):
+        return torch.randn(tuple(shape), generator=gen, device=device, dtype=torch.float32) * std + mean
+
+    d, f = spec.dim, spec.dim * spec.ff_mult
+    blocks = []
+    for _ in range(num_blocks):
+        p: dict[str, torch.Tensor] = {}
+        for prefix in ("attn1", "attn2"):
+            for name in ("to_q", "to_k", "to_v", "to_out"):
+                p[f"{prefix}.{name}.weight"] = bf16(rnd((d, d)))
+                p[f"{prefix}.{name}.bias"] = bf16(rnd((d,)))
+            p[f"{prefix}.to_gate_logits.weight"] = bf16(rnd((spec.heads, d)))
+            p[f"{prefix}.to_gate_logits.bias"] = bf16(rnd((spec.heads,)))
+            for name in ("q_norm", "k_norm"):
+                p[f"{prefix}.{name}.weight"] = bf16(rnd((d,), 0.02, 1.0))
+        p["ff.proj_in.weight"], p["ff.proj_in.bias"] = bf16(rnd((f, d))), bf16(rnd((f,)))
+        p["ff.proj_out.weight"], p["ff.proj_out.bias"] = bf16(rnd((d, f))), bf16(rnd((d,)))
+        p["scale_shift_table"] = rnd((9, d))
+        p["prompt_scale_shift_table"] = rnd((2, d))
+        if spec.bits:
+            p = quantize_ltx_params(p, spec.bits, spec.group_size)
+        blocks.append(build_ltx_block(spec, p, device))
+        del p
+    top: dict[str, torch.Tensor] = {}
+
+    def lin(name: str, n: int, k: int) -> None:
+        top[f"{name}.weight"], top[f"{name}.bias"] = bf16(rnd((n, k))), bf16(rnd((n,)))
+
+    lin("patchify_proj", d, in_channels)
+    for prefix, rows in (("adaln_single", 9), ("prompt_adaln_single", 2)):
+        lin(f"{prefix}.emb.timestep_embedder.linear_1", d, 256)
+        lin(f"{prefix}.emb.timestep_embedder.linear_2", d, d)
+        lin(f"{prefix}.linear", rows * d, d)
+    top["scale_shift_table"] = bf16(rnd((2, d)))
+    lin("proj_out", out_channels, d)
+    top["blocks"] = []
+    model = build_ltx_model(spec, top, device, in_channels=in_channels, out_channels=out_channels)
+    model.transformer_blocks = blocks
     return model
 
 
@@ -417,4 +466,5 @@ __all__ = [
     "ltx_positions",
     "normal",
     "quantize_ltx_params",
+    "random_ltx_model",
 ]
