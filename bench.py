@@ -109,6 +109,8 @@ def main() -> int:
                         help="time one whole denoising step of the video transformer instead of one block")
     parser.add_argument("--blocks", type=int, default=48, help="blocks of the --denoise-step transformer")
     parser.add_argument("--grid", type=str, default="", help="T,H,W latent grid for --denoise-step")
+    parser.add_argument("--load-checkpoint", action="store_true",
+                        help="time loading a --blocks-block checkpoint into HBM, plain and quantized on load")
     parser.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                         help="only run 5 device-to-device copies of MIB MiB (the known-size kernel that "
                              "scales the FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -128,6 +130,8 @@ def main() -> int:
         return 2
     if args.denoise_step:
         return denoise_main(args)
+    if args.load_checkpoint:
+        return load_main(args)
 
     import torch
 
@@ -255,6 +259,103 @@ def main() -> int:
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result))
+    return 0
+
+
+def load_main(args) -> int:
+    """Checkpoint -> HBM: the staged safetensors loader and quantize-on-load, on a synthetic
+    reference-named checkpoint written to a temporary directory (so read from the page cache:
+    this times the host-memory -> HBM path, not a disk)."""
+    import tempfile
+    from pathlib import Path
+
+    import torch
+    from safetensors.torch import save_file
+
+    from kinomlx_amd import _lib, workloads
+    from kinomlx_amd.io import inspect_safetensors, load_to_device
+    from kinomlx_amd.ltx2.weights import load_transformer
+
+    device = torch.device("cuda:0")
+    spec = workloads.CONFIGS[3]
+    model = workloads.random_ltx_model(spec, args.blocks, device, seed=3)
+    tensors = {}
+    for i, block in enumerate(model.transformer_blocks):
+        pre = f"model.diffusion_model.transformer_blocks.{i}"
+        for a in ("attn1", "attn2"):
+            attn = getattr(block, a)
+            for n in ("to_q", "to_k", "to_v", "to_out", "to_gate_logits"):
+                layer = getattr(attn, n)
+                src = f"{pre}.{a}.{n}" + (".0" if n == "to_out" else "")
+                tensors[f"{src}.weight"] = layer.weight.cpu().contiguous()
+                tensors[f"{src}.bias"] = layer.bias.cpu()
+            tensors[f"{pre}.{a}.q_norm.weight"] = attn.q_norm.weight.cpu()
+            tensors[f"{pre}.{a}.k_norm.weight"] = attn.k_norm.weight.cpu()
+        for src, layer in ((f"{pre}.ff.net.0.proj", block.ff.project_in.proj), (f"{pre}.ff.net.2", block.ff.project_out)):
+            tensors[f"{src}.weight"] = layer.weight.cpu().contiguous()
+            tensors[f"{src}.bias"] = layer.bias.cpu()
+        tensors[f"{pre}.scale_shift_table"] = block.scale_shift_table.cpu()
+        tensors[f"{pre}.prompt_scale_shift_table"] = block.prompt_scale_shift_table.cpu()
+    top = {"patchify_proj": model.patchify_proj, "proj_out": model.proj_out,
+           "adaln_single.linear": model.adaln_single.linear,
+           "prompt_adaln_single.linear": model.prompt_adaln_single.linear}
+    for prefix in ("adaln_single", "prompt_adaln_single"):
+        emb = getattr(model, prefix).emb.timestep_embedder
+        top[f"{prefix}.emb.timestep_embedder.linear_1"] = emb.linear_1
+        top[f"{prefix}.emb.timestep_embedder.linear_2"] = emb.linear_2
+    for name, layer in top.items():
+        tensors[f"model.diffusion_model.{name}.weight"] = layer.weight.cpu().contiguous()
+        tensors[f"model.diffusion_model.{name}.bias"] = layer.bias.cpu()
+    tensors["model.diffusion_model.scale_shift_table"] = model.scale_shift_table.cpu()
+    del model
+    torch.cuda.empty_cache()
+    with tempfile.TemporaryDirectory(dir="/tmp") as tmp:
+        path = Path(tmp) / "ltx.safetensors"
+        save_file(tensors, str(path))
+        del tensors
+        payload = inspect_safetensors(path).payload_bytes
+        load_to_device(path, device)  # warm the page cache and the allocator
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        loaded = load_to_device(path, device)
+        torch.cuda.synchronize()
+        raw_s = time.perf_counter() - t0
+        del loaded
+        torch.cuda.empty_cache()
+        t0 = time.perf_counter()
+        plain = load_transformer(path, device)
+        torch.cuda.synchronize()
+        plain_s = time.perf_counter() - t0
+        del plain
+        torch.cuda.empty_cache()
+        timer = _lib.LaunchTimer()
+        _lib.set_timer(timer)
+        t0 = time.perf_counter()
+        quant = load_transformer(path, device, quantize_bits=4)
+        torch.cuda.synchronize()
+        quant_s = time.perf_counter() - t0
+        _lib.set_timer(None)
+        del quant
+    q = [(cargs, ms) for name, cargs, ms in timer.durations_ms() if name == "kx_quantize_affine_bf16"]
+    q_bytes = sum(c[5] * c[6] * 2 + c[5] * c[6] * 4 // 8 + 4 * c[5] * c[6] // 64 for c, _ in q)
+    q_ms = sum(ms for _, ms in q)
+    result = {
+        "metric": "LTX-2 checkpoint -> HBM load GB/s (safetensors, page-cached) and quantize-on-load GB/s",
+        "value": round(payload / raw_s / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "higher_is_better": True,
+        "dtype": "bf16 -> int4 g64",
+        "data": "synthetic reference-named checkpoint (N(0,0.02) weights), written to /tmp then read back",
+        "config": {"workload": f"LTX2-like video transformer, {args.blocks} blocks, config-3 block shape",
+                   "payload_bytes": payload},
+        "load_to_device_s": round(raw_s, 3),
+        "load_transformer_bf16_s": round(plain_s, 3),
+        "load_transformer_int4_s": round(quant_s, 3),
+        "quantize_kernel": {"launches": len(q), "ms": round(q_ms, 3),
+                            "hbm_gbs": round(q_bytes / (q_ms * 1e-3) / 1e9, 1) if q_ms else None},
+    }
     print(json.dumps(result))
     return 0
 

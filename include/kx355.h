@@ -202,6 +202,19 @@ int kx_dequant_affine_bf16(const uint32_t* wq, const void* scales, const void* b
                            int64_t n, int64_t k, int group_size, int bits, kx_stream_t stream);
 
 /*
+ * Quantize-on-load: bf16 weight w (n, k) at row stride ldw -> the packed affine format above
+ * (wq (n, k * bits / 32) uint32, scales / biases (n, k / 64) bf16). Per group of 64 along K:
+ * scale = bf16((max - min) / (2^bits - 1)) (1 when not positive), bias = bf16(min),
+ * code = clamp(rint((w - bias) / scale), 0, 2^bits - 1) in fp32. Replaces the mx.quantize call
+ * of the weight preparation (kinomlx/models/ltx2/preparation.py:139-157, affine mode, defaults
+ * kinomlx/models/ltx2/weights/tensors.py:185-203); the scale/bias choice is this build's own
+ * (MLX's quantizer is not part of the reference tree). Requires k % 64 == 0, ldw % 8 == 0 and a
+ * 16-byte aligned w; group_size 64, bits 4 or 8.
+ */
+int kx_quantize_affine_bf16(const void* w, int64_t ldw, uint32_t* wq, void* scales, void* biases,
+                            int64_t n, int64_t k, int group_size, int bits, kx_stream_t stream);
+
+/*
  * Load-time layout for kx_qgemm_affine_tiled_bf16 (no counterpart in the reference: its
  * quantized weights stay in the packed layout above; this is the same data regrouped so that
  * each 256-row weight tile and 32-wide K stage is one contiguous block). With npad = n rounded

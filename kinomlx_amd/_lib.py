@@ -72,6 +72,7 @@ SIGNATURES: dict[str, list] = {
         _I64, _P,
     ],
     "kx_dequant_affine_bf16": [_P, _P, _P, _P, _I64, _I64, _I, _I, _P],
+    "kx_quantize_affine_bf16": [_P, _I64, _P, _P, _P, _I64, _I64, _I, _I, _P],
     "kx_qweight_tile_affine": [_P, _P, _P, _P, _P, _I64, _I64, _I, _I, _P],
     "kx_qgemm_affine_tiled_bf16": [
         _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I, _P, _I64, _P, _I64, _I64, _P,
@@ -538,3 +539,15 @@ def launch_all_finite(x, flag) -> None:
     if flag.dtype != torch.int32 or flag.numel() < 1:
         raise ValueError("all_finite: flag must be an int32 device tensor")
     _call("kx_all_finite", _ptr(x), x.numel(), _dtype_code(x, "all_finite"), _ptr(flag), _stream())
+
+
+def launch_quantize(w, words, scales, biases, *, group_size: int, bits: int) -> None:
+    """Packed affine (words, scales, biases) <- bf16 weight w (n, k) with contiguous rows."""
+    _check_gpu("quantize_affine", w, words, scales, biases)
+    n, k = (int(v) for v in w.shape)
+    if w.dtype != torch.bfloat16 or w.stride(-1) != 1:
+        raise ValueError("quantize_affine: the weight must be bfloat16 with contiguous rows")
+    if words.shape != (n, k * bits // 32) or scales.shape != (n, k // group_size) or biases.shape != scales.shape:
+        raise ValueError("quantize_affine: output shapes do not match the weight")
+    _call("kx_quantize_affine_bf16", _ptr(w), w.stride(0), _ptr(words), _ptr(scales), _ptr(biases), n, k,
+          group_size, bits, _stream())

@@ -1,0 +1,106 @@
+// Quantize-on-load: a bf16 (out, in) weight -> the packed group-wise affine format the quantized
+// GEMMs read (uint32 words holding 32 / bits codes each, lowest bits first; one bf16 scale and
+// bias per group of 64 along K).
+//
+// Per group: lo, hi = min, max (exact in fp32); scale = bf16((hi - lo) / (2^bits - 1)), 1 when
+// that is not positive; bias = bf16(lo); code = clamp(rint((w - bias) / scale), 0, 2^bits - 1)
+// with the fp32 subtraction and correctly rounded division. The dequantized weight is then
+// bf16(scale * code + bias) (kx_dequant_affine_bf16). HBM-bound: one read of the weight, an
+// eighth (int4) or a quarter (int8) of it written back.
+#include <math.h>
+
+#include "common.h"
+
+namespace kx {
+namespace {
+
+constexpr int QGROUP = 64;
+
+// Eight lanes per (row, group): lane `sub` holds values 8 sub .. 8 sub + 7 (one 16-byte load), so a
+// wave reads eight whole groups = 1 KB of contiguous weight per load; min / max are reduced over
+// the eight lanes with three xor shuffles. Each lane packs its own eight codes: one word (int4) or
+// two (int8), written contiguously across the group's lanes.
+template <int BITS>
+__global__ __launch_bounds__(256) void quantize_affine_kernel(const uint16_t* __restrict__ w, int64_t ldw,
+                                                              uint32_t* __restrict__ words,
+                                                              uint16_t* __restrict__ scales,
+                                                              uint16_t* __restrict__ biases, int64_t groups,
+                                                              int64_t groups_per_row) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t g = t >> 3;
+  const int sub = (int)(t & 7);
+  // the grid covers whole groups (8 lanes each) and every lane of a partial last wave is out of
+  // range together, so the shuffles below only ever read lanes of the same group
+  if (g >= groups) return;
+  const int64_t row = g / groups_per_row, col = g - row * groups_per_row;
+  float v[8];
+  unpack8(*reinterpret_cast<const uint4*>(w + row * ldw + col * QGROUP + sub * 8), v);
+  float lo = v[0], hi = v[0];
+#pragma unroll
+  for (int i = 1; i < 8; ++i) {
+    lo = fminf(lo, v[i]);
+    hi = fmaxf(hi, v[i]);
+  }
+#pragma unroll
+  for (int o = 1; o < 8; o <<= 1) {
+    lo = fminf(lo, __shfl_xor(lo, o, 8));
+    hi = fmaxf(hi, __shfl_xor(hi, o, 8));
+  }
+  constexpr int LEVELS = (1 << BITS) - 1;
+  float scale = (hi - lo) / (float)LEVELS;
+  if (!(scale > 0.0f)) scale = 1.0f;
+  uint16_t scale_bits = f2bf(scale);
+  float s = bf2f(scale_bits);
+  if (!(s > 0.0f)) {
+    scale_bits = f2bf(1.0f);
+    s = 1.0f;
+  }
+  const uint16_t bias_bits = f2bf(lo);
+  const float b = bf2f(bias_bits);
+  uint32_t code[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) code[i] = (uint32_t)fminf(fmaxf(rintf((v[i] - b) / s), 0.0f), (float)LEVELS);
+  if constexpr (BITS == 4) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) word |= code[i] << (4 * i);
+    words[g * 8 + sub] = word;
+  } else {
+    uint2 pair;
+    pair.x = code[0] | (code[1] << 8) | (code[2] << 16) | (code[3] << 24);
+    pair.y = code[4] | (code[5] << 8) | (code[6] << 16) | (code[7] << 24);
+    reinterpret_cast<uint2*>(words)[g * 8 + sub] = pair;
+  }
+  if (sub == 0) {
+    scales[g] = scale_bits;
+    biases[g] = bias_bits;
+  }
+}
+
+}  // namespace
+}  // namespace kx
+
+using namespace kx;
+
+extern "C" int kx_quantize_affine_bf16(const void* w, int64_t ldw, uint32_t* wq, void* scales, void* biases,
+                                       int64_t n, int64_t k, int group_size, int bits, kx_stream_t stream) {
+  KX_REQUIRE(w && wq && scales && biases, "kx_quantize_affine_bf16: null tensor");
+  KX_REQUIRE(bits == 4 || bits == 8, "kx_quantize_affine_bf16: bits must be 4 or 8, got %d", bits);
+  KX_REQUIRE(group_size == QGROUP, "kx_quantize_affine_bf16: group_size must be 64, got %d", group_size);
+  KX_REQUIRE(n >= 0 && k > 0 && k % QGROUP == 0 && ldw >= k && ldw % 8 == 0 && aligned16(w),
+             "kx_quantize_affine_bf16: bad shape (n=%lld k=%lld ldw=%lld; k %% 64 == 0, 16-byte rows)",
+             (long long)n, (long long)k, (long long)ldw);
+  KX_REQUIRE(aligned8(wq), "kx_quantize_affine_bf16: wq must be 8-byte aligned");
+  const int64_t groups = n * (k / QGROUP);
+  KX_REQUIRE(groups * 8 / 256 < (1ll << 31), "kx_quantize_affine_bf16: too many groups");
+  if (groups == 0) return KX_OK;
+  const unsigned grid = (unsigned)((groups * 8 + 255) / 256);
+  hipStream_t s = (hipStream_t)stream;
+  if (bits == 4)
+    quantize_affine_kernel<4><<<grid, 256, 0, s>>>((const uint16_t*)w, ldw, wq, (uint16_t*)scales,
+                                                   (uint16_t*)biases, groups, k / QGROUP);
+  else
+    quantize_affine_kernel<8><<<grid, 256, 0, s>>>((const uint16_t*)w, ldw, wq, (uint16_t*)scales,
+                                                   (uint16_t*)biases, groups, k / QGROUP);
+  return check_launch("kx_quantize_affine_bf16");
+}

@@ -70,13 +70,30 @@ def unpack(words: torch.Tensor, bits: int) -> torch.Tensor:
 
 def quantize(weight: torch.Tensor, group_size: int = DEFAULT_GROUP_SIZE, bits: int = DEFAULT_BITS,
              mode: str = "affine") -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """``(out, in)`` weight -> ``(words, scales, biases)`` in the packed affine format."""
+    """``(out, in)`` weight -> ``(words, scales, biases)`` in the packed affine format.
+
+    On the GPU this is the quantize-on-load kernel (``kx_quantize_affine_bf16``) on the bf16
+    weight. A weight still in host memory (a checkpoint prepared on a machine without a GPU,
+    synthetic test weights) is packed by the same arithmetic in torch on the host: the two are
+    bit-identical on bf16 weights (tested). The kernel reads bf16: a GPU weight in another dtype
+    is cast to bf16 first, as the reference casts to the transformer dtype before quantizing
+    (``preparation.py:146-147``)."""
     quant_defaults(mode, group_size, bits)
     _check_format(group_size, bits)
-    w = weight.float()
-    n, k = w.shape
+    n, k = (int(v) for v in weight.shape)
     if k % group_size:
         raise ValueError("the input width must be a multiple of the group size")
+    if weight.is_cuda:
+        w = weight.to(torch.bfloat16)
+        if w.stride(-1) != 1 or w.stride(0) % 8 or w.data_ptr() % 16:
+            w = w.contiguous()
+        words = torch.empty((n, k * bits // 32), dtype=torch.int32, device=w.device)
+        scales = torch.empty((n, k // group_size), dtype=torch.bfloat16, device=w.device)
+        biases = torch.empty_like(scales)
+        if n:
+            _lib.launch_quantize(w, words, scales, biases, group_size=group_size, bits=bits)
+        return words, scales, biases
+    w = weight.float()
     levels = (1 << bits) - 1
     groups = w.reshape(n, k // group_size, group_size)
     lo = groups.amin(dim=-1)

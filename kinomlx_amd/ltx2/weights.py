@@ -1,0 +1,201 @@
+"""LTX-2 transformer checkpoints on MI355X: source-key conversion, loading into HBM and
+quantize-on-load.
+
+Mirror of ``convert_checkpoint_key`` and its tables (``kinomlx/models/ltx2/transformer/graph.py:
+84-115,322-359``) and of the quantize step of the weight preparation (``kinomlx/models/ltx2/
+preparation.py:139-157``: ``mx.quantize(w, group_size, bits, mode="affine")`` on the block
+linears). The tensors move from the file to HBM through ``kinomlx_amd.io.load_to_device``; the
+quantization is the ``kx_quantize_affine_bf16`` kernel on the resident bf16 weight, followed by
+the quantized GEMM's one-time tiled layout.
+"""
+
+from __future__ import annotations
+
+import re
+from dataclasses import dataclass
+from pathlib import Path
+
+import torch
+
+from ..io.safetensors import inspect_safetensors, load_to_device
+from ..kernels.quantized import QuantizedLinear, quantize
+from .attention import Linear
+from .model import LTXAVModel
+
+DIFFUSION_PREFIX = "model.diffusion_model."
+_DIFFUSION_PREFIXES = (DIFFUSION_PREFIX, "diffusion_model.", "")
+_TRANSFORMER_ROOTS = (
+    "adaln_single.",
+    "audio_adaln_single.",
+    "audio_patchify_proj.",
+    "audio_proj_out.",
+    "audio_prompt_adaln_single.",
+    "audio_scale_shift_table",
+    "av_ca_a2v_gate_adaln_single.",
+    "av_ca_audio_scale_shift_adaln_single.",
+    "av_ca_v2a_gate_adaln_single.",
+    "av_ca_video_scale_shift_adaln_single.",
+    "keyframes_abs_pos_embedding",
+    "norm_out.",
+    "audio_norm_out.",
+    "patchify_proj.",
+    "proj_out.",
+    "prompt_adaln_single.",
+    "scale_shift_table",
+    "transformer_blocks.",
+)
+_VIDEO_ONLY_SKIP_FRAGMENTS = ("av_ca", "a2v", "audio")
+_REPLACEMENTS = (
+    (re.compile(r"\.to_out\.0\."), ".to_out."),
+    (re.compile(r"(^|\.)ff\.net\.0\.proj\."), r"\1ff.project_in.proj."),
+    (re.compile(r"(^|\.)ff\.net\.2\."), r"\1ff.project_out."),
+    (re.compile(r"(^|\.)audio_ff\.net\.0\.proj\."), r"\1audio_ff.project_in.proj."),
+    (re.compile(r"(^|\.)audio_ff\.net\.2\."), r"\1audio_ff.project_out."),
+)
+
+# the block linears the reference quantizes (attention projections and the feed-forward)
+QUANTIZED_LINEARS = tuple(
+    f"{a}.{n}" for a in ("attn1", "attn2") for n in ("to_q", "to_k", "to_v", "to_out", "to_gate_logits")
+) + ("ff.project_in.proj", "ff.project_out")
+
+
+@dataclass(frozen=True)
+class ConvertedTransformerKey:
+    """One normalized source key and its alias priority (lower wins)."""
+
+    target_key: str
+    priority: int
+
+
+def _strip_source_wrapper(key: str) -> tuple[str, int] | None:
+    for priority, prefix in enumerate(_DIFFUSION_PREFIXES[:-1]):
+        if key.startswith(prefix):
+            return key[len(prefix):], priority
+    for offset, prefix in enumerate(_DIFFUSION_PREFIXES[:-1], start=3):
+        position = key.find("." + prefix)
+        if position >= 0:
+            return key[position + 1 + len(prefix):], offset
+    if key.startswith(_TRANSFORMER_ROOTS):
+        return key, 2
+    for root in _TRANSFORMER_ROOTS:
+        position = key.find("." + root)
+        if position >= 0:
+            return key[position + 1:], 6
+    return None
+
+
+def convert_checkpoint_key(checkpoint_key: str, *, include_audio: bool = False) -> ConvertedTransformerKey | None:
+    """Source key -> model key, or None for keys outside the (video) transformer
+    (``graph.py:341-359``)."""
+    stripped = _strip_source_wrapper(checkpoint_key)
+    if stripped is None:
+        return None
+    logical, priority = stripped
+    if "embeddings_connector." in logical:
+        return None
+    if not include_audio and any(fragment in logical.lower() for fragment in _VIDEO_ONLY_SKIP_FRAGMENTS):
+        return None
+    for pattern, replacement in _REPLACEMENTS:
+        logical = pattern.sub(replacement, logical)
+    return ConvertedTransformerKey(logical, priority)
+
+
+def checkpoint_bindings(path: Path | str) -> dict[str, str]:
+    """Model key -> source key for every transformer tensor of the file; where several source
+    keys alias one model key, the lowest priority wins (ties are an error)."""
+    chosen: dict[str, tuple[int, str]] = {}
+    for name in inspect_safetensors(path).tensor_names:
+        converted = convert_checkpoint_key(name)
+        if converted is None:
+            continue
+        previous = chosen.get(converted.target_key)
+        if previous is not None and previous[0] == converted.priority:
+            raise ValueError(f"{path}: {previous[1]!r} and {name!r} both map to {converted.target_key!r}")
+        if previous is None or converted.priority < previous[0]:
+            chosen[converted.target_key] = (converted.priority, name)
+    return {target: source for target, (_, source) in chosen.items()}
+
+
+def _bf16(t: torch.Tensor) -> torch.Tensor:
+    return t if t.dtype == torch.bfloat16 else t.to(torch.bfloat16)
+
+
+def load_transformer(path: Path | str, device, *, heads: int = 32, head_dim: int = 128,
+                     quantize_bits: int | None = None, group_size: int = 64, fuse: bool = True,
+                     strict: bool = True) -> LTXAVModel:
+    """Build the video ``LTXAVModel`` from a safetensors checkpoint with its tensors in HBM.
+
+    Linear weights and biases are held in bf16 and the modulation tables in fp32. With
+    ``quantize_bits`` (4 or 8) every block linear of ``QUANTIZED_LINEARS`` is quantized on the
+    device into the group-``group_size`` affine format and its bf16 weight released. With
+    ``strict``, a transformer tensor the model has no place for is an error."""
+    bindings = checkpoint_bindings(path)
+    tensors = load_to_device(path, device, names=bindings.values())
+    params = {target: tensors.pop(source) for target, source in bindings.items()}
+    used: set[str] = set()
+
+    def take(key: str) -> torch.Tensor:
+        if key not in params:
+            raise KeyError(f"{path}: checkpoint has no tensor for {key!r}")
+        used.add(key)
+        return params[key]
+
+    def linear(prefix: str, quantized: bool = False):
+        weight = _bf16(take(f"{prefix}.weight"))
+        bias = _bf16(take(f"{prefix}.bias")) if f"{prefix}.bias" in params else None
+        if quantized and quantize_bits:
+            words, scales, biases = quantize(weight, group_size, quantize_bits)
+            params[f"{prefix}.weight"] = None
+            return QuantizedLinear(words, scales, biases, bias, group_size=group_size, bits=quantize_bits)
+        return Linear(weight, bias)
+
+    layers = sorted({int(k.split(".")[1]) for k in params if k.startswith("transformer_blocks.")})
+    if layers != list(range(len(layers))) or not layers:
+        raise ValueError(f"{path}: transformer blocks must be numbered 0..n-1, found {layers[:8]}...")
+    patchify = take("patchify_proj.weight")
+    proj_out = take("proj_out.weight")
+    dim = int(patchify.shape[0])
+    if dim != heads * head_dim:
+        raise ValueError(f"{path}: hidden size {dim} does not match {heads} heads x {head_dim}")
+    model = LTXAVModel(num_layers=len(layers), video_heads=heads, video_head_dim=head_dim,
+                       video_in_channels=int(patchify.shape[1]), video_out_channels=int(proj_out.shape[0]),
+                       video_context_dim=dim, use_prompt_adaln_single="prompt_adaln_single.linear.weight" in params)
+    model.patchify_proj = linear("patchify_proj")
+    model.proj_out = linear("proj_out")
+    model.scale_shift_table = take("scale_shift_table")
+    adalns = [("adaln_single", model.adaln_single)]
+    if model.prompt_adaln_single is not None:
+        adalns.append(("prompt_adaln_single", model.prompt_adaln_single))
+    for prefix, adaln in adalns:
+        embedder = adaln.emb.timestep_embedder
+        embedder.linear_1 = linear(f"{prefix}.emb.timestep_embedder.linear_1")
+        embedder.linear_2 = linear(f"{prefix}.emb.timestep_embedder.linear_2")
+        adaln.linear = linear(f"{prefix}.linear")
+    for index, block in zip(layers, model.transformer_blocks):
+        prefix = f"transformer_blocks.{index}"
+        for name in ("attn1", "attn2"):
+            attn = getattr(block, name)
+            for proj in ("to_q", "to_k", "to_v", "to_out", "to_gate_logits"):
+                setattr(attn, proj, linear(f"{prefix}.{name}.{proj}", quantized=True))
+            attn.q_norm.weight = take(f"{prefix}.{name}.q_norm.weight")
+            attn.k_norm.weight = take(f"{prefix}.{name}.k_norm.weight")
+        block.ff.project_in.proj = linear(f"{prefix}.ff.project_in.proj", quantized=True)
+        block.ff.project_out = linear(f"{prefix}.ff.project_out", quantized=True)
+        block.scale_shift_table = take(f"{prefix}.scale_shift_table").float()
+        block.prompt_scale_shift_table = take(f"{prefix}.prompt_scale_shift_table").float()
+        if fuse:
+            block.fuse_projections()
+    unused = sorted(set(params) - used)
+    if strict and unused:
+        raise ValueError(f"{path}: transformer tensors with no place in the video model: {unused[:6]}")
+    return model
+
+
+__all__ = [
+    "DIFFUSION_PREFIX",
+    "QUANTIZED_LINEARS",
+    "ConvertedTransformerKey",
+    "checkpoint_bindings",
+    "convert_checkpoint_key",
+    "load_transformer",
+]
