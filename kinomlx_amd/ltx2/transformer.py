@@ -142,9 +142,16 @@ class TransformerArgs:
 
 
 class BasicAVTransformerBlock:
-    """One LTX-2 block, video branch (``transformer.py:85-421``). Weights are assigned after
+    """One LTX-2 block (``transformer.py:85-421``): the video stream, and with ``audio_config``
+    the audio stream and the audio <-> video cross-attention. Weights are assigned after
     construction: ``attn1``/``attn2`` (``Attention``), ``ff`` (``FeedForward``),
-    ``scale_shift_table`` ``(9, D)`` and ``prompt_scale_shift_table`` ``(2, D)``."""
+    ``scale_shift_table`` ``(9, D)``, ``prompt_scale_shift_table`` ``(2, D)``; for audio the same
+    with an ``audio_`` prefix, plus ``audio_to_video_attn``, ``video_to_audio_attn`` and the
+    ``(5, D)`` tables ``scale_shift_table_a2v_ca_video`` / ``scale_shift_table_a2v_ca_audio``.
+
+    Each stream's residual is carried in FP32 between its branches (attention, text
+    cross-attention, A/V cross-attention, feed-forward) and rounded once at the end; the
+    branches' gated residuals are formed in the output GEMMs' epilogues."""
 
     def __init__(self, idx: int, *, video_config: TransformerConfig, audio_config: TransformerConfig | None = None,
                  rope_type: LTXRopeType = LTXRopeType.SPLIT, norm_eps: float = 1e-6) -> None:
@@ -152,24 +159,47 @@ class BasicAVTransformerBlock:
         self.norm_eps = norm_eps
         self.video_config = video_config
         self.audio_config = audio_config
-        backend = {
-            "compile_attention": video_config.compile_attention,
-            "dense_kernel": video_config.dense_attention_kernel,
-        }
+        v_backend = {"compile_attention": video_config.compile_attention,
+                     "dense_kernel": video_config.dense_attention_kernel}
         self.attn1 = Attention(video_config.dim, heads=video_config.heads, dim_head=video_config.head_dim,
                                norm_eps=norm_eps, rope_type=rope_type,
-                               apply_gated_attention=video_config.apply_gated_attention, **backend)
+                               apply_gated_attention=video_config.apply_gated_attention, **v_backend)
         self.attn2 = Attention(video_config.dim, context_dim=video_config.context_dim, heads=video_config.heads,
                                dim_head=video_config.head_dim, norm_eps=norm_eps, rope_type=rope_type,
-                               apply_gated_attention=video_config.apply_gated_attention, **backend)
+                               apply_gated_attention=video_config.apply_gated_attention, **v_backend)
         self.ff = FeedForward(video_config.dim, bias=video_config.ff_bias)
         self.scale_shift_table: torch.Tensor | None = None
         self.prompt_scale_shift_table: torch.Tensor | None = None
+        if audio_config is None:
+            return
+        a = audio_config
+        a_backend = {"compile_attention": a.compile_attention, "dense_kernel": a.dense_attention_kernel}
+        self.audio_attn1 = Attention(a.dim, heads=a.heads, dim_head=a.head_dim, norm_eps=norm_eps, rope_type=rope_type,
+                                     apply_gated_attention=a.apply_gated_attention, **a_backend)
+        self.audio_attn2 = Attention(a.dim, context_dim=a.context_dim, heads=a.heads, dim_head=a.head_dim,
+                                     norm_eps=norm_eps, rope_type=rope_type,
+                                     apply_gated_attention=a.apply_gated_attention, **a_backend)
+        self.audio_ff = FeedForward(a.dim, bias=a.ff_bias)
+        self.audio_scale_shift_table: torch.Tensor | None = None
+        self.audio_prompt_scale_shift_table: torch.Tensor | None = None
+        self.audio_to_video_attn = Attention(video_config.dim, context_dim=a.dim, heads=a.heads, dim_head=a.head_dim,
+                                             norm_eps=norm_eps, rope_type=rope_type,
+                                             apply_gated_attention=video_config.apply_gated_attention, **v_backend)
+        self.video_to_audio_attn = Attention(a.dim, context_dim=video_config.dim, heads=a.heads, dim_head=a.head_dim,
+                                             norm_eps=norm_eps, rope_type=rope_type,
+                                             apply_gated_attention=a.apply_gated_attention, **a_backend)
+        self.scale_shift_table_a2v_ca_audio: torch.Tensor | None = None
+        self.scale_shift_table_a2v_ca_video: torch.Tensor | None = None
 
     def fuse_projections(self) -> None:
-        """Fuse Q/K/V of the self-attention and K/V of the text cross-attention."""
+        """Fuse Q/K/V of the self-attentions and K/V of the text cross-attentions."""
         self.attn1.fuse_projections(self_attention=True)
         self.attn2.fuse_projections(self_attention=False)
+        if self.audio_config is not None:
+            self.audio_attn1.fuse_projections(self_attention=True)
+            self.audio_attn2.fuse_projections(self_attention=False)
+            self.audio_to_video_attn.fuse_projections(self_attention=False)
+            self.video_to_audio_attn.fuse_projections(self_attention=False)
 
     @staticmethod
     def _ada_values(table: torch.Tensor, timestep: torch.Tensor, start: int, stop: int) -> tuple[torch.Tensor, ...]:
@@ -177,10 +207,21 @@ class BasicAVTransformerBlock:
         values = (table[start:stop][None, None].float() + timestep[:, :, start:stop, :].float()).contiguous()
         return tuple(values[:, :, i, :] for i in range(stop - start))
 
-    def _text_cross_attention(self, value: torch.Tensor, args: TransformerArgs, ada: torch.Tensor) -> torch.Tensor:
+    @staticmethod
+    def _av_ada_values(table: torch.Tensor, scale_shift: torch.Tensor, gate_timestep: torch.Tensor):
+        """``(scale_a2v, shift_a2v, scale_v2a, shift_v2a, gate)`` from a ``(5, D)`` table
+        (``transformer.py:188-199``)."""
+        ss = (table[:4][None, None].float() + scale_shift.float()).contiguous()
+        g = (table[4:5][None, None].float() + gate_timestep.float()).contiguous()
+        return (*(ss[:, :, i, :] for i in range(4)), g[:, :, 0, :])
+
+    def _text_cross_attention(self, value: torch.Tensor, args: TransformerArgs, ada: torch.Tensor,
+                              attention: Attention | None = None, prompt_table: torch.Tensor | None = None) -> torch.Tensor:
         """``x + gate(attn2(adaln(x), modulate(context)))`` with the residual in the output
         GEMM (``transformer.py:201-223`` and ``:266-276``)."""
-        prompt = self.prompt_scale_shift_table[None, None].float()
+        attention = self.attn2 if attention is None else attention
+        prompt_table = self.prompt_scale_shift_table if prompt_table is None else prompt_table
+        prompt = prompt_table[None, None].float()
         if args.prompt_timestep is not None:
             prompt = prompt + args.prompt_timestep.float()
         prompt = prompt.contiguous()
@@ -188,30 +229,74 @@ class BasicAVTransformerBlock:
         context = modulate(args.context, prompt[:, :, 1], prompt[:, :, 0])
         if args.context_mask is not None:
             raise ValueError("masked text cross-attention is not built for MI355X")
-        return self.attn2(query, context=context, residual=value, gate=ada[:, :, 8], out_dtype=torch.float32)
+        return attention(query, context=context, residual=value, gate=ada[:, :, 8], out_dtype=torch.float32)
+
+    def _first_branches(self, args: TransformerArgs, table, attn1: Attention, attn2: Attention, prompt_table):
+        """Self-attention then text cross-attention, FP32 residual out."""
+        if args.self_attention_mask is not None:
+            raise ValueError("masked self-attention is not built for MI355X")
+        if args.sparse_attention is not None:
+            raise ValueError("sparse (Sol-Attn) attention is not built for MI355X")
+        x = args.x
+        ada = (table[None, None].float() + args.timesteps.float()).contiguous()
+        normalized = adaln(x, ada[:, :, 1], ada[:, :, 0], self.norm_eps)
+        x1 = attn1(normalized, pe=args.positional_embeddings, residual=x, gate=ada[:, :, 2], out_dtype=torch.float32)
+        return self._text_cross_attention(x1, args, ada, attn2, prompt_table), ada
 
     def __call__(self, video: TransformerArgs | None, audio: TransformerArgs | None = None):
-        if audio is not None:
-            raise ValueError("the audio stream and A/V attention are not built for MI355X")
-        if video is None or not video.enabled or video.x.numel() == 0:
+        video_present = video is not None and video.x.numel() > 0
+        audio_present = audio is not None and audio.x.numel() > 0
+        if audio_present and self.audio_config is None:
+            raise ValueError("this block has no audio stream (constructed without audio_config)")
+        run_video = video_present and video.enabled
+        run_audio = audio_present and audio.enabled
+        run_a2v = run_video and audio_present
+        run_v2a = run_audio and video_present
+        if not (run_video or run_audio):
             return video, audio
-        if video.self_attention_mask is not None:
-            raise ValueError("masked self-attention is not built for MI355X")
-        if video.sparse_attention is not None:
-            raise ValueError("sparse (Sol-Attn) attention is not built for MI355X")
-        x = video.x
-        ada = (self.scale_shift_table[None, None].float() + video.timesteps.float()).contiguous()
 
-        # x1, x2: the residual stream in FP32 between the branches; one rounding at the end.
-        normalized = adaln(x, ada[:, :, 1], ada[:, :, 0], self.norm_eps)
-        x1 = self.attn1(normalized, pe=video.positional_embeddings, residual=x, gate=ada[:, :, 2],
-                        out_dtype=torch.float32)
-
-        x2 = self._text_cross_attention(x1, video, ada)
-
-        normalized = adaln(x2, ada[:, :, 4], ada[:, :, 3], self.norm_eps)
-        out = self.ff(normalized, residual=x2, gate=ada[:, :, 5], out_dtype=x.dtype)
-        return replace(video, x=out), audio
+        video_value = video.x if video_present else None
+        audio_value = audio.x if audio_present else None
+        if run_video:
+            video_value, video_ada = self._first_branches(video, self.scale_shift_table, self.attn1, self.attn2,
+                                                          self.prompt_scale_shift_table)
+        if run_audio:
+            audio_value, audio_ada = self._first_branches(audio, self.audio_scale_shift_table, self.audio_attn1,
+                                                          self.audio_attn2, self.audio_prompt_scale_shift_table)
+        if run_a2v or run_v2a:
+            for args in (video, audio):
+                if (args.cross_scale_shift_timestep is None or args.cross_gate_timestep is None
+                        or args.cross_positional_embeddings is None):
+                    raise ValueError("A/V attention requires cross-modal preprocessing")
+            a_scale_a2v, a_shift_a2v, a_scale_v2a, a_shift_v2a, gate_v2a = self._av_ada_values(
+                self.scale_shift_table_a2v_ca_audio, audio.cross_scale_shift_timestep, audio.cross_gate_timestep)
+            v_scale_a2v, v_shift_a2v, v_scale_v2a, v_shift_v2a, gate_a2v = self._av_ada_values(
+                self.scale_shift_table_a2v_ca_video, video.cross_scale_shift_timestep, video.cross_gate_timestep)
+            video_base, audio_base = video_value, audio_value
+            # rms_norm(x) * (1 + scale) + shift is one AdaLN pass per (stream, direction)
+            if run_a2v:
+                query = adaln(video_base, v_scale_a2v, v_shift_a2v, self.norm_eps)
+                context = adaln(audio_base, a_scale_a2v, a_shift_a2v, self.norm_eps)
+                video_value = self.audio_to_video_attn(
+                    query, context=context, pe=video.cross_positional_embeddings,
+                    k_pe=audio.cross_positional_embeddings, residual=video_base, gate=gate_a2v,
+                    out_dtype=torch.float32)
+            if run_v2a:
+                query = adaln(audio_base, a_scale_v2a, a_shift_v2a, self.norm_eps)
+                context = adaln(video_base, v_scale_v2a, v_shift_v2a, self.norm_eps)
+                audio_value = self.video_to_audio_attn(
+                    query, context=context, pe=audio.cross_positional_embeddings,
+                    k_pe=video.cross_positional_embeddings, residual=audio_base, gate=gate_v2a,
+                    out_dtype=torch.float32)
+        if run_video:
+            normalized = adaln(video_value, video_ada[:, :, 4], video_ada[:, :, 3], self.norm_eps)
+            video = replace(video, x=self.ff(normalized, residual=video_value, gate=video_ada[:, :, 5],
+                                             out_dtype=video.x.dtype))
+        if run_audio:
+            normalized = adaln(audio_value, audio_ada[:, :, 4], audio_ada[:, :, 3], self.norm_eps)
+            audio = replace(audio, x=self.audio_ff(normalized, residual=audio_value, gate=audio_ada[:, :, 5],
+                                                   out_dtype=audio.x.dtype))
+        return video, audio
 
 
 __all__ = [

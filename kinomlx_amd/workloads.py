@@ -187,6 +187,94 @@ def build_ltx_block(spec: LTXSpec, p: dict[str, torch.Tensor], device, *, fuse: 
     return block
 
 
+@dataclass(frozen=True)
+class LTXAudioSpec:
+    """The audio stream of a joint LTX-2 block: ``tokens`` audio latents (25 per second of
+    video), text via cross-attention, ``heads`` equal to the video stream's."""
+
+    tokens: int
+    text_tokens: int
+    dim: int = 2048
+    heads: int = 32
+    head_dim: int = 64
+    ff_mult: int = 4
+
+
+def _ltx_cross_params(p: dict, seed: int, prefix: str, qdim: int, cdim: int, heads: int, head_dim: int) -> None:
+    inner = heads * head_dim
+    for name, shape in (("to_q", (inner, qdim)), ("to_k", (inner, cdim)), ("to_v", (inner, cdim)),
+                        ("to_out", (qdim, inner))):
+        p[f"{prefix}.{name}.weight"] = bf16(normal(seed, f"{prefix}.{name}.weight", shape, 0.02))
+        p[f"{prefix}.{name}.bias"] = bf16(normal(seed, f"{prefix}.{name}.bias", (shape[0],), 0.02))
+    p[f"{prefix}.to_gate_logits.weight"] = bf16(normal(seed, f"{prefix}.to_gate_logits.weight", (heads, qdim), 0.02))
+    p[f"{prefix}.to_gate_logits.bias"] = bf16(normal(seed, f"{prefix}.to_gate_logits.bias", (heads,), 0.02))
+    for name in ("q_norm", "k_norm"):
+        p[f"{prefix}.{name}.weight"] = bf16(normal(seed, f"{prefix}.{name}.weight", (inner,), 0.02, 1.0))
+
+
+def ltx_av_params(spec: LTXSpec, audio: LTXAudioSpec, seed: int = 0) -> dict[str, torch.Tensor]:
+    """Dense bf16 parameters of one joint A/V block: the video block of ``ltx_params``, the audio
+    stream under ``audio_`` names, both cross-attentions and their ``(5, D)`` tables, and the
+    per-step rows (``timesteps`` (1, 1, 9, D), ``audio_timesteps``, ``cross_ss`` (1, 1, 4, D),
+    ``cross_gate`` (1, 1, 1, D) and their audio forms)."""
+    p = ltx_params(spec, seed)
+    a = ltx_params(LTXSpec(grid=(1, 1, audio.tokens), text_tokens=audio.text_tokens, dim=audio.dim,
+                           heads=audio.heads, head_dim=audio.head_dim, ff_mult=audio.ff_mult), seed + 7919)
+    for name, value in a.items():
+        p[f"audio_{name}"] = value
+    _ltx_cross_params(p, seed, "audio_to_video_attn", spec.dim, audio.dim, audio.heads, audio.head_dim)
+    _ltx_cross_params(p, seed, "video_to_audio_attn", audio.dim, spec.dim, audio.heads, audio.head_dim)
+    p["scale_shift_table_a2v_ca_video"] = normal(seed, "av_table_video", (5, spec.dim), 0.02)
+    p["scale_shift_table_a2v_ca_audio"] = normal(seed, "av_table_audio", (5, audio.dim), 0.02)
+    for pre, d in (("", spec.dim), ("audio_", audio.dim)):
+        p[f"{pre}cross_ss"] = bf16(normal(seed, f"{pre}cross_ss", (1, 1, 4, d), 0.3))
+        p[f"{pre}cross_gate"] = bf16(normal(seed, f"{pre}cross_gate", (1, 1, 1, d), 0.3))
+    return p
+
+
+def ltx_av_inputs(spec: LTXSpec, audio: LTXAudioSpec, seed: int = 0) -> dict[str, torch.Tensor]:
+    """``ltx_inputs`` plus the audio stream ``(1, Ta, Da)``, its context and its ``(1, 1, Ta, 2)``
+    temporal bounds."""
+    out = ltx_inputs(spec, seed)
+    out["audio_x"] = bf16(normal(seed, "audio_x", (1, audio.tokens, audio.dim)))
+    out["audio_context"] = bf16(normal(seed, "audio_context", (1, audio.text_tokens, audio.dim)))
+    start = torch.arange(audio.tokens, dtype=torch.float32)
+    out["audio_positions"] = torch.stack([start, start + 1.0], dim=-1)[None, None]
+    return out
+
+
+def build_ltx_av_block(spec: LTXSpec, audio: LTXAudioSpec, p: dict, device, *, fuse: bool = True):
+    """The MI355X joint ``BasicAVTransformerBlock`` holding ``p``'s weights on ``device``."""
+    from .ltx2.transformer import BasicAVTransformerBlock, TransformerConfig
+
+    vcfg = TransformerConfig(dim=spec.dim, heads=spec.heads, head_dim=spec.head_dim, context_dim=spec.dim)
+    acfg = TransformerConfig(dim=audio.dim, heads=audio.heads, head_dim=audio.head_dim, context_dim=audio.dim)
+    block = BasicAVTransformerBlock(0, video_config=vcfg, audio_config=acfg)
+    for pre in ("", "audio_"):
+        for a in ("attn1", "attn2"):
+            attn = getattr(block, f"{pre}{a}")
+            for n in ("to_q", "to_k", "to_v", "to_out", "to_gate_logits"):
+                setattr(attn, n, _layer(p, f"{pre}{a}.{n}", device))
+            attn.q_norm.weight = p[f"{pre}{a}.q_norm.weight"].to(device)
+            attn.k_norm.weight = p[f"{pre}{a}.k_norm.weight"].to(device)
+        ff = getattr(block, f"{pre}ff")
+        ff.project_in.proj = _layer(p, f"{pre}ff.proj_in", device)
+        ff.project_out = _layer(p, f"{pre}ff.proj_out", device)
+        setattr(block, f"{pre}scale_shift_table", p[f"{pre}scale_shift_table"].to(device))
+        setattr(block, f"{pre}prompt_scale_shift_table", p[f"{pre}prompt_scale_shift_table"].to(device))
+    for a in ("audio_to_video_attn", "video_to_audio_attn"):
+        attn = getattr(block, a)
+        for n in ("to_q", "to_k", "to_v", "to_out", "to_gate_logits"):
+            setattr(attn, n, _layer(p, f"{a}.{n}", device))
+        attn.q_norm.weight = p[f"{a}.q_norm.weight"].to(device)
+        attn.k_norm.weight = p[f"{a}.k_norm.weight"].to(device)
+    block.scale_shift_table_a2v_ca_video = p["scale_shift_table_a2v_ca_video"].to(device)
+    block.scale_shift_table_a2v_ca_audio = p["scale_shift_table_a2v_ca_audio"].to(device)
+    if fuse:
+        block.fuse_projections()
+    return block
+
+
 def ltx_model_params(spec: LTXSpec, num_blocks: int, *, in_channels: int = 128, out_channels: int = 128,
                      seed: int = 0) -> dict:
     """Dense bf16 parameters of an LTX video transformer: ``blocks`` (one ``ltx_params`` dict per
@@ -452,6 +540,8 @@ __all__ = [
     "LTXSpec",
     "build_flux_double_block",
     "build_flux_single_block",
+    "LTXAudioSpec",
+    "build_ltx_av_block",
     "build_ltx_block",
     "build_ltx_model",
     "flux_tables",
@@ -459,6 +549,8 @@ __all__ = [
     "flux_inputs",
     "flux_params",
     "flux_rope",
+    "ltx_av_inputs",
+    "ltx_av_params",
     "ltx_inputs",
     "ltx_model_inputs",
     "ltx_model_params",

@@ -37,6 +37,7 @@ __all__ = [
     "krea_block",
     "ltx_attention",
     "ltx_feed_forward",
+    "ltx_av_block",
     "ltx_video_block",
     "sigmoid",
 ]
@@ -68,12 +69,13 @@ def _keep(value: np.ndarray) -> np.ndarray:
     return value
 
 
-def ltx_attention(params: dict, prefix: str, value, *, heads: int, context=None, pe=None, eps=1e-6,
+def ltx_attention(params: dict, prefix: str, value, *, heads: int, context=None, pe=None, k_pe=None, eps=1e-6,
                   store=_keep):
     """LTX ``Attention.__call__`` without mask or sparse routing
     (``kinomlx/models/ltx2/transformer/attention.py:291-371``): gate logits ``2*sigmoid``,
     full-width weighted RMSNorm on Q and K, split RoPE, SDPA, per-head gate, output projection.
-    ``store`` is applied to every array the reference materialises (see ``ltx_video_block``)."""
+    ``store`` is applied to every array the reference materialises (see ``ltx_video_block``).
+    ``k_pe`` rotates the keys with their own tables (the A/V cross-attention, ``:342-344``)."""
     x = np.asarray(value, dtype=F32)
     source = x if context is None else np.asarray(context, dtype=F32)
     head_gate = None
@@ -85,7 +87,8 @@ def ltx_attention(params: dict, prefix: str, value, *, heads: int, context=None,
     if pe is not None:
         cos, sin = pe
         q = store(split_rope(q[None], cos, sin)[0])
-        k = store(split_rope(k[None], cos, sin)[0])
+        k_cos, k_sin = pe if k_pe is None else k_pe
+        k = store(split_rope(k[None], k_cos, k_sin)[0])
     out = store(attention(q, k, v, heads=heads))
     if head_gate is not None:
         tokens, width = out.shape
@@ -315,3 +318,56 @@ def krea_block(params: dict, value, modulation, rotary, *, heads: int, kv_heads:
     hidden = store(store(silu(store(_lin(params, "ff.gate", f)))) * store(_lin(params, "ff.up", f)))
     ff = store(_lin(params, "ff.down", hidden))
     return store((x + store(post_g * ff)).astype(F32))
+
+
+def _ltx_first_branches(params: dict, pre: str, x, context, pe, *, heads: int, eps: float, store):
+    """Self-attention then text cross-attention of one stream (``transformer.py:244-308``)."""
+    ada = np.asarray(params[f"{pre}ada"], dtype=F32)
+    prompt = np.asarray(params[f"{pre}prompt"], dtype=F32)
+
+    def _adaln(v, scale, shift):
+        return store((store(rms_norm(v, eps=eps)) * (F32(1.0) + scale) + shift).astype(F32))
+
+    value = np.asarray(x, dtype=F32)
+    attended = ltx_attention(params, f"{pre}attn1", _adaln(value, ada[1], ada[0]), heads=heads, pe=pe, eps=eps,
+                             store=store)
+    value = store(gated_residual(value, attended, ada[2]))
+    query = _adaln(value, ada[7], ada[6])
+    ctx = store(modulate(context, prompt[1], prompt[0]))
+    cross = ltx_attention(params, f"{pre}attn2", query, heads=heads, context=ctx, eps=eps, store=store)
+    return store((value + store(gate(cross, ada[8]))).astype(F32)), _adaln
+
+
+def ltx_av_block(params: dict, video_x, audio_x, video_context, audio_context, pe, audio_pe, cross_pe,
+                 audio_cross_pe, *, heads: int, audio_heads: int, eps: float = 1e-6, bf16_graph: bool = False):
+    """``BasicAVTransformerBlock.__call__`` with both streams enabled
+    (``kinomlx/models/ltx2/transformer/transformer.py:225-421``): each stream's self- and text
+    cross-attention, then the audio -> video and video -> audio cross-attention from the
+    RMS-normalized bases of both streams (``:310-371``), then each stream's feed-forward.
+
+    ``params`` holds the video block's names as ``ltx_video_block`` (``ada`` (9, Dv),
+    ``prompt`` (2, Dv)), the audio stream's under an ``audio_`` prefix (``audio_attn1.*``,
+    ``audio_attn2.*``, ``audio_ff.*``, ``audio_ada``, ``audio_prompt``), the cross-attentions
+    ``audio_to_video_attn.*`` / ``video_to_audio_attn.*`` and the ``(5, D)`` rows ``av_video`` /
+    ``av_audio`` = table + cross timesteps (``:188-199``): scale a2v, shift a2v, scale v2a,
+    shift v2a, gate. Returns ``(video, audio)``, tokens leading."""
+    store = to_bf16 if bf16_graph else _keep
+    v, _adaln = _ltx_first_branches(params, "", video_x, video_context, pe, heads=heads, eps=eps, store=store)
+    a, _ = _ltx_first_branches(params, "audio_", audio_x, audio_context, audio_pe, heads=audio_heads, eps=eps,
+                               store=store)
+    av_v = np.asarray(params["av_video"], dtype=F32)
+    av_a = np.asarray(params["av_audio"], dtype=F32)
+    v_norm, a_norm = store(rms_norm(v, eps=eps)), store(rms_norm(a, eps=eps))
+    a2v = ltx_attention(params, "audio_to_video_attn", store(modulate(v_norm, av_v[0], av_v[1])), heads=audio_heads,
+                        context=store(modulate(a_norm, av_a[0], av_a[1])), pe=cross_pe, k_pe=audio_cross_pe, eps=eps,
+                        store=store)
+    v2a = ltx_attention(params, "video_to_audio_attn", store(modulate(a_norm, av_a[2], av_a[3])), heads=audio_heads,
+                        context=store(modulate(v_norm, av_v[2], av_v[3])), pe=audio_cross_pe, k_pe=cross_pe, eps=eps,
+                        store=store)
+    v = store(gated_residual(v, a2v, av_v[4]))
+    a = store(gated_residual(a, v2a, av_a[4]))
+    ada, audio_ada = np.asarray(params["ada"], dtype=F32), np.asarray(params["audio_ada"], dtype=F32)
+    v = store(gated_residual(v, ltx_feed_forward(params, "ff", _adaln(v, ada[4], ada[3]), store), ada[5]))
+    a = store(gated_residual(a, ltx_feed_forward(params, "audio_ff", _adaln(a, audio_ada[4], audio_ada[3]), store),
+                             audio_ada[5]))
+    return v, a

@@ -1,0 +1,73 @@
+"""The joint audio/video LTX-2 block on the GPU against the oracle (block bar: cosine >= 0.9995,
+max abs <= max(2e-2, the reference bf16 graph's own error), for both streams)."""
+
+import numpy as np
+import pytest
+import torch
+
+from kinomlx_amd import workloads
+from kinomlx_amd.ltx2.rope import precompute_freqs_cis
+from kinomlx_amd.ltx2.transformer import TransformerArgs
+from tests._av import AUDIO, SPEC, oracle_av_params, oracle_run, tables
+from tests.conftest import cosine, max_abs
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(got, ref, graph):
+    c, m, g = cosine(got, ref), max_abs(got, ref), max_abs(graph, ref)
+    print(f"cosine {c:.7f} max_abs {m:.4g} (reference bf16 graph {g:.4g}) max|ref| {np.abs(ref).max():.3f}")
+    assert np.all(np.isfinite(got)) and c >= 0.9995 and m <= max(2e-2, g), (c, m, g)
+
+
+def _args(p, inputs, device):
+    inner = AUDIO.heads * AUDIO.head_dim
+    vpos, apos = inputs["positions"].to(device), inputs["audio_positions"].to(device)
+    pe = precompute_freqs_cis(vpos, dim=SPEC.dim, use_middle_indices_grid=True, num_attention_heads=SPEC.heads)
+    audio_pe = precompute_freqs_cis(apos, dim=AUDIO.dim, max_pos=(20,), use_middle_indices_grid=True,
+                                    num_attention_heads=AUDIO.heads)
+    cross = precompute_freqs_cis(vpos[:, 0:1], dim=inner, max_pos=(20,), use_middle_indices_grid=True,
+                                 num_attention_heads=AUDIO.heads)
+    audio_cross = precompute_freqs_cis(apos[:, 0:1], dim=inner, max_pos=(20,), use_middle_indices_grid=True,
+                                       num_attention_heads=AUDIO.heads)
+    d = lambda k: p[k].to(device)  # noqa: E731
+    video = TransformerArgs(x=inputs["x"].to(device), context=inputs["context"].to(device), timesteps=d("timesteps"),
+                            positional_embeddings=pe, cross_positional_embeddings=cross,
+                            cross_scale_shift_timestep=d("cross_ss"), cross_gate_timestep=d("cross_gate"))
+    audio = TransformerArgs(x=inputs["audio_x"].to(device), context=inputs["audio_context"].to(device),
+                            timesteps=d("audio_timesteps"), positional_embeddings=audio_pe,
+                            cross_positional_embeddings=audio_cross, cross_scale_shift_timestep=d("audio_cross_ss"),
+                            cross_gate_timestep=d("audio_cross_gate"))
+    return video, audio
+
+
+@pytest.mark.parametrize("fuse", [True, False])
+def test_av_block_matches_oracle(device, fuse):
+    p = workloads.ltx_av_params(SPEC, AUDIO)
+    inputs = workloads.ltx_av_inputs(SPEC, AUDIO)
+    block = workloads.build_ltx_av_block(SPEC, AUDIO, p, device, fuse=fuse)
+    video, audio = _args(p, inputs, device)
+    out_v, out_a = block(video, audio)
+    torch.cuda.synchronize()
+    op = oracle_av_params(p)
+    pes = tables(inputs)
+    ref_v, ref_a = oracle_run(op, inputs, pes)
+    graph_v, graph_a = oracle_run(op, inputs, pes, bf16_graph=True)
+    _check(out_v.x[0].float().cpu().numpy(), ref_v, graph_v)
+    _check(out_a.x[0].float().cpu().numpy(), ref_a, graph_a)
+
+
+def test_disabled_audio_still_feeds_video(device):
+    """A present but disabled audio stream is left as it is and still supplies the audio ->
+    video K/V; the video output then differs from a block run without audio."""
+    p = workloads.ltx_av_params(SPEC, AUDIO)
+    inputs = workloads.ltx_av_inputs(SPEC, AUDIO)
+    block = workloads.build_ltx_av_block(SPEC, AUDIO, p, device)
+    video, audio = _args(p, inputs, device)
+    from dataclasses import replace
+
+    off = replace(audio, enabled=False)
+    out_v, out_a = block(video, off)
+    assert out_a is off
+    alone, _ = block(video, None)
+    assert not torch.equal(out_v.x, alone.x)
