@@ -1,10 +1,9 @@
-"""One LTX-2 denoising step on MI355X: the X0 transformer call, the Euler update and the finite
-check.
+"""One LTX-2 denoising step on MI355X: the X0 transformer call, the Euler updates and the finite
+checks, for the video stream alone or with the audio stream.
 
 Mirror of the deterministic-Euler path of ``kinomlx/models/ltx2/denoise.py``
 (``LTX2DenoiseError`` ``:11-12``, ``_advance_sample`` ``:60-85``, ``_advance_state``
-``:100-120``, ``modality_from_state`` ``:123-156``, ``denoise_step`` ``:159-258``) for the video
-stream. The finite check is one reduction kernel over the new latent; its one-int flag is the
+``:100-120``, ``modality_from_state`` ``:123-156``, ``denoise_step`` ``:159-258``). The finite check is one reduction kernel over the new latent; its one-int flag is the
 step's only device-to-host read, as ``mx.stack([...]).tolist()`` is the reference's.
 """
 
@@ -66,29 +65,42 @@ def _advance_sample(sample: torch.Tensor, denoised: torch.Tensor, *, sigma: floa
 def denoise_step(video_state: LatentState, audio_state: LatentState | None = None, *, sigma: float,
                  sigma_next: float, transformer, video_context: torch.Tensor,
                  audio_context: torch.Tensor | None = None, video_context_mask: torch.Tensor | None = None,
-                 video_keyframes_mask: torch.Tensor | None = None, video_enabled: bool = True,
+                 audio_context_mask: torch.Tensor | None = None, video_keyframes_mask: torch.Tensor | None = None,
+                 video_enabled: bool = True, audio_enabled: bool = True,
                  step_kind: DenoiseStepKind = "deterministic-euler", video_noise: torch.Tensor | None = None,
+                 audio_noise: torch.Tensor | None = None,
                  video_sparse_attention: object | None = None) -> tuple[LatentState, LatentState | None]:
-    """Run one X0 transformer call and the Euler update of the video stream, then check the
-    new latent is finite (``denoise.py:159-258``). ``transformer`` is an ``X0Model``."""
-    if audio_state is not None or audio_context is not None:
-        raise ValueError("the audio stream is not built for MI355X")
+    """Run one X0 transformer call and the Euler update of each enabled stream, then check the
+    new latents are finite (``denoise.py:159-258``). ``transformer`` is an ``X0Model``."""
     video_modality = modality_from_state(video_state, video_context, sigma, enabled=video_enabled,
                                          context_mask=video_context_mask, keyframes_mask=video_keyframes_mask,
                                          sparse_attention=video_sparse_attention)
-    video_denoised, _ = transformer(video_modality, None)
+    audio_modality = None
+    if audio_state is not None:
+        if audio_context is None:
+            raise ValueError("audio context is required for an audio latent state")
+        audio_modality = modality_from_state(audio_state, audio_context, sigma, enabled=audio_enabled,
+                                             context_mask=audio_context_mask)
+    video_denoised, audio_denoised = transformer(video_modality, audio_modality)
+    active = []
     if video_enabled:
         if video_denoised is None:
             raise RuntimeError("transformer returned no video prediction")
-        prediction = post_process_latent(video_denoised, video_state)
-        latent = _advance_sample(video_state.latent, prediction, sigma=sigma, sigma_next=sigma_next,
-                                 step_kind=step_kind, noise=video_noise)
+        latent = _advance_sample(video_state.latent, post_process_latent(video_denoised, video_state), sigma=sigma,
+                                 sigma_next=sigma_next, step_kind=step_kind, noise=video_noise)
         video_state = replace(video_state, latent=latent)
-        if not all_finite(video_state.latent):
-            raise LTX2DenoiseError(
-                f"LTX-2 denoising produced a nonfinite video latent in {video_state.latent.dtype}."
-            )
-    return video_state, None
+        active.append(("video", video_state.latent))
+    if audio_state is not None and audio_enabled:
+        if audio_denoised is None:
+            raise RuntimeError("transformer returned no audio prediction")
+        latent = _advance_sample(audio_state.latent, post_process_latent(audio_denoised, audio_state), sigma=sigma,
+                                 sigma_next=sigma_next, step_kind=step_kind, noise=audio_noise)
+        audio_state = replace(audio_state, latent=latent)
+        active.append(("audio", audio_state.latent))
+    for modality, value in active:
+        if not all_finite(value):
+            raise LTX2DenoiseError(f"LTX-2 denoising produced a nonfinite {modality} latent in {value.dtype}.")
+    return video_state, audio_state
 
 
 __all__ = [

@@ -383,6 +383,111 @@ def random_ltx_model(spec: LTXSpec, num_blocks: int, device, *, in_channels: int
     return model
 
 
+_AV_STEP_ROWS = ("timesteps", "audio_timesteps", "cross_ss", "cross_gate", "audio_cross_ss", "audio_cross_gate")
+
+
+def _av_top_params(p: dict, spec: LTXSpec, audio: LTXAudioSpec, in_channels: int, out_channels: int, lin) -> None:
+    for pre, d in (("", spec.dim), ("audio_", audio.dim)):
+        lin(f"{pre}patchify_proj", d, in_channels)
+        for name, rows in ((f"{pre}adaln_single", 9), (f"{pre}prompt_adaln_single", 2)):
+            lin(f"{name}.emb.timestep_embedder.linear_1", d, 256)
+            lin(f"{name}.emb.timestep_embedder.linear_2", d, d)
+            lin(f"{name}.linear", rows * d, d)
+        lin(f"{pre}proj_out", out_channels, d)
+    for name, d, rows in (("av_ca_video_scale_shift_adaln_single", spec.dim, 4),
+                          ("av_ca_a2v_gate_adaln_single", spec.dim, 1),
+                          ("av_ca_audio_scale_shift_adaln_single", audio.dim, 4),
+                          ("av_ca_v2a_gate_adaln_single", audio.dim, 1)):
+        lin(f"{name}.emb.timestep_embedder.linear_1", d, 256)
+        lin(f"{name}.emb.timestep_embedder.linear_2", d, d)
+        lin(f"{name}.linear", rows * d, d)
+
+
+def ltx_av_model_params(spec: LTXSpec, audio: LTXAudioSpec, num_blocks: int, *, in_channels: int = 128,
+                        out_channels: int = 128, seed: int = 0) -> dict:
+    """Dense bf16 parameters of a joint audio/video LTX transformer: ``blocks`` (``ltx_av_params``
+    per block, without the per-step rows), both streams' patchify / AdaLN / prompt / output
+    parts, the four A/V AdaLN producers and the two ``(2, D)`` output tables."""
+    p: dict = {"blocks": []}
+    for index in range(num_blocks):
+        block = ltx_av_params(spec, audio, seed * 1000 + index)
+        for name in _AV_STEP_ROWS:
+            block.pop(name)
+        p["blocks"].append(block)
+
+    def lin(name: str, n: int, k: int) -> None:
+        p[f"{name}.weight"] = bf16(normal(seed, f"model.{name}.weight", (n, k), 0.02))
+        p[f"{name}.bias"] = bf16(normal(seed, f"model.{name}.bias", (n,), 0.02))
+
+    _av_top_params(p, spec, audio, in_channels, out_channels, lin)
+    p["scale_shift_table"] = bf16(normal(seed, "model.scale_shift_table", (2, spec.dim), 0.02))
+    p["audio_scale_shift_table"] = bf16(normal(seed, "model.audio_scale_shift_table", (2, audio.dim), 0.02))
+    return p
+
+
+def ltx_av_model_inputs(spec: LTXSpec, audio: LTXAudioSpec, *, in_channels: int = 128, seed: int = 0) -> dict:
+    """``ltx_model_inputs`` plus the audio latent ``(1, Ta, C)``, audio context and bounds."""
+    out = ltx_model_inputs(spec, in_channels=in_channels, seed=seed)
+    out["audio_latent"] = bf16(normal(seed, "audio_latent", (1, audio.tokens, in_channels)))
+    out["audio_context"] = bf16(normal(seed, "audio_context", (1, audio.text_tokens, audio.dim)))
+    start = torch.arange(audio.tokens, dtype=torch.float32)
+    out["audio_positions"] = torch.stack([start, start + 1.0], dim=-1)[None, None]
+    return out
+
+
+def build_ltx_av_model(spec: LTXSpec, audio: LTXAudioSpec, p: dict, device, *, in_channels: int = 128,
+                       out_channels: int = 128, fuse: bool = True):
+    """The MI355X joint ``LTXAVModel`` holding ``p``'s weights on ``device``."""
+    from .ltx2.model import LTXAVModel
+
+    model = LTXAVModel(num_layers=max(1, len(p["blocks"])), video_heads=spec.heads, video_head_dim=spec.head_dim,
+                       audio_heads=audio.heads, audio_head_dim=audio.head_dim, video_in_channels=in_channels,
+                       video_out_channels=out_channels, audio_in_channels=in_channels,
+                       audio_out_channels=out_channels, video_context_dim=spec.dim)
+    model.transformer_blocks = [build_ltx_av_block(spec, audio, b, device, fuse=fuse) for b in p["blocks"]]
+    for pre in ("", "audio_"):
+        setattr(model, f"{pre}patchify_proj", _layer(p, f"{pre}patchify_proj", device))
+        setattr(model, f"{pre}proj_out", _layer(p, f"{pre}proj_out", device))
+        setattr(model, f"{pre}scale_shift_table", p[f"{pre}scale_shift_table"].to(device))
+        _assign_adaln(getattr(model, f"{pre}adaln_single"), p, f"{pre}adaln_single", device)
+        _assign_adaln(getattr(model, f"{pre}prompt_adaln_single"), p, f"{pre}prompt_adaln_single", device)
+    for name in ("av_ca_video_scale_shift_adaln_single", "av_ca_a2v_gate_adaln_single",
+                 "av_ca_audio_scale_shift_adaln_single", "av_ca_v2a_gate_adaln_single"):
+        _assign_adaln(getattr(model, name), p, name, device)
+    return model
+
+
+def random_ltx_av_model(spec: LTXSpec, audio: LTXAudioSpec, num_blocks: int, device, *, in_channels: int = 128,
+                        out_channels: int = 128, seed: int = 0):
+    """A joint ``LTXAVModel`` of ``num_blocks`` blocks with every tensor drawn on ``device``
+    (N(0, 0.02); norm scales N(1, 0.02)) in the shapes of ``ltx_av_model_params`` (for timing)."""
+    gen = torch.Generator(device=device).manual_seed(seed)
+    template = ltx_av_params(spec, audio, seed)
+
+    def draw(name: str, like: torch.Tensor) -> torch.Tensor:
+        mean = 1.0 if name.endswith("norm.weight") else 0.0
+        value = torch.randn(tuple(like.shape), generator=gen, device=device) * 0.02 + mean
+        return value.to(like.dtype)
+
+    blocks = []
+    for _ in range(num_blocks):
+        b = {k: draw(k, v) for k, v in template.items() if k not in _AV_STEP_ROWS}
+        blocks.append(build_ltx_av_block(spec, audio, b, device))
+        del b
+    top: dict = {"blocks": []}
+
+    def lin(name: str, n: int, k: int) -> None:
+        top[f"{name}.weight"] = draw(name, torch.empty((n, k), dtype=torch.bfloat16))
+        top[f"{name}.bias"] = draw(name, torch.empty((n,), dtype=torch.bfloat16))
+
+    _av_top_params(top, spec, audio, in_channels, out_channels, lin)
+    top["scale_shift_table"] = draw("t", torch.empty((2, spec.dim), dtype=torch.bfloat16))
+    top["audio_scale_shift_table"] = draw("t", torch.empty((2, audio.dim), dtype=torch.bfloat16))
+    model = build_ltx_av_model(spec, audio, top, device, in_channels=in_channels, out_channels=out_channels)
+    model.transformer_blocks = blocks
+    return model
+
+
 # ---- FLUX.2 / config 1 ---------------------------------------------------------------------------
 
 
@@ -542,6 +647,7 @@ __all__ = [
     "build_flux_single_block",
     "LTXAudioSpec",
     "build_ltx_av_block",
+    "build_ltx_av_model",
     "build_ltx_block",
     "build_ltx_model",
     "flux_tables",
@@ -550,6 +656,8 @@ __all__ = [
     "flux_params",
     "flux_rope",
     "ltx_av_inputs",
+    "ltx_av_model_inputs",
+    "ltx_av_model_params",
     "ltx_av_params",
     "ltx_inputs",
     "ltx_model_inputs",
@@ -558,5 +666,6 @@ __all__ = [
     "ltx_positions",
     "normal",
     "quantize_ltx_params",
+    "random_ltx_av_model",
     "random_ltx_model",
 ]

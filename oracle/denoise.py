@@ -13,7 +13,7 @@ import math
 
 import numpy as np
 
-from .blocks import ltx_video_block
+from .blocks import ltx_av_block, ltx_video_block
 from .ops import F32, layer_norm, linear, silu, to_bf16
 
 __all__ = [
@@ -21,6 +21,7 @@ __all__ = [
     "all_finite",
     "euler_step",
     "euler_velocity_step",
+    "ltx_av_forward",
     "ltx_forward",
     "output_head",
     "post_process_latent",
@@ -120,6 +121,53 @@ def ltx_forward(params: dict, latent, context, timesteps, sigma, pe, *, heads: i
         p["prompt"] = _f32(block["prompt_scale_shift_table"]) + prompt
         x = to_bf16(ltx_video_block(p, x, context, pe, heads=heads, eps=eps, bf16_graph=bf16_graph))
     return output_head(params, x[None], to_bf16(embedded).reshape(1, 1, d), eps=eps, bf16_graph=bf16_graph)[0]
+
+
+def ltx_av_forward(params: dict, latent, audio_latent, context, audio_context, timesteps, audio_timesteps, sigma,
+                   audio_sigma, pes, *, heads: int, audio_heads: int, num_blocks: int, timestep_scale: float = 1000.0,
+                   av_gate_scale: float = 1000.0, eps: float = 1e-6, bf16_graph: bool = False):
+    """Joint audio/video ``LTXAVModel.__call__`` for batch 1 (``model.py:595-635``) with both
+    streams' preprocessing (``preprocessing.py:134-214``): patchify, the AdaLN / prompt rows, the
+    A/V scale-shift rows from each stream's own timesteps and the A/V gate rows from the other
+    stream's sigma times ``av_gate_scale``; ``ltx_av_block`` per block; both output heads.
+    ``pes`` = (video, audio, video cross, audio cross) tables. Returns the two ``(T, C)``
+    velocities."""
+    store = to_bf16 if bf16_graph else (lambda v: v)
+    bf = to_bf16
+    v = bf(store(linear(latent, params["patchify_proj.weight"], params["patchify_proj.bias"])))
+    a = bf(store(linear(audio_latent, params["audio_patchify_proj.weight"], params["audio_patchify_proj.bias"])))
+    dv, da = v.shape[-1], a.shape[-1]
+
+    def rows(prefix, t, scale, n, d):
+        mod, emb = adaln_single(params, prefix, t, time_scale=scale, bf16_graph=bf16_graph)
+        return bf(mod).reshape(n, d), bf(emb).reshape(d)
+
+    mod_v, emb_v = rows("adaln_single", timesteps, timestep_scale, 9, dv)
+    prompt_v, _ = rows("prompt_adaln_single", sigma, timestep_scale, 2, dv)
+    mod_a, emb_a = rows("audio_adaln_single", audio_timesteps, timestep_scale, 9, da)
+    prompt_a, _ = rows("audio_prompt_adaln_single", audio_sigma, timestep_scale, 2, da)
+    ss_v, _ = rows("av_ca_video_scale_shift_adaln_single", timesteps, timestep_scale, 4, dv)
+    gate_v, _ = rows("av_ca_a2v_gate_adaln_single", audio_sigma, av_gate_scale, 1, dv)
+    ss_a, _ = rows("av_ca_audio_scale_shift_adaln_single", audio_timesteps, timestep_scale, 4, da)
+    gate_a, _ = rows("av_ca_v2a_gate_adaln_single", sigma, av_gate_scale, 1, da)
+    for block in params["blocks"][:num_blocks]:
+        p = {k: val for k, val in block.items() if "scale_shift_table" not in k}
+        p["ada"] = _f32(block["scale_shift_table"]) + mod_v
+        p["prompt"] = _f32(block["prompt_scale_shift_table"]) + prompt_v
+        p["audio_ada"] = _f32(block["audio_scale_shift_table"]) + mod_a
+        p["audio_prompt"] = _f32(block["audio_prompt_scale_shift_table"]) + prompt_a
+        tv, ta = _f32(block["scale_shift_table_a2v_ca_video"]), _f32(block["scale_shift_table_a2v_ca_audio"])
+        p["av_video"] = np.concatenate([tv[:4] + ss_v, tv[4:5] + gate_v])
+        p["av_audio"] = np.concatenate([ta[:4] + ss_a, ta[4:5] + gate_a])
+        v, a = ltx_av_block(p, v, a, context, audio_context, *pes, heads=heads, audio_heads=audio_heads, eps=eps,
+                            bf16_graph=bf16_graph)
+        v, a = bf(v), bf(a)
+    head_v = {"scale_shift_table": params["scale_shift_table"], "proj_out.weight": params["proj_out.weight"],
+              "proj_out.bias": params["proj_out.bias"]}
+    head_a = {"scale_shift_table": params["audio_scale_shift_table"],
+              "proj_out.weight": params["audio_proj_out.weight"], "proj_out.bias": params["audio_proj_out.bias"]}
+    return (output_head(head_v, v[None], emb_v.reshape(1, 1, dv), eps=eps, bf16_graph=bf16_graph)[0],
+            output_head(head_a, a[None], emb_a.reshape(1, 1, da), eps=eps, bf16_graph=bf16_graph)[0])
 
 
 def to_denoised(latent, velocity, timesteps) -> np.ndarray:

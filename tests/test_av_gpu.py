@@ -71,3 +71,91 @@ def test_disabled_audio_still_feeds_video(device):
     assert out_a is off
     alone, _ = block(video, None)
     assert not torch.equal(out_v.x, alone.x)
+
+
+# ---- the joint transformer forward and denoising step ------------------------------------------
+
+CHANNELS = 32
+
+
+def _model_case():
+    import oracle
+
+    p = workloads.ltx_av_model_params(SPEC, AUDIO, 2, in_channels=CHANNELS, out_channels=CHANNELS)
+    op = {}
+    for name, value in p.items():
+        op[name] = [{k: v.float().numpy() for k, v in b.items()} for b in value] if name == "blocks" \
+            else value.float().numpy()
+    inputs = workloads.ltx_av_model_inputs(SPEC, AUDIO, in_channels=CHANNELS)
+    vpos, apos = inputs["positions"].numpy(), inputs["audio_positions"].numpy()
+    inner = AUDIO.heads * AUDIO.head_dim
+    pes = (oracle.precompute_freqs_cis(vpos, dim=SPEC.dim, use_middle_indices_grid=True, num_attention_heads=SPEC.heads),
+           oracle.precompute_freqs_cis(apos, dim=AUDIO.dim, max_pos=(20,), use_middle_indices_grid=True,
+                                       num_attention_heads=AUDIO.heads),
+           oracle.precompute_freqs_cis(vpos[:, 0:1], dim=inner, max_pos=(20,), use_middle_indices_grid=True,
+                                       num_attention_heads=AUDIO.heads),
+           oracle.precompute_freqs_cis(apos[:, 0:1], dim=inner, max_pos=(20,), use_middle_indices_grid=True,
+                                       num_attention_heads=AUDIO.heads))
+    return p, op, inputs, pes
+
+
+def _oracle_velocities(op, inputs, pes, sigma, bf16_graph=False):
+    import oracle
+
+    s = np.array([sigma], np.float32)
+    return oracle.ltx_av_forward(op, inputs["latent"][0].float().numpy(), inputs["audio_latent"][0].float().numpy(),
+                                 inputs["context"][0].float().numpy(), inputs["audio_context"][0].float().numpy(),
+                                 s, s, s, s, pes, heads=SPEC.heads, audio_heads=AUDIO.heads, num_blocks=2,
+                                 bf16_graph=bf16_graph)
+
+
+def test_av_transformer_forward_matches_oracle(device):
+    from kinomlx_amd.ltx2.wrappers import Modality
+
+    p, op, inputs, pes = _model_case()
+    model = workloads.build_ltx_av_model(SPEC, AUDIO, p, device, in_channels=CHANNELS, out_channels=CHANNELS)
+    sig = torch.full((1,), 0.7, device=device)
+    video = Modality(latent=inputs["latent"].to(device), context=inputs["context"].to(device), timesteps=sig,
+                     sigma=sig, positions=inputs["positions"].to(device))
+    audio = Modality(latent=inputs["audio_latent"].to(device), context=inputs["audio_context"].to(device),
+                     timesteps=sig, sigma=sig, positions=inputs["audio_positions"].to(device))
+    vel_v, vel_a = model(video, audio)
+    ref_v, ref_a = _oracle_velocities(op, inputs, pes, 0.7)
+    graph_v, graph_a = _oracle_velocities(op, inputs, pes, 0.7, bf16_graph=True)
+    _check(vel_v[0].float().cpu().numpy(), ref_v, graph_v)
+    _check(vel_a[0].float().cpu().numpy(), ref_a, graph_a)
+
+
+def test_av_denoise_step_matches_oracle(device):
+    import oracle
+    from kinomlx_amd.ltx2.denoise import denoise_step
+    from kinomlx_amd.ltx2.state import LatentState
+    from kinomlx_amd.ltx2.wrappers import X0Model
+    from oracle.ops import to_bf16
+
+    p, op, inputs, pes = _model_case()
+    model = X0Model(workloads.build_ltx_av_model(SPEC, AUDIO, p, device, in_channels=CHANNELS,
+                                                 out_channels=CHANNELS))
+
+    def state(latent, positions):
+        latent = latent.to(device)
+        return LatentState(latent=latent, denoise_mask=torch.ones((1, latent.shape[1], 1), device=device),
+                           positions=positions.to(device), clean_latent=latent)
+
+    sigma, nxt = 0.7, 0.45
+    vs, aus = denoise_step(state(inputs["latent"], inputs["positions"]),
+                           state(inputs["audio_latent"], inputs["audio_positions"]), sigma=sigma, sigma_next=nxt,
+                           transformer=model, video_context=inputs["context"].to(device),
+                           audio_context=inputs["audio_context"].to(device))
+
+    def step(graph):
+        out = []
+        for lat, vel in zip((inputs["latent"], inputs["audio_latent"]), _oracle_velocities(op, inputs, pes, sigma, graph)):
+            x = lat.float().numpy()
+            d = to_bf16(oracle.to_denoised(x, to_bf16(vel)[None], np.array([sigma], np.float32)))
+            out.append(to_bf16(oracle.euler_step(x, d, sigma, nxt))[0])
+        return out
+
+    (ref_v, ref_a), (g_v, g_a) = step(False), step(True)
+    _check(vs.latent[0].float().cpu().numpy(), ref_v, g_v)
+    _check(aus.latent[0].float().cpu().numpy(), ref_a, g_a)
