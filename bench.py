@@ -109,6 +109,9 @@ def main() -> int:
                         help="time one whole denoising step of the video transformer instead of one block")
     parser.add_argument("--blocks", type=int, default=48, help="blocks of the --denoise-step transformer")
     parser.add_argument("--grid", type=str, default="", help="T,H,W latent grid for --denoise-step")
+    parser.add_argument("--audio-tokens", type=int, default=0,
+                        help="with --denoise-step: add the audio stream (this many latents, 25 per second) and "
+                             "the A/V cross-attention to every block")
     parser.add_argument("--load-checkpoint", action="store_true",
                         help="time loading a --blocks-block checkpoint into HBM, plain and quantized on load")
     parser.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -375,8 +378,12 @@ def denoise_main(args) -> int:
     spec = workloads.CONFIGS[args.config]
     if args.grid:
         spec = dataclasses.replace(spec, grid=tuple(int(v) for v in args.grid.split(",")))
+    audio = workloads.LTXAudioSpec(tokens=args.audio_tokens, text_tokens=spec.text_tokens) if args.audio_tokens else None
     build0 = time.perf_counter()
-    model = X0Model(workloads.random_ltx_model(spec, args.blocks, device))
+    if audio is None:
+        model = X0Model(workloads.random_ltx_model(spec, args.blocks, device))
+    else:
+        model = X0Model(workloads.random_ltx_av_model(spec, audio, args.blocks, device))
     torch.cuda.synchronize()
     build_s = time.perf_counter() - build0
     gen = torch.Generator(device=device).manual_seed(1)
@@ -385,10 +392,19 @@ def denoise_main(args) -> int:
     positions = workloads.ltx_positions(spec.grid).to(device)
     state = LatentState(latent=latent, denoise_mask=torch.ones((1, spec.tokens, 1), device=device),
                         positions=positions, clean_latent=latent)
+    audio_state = audio_context = None
+    if audio is not None:
+        a_latent = torch.randn((1, audio.tokens, 128), generator=gen, device=device).to(torch.bfloat16)
+        audio_context = torch.randn((1, audio.text_tokens, audio.dim), generator=gen, device=device).to(torch.bfloat16)
+        start = torch.arange(audio.tokens, dtype=torch.float32, device=device)
+        audio_state = LatentState(latent=a_latent, denoise_mask=torch.ones((1, audio.tokens, 1), device=device),
+                                  positions=torch.stack([start, start + 1.0], dim=-1)[None, None],
+                                  clean_latent=a_latent)
     sigmas = (0.909375, 0.725, 0.421875)
 
     def step(s):
-        return denoise_step(s, sigma=sigmas[0], sigma_next=sigmas[1], transformer=model, video_context=context)[0]
+        return denoise_step(s, audio_state, sigma=sigmas[0], sigma_next=sigmas[1], transformer=model,
+                            video_context=context, audio_context=audio_context)[0]
 
     for _ in range(args.warmup):
         step(state)
@@ -418,6 +434,7 @@ def denoise_main(args) -> int:
     if args.breakdown:
         for label, ms in sorted(kernel_ms.items(), key=lambda kv: -kv[1]):
             print(f"{ms:9.3f} ms/step  x{len(per_kernel[label]) // args.steps}  {label}", file=sys.stderr)
+    same_work = (spec.tokens == 5376 and audio is not None and args.blocks == 48 and not spec.bits)
     result = {
         "metric": "LTX-2 video denoising step ms (X0 transformer + Euler update + finite check)",
         "value": round(ms_per_step, 2),
@@ -428,11 +445,13 @@ def denoise_main(args) -> int:
         "ms_per_step": round(ms_per_step, 2),
         "higher_is_better": False,
         "scaling": "weak",
-        "vs_baseline": None,
+        "vs_baseline": round(ms_per_step / 18000.0, 5) if same_work else None,
         "dtype": "bf16",
         "data": "synthetic (N(0,0.02) weights drawn on the device, N(0,1) latent and context; no checkpoint)",
         "config": {
-            "workload": f"LTX2-like video transformer, {args.blocks} blocks, BASELINE config {args.config} block shape",
+            "workload": (f"LTX2-like {'joint audio/video' if audio else 'video'} transformer, {args.blocks} blocks, "
+                         f"BASELINE config {args.config} block shape"),
+            "audio_tokens": audio.tokens if audio else 0,
             "video_tokens": spec.tokens,
             "latent_grid_thw": list(spec.grid),
             "text_tokens": spec.text_tokens,
@@ -442,6 +461,8 @@ def denoise_main(args) -> int:
             "batch": 1,
         },
         "block_tflops": round(block_flops / (ms_per_step * 1e-3) / 1e12, 1),
+        "published_reference": {"s_per_step": 18.0, "workload": "stage-2 768x448x121: 5376 video tokens, 48 joint "
+                                "A/V blocks, FP16, Apple silicon", "source": "docs/ltx2/performance.md:17-28"},
         "attention_ms": round(attn_ms, 2),
         "gemm_ms": round(gemm_ms, 2),
         "outside_block_kernels_ms": round(sum(v for k, v in kernel_ms.items() if name_of[k] in outside), 3),
