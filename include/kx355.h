@@ -92,6 +92,20 @@ int kx_rmsnorm_rope_bf16(const void* x, int64_t ldx, void* y, int64_t ldy, int64
                          int64_t head_dim, kx_stream_t stream);
 
 /*
+ * kx_attention_gqa_fwd_bf16 with an additive score bias (the reference's masked SDPA,
+ * kinomlx/models/ltx2/transformer/attention.py:136-185, masks from preprocessing.py:85-105):
+ * score(b, h, i, j) = q_i . k_j * scale + bias[b * bias_bs + h * bias_hs + i * bias_qs + j],
+ * bias bf16 with keys contiguous (strides in elements, 0 broadcasts; multiples of 4, 8-byte
+ * aligned). A bias below -1e20 * scale (-inf, the bf16 minimum) removes the key (p = 0); a row
+ * with every key removed averages V uniformly (the reference's equal finite scores).
+ */
+int kx_attention_bias_fwd_bf16(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v,
+                               int64_t ldv, void* o, int64_t ldo, int64_t batch, int64_t tq,
+                               int64_t tk, int64_t heads, int64_t kv_heads, int64_t head_dim,
+                               float scale, const void* gate, int64_t ld_gate, const void* bias,
+                               int64_t bias_bs, int64_t bias_hs, int64_t bias_qs, kx_stream_t stream);
+
+/*
  * Split-half RoPE, standalone: replaces split_rope.rotate (kinomlx/kernels/split_rope.py:144-163,
  * arithmetic :35-56). x/y are (batch, tokens, heads * 2 * half) rows at stride ldx/ldy; tables
  * token-major (table_batch, tokens, heads * half), table_batched selects per-batch tables.

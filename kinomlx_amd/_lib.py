@@ -64,6 +64,10 @@ SIGNATURES: dict[str, list] = {
     "kx_attention_gqa_fwd_bf16": [
         _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _I64, _P,
     ],
+    "kx_attention_bias_fwd_bf16": [
+        _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _I64, _P, _I64, _I64,
+        _I64, _P,
+    ],
     "kx_gemm_bf16": [
         _P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _I64, _P, _I64, _I64, _P,
     ],
@@ -317,11 +321,21 @@ def launch_rope_pair(x, out, cos, sin, *, heads, head_dim, table_ld, table_hs, t
     )
 
 
-def launch_attention(q, k, v, out, *, batch, tq, tk, heads, head_dim, scale, gate=None, kv_heads=None) -> None:
-    _check_gpu("attention", q, k, v, out, gate)
+def launch_attention(q, k, v, out, *, batch, tq, tk, heads, head_dim, scale, gate=None, kv_heads=None,
+                     bias=None, bias_strides=None) -> None:
+    _check_gpu("attention", q, k, v, out, gate, bias)
     ld_gate = 0
     if gate is not None:
         _, _, ld_gate = _rows(gate, "attention gate")
+    if bias is not None:
+        if bias.dtype != torch.bfloat16 or bias_strides is None:
+            raise ValueError("attention bias: bfloat16 values with (batch, head, query) strides")
+        _call(
+            "kx_attention_bias_fwd_bf16", _ptr(q), q.stride(-2), _ptr(k), k.stride(-2), _ptr(v), v.stride(-2),
+            _ptr(out), out.stride(-2), batch, tq, tk, heads, kv_heads or heads, head_dim, scale, _ptr(gate), ld_gate,
+            _ptr(bias), *bias_strides, _stream(),
+        )
+        return
     if kv_heads is not None and kv_heads != heads:
         _call(
             "kx_attention_gqa_fwd_bf16", _ptr(q), q.stride(-2), _ptr(k), k.stride(-2), _ptr(v),

@@ -68,12 +68,25 @@ __device__ __forceinline__ bf16x8 read_vt(const uint8_t* p, int second) {
   return __builtin_bit_cast(bf16x8, make_uint4(lo2.x, lo2.y, hi2.x, hi2.y));
 }
 
-template <int D>
+// Optional additive score bias (the reference's SDPA mask): bias[b * bs + h * hs + q * qs + key]
+// in bf16, added as bias / scale to the raw score (so that the scaled score gains `bias`). A bias
+// below -1e20 after that division (-inf, the bf16 minimum) removes the key: its score becomes the
+// sentinel -1e30 exactly (the raw score is far below its ulp), whose p is 0 — or 1 when every key
+// the row has seen is removed, so that a fully masked row averages V uniformly, as the
+// reference's equal finite scores do. (The sentinel's p is selected, not computed: the FMA of
+// the exp2 argument would leave the rounding error of -1e30 * scale, ~1e21, in the exponent.)
+struct ScoreBias {
+  const uint16_t* ptr;
+  int64_t bs, hs, qs;
+  float mul;  // 1 / scale
+};
+
+template <int D, bool BIAS>
 __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
     const uint16_t* __restrict__ Q, int64_t ldq, const uint16_t* __restrict__ K, int64_t ldk,
     const uint16_t* __restrict__ V, int64_t ldv, uint16_t* __restrict__ O, int64_t ldo, int tq,
     int tk, int heads, int kv_group, float scale_log2, const uint16_t* __restrict__ gate,
-    int64_t ld_gate, int qtiles) {
+    int64_t ld_gate, int qtiles, ScoreBias bias) {
   constexpr int ROWB = D * 2;             // bytes per K / V row
   constexpr int CPR = ROWB / 16;          // 16-byte chunks per row
   constexpr int RPI = 64 / CPR;           // rows per DMA instruction
@@ -181,6 +194,29 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
       }
     }
     const int j0 = it * BKV;
+    if constexpr (BIAS) {
+      // lane: query qrow, keys j0 + 32 kb + 8 g + 4 lhalf + (0..3) = elements 4 g .. 4 g + 3
+      const uint16_t* brow = bias.ptr + (int64_t)b * bias.bs + (int64_t)h * bias.hs + (int64_t)qrow * bias.qs;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int key = j0 + kb * 32 + 8 * g + 4 * lhalf;
+          float bv[4];
+          if (key + 3 < tk) {
+            const uint2 w = *reinterpret_cast<const uint2*>(brow + key);
+            bv[0] = lo_f(w.x); bv[1] = hi_f(w.x); bv[2] = lo_f(w.y); bv[3] = hi_f(w.y);
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) bv[i] = key + i < tk ? bf2f(brow[key + i]) : 0.0f;
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float add = bv[i] * bias.mul;
+            s[kb][4 * g + i] += add < -1e20f ? -1e30f : add;
+          }
+        }
+    }
     if (j0 + BKV > tk) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
@@ -209,6 +245,7 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
 
     // P^T in bf16 as the B operand: elements 8hf .. 8hf+7 of block kb
     const float mc = m_run * scale_log2;
+    const float removed_p = m_run == -1e30f ? 1.0f : 0.0f;  // p of a removed key (bias variant)
     bf16x8 pb[2][2];
     float psum = 0.0f;
 #pragma unroll
@@ -217,7 +254,8 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
       for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float p = __builtin_amdgcn_exp2f(fmaf(s[kb][8 * hf + e], scale_log2, -mc));
+          float p = __builtin_amdgcn_exp2f(fmaf(s[kb][8 * hf + e], scale_log2, -mc));
+          if constexpr (BIAS) p = s[kb][8 * hf + e] == -1e30f ? removed_p : p;
           psum += p;
           pb[kb][hf][e] = (__bf16)p;
         }
@@ -256,13 +294,20 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
 template <int D>
 int launch_attn(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
                 void* o, int64_t ldo, int64_t batch, int64_t tq, int64_t tk, int64_t heads,
-                int64_t kv_heads, float scale, const void* gate, int64_t ld_gate, hipStream_t s) {
+                int64_t kv_heads, float scale, const void* gate, int64_t ld_gate, ScoreBias bias,
+                hipStream_t s) {
   const int qtiles = (int)((tq + BQ - 1) / BQ);
   const int64_t blocks = (int64_t)qtiles * heads * batch;
-  attn_fwd_kernel<D><<<(unsigned)blocks, NWAVE * 64, 0, s>>>(
-      (const uint16_t*)q, ldq, (const uint16_t*)k, ldk, (const uint16_t*)v, ldv, (uint16_t*)o,
-      ldo, (int)tq, (int)tk, (int)heads, (int)(heads / kv_heads), scale * 1.4426950408889634f,
-      (const uint16_t*)gate, ld_gate, qtiles);
+  if (bias.ptr)
+    attn_fwd_kernel<D, true><<<(unsigned)blocks, NWAVE * 64, 0, s>>>(
+        (const uint16_t*)q, ldq, (const uint16_t*)k, ldk, (const uint16_t*)v, ldv, (uint16_t*)o,
+        ldo, (int)tq, (int)tk, (int)heads, (int)(heads / kv_heads), scale * 1.4426950408889634f,
+        (const uint16_t*)gate, ld_gate, qtiles, bias);
+  else
+    attn_fwd_kernel<D, false><<<(unsigned)blocks, NWAVE * 64, 0, s>>>(
+        (const uint16_t*)q, ldq, (const uint16_t*)k, ldk, (const uint16_t*)v, ldv, (uint16_t*)o,
+        ldo, (int)tq, (int)tk, (int)heads, (int)(heads / kv_heads), scale * 1.4426950408889634f,
+        (const uint16_t*)gate, ld_gate, qtiles, bias);
   return check_launch("kx_attention_fwd_bf16");
 }
 
@@ -275,7 +320,8 @@ namespace {
 int attention_entry(const char* name, const void* q, int64_t ldq, const void* k, int64_t ldk,
                     const void* v, int64_t ldv, void* o, int64_t ldo, int64_t batch, int64_t tq,
                     int64_t tk, int64_t heads, int64_t kv_heads, int64_t head_dim, float scale,
-                    const void* gate, int64_t ld_gate, kx_stream_t stream) {
+                    const void* gate, int64_t ld_gate, kx_stream_t stream,
+                    ScoreBias bias = ScoreBias{nullptr, 0, 0, 0, 0.0f}) {
   KX_REQUIRE(q && k && v && o, "%s: null tensor", name);
   KX_REQUIRE(head_dim == 64 || head_dim == 128, "%s: head_dim must be 64 or 128, got %lld", name,
              (long long)head_dim);
@@ -297,9 +343,9 @@ int attention_entry(const char* name, const void* q, int64_t ldq, const void* k,
   if (tq == 0 || batch == 0) return KX_OK;
   if (head_dim == 128)
     return launch_attn<128>(q, ldq, k, ldk, v, ldv, o, ldo, batch, tq, tk, heads, kv_heads, scale,
-                            gate, ld_gate, (hipStream_t)stream);
+                            gate, ld_gate, bias, (hipStream_t)stream);
   return launch_attn<64>(q, ldq, k, ldk, v, ldv, o, ldo, batch, tq, tk, heads, kv_heads, scale,
-                         gate, ld_gate, (hipStream_t)stream);
+                         gate, ld_gate, bias, (hipStream_t)stream);
 }
 }  // namespace
 
@@ -319,4 +365,22 @@ extern "C" int kx_attention_fwd_bf16(const void* q, int64_t ldq, const void* k, 
                                      int64_t ld_gate, kx_stream_t stream) {
   return attention_entry("kx_attention_fwd_bf16", q, ldq, k, ldk, v, ldv, o, ldo, batch, tq, tk,
                          heads, heads, head_dim, scale, gate, ld_gate, stream);
+}
+
+extern "C" int kx_attention_bias_fwd_bf16(const void* q, int64_t ldq, const void* k, int64_t ldk,
+                                          const void* v, int64_t ldv, void* o, int64_t ldo,
+                                          int64_t batch, int64_t tq, int64_t tk, int64_t heads,
+                                          int64_t kv_heads, int64_t head_dim, float scale,
+                                          const void* gate, int64_t ld_gate, const void* bias,
+                                          int64_t bias_bs, int64_t bias_hs, int64_t bias_qs,
+                                          kx_stream_t stream) {
+  KX_REQUIRE(bias, "kx_attention_bias_fwd_bf16: null bias");
+  KX_REQUIRE(aligned8(bias) && bias_bs >= 0 && bias_hs >= 0 && bias_qs >= 0 && bias_bs % 4 == 0 &&
+                 bias_hs % 4 == 0 && bias_qs % 4 == 0,
+             "kx_attention_bias_fwd_bf16: bias must be 8-byte aligned with non-negative strides that "
+             "are multiples of 4 elements");
+  KX_REQUIRE(scale > 0.0f && isfinite(scale), "kx_attention_bias_fwd_bf16: scale must be positive");
+  return attention_entry("kx_attention_bias_fwd_bf16", q, ldq, k, ldk, v, ldv, o, ldo, batch, tq, tk,
+                         heads, kv_heads, head_dim, scale, gate, ld_gate, stream,
+                         ScoreBias{(const uint16_t*)bias, bias_bs, bias_hs, bias_qs, 1.0f / scale});
 }

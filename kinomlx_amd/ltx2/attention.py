@@ -263,10 +263,8 @@ class Attention:
     def attend(self, value: torch.Tensor, *, context: torch.Tensor | None = None,
                mask: torch.Tensor | None = None, pe=None, k_pe=None) -> torch.Tensor:
         """Everything before the output projection (gated attention output ``(B, T, inner)``)."""
-        if mask is not None:
-            raise ValueError("masked attention is not built for MI355X")
         gate, q, k, v = self.project(value, context=context, pe=pe, k_pe=k_pe)
-        return _dense.batched_attention(q, k, v, heads=self.heads, gate=gate)
+        return _dense.batched_attention(q, k, v, heads=self.heads, gate=gate, mask=mask)
 
     def __call__(self, value: torch.Tensor, *, context: torch.Tensor | None = None,
                  mask: torch.Tensor | None = None, pe=None, k_pe=None, sparse=None,

@@ -40,9 +40,39 @@ def applies(query: torch.Tensor, key: torch.Tensor, *, heads: int) -> bool:
     )
 
 
+def score_bias(mask: torch.Tensor, *, batch: int, heads: int, tq: int, tk: int) -> tuple[torch.Tensor, tuple]:
+    """An SDPA mask as the kernel's additive bf16 bias and its (batch, head, query) strides.
+
+    Shapes follow ``_prepare_attention_mask`` (``attention.py:136-141``): ``(Tq, Tk)`` is shared
+    by every batch and head, ``(B, Tq, Tk)`` by every head, ``(B | 1, H | 1, Tq | 1, Tk)`` as
+    given. A boolean mask keeps its True keys (False -> -inf); other dtypes are cast to bf16 and
+    added to the scaled scores. Broadcast axes get stride 0; rows are padded to a multiple of 4
+    keys when the layout needs it."""
+    if mask.dim() == 2:
+        mask = mask[None, None]
+    elif mask.dim() == 3:
+        mask = mask[:, None]
+    if mask.dim() != 4 or mask.shape[-1] != tk:
+        raise ValueError(f"attention mask must end in the key axis ({tk}), got {tuple(mask.shape)}")
+    for axis, full in zip(range(3), (batch, heads, tq)):
+        if mask.shape[axis] not in (1, full):
+            raise ValueError(f"attention mask {tuple(mask.shape)} does not broadcast to ({batch}, {heads}, {tq}, {tk})")
+    if mask.dtype == torch.bool:
+        mask = torch.where(mask, 0.0, float("-inf"))
+    mask = mask.to(torch.bfloat16)
+    strides = [mask.stride(a) if mask.shape[a] != 1 else 0 for a in range(3)]
+    if mask.stride(-1) != 1 or any(st % 4 for st in strides) or mask.data_ptr() % 8:
+        padded = torch.zeros((*mask.shape[:3], (tk + 3) // 4 * 4), dtype=torch.bfloat16, device=mask.device)
+        padded[..., :tk] = mask
+        mask = padded
+        strides = [mask.stride(a) if mask.shape[a] != 1 else 0 for a in range(3)]
+    return mask, tuple(strides)
+
+
 def _attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, heads: int, batch: int,
                tq: int, tk: int, dim: int, gate: torch.Tensor | None, scale: float | None,
-               out: torch.Tensor | None = None, kv_heads: int | None = None) -> torch.Tensor:
+               out: torch.Tensor | None = None, kv_heads: int | None = None,
+               mask: torch.Tensor | None = None) -> torch.Tensor:
     if out is None:
         out = torch.empty((batch, tq, heads * dim), dtype=q.dtype, device=q.device)
     elif (out.dtype != q.dtype or tuple(out.shape) != (batch, tq, heads * dim) or out.stride(-1) != 1
@@ -52,9 +82,12 @@ def _attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, heads: int,
         if gate.dtype != torch.bfloat16 or tuple(gate.shape[-1:]) != (heads,):
             raise ValueError(f"attention gate must be bf16 (..., {heads})")
         gate = gate.reshape(batch * tq, heads)
+    bias = strides = None
+    if mask is not None:
+        bias, strides = score_bias(mask, batch=batch, heads=heads, tq=tq, tk=tk)
     _lib.launch_attention(
         q, k, v, out, batch=batch, tq=tq, tk=tk, heads=heads, head_dim=dim,
-        scale=dim ** -0.5 if scale is None else scale, gate=gate, kv_heads=kv_heads,
+        scale=dim ** -0.5 if scale is None else scale, gate=gate, kv_heads=kv_heads, bias=bias, bias_strides=strides,
     )
     return out
 
@@ -96,12 +129,13 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, heads:
 
 def batched_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, heads: int,
                       gate: torch.Tensor | None = None, scale: float | None = None,
-                      out: torch.Tensor | None = None, kv_heads: int | None = None) -> torch.Tensor:
+                      out: torch.Tensor | None = None, kv_heads: int | None = None,
+                      mask: torch.Tensor | None = None) -> torch.Tensor:
     """``(batch, tokens, heads * dim)`` form of ``dense_attention``; q/k/v (and ``out``, when
     given) may be strided row views, e.g. column slices of a fused QKV projection or of the
     buffer the next projection reads. With ``kv_heads`` (grouped-query attention) k and v hold
     ``kv_heads * dim`` columns and query head ``h`` reads key/value head
-    ``h // (heads // kv_heads)``."""
+    ``h // (heads // kv_heads)``. ``mask`` is the SDPA mask (``score_bias``)."""
     if q.dim() != 3 or k.dim() != 3 or v.shape != k.shape or q.shape[0] != k.shape[0]:
         raise ValueError("batched attention needs (batch, tokens, heads * dim) q, k and v")
     width = q.shape[-1]
@@ -118,7 +152,7 @@ def batched_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, head
         if t.stride(-1) != 1 or (batch > 1 and t.stride(0) != t.shape[1] * t.stride(1)):
             raise ValueError(f"attention {name} must have contiguous rows, evenly strided over the batch")
     return _attention(q, k, v, heads=heads, batch=batch, tq=tq, tk=tk, dim=dim, gate=gate, scale=scale, out=out,
-                      kv_heads=kv_heads)
+                      kv_heads=kv_heads, mask=mask)
 
 
-__all__ = ["HEAD_DIMS", "applies", "batched_attention", "dense_attention"]
+__all__ = ["HEAD_DIMS", "applies", "batched_attention", "dense_attention", "score_bias"]

@@ -30,6 +30,11 @@ from .transformer import BasicAVTransformerBlock, TransformerArgs, TransformerCo
 from .wrappers import Modality
 
 
+# bf16 limits used by the reference's masks (``preprocessing.py:14-23``)
+_MINIMUM = -3.3895313892515355e38
+_TINY = 1.1754943508222875e-38
+
+
 class ModalityPreprocessor:
     """Prepare one stream and its A/V cross-attention inputs (``preprocessing.py:26-214``):
     ``patchify_proj``, the AdaLN rows, the prompt rows, the RoPE tables, and with a cross
@@ -64,6 +69,31 @@ class ModalityPreprocessor:
             raise ValueError("modality sigma must be scalar or have shape (batch,)")
         return value
 
+    def _context_mask(self, mask: torch.Tensor | None) -> torch.Tensor | None:
+        """Text mask -> additive bias in the compute dtype (``preprocessing.py:85-96``): float masks
+        as given ((B, Tc) -> (B, 1, 1, Tc), (B, T, Tc) -> (B, 1, T, Tc)); others 0 where set and the
+        dtype minimum where not."""
+        if mask is None:
+            return None
+        dtype = self.model.compute_dtype
+        if mask.dtype in (torch.float16, torch.bfloat16, torch.float32):
+            if mask.dim() == 2:
+                mask = mask[:, None, None, :]
+            elif mask.dim() == 3:
+                mask = mask[:, None, :, :]
+            return mask.to(dtype)
+        return ((mask.to(dtype) - 1.0) * -_MINIMUM).reshape(mask.shape[0], 1, -1, mask.shape[-1])
+
+    @staticmethod
+    def _self_attention_mask(mask: torch.Tensor | None, dtype: torch.dtype) -> torch.Tensor | None:
+        """Soft self-attention mask in [0, 1] -> log bias (``preprocessing.py:98-105``): log(max(m,
+        tiny)) where m > 0, the dtype minimum elsewhere, as (B, 1, T, T)."""
+        if mask is None:
+            return None
+        value = mask.float()
+        log_bias = torch.log(torch.clamp(value, min=_TINY))
+        return torch.where(value > 0, log_bias, torch.full_like(value, _MINIMUM))[:, None, ...].to(dtype)
+
     def _rope(self, positions: torch.Tensor, *, dim: int, max_pos: tuple[int, ...]):
         m = self.model
         return precompute_freqs_cis(positions, dim=dim, out_dtype=torch.float32, theta=m.theta, max_pos=max_pos,
@@ -75,8 +105,6 @@ class ModalityPreprocessor:
         m = self.model
         if modality.keyframes_mask is not None:
             raise ValueError("keyframe position embeddings are not built for MI355X")
-        if modality.context_mask is not None or modality.attention_mask is not None:
-            raise ValueError("masked attention is not built for MI355X")
         hidden = self._part("patchify_proj")(modality.latent)
         batch = hidden.shape[0]
         timestep, embedded = self._timestep(modality.timesteps, self._part("adaln_single"), batch, m.timestep_scale)
@@ -88,6 +116,8 @@ class ModalityPreprocessor:
         args = TransformerArgs(
             x=hidden,
             context=modality.context.reshape(batch, -1, self.inner_dim),
+            context_mask=self._context_mask(modality.context_mask),
+            self_attention_mask=self._self_attention_mask(modality.attention_mask, m.compute_dtype),
             timesteps=timestep,
             positional_embeddings=modality.positional_embeddings
             or self._rope(modality.positions, dim=self.inner_dim, max_pos=self.max_pos),

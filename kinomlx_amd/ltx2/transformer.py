@@ -1,10 +1,10 @@
-"""The LTX-2 DiT block's video branch on MI355X.
+"""The LTX-2 DiT block on MI355X.
 
 Mirror of ``kinomlx/models/ltx2/transformer/transformer.py``: the modulation helpers
 (``adaln``, ``gated_residual``, ``modulate``, ``gate``; the reference's private ``_adaln`` ...
 and their ``mx.compile``d forms, ``:16-45``), ``TransformerConfig``, ``TransformerArgs`` and
-``BasicAVTransformerBlock`` with its video branch (``:225-276,373-392``) and text cross-attention
-(``:201-223``).
+``BasicAVTransformerBlock`` with its video and audio streams (``:225-421``), text
+cross-attention (``:201-223``) and audio <-> video cross-attention (``:310-371``).
 
 Kernel schedule of one block (B=1, T video tokens, Tc text tokens):
   AdaLN(x) -> [QKV GEMM, gate GEMM (2*sigmoid)] -> Q/K norm+RoPE -> flash attention (gated)
@@ -15,8 +15,10 @@ block's three branches the residual stream is carried in FP32 (written by the ou
 epilogues, read by the next AdaLN and epilogue) and rounded to bf16 once, by the last epilogue;
 every other intermediate is bf16. The reference rounds the stream after each branch
 (``transformer.py:26-30`` casts to ``value.dtype``); carrying it costs 2 x T x D x 2 extra bytes
-per branch and removes two of the block's output roundings. The audio stream, A/V
-cross-attention, masks and sparse attention are not built.
+per branch and removes two of the block's output roundings. The audio stream follows the same
+schedule at its own width, then the A/V cross-attention of each stream reads the other's
+(AdaLN-modulated) value. Masks become an additive score bias inside the attention kernel;
+sparse (Sol-Attn) attention is not built.
 """
 
 from __future__ import annotations
@@ -227,20 +229,18 @@ class BasicAVTransformerBlock:
         prompt = prompt.contiguous()
         query = adaln(value, ada[:, :, 7], ada[:, :, 6], self.norm_eps)
         context = modulate(args.context, prompt[:, :, 1], prompt[:, :, 0])
-        if args.context_mask is not None:
-            raise ValueError("masked text cross-attention is not built for MI355X")
-        return attention(query, context=context, residual=value, gate=ada[:, :, 8], out_dtype=torch.float32)
+        return attention(query, context=context, mask=args.context_mask, residual=value, gate=ada[:, :, 8],
+                         out_dtype=torch.float32)
 
     def _first_branches(self, args: TransformerArgs, table, attn1: Attention, attn2: Attention, prompt_table):
         """Self-attention then text cross-attention, FP32 residual out."""
-        if args.self_attention_mask is not None:
-            raise ValueError("masked self-attention is not built for MI355X")
         if args.sparse_attention is not None:
             raise ValueError("sparse (Sol-Attn) attention is not built for MI355X")
         x = args.x
         ada = (table[None, None].float() + args.timesteps.float()).contiguous()
         normalized = adaln(x, ada[:, :, 1], ada[:, :, 0], self.norm_eps)
-        x1 = attn1(normalized, pe=args.positional_embeddings, residual=x, gate=ada[:, :, 2], out_dtype=torch.float32)
+        x1 = attn1(normalized, pe=args.positional_embeddings, mask=args.self_attention_mask, residual=x,
+                   gate=ada[:, :, 2], out_dtype=torch.float32)
         return self._text_cross_attention(x1, args, ada, attn2, prompt_table), ada
 
     def __call__(self, video: TransformerArgs | None, audio: TransformerArgs | None = None):

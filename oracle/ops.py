@@ -308,13 +308,15 @@ def krea_apply_rotary(queries, keys, cos, sin) -> tuple[np.ndarray, np.ndarray]:
 # Attention and linear products
 
 
-def attention(q, k, v, *, heads: int, scale: float | None = None) -> np.ndarray:
+def attention(q, k, v, *, heads: int, scale: float | None = None, bias=None) -> np.ndarray:
     """Non-causal softmax attention on token-major flattened heads.
 
     ``q`` is ``(Tq, H * Dh)``, ``k``/``v`` are ``(Tk, H * Dh)``; output ``(Tq, H * Dh)``.
-    ``softmax(q k^T * Dh^-0.5) v`` per head, FP32 scores and accumulation (contract of
-    ``kinomlx/models/ltx2/kernels/dense_attention.py:87-153``; SDPA fallback
-    ``kinomlx/models/ltx2/transformer/attention.py:144-161``).
+    ``softmax(q k^T * Dh^-0.5 + bias) v`` per head, FP32 scores and accumulation (contract of
+    ``kinomlx/models/ltx2/kernels/dense_attention.py:87-153``; SDPA
+    ``kinomlx/models/ltx2/transformer/attention.py:144-185``). ``bias`` (optional, additive, the
+    SDPA mask) broadcasts as ``(H | 1, Tq | 1, Tk)``; a row whose biases are all the dtype
+    minimum keeps equal scores, as in the reference.
     """
     q = _f32(q)
     k = _f32(k)
@@ -324,6 +326,8 @@ def attention(q, k, v, *, heads: int, scale: float | None = None) -> np.ndarray:
     dh = width // heads
     sc = F32(dh ** -0.5 if scale is None else scale)
     out = np.empty((tq, width), F32)
+    if bias is not None:
+        bias = np.broadcast_to(_f32(bias), (heads, tq, tk))
     for h in range(heads):
         sl = slice(h * dh, (h + 1) * dh)
         qh = q[:, sl]
@@ -332,6 +336,8 @@ def attention(q, k, v, *, heads: int, scale: float | None = None) -> np.ndarray:
         for start in range(0, tq, 2048):
             stop = min(tq, start + 2048)
             scores = (qh[start:stop] @ kh.T) * sc
+            if bias is not None:
+                scores = (scores + bias[h, start:stop]).astype(F32)
             scores -= scores.max(axis=-1, keepdims=True)
             np.exp(scores, out=scores)
             denom = scores.sum(axis=-1, keepdims=True, dtype=F32)
