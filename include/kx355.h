@@ -193,6 +193,20 @@ int kx_gemm_bf16(const void* a, int64_t lda, const void* w, int64_t ldw, const v
                  int64_t gate_stride, kx_stream_t stream);
 
 /*
+ * kx_gemm_bf16 for products whose output tiles leave most CUs idle (a few hundred rows): K is
+ * cut into `splits` slices, each multiplied by its own row of workgroups into an fp32 partial
+ * product in `workspace` (splits * m * n floats, caller-owned), then one pass sums the slices and
+ * applies the epilogue (bias, activation, gated residual, output type) as kx_gemm_bf16 does.
+ * Same products as the reference call of kx_gemm_bf16 (mpp_linear.linear / mx.addmm,
+ * kinomlx/kernels/mpp_linear.py:469-506); the sum order over K differs (fp32 throughout).
+ * Requires n % 4 == 0, k % (32 * splits) == 0, 2 <= splits <= 64.
+ */
+int kx_gemm_splitk_bf16(const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias, void* c,
+                        int64_t ldc, int64_t m, int64_t n, int64_t k, int epilogue, const void* resid,
+                        int64_t ldr, const float* gate, int64_t gate_div, int64_t gate_stride, void* workspace,
+                        int64_t workspace_bytes, int splits, kx_stream_t stream);
+
+/*
  * Group-wise affine int4/int8 weight-quantized linear, dequantized inside the MFMA mainloop:
  * replaces nn.QuantizedLinear / mx.quantized_matmul(x, wq, scales, biases, transpose=True,
  * group_size, bits, mode="affine") + bias (kinomlx/models/ltx2/weights/quantization.py:28-44,

@@ -71,6 +71,9 @@ SIGNATURES: dict[str, list] = {
     "kx_gemm_bf16": [
         _P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _I64, _P, _I64, _I64, _P,
     ],
+    "kx_gemm_splitk_bf16": [
+        _P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _I64, _P, _I64, _I64, _P, _I64, _I, _P,
+    ],
     "kx_qgemm_affine_bf16": [
         _P, _I64, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I, _I, _P, _I64, _P, _I64,
         _I64, _P,
@@ -377,10 +380,34 @@ def launch_gemm(a, w, out, *, bias=None, flags: int = 0, resid=None, gate=None) 
     if resid is not None:
         _, _, ldr = _rows(resid, "linear residual")
         div, stride = _mod_rows(gate, m, n, "linear gate")
+    splits = splitk_splits(m, n, k)
+    if splits > 1 and a.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0 and lda <= (1 << 22) and ldw <= (1 << 22):
+        work = torch.empty(splits * m * n, dtype=torch.float32, device=a.device)
+        _call(
+            "kx_gemm_splitk_bf16", _ptr(a), lda, _ptr(w), ldw, _ptr(bias), _ptr(out), ldc, m, n, k, flags,
+            _ptr(resid), ldr, _ptr(gate), div, stride, _ptr(work), work.numel() * 4, splits, _stream(),
+        )
+        return
     _call(
         "kx_gemm_bf16", _ptr(a), lda, _ptr(w), ldw, _ptr(bias), _ptr(out), ldc, m, n, k, flags,
         _ptr(resid), ldr, _ptr(gate), div, stride, _stream(),
     )
+
+
+def splitk_splits(m: int, n: int, k: int) -> int:
+    """K slices for a product whose output tiles (64 x 128) leave most of the 256 CUs idle:
+    the most slices (up to 16) that keep at most 512 workgroups, a slice of at least 256 and a
+    whole number of 32-wide stages per slice; 1 means no split."""
+    if m > 512 or n <= 64 or n % 4 or k < 1024:
+        return 1
+    tiles = -(-m // 64) * -(-n // 128)
+    if tiles >= 128:
+        return 1
+    best = 1
+    for splits in (2, 4, 8, 16):
+        if tiles * splits <= 512 and k % (32 * splits) == 0 and k // splits >= 256:
+            best = splits
+    return best
 
 
 def launch_qgemm(a, words, scales, biases, out, *, n, k, group_size, bits, bias=None,

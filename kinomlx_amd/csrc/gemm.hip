@@ -539,6 +539,14 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave & 1, wn = wave >> 1;
   const int lrow = lane & 31, lhalf = lane >> 5;
+  if constexpr (QB == 0 && GMODE == 0 && OUTF32) {
+    // split-K (grid.y > 1): workgroup row y multiplies K slice y (K is the slice length) and
+    // writes its fp32 partial product to plane y of C (planes M * ldc floats apart)
+    const int64_t y = blockIdx.y;
+    A += y * K;
+    W += y * K;
+    C = static_cast<float*>(C) + y * (int64_t)M * ldc;
+  }
 
   // tile coordinates: XCD-contiguous, then grouped by 8 tile rows for L2 reuse
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
@@ -1093,6 +1101,38 @@ int dispatch(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, Qua
   }
 }
 
+// Split-K reduction: c = epilogue(sum over the planes of the fp32 partial products), 4 columns
+// of one row per thread (the planes are (M, N) fp32, N a multiple of 4).
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ parts, int splits,
+                                                            int M, int N, void* __restrict__ C, int64_t ldc,
+                                                            Epilogue epi, bool vec_ok) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t per_row = N / 4;
+  if (idx >= (int64_t)M * per_row) return;
+  const int m = (int)(idx / per_row), n = (int)(idx - m * per_row) * 4;
+  const int64_t plane = (int64_t)M * N;
+  float4 acc = *reinterpret_cast<const float4*>(parts + (int64_t)m * N + n);
+  for (int y = 1; y < splits; ++y) {
+    const float4 p = *reinterpret_cast<const float4*>(parts + y * plane + (int64_t)m * N + n);
+    acc.x += p.x;
+    acc.y += p.y;
+    acc.z += p.z;
+    acc.w += p.w;
+  }
+  float v[4] = {acc.x, acc.y, acc.z, acc.w};
+  epilogue_store4(v, m, n, N, epi, C, ldc, vec_ok);
+}
+
+template <int BM, int BN>
+int launch_splitk(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, float* parts, int m, int n,
+                  int k, int splits, hipStream_t s) {
+  const dim3 grid((unsigned)(((m + BM - 1) / BM) * ((n + BN - 1) / BN)), (unsigned)splits);
+  const Epilogue plain{nullptr, nullptr, 0, nullptr, 1, 0, KX_EPI_OUT_F32};
+  gemm_lds_kernel<BM, BN, 0, false, 0, true><<<grid, 256, 0, s>>>(a, lda, w, ldw, QuantW{}, parts, n, m, n,
+                                                                   k / splits, plain);
+  return KX_OK;
+}
+
 // Tiled affine weights: for 256-row tile nb and 32-wide K stage kb, the rows' packed bytes of the
 // stage are one block of 256 * (32 * bits / 8) bytes; for the 128-wide window p, the rows'
 // (scale 2p, scale 2p+1, bias 2p, bias 2p+1) are one block of 256 * 8 bytes. Rows past n repeat
@@ -1282,4 +1322,41 @@ extern "C" int kx_qgemm_affine_tiled_bf16(const void* a, int64_t lda, const void
     else launch_lds<192, 256, 8, true>((const uint16_t*)a, lda, nullptr, 0, qw, c, ldc, (int)m, (int)n, (int)k, epi, s);
   }
   return check_launch("kx_qgemm_affine_tiled_bf16");
+}
+
+extern "C" int kx_gemm_splitk_bf16(const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias,
+                                   void* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int epilogue,
+                                   const void* resid, int64_t ldr, const float* gate, int64_t gate_div,
+                                   int64_t gate_stride, void* workspace, int64_t workspace_bytes, int splits,
+                                   kx_stream_t stream) {
+  KX_REQUIRE(a && w && c && workspace, "kx_gemm_splitk_bf16: null tensor");
+  KX_REQUIRE(splits >= 2 && splits <= 64, "kx_gemm_splitk_bf16: splits must be 2..64, got %d", splits);
+  KX_REQUIRE(m > 0 && n > 0 && k > 0 && m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 30) && n % 4 == 0 &&
+                 k % (splits * DBK) == 0,
+             "kx_gemm_splitk_bf16: bad shape (m=%lld n=%lld k=%lld; n %% 4 == 0, k %% (32 splits) == 0)",
+             (long long)m, (long long)n, (long long)k);
+  KX_REQUIRE(lda % 8 == 0 && ldw % 8 == 0 && lda >= k && ldw >= k && ldc >= n && lda <= (1 << 22) &&
+                 ldw <= (1 << 22),
+             "kx_gemm_splitk_bf16: bad strides");
+  KX_REQUIRE(aligned16(a) && aligned16(w) && aligned8(c) && aligned16(workspace),
+             "kx_gemm_splitk_bf16: a/w/workspace must be 16-byte and c 8-byte aligned");
+  KX_REQUIRE(workspace_bytes >= (int64_t)splits * m * n * 4,
+             "kx_gemm_splitk_bf16: workspace of %lld bytes is below splits * m * n * 4 = %lld",
+             (long long)workspace_bytes, (long long)splits * m * n * 4);
+  const int rc = check_epilogue("kx_gemm_splitk_bf16", epilogue, bias, c, ldc, resid, ldr, n, gate, gate_div,
+                                gate_stride);
+  if (rc) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  float* parts = static_cast<float*>(workspace);
+  if (pick_lds_cfg(m, n) == 3)
+    launch_splitk<64, 128>((const uint16_t*)a, lda, (const uint16_t*)w, ldw, parts, (int)m, (int)n, (int)k, splits, s);
+  else
+    launch_splitk<128, 128>((const uint16_t*)a, lda, (const uint16_t*)w, ldw, parts, (int)m, (int)n, (int)k, splits,
+                            s);
+  const Epilogue epi{(const uint16_t*)bias, resid, ldr, gate, gate_div, gate_stride, epilogue};
+  const bool vec_ok = (ldc % 4 == 0) && (!(epilogue & KX_EPI_GATED_RESIDUAL) || ldr % 4 == 0);
+  const int64_t threads = m * (n / 4);
+  splitk_reduce_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, s>>>(parts, splits, (int)m, (int)n, c, ldc, epi,
+                                                                         vec_ok);
+  return check_launch("kx_gemm_splitk_bf16");
 }
