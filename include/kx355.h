@@ -106,6 +106,21 @@ int kx_attention_bias_fwd_bf16(const void* q, int64_t ldq, const void* k, int64_
                                int64_t bias_bs, int64_t bias_hs, int64_t bias_qs, kx_stream_t stream);
 
 /*
+ * kx_attention_bias_fwd_bf16 (bias may be NULL) split over keys, for calls with few query tiles
+ * and many keys (the 127-query audio -> video direction): the keys are cut into at most `splits`
+ * slices of whole 64-key tiles, each slice's workgroups write unnormalized fp32 O rows and
+ * (running max, row sum) into `workspace` (splits * batch * heads * tq * (head_dim + 2) floats,
+ * caller-owned), and one pass merges the slices (rescaling each by 2^(m - max)), normalizes,
+ * gates and rounds. Same result as the unsplit call up to the order of the fp32 sums.
+ */
+int kx_attention_split_fwd_bf16(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v,
+                                int64_t ldv, void* o, int64_t ldo, int64_t batch, int64_t tq, int64_t tk,
+                                int64_t heads, int64_t kv_heads, int64_t head_dim, float scale,
+                                const void* gate, int64_t ld_gate, const void* bias, int64_t bias_bs,
+                                int64_t bias_hs, int64_t bias_qs, void* workspace, int64_t workspace_bytes,
+                                int splits, kx_stream_t stream);
+
+/*
  * Split-half RoPE, standalone: replaces split_rope.rotate (kinomlx/kernels/split_rope.py:144-163,
  * arithmetic :35-56). x/y are (batch, tokens, heads * 2 * half) rows at stride ldx/ldy; tables
  * token-major (table_batch, tokens, heads * half), table_batched selects per-batch tables.

@@ -68,6 +68,10 @@ SIGNATURES: dict[str, list] = {
         _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _I64, _P, _I64, _I64,
         _I64, _P,
     ],
+    "kx_attention_split_fwd_bf16": [
+        _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _I64, _P, _I64, _I64,
+        _I64, _P, _I64, _I, _P,
+    ],
     "kx_gemm_bf16": [
         _P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _I64, _P, _I64, _I64, _P,
     ],
@@ -330,9 +334,20 @@ def launch_attention(q, k, v, out, *, batch, tq, tk, heads, head_dim, scale, gat
     ld_gate = 0
     if gate is not None:
         _, _, ld_gate = _rows(gate, "attention gate")
+    if bias is not None and (bias.dtype != torch.bfloat16 or bias_strides is None):
+        raise ValueError("attention bias: bfloat16 values with (batch, head, query) strides")
+    splits = attention_splits(batch, tq, tk, heads)
+    if splits > 1:
+        chunk = -(-(-(-tk // splits)) // 64) * 64
+        used = -(-tk // chunk)
+        work = torch.empty(used * batch * heads * tq * (head_dim + 2), dtype=torch.float32, device=q.device)
+        _call(
+            "kx_attention_split_fwd_bf16", _ptr(q), q.stride(-2), _ptr(k), k.stride(-2), _ptr(v), v.stride(-2),
+            _ptr(out), out.stride(-2), batch, tq, tk, heads, kv_heads or heads, head_dim, scale, _ptr(gate), ld_gate,
+            _ptr(bias), *(bias_strides or (0, 0, 0)), _ptr(work), work.numel() * 4, splits, _stream(),
+        )
+        return
     if bias is not None:
-        if bias.dtype != torch.bfloat16 or bias_strides is None:
-            raise ValueError("attention bias: bfloat16 values with (batch, head, query) strides")
         _call(
             "kx_attention_bias_fwd_bf16", _ptr(q), q.stride(-2), _ptr(k), k.stride(-2), _ptr(v), v.stride(-2),
             _ptr(out), out.stride(-2), batch, tq, tk, heads, kv_heads or heads, head_dim, scale, _ptr(gate), ld_gate,
@@ -351,6 +366,16 @@ def launch_attention(q, k, v, out, *, batch, tq, tk, heads, head_dim, scale, gat
         v.stride(-2), _ptr(out), out.stride(-2), batch, tq, tk, heads, head_dim, scale,
         _ptr(gate), ld_gate, _stream(),
     )
+
+
+def attention_splits(batch: int, tq: int, tk: int, heads: int) -> int:
+    """Key slices for an attention call whose query tiles (384 queries x 1 head) fill under half
+    the 256 CUs and that has at least 1024 keys: about 512 workgroups, at least 256 keys per
+    slice, at most 16 slices; 1 means no split."""
+    blocks = -(-tq // 384) * heads * batch
+    if blocks >= 128 or tk < 1024:
+        return 1
+    return max(1, min(16, -(-512 // blocks), tk // 256))
 
 
 def _dtype_flags(out, resid, name: str) -> int:

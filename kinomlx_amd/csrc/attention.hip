@@ -81,12 +81,21 @@ struct ScoreBias {
   float mul;  // 1 / scale
 };
 
-template <int D, bool BIAS>
+// Split over keys (few query tiles, many keys): grid row y takes keys [y * chunk, (y + 1) * chunk)
+// and writes its unnormalized fp32 O rows and (running max in the exp2 domain, row sum) to the
+// workspace; attn_combine_kernel merges the slices.
+struct SplitOut {
+  float* o;   // (splits, batch * heads, tq, D)
+  float* ml;  // (splits, batch * heads, tq, 2)
+  int chunk;  // keys per slice, a multiple of BKV
+};
+
+template <int D, bool BIAS, bool SPLIT>
 __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
     const uint16_t* __restrict__ Q, int64_t ldq, const uint16_t* __restrict__ K, int64_t ldk,
     const uint16_t* __restrict__ V, int64_t ldv, uint16_t* __restrict__ O, int64_t ldo, int tq,
-    int tk, int heads, int kv_group, float scale_log2, const uint16_t* __restrict__ gate,
-    int64_t ld_gate, int qtiles, ScoreBias bias) {
+    int tk_all, int heads, int kv_group, float scale_log2, const uint16_t* __restrict__ gate,
+    int64_t ld_gate, int qtiles, ScoreBias bias, SplitOut split) {
   constexpr int ROWB = D * 2;             // bytes per K / V row
   constexpr int CPR = ROWB / 16;          // 16-byte chunks per row
   constexpr int RPI = 64 / CPR;           // rows per DMA instruction
@@ -108,8 +117,14 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
   const int h = bh % heads, b = bh / heads;
   const uint16_t* Qb = Q + (int64_t)b * tq * ldq + (int64_t)h * D;
   const int hk = h / kv_group;  // grouped-query attention: kv_group query heads share a K/V head
-  const char* Kb = reinterpret_cast<const char*>(K + (int64_t)b * tk * ldk + (int64_t)hk * D);
-  const char* Vb = reinterpret_cast<const char*>(V + (int64_t)b * tk * ldv + (int64_t)hk * D);
+  // this workgroup's keys: all of them, or one slice of the split form
+  int j_begin = 0, tk = tk_all;
+  if constexpr (SPLIT) {
+    j_begin = blockIdx.y * split.chunk;
+    tk = min(tk_all - j_begin, split.chunk);
+  }
+  const char* Kb = reinterpret_cast<const char*>(K + ((int64_t)b * tk_all + j_begin) * ldk + (int64_t)hk * D);
+  const char* Vb = reinterpret_cast<const char*>(V + ((int64_t)b * tk_all + j_begin) * ldv + (int64_t)hk * D);
 
   const int q0 = qt * BQ + wave * 32;
   const int qrow = min(q0 + lrow, tq - 1);
@@ -196,7 +211,8 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
     const int j0 = it * BKV;
     if constexpr (BIAS) {
       // lane: query qrow, keys j0 + 32 kb + 8 g + 4 lhalf + (0..3) = elements 4 g .. 4 g + 3
-      const uint16_t* brow = bias.ptr + (int64_t)b * bias.bs + (int64_t)h * bias.hs + (int64_t)qrow * bias.qs;
+      const uint16_t* brow =
+          bias.ptr + (int64_t)b * bias.bs + (int64_t)h * bias.hs + (int64_t)qrow * bias.qs + j_begin;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -277,6 +293,18 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
   const int q = q0 + lrow;
   if (q >= tq) return;
+  if constexpr (SPLIT) {
+    const int64_t row = ((int64_t)blockIdx.y * (gridDim.x / qtiles) + bh) * tq + q;
+    float* orow = split.o + row * D;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<float4*>(orow + db * 32 + 8 * g + 4 * lhalf) =
+            make_float4(o[db][4 * g + 0], o[db][4 * g + 1], o[db][4 * g + 2], o[db][4 * g + 3]);
+    if (lhalf == 0) *reinterpret_cast<float2*>(split.ml + 2 * row) = make_float2(m_run * scale_log2, l_tot);
+    return;
+  }
   float scale_out = 1.0f / l_tot;
   if (gate) scale_out *= bf2f(gate[((int64_t)b * tq + q) * ld_gate + h]);
   uint16_t* orow = O + ((int64_t)b * tq + q) * ldo + (int64_t)h * D;
@@ -291,23 +319,79 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
     }
 }
 
+// out = (sum_y 2^(m_y - M) O_y) / (sum_y 2^(m_y - M) l_y) * gate, M = max_y m_y: the slices of the
+// split form merged (4 dims of one row per thread).
+template <int D>
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ part_o,
+                                                           const float* __restrict__ part_ml, int splits,
+                                                           int64_t rows, int tq, int heads,
+                                                           uint16_t* __restrict__ O, int64_t ldo,
+                                                           const uint16_t* __restrict__ gate, int64_t ld_gate) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= rows * (D / 4)) return;
+  const int64_t row = idx / (D / 4);  // (b * heads + h) * tq + q
+  const int d = (int)(idx - row * (D / 4)) * 4;
+  float mx = -INFINITY;
+  for (int y = 0; y < splits; ++y) mx = fmaxf(mx, part_ml[2 * (y * rows + row)]);
+  float l = 0.0f;
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (int y = 0; y < splits; ++y) {
+    const float2 ml = *reinterpret_cast<const float2*>(part_ml + 2 * (y * rows + row));
+    const float w = __builtin_amdgcn_exp2f(ml.x - mx);
+    const float4 p = *reinterpret_cast<const float4*>(part_o + (y * rows + row) * D + d);
+    l += w * ml.y;
+    acc.x += w * p.x;
+    acc.y += w * p.y;
+    acc.z += w * p.z;
+    acc.w += w * p.w;
+  }
+  const int q = (int)(row % tq);
+  const int64_t bh = row / tq;
+  const int h = (int)(bh % heads), b = (int)(bh / heads);
+  float scale_out = 1.0f / l;
+  if (gate) scale_out *= bf2f(gate[((int64_t)b * tq + q) * ld_gate + h]);
+  uint2 w2;
+  w2.x = pack2(acc.x * scale_out, acc.y * scale_out);
+  w2.y = pack2(acc.z * scale_out, acc.w * scale_out);
+  *reinterpret_cast<uint2*>(O + ((int64_t)b * tq + q) * ldo + (int64_t)h * D + d) = w2;
+}
+
+template <int D, bool BIAS, bool SPLIT>
+void launch_attn_t(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv, void* o,
+                   int64_t ldo, int64_t tq, int64_t tk, int64_t heads, int64_t kv_heads, float scale,
+                   const void* gate, int64_t ld_gate, ScoreBias bias, SplitOut split, dim3 grid, int qtiles,
+                   hipStream_t s) {
+  attn_fwd_kernel<D, BIAS, SPLIT><<<grid, NWAVE * 64, 0, s>>>(
+      (const uint16_t*)q, ldq, (const uint16_t*)k, ldk, (const uint16_t*)v, ldv, (uint16_t*)o, ldo, (int)tq,
+      (int)tk, (int)heads, (int)(heads / kv_heads), scale * 1.4426950408889634f, (const uint16_t*)gate, ld_gate,
+      qtiles, bias, split);
+}
+
 template <int D>
 int launch_attn(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
                 void* o, int64_t ldo, int64_t batch, int64_t tq, int64_t tk, int64_t heads,
                 int64_t kv_heads, float scale, const void* gate, int64_t ld_gate, ScoreBias bias,
-                hipStream_t s) {
+                SplitOut split, int splits, hipStream_t s) {
   const int qtiles = (int)((tq + BQ - 1) / BQ);
   const int64_t blocks = (int64_t)qtiles * heads * batch;
-  if (bias.ptr)
-    attn_fwd_kernel<D, true><<<(unsigned)blocks, NWAVE * 64, 0, s>>>(
-        (const uint16_t*)q, ldq, (const uint16_t*)k, ldk, (const uint16_t*)v, ldv, (uint16_t*)o,
-        ldo, (int)tq, (int)tk, (int)heads, (int)(heads / kv_heads), scale * 1.4426950408889634f,
-        (const uint16_t*)gate, ld_gate, qtiles, bias);
-  else
-    attn_fwd_kernel<D, false><<<(unsigned)blocks, NWAVE * 64, 0, s>>>(
-        (const uint16_t*)q, ldq, (const uint16_t*)k, ldk, (const uint16_t*)v, ldv, (uint16_t*)o,
-        ldo, (int)tq, (int)tk, (int)heads, (int)(heads / kv_heads), scale * 1.4426950408889634f,
-        (const uint16_t*)gate, ld_gate, qtiles, bias);
+  const dim3 grid((unsigned)blocks, (unsigned)splits);
+  if (splits > 1) {
+    if (bias.ptr)
+      launch_attn_t<D, true, true>(q, ldq, k, ldk, v, ldv, o, ldo, tq, tk, heads, kv_heads, scale, gate, ld_gate,
+                                   bias, split, grid, qtiles, s);
+    else
+      launch_attn_t<D, false, true>(q, ldq, k, ldk, v, ldv, o, ldo, tq, tk, heads, kv_heads, scale, gate, ld_gate,
+                                    bias, split, grid, qtiles, s);
+    const int64_t rows = batch * heads * tq;
+    attn_combine_kernel<D><<<(unsigned)((rows * (D / 4) + 255) / 256), 256, 0, s>>>(
+        split.o, split.ml, splits, rows, (int)tq, (int)heads, (uint16_t*)o, ldo, (const uint16_t*)gate, ld_gate);
+  } else if (bias.ptr) {
+    launch_attn_t<D, true, false>(q, ldq, k, ldk, v, ldv, o, ldo, tq, tk, heads, kv_heads, scale, gate, ld_gate,
+                                  bias, split, grid, qtiles, s);
+  } else {
+    launch_attn_t<D, false, false>(q, ldq, k, ldk, v, ldv, o, ldo, tq, tk, heads, kv_heads, scale, gate, ld_gate,
+                                   bias, split, grid, qtiles, s);
+  }
   return check_launch("kx_attention_fwd_bf16");
 }
 
@@ -321,7 +405,8 @@ int attention_entry(const char* name, const void* q, int64_t ldq, const void* k,
                     const void* v, int64_t ldv, void* o, int64_t ldo, int64_t batch, int64_t tq,
                     int64_t tk, int64_t heads, int64_t kv_heads, int64_t head_dim, float scale,
                     const void* gate, int64_t ld_gate, kx_stream_t stream,
-                    ScoreBias bias = ScoreBias{nullptr, 0, 0, 0, 0.0f}) {
+                    ScoreBias bias = ScoreBias{nullptr, 0, 0, 0, 0.0f},
+                    SplitOut split = SplitOut{nullptr, nullptr, 0}, int splits = 1) {
   KX_REQUIRE(q && k && v && o, "%s: null tensor", name);
   KX_REQUIRE(head_dim == 64 || head_dim == 128, "%s: head_dim must be 64 or 128, got %lld", name,
              (long long)head_dim);
@@ -343,9 +428,9 @@ int attention_entry(const char* name, const void* q, int64_t ldq, const void* k,
   if (tq == 0 || batch == 0) return KX_OK;
   if (head_dim == 128)
     return launch_attn<128>(q, ldq, k, ldk, v, ldv, o, ldo, batch, tq, tk, heads, kv_heads, scale,
-                            gate, ld_gate, bias, (hipStream_t)stream);
+                            gate, ld_gate, bias, split, splits, (hipStream_t)stream);
   return launch_attn<64>(q, ldq, k, ldk, v, ldv, o, ldo, batch, tq, tk, heads, kv_heads, scale,
-                         gate, ld_gate, bias, (hipStream_t)stream);
+                         gate, ld_gate, bias, split, splits, (hipStream_t)stream);
 }
 }  // namespace
 
@@ -383,4 +468,36 @@ extern "C" int kx_attention_bias_fwd_bf16(const void* q, int64_t ldq, const void
   return attention_entry("kx_attention_bias_fwd_bf16", q, ldq, k, ldk, v, ldv, o, ldo, batch, tq, tk,
                          heads, kv_heads, head_dim, scale, gate, ld_gate, stream,
                          ScoreBias{(const uint16_t*)bias, bias_bs, bias_hs, bias_qs, 1.0f / scale});
+}
+
+extern "C" int kx_attention_split_fwd_bf16(const void* q, int64_t ldq, const void* k, int64_t ldk,
+                                           const void* v, int64_t ldv, void* o, int64_t ldo, int64_t batch,
+                                           int64_t tq, int64_t tk, int64_t heads, int64_t kv_heads,
+                                           int64_t head_dim, float scale, const void* gate, int64_t ld_gate,
+                                           const void* bias, int64_t bias_bs, int64_t bias_hs, int64_t bias_qs,
+                                           void* workspace, int64_t workspace_bytes, int splits,
+                                           kx_stream_t stream) {
+  const char* name = "kx_attention_split_fwd_bf16";
+  KX_REQUIRE(workspace && aligned16(workspace), "%s: workspace must be a 16-byte aligned buffer", name);
+  KX_REQUIRE(splits >= 2 && splits <= 256 && tk > 0, "%s: splits must be 2..256, got %d", name, splits);
+  KX_REQUIRE(ldo % 4 == 0 && aligned8(o), "%s: output rows must be 8-byte aligned", name);
+  // keys per slice: a whole number of 64-key tiles; the slices actually used cover tk exactly
+  const int64_t chunk = ((tk + splits - 1) / splits + BKV - 1) / BKV * BKV;
+  const int used = (int)((tk + chunk - 1) / chunk);
+  const int64_t rows = batch * heads * tq;
+  KX_REQUIRE(workspace_bytes >= (int64_t)used * rows * (head_dim + 2) * 4,
+             "%s: workspace of %lld bytes is below splits * batch * heads * tq * (head_dim + 2) * 4", name,
+             (long long)workspace_bytes);
+  ScoreBias sb{nullptr, 0, 0, 0, 0.0f};
+  if (bias) {
+    KX_REQUIRE(aligned8(bias) && bias_bs >= 0 && bias_hs >= 0 && bias_qs >= 0 && bias_bs % 4 == 0 &&
+                   bias_hs % 4 == 0 && bias_qs % 4 == 0,
+               "%s: bias must be 8-byte aligned with non-negative strides that are multiples of 4", name);
+    KX_REQUIRE(scale > 0.0f && isfinite(scale), "%s: scale must be positive", name);
+    sb = ScoreBias{(const uint16_t*)bias, bias_bs, bias_hs, bias_qs, 1.0f / scale};
+  }
+  float* ws = static_cast<float*>(workspace);
+  const SplitOut split{ws, ws + (int64_t)used * rows * head_dim, (int)chunk};
+  return attention_entry(name, q, ldq, k, ldk, v, ldv, o, ldo, batch, tq, tk, heads, kv_heads, head_dim, scale,
+                         gate, ld_gate, stream, sb, split, used);
 }
