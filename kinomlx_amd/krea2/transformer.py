@@ -187,8 +187,15 @@ class Krea2Attention:
         ``residual + gate * .`` is formed in the ``to_out`` epilogue, written as ``out_dtype``."""
         if hidden_states.dim() != 3 or hidden_states.shape[-1] != self.hidden_size:
             raise ValueError(f"Krea attention expects [batch, sequence, {self.hidden_size}] hidden states")
+        batch, length = int(hidden_states.shape[0]), int(hidden_states.shape[1])
+        key_mask = None
         if attention_mask is not None:
-            raise ValueError("masked Krea attention is not built for MI355X")
+            # a boolean (batch, length) key mask; masked queries are zeroed (model.py:164-196)
+            if attention_mask.dtype != torch.bool:
+                raise ValueError("Krea attention mask must use a boolean dtype")
+            if tuple(attention_mask.shape) != (batch, length):
+                raise ValueError("Krea attention mask must match batch and sequence dimensions")
+            key_mask = attention_mask[:, None, None, :]
         if reference_attention is not None:
             raise ValueError("reference attention capture is not built for MI355X")
         q_width = self.num_heads * self.head_dim
@@ -203,7 +210,10 @@ class Krea2Attention:
         q = _norm_rope_rows(q_raw, self.norm_q, rotary, self.num_heads)
         k = _norm_rope_rows(k_raw, self.norm_k, rotary, self.num_kv_heads)
         attended = _dense.batched_attention(q, k, v, heads=self.num_heads, kv_heads=self.num_kv_heads,
-                                            scale=self.scale)
+                                            scale=self.scale, mask=key_mask)
+        if attention_mask is not None:
+            # the query selection rides on the gate: a zero gate row zeroes the attended row
+            sigmoid_gate = sigmoid_gate.masked_fill(~attention_mask[..., None], 0.0)
         gated = torch.empty_like(attended)
         _lib.launch_gated_residual(None, attended.view(-1, q_width), gated.view(-1, q_width),
                                    sigmoid_gate.view(-1, q_width))

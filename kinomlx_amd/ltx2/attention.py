@@ -134,14 +134,12 @@ def dense_kernel_attention(query: torch.Tensor, key: torch.Tensor, value: torch.
 def scaled_dot_product_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, *, heads: int,
                                  dim_head: int, mask: torch.Tensor | None = None,
                                  compile_attention: bool = True) -> torch.Tensor:
-    """Unmasked attention on flattened-head inputs (``attention.py:224-246``). Masked attention
-    is not built for MI355X and raises."""
+    """Attention on flattened-head inputs (``attention.py:224-246``); ``mask`` is the SDPA mask
+    (``_prepare_attention_mask``, ``:136-141``), added to the scores inside the kernel."""
     del compile_attention
-    if mask is not None:
-        raise ValueError("masked attention is not built for MI355X")
     if query.shape[-1] != heads * dim_head:
         raise ValueError("query width must be heads * dim_head")
-    return _dense.batched_attention(query, key, value, heads=heads)
+    return _dense.batched_attention(query, key, value, heads=heads, mask=mask)
 
 
 def _cat_layers(layers):

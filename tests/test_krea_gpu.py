@@ -104,3 +104,22 @@ def test_grouped_query_attention_kernel(device, heads, kv_heads, dh):
     vf = np.repeat(v.reshape(tk, kv_heads, dh), group, axis=1).reshape(tk, -1)
     ref = oracle.attention(q, kf, vf, heads=heads)
     assert rel_l2(got, ref) < 8e-3 and max_abs(got, ref) < 2e-2
+
+
+def test_krea_key_mask_equals_the_truncated_sequence(device):
+    """A boolean (batch, length) mask: the valid queries see only the valid keys, so their rows
+    equal the block run on the valid prefix alone; the masked queries' attention is zero
+    (``model.py:164-196``)."""
+    hidden, heads, kv_heads, tokens, keep = 512, 4, 2, 80, 53
+    p, _, x, tmod, ids = krea_case(hidden, heads, kv_heads, tokens, 1024)
+    rope = krea.Krea2RotaryEmbedding(theta=1000.0, axes_dims=(32, 32, 64))
+    cos, sin = rope(ids.to(device))
+    block = build_krea_block(p, hidden, heads, kv_heads, device)
+    mask = torch.zeros((1, tokens), dtype=torch.bool, device=device)
+    mask[:, :keep] = True
+    masked = _np(block(x.to(device), time_modulation=tmod.to(device), rotary=(cos, sin), attention_mask=mask)[0])
+    short = _np(block(x[:, :keep].contiguous().to(device), time_modulation=tmod.to(device),
+                      rotary=(cos[:, :keep].contiguous(), sin[:, :keep].contiguous()), attention_mask=None)[0])
+    assert cosine(masked[:keep], short) > 0.999999 and max_abs(masked[:keep], short) <= 2 ** -6 * np.abs(short).max()
+    with pytest.raises(ValueError, match="boolean"):
+        block(x.to(device), time_modulation=tmod.to(device), rotary=(cos, sin), attention_mask=mask.float())
