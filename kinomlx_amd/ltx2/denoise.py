@@ -26,11 +26,13 @@ class LTX2DenoiseError(RuntimeError):
     """A completed denoise step produced nonfinite active latents."""
 
 
-def all_finite(value: torch.Tensor) -> bool:
-    """``mx.all(mx.isfinite(value))`` through the finite-check kernel (one host read)."""
-    flag = torch.empty(1, dtype=torch.int32, device=value.device)
-    _lib.launch_all_finite(value.contiguous(), flag)
-    return bool(flag.item())
+def all_finite(*values: torch.Tensor) -> list[bool]:
+    """``mx.all(mx.isfinite(value))`` per tensor through the finite-check kernel, with one host
+    read for all of them (the reference stacks the flags and reads them once, ``:244-258``)."""
+    flags = torch.empty(len(values), dtype=torch.int32, device=values[0].device)
+    for index, value in enumerate(values):
+        _lib.launch_all_finite(value.contiguous(), flags[index:index + 1])
+    return [bool(v) for v in flags.tolist()]
 
 
 def modality_from_state(state: LatentState, context: torch.Tensor, sigma: float, *, enabled: bool = True,
@@ -97,9 +99,10 @@ def denoise_step(video_state: LatentState, audio_state: LatentState | None = Non
                                  sigma_next=sigma_next, step_kind=step_kind, noise=audio_noise)
         audio_state = replace(audio_state, latent=latent)
         active.append(("audio", audio_state.latent))
-    for modality, value in active:
-        if not all_finite(value):
-            raise LTX2DenoiseError(f"LTX-2 denoising produced a nonfinite {modality} latent in {value.dtype}.")
+    if active:
+        for (modality, value), valid in zip(active, all_finite(*(v for _, v in active))):
+            if not valid:
+                raise LTX2DenoiseError(f"LTX-2 denoising produced a nonfinite {modality} latent in {value.dtype}.")
     return video_state, audio_state
 
 

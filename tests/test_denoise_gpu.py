@@ -259,14 +259,15 @@ def test_composite_random_mask_is_bit_exact(device):
 def test_finite_check(device, dtype):
     n = 3_000_001  # several grid-stride passes of the capped grid
     x = torch.zeros(n, dtype=dtype, device=device)
-    assert all_finite(x)
+    assert all_finite(x) == [True]
     for index in (0, 777_777, n - 1):
         for bad in (float("nan"), float("inf"), float("-inf")):
             y = x.clone()
             y[index] = bad
-            assert not all_finite(y), (index, bad)
-    assert all_finite(torch.zeros(0, dtype=dtype, device=device))
-    assert all_finite(torch.full((5,), 3.0e38, dtype=torch.float32, device=device))
+            assert all_finite(y) == [False], (index, bad)
+            assert all_finite(x, y, x) == [True, False, True]
+    assert all_finite(torch.zeros(0, dtype=dtype, device=device)) == [True]
+    assert all_finite(torch.full((5,), 3.0e38, dtype=torch.float32, device=device)) == [True]
 
 
 # ---- the denoise step's control flow (reference test_denoise.py:13-67) -----------------------------
