@@ -763,15 +763,28 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
 #pragma unroll
         for (int j = 0; j < MB; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fw[b][i], fa[b][j], acc[i][j], 0, 0, 0);
-      // the fragment reads for the next step first, then MFMAs with the DMA issues between them
-      __builtin_amdgcn_sched_group_barrier(0x100, MB + NB, 0);
+      // the next step's fragment reads one per MFMA (a burst of them fills the LDS command queue
+      // and stalls the wave before its MFMAs), then the DMA issues between the remaining MFMAs
+      constexpr int NRD = MB + NB, NMF = NB * MB;
+      constexpr int PAIRS = NRD < NMF ? NRD : NMF;
+      constexpr int DMF = DPS < NMF - PAIRS ? DPS : NMF - PAIRS;
 #pragma unroll
-      for (int q = 0; q < DPS; ++q) {
+      for (int q = 0; q < PAIRS; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      }
+      if constexpr (NRD > PAIRS) __builtin_amdgcn_sched_group_barrier(0x100, NRD - PAIRS, 0);
+#pragma unroll
+      for (int q = 0; q < DMF; ++q) {
         __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       }
-      __builtin_amdgcn_sched_group_barrier(0x008, NB * MB - DPS, 0);
+      if constexpr (DPS > DMF) {
+        __builtin_amdgcn_sched_group_barrier(0x002, DPS - DMF, 0);
+        __builtin_amdgcn_sched_group_barrier(0x020, DPS - DMF, 0);
+      }
+      if constexpr (NMF > PAIRS + DMF) __builtin_amdgcn_sched_group_barrier(0x008, NMF - PAIRS - DMF, 0);
     }
     cur_i = nxt_i;
   }
