@@ -221,6 +221,24 @@ int kx_gemm_splitk_bf16(const void* a, int64_t lda, const void* w, int64_t ldw, 
                         int64_t ldr, const float* gate, int64_t gate_div, int64_t gate_stride, void* workspace,
                         int64_t workspace_bytes, int splits, kx_stream_t stream);
 
+/* Size of the static device array kx_gemm_splitk_noalloc_bf16 keeps its partial products in. */
+#define KX_SPLITK_SCRATCH_BYTES (16ll << 20)
+
+/*
+ * kx_gemm_splitk_bf16 without a workspace argument, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It
+ * has no counterpart in the reference. The fp32 partial products go to a static device array of
+ * KX_SPLITK_SCRATCH_BYTES (16 MiB) that each device holds from the library's load until the
+ * process ends; the call allocates nothing and returns KX_ERR_INVALID when splits * m * n * 4
+ * exceeds it. Every call on a device shares that device's array: calls that overlap on one device
+ * (two streams, or two threads) race, so the caller orders them. Same kernels, results and checks
+ * as kx_gemm_splitk_bf16 (bit-identical output).
+ */
+int kx_gemm_splitk_noalloc_bf16(const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias,
+                                void* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int epilogue,
+                                const void* resid, int64_t ldr, const float* gate, int64_t gate_div,
+                                int64_t gate_stride, int splits, kx_stream_t stream);
+
 /*
  * Group-wise affine int4/int8 weight-quantized linear, dequantized inside the MFMA mainloop:
  * replaces nn.QuantizedLinear / mx.quantized_matmul(x, wq, scales, biases, transpose=True,

@@ -78,6 +78,9 @@ SIGNATURES: dict[str, list] = {
     "kx_gemm_splitk_bf16": [
         _P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _I64, _P, _I64, _I64, _P, _I64, _I, _P,
     ],
+    "kx_gemm_splitk_noalloc_bf16": [
+        _P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _I64, _P, _I64, _I64, _I, _P,
+    ],
     "kx_qgemm_affine_bf16": [
         _P, _I64, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I, _I, _P, _I64, _P, _I64,
         _I64, _P,

@@ -19,6 +19,7 @@
 // inside the mainloop; the MFMA loop is shared with the dense path.
 #include <stdlib.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -1337,30 +1338,31 @@ extern "C" int kx_qgemm_affine_tiled_bf16(const void* a, int64_t lda, const void
   return check_launch("kx_qgemm_affine_tiled_bf16");
 }
 
-extern "C" int kx_gemm_splitk_bf16(const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias,
-                                   void* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int epilogue,
-                                   const void* resid, int64_t ldr, const float* gate, int64_t gate_div,
-                                   int64_t gate_stride, void* workspace, int64_t workspace_bytes, int splits,
-                                   kx_stream_t stream) {
-  KX_REQUIRE(a && w && c && workspace, "kx_gemm_splitk_bf16: null tensor");
-  KX_REQUIRE(splits >= 2 && splits <= 64, "kx_gemm_splitk_bf16: splits must be 2..64, got %d", splits);
+namespace {
+
+// Argument checks shared by the two split-K entry points (no GPU call).
+int check_splitk(const char* what, const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias,
+                 void* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int epilogue, const void* resid,
+                 int64_t ldr, const float* gate, int64_t gate_div, int64_t gate_stride, int splits) {
+  KX_REQUIRE(a && w && c, "%s: null tensor", what);
+  KX_REQUIRE(splits >= 2 && splits <= 64, "%s: splits must be 2..64, got %d", what, splits);
   KX_REQUIRE(m > 0 && n > 0 && k > 0 && m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 30) && n % 4 == 0 &&
                  k % (splits * DBK) == 0,
-             "kx_gemm_splitk_bf16: bad shape (m=%lld n=%lld k=%lld; n %% 4 == 0, k %% (32 splits) == 0)",
-             (long long)m, (long long)n, (long long)k);
+             "%s: bad shape (m=%lld n=%lld k=%lld; n %% 4 == 0, k %% (32 splits) == 0)", what, (long long)m,
+             (long long)n, (long long)k);
   KX_REQUIRE(lda % 8 == 0 && ldw % 8 == 0 && lda >= k && ldw >= k && ldc >= n && lda <= (1 << 22) &&
                  ldw <= (1 << 22),
-             "kx_gemm_splitk_bf16: bad strides");
-  KX_REQUIRE(aligned16(a) && aligned16(w) && aligned8(c) && aligned16(workspace),
-             "kx_gemm_splitk_bf16: a/w/workspace must be 16-byte and c 8-byte aligned");
-  KX_REQUIRE(workspace_bytes >= (int64_t)splits * m * n * 4,
-             "kx_gemm_splitk_bf16: workspace of %lld bytes is below splits * m * n * 4 = %lld",
-             (long long)workspace_bytes, (long long)splits * m * n * 4);
-  const int rc = check_epilogue("kx_gemm_splitk_bf16", epilogue, bias, c, ldc, resid, ldr, n, gate, gate_div,
-                                gate_stride);
-  if (rc) return rc;
-  hipStream_t s = (hipStream_t)stream;
-  float* parts = static_cast<float*>(workspace);
+             "%s: bad strides", what);
+  KX_REQUIRE(aligned16(a) && aligned16(w) && aligned8(c), "%s: a/w must be 16-byte and c 8-byte aligned", what);
+  return check_epilogue(what, epilogue, bias, c, ldc, resid, ldr, n, gate, gate_div, gate_stride);
+}
+
+// Both passes of a split-K product on `parts` (splits * m * n floats): every slice writes all of its
+// (m, n) plane before the reduction reads it, so `parts` needs no clearing between calls.
+int run_splitk(const char* what, const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias,
+               void* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int epilogue, const void* resid,
+               int64_t ldr, const float* gate, int64_t gate_div, int64_t gate_stride, float* parts, int splits,
+               hipStream_t s) {
   if (pick_lds_cfg(m, n) == 3)
     launch_splitk<64, 128>((const uint16_t*)a, lda, (const uint16_t*)w, ldw, parts, (int)m, (int)n, (int)k, splits, s);
   else
@@ -1371,5 +1373,73 @@ extern "C" int kx_gemm_splitk_bf16(const void* a, int64_t lda, const void* w, in
   const int64_t threads = m * (n / 4);
   splitk_reduce_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, s>>>(parts, splits, (int)m, (int)n, c, ldc, epi,
                                                                          vec_ok);
-  return check_launch("kx_gemm_splitk_bf16");
+  return check_launch(what);
+}
+
+// The no-allocation variant's partial products: one static array per device (the HIP runtime
+// places a copy on each device that loads this code object, for the life of the process). Host
+// code never passes `scratch` itself to a kernel (on the host it names a stand-in, not a device
+// address); it passes the device address hipGetSymbolAddress returns for the current device.
+static __device__ __align__(256) float scratch[KX_SPLITK_SCRATCH_BYTES / 4];
+
+constexpr int KX_MAX_DEVICES = 64;
+std::mutex g_scratch_mutex;
+float* g_scratch_ptr[KX_MAX_DEVICES] = {};
+
+// The current device's address of `scratch`, looked up on the first call on that device (with the
+// device current) and kept per device.
+int scratch_address(const char* what, float** out) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return set_error(KX_ERR_LAUNCH, "%s: hipGetDevice failed: %s", what, hipGetErrorString(err));
+  if (dev < 0 || dev >= KX_MAX_DEVICES) return set_error(KX_ERR_UNSUPPORTED, "%s: device %d out of range", what, dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !p)
+      return set_error(KX_ERR_LAUNCH, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", what, dev,
+                       hipGetErrorString(err));
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return KX_OK;
+}
+
+}  // namespace
+
+extern "C" int kx_gemm_splitk_bf16(const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias,
+                                   void* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int epilogue,
+                                   const void* resid, int64_t ldr, const float* gate, int64_t gate_div,
+                                   int64_t gate_stride, void* workspace, int64_t workspace_bytes, int splits,
+                                   kx_stream_t stream) {
+  const char* what = "kx_gemm_splitk_bf16";
+  KX_REQUIRE(workspace, "%s: null tensor", what);
+  const int rc = check_splitk(what, a, lda, w, ldw, bias, c, ldc, m, n, k, epilogue, resid, ldr, gate, gate_div,
+                              gate_stride, splits);
+  if (rc) return rc;
+  KX_REQUIRE(aligned16(workspace), "%s: workspace must be 16-byte aligned", what);
+  KX_REQUIRE(workspace_bytes >= (int64_t)splits * m * n * 4,
+             "%s: workspace of %lld bytes is below splits * m * n * 4 = %lld", what, (long long)workspace_bytes,
+             (long long)splits * m * n * 4);
+  return run_splitk(what, a, lda, w, ldw, bias, c, ldc, m, n, k, epilogue, resid, ldr, gate, gate_div, gate_stride,
+                    static_cast<float*>(workspace), splits, (hipStream_t)stream);
+}
+
+extern "C" int kx_gemm_splitk_noalloc_bf16(const void* a, int64_t lda, const void* w, int64_t ldw,
+                                           const void* bias, void* c, int64_t ldc, int64_t m, int64_t n, int64_t k,
+                                           int epilogue, const void* resid, int64_t ldr, const float* gate,
+                                           int64_t gate_div, int64_t gate_stride, int splits, kx_stream_t stream) {
+  const char* what = "kx_gemm_splitk_noalloc_bf16";
+  const int rc = check_splitk(what, a, lda, w, ldw, bias, c, ldc, m, n, k, epilogue, resid, ldr, gate, gate_div,
+                              gate_stride, splits);
+  if (rc) return rc;
+  KX_REQUIRE((int64_t)splits * m * n * 4 <= KX_SPLITK_SCRATCH_BYTES,
+             "%s: splits * m * n * 4 = %lld bytes exceeds the %lld-byte static scratch", what,
+             (long long)splits * m * n * 4, (long long)KX_SPLITK_SCRATCH_BYTES);
+  float* parts = nullptr;
+  const int arc = scratch_address(what, &parts);
+  if (arc) return arc;
+  return run_splitk(what, a, lda, w, ldw, bias, c, ldc, m, n, k, epilogue, resid, ldr, gate, gate_div, gate_stride,
+                    parts, splits, (hipStream_t)stream);
 }
