@@ -271,9 +271,14 @@ class DoubleBlock:
         self.attn.fuse_projections()
 
     def __call__(self, image: torch.Tensor, text: torch.Tensor, image_mod: torch.Tensor, text_mod: torch.Tensor,
-                 positions: tuple[torch.Tensor, torch.Tensor], reference_kv=None, layer: int = 0):
-        if image.dtype != torch.bfloat16 or text.dtype != torch.bfloat16:
-            raise ValueError("DoubleBlock takes bfloat16 image and text on MI355X")
+                 positions: tuple[torch.Tensor, torch.Tensor], reference_kv=None, layer: int = 0, *,
+                 out_dtype: torch.dtype | None = None):
+        """``(image, text)`` after the block, in ``out_dtype`` (default: the input dtype). The
+        streams may be bfloat16 (the reference's hidden dtype) or an FP32 residual stream carried
+        across blocks, which skips the rounding of the hidden state between blocks."""
+        if image.dtype != text.dtype or image.dtype not in (torch.bfloat16, torch.float32):
+            raise ValueError("DoubleBlock takes bfloat16 (or fp32 residual stream) image and text on MI355X")
+        out_dtype = image.dtype if out_dtype is None else out_dtype
         shift, scale, gate, ff_shift, ff_scale, ff_gate = _split_mod(image_mod, 6)
         ts, tc, tg, fs, fc, fg = _split_mod(text_mod, 6)
         # image1/text1: the residual streams in FP32 between the two adds
@@ -281,9 +286,8 @@ class DoubleBlock:
             normalized(image, shift, scale), normalized(text, ts, tc), positions, reference_kv, layer,
             image_residual=image, image_gate=gate, text_residual=text, text_gate=tg, out_dtype=torch.float32,
         )
-        image2 = self.ff(normalized(image1, ff_shift, ff_scale), residual=image1, gate=ff_gate,
-                         out_dtype=image.dtype)
-        text2 = self.ff_context(normalized(text1, fs, fc), residual=text1, gate=fg, out_dtype=text.dtype)
+        image2 = self.ff(normalized(image1, ff_shift, ff_scale), residual=image1, gate=ff_gate, out_dtype=out_dtype)
+        text2 = self.ff_context(normalized(text1, fs, fc), residual=text1, gate=fg, out_dtype=out_dtype)
         return image2, text2
 
 
@@ -332,12 +336,15 @@ class SingleBlock:
         self.attn = SingleAttention(heads=heads, head_dim=head_dim)
 
     def __call__(self, value: torch.Tensor, modulation: torch.Tensor, positions: tuple[torch.Tensor, torch.Tensor],
-                 reference_kv=None, layer: int = 0, text_tokens: int = 0) -> torch.Tensor:
-        if value.dtype != torch.bfloat16:
-            raise ValueError("SingleBlock takes bfloat16 values on MI355X")
+                 reference_kv=None, layer: int = 0, text_tokens: int = 0, *,
+                 out_dtype: torch.dtype | None = None) -> torch.Tensor:
+        """The block's output in ``out_dtype`` (default: the input dtype); ``value`` may be
+        bfloat16 or an FP32 residual stream carried across blocks."""
+        if value.dtype not in (torch.bfloat16, torch.float32):
+            raise ValueError("SingleBlock takes bfloat16 (or fp32 residual stream) values on MI355X")
         shift, scale, gate = _split_mod(modulation, 3)
         return self.attn(normalized(value, shift, scale), positions, reference_kv, layer, text_tokens,
-                         residual=value, gate=gate, out_dtype=value.dtype)
+                         residual=value, gate=gate, out_dtype=value.dtype if out_dtype is None else out_dtype)
 
 
 class Modulation:

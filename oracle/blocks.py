@@ -30,6 +30,7 @@ from .ops import (
 )
 
 __all__ = [
+    "KX_SITES",
     "config1_double_block",
     "flux_double_block",
     "flux_single_block",
@@ -39,6 +40,7 @@ __all__ = [
     "ltx_feed_forward",
     "ltx_av_block",
     "ltx_video_block",
+    "rounding",
     "sigmoid",
 ]
 
@@ -65,8 +67,31 @@ def _lin(params: dict, name: str, value: np.ndarray) -> np.ndarray:
     return linear(value, params[f"{name}.weight"], bias)
 
 
-def _keep(value: np.ndarray) -> np.ndarray:
+def _keep(value: np.ndarray, site: str = "graph") -> np.ndarray:
     return value
+
+
+# Rounding sites of a bf16 execution: where an array is stored in the activation dtype. The
+# reference's MLX graph stores every intermediate (``bf16_graph``). This build's MI355X path
+# stores only the operands its kernels read in bf16 (``KX_SITES``): the modulated norm output, each
+# projection that feeds another kernel, the 2*sigmoid head gate, Q/K after their norm (and RoPE) in
+# one rounding, the (gated) attention output, the modulated text context and the GELU / SwiGLU
+# output; the output projections write the residual stream in FP32 through their epilogues.
+KX_SITES = frozenset({"norm", "proj", "gate", "qk", "attn_gated", "ctx", "act"})
+
+
+def rounding(mode) -> callable:
+    """``store(value, site)`` for a rounding mode: ``None``/``False`` (FP32 evaluation),
+    ``True``/``"graph"`` (the reference's bf16 graph: every site), ``"kx"`` (``KX_SITES``) or an
+    explicit set of site names."""
+    if not mode:
+        return _keep
+    if mode is True or mode == "graph":
+        return lambda value, site="graph": to_bf16(value)
+    sites = KX_SITES if mode == "kx" else mode
+    if isinstance(sites, (set, frozenset)):
+        return lambda value, site="graph": to_bf16(value) if site in sites else value
+    raise ValueError(f"unknown rounding mode {mode!r}")
 
 
 def ltx_attention(params: dict, prefix: str, value, *, heads: int, context=None, pe=None, k_pe=None, eps=1e-6,
@@ -80,31 +105,35 @@ def ltx_attention(params: dict, prefix: str, value, *, heads: int, context=None,
     source = x if context is None else np.asarray(context, dtype=F32)
     head_gate = None
     if f"{prefix}.to_gate_logits.weight" in params or f"{prefix}.to_gate_logits.wq" in params:
-        head_gate = store(F32(2.0) * store(sigmoid(store(_lin(params, f"{prefix}.to_gate_logits", x)))))
-    v = store(_lin(params, f"{prefix}.to_v", source))
-    q = store(rms_norm(store(_lin(params, f"{prefix}.to_q", x)), params[f"{prefix}.q_norm.weight"], eps))
-    k = store(rms_norm(store(_lin(params, f"{prefix}.to_k", source)), params[f"{prefix}.k_norm.weight"], eps))
+        logits = store(_lin(params, f"{prefix}.to_gate_logits", x), "gate_logits")
+        head_gate = store(F32(2.0) * store(sigmoid(logits), "gate_sigmoid"), "gate")
+    v = store(_lin(params, f"{prefix}.to_v", source), "proj")
+    q = store(rms_norm(store(_lin(params, f"{prefix}.to_q", x), "proj"), params[f"{prefix}.q_norm.weight"], eps),
+              "qk_norm")
+    k = store(rms_norm(store(_lin(params, f"{prefix}.to_k", source), "proj"), params[f"{prefix}.k_norm.weight"],
+                       eps), "qk_norm")
     if pe is not None:
         cos, sin = pe
-        q = store(split_rope(q[None], cos, sin)[0])
+        q = split_rope(q[None], cos, sin)[0]
         k_cos, k_sin = pe if k_pe is None else k_pe
-        k = store(split_rope(k[None], k_cos, k_sin)[0])
-    out = store(attention(q, k, v, heads=heads))
+        k = split_rope(k[None], k_cos, k_sin)[0]
+    q, k = store(q, "qk"), store(k, "qk")
+    out = store(attention(q, k, v, heads=heads), "attn")
     if head_gate is not None:
         tokens, width = out.shape
-        out = store((out.reshape(tokens, heads, width // heads) * head_gate[:, :, None]).reshape(tokens, width))
-    return store(_lin(params, f"{prefix}.to_out", out))
+        out = (out.reshape(tokens, heads, width // heads) * head_gate[:, :, None]).reshape(tokens, width)
+    return store(_lin(params, f"{prefix}.to_out", store(out, "attn_gated")), "out_proj")
 
 
 def ltx_feed_forward(params: dict, prefix: str, value, store=_keep) -> np.ndarray:
     """``project_out(gelu_approx(project_in(x)))``
     (``kinomlx/models/ltx2/transformer/feed_forward.py:80-97``)."""
-    hidden = store(gelu_approx(store(_lin(params, f"{prefix}.proj_in", value))))
-    return store(_lin(params, f"{prefix}.proj_out", hidden))
+    hidden = store(gelu_approx(store(_lin(params, f"{prefix}.proj_in", value), "ff_in")), "act")
+    return store(_lin(params, f"{prefix}.proj_out", hidden), "out_proj")
 
 
 def ltx_video_block(params: dict, x, context, pe, *, heads: int, eps: float = 1e-6,
-                    bf16_graph: bool = False) -> np.ndarray:
+                    bf16_graph: bool = False, rounding_mode=None) -> np.ndarray:
     """Video branch of ``BasicAVTransformerBlock.__call__``
     (``kinomlx/models/ltx2/transformer/transformer.py:225-276,373-392``) with the text
     cross-attention of ``:201-223``.
@@ -120,27 +149,28 @@ def ltx_video_block(params: dict, x, context, pe, *, heads: int, eps: float = 1e
     sigmoid and the doubled gate (``attention.py:319-325``), Q/K norms, RoPE, attention, the
     per-head gate product, the gated residual (``transformer.py:26-30``), ``_gate`` and the
     cross-attention sum (``:266-276``), GELU (``feed_forward.py:80-97``). It measures the error
-    the reference itself carries against the FP32 evaluation.
+    the reference itself carries against the FP32 evaluation. ``rounding_mode="kx"`` rounds only
+    where this build's MI355X path stores bf16 (``KX_SITES``).
     """
-    store = to_bf16 if bf16_graph else _keep
+    store = rounding(rounding_mode or bf16_graph)
     ada = np.asarray(params["ada"], dtype=F32)
     prompt = np.asarray(params["prompt"], dtype=F32)
     value = np.asarray(x, dtype=F32)
 
     def _adaln(v, scale, shift):
-        return store((store(rms_norm(v, eps=eps)) * (F32(1.0) + scale) + shift).astype(F32))
+        return store((store(rms_norm(v, eps=eps), "norm_raw") * (F32(1.0) + scale) + shift).astype(F32), "norm")
 
     normalized_x = _adaln(value, ada[1], ada[0])
     attended = ltx_attention(params, "attn1", normalized_x, heads=heads, pe=pe, eps=eps, store=store)
-    value = store(gated_residual(value, attended, ada[2]))
+    value = store(gated_residual(value, attended, ada[2]), "resid")
 
     query = _adaln(value, ada[7], ada[6])
-    ctx = store(modulate(context, prompt[1], prompt[0]))
+    ctx = store(modulate(context, prompt[1], prompt[0]), "ctx")
     cross = ltx_attention(params, "attn2", query, heads=heads, context=ctx, eps=eps, store=store)
-    value = store((value + store(gate(cross, ada[8]))).astype(F32))
+    value = store((value + store(gate(cross, ada[8]), "gated")).astype(F32), "resid")
 
     normalized_x = _adaln(value, ada[4], ada[3])
-    return store(gated_residual(value, ltx_feed_forward(params, "ff", normalized_x, store), ada[5]))
+    return store(gated_residual(value, ltx_feed_forward(params, "ff", normalized_x, store), ada[5]), "resid")
 
 
 def _heads_norm(value, weight, heads: int, eps: float = 1e-6) -> np.ndarray:
@@ -161,9 +191,9 @@ def _joint_attention(q_parts, k_parts, v_parts, rope, heads: int, store=_keep) -
     k = np.concatenate(k_parts, axis=0)
     v = np.concatenate(v_parts, axis=0)
     cos, sin = rope
-    q = store(_heads_rope(q, cos, sin, heads))
-    k = store(_heads_rope(k, cos, sin, heads))
-    return store(attention(q, k, v, heads=heads))
+    q = store(_heads_rope(q, cos, sin, heads), "qk")
+    k = store(_heads_rope(k, cos, sin, heads), "qk")
+    return store(store(attention(q, k, v, heads=heads), "attn"), "attn_gated")
 
 
 def _flux_normalized(store):
@@ -171,8 +201,8 @@ def _flux_normalized(store):
     activation dtype, then the compiled modulation (``flux2/transformer.py:56-60``)."""
 
     def run(value, shift, scale):
-        n = store(layer_norm(value))
-        return store((n * (F32(1.0) + scale) + shift).astype(F32))
+        n = store(layer_norm(value), "norm_raw")
+        return store((n * (F32(1.0) + scale) + shift).astype(F32), "norm")
 
     return run
 
@@ -183,13 +213,13 @@ def _flux_swiglu(store):
 
     def run(value):
         half = value.shape[-1] // 2
-        return store((store(silu(value[..., :half])) * value[..., half:]).astype(F32))
+        return store((store(silu(value[..., :half]), "act_silu") * value[..., half:]).astype(F32), "act")
 
     return run
 
 
 def flux_double_block(params: dict, image, text, image_mod, text_mod, rope, *, heads: int, ff: str = "swiglu",
-                      bf16_graph: bool = False):
+                      bf16_graph: bool = False, rounding_mode=None):
     """FLUX.2 ``DoubleBlock.__call__`` (``kinomlx/models/flux2/transformer.py:136-167``) with
     ``DoubleAttention`` (``:88-133``): LayerNorm modulation, per-head QKNorm, joint [text, image]
     attention with adjacent-pair RoPE, gated residuals.
@@ -202,8 +232,9 @@ def flux_double_block(params: dict, image, text, image_mod, text_mod, rope, *, h
     materialises in the activation dtype is rounded to bf16 — the layer norm and the modulated
     value, each projection, the QK norms, each rotation, the attention output, the gate
     products and the residual sums (``:155-166``), SiLU and the SwiGLU product.
+    ``rounding_mode="kx"`` rounds only where this build's MI355X path stores bf16 (``KX_SITES``).
     """
-    store = to_bf16 if bf16_graph else _keep
+    store = rounding(rounding_mode or bf16_graph)
     norm = _flux_normalized(store)
     glu = _flux_swiglu(store)
     image = np.asarray(image, dtype=F32)
@@ -211,11 +242,11 @@ def flux_double_block(params: dict, image, text, image_mod, text_mod, rope, *, h
     im = np.asarray(image_mod, dtype=F32)
     tm = np.asarray(text_mod, dtype=F32)
 
-    def lin(name, value):
-        return store(_lin(params, name, value))
+    def lin(name, value, site="proj"):
+        return store(_lin(params, name, value), site)
 
     def qk(name, norm_name, value):
-        return store(_heads_norm(lin(name, value), params[norm_name], heads))
+        return store(_heads_norm(lin(name, value), params[norm_name], heads), "qk_norm")
 
     img_n = norm(image, im[0], im[1])
     txt_n = norm(text, tm[0], tm[1])
@@ -224,45 +255,48 @@ def flux_double_block(params: dict, image, text, image_mod, text_mod, rope, *, h
     v = [lin("attn.add_v_proj", txt_n), lin("attn.to_v", img_n)]
     result = _joint_attention(q, k, v, rope, heads, store)
     t_text = text.shape[0]
-    ai = lin("attn.to_out", result[t_text:])
-    at = lin("attn.to_add_out", result[:t_text])
-    image = store((image + store(im[2] * ai)).astype(F32))
-    text = store((text + store(tm[2] * at)).astype(F32))
+    ai = lin("attn.to_out", result[t_text:], "out_proj")
+    at = lin("attn.to_add_out", result[:t_text], "out_proj")
+    image = store((image + store(im[2] * ai, "gated")).astype(F32), "resid")
+    text = store((text + store(tm[2] * at, "gated")).astype(F32), "resid")
 
     def feed_forward(prefix: str, value):
         if ff == "swiglu":
-            return lin(f"{prefix}.linear_out", glu(lin(f"{prefix}.linear_in", value)))
+            return lin(f"{prefix}.linear_out", glu(lin(f"{prefix}.linear_in", value)), "out_proj")
         return ltx_feed_forward(params, prefix, value, store)
 
-    image = store((image + store(im[5] * feed_forward("ff", norm(image, im[3], im[4])))).astype(F32))
-    text = store((text + store(tm[5] * feed_forward("ff_context", norm(text, tm[3], tm[4])))).astype(F32))
+    image = store((image + store(im[5] * feed_forward("ff", norm(image, im[3], im[4])), "gated")).astype(F32), "resid")
+    text = store((text + store(tm[5] * feed_forward("ff_context", norm(text, tm[3], tm[4])), "gated")).astype(F32),
+                 "resid")
     return image, text
 
 
-def flux_single_block(params: dict, value, modulation, rope, *, heads: int, width: int, bf16_graph: bool = False):
+def flux_single_block(params: dict, value, modulation, rope, *, heads: int, width: int, bf16_graph: bool = False,
+                      rounding_mode=None):
     """FLUX.2 ``SingleBlock.__call__`` (``kinomlx/models/flux2/transformer.py:201-220``) with
     ``SingleAttention`` (``:170-198``): one fused projection split [D, 2D, 3D], per-head QKNorm,
     adjacent-pair RoPE, ``to_out(concat[attention, swiglu(mlp)])``, gated residual.
-    ``modulation`` is ``(3, D)``: shift, scale, gate. ``bf16_graph`` as ``flux_double_block``."""
-    store = to_bf16 if bf16_graph else _keep
+    ``modulation`` is ``(3, D)``: shift, scale, gate. ``bf16_graph`` and ``rounding_mode`` as
+    ``flux_double_block``."""
+    store = rounding(rounding_mode or bf16_graph)
     x = np.asarray(value, dtype=F32)
     mod = np.asarray(modulation, dtype=F32)
     n = _flux_normalized(store)(x, mod[0], mod[1])
-    fused = store(_lin(params, "attn.to_qkv_mlp_proj", n))
+    fused = store(_lin(params, "attn.to_qkv_mlp_proj", n), "proj")
     q, k, v, mlp = fused[:, :width], fused[:, width : 2 * width], fused[:, 2 * width : 3 * width], fused[:, 3 * width :]
-    q = store(_heads_norm(q, params["attn.norm_q.weight"], heads))
-    k = store(_heads_norm(k, params["attn.norm_k.weight"], heads))
+    q = store(_heads_norm(q, params["attn.norm_q.weight"], heads), "qk_norm")
+    k = store(_heads_norm(k, params["attn.norm_k.weight"], heads), "qk_norm")
     attn = _joint_attention([q], [k], [v], rope, heads, store)
-    out = store(_lin(params, "attn.to_out", np.concatenate([attn, _flux_swiglu(store)(mlp)], axis=-1)))
-    return store((x + store(mod[2] * out)).astype(F32))
+    out = store(_lin(params, "attn.to_out", np.concatenate([attn, _flux_swiglu(store)(mlp)], axis=-1)), "out_proj")
+    return store((x + store(mod[2] * out, "gated")).astype(F32), "resid")
 
 
 def config1_double_block(params: dict, image, text, image_mod, text_mod, rope, *, heads: int,
-                         bf16_graph: bool = False):
+                         bf16_graph: bool = False, rounding_mode=None):
     """This build's config-1 block: the FLUX.2 double-stream structure with LTX's GELU-tanh
     feed-forward (biases on the feed-forward only) and Krea-style per-axis RoPE tables."""
     return flux_double_block(params, image, text, image_mod, text_mod, rope, heads=heads, ff="gelu",
-                             bf16_graph=bf16_graph)
+                             bf16_graph=bf16_graph, rounding_mode=rounding_mode)
 
 
 def krea_attention(params: dict, prefix: str, value, *, heads: int, kv_heads: int, eps: float, rotary=None,
@@ -301,7 +335,7 @@ def krea_block(params: dict, value, modulation, rotary, *, heads: int, kv_heads:
     ``norm1``/``norm2`` are zero-centred RMSNorms with weights (``:29-46``); the feed-forward is
     ``down(silu(gate(x)) * up(x))`` (``:199-214``). ``bf16_graph=True`` rounds every array the
     MLX graph materialises to bf16, as ``ltx_video_block`` does."""
-    store = to_bf16 if bf16_graph else _keep
+    store = rounding(bf16_graph)
     x = np.asarray(value, dtype=F32)
     mod = np.asarray(modulation, dtype=F32)
     pre_s, pre_sh, pre_g, post_s, post_sh, post_g = mod
@@ -351,7 +385,7 @@ def ltx_av_block(params: dict, video_x, audio_x, video_context, audio_context, p
     ``audio_to_video_attn.*`` / ``video_to_audio_attn.*`` and the ``(5, D)`` rows ``av_video`` /
     ``av_audio`` = table + cross timesteps (``:188-199``): scale a2v, shift a2v, scale v2a,
     shift v2a, gate. Returns ``(video, audio)``, tokens leading."""
-    store = to_bf16 if bf16_graph else _keep
+    store = rounding(bf16_graph)
     v, _adaln = _ltx_first_branches(params, "", video_x, video_context, pe, heads=heads, eps=eps, store=store)
     a, _ = _ltx_first_branches(params, "audio_", audio_x, audio_context, audio_pe, heads=audio_heads, eps=eps,
                                store=store)

@@ -99,3 +99,21 @@ def build_krea_block(p, hidden, heads, kv_heads, device, *, fuse=True):
     if fuse:
         block.fuse_projections()
     return block
+
+
+def dense_params(op: dict) -> dict:
+    """Oracle parameters with every affine-quantized layer replaced by its dequantized weight
+    (``name.weight`` = the oracle's bit-exact ``bf16(scale * q + bias)`` as float32), the operand
+    the quantized GEMM multiplies; for the FP32 torch evaluation of quantized blocks."""
+    out = {}
+    for name, value in op.items():
+        if name.endswith((".scales", ".biases", ".group_size", ".bits")):
+            continue
+        if name.endswith(".wq"):
+            base = name[:-len(".wq")]
+            out[f"{base}.weight"] = oracle.dequantize_affine(
+                value, op[f"{base}.scales"], op[f"{base}.biases"], group_size=int(op[f"{base}.group_size"]),
+                bits=int(op[f"{base}.bits"]))
+        else:
+            out[name] = value
+    return out

@@ -8,13 +8,33 @@ oracle would take minutes. ``tests/test_blocks_cpu.py`` pins it against the nump
 import torch
 
 
-def _keep(x):
+def _keep(x, site="graph"):
     return x
 
 
-def bf16_store(x):
+def bf16_store(x, site="graph"):
     """Round an FP32 tensor to bf16 values (kept in FP32): the reference's materialised arrays."""
     return x.to(torch.bfloat16).float()
+
+
+# This build's bf16 storage points (the same names as ``oracle.blocks.KX_SITES``).
+KX_SITES = frozenset({"norm", "proj", "gate", "qk", "attn_gated", "ctx", "act"})
+
+
+def _kx_store(x, site="graph"):
+    return x.to(torch.bfloat16).float() if site in KX_SITES else x
+
+
+def rounding(mode):
+    """``None``/``False``: FP32; ``True``/``"graph"``: the reference's bf16 graph; ``"kx"``: only
+    where the MI355X path stores bf16 (as ``oracle.blocks.rounding``)."""
+    if not mode:
+        return _keep
+    if mode is True or mode == "graph":
+        return bf16_store
+    if mode == "kx":
+        return _kx_store
+    raise ValueError(f"unknown rounding mode {mode!r}")
 
 
 def _lin(p, name, x):
@@ -54,31 +74,33 @@ def _attention(q, k, v, heads):
 
 def _ltx_attention(p, prefix, x, heads, context=None, pe=None, st=_keep):
     source = x if context is None else context
-    gate = st(2 * st(torch.sigmoid(st(_lin(p, f"{prefix}.to_gate_logits", x)))))
-    v = st(_lin(p, f"{prefix}.to_v", source))
-    q = st(_rms(st(_lin(p, f"{prefix}.to_q", x)), p[f"{prefix}.q_norm.weight"]))
-    k = st(_rms(st(_lin(p, f"{prefix}.to_k", source)), p[f"{prefix}.k_norm.weight"]))
+    gate = st(2 * st(torch.sigmoid(st(_lin(p, f"{prefix}.to_gate_logits", x), "gate_logits")), "gate_sigmoid"),
+              "gate")
+    v = st(_lin(p, f"{prefix}.to_v", source), "proj")
+    q = st(_rms(st(_lin(p, f"{prefix}.to_q", x), "proj"), p[f"{prefix}.q_norm.weight"]), "qk_norm")
+    k = st(_rms(st(_lin(p, f"{prefix}.to_k", source), "proj"), p[f"{prefix}.k_norm.weight"]), "qk_norm")
     if pe is not None:
-        q, k = st(_split_rope(q, *pe)), st(_split_rope(k, *pe))
-    o = st(_attention(q, k, v, heads))
+        q, k = _split_rope(q, *pe), _split_rope(k, *pe)
+    q, k = st(q, "qk"), st(k, "qk")
+    o = st(_attention(q, k, v, heads), "attn")
     t, width = o.shape
-    o = st((o.reshape(t, heads, width // heads) * gate[:, :, None]).reshape(t, width))
-    return st(_lin(p, f"{prefix}.to_out", o))
+    o = st((o.reshape(t, heads, width // heads) * gate[:, :, None]).reshape(t, width), "attn_gated")
+    return st(_lin(p, f"{prefix}.to_out", o), "out_proj")
 
 
-def ltx_video_block(p, x, context, pe, heads, bf16_graph=False):
+def ltx_video_block(p, x, context, pe, heads, bf16_graph=False, rounding_mode=None):
     """``p``: fp32 tensors named as in ``oracle.ltx_video_block`` (dense weights);
-    ``bf16_graph`` rounds at the same points as the oracle's ``bf16_graph`` mode."""
-    st = bf16_store if bf16_graph else _keep
+    ``bf16_graph`` / ``rounding_mode`` round at the same sites as the oracle's modes."""
+    st = rounding(rounding_mode or bf16_graph)
     ada, prompt = p["ada"], p["prompt"]
-    n = st(st(_rms(x)) * (1 + ada[1]) + ada[0])
-    x = st(x + _ltx_attention(p, "attn1", n, heads, pe=pe, st=st) * ada[2])
-    q = st(st(_rms(x)) * (1 + ada[7]) + ada[6])
-    ctx = st(context * (1 + prompt[1]) + prompt[0])
-    x = st(x + st(_ltx_attention(p, "attn2", q, heads, context=ctx, st=st) * ada[8]))
-    n = st(st(_rms(x)) * (1 + ada[4]) + ada[3])
-    h = st(torch.nn.functional.gelu(st(_lin(p, "ff.proj_in", n)), approximate="tanh"))
-    return st(x + st(_lin(p, "ff.proj_out", h)) * ada[5])
+    n = st(st(_rms(x), "norm_raw") * (1 + ada[1]) + ada[0], "norm")
+    x = st(x + _ltx_attention(p, "attn1", n, heads, pe=pe, st=st) * ada[2], "resid")
+    q = st(st(_rms(x), "norm_raw") * (1 + ada[7]) + ada[6], "norm")
+    ctx = st(context * (1 + prompt[1]) + prompt[0], "ctx")
+    x = st(x + st(_ltx_attention(p, "attn2", q, heads, context=ctx, st=st) * ada[8], "gated"), "resid")
+    n = st(st(_rms(x), "norm_raw") * (1 + ada[4]) + ada[3], "norm")
+    h = st(torch.nn.functional.gelu(st(_lin(p, "ff.proj_in", n), "ff_in"), approximate="tanh"), "act")
+    return st(x + st(_lin(p, "ff.proj_out", h), "out_proj") * ada[5], "resid")
 
 
 def _layer_norm(x, eps=1e-6):
@@ -104,21 +126,21 @@ def _heads_rms(x, w, heads):
 
 def _swiglu(x, st):
     half = x.shape[-1] // 2
-    return st(st(torch.nn.functional.silu(x[..., :half])) * x[..., half:])
+    return st(st(torch.nn.functional.silu(x[..., :half]), "act_silu") * x[..., half:], "act")
 
 
-def flux_double_block(p, image, text, im, tm, rope, heads, ff="swiglu", bf16_graph=False):
-    """Torch form of ``oracle.flux_double_block`` (same names, same rounding points)."""
-    st = bf16_store if bf16_graph else _keep
+def flux_double_block(p, image, text, im, tm, rope, heads, ff="swiglu", bf16_graph=False, rounding_mode=None):
+    """Torch form of ``oracle.flux_double_block`` (same names, same rounding sites)."""
+    st = rounding(rounding_mode or bf16_graph)
 
     def norm(x, shift, scale):
-        return st(st(_layer_norm(x)) * (1 + scale) + shift)
+        return st(st(_layer_norm(x), "norm_raw") * (1 + scale) + shift, "norm")
 
-    def lin(name, x):
-        return st(_lin(p, name, x))
+    def lin(name, x, site="proj"):
+        return st(_lin(p, name, x), site)
 
     def qk(name, norm_name, x):
-        return st(_heads_rms(lin(name, x), p[norm_name], heads))
+        return st(_heads_rms(lin(name, x), p[norm_name], heads), "qk_norm")
 
     img_n, txt_n = norm(image, im[0], im[1]), norm(text, tm[0], tm[1])
     q = torch.cat([qk("attn.add_q_proj", "attn.norm_added_q.weight", txt_n),
@@ -126,31 +148,31 @@ def flux_double_block(p, image, text, im, tm, rope, heads, ff="swiglu", bf16_gra
     k = torch.cat([qk("attn.add_k_proj", "attn.norm_added_k.weight", txt_n),
                    qk("attn.to_k", "attn.norm_k.weight", img_n)])
     v = torch.cat([lin("attn.add_v_proj", txt_n), lin("attn.to_v", img_n)])
-    q, k = st(_pair_rope(q, *rope, heads)), st(_pair_rope(k, *rope, heads))
-    result = st(_attention(q, k, v, heads))
+    q, k = st(_pair_rope(q, *rope, heads), "qk"), st(_pair_rope(k, *rope, heads), "qk")
+    result = st(st(_attention(q, k, v, heads), "attn"), "attn_gated")
     tt = text.shape[0]
-    image = st(image + st(im[2] * lin("attn.to_out", result[tt:])))
-    text = st(text + st(tm[2] * lin("attn.to_add_out", result[:tt])))
+    image = st(image + st(im[2] * lin("attn.to_out", result[tt:], "out_proj"), "gated"), "resid")
+    text = st(text + st(tm[2] * lin("attn.to_add_out", result[:tt], "out_proj"), "gated"), "resid")
 
     def feed_forward(prefix, x):
         if ff == "swiglu":
-            return lin(f"{prefix}.linear_out", _swiglu(lin(f"{prefix}.linear_in", x), st))
-        h = st(torch.nn.functional.gelu(lin(f"{prefix}.proj_in", x), approximate="tanh"))
-        return lin(f"{prefix}.proj_out", h)
+            return lin(f"{prefix}.linear_out", _swiglu(lin(f"{prefix}.linear_in", x), st), "out_proj")
+        h = st(torch.nn.functional.gelu(lin(f"{prefix}.proj_in", x, "ff_in"), approximate="tanh"), "act")
+        return lin(f"{prefix}.proj_out", h, "out_proj")
 
-    image = st(image + st(im[5] * feed_forward("ff", norm(image, im[3], im[4]))))
-    text = st(text + st(tm[5] * feed_forward("ff_context", norm(text, tm[3], tm[4]))))
+    image = st(image + st(im[5] * feed_forward("ff", norm(image, im[3], im[4])), "gated"), "resid")
+    text = st(text + st(tm[5] * feed_forward("ff_context", norm(text, tm[3], tm[4])), "gated"), "resid")
     return image, text
 
 
-def flux_single_block(p, x, mod, rope, heads, width, bf16_graph=False):
+def flux_single_block(p, x, mod, rope, heads, width, bf16_graph=False, rounding_mode=None):
     """Torch form of ``oracle.flux_single_block``."""
-    st = bf16_store if bf16_graph else _keep
-    n = st(st(_layer_norm(x)) * (1 + mod[1]) + mod[0])
-    fused = st(_lin(p, "attn.to_qkv_mlp_proj", n))
-    q = st(_heads_rms(fused[:, :width], p["attn.norm_q.weight"], heads))
-    k = st(_heads_rms(fused[:, width:2 * width], p["attn.norm_k.weight"], heads))
-    q, k = st(_pair_rope(q, *rope, heads)), st(_pair_rope(k, *rope, heads))
-    attn = st(_attention(q, k, fused[:, 2 * width:3 * width], heads))
-    out = st(_lin(p, "attn.to_out", torch.cat([attn, _swiglu(fused[:, 3 * width:], st)], -1)))
-    return st(x + st(mod[2] * out))
+    st = rounding(rounding_mode or bf16_graph)
+    n = st(st(_layer_norm(x), "norm_raw") * (1 + mod[1]) + mod[0], "norm")
+    fused = st(_lin(p, "attn.to_qkv_mlp_proj", n), "proj")
+    q = st(_heads_rms(fused[:, :width], p["attn.norm_q.weight"], heads), "qk_norm")
+    k = st(_heads_rms(fused[:, width:2 * width], p["attn.norm_k.weight"], heads), "qk_norm")
+    q, k = st(_pair_rope(q, *rope, heads), "qk"), st(_pair_rope(k, *rope, heads), "qk")
+    attn = st(st(_attention(q, k, fused[:, 2 * width:3 * width], heads), "attn"), "attn_gated")
+    out = st(_lin(p, "attn.to_out", torch.cat([attn, _swiglu(fused[:, 3 * width:], st)], -1)), "out_proj")
+    return st(x + st(mod[2] * out, "gated"), "resid")

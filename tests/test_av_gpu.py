@@ -1,5 +1,6 @@
-"""The joint audio/video LTX-2 block on the GPU against the oracle (block bar: cosine >= 0.9995,
-max abs <= max(2e-2, the reference bf16 graph's own error), for both streams)."""
+"""The joint audio/video LTX-2 block on the GPU against the oracle (block bar, both streams:
+cosine >= 0.9995 and |got - ref| <= 2e-2 + ulp_bf16(ref) / 2 elementwise, ``assert_block_bar``;
+the reference's own bf16 graph is printed beside it)."""
 
 import numpy as np
 import pytest
@@ -9,15 +10,13 @@ from kinomlx_amd import workloads
 from kinomlx_amd.ltx2.rope import precompute_freqs_cis
 from kinomlx_amd.ltx2.transformer import TransformerArgs
 from tests._av import AUDIO, SPEC, oracle_av_params, oracle_run, tables
-from tests.conftest import cosine, max_abs
+from tests.conftest import assert_block_bar
 
 pytestmark = pytest.mark.gpu
 
 
 def _check(got, ref, graph):
-    c, m, g = cosine(got, ref), max_abs(got, ref), max_abs(graph, ref)
-    print(f"cosine {c:.7f} max_abs {m:.4g} (reference bf16 graph {g:.4g}) max|ref| {np.abs(ref).max():.3f}")
-    assert np.all(np.isfinite(got)) and c >= 0.9995 and m <= max(2e-2, g), (c, m, g)
+    assert_block_bar(got, ref, "a/v", context=graph)
 
 
 def _args(p, inputs, device):

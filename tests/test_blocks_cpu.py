@@ -88,3 +88,51 @@ def test_torch_reference_matches_oracle_flux_single_block():
     got = _torch_ref.flux_single_block(tp, torch.from_numpy(x), torch.from_numpy(op["single_mod"]),
                                        tuple(torch.from_numpy(t) for t in rope), spec.heads, spec.dim).numpy()
     assert max_abs(got, ref) < 1e-4
+
+
+def test_kx_rounding_mode_matches_between_torch_and_oracle_and_sits_between_fp32_and_graph():
+    """The ``kx`` mode (bf16 only where the MI355X path stores bf16) agrees between the two
+    restatements; it rounds a strict subset of the graph's sites: its error against FP32 is
+    nonzero and below the graph's, and the block output (an FP32 residual stream) is not rounded."""
+    spec = workloads.LTXSpec(grid=(2, 3, 4), text_tokens=5, dim=256, heads=2, head_dim=128)
+    _, op, inputs, pe = ltx_case(spec)
+    x = inputs["x"][0].float().numpy()
+    ctx = inputs["context"][0].float().numpy()
+    fp32 = oracle.ltx_video_block(op, x, ctx, pe, heads=2)
+    graph = oracle.ltx_video_block(op, x, ctx, pe, heads=2, bf16_graph=True)
+    kx = oracle.ltx_video_block(op, x, ctx, pe, heads=2, rounding_mode="kx")
+    tp = {k: torch.from_numpy(np.asarray(v)) for k, v in op.items()}
+    got = _torch_ref.ltx_video_block(tp, torch.from_numpy(x), torch.from_numpy(ctx),
+                                     tuple(torch.from_numpy(t) for t in pe), heads=2, rounding_mode="kx").numpy()
+    assert max_abs(got, kx) < 0.25 * max_abs(kx, fp32)
+    assert 0 < max_abs(kx, fp32) < max_abs(graph, fp32)
+    assert not np.array_equal(kx, oracle.to_bf16(kx))
+    assert oracle.KX_SITES == _torch_ref.KX_SITES
+
+
+def test_kx_rounding_mode_flux_blocks():
+    for ff in ("swiglu", "gelu"):
+        spec, (p, op, single, inputs, rope) = _flux_small(ff)
+        image, text = inputs["image"][0].float().numpy(), inputs["text"][0].float().numpy()
+        rope_t = tuple(torch.from_numpy(t) for t in rope)
+        tp = {k: torch.from_numpy(np.asarray(v)) for k, v in op.items()}
+        outs = {}
+        for mode in (None, "graph", "kx"):
+            outs[mode] = oracle.flux_double_block(op, image, text, op["image_mod"], op["text_mod"], rope,
+                                                  heads=spec.heads, ff=ff, rounding_mode=mode)
+        gi, gt = _torch_ref.flux_double_block(tp, torch.from_numpy(image), torch.from_numpy(text), tp["image_mod"],
+                                              tp["text_mod"], rope_t, spec.heads, ff=ff, rounding_mode="kx")
+        for i, got in enumerate((gi.numpy(), gt.numpy())):
+            err_kx = max_abs(outs["kx"][i], outs[None][i])
+            assert max_abs(got, outs["kx"][i]) < 0.25 * err_kx
+            assert 0 < err_kx < max_abs(outs["graph"][i], outs[None][i])
+        if ff == "swiglu":
+            x = np.concatenate([text, image])
+            ref = {m: oracle.flux_single_block(single, x, op["single_mod"], rope, heads=spec.heads, width=spec.dim,
+                                               rounding_mode=m) for m in (None, "graph", "kx")}
+            sp = {k: torch.from_numpy(np.asarray(v)) for k, v in single.items()}
+            got = _torch_ref.flux_single_block(sp, torch.from_numpy(x), torch.from_numpy(op["single_mod"]), rope_t,
+                                               spec.heads, spec.dim, rounding_mode="kx").numpy()
+            err_kx = max_abs(ref["kx"], ref[None])
+            assert max_abs(got, ref["kx"]) < 0.25 * err_kx
+            assert 0 < err_kx < max_abs(ref["graph"], ref[None])

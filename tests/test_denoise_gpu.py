@@ -6,7 +6,8 @@ Bars: the element-wise passes (X0, composite, Euler, finite check) are one FP32 
 the reference's roundings, so they are compared bit for bit with the oracle. The transcendental
 tables (timestep features, RoPE) are compared within a few FP32 ulps of the angle (the error of
 any FP32 sin / cos / exp implementation: |d| <= 1e-6 + 5e-7 |angle|). Outputs of GEMM chains
-use the block bar: cosine >= 0.9995 and max abs <= max(2e-2, the reference bf16 graph's error).
+use the block bar: cosine >= 0.9995 and |got - ref| <= 2e-2 + ulp_bf16(ref) / 2 elementwise
+(``assert_block_bar``; the reference's own bf16 graph is printed beside it).
 """
 
 import math
@@ -25,7 +26,7 @@ from kinomlx_amd.ltx2.timestep import get_timestep_embedding
 from kinomlx_amd.ltx2.wrappers import Modality, X0Model, _to_denoised
 from kinomlx_amd.samplers.steps import euler_step, euler_velocity_step
 from oracle.ops import F32, to_bf16
-from tests.conftest import cosine, max_abs
+from tests.conftest import assert_block_bar
 
 pytestmark = pytest.mark.gpu
 
@@ -103,11 +104,7 @@ def _model_case(num_blocks=2, seed=0):
 
 
 def _check(got, ref, graph):
-    c, m, g = cosine(got, ref), max_abs(got, ref), max_abs(graph, ref)
-    print(f"cosine {c:.7f} max_abs {m:.4g} (reference bf16 graph {g:.4g}) max|ref| {np.abs(ref).max():.3f}")
-    assert np.all(np.isfinite(got))
-    assert c >= 0.9995, c
-    assert m <= max(2e-2, g), (m, g)
+    assert_block_bar(got, ref, "", context=graph)
 
 
 def test_adaln_single_matches_oracle(device):

@@ -1,10 +1,12 @@
 """FLUX.2 and config-1 block parity on the GPU, through the MI355X operator surface
 (``kinomlx_amd.flux2``), against the FP32 oracle on the same seeded inputs.
 
-Tolerance (north star): cosine similarity >= 0.9995 and max abs error <= 2e-2 between the bf16
-block output and the FP32 evaluation; where outputs are large enough that one bf16 rounding of
-the output alone exceeds 2e-2, the bar is the reference's own bf16 execution error against the
-same FP32 evaluation (``bf16_graph=True``), as for the LTX block. The standalone adjacent-pair
+Bars (``tests.conftest.assert_block_parity``) against the FP32 evaluation: at D <= 1024 the north
+star (cosine similarity >= 0.9995 and every element within 2e-2 beyond the bf16 output's own
+rounding; the literal max abs error <= 2e-2 for blocks run with an FP32 residual stream, FP32 in
+and out); at D = 4096 (config 2) cosine >= 0.9995, relative L2 <= 6e-3 and an RMS error within
+1.25x the rounding noise of the FP32 evaluation rounded where this build stores bf16. Config 2's
+double block hands its output to the single block in FP32. The standalone adjacent-pair
 ``rotate`` is bit-exact.
 """
 
@@ -18,35 +20,29 @@ from kinomlx_amd.flux2 import kv as flux_kv
 from kinomlx_amd.flux2 import transformer as flux
 from tests import _torch_ref
 from tests._blocks import flux_case
-from tests.conftest import cosine, max_abs, rel_l2
+from tests.conftest import assert_block_parity, max_abs, rel_l2
 
 pytestmark = pytest.mark.gpu
 F32 = np.float32
-COS_MIN = 0.9995
-MAX_ABS = 2e-2
 
 
 def _np(t):
     return t.float().cpu().numpy()
 
 
-def _check(got, ref, graph, what):
-    assert np.all(np.isfinite(got)), what
-    c, m, g = cosine(got, ref), max_abs(got, ref), max_abs(graph, ref)
-    print(f"{what}: cosine {c:.7f} max_abs {m:.4g} (reference bf16 graph {g:.4g}) max|ref| {np.abs(ref).max():.3f}")
-    assert c >= COS_MIN, (what, c)
-    assert m <= max(MAX_ABS, g), (what, m, g)
-    if np.abs(ref).max() < 4.0:
-        assert m <= MAX_ABS, (what, m)
+def _check(got, ref, kx, graph, what, fp32_out=False, fp32_bar=True):
+    assert_block_parity(got, ref, what, ref_kx=kx, graph=graph, fp32_out=fp32_out, small=fp32_bar)
 
 
-def _run_double(spec, p, inputs, device, *, fuse=True, batch=1):
+def _run_double(spec, p, inputs, device, *, fuse=True, batch=1, fp32=False, out_dtype=None):
     block = workloads.build_flux_double_block(spec, p, device, fuse=fuse)
     image = inputs["image"].to(device).expand(batch, -1, -1).contiguous()
     text = inputs["text"].to(device).expand(batch, -1, -1).contiguous()
+    if fp32:
+        image, text = image.float(), text.float()
     im = p["image_mod"].reshape(1, -1).to(device).expand(batch, -1)
     tm = p["text_mod"].reshape(1, -1).to(device).expand(batch, -1)
-    i_out, t_out = block(image, text, im, tm, workloads.flux_tables(spec, device))
+    i_out, t_out = block(image, text, im, tm, workloads.flux_tables(spec, device), out_dtype=out_dtype)
     torch.cuda.synchronize()
     return i_out, t_out
 
@@ -67,8 +63,14 @@ def test_double_block_matches_oracle(device, spec):
     args = (op, image, text, op["image_mod"], op["text_mod"], rope)
     ri, rt = oracle.flux_double_block(*args, heads=spec.heads, ff=spec.ff)
     gi, gt = oracle.flux_double_block(*args, heads=spec.heads, ff=spec.ff, bf16_graph=True)
-    _check(_np(i_out[0]), ri, gi, "image")
-    _check(_np(t_out[0]), rt, gt, "text")
+    ki, kt = oracle.flux_double_block(*args, heads=spec.heads, ff=spec.ff, rounding_mode="kx")
+    small = spec.dim <= 1024
+    _check(_np(i_out[0]), ri, ki, gi, "image", fp32_bar=small)
+    _check(_np(t_out[0]), rt, kt, gt, "text", fp32_bar=small)
+    i32, t32 = _run_double(spec, p, inputs, device, fp32=True)
+    assert i32.dtype == torch.float32
+    _check(_np(i32[0]), ri, ki, None, "  image fp32 out", fp32_out=True, fp32_bar=small)
+    _check(_np(t32[0]), rt, kt, None, "  text fp32 out", fp32_out=True, fp32_bar=small)
 
 
 def test_config1_block_full_size_matches_oracle(device):
@@ -81,8 +83,12 @@ def test_config1_block_full_size_matches_oracle(device):
     args = (op, image, text, op["image_mod"], op["text_mod"], rope)
     ri, rt = oracle.config1_double_block(*args, heads=spec.heads)
     gi, gt = oracle.config1_double_block(*args, heads=spec.heads, bf16_graph=True)
-    _check(_np(i_out[0]), ri, gi, "config1 image")
-    _check(_np(t_out[0]), rt, gt, "config1 text")
+    ki, kt = oracle.config1_double_block(*args, heads=spec.heads, rounding_mode="kx")
+    _check(_np(i_out[0]), ri, ki, gi, "config1 image")
+    _check(_np(t_out[0]), rt, kt, gt, "config1 text")
+    i32, t32 = _run_double(spec, p, inputs, device, fp32=True)
+    _check(_np(i32[0]), ri, ki, None, "config1 image fp32 out", fp32_out=True)
+    _check(_np(t32[0]), rt, kt, None, "config1 text fp32 out", fp32_out=True)
 
 
 def test_double_block_unfused_and_batched_agree_with_fused(device):
@@ -103,36 +109,51 @@ def test_single_block_matches_oracle(device, dim, heads, hidden):
     p, op, single, inputs, rope = flux_case(spec)
     x = torch.cat([inputs["text"], inputs["image"]], dim=1)
     block = workloads.build_flux_single_block(spec, p, device)
-    got = block(x.to(device), p["single_mod"].reshape(1, -1).to(device), workloads.flux_tables(spec, device))
+    mod, tables = p["single_mod"].reshape(1, -1).to(device), workloads.flux_tables(spec, device)
+    got = block(x.to(device), mod, tables)
     xn = x[0].float().numpy()
     ref = oracle.flux_single_block(single, xn, op["single_mod"], rope, heads=heads, width=dim)
     graph = oracle.flux_single_block(single, xn, op["single_mod"], rope, heads=heads, width=dim, bf16_graph=True)
-    _check(_np(got[0]), ref, graph, "single")
+    kx = oracle.flux_single_block(single, xn, op["single_mod"], rope, heads=heads, width=dim, rounding_mode="kx")
+    small = dim <= 1024
+    _check(_np(got[0]), ref, kx, graph, "single", fp32_bar=small)
+    got32 = block(x.to(device).float(), mod, tables)
+    assert got32.dtype == torch.float32
+    _check(_np(got32[0]), ref, kx, None, "  single fp32 out", fp32_out=True, fp32_bar=small)
 
 
 def test_config2_double_then_single_full_size_matches_fp32_evaluation(device):
     """Config 2 at full size: 4096 image (64 x 64) + 512 text tokens, D = 4096, 32 x 128,
-    SwiGLU 12288; one double-stream block, then one single-stream block over [text, image]."""
+    SwiGLU 12288; one double-stream block, then one single-stream block over [text, image],
+    with the residual stream handed between the blocks in FP32."""
     spec = workloads.CONFIGS[2]
     p, op, single, inputs, rope = flux_case(spec)
-    i_out, t_out = _run_double(spec, p, inputs, device)
+    i_out, t_out = _run_double(spec, p, inputs, device, out_dtype=torch.float32)
+    assert i_out.dtype == torch.float32
     sblock = workloads.build_flux_single_block(spec, p, device)
     tables = workloads.flux_tables(spec, device)
-    got = _np(sblock(torch.cat([t_out, i_out], dim=1), p["single_mod"].reshape(1, -1).to(device), tables)[0])
+    mod = p["single_mod"].reshape(1, -1).to(device)
+    joined = torch.cat([t_out, i_out], dim=1)
+    got = _np(sblock(joined, mod, tables, out_dtype=torch.bfloat16)[0])
+    got32 = _np(sblock(joined, mod, tables)[0])
+    del sblock, joined
 
     tp = {k: torch.from_numpy(np.asarray(v)).to(device) for k, v in op.items()}
     sp = {k: torch.from_numpy(np.asarray(v)).to(device) for k, v in single.items()}
     rope_d = tuple(torch.from_numpy(t).to(device) for t in rope)
     image, text = inputs["image"][0].float().to(device), inputs["text"][0].float().to(device)
     torch.backends.cuda.matmul.allow_tf32 = False
-    outs = []
+    outs = {}
     with torch.no_grad():
-        for graph in (False, True):
+        for mode in (None, "kx", "graph"):
             ri, rt = _torch_ref.flux_double_block(tp, image, text, tp["image_mod"], tp["text_mod"], rope_d,
-                                                  spec.heads, bf16_graph=graph)
-            outs.append(_torch_ref.flux_single_block(sp, torch.cat([rt, ri]), tp["single_mod"], rope_d, spec.heads,
-                                                     spec.dim, bf16_graph=graph).cpu().numpy())
-    _check(got, outs[0], outs[1], "config2 double+single")
+                                                  spec.heads, rounding_mode=mode)
+            if mode == "graph":  # the reference hands the hidden state between blocks in bf16
+                ri, rt = _torch_ref.bf16_store(ri), _torch_ref.bf16_store(rt)
+            outs[mode] = _torch_ref.flux_single_block(sp, torch.cat([rt, ri]), tp["single_mod"], rope_d, spec.heads,
+                                                      spec.dim, rounding_mode=mode).cpu().numpy()
+    _check(got, outs[None], outs["kx"], outs["graph"], "config2 double+single", fp32_bar=False)
+    _check(got32, outs[None], outs["kx"], None, "config2 double+single fp32 out", fp32_out=True, fp32_bar=False)
 
 
 # ---- the standalone operator surface ---------------------------------------------------------

@@ -3,7 +3,8 @@ same seeded inputs.
 
 Bars: ``apply_rotary_embedding`` is bit-exact; the zero-centred norm within one bf16 ulp-level
 relative L2; grouped-query attention within the reference's attention tolerance; the block at
-cosine >= 0.9995 and max abs <= max(2e-2, the reference's own bf16 execution error).
+the block bar (cosine >= 0.9995 and |got - ref| <= 2e-2 + ulp_bf16(ref) / 2 elementwise,
+``assert_block_bar``), with the reference's own bf16 execution printed beside it.
 """
 
 import numpy as np
@@ -14,7 +15,7 @@ import oracle
 from kinomlx_amd.krea2 import transformer as krea
 from kinomlx_amd.ltx2 import dense_attention
 from tests._blocks import build_krea_block, krea_case
-from tests.conftest import cosine, max_abs, rel_l2
+from tests.conftest import assert_block_bar, cosine, max_abs, rel_l2
 
 pytestmark = pytest.mark.gpu
 F32 = np.float32
@@ -41,9 +42,7 @@ def test_krea_block_matches_oracle(device, hidden, heads, kv_heads, tokens, ff):
     xn = x[0].float().numpy()
     ref = oracle.krea_block(op, xn, mod, rot, heads=heads, kv_heads=kv_heads)
     graph = oracle.krea_block(op, xn, mod, rot, heads=heads, kv_heads=kv_heads, bf16_graph=True)
-    c, m, g = cosine(got, ref), max_abs(got, ref), max_abs(graph, ref)
-    print(f"krea block: cosine {c:.7f} max_abs {m:.4g} (reference bf16 graph {g:.4g}) max|ref| {np.abs(ref).max():.3f}")
-    assert c >= 0.9995 and m <= max(2e-2, g)
+    assert_block_bar(got, ref, "krea block", context=graph)
 
 
 def test_krea_block_unfused_and_batched_agree(device):
