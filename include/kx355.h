@@ -303,6 +303,15 @@ int kx_qgemm_affine_tiled_bf16(const void* a, int64_t lda, const void* wt, const
                                const float* gate, int64_t gate_div, int64_t gate_stride,
                                kx_stream_t stream);
 
+/* Modulation values: out[b, t, r, c] = fp32(table[r, c]) + fp32(ts[b, t, r, c]) for a (rows, dim)
+ * table (KX_F32 or KX_BF16) and an optional timestep modulation ts (null: the table alone) with
+ * element strides ts_bs / ts_ts / ts_rs (dim contiguous); out is fp32 (batch, tokens, rows, dim)
+ * contiguous. BasicAVTransformerBlock._ada_values and the prompt / A/V tables
+ * (kinomlx/models/ltx2/transformer/transformer.py:179-199,209-219): scale_shift_table + timestep. */
+int kx_table_add_f32(const void* table, int table_dtype, const void* ts, int ts_dtype, int64_t ts_bs,
+                     int64_t ts_ts, int64_t ts_rs, float* out, int64_t batch, int64_t tokens, int64_t rows,
+                     int64_t dim, kx_stream_t stream);
+
 /* tanh GELU in fp32, inner argument clamped to +-10: fused_ops.gelu_approx
  * (kinomlx/kernels/fused_ops.py:27-35,327-350). */
 int kx_gelu_tanh_bf16(const void* x, void* y, int64_t count, kx_stream_t stream);

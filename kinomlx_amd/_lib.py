@@ -91,6 +91,7 @@ SIGNATURES: dict[str, list] = {
     "kx_qgemm_affine_tiled_bf16": [
         _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I, _P, _I64, _P, _I64, _I64, _P,
     ],
+    "kx_table_add_f32": [_P, _I, _P, _I, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P],
     "kx_gelu_tanh_bf16": [_P, _P, _I64, _P],
     "kx_silu_bf16": [_P, _P, _I64, _P],
     "kx_swiglu_bf16": [_P, _I64, _P, _I64, _I64, _I64, _P],
@@ -514,6 +515,28 @@ def launch_modulate(x, out, shift, scale) -> None:
         "kx_modulate_bf16", _ptr(x), ldx, _ptr(out), ldy, rows, dim, _ptr(shift), _ptr(scale),
         div, stride, _stream(),
     )
+
+
+def table_add(table: torch.Tensor, ts: torch.Tensor | None) -> torch.Tensor:
+    """``fp32(table) + fp32(ts)`` as a new contiguous fp32 ``(B, T, rows, D)`` tensor: ``table`` is
+    ``(rows, D)`` (fp32 or bf16), ``ts`` ``(B, T, rows, D)`` with a contiguous last axis, or ``None``
+    (the table alone, as ``(1, 1, rows, D)``)."""
+    _check_gpu("table_add", table, ts)
+    if table.dim() != 2 or table.stride(-1) != 1 or (table.shape[0] > 1 and table.stride(0) != table.shape[1]):
+        raise ValueError("table_add: table must be a contiguous (rows, dim) tensor")
+    rows, dim = table.shape
+    if ts is None:
+        batch, tokens, bs, tstride, rs, ts_code = 1, 1, 0, 0, 0, KX_F32
+    else:
+        if ts.dim() != 4 or ts.shape[2:] != (rows, dim) or ts.stride(-1) != 1:
+            raise ValueError(f"table_add: timestep modulation {tuple(ts.shape)} does not match table {(rows, dim)}")
+        batch, tokens = ts.shape[:2]
+        bs, tstride, rs = ts.stride(0), ts.stride(1), ts.stride(2)
+        ts_code = _dtype_code(ts, "table_add timestep")
+    out = torch.empty((batch, tokens, rows, dim), dtype=torch.float32, device=table.device)
+    _call("kx_table_add_f32", _ptr(table), _dtype_code(table, "table_add table"), _ptr(ts), ts_code, bs, tstride, rs,
+          _ptr(out), batch, tokens, rows, dim, _stream())
+    return out
 
 
 def launch_gated_residual(x, r, out, gate) -> None:

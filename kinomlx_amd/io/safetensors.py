@@ -191,11 +191,15 @@ def load_to_device(path: Path | str, device, names: Iterable[str] | None = None)
     staging = [torch.empty(STAGING_BYTES, dtype=torch.uint8, pin_memory=True) for _ in range(2)]
     done = [None, None]
     stream = torch.cuda.Stream(device=device)
+    # the destination buffers come from the caching allocator on the current stream: memory it
+    # hands back may still be in use by work queued there, so the copy stream waits for it
+    stream.wait_stream(torch.cuda.current_stream(device))
     out: dict[str, torch.Tensor] = {}
     which = 0
     for t in sorted(chosen, key=lambda t: t.data_offsets):
         dtype, _ = DTYPES[t.dtype]
         raw = torch.empty(t.byte_count, dtype=torch.uint8, device=device)
+        raw.record_stream(stream)
         for offset in range(0, t.byte_count, STAGING_BYTES):
             size = min(STAGING_BYTES, t.byte_count - offset)
             if done[which] is not None:
@@ -209,6 +213,8 @@ def load_to_device(path: Path | str, device, names: Iterable[str] | None = None)
             which ^= 1
         out[t.name] = raw.view(dtype).view(t.shape) if t.byte_count else torch.empty(t.shape, dtype=dtype,
                                                                                        device=device)
+    # the tensors are used on the current stream: it waits for the last copies
+    torch.cuda.current_stream(device).wait_stream(stream)
     stream.synchronize()
     return out
 

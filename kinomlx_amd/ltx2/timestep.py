@@ -35,7 +35,8 @@ def get_timestep_embedding(timesteps: torch.Tensor, embedding_dim: int = 256, *,
 
 
 class TimestepEmbedding:
-    """Two-layer SiLU MLP for sinusoidal timestep features (``timestep.py:31-49``).
+    """``linear_2(silu(linear_1(features)))`` over the sinusoidal features, with SiLU in the
+    first GEMM's epilogue (``timestep.py:31-49``).
     ``linear_1`` and ``linear_2`` (``Linear`` with biases) are assigned after construction."""
 
     def __init__(self, embedding_dim: int) -> None:
@@ -58,7 +59,8 @@ class TimestepEmbedding:
 
 
 class CombinedTimestepEmbeddings:
-    """Checkpoint-shaped owner for the timestep MLP (``timestep.py:52-60``)."""
+    """Holds the timestep MLP under the attribute path the checkpoint keys use
+    (``emb.timestep_embedder``; ``timestep.py:52-60``)."""
 
     def __init__(self, embedding_dim: int) -> None:
         self.timestep_embedder = TimestepEmbedding(embedding_dim)

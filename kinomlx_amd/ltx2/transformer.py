@@ -206,15 +206,15 @@ class BasicAVTransformerBlock:
     @staticmethod
     def _ada_values(table: torch.Tensor, timestep: torch.Tensor, start: int, stop: int) -> tuple[torch.Tensor, ...]:
         """``table[start:stop] + timestep[:, :, start:stop]`` split per row (``:179-186``)."""
-        values = (table[start:stop][None, None].float() + timestep[:, :, start:stop, :].float()).contiguous()
+        values = _lib.table_add(table[start:stop], timestep[:, :, start:stop, :])
         return tuple(values[:, :, i, :] for i in range(stop - start))
 
     @staticmethod
     def _av_ada_values(table: torch.Tensor, scale_shift: torch.Tensor, gate_timestep: torch.Tensor):
         """``(scale_a2v, shift_a2v, scale_v2a, shift_v2a, gate)`` from a ``(5, D)`` table
         (``transformer.py:188-199``)."""
-        ss = (table[:4][None, None].float() + scale_shift.float()).contiguous()
-        g = (table[4:5][None, None].float() + gate_timestep.float()).contiguous()
+        ss = _lib.table_add(table[:4], scale_shift)
+        g = _lib.table_add(table[4:5], gate_timestep)
         return (*(ss[:, :, i, :] for i in range(4)), g[:, :, 0, :])
 
     def _text_cross_attention(self, value: torch.Tensor, args: TransformerArgs, ada: torch.Tensor,
@@ -223,10 +223,7 @@ class BasicAVTransformerBlock:
         GEMM (``transformer.py:201-223`` and ``:266-276``)."""
         attention = self.attn2 if attention is None else attention
         prompt_table = self.prompt_scale_shift_table if prompt_table is None else prompt_table
-        prompt = prompt_table[None, None].float()
-        if args.prompt_timestep is not None:
-            prompt = prompt + args.prompt_timestep.float()
-        prompt = prompt.contiguous()
+        prompt = _lib.table_add(prompt_table, args.prompt_timestep)
         query = adaln(value, ada[:, :, 7], ada[:, :, 6], self.norm_eps)
         context = modulate(args.context, prompt[:, :, 1], prompt[:, :, 0])
         return attention(query, context=context, mask=args.context_mask, residual=value, gate=ada[:, :, 8],
@@ -237,7 +234,7 @@ class BasicAVTransformerBlock:
         if args.sparse_attention is not None:
             raise ValueError("sparse (Sol-Attn) attention is not built for MI355X")
         x = args.x
-        ada = (table[None, None].float() + args.timesteps.float()).contiguous()
+        ada = _lib.table_add(table, args.timesteps)
         normalized = adaln(x, ada[:, :, 1], ada[:, :, 0], self.norm_eps)
         x1 = attn1(normalized, pe=args.positional_embeddings, mask=args.self_attention_mask, residual=x,
                    gate=ada[:, :, 2], out_dtype=torch.float32)

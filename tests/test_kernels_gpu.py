@@ -601,3 +601,22 @@ def test_skinny_linear_matches_oracle(device, m, n, k, bits, epilogue):
 def test_env_tile_override_is_restored():
     assert os.environ.get("KX355_GEMM_TILE") in (None, "")
     assert os.environ.get("KX355_GEMM_LDS_TILE") in (None, "")
+
+
+@pytest.mark.parametrize("table_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("ts_dtype", [torch.bfloat16, torch.float32, None])
+def test_table_add_is_bit_exact(device, table_dtype, ts_dtype):
+    """``kx_table_add_f32``: fp32(table) + fp32(timestep modulation), the block's ``_ada_values``
+    (``transformer.py:179-186``), for whole tables and row slices of a strided timestep tensor."""
+    g = torch.Generator().manual_seed(11)
+    table = torch.randn((9, 640), generator=g).to(table_dtype).to(device)
+    if ts_dtype is None:
+        got = _lib.table_add(table, None)
+        assert got.shape == (1, 1, 9, 640)
+        assert torch.equal(got[0, 0], table.float())
+        return
+    ts = torch.randn((2, 3, 9, 640), generator=g).to(ts_dtype).to(device)
+    got = _lib.table_add(table, ts)
+    assert torch.equal(got, table[None, None].float() + ts.float())
+    part = _lib.table_add(table[3:6], ts[:, :, 3:6, :])
+    assert torch.equal(part, table[3:6][None, None].float() + ts[:, :, 3:6, :].float())
