@@ -50,6 +50,29 @@ def _kernel_flops(name: str, args: tuple) -> float:
     return 0.0
 
 
+def _kernel_bytes(name: str, args: tuple) -> float:
+    """Algorithmic HBM bytes of one launch of a memory-bound kernel (each operand read or written
+    once; 0 for the MFMA-bound kernels)."""
+    if name == "kx_adaln_norm_bf16":
+        rows, dim, kind = args[4], args[5], args[11]
+        return rows * dim * ((4 if kind & 16 else 2) + 2) + 2 * dim * 4
+    if name == "kx_qk_rmsnorm_rope_bf16":
+        rows, dim = args[8], args[9]
+        return 2 * rows * dim * (2 + 2) + 2 * rows * (dim // 2) * 4
+    if name == "kx_rmsnorm_rope_bf16":
+        rows, dim, rope = args[4], args[5], args[11]
+        return rows * dim * (2 + 2) + (2 * rows * (dim // 2) * 4 if rope else 0)
+    if name == "kx_modulate_bf16":
+        return args[4] * args[5] * (2 + 2)
+    if name == "kx_table_add_f32":
+        count = args[8] * args[9] * args[10] * args[11]
+        return count * 4 + (count * (2 if args[3] else 4) if args[2] else 0) + args[10] * args[11] * (2 if args[1] else 4)
+    if name == "kx_gemm_bf16" and args[8] <= 64:
+        m, n, k = args[7], args[8], args[9]
+        return (m * k + n * k + m * n) * 2
+    return 0.0
+
+
 def _kernel_label(name: str, args: tuple) -> str:
     if name == "kx_gemm_bf16":
         return f"gemm m{args[7]} n{args[8]} k{args[9]}"
@@ -114,10 +137,16 @@ def main() -> int:
                              "the A/V cross-attention to every block")
     parser.add_argument("--load-checkpoint", action="store_true",
                         help="time loading a --blocks-block checkpoint into HBM, plain and quantized on load")
+    parser.add_argument("--launch-log", type=str, default="",
+                        help="write one block's launch sequence (labels, FLOPs, bytes) as JSON to this path")
+    parser.add_argument("--profile-summary", type=str, default="", metavar="DIR",
+                        help="only summarize the rocprofv3 runs under DIR (see profiles/) as a markdown table")
     parser.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                         help="only run 5 device-to-device copies of MIB MiB (the known-size kernel that "
                              "scales the FETCH_SIZE / WRITE_SIZE counters) and exit")
     args = parser.parse_args()
+    if args.profile_summary:
+        return profile_summary(args.profile_summary)
     if args.calibrate_copy:
         import torch
 
@@ -199,6 +228,12 @@ def main() -> int:
         flops_of[label] = _kernel_flops(name, cargs)
         name_of[label] = name
     kernel_ms_per_step = {k: sum(v) / args.steps for k, v in per_kernel.items()}
+    if args.launch_log:
+        records = timer.durations_ms()
+        per_block = len(records) // args.steps
+        with open(args.launch_log, "w") as fh:
+            json.dump([{"label": _kernel_label(n, a), "entry": n, "flops": _kernel_flops(n, a),
+                        "bytes": _kernel_bytes(n, a)} for n, a, _ in records[:per_block]], fh, indent=1)
     dominant = max(kernel_ms_per_step, key=kernel_ms_per_step.get)
     dom_avg_ms = statistics.mean(per_kernel[dominant])
     dom_tflops = flops_of[dominant] / (dom_avg_ms * 1e-3) / 1e12
@@ -274,6 +309,106 @@ def main() -> int:
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result))
+    return 0
+
+
+def profile_summary(root: str) -> int:
+    """Markdown table of one block's kernels from rocprofv3 runs of this script: ``root/trace``
+    (``--kernel-trace``), ``root/mfma`` (``--pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE``),
+    ``root/fetch`` / ``root/write`` (``FETCH_SIZE`` / ``WRITE_SIZE``), ``root/copy_fetch`` /
+    ``root/copy_write`` (the same counters over ``--calibrate-copy 1024``) and ``root/launches.json``
+    (``--launch-log``). Dispatches of the kx kernels are matched to the block's launch sequence by
+    position (every block launches the same sequence), so launches of one kernel with different
+    shapes (self- and cross-attention) get their own rows."""
+    import csv
+    import glob
+
+    with open(os.path.join(root, "launches.json")) as fh:
+        launches = json.load(fh)
+    period = len(launches)
+
+    def kx_rows(sub, pattern):
+        files = glob.glob(os.path.join(root, sub, "**", pattern), recursive=True)
+        if not files:
+            return None
+        with open(files[0]) as fh:
+            return [r for r in csv.DictReader(fh)]
+
+    def per_position(values):
+        # values: per kx dispatch in order -> list per launch position (blocks aligned at the end)
+        usable = len(values) - len(values) % period
+        vals = values[len(values) - usable:]
+        out = [[] for _ in range(period)]
+        for i, v in enumerate(vals):
+            out[i % period].append(v)
+        return out
+
+    trace = sorted(kx_rows("trace", "*kernel_trace.csv"), key=lambda r: int(r["Dispatch_Id"]))
+    durations, names = [], []
+    for r in trace:
+        if "kx::" in r["Kernel_Name"]:
+            durations.append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+            names.append(r["Kernel_Name"])
+    dur = per_position(durations)
+    kname = per_position(names)
+
+    def counters(sub, names_wanted):
+        rows = kx_rows(sub, "*counter_collection.csv")
+        if rows is None:
+            return {}
+        per = defaultdict(lambda: defaultdict(float))
+        order = []
+        for r in rows:
+            if "kx::" not in r["Kernel_Name"] and "copy" not in sub:
+                continue
+            d = int(r["Dispatch_Id"])
+            if d not in per:
+                order.append(d)
+            per[d][r["Counter_Name"]] += float(r["Counter_Value"])
+        return {c: [per[d].get(c, 0.0) for d in sorted(order)] for c in names_wanted}
+
+    mfma = counters("mfma", ["SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE"])
+    fetch = counters("fetch", ["FETCH_SIZE"]).get("FETCH_SIZE")
+    write = counters("write", ["WRITE_SIZE"]).get("WRITE_SIZE")
+    copy_f = counters("copy_fetch", ["FETCH_SIZE"]).get("FETCH_SIZE")
+    copy_w = counters("copy_write", ["WRITE_SIZE"]).get("WRITE_SIZE")
+    # FETCH_SIZE / WRITE_SIZE are KiB per dispatch; scale by what they read for a 1 GiB copy
+    fscale = (1 << 30) / (max(copy_f) * 1024) if copy_f else None
+    wscale = (1 << 30) / (max(copy_w) * 1024) if copy_w else None
+    busy = per_position(mfma["SQ_VALU_MFMA_BUSY_CYCLES"]) if mfma else None
+    gui = per_position(mfma["GRBM_GUI_ACTIVE"]) if mfma else None
+    fpos = per_position(fetch) if fetch else None
+    wpos = per_position(write) if write else None
+
+    print(f"Counter scale from a 1 GiB device copy: FETCH_SIZE x{fscale:.3f}, WRITE_SIZE x{wscale:.3f}." if fscale
+          else "No copy calibration.")
+    print()
+    print("| # | launch | kernel | avg us | TFLOP/s | of 2.5 PF | MFMA busy | algorithmic GB/s | of 8 TB/s "
+          "| HBM fetch MB | HBM write MB |")
+    print("|---|---|---|---|---|---|---|---|---|---|---|")
+    total_us = 0.0
+    for i, entry in enumerate(launches):
+        avg = statistics.mean(dur[i])
+        total_us += avg
+        kernel = kname[i][0].replace("kx::(anonymous namespace)::", "").split("(")[0]
+        tf = entry["flops"] / (avg * 1e-6) / 1e12 if entry["flops"] else None
+        gbs = entry["bytes"] / (avg * 1e-6) / 1e9 if entry["bytes"] else None
+        b = None
+        if busy:
+            # SQ_VALU_MFMA_BUSY_CYCLES sums the 1024 SIMDs; GRBM_GUI_ACTIVE sums the 8 XCDs' cycles
+            cyc = statistics.mean(gui[i]) / 8
+            b = statistics.mean(busy[i]) / (1024 * cyc) if cyc else None
+        fm = statistics.mean(fpos[i]) * 1024 * fscale / 1e6 if fpos and fscale else None
+        wm = statistics.mean(wpos[i]) * 1024 * wscale / 1e6 if wpos and wscale else None
+
+        def f(x, fmt):
+            return fmt.format(x) if x is not None else "-"
+
+        print(f"| {i} | {entry['label']} | `{kernel}` | {avg:.1f} | {f(tf, '{:.0f}')} | "
+              f"{f(tf / PEAK_BF16_TFLOPS if tf else None, '{:.3f}')} | {f(b if tf else None, '{:.2f}')} | "
+              f"{f(gbs, '{:.0f}')} | {f(gbs / PEAK_HBM_GBS if gbs else None, '{:.2f}')} | "
+              f"{f(fm, '{:.1f}')} | {f(wm, '{:.1f}')} |")
+    print(f"\nSum of the block's kernels: {total_us / 1e3:.3f} ms ({len(dur[0])} blocks traced).")
     return 0
 
 
