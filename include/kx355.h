@@ -303,6 +303,43 @@ int kx_qgemm_affine_tiled_bf16(const void* a, int64_t lda, const void* wt, const
                                const float* gate, int64_t gate_div, int64_t gate_stride,
                                kx_stream_t stream);
 
+/*
+ * mxfp8 weight-quantized linear (OCP MX: FP8 E4M3 elements, one E8M0 scale byte per group of 32
+ * along K), dequantized inside the MFMA mainloop: replaces nn.QuantizedLinear /
+ * mx.quantized_matmul(x, wq, scales, transpose=True, group_size=32, bits=8, mode="mxfp8") + bias,
+ * the mode transformer_quantize="mxfp8-blocks" installs on every block linear
+ * (kinomlx/models/ltx2/weights/quantization.py:199-216, tensors.py:185-203). wq: uint32
+ * (n, k / 4), element j of a word in byte j; scales: uint8 (n, k / 32). The weight operand is
+ * bf16(e4m3(q) * 2^(s - 127)), exact. Epilogue flags and residual/gate as kx_gemm_bf16.
+ * Requires group_size == 32 and k % 32 == 0.
+ */
+int kx_qgemm_mxfp8_bf16(const void* a, int64_t lda, const uint32_t* wq, const void* scales,
+                        const void* bias, void* c, int64_t ldc, int64_t m, int64_t n, int64_t k,
+                        int group_size, int epilogue, const void* resid, int64_t ldr, const float* gate,
+                        int64_t gate_div, int64_t gate_stride, kx_stream_t stream);
+
+/*
+ * mxfp8 weights -> the bf16 (n, k) weight (out features n, in features k), exactly. transposed = 0:
+ * the layout above (wq (n, k / 4), scales (n, k / 32)). transposed = 1: the pretransposed layout
+ * of transformer_quantize="mxfp8-blocks-pretranspose", quantized from weight.T (wq (k, n / 4),
+ * scales (k, n / 32), groups along n), which _PretransposedQuantizedLinear multiplies with
+ * mx.quantized_matmul(..., transpose=False) (kinomlx/models/ltx2/weights/quantization.py:17-44,
+ * kinomlx/models/ltx2/preparation.py:139-157); transposed needs n % 32 == 0 and k % 8 == 0.
+ */
+int kx_dequant_mxfp8_bf16(const uint32_t* wq, const void* scales, void* out, int64_t n, int64_t k,
+                          int group_size, int transposed, kx_stream_t stream);
+
+/*
+ * Quantize-on-load to mxfp8: bf16 w (n, k) at row stride ldw -> wq (n, k / 4) uint32 and scales
+ * (n, k / 32) uint8. Per group of 32: X = floor(log2(max |w|)) - 8 clamped to [-127, 127] (-127 for
+ * a zero group), scale byte X + 127, codes E4M3(w * 2^-X) rounded to nearest even, saturated at
+ * +-448 (the OCP MX conversion). Replaces mx.quantize(weight, 32, 8, mode="mxfp8") of the weight
+ * preparation (kinomlx/models/ltx2/preparation.py:139-157); MLX's own exponent choice is not part of
+ * the reference tree. Requires group_size 32, k % 32 == 0, ldw % 8 == 0, 16-byte aligned w.
+ */
+int kx_quantize_mxfp8_bf16(const void* w, int64_t ldw, uint32_t* wq, void* scales, int64_t n, int64_t k,
+                           int group_size, kx_stream_t stream);
+
 /* Modulation values: out[b, t, r, c] = fp32(table[r, c]) + fp32(ts[b, t, r, c]) for a (rows, dim)
  * table (KX_F32 or KX_BF16) and an optional timestep modulation ts (null: the table alone) with
  * element strides ts_bs / ts_ts / ts_rs (dim contiguous); out is fp32 (batch, tokens, rows, dim)

@@ -92,6 +92,11 @@ SIGNATURES: dict[str, list] = {
         _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I, _P, _I64, _P, _I64, _I64, _P,
     ],
     "kx_table_add_f32": [_P, _I, _P, _I, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P],
+    "kx_qgemm_mxfp8_bf16": [
+        _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I, _P, _I64, _P, _I64, _I64, _P,
+    ],
+    "kx_dequant_mxfp8_bf16": [_P, _P, _P, _I64, _I64, _I, _I, _P],
+    "kx_quantize_mxfp8_bf16": [_P, _I64, _P, _P, _I64, _I64, _I, _P],
     "kx_gelu_tanh_bf16": [_P, _P, _I64, _P],
     "kx_silu_bf16": [_P, _P, _I64, _P],
     "kx_swiglu_bf16": [_P, _I64, _P, _I64, _I64, _I64, _P],
@@ -456,6 +461,52 @@ def launch_qgemm(a, words, scales, biases, out, *, n, k, group_size, bits, bias=
         _ptr(out), ldc, m, n, k, group_size, bits, flags, _ptr(resid), ldr, _ptr(gate), div,
         stride, _stream(),
     )
+
+
+def launch_qgemm_mxfp8(a, words, scales, out, *, n, k, group_size=32, bias=None, flags: int = 0, resid=None,
+                       gate=None) -> None:
+    """``out = epilogue(a @ dequant(words, scales).T)`` for mxfp8 weights (words (n, k / 4) uint32,
+    scales (n, k / 32) uint8)."""
+    _check_gpu("qgemm_mxfp8", a, words, scales, out, bias, resid, gate)
+    if words.shape != (n, k // 4) or scales.shape != (n, k // group_size) or scales.dtype != torch.uint8:
+        raise ValueError("mxfp8 linear: words must be (n, k / 4) and scales (n, k / 32) uint8")
+    flags |= _dtype_flags(out, resid, "quantized linear")
+    m, ka, lda = _rows(a, "quantized linear input")
+    if ka != k:
+        raise ValueError(f"quantized linear: input width {ka} does not match {k}")
+    _, _, ldc = _rows(out, "quantized linear output")
+    ldr, div, stride = 0, 1, 0
+    if resid is not None:
+        _, _, ldr = _rows(resid, "quantized linear residual")
+        div, stride = _mod_rows(gate, m, n, "quantized linear gate")
+    _call(
+        "kx_qgemm_mxfp8_bf16", _ptr(a), lda, _ptr(words), _ptr(scales), _ptr(bias), _ptr(out), ldc, m, n, k,
+        group_size, flags, _ptr(resid), ldr, _ptr(gate), div, stride, _stream(),
+    )
+
+
+def launch_dequant_mxfp8(words, scales, out, *, n, k, group_size=32, transposed: bool = False) -> None:
+    """The bf16 (n, k) weight of mxfp8 ``words``/``scales``: the (n, k / 4) layout, or with
+    ``transposed`` the (k, n / 4) layout quantized from ``weight.T``."""
+    _check_gpu("dequant_mxfp8", words, scales, out)
+    rows, cols = (k, n) if transposed else (n, k)
+    if words.shape != (rows, cols // 4) or scales.shape != (rows, cols // group_size):
+        raise ValueError("dequant_mxfp8: packed shapes do not match (n, k)")
+    if out.shape != (n, k) or out.dtype != torch.bfloat16 or not out.is_contiguous():
+        raise ValueError("dequant_mxfp8: out must be a contiguous bf16 (n, k) tensor")
+    _call("kx_dequant_mxfp8_bf16", _ptr(words), _ptr(scales), _ptr(out), n, k, group_size, int(transposed),
+          _stream())
+
+
+def launch_quantize_mxfp8(w, words, scales, *, group_size: int = 32) -> None:
+    """mxfp8 (words, scales) <- bf16 weight w (n, k) with contiguous rows."""
+    _check_gpu("quantize_mxfp8", w, words, scales)
+    n, k = (int(v) for v in w.shape)
+    if w.dtype != torch.bfloat16 or w.stride(-1) != 1:
+        raise ValueError("quantize_mxfp8: the weight must be bfloat16 with contiguous rows")
+    if words.shape != (n, k // 4) or scales.shape != (n, k // group_size) or scales.dtype != torch.uint8:
+        raise ValueError("quantize_mxfp8: output shapes do not match the weight")
+    _call("kx_quantize_mxfp8_bf16", _ptr(w), w.stride(0), _ptr(words), _ptr(scales), n, k, group_size, _stream())
 
 
 def launch_tile_weights(words, scales, biases, wt, sbt, *, n, k, group_size, bits) -> None:

@@ -16,7 +16,10 @@
 //
 // Quantized weights: the stage's packed words and per-group bf16 scale/bias are loaded into
 // registers instead, and dequantized (bf16(fp32(scale) * q + fp32(bias))) on their way into LDS,
-// inside the mainloop; the MFMA loop is shared with the dense path.
+// inside the mainloop; the MFMA loop is shared with the dense path. mxfp8 weights (OCP MX: FP8
+// E4M3 elements, one E8M0 scale byte per 32 along K) take the same route: each element is
+// converted to fp32 exactly (v_cvt_pk_f32_fp8) and multiplied by its power-of-two scale (exact),
+// so the bf16 operand equals the format's value.
 #include <stdlib.h>
 
 #include <mutex>
@@ -44,7 +47,27 @@ struct QuantW {
   const uint32_t* words;  // (n, k * bits / 32)
   const uint16_t* scales;  // (n, k / 64)
   const uint16_t* biases;  // (n, k / 64)
+  const uint8_t* e8m0;     // mxfp8: (n, k / 32) scale bytes
 };
+
+// Weight-mode template code: 0 dense bf16, 4 / 8 affine int4 / int8, QMX8 mxfp8 (8-bit codes).
+constexpr int QMX8 = 9;
+template <int QB>
+constexpr int qbits() { return QB == QMX8 ? 8 : QB; }
+
+// 2^(s - 127) for an E8M0 scale byte (s = 0: 2^-127, an fp32 subnormal; s = 255: NaN).
+__device__ __forceinline__ float e8m0_f32(uint32_t s) {
+  const uint32_t bits = s == 0 ? 0x00400000u : (s == 255 ? 0x7FC00000u : s << 23);
+  return __uint_as_float(bits);
+}
+
+// Four E4M3 bytes of w (lowest first) times a power-of-two scale, as four bf16 (two words). The
+// fp8 -> fp32 conversion is exact, and so is the product while it stays in the fp32 normal range.
+__device__ __forceinline__ uint2 mx8_quad(uint32_t w, float scale) {
+  const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
+  const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
+  return make_uint2(pack2(lo.x * scale, lo.y * scale), pack2(hi.x * scale, hi.y * scale));
+}
 
 __device__ __forceinline__ int lds_off(int r, int c) { return r * ROWB + ((c ^ (r & 7)) << 4); }
 
@@ -60,6 +83,10 @@ __device__ __forceinline__ float apply_act(float v, int act) {
 
 template <int BITS>
 __device__ __forceinline__ uint4 dequant8(const uint32_t* wd, float s, float b) {
+  if constexpr (BITS == QMX8) {
+    const uint2 q0 = mx8_quad(wd[0], s), q1 = mx8_quad(wd[1], s);
+    return make_uint4(q0.x, q0.y, q1.x, q1.y);
+  }
   float v[8];
   if (BITS == 4) {
     const uint32_t w = wd[0];
@@ -75,7 +102,7 @@ __device__ __forceinline__ uint4 dequant8(const uint32_t* wd, float s, float b) 
   return pack8(v);
 }
 
-// QB = 0: dense bf16 weights; QB = 4 / 8: affine quantized weights of that many bits.
+// QB = 0: dense bf16 weights; QB = 4 / 8: affine quantized weights of that many bits; QMX8: mxfp8.
 template <int BM, int BN, int WM, int WN, int QB>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ W, int64_t ldw,
@@ -85,7 +112,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(
   constexpr int MB = WT_M / 32, NB = WT_N / 32;
   constexpr int A_PER = BM * (BK / 8) / NT;
   constexpr int W_PER = BN * (BK / 8) / NT;
-  constexpr int QWORDS = QB == 8 ? 2 : 1;
+  constexpr int QBITS = qbits<QB>();
+  constexpr int QWORDS = QBITS == 8 ? 2 : 1;
   static_assert(A_PER * NT == BM * (BK / 8) && W_PER * NT == BN * (BK / 8), "tile/threads");
   static_assert(MB >= 1 && NB >= 1, "wave tile");
   constexpr int STAGE = (BM + BN) * ROWB;
@@ -135,6 +163,15 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(
         uint4 v = *reinterpret_cast<const uint4*>(W + (int64_t)gn * ldw + min(gk, K - 8));
         if (gk >= K) v = make_uint4(0, 0, 0, 0);
         rw[i] = v;
+      } else if constexpr (QB == QMX8) {
+        // K % 32 == 0: a stage's second 32-wide half may lie past K; it reads the last group and
+        // is zeroed (zero codes dequantize to zero)
+        const int gkc = min(gk, K - 8);
+        const int64_t wrow = (int64_t)gn * (K / 4);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) rq[i][j] = gk < K ? qw.words[wrow + gkc / 4 + j] : 0u;
+        rs[i] = e8m0_f32(qw.e8m0[(int64_t)gn * (K / 32) + gkc / 32]);
+        rb[i] = 0.0f;
       } else {
         const int64_t wrow = (int64_t)gn * (K * QB / 32);
 #pragma unroll
@@ -309,6 +346,67 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint32_t* __restrict
   *reinterpret_cast<uint4*>(out + r * k + kk) = dequant8<BITS>(tmp, bf2f(scales[g]), bf2f(biases[g]));
 }
 
+// mxfp8 in the reference layout: (n, k / 4) words and (n, k / 32) scale bytes -> (n, k) bf16, eight
+// values per thread.
+__global__ __launch_bounds__(256) void dequant_mx8_kernel(const uint32_t* __restrict__ words,
+                                                          const uint8_t* __restrict__ scales,
+                                                          uint16_t* __restrict__ out, int64_t n, int64_t k) {
+  const int64_t chunks_per_row = k / 8;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= n * chunks_per_row) return;
+  const int64_t r = idx / chunks_per_row, c = idx - r * chunks_per_row;
+  const uint2 w = *reinterpret_cast<const uint2*>(words + r * (k / 4) + 2 * c);
+  uint32_t tmp[2] = {w.x, w.y};
+  *reinterpret_cast<uint4*>(out + r * k + 8 * c) =
+      dequant8<QMX8>(tmp, e8m0_f32(scales[r * (k / 32) + c / 4]), 0.0f);
+}
+
+// mxfp8 in the pretransposed layout (quantized from weight.T: (k, n / 4) words and (k, n / 32)
+// scale bytes, groups along n) -> the (n, k) bf16 weight, through 64 x 64 LDS tiles: a thread
+// dequantizes 16 consecutive n of one k row and writes them transposed into the tile, then
+// writes 16 consecutive k of one n row. n % 32 == 0 and k % 8 == 0 keep every 16-run of n and
+// every 8-run of k either wholly inside the matrix or wholly outside.
+__global__ __launch_bounds__(256) void dequant_mx8_t_kernel(const uint32_t* __restrict__ words,
+                                                            const uint8_t* __restrict__ scales,
+                                                            uint16_t* __restrict__ out, int64_t n, int64_t k) {
+  __shared__ uint16_t tile[64][64 + 2];
+  const int t = threadIdx.x;
+  const int64_t n0 = (int64_t)blockIdx.x * 64, k0 = (int64_t)blockIdx.y * 64;
+  {
+    const int kl = t >> 2, nl = (t & 3) * 16;
+    const int64_t kk = k0 + kl, nn = n0 + nl;
+    if (kk < k && nn < n) {
+      const uint4 w = *reinterpret_cast<const uint4*>(words + kk * (n / 4) + nn / 4);
+      const float sc = e8m0_f32(scales[kk * (n / 32) + nn / 32]);
+      const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint2 q = mx8_quad(wv[j], sc);
+        tile[nl + 4 * j][kl] = (uint16_t)(q.x & 0xffffu);
+        tile[nl + 4 * j + 1][kl] = (uint16_t)(q.x >> 16);
+        tile[nl + 4 * j + 2][kl] = (uint16_t)(q.y & 0xffffu);
+        tile[nl + 4 * j + 3][kl] = (uint16_t)(q.y >> 16);
+      }
+    }
+  }
+  __syncthreads();
+  const int nl = t >> 2, kl = (t & 3) * 16;
+  const int64_t nn = n0 + nl;
+  if (nn >= n) return;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int64_t kk = k0 + kl + 8 * h;
+    if (kk >= k) break;
+    const uint16_t* src = &tile[nl][kl + 8 * h];
+    uint4 v;
+    v.x = src[0] | ((uint32_t)src[1] << 16);
+    v.y = src[2] | ((uint32_t)src[3] << 16);
+    v.z = src[4] | ((uint32_t)src[5] << 16);
+    v.w = src[6] | ((uint32_t)src[7] << 16);
+    *reinterpret_cast<uint4*>(out + nn * k + kk) = v;
+  }
+}
+
 // ---- direct-to-LDS pipelined kernel (K % 32 == 0) -----------------------------------------------
 //
 // Operand tiles go from global memory straight into LDS with global_load_lds_dwordx4 (no VGPR
@@ -409,20 +507,23 @@ __device__ __forceinline__ void epilogue_store4(float v[4], int m, int n, int N,
 // q < 256), so the fma rounds once, like the separate multiply and add.
 template <int QB>
 struct DqIn {
-  uint32_t words[DBK * QB / 32];
-  uint32_t sw, bw;  // scale and bias pairs of the stage's two-group window
+  uint32_t words[DBK * qbits<QB>() / 32];
+  uint32_t sw, bw;  // scale and bias pairs of the stage's two-group window (mxfp8: four scale bytes)
 };
 // TL: scale / bias pairs interleaved per row (s0 s1 b0 b1, the tiled layout); otherwise the
 // scale pairs of all rows then the bias pairs.
 template <int QB, bool TL>
 __device__ __forceinline__ void dequant_load(const uint8_t* wq, const uint8_t* sb, int bn, int r, DqIn<QB>& in) {
-  constexpr int QROW = DBK * QB / 8;  // packed bytes per row per stage
+  constexpr int QROW = DBK * qbits<QB>() / 8;  // packed bytes per row per stage
 #pragma unroll
   for (int c = 0; c < QROW / 16; ++c) {
     const uint4 v = *reinterpret_cast<const uint4*>(wq + r * QROW + 16 * c);
     in.words[4 * c] = v.x; in.words[4 * c + 1] = v.y; in.words[4 * c + 2] = v.z; in.words[4 * c + 3] = v.w;
   }
-  if (TL) {
+  if constexpr (QB == QMX8) {
+    in.sw = *reinterpret_cast<const uint32_t*>(sb + 4 * r);
+    in.bw = 0u;
+  } else if (TL) {
     const uint2 p = *reinterpret_cast<const uint2*>(sb + 8 * r);
     in.sw = p.x;
     in.bw = p.y;
@@ -438,6 +539,16 @@ __device__ __forceinline__ void dequant_piece(const DqIn<QB>& in, int h, float s
                                               int r, uint8_t* wd) {
   const int c = h >> 1, hf = h & 1;
   float v[4];
+  if constexpr (QB == QMX8) {
+    const uint2 q = mx8_quad(in.words[2 * c + hf], sc);
+    if (hf == 0) {
+      out[0] = q.x;
+      out[1] = q.y;
+    } else {
+      *reinterpret_cast<uint4*>(wd + r * DROW + ((c ^ dswz(r)) << 4)) = make_uint4(out[0], out[1], q.x, q.y);
+    }
+    return;
+  }
   if (QB == 4) {
     // nibbles 4hf .. 4hf+3 of word c: even ones in the low nibbles of bytes 2hf, 2hf+1
     const uint32_t lo = in.words[c] & 0x0F0F0F0Fu, hi = (in.words[c] >> 4) & 0x0F0F0F0Fu;
@@ -459,17 +570,31 @@ __device__ __forceinline__ void dequant_piece(const DqIn<QB>& in, int h, float s
     *reinterpret_cast<uint4*>(wd + r * DROW + ((c ^ dswz(r)) << 4)) = make_uint4(out[0], out[1], p0, p1);
   }
 }
+// Scale and bias of K stage kt within the loaded window: affine, group kt / 2 of the pair
+// (64-wide groups); mxfp8, scale byte kt % 4 of the word (32-wide groups).
 template <int QB>
-__device__ __forceinline__ void dequant_store(const DqIn<QB>& in, int r, int half, uint8_t* wd) {
-  const float sc = half ? hi_f(in.sw) : lo_f(in.sw);
-  const float bi = half ? hi_f(in.bw) : lo_f(in.bw);
+__device__ __forceinline__ void dequant_scale(const DqIn<QB>& in, int kt, float& sc, float& bi) {
+  if constexpr (QB == QMX8) {
+    sc = e8m0_f32((in.sw >> (8 * (kt & 3))) & 255u);
+    bi = 0.0f;
+  } else {
+    const bool half = (kt >> 1) & 1;
+    sc = half ? hi_f(in.sw) : lo_f(in.sw);
+    bi = half ? hi_f(in.bw) : lo_f(in.bw);
+  }
+}
+template <int QB>
+__device__ __forceinline__ void dequant_store(const DqIn<QB>& in, int r, int kt, uint8_t* wd) {
+  float sc, bi;
+  dequant_scale<QB>(in, kt, sc, bi);
   uint32_t out[2];
 #pragma unroll
   for (int h = 0; h < 2 * DCPR; ++h) dequant_piece<QB>(in, h, sc, bi, out, r, wd);
 }
 
 // QB = 0: bf16 weights, DMA'd like the activations. QB = 4 / 8: affine quantized weights; each
-// stage DMAs the packed words and the scale / bias pairs of its 64-wide group, and the workgroup
+// stage DMAs the packed words and the scale / bias pairs of its 64-wide group (QMX8: the word of
+// four E8M0 scale bytes holding its 32-wide group), and the workgroup
 // dequantizes stage kt+1 into one of two bf16 tiles while the MFMAs consume stage kt. TL: the
 // weights are in the tiled layout (one contiguous block per 256-row tile and stage, see
 // kx_qweight_tile_affine), else in the reference layout (one 16- or 4-byte piece per row).
@@ -510,12 +635,13 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ W, int64_t ldw,
     QuantW qw, void* __restrict__ C, int64_t ldc, int M, int N, int K, Epilogue epi) {
   constexpr int A_INST = BM / DRPI / 4;
-  constexpr int QROW = DBK * QB / 8;                                  // packed bytes per row
+  constexpr int QROW = DBK * qbits<QB>() / 8;                         // packed bytes per row
   constexpr int WQ_INST = QB ? BN * QROW / 1024 / 4 : 0;              // packed words, per wave
-  constexpr int SB_INST = QB ? 2 * BN / 64 / 4 : 0;                   // scale and bias pairs
+  constexpr int SB_BYTES = QB == QMX8 ? 4 : 8;                        // scale (bias) bytes per row
+  constexpr int SB_INST = QB ? SB_BYTES * BN / 256 / 4 : 0;           // scale and bias pairs
   constexpr int W_INST = QB ? WQ_INST + SB_INST : BN / DRPI / 4;
   constexpr int PER = A_INST + W_INST;  // DMA instructions per wave per stage
-  constexpr int W_BYTES = QB ? BN * QROW + BN * 8 : BN * DROW;
+  constexpr int W_BYTES = QB ? BN * QROW + BN * SB_BYTES : BN * DROW;
   constexpr int STAGE = BM * DROW + W_BYTES;
   constexpr int WD_OFF = DNS * STAGE;    // two dequantized bf16 weight tiles follow the ring
   constexpr int RING = QB ? WD_OFF + 2 * BN * DROW : DNS * STAGE;
@@ -534,6 +660,7 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
   static_assert(A_INST * DRPI * 4 == BM && MB >= 1 && NB >= 2, "tile");
   static_assert(QB == 0 ? (BN / DRPI / 4) * DRPI * 4 == BN : (BN == 256 && WQ_INST >= 1), "weight tile");
   static_assert(MB + NB <= 15 && WAITN >= 0, "pipeline");
+  static_assert(!(TL && QB == QMX8), "mxfp8 weights are read in the reference layout only");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -572,7 +699,7 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
   const char* w_base;   // bf16 weights, or the packed words
   const char* s_base = nullptr;  // scale pairs (bias pairs follow at b_base)
   const char* b_base = nullptr;
-  const int64_t qrow_bytes = (int64_t)K * QB / 8, groups = K / 64;
+  const int64_t qrow_bytes = (int64_t)K * qbits<QB>() / 8, groups = K / 64;
   if constexpr (QB == 0) {
 #pragma unroll
     for (int i = 0; i < W_INST; ++i) {
@@ -598,16 +725,21 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
       const int r = (wave * WQ_INST + i) * RPW + lane / (QROW / 16);
       vo[A_INST + i] = (uint32_t)((int64_t)(min(n0 + r, N - 1) - n0) * qrow_bytes + (lane % (QROW / 16)) * 16);
     }
-    // scale / bias pairs: 64 rows x 4 bytes per instruction
+    // scale / bias pairs (mxfp8: scale-byte quads): 64 rows x 4 bytes per instruction
+    const int64_t sb_row = QB == QMX8 ? K / 32 : groups * 2;  // bytes per row of the scale array
 #pragma unroll
     for (int i = 0; i < SB_INST; ++i) {
       const int g = wave * SB_INST + i;
       const int r = (g % (BN / 64)) * 64 + lane;
-      vo[A_INST + WQ_INST + i] = (uint32_t)((int64_t)(min(n0 + r, N - 1) - n0) * groups * 2);
+      vo[A_INST + WQ_INST + i] = (uint32_t)((int64_t)(min(n0 + r, N - 1) - n0) * sb_row);
     }
     w_base = reinterpret_cast<const char*>(qw.words) + (int64_t)n0 * qrow_bytes;
-    s_base = reinterpret_cast<const char*>(qw.scales) + (int64_t)n0 * groups * 2;
-    b_base = reinterpret_cast<const char*>(qw.biases) + (int64_t)n0 * groups * 2;
+    if constexpr (QB == QMX8) {
+      s_base = reinterpret_cast<const char*>(qw.e8m0) + (int64_t)n0 * sb_row;
+    } else {
+      s_base = reinterpret_cast<const char*>(qw.scales) + (int64_t)n0 * sb_row;
+      b_base = reinterpret_cast<const char*>(qw.biases) + (int64_t)n0 * sb_row;
+    }
   }
   auto dma = [&](int i, uint8_t* buf, int k0) {
     if (i < A_INST) {
@@ -624,8 +756,13 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
       __builtin_amdgcn_global_load_lds((const void*)(s_base + (int64_t)(k0 / 128) * (BN * 8) + vo[i]),
                                        KX_LDS(buf + BM * DROW + BN * QROW + g * 256), 4, 0, 0);
     } else if (i < A_INST + WQ_INST) {
-      __builtin_amdgcn_global_load_lds((const void*)(w_base + (int64_t)k0 * QB / 8 + vo[i]),
+      __builtin_amdgcn_global_load_lds((const void*)(w_base + (int64_t)k0 * qbits<QB>() / 8 + vo[i]),
                                        KX_LDS(buf + BM * DROW + (wave * WQ_INST + i - A_INST) * 1024), 16, 0, 0);
+    } else if constexpr (QB == QMX8) {
+      // the scale-byte quad holding group k0 / 32 (k0 / 32 rounded down to a multiple of 4)
+      const int g = wave * SB_INST + (i - A_INST - WQ_INST);
+      __builtin_amdgcn_global_load_lds((const void*)(s_base + (int64_t)((k0 >> 5) & ~3) + vo[i]),
+                                       KX_LDS(buf + BM * DROW + BN * QROW + g * 256), 4, 0, 0);
     } else {
       // the pair of groups holding group k0 / 64 (k0 / 64 rounded down to even)
       const int g = wave * SB_INST + (i - A_INST - WQ_INST);
@@ -668,7 +805,7 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
     }
   };
   auto dequant_out = [&](int kt) {  // stage kt's bf16 weights into its tile
-    if constexpr (QB != 0) dequant_store<QB>(dq, tid, (kt >> 1) & 1, smem + WD_OFF + (kt & 1) * BN * DROW);
+    if constexpr (QB != 0) dequant_store<QB>(dq, tid, kt, smem + WD_OFF + (kt & 1) * BN * DROW);
   };
 
   f32x16 acc[NB][MB];
@@ -722,8 +859,8 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
         for (int d = 0; d < DPS; ++d)
           if (d < PER) dma(d, iss, k_iss);
         const int kq = kt + 1;
-        const float sc = ((kq >> 1) & 1) ? hi_f(dq.sw) : lo_f(dq.sw);
-        const float bi = ((kq >> 1) & 1) ? hi_f(dq.bw) : lo_f(dq.bw);
+        float sc, bi;
+        dequant_scale<QB ? QB : 4>(dq, kq, sc, bi);
         uint8_t* wd = smem + WD_OFF + (kq & 1) * BN * DROW;
         uint32_t piece[2];
         __builtin_amdgcn_sched_barrier(0);
@@ -945,6 +1082,11 @@ __global__ __launch_bounds__(NWK * 64) void gemm_skinny_kernel(
   auto wfrag = [&](int k) -> bf16x8 {  // k: this lane's 8 values start at k (k % 8 == 0)
     if constexpr (QB == 0) {
       return *reinterpret_cast<const bf16x8*>(W + (int64_t)n * ldw + k);
+    } else if constexpr (QB == QMX8) {
+      const float sc = e8m0_f32(qw.e8m0[(int64_t)n * (K / 32) + k / 32]);
+      const uint32_t* wd = qw.words + (int64_t)n * (K / 4) + k / 4;
+      uint32_t tmp[2] = {wd[0], wd[1]};
+      return __builtin_bit_cast(bf16x8, dequant8<QMX8>(tmp, sc, 0.0f));
     } else {
       const int64_t g = (int64_t)n * (K / 64) + k / 64;
       const float sc = bf2f(qw.scales[g]), bi = bf2f(qw.biases[g]);
@@ -1085,9 +1227,11 @@ int dispatch(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, Qua
   // scale / bias rows; tile 2 (or a narrow N) selects the register-staged kernel
   // (a few hundred rows leave most CUs idle with its 192 / 256-row tiles: they take the
   // register-staged kernel's small tiles instead)
+  const bool sb_aligned = QB == QMX8 ? (reinterpret_cast<uintptr_t>(qw.e8m0) & 3) == 0
+                                     : (reinterpret_cast<uintptr_t>(qw.scales) & 3) == 0 &&
+                                           (reinterpret_cast<uintptr_t>(qw.biases) & 3) == 0;
   if (QB != 0 && k % 128 == 0 && lda <= (1 << 22) && n >= 128 && m >= 512 && !use_legacy &&
-      aligned16(qw.words) && (reinterpret_cast<uintptr_t>(qw.scales) & 3) == 0 &&
-      (reinterpret_cast<uintptr_t>(qw.biases) & 3) == 0) {
+      aligned16(qw.words) && sb_aligned) {
     const int cfg = pick_lds_cfg(m, n);
     const int64_t t256 = ((m + 255) / 256) * ((n + 255) / 256), t192 = ((m + 191) / 192) * ((n + 255) / 256);
     const bool tall = cfg == 0 || (cfg != 1 && (t256 + 255) / 256 * 256 <= (t192 + 255) / 256 * 192);
@@ -1282,6 +1426,50 @@ extern "C" int kx_dequant_affine_bf16(const uint32_t* wq, const void* scales, co
     dequant_kernel<8><<<blocks, 256, 0, (hipStream_t)stream>>>(
         wq, (const uint16_t*)scales, (const uint16_t*)biases, (uint16_t*)out, n, k, group_size);
   return check_launch("kx_dequant_affine_bf16");
+}
+
+extern "C" int kx_qgemm_mxfp8_bf16(const void* a, int64_t lda, const uint32_t* wq, const void* scales,
+                                   const void* bias, void* c, int64_t ldc, int64_t m, int64_t n, int64_t k,
+                                   int group_size, int epilogue, const void* resid, int64_t ldr, const float* gate,
+                                   int64_t gate_div, int64_t gate_stride, kx_stream_t stream) {
+  const char* what = "kx_qgemm_mxfp8_bf16";
+  KX_REQUIRE(a && wq && scales && c, "%s: null tensor", what);
+  KX_REQUIRE(group_size == 32, "%s: group_size must be 32, got %d", what, group_size);
+  KX_REQUIRE(m >= 0 && n >= 0 && k > 0 && k % 32 == 0 && m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 30),
+             "%s: bad shape (m=%lld n=%lld k=%lld; k must be a multiple of 32)", what, (long long)m, (long long)n,
+             (long long)k);
+  KX_REQUIRE(lda % 8 == 0 && lda >= k && ldc >= n && aligned16(a) && aligned8(c) && aligned8(wq),
+             "%s: bad stride or alignment", what);
+  const int rc = check_epilogue(what, epilogue, bias, c, ldc, resid, ldr, n, gate, gate_div, gate_stride);
+  if (rc) return rc;
+  if (m == 0 || n == 0) return KX_OK;
+  const Epilogue epi{(const uint16_t*)bias, resid, ldr, gate, gate_div, gate_stride, epilogue};
+  const QuantW qw{wq, nullptr, nullptr, (const uint8_t*)scales};
+  dispatch<QMX8>((const uint16_t*)a, lda, nullptr, 0, qw, c, ldc, m, n, k, epi, (hipStream_t)stream);
+  return check_launch(what);
+}
+
+extern "C" int kx_dequant_mxfp8_bf16(const uint32_t* wq, const void* scales, void* out, int64_t n, int64_t k,
+                                     int group_size, int transposed, kx_stream_t stream) {
+  const char* what = "kx_dequant_mxfp8_bf16";
+  KX_REQUIRE(wq && scales && out, "%s: null tensor", what);
+  KX_REQUIRE(group_size == 32, "%s: group_size must be 32, got %d", what, group_size);
+  KX_REQUIRE(n >= 0 && k >= 0 && n < (1ll << 31) && k < (1ll << 31), "%s: bad shape", what);
+  KX_REQUIRE(transposed ? (n % 32 == 0 && k % 8 == 0) : k % 32 == 0,
+             "%s: the grouped axis must be a multiple of 32 (and k of 8 when transposed): n=%lld k=%lld", what,
+             (long long)n, (long long)k);
+  KX_REQUIRE(aligned16(out) && (transposed ? aligned16(wq) : aligned8(wq)), "%s: out (and wq) misaligned", what);
+  if (n == 0 || k == 0) return KX_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (transposed) {
+    const dim3 grid((unsigned)((n + 63) / 64), (unsigned)((k + 63) / 64));
+    dequant_mx8_t_kernel<<<grid, 256, 0, s>>>(wq, (const uint8_t*)scales, (uint16_t*)out, n, k);
+  } else {
+    const int64_t total = n * (k / 8);
+    dequant_mx8_kernel<<<(unsigned)((total + 255) / 256), 256, 0, s>>>(wq, (const uint8_t*)scales, (uint16_t*)out,
+                                                                       n, k);
+  }
+  return check_launch(what);
 }
 
 extern "C" int kx_qweight_tile_affine(const uint32_t* wq, const void* scales, const void* biases,

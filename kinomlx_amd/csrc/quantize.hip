@@ -6,7 +6,7 @@
 // that is not positive; bias = bf16(lo); code = clamp(rint((w - bias) / scale), 0, 2^bits - 1)
 // with the fp32 subtraction and correctly rounded division. The dequantized weight is then
 // bf16(scale * code + bias) (kx_dequant_affine_bf16). HBM-bound: one read of the weight, an
-// eighth (int4) or a quarter (int8) of it written back.
+// eighth (int4) or a quarter (int8) of it written back. The mxfp8 quantizer (OCP MX) follows.
 #include <math.h>
 
 #include "common.h"
@@ -77,10 +77,87 @@ __global__ __launch_bounds__(256) void quantize_affine_kernel(const uint16_t* __
   }
 }
 
+// ---- mxfp8 (OCP MX: FP8 E4M3 elements, one E8M0 scale per 32 along K) ---------------------------
+//
+// Per group: X = floor(log2(max |w|)) - 8 (8: the exponent of E4M3's largest normal, 448), clamped
+// to [-127, 127], and -127 for an all-zero group; scale byte X + 127; element code = E4M3 of
+// w * 2^-X rounded to nearest even and saturated at +-448. Every step is exact in fp32 except the
+// one rounding to E4M3.
+
+// |v| -> E4M3 code (sign from v's sign bit; NaN -> 0x7F).
+__device__ __forceinline__ uint32_t e4m3_rne(float v) {
+  if (v != v) return 0x7Fu;
+  const uint32_t sign = (__float_as_uint(v) >> 24) & 0x80u;
+  const float a = fabsf(v);
+  uint32_t code;
+  if (a >= 448.0f) {
+    code = 0x7Eu;
+  } else if (a < 0.015625f) {
+    code = (uint32_t)rintf(a * 512.0f);  // subnormal steps of 2^-9; 8 steps is 2^-6 (code 8)
+  } else {
+    int e;
+    frexpf(a, &e);
+    const int ex = e - 1;  // a in [2^ex, 2^(ex+1)), ex in [-6, 8]: 8 steps of 2^(ex-3) per binade
+    code = (uint32_t)(((ex + 7) << 3) + (int)rintf(ldexpf(a, 3 - ex)) - 8);  // 16 steps carry to ex+1
+  }
+  return sign | code;
+}
+
+// Four lanes per group of 32: lane `sub` holds values 8 sub .. 8 sub + 7 (one 16-byte load) and
+// writes their two packed words; the group maximum is reduced over the four lanes.
+__global__ __launch_bounds__(256) void quantize_mx8_kernel(const uint16_t* __restrict__ w, int64_t ldw,
+                                                           uint32_t* __restrict__ words, uint8_t* __restrict__ scales,
+                                                           int64_t groups, int64_t groups_per_row) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t g = t >> 2;
+  const int sub = (int)(t & 3);
+  // whole groups of four lanes are in or out of range together, so the shuffles stay in a group
+  if (g >= groups) return;
+  const int64_t row = g / groups_per_row, col = g - row * groups_per_row;
+  float v[8];
+  unpack8(*reinterpret_cast<const uint4*>(w + row * ldw + col * 32 + sub * 8), v);
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+#pragma unroll
+  for (int o = 1; o < 4; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 4));
+  int x = -127;
+  if (amax > 0.0f) {
+    int e;
+    frexpf(amax, &e);
+    x = min(max(e - 1 - 8, -127), 127);
+  }
+  uint32_t code[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) code[i] = e4m3_rne(ldexpf(v[i], -x));
+  uint2 pair;
+  pair.x = code[0] | (code[1] << 8) | (code[2] << 16) | (code[3] << 24);
+  pair.y = code[4] | (code[5] << 8) | (code[6] << 16) | (code[7] << 24);
+  reinterpret_cast<uint2*>(words)[g * 4 + sub] = pair;
+  if (sub == 0) scales[g] = (uint8_t)(x + 127);
+}
+
 }  // namespace
 }  // namespace kx
 
 using namespace kx;
+
+extern "C" int kx_quantize_mxfp8_bf16(const void* w, int64_t ldw, uint32_t* wq, void* scales, int64_t n, int64_t k,
+                                      int group_size, kx_stream_t stream) {
+  const char* what = "kx_quantize_mxfp8_bf16";
+  KX_REQUIRE(w && wq && scales, "%s: null tensor", what);
+  KX_REQUIRE(group_size == 32, "%s: group_size must be 32, got %d", what, group_size);
+  KX_REQUIRE(n >= 0 && k > 0 && k % 32 == 0 && ldw >= k && ldw % 8 == 0 && aligned16(w),
+             "%s: bad shape (n=%lld k=%lld ldw=%lld; k %% 32 == 0, 16-byte rows)", what, (long long)n, (long long)k,
+             (long long)ldw);
+  KX_REQUIRE(aligned8(wq), "%s: wq must be 8-byte aligned", what);
+  const int64_t groups = n * (k / 32);
+  KX_REQUIRE(groups * 4 / 256 < (1ll << 31), "%s: too many groups", what);
+  if (groups == 0) return KX_OK;
+  quantize_mx8_kernel<<<(unsigned)((groups * 4 + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+      (const uint16_t*)w, ldw, wq, (uint8_t*)scales, groups, k / 32);
+  return check_launch(what);
+}
 
 extern "C" int kx_quantize_affine_bf16(const void* w, int64_t ldw, uint32_t* wq, void* scales, void* biases,
                                        int64_t n, int64_t k, int group_size, int bits, kx_stream_t stream) {

@@ -1,9 +1,10 @@
-"""Group-wise affine int4/int8 weight-quantized linear layers on MI355X.
+"""Weight-quantized linear layers on MI355X: group-wise affine int4/int8 and mxfp8.
 
-Replaces ``nn.QuantizedLinear`` / ``mx.quantized_matmul(..., mode="affine")`` as the LTX-2 loader
-installs them (``kinomlx/models/ltx2/weights/quantization.py:17-44``, ``:221-274``; defaults
-``kinomlx/models/ltx2/weights/tensors.py:185-203``: affine -> group 64, 4 bits; quantizer call
-``kinomlx/models/ltx2/preparation.py:139-157``).
+Replaces ``nn.QuantizedLinear`` / ``mx.quantized_matmul(..., mode=...)`` and
+``_PretransposedQuantizedLinear`` as the LTX-2 loader installs them
+(``kinomlx/models/ltx2/weights/quantization.py:17-44``, ``:199-274``; defaults
+``kinomlx/models/ltx2/weights/tensors.py:185-203``: affine -> group 64, 4 bits, mxfp8 -> group 32,
+8 bits; quantizer call ``kinomlx/models/ltx2/preparation.py:139-157``).
 
 Format: ``weight`` uint32 words ``(out, in * bits / 32)`` (stored in an int32 tensor), element
 ``j`` of a word at bits ``[bits*j, bits*(j+1))``; ``scales`` and ``biases`` bf16 ``(out, in /
@@ -17,6 +18,19 @@ stage in one contiguous block), prepared once on construction and used by every 
 ``quantize`` is this build's deterministic quantizer (MLX's own scale/bias selection is not
 reproduced): per group ``scale = bf16((max - min) / (2^bits - 1))``, ``bias = bf16(min)``,
 ``q = clip(round((w - bias) / scale), 0, 2^bits - 1)``.
+
+mxfp8 (OCP MX): ``weight`` uint32 words ``(out, in / 4)`` of four FP8 E4M3 codes (element ``j`` in
+byte ``j``), ``scales`` uint8 ``(out, in / 32)`` E8M0 exponents, no biases; ``w = e4m3(q) *
+2^(s - 127)``, exact in bf16. The GEMM converts the codes inside its mainloop. The pretransposed
+layout of ``transformer_quantize="mxfp8-blocks-pretranspose"`` (packed from ``weight.T``: words
+``(in, out / 4)``, scales ``(in, out / 32)``, groups along the output axis) shares no group with
+the ``(out, in)`` layout the GEMM streams, so ``PretransposedQuantizedLinear`` dequantizes it
+once, exactly, to the bf16 ``(out, in)`` weight and runs the dense GEMM. ``quantize_mxfp8`` is
+the OCP MX conversion (shared exponent ``floor(log2(max |w|)) - 8``, elements rounded to nearest
+even and saturated at 448); MLX's own exponent choice is not reproduced.
+
+``quant_defaults`` knows the reference's four modes; mxfp4 and nvfp4 layers raise
+``NotImplementedError`` on MI355X.
 """
 
 from __future__ import annotations
@@ -28,18 +42,33 @@ from .mpp_linear import ACTIVATIONS
 
 DEFAULT_GROUP_SIZE = 64
 DEFAULT_BITS = 4
-_MODES = ("affine",)
+# (group_size, bits) per mode (``weights/tensors.py:185-203``)
+_DEFAULTS = {"affine": (64, 4), "mxfp4": (32, 4), "mxfp8": (32, 8), "nvfp4": (16, 4)}
+KERNEL_MODES = ("affine", "mxfp8")
 
 
 def quant_defaults(mode: str, group_size: int | None, bits: int | None) -> tuple[int, int]:
-    """(group_size, bits) with the affine defaults (``weights/tensors.py:185-203``)."""
-    if mode not in _MODES:
-        raise ValueError(f"Unsupported quantization mode on MI355X: {mode}")
-    g = DEFAULT_GROUP_SIZE if group_size is None else group_size
-    b = DEFAULT_BITS if bits is None else bits
+    """(group_size, bits) with the mode's defaults filled in (``weights/tensors.py:185-203``)."""
+    if mode not in _DEFAULTS:
+        raise ValueError(f"Unsupported FF quantization mode: {mode}")
+    g0, b0 = _DEFAULTS[mode]
+    g = g0 if group_size is None else group_size
+    b = b0 if bits is None else bits
     if g <= 0 or b <= 0:
         raise ValueError("quantization group size and bits must be positive")
     return g, b
+
+
+def _check_mode(mode: str, group_size: int, bits: int) -> None:
+    """A mode, group size and width this build has kernels for."""
+    quant_defaults(mode, group_size, bits)
+    if mode not in KERNEL_MODES:
+        raise NotImplementedError(f"{mode} quantized linears have no MI355X kernel (affine and mxfp8 do)")
+    if mode == "mxfp8":
+        if (group_size, bits) != (32, 8):
+            raise ValueError(f"mxfp8 takes group size 32 and 8 bits, got {group_size} and {bits}")
+    else:
+        _check_format(group_size, bits)
 
 
 def _check_format(group_size: int, bits: int) -> None:
@@ -120,6 +149,46 @@ def dequantize(words: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, 
     return out
 
 
+def quantize_mxfp8(weight: torch.Tensor, group_size: int = 32) -> tuple[torch.Tensor, torch.Tensor]:
+    """``(out, in)`` weight -> mxfp8 ``(words (out, in / 4) int32, scales (out, in / 32) uint8)``.
+
+    On the GPU: the quantize-on-load kernel (``kx_quantize_mxfp8_bf16``) on the bf16 weight. A
+    host weight is converted by the same arithmetic in torch (the E4M3 rounding is torch's
+    round-to-nearest-even ``float8_e4m3fn`` cast after clamping to +-448): bit-identical on bf16
+    weights (tested)."""
+    if group_size != 32:
+        raise ValueError(f"mxfp8 takes group size 32, got {group_size}")
+    n, k = (int(v) for v in weight.shape)
+    if k % 32:
+        raise ValueError(f"mxfp8 groups the last axis by 32: cannot quantize a {n} x {k} matrix")
+    if weight.is_cuda:
+        w = weight.to(torch.bfloat16)
+        if w.stride(-1) != 1 or w.stride(0) % 8 or w.data_ptr() % 16:
+            w = w.contiguous()
+        words = torch.empty((n, k // 4), dtype=torch.int32, device=w.device)
+        scales = torch.empty((n, k // 32), dtype=torch.uint8, device=w.device)
+        if n:
+            _lib.launch_quantize_mxfp8(w, words, scales)
+        return words, scales
+    w = weight.to(torch.bfloat16).float().reshape(n, k // 32, 32)
+    amax = w.abs().amax(dim=-1)
+    _, e = torch.frexp(amax)
+    x = torch.where(amax > 0, (e.to(torch.int64) - 9).clamp(-127, 127), torch.full_like(e, -127, dtype=torch.int64))
+    scaled = torch.ldexp(w, (-x)[..., None].to(torch.float32))
+    codes = scaled.clamp(-448.0, 448.0).to(torch.float8_e4m3fn).view(torch.uint8).reshape(n, k)
+    return codes.contiguous().view(torch.int32), (x + 127).to(torch.uint8).contiguous()
+
+
+def dequantize_mxfp8(words: torch.Tensor, scales: torch.Tensor, *, transposed: bool = False) -> torch.Tensor:
+    """mxfp8 weight -> bf16 ``(out, in)``, exactly: ``words`` ``(out, in / 4)``, or with
+    ``transposed`` the pretransposed ``(in, out / 4)`` packing of ``weight.T``."""
+    rows, cols = int(words.shape[0]), int(words.shape[1]) * 4
+    n, k = (cols, rows) if transposed else (rows, cols)
+    out = torch.empty((n, k), dtype=torch.bfloat16, device=words.device)
+    _lib.launch_dequant_mxfp8(words.contiguous(), scales.contiguous(), out, n=n, k=k, transposed=transposed)
+    return out
+
+
 def tile_weights(words: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, *,
                  bits: int = DEFAULT_BITS, group_size: int = DEFAULT_GROUP_SIZE) -> tuple[torch.Tensor, torch.Tensor]:
     """Packed affine weights -> the kernel's tiled layout ``(wt, sbt)`` (uint8 tensors)."""
@@ -181,11 +250,29 @@ def quantized_matmul(
     out_dtype: torch.dtype | None = None,
 ) -> torch.Tensor:
     """``value @ dequant(weight)^T (+ bias)`` with dequantization inside the MFMA mainloop;
-    ``activation``/``residual``/``gate``/``out``/``out_dtype`` as ``mpp_linear.fused_linear``."""
+    ``activation``/``residual``/``gate``/``out``/``out_dtype`` as ``mpp_linear.fused_linear``.
+    ``mode="mxfp8"`` takes ``biases=None``; with ``transpose=False`` (mxfp8 only: the packing of
+    ``weight.T``) the weight is dequantized for the call and multiplied by the dense GEMM."""
+    _check_mode(mode, group_size, bits)
+    if mode == "mxfp8":
+        if biases is not None:
+            raise ValueError("mxfp8 weights carry no biases")
+        if not transpose:
+            from .mpp_linear import fused_linear
+
+            dense = dequantize_mxfp8(weight, scales, transposed=True)
+            return fused_linear(value, dense, None if bias is None else bias.to(torch.bfloat16), activation=activation,
+                                residual=residual, gate=gate, out=out, out_dtype=out_dtype)
+        n = int(weight.shape[0])
+        k = int(weight.shape[1]) * 4
+        a, out, flags, bias, resid2, gate32 = _prepare_call(value, n, k, bias, activation, residual, gate,
+                                                            out_dtype, out)
+        if a.shape[0]:
+            _lib.launch_qgemm_mxfp8(a, weight, scales, out.view(-1, n), n=n, k=k, bias=bias, flags=flags,
+                                    resid=resid2, gate=gate32)
+        return out
     if not transpose:
-        raise ValueError("the MI355X quantized linear takes the (out, in) packing (transpose=True)")
-    quant_defaults(mode, group_size, bits)
-    _check_format(group_size, bits)
+        raise ValueError("the MI355X affine quantized linear takes the (out, in) packing (transpose=True)")
     n = int(weight.shape[0])
     k = int(weight.shape[1]) * 32 // bits
     if scales.shape != (n, k // group_size) or biases.shape != scales.shape:
@@ -202,14 +289,17 @@ def quantized_matmul(
 
 
 class QuantizedLinear:
-    """``nn.QuantizedLinear`` counterpart: packed affine weight, bf16 scales/biases, optional
-    bf16 bias; ``layer(x) = quantized_matmul(x, ...) + bias`` (bias fused in the epilogue)."""
+    """``nn.QuantizedLinear`` counterpart: packed affine weight with bf16 scales/biases, or an
+    mxfp8 weight with uint8 scales (``biases`` None); optional bf16 bias;
+    ``layer(x) = quantized_matmul(x, ...) + bias`` (bias fused in the epilogue)."""
 
-    def __init__(self, weight: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
-                 bias: torch.Tensor | None = None, *, group_size: int = DEFAULT_GROUP_SIZE,
-                 bits: int = DEFAULT_BITS, mode: str = "affine") -> None:
-        quant_defaults(mode, group_size, bits)
-        _check_format(group_size, bits)
+    def __init__(self, weight: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor | None,
+                 bias: torch.Tensor | None = None, *, group_size: int | None = None,
+                 bits: int | None = None, mode: str = "affine") -> None:
+        group_size, bits = quant_defaults(mode, group_size, bits)
+        _check_mode(mode, group_size, bits)
+        if (biases is None) != (mode == "mxfp8"):
+            raise ValueError("affine weights carry biases and mxfp8 weights none")
         self.weight = weight
         self.scales = scales
         self.biases = biases
@@ -225,13 +315,20 @@ class QuantizedLinear:
         self._dense = None
         k = int(weight.shape[1]) * 32 // bits
         if weight.is_cuda and int(weight.shape[0]) <= 64:
-            self._dense = dequantize(weight, scales, biases, group_size=group_size, bits=bits)
-        elif weight.is_cuda and k % 128 == 0 and int(weight.shape[0]) >= 128:
+            self._dense = (dequantize_mxfp8(weight, scales) if mode == "mxfp8"
+                           else dequantize(weight, scales, biases, group_size=group_size, bits=bits))
+        elif weight.is_cuda and mode == "affine" and k % 128 == 0 and int(weight.shape[0]) >= 128:
             self._tiled = tile_weights(weight, scales, biases, bits=bits, group_size=group_size)
 
     @classmethod
     def from_linear(cls, weight: torch.Tensor, bias: torch.Tensor | None = None, *,
-                    group_size: int = DEFAULT_GROUP_SIZE, bits: int = DEFAULT_BITS) -> "QuantizedLinear":
+                    group_size: int | None = None, bits: int | None = None,
+                    mode: str = "affine") -> "QuantizedLinear":
+        group_size, bits = quant_defaults(mode, group_size, bits)
+        if mode == "mxfp8":
+            _check_mode(mode, group_size, bits)
+            words, scales = quantize_mxfp8(weight, group_size)
+            return cls(words, scales, None, bias, group_size=group_size, bits=bits, mode=mode)
         words, scales, biases = quantize(weight, group_size, bits)
         return cls(words, scales, biases, bias, group_size=group_size, bits=bits)
 
@@ -268,12 +365,64 @@ class QuantizedLinear:
         )
 
 
+class PretransposedQuantizedLinear:
+    """``_PretransposedQuantizedLinear`` counterpart (``quantization.py:17-44``): an mxfp8 weight
+    packed from ``weight.T`` (words ``(in, out / 4)``, scales ``(in, out / 32)``), multiplied as
+    ``mx.quantized_matmul(x, w, scales, transpose=False) + bias``. Its groups run along the output
+    axis, so it is dequantized once, exactly, to the bf16 ``(out, in)`` weight, and each call is
+    the dense GEMM with the bias (and any activation / gated residual) in its epilogue."""
+
+    def __init__(self, weight: torch.Tensor, scales: torch.Tensor, bias: torch.Tensor | None = None, *,
+                 group_size: int | None = None, bits: int | None = None, mode: str = "mxfp8") -> None:
+        group_size, bits = quant_defaults(mode, group_size, bits)
+        if mode != "mxfp8":
+            raise NotImplementedError(f"pretransposed {mode} weights have no MI355X path (mxfp8 does)")
+        _check_mode(mode, group_size, bits)
+        self.weight = weight
+        self.scales = scales
+        self.bias = bias
+        self.group_size = group_size
+        self.bits = bits
+        self.mode = mode
+        self._dense = dequantize_mxfp8(weight, scales, transposed=True) if weight.is_cuda else None
+
+    @classmethod
+    def from_linear(cls, weight: torch.Tensor, bias: torch.Tensor | None = None) -> "PretransposedQuantizedLinear":
+        """Pack ``weight.T`` as the reference's ``mxfp8-blocks-pretranspose`` preparation does
+        (``preparation.py:139-157``)."""
+        words, scales = quantize_mxfp8(weight.t().contiguous())
+        return cls(words, scales, bias)
+
+    @property
+    def out_features(self) -> int:
+        return int(self.weight.shape[1]) * 4
+
+    @property
+    def in_features(self) -> int:
+        return int(self.weight.shape[0])
+
+    def __call__(self, value: torch.Tensor, *, activation: str | None = None,
+                 residual: torch.Tensor | None = None, gate: torch.Tensor | None = None,
+                 out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+        from .mpp_linear import fused_linear
+
+        if self._dense is None:
+            raise RuntimeError("the pretransposed quantized linear runs on the GPU: move its weight to cuda first")
+        bias = None if self.bias is None else self.bias.to(torch.bfloat16)
+        return fused_linear(value, self._dense, bias, activation=activation, residual=residual, gate=gate, out=out,
+                            out_dtype=out_dtype)
+
+
 __all__ = [
+    "KERNEL_MODES",
+    "PretransposedQuantizedLinear",
     "QuantizedLinear",
     "dequantize",
+    "dequantize_mxfp8",
     "pack",
     "quant_defaults",
     "quantize",
+    "quantize_mxfp8",
     "quantized_matmul",
     "tile_weights",
     "unpack",

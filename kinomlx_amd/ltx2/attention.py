@@ -21,7 +21,7 @@ import torch
 
 from .. import _lib
 from ..kernels import fused_ops, mpp_linear, split_rope
-from ..kernels.quantized import QuantizedLinear
+from ..kernels.quantized import PretransposedQuantizedLinear, QuantizedLinear
 from . import dense_attention as _dense
 from .rope import LTXRopeType
 
@@ -143,33 +143,45 @@ def scaled_dot_product_attention(query: torch.Tensor, key: torch.Tensor, value: 
 
 
 def _cat_layers(layers):
-    """One fused layer whose output row blocks are ``layers`` in order, and views back into it."""
-    if all(isinstance(layer, Linear) for layer in layers):
-        weight = torch.cat([layer.weight for layer in layers], dim=0).contiguous()
+    """One fused layer whose output row blocks are ``layers`` in order, and views back into it.
+    Dense layers (and pretransposed mxfp8 layers, which run on their exact bf16 dequantization)
+    fuse into one dense layer; quantized layers of one mode and format into one quantized layer
+    (their packed rows, scales and biases are per output row)."""
+    if all(isinstance(layer, (Linear, PretransposedQuantizedLinear)) for layer in layers):
+        def dense(layer):
+            return layer.weight if isinstance(layer, Linear) else layer._dense
+
+        if any(dense(layer) is None for layer in layers):
+            return None
+        weight = torch.cat([dense(layer) for layer in layers], dim=0).contiguous()
         has_bias = [layer.bias is not None for layer in layers]
         bias = None
         if any(has_bias):
             bias = torch.cat([
-                layer.bias if layer.bias is not None else torch.zeros(layer.out_features, dtype=weight.dtype,
-                                                                      device=weight.device)
+                layer.bias.to(weight.dtype) if layer.bias is not None else
+                torch.zeros(layer.out_features, dtype=weight.dtype, device=weight.device)
                 for layer in layers
             ]).contiguous()
         fused = Linear(weight, bias)
         start = 0
         for layer in layers:
             stop = start + layer.out_features
-            layer.weight = weight[start:stop]
+            if isinstance(layer, Linear):
+                layer.weight = weight[start:stop]
+            else:
+                layer._dense = weight[start:stop]
             if layer.bias is not None:
                 layer.bias = bias[start:stop]
             start = stop
         return fused
     if all(isinstance(layer, QuantizedLinear) for layer in layers):
         first = layers[0]
-        if any((layer.bits, layer.group_size) != (first.bits, first.group_size) for layer in layers):
+        if any((layer.mode, layer.bits, layer.group_size) != (first.mode, first.bits, first.group_size)
+               for layer in layers):
             return None
         words = torch.cat([layer.weight for layer in layers], dim=0).contiguous()
         scales = torch.cat([layer.scales for layer in layers], dim=0).contiguous()
-        biases = torch.cat([layer.biases for layer in layers], dim=0).contiguous()
+        biases = None if first.biases is None else torch.cat([layer.biases for layer in layers], dim=0).contiguous()
         bias = None
         if any(layer.bias is not None for layer in layers):
             bias = torch.cat([
@@ -177,7 +189,8 @@ def _cat_layers(layers):
                 torch.zeros(layer.out_features, dtype=torch.bfloat16, device=words.device)
                 for layer in layers
             ]).contiguous()
-        return QuantizedLinear(words, scales, biases, bias, group_size=first.group_size, bits=first.bits)
+        return QuantizedLinear(words, scales, biases, bias, group_size=first.group_size, bits=first.bits,
+                               mode=first.mode)
     return None
 
 

@@ -1,12 +1,15 @@
-"""LTX-2 transformer checkpoints on MI355X: source-key conversion, loading into HBM and
-quantize-on-load.
+"""LTX-2 transformer checkpoints on MI355X: source-key conversion, loading into HBM, prepared
+(``__quant__.`` / ``__layout__.``) tensors and quantize-on-load.
 
 Mirror of ``convert_checkpoint_key`` and its tables (``kinomlx/models/ltx2/transformer/graph.py:
-84-115,322-359``) and of the quantize step of the weight preparation (``kinomlx/models/ltx2/
-preparation.py:139-157``: ``mx.quantize(w, group_size, bits, mode="affine")`` on the block
-linears). The tensors move from the file to HBM through ``kinomlx_amd.io.load_to_device``; the
-quantization is the ``kx_quantize_affine_bf16`` kernel on the resident bf16 weight, followed by
-the quantized GEMM's one-time tiled layout.
+84-115,322-359``), of the quantize step of the weight preparation (``kinomlx/models/ltx2/
+preparation.py:139-157``: ``mx.quantize(w or w.T, group_size, bits, mode)`` on the block linears
+that ``quant_mode_for_key`` routes, ``kinomlx/models/ltx2/weights/tensors.py:256-283``), and of the
+binding of prepared checkpoints (``kinomlx/models/ltx2/weights/loading.py:82-110``: keys under
+``__quant__.`` are packed linears whose mode comes from the settings, ``quantization.py:199-274``;
+keys under ``__layout__.`` are ``weight_t``, the transposed dense weight). The tensors move from the
+file to HBM through ``kinomlx_amd.io.load_to_device``; on-load quantization runs the
+``kx_quantize_affine_bf16`` / ``kx_quantize_mxfp8_bf16`` kernels on the resident bf16 weight.
 """
 
 from __future__ import annotations
@@ -18,10 +21,14 @@ from pathlib import Path
 import torch
 
 from ..io.safetensors import inspect_safetensors, load_to_device
-from ..kernels.quantized import QuantizedLinear, quantize
+from ..kernels.quantized import PretransposedQuantizedLinear, QuantizedLinear, quant_defaults, quantize
 from .attention import Linear
 from .model import LTXAVModel
 
+QUANT_KEY_PREFIX = "__quant__."
+LAYOUT_KEY_PREFIX = "__layout__."
+# TransformerQuantize (kinomlx/models/ltx2/weights/schema.py:13-21)
+TRANSFORMER_QUANTIZE_MODES = ("off", "mxfp8-blocks", "mxfp8-blocks-pretranspose")
 DIFFUSION_PREFIX = "model.diffusion_model."
 _DIFFUSION_PREFIXES = (DIFFUSION_PREFIX, "diffusion_model.", "")
 _TRANSFORMER_ROOTS = (
@@ -102,9 +109,15 @@ def convert_checkpoint_key(checkpoint_key: str, *, include_audio: bool = False) 
 
 def checkpoint_bindings(path: Path | str) -> dict[str, str]:
     """Model key -> source key for every transformer tensor of the file; where several source
-    keys alias one model key, the lowest priority wins (ties are an error)."""
+    keys alias one model key, the lowest priority wins (ties are an error). Prepared tensors keep
+    their prefix: ``__quant__.<key>`` and ``__layout__.<key>`` (``loading.py:89-100``)."""
     chosen: dict[str, tuple[int, str]] = {}
     for name in inspect_safetensors(path).tensor_names:
+        if name.startswith((QUANT_KEY_PREFIX, LAYOUT_KEY_PREFIX)):
+            if name in chosen:
+                raise ValueError(f"{path}: duplicate prepared tensor {name!r}")
+            chosen[name] = (-1, name)
+            continue
         converted = convert_checkpoint_key(name)
         if converted is None:
             continue
@@ -120,19 +133,58 @@ def _bf16(t: torch.Tensor) -> torch.Tensor:
     return t if t.dtype == torch.bfloat16 else t.to(torch.bfloat16)
 
 
+def _words(t: torch.Tensor) -> torch.Tensor:
+    """Packed uint32 words as the int32 tensor the quantized kernels take (same bits)."""
+    return t.view(torch.int32) if t.dtype == torch.uint32 else t
+
+
+def quant_pretransposed(transformer_quantize: str) -> bool:
+    """``tensors.py:279-280``."""
+    return transformer_quantize == "mxfp8-blocks-pretranspose"
+
+
+def quant_mode_for_base(base: str, *, transformer_quantize: str = "off",
+                        video_ff_quantize_specs: tuple[tuple[str, str], ...] = ()) -> str | None:
+    """The quantization mode of a block linear (``quantization.py:199-218``): mxfp8 for every
+    block linear under an mxfp8 ``transformer_quantize``, else the feed-forward spec's mode."""
+    if transformer_quantize not in TRANSFORMER_QUANTIZE_MODES:
+        raise ValueError(f"Unsupported transformer weight quantization mode: {transformer_quantize}")
+    if transformer_quantize != "off" and base in QUANTIZED_LINEARS:
+        return "mxfp8"
+    targets = {"ff.project_in.proj": "project_in", "ff.project_out": "project_out"}
+    if base in targets:
+        for target, mode in video_ff_quantize_specs:
+            if target == targets[base]:
+                return mode
+    return None
+
+
 def load_transformer(path: Path | str, device, *, heads: int = 32, head_dim: int = 128,
-                     quantize_bits: int | None = None, group_size: int = 64, fuse: bool = True,
-                     strict: bool = True) -> LTXAVModel:
+                     quantize_bits: int | None = None, group_size: int = 64, transformer_quantize: str = "off",
+                     transformer_quantize_exclude_layers: tuple[int, ...] = (),
+                     video_ff_quantize_specs: tuple[tuple[str, str], ...] = (),
+                     video_ff_quantize_layers: tuple[int, ...] = (),
+                     video_ff_quantize_group_size: int | None = None, video_ff_quantize_bits: int | None = None,
+                     fuse: bool = True, strict: bool = True) -> LTXAVModel:
     """Build the video ``LTXAVModel`` from a safetensors checkpoint with its tensors in HBM.
 
-    Linear weights and biases are held in bf16 and the modulation tables in fp32. With
-    ``quantize_bits`` (4 or 8) every block linear of ``QUANTIZED_LINEARS`` is quantized on the
-    device into the group-``group_size`` affine format and its bf16 weight released. With
-    ``strict``, a transformer tensor the model has no place for is an error."""
+    Linear weights and biases are held in bf16 and the modulation tables in fp32. A block linear
+    takes, in this order: its prepared packed tensors (``__quant__.<base>.weight`` / ``.scales``
+    / ``.biases``, mode from ``quant_mode_for_base`` and ``quant_defaults``; the
+    ``mxfp8-blocks-pretranspose`` packing is of ``weight.T``); its prepared ``__layout__.<base>.
+    weight_t``; or its dense weight, quantized on the device when the settings route it
+    (``transformer_quantize`` for every block linear, ``video_ff_quantize_specs`` for the
+    feed-forward targets of ``video_ff_quantize_layers`` (all when empty), layers in
+    ``transformer_quantize_exclude_layers`` never), or with ``quantize_bits`` (4 or 8) into the
+    group-``group_size`` affine format. With ``strict``, a transformer tensor the model has no
+    place for is an error."""
+    if transformer_quantize not in TRANSFORMER_QUANTIZE_MODES:
+        raise ValueError(f"Unsupported transformer weight quantization mode: {transformer_quantize}")
     bindings = checkpoint_bindings(path)
     tensors = load_to_device(path, device, names=bindings.values())
     params = {target: tensors.pop(source) for target, source in bindings.items()}
     used: set[str] = set()
+    pretransposed = quant_pretransposed(transformer_quantize)
 
     def take(key: str) -> torch.Tensor:
         if key not in params:
@@ -140,16 +192,59 @@ def load_transformer(path: Path | str, device, *, heads: int = 32, head_dim: int
         used.add(key)
         return params[key]
 
-    def linear(prefix: str, quantized: bool = False):
-        weight = _bf16(take(f"{prefix}.weight"))
+    def routed_mode(layer: int, base: str) -> str | None:
+        if layer in transformer_quantize_exclude_layers:
+            return None
+        if transformer_quantize != "off" and base in QUANTIZED_LINEARS:
+            return "mxfp8"
+        if video_ff_quantize_layers and layer not in video_ff_quantize_layers:
+            return None
+        return quant_mode_for_base(base, video_ff_quantize_specs=video_ff_quantize_specs)
+
+    def linear(prefix: str, layer: int | None = None, base: str | None = None):
         bias = _bf16(take(f"{prefix}.bias")) if f"{prefix}.bias" in params else None
-        if quantized and quantize_bits:
+        quant = f"{QUANT_KEY_PREFIX}{prefix}"
+        if f"{quant}.weight" in params or f"{quant}.scales" in params:
+            if base is None:
+                raise ValueError(f"{path}: unexpected non-block quantized weight key: {quant}.weight")
+            mode = quant_mode_for_base(base, transformer_quantize=transformer_quantize,
+                                       video_ff_quantize_specs=video_ff_quantize_specs)
+            if mode is None:
+                raise ValueError(f"Missing quantization mode for transformer target: {base}")
+            missing = sorted({"weight", "scales"} - {p for p in ("weight", "scales") if f"{quant}.{p}" in params})
+            if missing:
+                raise ValueError(f"Incomplete quantized weight target {base}: missing {', '.join(missing)}")
+            gs, bits = quant_defaults(mode, video_ff_quantize_group_size, video_ff_quantize_bits)
+            words, scales = _words(take(f"{quant}.weight")), take(f"{quant}.scales")
+            biases = take(f"{quant}.biases") if f"{quant}.biases" in params else None
+            if pretransposed and mode == "mxfp8":
+                return PretransposedQuantizedLinear(words, scales, bias, group_size=gs, bits=bits, mode=mode)
+            return QuantizedLinear(words, scales, None if biases is None else _bf16(biases), bias, group_size=gs,
+                                   bits=bits, mode=mode)
+        layout = f"{LAYOUT_KEY_PREFIX}{prefix}.weight_t"
+        if layout in params:
+            return Linear(_bf16(take(layout)).t().contiguous(), bias)
+        weight = _bf16(take(f"{prefix}.weight"))
+        mode = routed_mode(layer, base) if base is not None else None
+        if mode is not None:
+            gs, bits = quant_defaults(mode, video_ff_quantize_group_size, video_ff_quantize_bits)
+            params[f"{prefix}.weight"] = None
+            if pretransposed and mode == "mxfp8":
+                return PretransposedQuantizedLinear.from_linear(weight, bias)
+            return QuantizedLinear.from_linear(weight, bias, group_size=gs, bits=bits, mode=mode)
+        if base is not None and quantize_bits:
             words, scales, biases = quantize(weight, group_size, quantize_bits)
             params[f"{prefix}.weight"] = None
             return QuantizedLinear(words, scales, biases, bias, group_size=group_size, bits=quantize_bits)
         return Linear(weight, bias)
 
-    layers = sorted({int(k.split(".")[1]) for k in params if k.startswith("transformer_blocks.")})
+    def block_index(key: str) -> int | None:
+        for prefix in (QUANT_KEY_PREFIX, LAYOUT_KEY_PREFIX, ""):
+            if key.startswith(prefix + "transformer_blocks."):
+                return int(key[len(prefix):].split(".")[1])
+        return None
+
+    layers = sorted({i for i in map(block_index, params) if i is not None})
     if layers != list(range(len(layers))) or not layers:
         raise ValueError(f"{path}: transformer blocks must be numbered 0..n-1, found {layers[:8]}...")
     patchify = take("patchify_proj.weight")
@@ -176,11 +271,11 @@ def load_transformer(path: Path | str, device, *, heads: int = 32, head_dim: int
         for name in ("attn1", "attn2"):
             attn = getattr(block, name)
             for proj in ("to_q", "to_k", "to_v", "to_out", "to_gate_logits"):
-                setattr(attn, proj, linear(f"{prefix}.{name}.{proj}", quantized=True))
+                setattr(attn, proj, linear(f"{prefix}.{name}.{proj}", index, f"{name}.{proj}"))
             attn.q_norm.weight = take(f"{prefix}.{name}.q_norm.weight")
             attn.k_norm.weight = take(f"{prefix}.{name}.k_norm.weight")
-        block.ff.project_in.proj = linear(f"{prefix}.ff.project_in.proj", quantized=True)
-        block.ff.project_out = linear(f"{prefix}.ff.project_out", quantized=True)
+        block.ff.project_in.proj = linear(f"{prefix}.ff.project_in.proj", index, "ff.project_in.proj")
+        block.ff.project_out = linear(f"{prefix}.ff.project_out", index, "ff.project_out")
         block.scale_shift_table = take(f"{prefix}.scale_shift_table").float()
         block.prompt_scale_shift_table = take(f"{prefix}.prompt_scale_shift_table").float()
         if fuse:
@@ -193,6 +288,11 @@ def load_transformer(path: Path | str, device, *, heads: int = 32, head_dim: int
 
 __all__ = [
     "DIFFUSION_PREFIX",
+    "LAYOUT_KEY_PREFIX",
+    "QUANT_KEY_PREFIX",
+    "TRANSFORMER_QUANTIZE_MODES",
+    "quant_mode_for_base",
+    "quant_pretransposed",
     "QUANTIZED_LINEARS",
     "ConvertedTransformerKey",
     "checkpoint_bindings",

@@ -17,6 +17,14 @@ __all__ = [
     "attention",
     "bf16_bits",
     "dequantize_affine",
+    "dequantize_mxfp8",
+    "e4m3_decode",
+    "e4m3_encode",
+    "e8m0_scale",
+    "mxfp8_linear",
+    "pack_bytes",
+    "quantize_mxfp8",
+    "unpack_bytes",
     "flux_rotary_positions",
     "fractional_positions",
     "frequency_grid",
@@ -436,3 +444,104 @@ def quantized_linear(value, words, scales, biases, bias=None, *, group_size: int
     dequantised weight and FP32 accumulation (``kinomlx/models/ltx2/weights/quantization.py:28-44``)."""
     weight = dequantize_affine(words, scales, biases, group_size=group_size, bits=bits)
     return linear(value, weight, bias)
+
+
+# ---------------------------------------------------------------------------------------------
+# MX block-scaled fp8 (``mode="mxfp8"``: group 32, 8 bits; ``kinomlx/models/ltx2/weights/
+# tensors.py:185-203``, ``preparation.py:139-157``, ``weights/quantization.py:17-44``). The
+# arithmetic lives in MLX (``mx.quantize`` / ``mx.quantized_matmul``, not vendored): the format
+# follows the OCP Microscaling (MX) v1.0 specification. Elements are FP8 E4M3 (OCP "FN": 1 sign,
+# 4 exponent bits with bias 7, 3 mantissa bits; exponent 0 is subnormal m * 2^-9; 0x7F / 0xFF
+# are NaN; no infinities; the largest finite value is 448), four per uint32 word little-endian
+# (element j at bits [8j, 8j+8)); each run of 32 elements along the quantized axis shares one
+# E8M0 scale byte S (2^(S - 127); 255 is NaN). Dequantisation is exact in bf16: an E4M3 value has
+# 4 significant bits and the scale is a power of two.
+
+E4M3_MAX = 448.0
+
+
+def e4m3_decode(codes) -> np.ndarray:
+    """FP8 E4M3 (OCP) bytes -> float32, exactly (NaN for 0x7F / 0xFF)."""
+    c = np.asarray(codes, dtype=np.uint32)
+    sign = np.where((c >> 7) & 1, -1.0, 1.0)
+    e = ((c >> 3) & 15).astype(np.int64)
+    m = (c & 7).astype(np.float64)
+    mag = np.where(e == 0, m * 2.0 ** -9, (1.0 + m / 8.0) * np.exp2(e - 7.0))
+    mag = np.where((e == 15) & (m == 7), np.nan, mag)
+    return (sign * mag).astype(F32)
+
+
+def e4m3_encode(value) -> np.ndarray:
+    """float -> FP8 E4M3 bytes, round to nearest even, saturating at +-448 (values already scaled
+    into the element range; NaN -> 0x7F; the sign survives underflow to zero)."""
+    v = np.asarray(value, dtype=np.float64)
+    a = np.nan_to_num(np.abs(v), nan=0.0, posinf=E4M3_MAX)
+    e = np.floor(np.log2(np.maximum(a, 2.0 ** -30)))
+    e = np.maximum(e, -6.0)  # below 2^-6 the spacing stays 2^-9 (subnormals)
+    quantum = np.exp2(e - 3.0)
+    q = np.minimum(np.rint(a / quantum) * quantum, E4M3_MAX)
+    # re-derive the fields from the rounded magnitude (rounding may carry into the exponent)
+    qe = np.floor(np.log2(np.maximum(q, 2.0 ** -30)))
+    normal = q >= 2.0 ** -6
+    exp_field = np.where(normal, qe + 7.0, 0.0)
+    mant = np.where(normal, (q / np.exp2(qe) - 1.0) * 8.0, q / 2.0 ** -9)
+    code = (exp_field.astype(np.uint32) << 3) | np.rint(mant).astype(np.uint32)
+    code = np.where(q == 0, 0, code) | np.where(np.signbit(v), 0x80, 0).astype(np.uint32)
+    return np.where(np.isnan(v), 0x7F, code).astype(np.uint8)
+
+
+def e8m0_scale(scales) -> np.ndarray:
+    """E8M0 scale bytes -> float32 powers of two 2^(S - 127) (NaN for 255)."""
+    s = np.asarray(scales, dtype=np.int64)
+    return np.where(s == 255, np.nan, np.exp2((s - 127).astype(np.float64))).astype(F32)
+
+
+def pack_bytes(codes: np.ndarray) -> np.ndarray:
+    """``(R, C)`` bytes -> ``(R, C / 4)`` little-endian uint32 words."""
+    c = np.ascontiguousarray(codes, dtype=np.uint8)
+    return c.view("<u4").reshape(c.shape[0], c.shape[1] // 4)
+
+
+def unpack_bytes(words: np.ndarray) -> np.ndarray:
+    """``(R, W)`` uint32 words -> ``(R, 4 W)`` bytes."""
+    w = np.ascontiguousarray(words, dtype="<u4")
+    return w.view(np.uint8).reshape(w.shape[0], w.shape[1] * 4)
+
+
+def quantize_mxfp8(weight, group_size: int = 32):
+    """``(R, C)`` -> ``(words (R, C/4) uint32, scales (R, C/group_size) uint8)`` along the last
+    axis, by the OCP MX conversion: shared exponent ``floor(log2(amax)) - 8`` (8 = the exponent of
+    E4M3's largest normal), clamped to the E8M0 range; elements RNE to E4M3 with saturation. This
+    build's deterministic quantizer (MLX's own exponent choice is not reproduced: parity
+    unpinned); a group of zeros gets S = 0."""
+    w = np.asarray(weight, dtype=np.float64)
+    r, c = w.shape
+    if c % group_size or group_size % 4:
+        raise ValueError("mxfp8 quantization needs the last axis a multiple of the group size")
+    g = w.reshape(r, c // group_size, group_size)
+    amax = np.abs(g).max(axis=-1)
+    exp = np.floor(np.log2(np.maximum(amax, 2.0 ** -200))) - 8.0
+    exp = np.clip(exp, -127.0, 127.0)
+    exp = np.where(amax == 0, -127.0, exp)
+    scaled = g / np.exp2(exp)[..., None]
+    codes = e4m3_encode(scaled).reshape(r, c)
+    return pack_bytes(codes), (exp + 127.0).astype(np.uint8)
+
+
+def dequantize_mxfp8(words, scales, *, group_size: int = 32) -> np.ndarray:
+    """Bit-exact dequantisation along the last axis: ``bf16(e4m3(q) * 2^(S-127))`` -> float32
+    ``(R, 4 W)``; the product is exact, so the bf16 rounding is the identity for any S in 1..254
+    whose result stays above the bf16 normal range."""
+    codes = unpack_bytes(words)
+    vals = e4m3_decode(codes).astype(np.float64)
+    s = np.repeat(e8m0_scale(scales).astype(np.float64), group_size, axis=1)[:, : codes.shape[1]]
+    return to_bf16((vals * s).astype(F32))
+
+
+def mxfp8_linear(value, words, scales, bias=None, *, group_size: int = 32, transposed: bool = True):
+    """``quantized_matmul(x, w, scales, transpose=transposed, group_size, bits=8, mode="mxfp8")
+    + bias``: with ``transposed`` the packed weight is ``(out, in / 4)`` grouped along ``in``
+    (``nn.QuantizedLinear``); without, it was built from ``weight.T`` and is ``(in, out / 4)``
+    grouped along ``out`` (``_PretransposedQuantizedLinear``, ``quantization.py:17-44``)."""
+    w = dequantize_mxfp8(words, scales, group_size=group_size)
+    return linear(value, w if transposed else np.ascontiguousarray(w.T), bias)

@@ -71,10 +71,51 @@ def test_linear_supports_and_applies():
 
 
 def test_quant_defaults_follow_the_reference():
+    """``tests/models/ltx2/weights/test_storage_weights.py:207-213`` and the table of
+    ``kinomlx/models/ltx2/weights/tensors.py:185-203``."""
+    assert quantized.quant_defaults("mxfp8", None, None) == (32, 8)
+    assert quantized.quant_defaults("affine", 128, 6) == (128, 6)
     assert quantized.quant_defaults("affine", None, None) == (64, 4)
-    assert quantized.quant_defaults("affine", None, 8) == (64, 8)
-    with pytest.raises(ValueError, match="mode"):
-        quantized.quant_defaults("mxfp4", None, None)
+    assert quantized.quant_defaults("mxfp4", None, None) == (32, 4)
+    assert quantized.quant_defaults("nvfp4", None, None) == (16, 4)
+    with pytest.raises(ValueError, match="must be positive"):
+        quantized.quant_defaults("affine", 0, 4)
+    with pytest.raises(ValueError, match="must be positive"):
+        quantized.quant_defaults("affine", 64, 0)
+    with pytest.raises(ValueError, match="Unsupported FF quantization mode"):
+        quantized.quant_defaults("int3", None, None)
+    # modes without an MI355X kernel are refused by the layer, not by the defaults
+    with pytest.raises(NotImplementedError, match="nvfp4"):
+        quantized.QuantizedLinear(torch.zeros((32, 8), dtype=torch.int32), torch.zeros((32, 2), dtype=torch.uint8),
+                                  None, mode="nvfp4")
+
+
+def test_quant_routing_covers_whole_block_and_targeted_ff_modes():
+    """``tests/models/ltx2/weights/test_storage_weights.py:175-206`` on the base-level routing
+    (``kinomlx/models/ltx2/weights/quantization.py:199-218``)."""
+    from kinomlx_amd.ltx2 import weights
+
+    assert weights.quant_mode_for_base("attn1.to_q", transformer_quantize="mxfp8-blocks") == "mxfp8"
+    assert weights.quant_mode_for_base("attn2.to_gate_logits", transformer_quantize="mxfp8-blocks-pretranspose") == "mxfp8"
+    assert weights.quant_mode_for_base("ff.project_out", video_ff_quantize_specs=(("project_out", "nvfp4"),)) == "nvfp4"
+    assert weights.quant_mode_for_base("ff.project_in.proj", video_ff_quantize_specs=(("project_out", "nvfp4"),)) is None
+    assert weights.quant_mode_for_base("attn1.to_q") is None
+    assert weights.quant_pretransposed("mxfp8-blocks-pretranspose") and not weights.quant_pretransposed("mxfp8-blocks")
+    with pytest.raises(ValueError, match="Unsupported transformer weight quantization mode"):
+        weights.quant_mode_for_base("attn1.to_q", transformer_quantize="fp8-blocks")
+
+
+def test_host_mxfp8_quantizer_is_bit_identical_to_the_oracle():
+    g = torch.Generator().manual_seed(4)
+    w = (torch.randn((64, 256), generator=g) * torch.exp2(torch.randint(-9, 9, (64, 1), generator=g).float()))
+    w = w.to(torch.bfloat16)
+    w[3, :32] = 0  # a zero group: scale byte 0
+    w[5, 7] = 1e30  # a group whose other elements underflow
+    w[6, 1] = -3e-39  # a bf16 subnormal
+    words, scales = quantized.quantize_mxfp8(w)
+    o_words, o_scales = oracle.quantize_mxfp8(w.float().numpy())
+    assert words.dtype == torch.int32 and scales.dtype == torch.uint8
+    assert np.array_equal(words.numpy().view(np.uint32), o_words) and np.array_equal(scales.numpy(), o_scales)
 
 
 @pytest.mark.parametrize("bits", [4, 8])

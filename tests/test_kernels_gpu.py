@@ -598,6 +598,127 @@ def test_skinny_linear_matches_oracle(device, m, n, k, bits, epilogue):
         assert np.all(np.abs(got - ref) <= 1e-5 * np.abs(ref) + 2e-5 * np.abs(ref).max())
 
 
+# ---- mxfp8 (OCP MX: E4M3 codes, one E8M0 scale per 32) -------------------------------------------
+
+
+def _mx_codes(r, rows, cols):
+    """Random E4M3 codes holding every one of the 256 codes except the two NaNs."""
+    finite = np.array([c for c in range(256) if c not in (0x7F, 0xFF)], dtype=np.uint8)
+    return finite[r.integers(0, finite.size, (rows, cols))]
+
+
+def test_mxfp8_dequant_is_exact_for_every_code_and_scale(device):
+    """Reference layout: every finite code under every scale byte whose products stay in the
+    normal fp32 range (10 .. 240), equal to the oracle's exact decode; NaN codes decode to NaN."""
+    scales_all = np.arange(10, 241, dtype=np.uint8)
+    n, k = scales_all.size, 256
+    codes = np.tile(np.arange(256, dtype=np.uint8), (n, 1))  # row i: all 256 codes, scale byte 10 + i
+    words = oracle.pack_bytes(codes)
+    scales = np.repeat(scales_all[:, None], k // 32, 1)
+    got = quantized.dequantize_mxfp8(torch.from_numpy(words.view(np.int32)).to(device), torch.from_numpy(scales).to(device))
+    ref = oracle.dequantize_mxfp8(words, scales)
+    g = _np(got)
+    assert np.array_equal(np.isnan(g), np.isnan(ref))
+    assert np.array_equal(g[~np.isnan(g)], ref[~np.isnan(ref)])
+
+
+@pytest.mark.parametrize(("out_f", "in_f"), [(352, 200), (64, 8), (96, 512)])
+def test_mxfp8_pretransposed_dequant_is_exact(device, out_f, in_f):
+    """The pretransposed packing of weight.T, (in, out / 4) words grouped along out: dequantized to
+    the (out, in) weight, equal to the oracle's (ragged 64 x 64 tiles on both axes)."""
+    r = _rng(out_f + in_f)
+    codes = _mx_codes(r, in_f, out_f)
+    words = oracle.pack_bytes(codes)
+    scales = r.integers(100, 140, (in_f, out_f // 32)).astype(np.uint8)
+    got = quantized.dequantize_mxfp8(torch.from_numpy(words.view(np.int32)).to(device),
+                                     torch.from_numpy(scales).to(device), transposed=True)
+    assert got.shape == (out_f, in_f)
+    assert np.array_equal(_np(got), oracle.dequantize_mxfp8(words, scales).T)
+
+
+@pytest.mark.parametrize("shape", [(128, 1024), (3, 96), (1000, 4096)])
+def test_gpu_mxfp8_quantizer_is_bit_identical_to_the_oracle(device, shape):
+    r = _rng(shape[0])
+    w = (r.standard_normal(shape) * np.exp2(r.integers(-10, 10, (shape[0], 1)))).astype(F32)
+    w[0, :32] = 0.0  # a zero group
+    w[-1, 5] = 3e30  # the rest of its group underflows
+    w[-1, 40] = -1e-39  # a bf16 subnormal
+    w = oracle.to_bf16(w)
+    words, scales = quantized.quantize_mxfp8(_bf(w, device))
+    o_words, o_scales = oracle.quantize_mxfp8(w)
+    assert np.array_equal(words.cpu().numpy().view(np.uint32), o_words)
+    assert np.array_equal(scales.cpu().numpy(), o_scales)
+    h_words, h_scales = quantized.quantize_mxfp8(torch.from_numpy(w).to(torch.bfloat16))  # host packing
+    assert torch.equal(words.cpu(), h_words) and torch.equal(scales.cpu(), h_scales)
+
+
+@pytest.mark.parametrize("tile", ["0", "1"])
+@pytest.mark.parametrize(("m", "n", "k"), [(512, 512, 512), (1000, 132, 384), (600, 256, 4096), (300, 520, 1024),
+                                           (9, 64, 256), (37, 48, 96), (200, 256, 96)])
+@pytest.mark.parametrize("epilogue", ["bias", "gated_f32"])
+def test_mxfp8_linear_matches_oracle(device, monkeypatch, tile, m, n, k, epilogue):
+    """``kx_qgemm_mxfp8_bf16`` on every kernel it dispatches to: the direct-to-LDS kernel at both of
+    its tiles (m >= 512, k % 128 == 0), the register-staged kernel (fewer rows, and k % 64 == 32:
+    a half-empty last stage), the skinny kernel (n <= 64); against the oracle's mxfp8 linear (the
+    dequantization is exact, so only the fp32 summation order differs) and, for the bias
+    epilogue, against the dense kernel on the exactly dequantized weight."""
+    monkeypatch.setenv("KX355_GEMM_LDS_TILE", tile)
+    r = _rng(m + n + k)
+    x = oracle.to_bf16((r.standard_normal((m, k)) * 0.5).astype(F32))
+    w = oracle.to_bf16((r.standard_normal((n, k)) * k ** -0.5).astype(F32))
+    b = oracle.to_bf16((r.standard_normal(n) * 0.02).astype(F32))
+    words, scales = oracle.quantize_mxfp8(w)
+    layer = quantized.QuantizedLinear(torch.from_numpy(words.view(np.int32)).to(device), torch.from_numpy(scales).to(device),
+                                      None, _bf(b, device), mode="mxfp8")
+    assert (layer.group_size, layer.bits) == (32, 8)
+    if n <= 64:
+        layer._dense = None  # the skinny kernel itself, not the layer's dequantized copy
+    ref = oracle.mxfp8_linear(x, words, scales, b)
+    if epilogue == "bias":
+        got = _np(layer(_bf(x, device)))
+        assert _gemm_close(got, ref)
+        dense = _np(mpp_linear.linear(_bf(x, device), quantized.dequantize_mxfp8(layer.weight, layer.scales),
+                                      _bf(b, device), transposed=True))
+        assert max_abs(got, dense) <= 2.0**-7 * np.abs(dense).max()
+    else:
+        resid = r.standard_normal((m, n)).astype(F32)
+        gate = r.standard_normal(n).astype(F32)
+        got = _np(layer(_bf(x, device), residual=_f32(resid, device), gate=_f32(gate, device), out_dtype=torch.float32))
+        full = resid + gate * ref
+        assert np.all(np.abs(got - full) <= 1e-5 * np.abs(full) + 2e-5 * np.abs(full).max())
+
+
+def test_mxfp8_identity_linear_returns_its_input(device):
+    """``tests/models/ltx2/weights/test_family.py:262-283``: the mxfp8 identity (eye(32)) bound as
+    a quantized linear returns its input; and as the pretransposed layer."""
+    eye = torch.eye(32, dtype=torch.bfloat16)
+    x = torch.ones((1, 32), dtype=torch.bfloat16, device=device)
+    layer = quantized.QuantizedLinear.from_linear(eye.to(device), mode="mxfp8")
+    assert torch.equal(layer(x), x)
+    layer._dense = None
+    assert torch.equal(layer(x), x)
+    pre = quantized.PretransposedQuantizedLinear.from_linear(eye.to(device))
+    assert torch.equal(pre(x), x)
+    y = torch.randn((5, 32), device=device).to(torch.bfloat16)
+    assert torch.equal(layer(y), y) and torch.equal(pre(y), y)
+
+
+def test_pretransposed_linear_is_the_dense_product_of_its_dequantized_weight(device):
+    r = _rng(77)
+    w = oracle.to_bf16((r.standard_normal((256, 512)) * 0.05).astype(F32))
+    x = oracle.to_bf16(r.standard_normal((300, 512)).astype(F32))
+    b = oracle.to_bf16((r.standard_normal(256) * 0.1).astype(F32))
+    layer = quantized.PretransposedQuantizedLinear.from_linear(_bf(w, device), _bf(b, device))
+    words, scales = oracle.quantize_mxfp8(np.ascontiguousarray(w.T))
+    assert np.array_equal(layer.weight.cpu().numpy().view(np.uint32), words)
+    ref = oracle.mxfp8_linear(x, words, scales, b, transposed=False)
+    assert _gemm_close(_np(layer(_bf(x, device))), ref)
+    # the functional form (transpose=False) gives the same product
+    got = quantized.quantized_matmul(_bf(x, device), layer.weight, layer.scales, None, transpose=False, group_size=32,
+                                     bits=8, mode="mxfp8", bias=_bf(b, device))
+    assert torch.equal(got, layer(_bf(x, device)))
+
+
 def test_env_tile_override_is_restored():
     assert os.environ.get("KX355_GEMM_TILE") in (None, "")
     assert os.environ.get("KX355_GEMM_LDS_TILE") in (None, "")

@@ -323,6 +323,75 @@ def test_quantizer_error_is_within_half_a_step(bits):
     assert np.all(np.abs(deq - w) <= step * 0.5 + np.abs(w) * 2**-7 + np.repeat(np.abs(biases), 64, 1) * 2**-7 + 1e-7)
 
 
+# ---- mxfp8 (OCP MX: E4M3 elements, E8M0 group scales) --------------------------------------------
+
+
+def test_e4m3_and_e8m0_decode_match_torch_float8_over_all_codes():
+    codes = np.arange(256)
+    as_torch = torch.arange(256, dtype=torch.int32).to(torch.uint8)
+    for ours, dtype in ((oracle.e4m3_decode(codes), torch.float8_e4m3fn), (oracle.e8m0_scale(codes), torch.float8_e8m0fnu)):
+        theirs = as_torch.view(dtype).float().numpy()
+        assert np.array_equal(np.isnan(ours), np.isnan(theirs))
+        assert np.array_equal(ours[~np.isnan(ours)], theirs[~np.isnan(theirs)])
+    v = oracle.e4m3_decode(codes)
+    assert v[0x7E] == 448 and v[0x01] == 2.0 ** -9 and v[0x38] == 1 and np.isnan(v[0x7F])
+
+
+def test_e4m3_encode_is_torch_rne_below_saturation_and_saturates_at_448():
+    r = _rng(30)
+    v = (r.standard_normal(200000) * np.exp2(r.integers(-14, 9, 200000))).astype(F32)
+    v = np.concatenate([np.clip(v, -460, 460), [0.0, -0.0, 2.0 ** -10, 3 * 2.0 ** -11, 1.5 * 2.0 ** -9, 2.5 * 2.0 ** -9, 240, 248]])
+    theirs = torch.from_numpy(v.astype(F32)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(oracle.e4m3_encode(v), theirs)
+    assert list(oracle.e4m3_encode([464, 1e9, -1e9, np.inf])) == [0x7E, 0x7E, 0xFE, 0x7E]
+    codes = np.arange(256)
+    finite = ~np.isnan(oracle.e4m3_decode(codes))
+    assert np.array_equal(oracle.e4m3_encode(oracle.e4m3_decode(codes))[finite], codes[finite])
+
+
+def test_mxfp8_identity_matches_reference_binding_test():
+    """``tests/models/ltx2/weights/test_family.py:262-283``: ``mx.quantize(eye(32), 32, 8,
+    "mxfp8")`` bound as a quantized linear returns its input."""
+    words, scales = oracle.quantize_mxfp8(np.eye(32, dtype=F32))
+    assert words.shape == (32, 8) and words.dtype == np.uint32 and scales.shape == (32, 1)
+    x = np.ones((1, 32), F32)
+    assert np.array_equal(oracle.mxfp8_linear(x, words, scales), x)
+    assert np.array_equal(oracle.mxfp8_linear(x, words, scales, transposed=False), x)
+
+
+def test_mxfp8_scale_is_ocp_shared_exponent_and_error_within_half_an_element_step():
+    r = _rng(31)
+    w = (r.standard_normal((24, 256)) * np.exp2(r.integers(-6, 3, (24, 1)))).astype(F32)
+    w[3, :32] = 0.0  # an all-zero group
+    words, scales = oracle.quantize_mxfp8(w)
+    groups = np.abs(w.reshape(24, 8, 32)).max(-1)
+    expect = np.where(groups > 0, np.floor(np.log2(np.maximum(groups, 1e-30))) - 8 + 127, 0)
+    assert np.array_equal(scales, expect.astype(np.uint8))
+    deq = oracle.dequantize_mxfp8(words, scales)
+    assert np.all(deq[3, :32] == 0)
+    # one E4M3 step at |v| is 2^(floor(log2|v|) - 3) (2^-9 below the normal range), times the scale;
+    # values scaled past 448 saturate there
+    s = np.repeat(np.exp2(scales.astype(np.float64) - 127), 32, 1)
+    scaled = np.abs(w) / s
+    step = np.exp2(np.maximum(np.floor(np.log2(np.maximum(scaled, 1e-30))), -6) - 3) * s
+    bound = np.where(scaled > 448, (scaled - 448) * s, step / 2) + np.abs(w) * 2.0 ** -9
+    assert np.all(np.abs(deq - w) <= bound)
+
+
+def test_mxfp8_pretransposed_layout_groups_the_output_axis():
+    r = _rng(32)
+    w = oracle.to_bf16((r.standard_normal((64, 96)) * 0.1).astype(F32))  # (out, in)
+    x = oracle.to_bf16(r.standard_normal((5, 96)).astype(F32))
+    plain = oracle.quantize_mxfp8(w)
+    pre = oracle.quantize_mxfp8(np.ascontiguousarray(w.T))  # (in, out / 4), groups along out
+    assert pre[0].shape == (96, 16) and pre[1].shape == (96, 2)
+    ref_plain = oracle.linear(x, oracle.dequantize_mxfp8(*plain))
+    ref_pre = oracle.linear(x, np.ascontiguousarray(oracle.dequantize_mxfp8(*pre).T))
+    assert np.array_equal(oracle.mxfp8_linear(x, *plain), ref_plain)
+    assert np.array_equal(oracle.mxfp8_linear(x, *pre, transposed=False), ref_pre)
+    assert rel_l2(ref_pre, oracle.linear(x, w)) < 0.05
+
+
 # ---- block compositions --------------------------------------------------------------------------
 
 

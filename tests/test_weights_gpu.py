@@ -4,7 +4,8 @@ a whole LTX-2 video transformer built from a reference-named checkpoint.
 Bars: every loaded tensor is bit-identical to what was written; the quantize kernel is
 bit-identical to the oracle's quantizer and to the host packing; a model loaded from the file
 (bf16, or quantized on load) gives bit-identical velocities to the same model assembled from
-the in-memory parameters.
+the in-memory parameters; a prepared (``__quant__.``) mxfp8 checkpoint gives bit-identical
+velocities to quantize-on-load.
 """
 
 import numpy as np
@@ -17,8 +18,9 @@ from kinomlx_amd import workloads
 from kinomlx_amd.io import load_to_device
 from kinomlx_amd.io import safetensors as st
 from kinomlx_amd.kernels import quantized
-from kinomlx_amd.ltx2.weights import load_transformer
+from kinomlx_amd.ltx2.weights import QUANTIZED_LINEARS, load_transformer
 from kinomlx_amd.ltx2.wrappers import Modality
+from tests.conftest import cosine, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -131,3 +133,83 @@ def test_strict_loading_rejects_unplaced_tensors(device, tmp_path):
     with pytest.raises(ValueError, match="no place in the video model"):
         load_transformer(path, device, heads=SPEC.heads, head_dim=SPEC.head_dim)
     assert load_transformer(path, device, heads=SPEC.heads, head_dim=SPEC.head_dim, strict=False).num_blocks == 1
+
+
+def _mlx_key(key: str) -> str:
+    return key.replace("ff.proj_in.", "ff.project_in.proj.").replace("ff.proj_out.", "ff.project_out.")
+
+
+def _write_prepared(p, path, *, pretransposed: bool):
+    """A prepared checkpoint as ``preparation.py:139-157`` writes one: MLX keys, and every block
+    linear's weight packed by mx.quantize(w or w.T, 32, 8, "mxfp8") under ``__quant__.``
+    (uint32 words, uint8 scales; the bias stays a normal tensor)."""
+    tensors = {}
+    for index, block in enumerate(p["blocks"]):
+        for name, value in block.items():
+            key = _mlx_key(f"transformer_blocks.{index}.{name}")
+            base = key[: -len(".weight")].split(".", 2)[2] if key.endswith(".weight") else None
+            if base in QUANTIZED_LINEARS:
+                words, scales = quantized.quantize_mxfp8(value.t().contiguous() if pretransposed else value)
+                tensors[f"__quant__.{key[: -len('.weight')]}.weight"] = words.view(torch.uint32)
+                tensors[f"__quant__.{key[: -len('.weight')]}.scales"] = scales
+            else:
+                tensors[key] = value.contiguous()
+    for name, value in p.items():
+        if name != "blocks":
+            tensors[name] = value.contiguous()
+    save_file(tensors, str(path))
+
+
+# 32 heads, as the reference model has: the pretransposed packing groups the gate-logit projection's
+# output axis (heads wide) by 32
+MX_SPEC = workloads.LTXSpec(grid=(2, 4, 8), text_tokens=16, dim=2048, heads=32, head_dim=64)
+
+
+@pytest.mark.parametrize("mode", ["mxfp8-blocks", "mxfp8-blocks-pretranspose"])
+def test_prepared_mxfp8_checkpoint_matches_quantize_on_load(device, tmp_path, mode):
+    """``transformer_quantize`` on a dense checkpoint (quantized on the device) and on a prepared
+    one (``__quant__.`` tensors bound straight into the quantized layers) give bit-identical
+    velocities; the pretransposed layers equal the dense model on their exactly dequantized
+    weights, the in-mainloop mxfp8 GEMM differs from it only in fp32 summation order."""
+    pre = mode.endswith("pretranspose")
+    p = workloads.ltx_model_params(MX_SPEC, 2, in_channels=CHANNELS, out_channels=CHANNELS)
+    dense_path, prepared_path = tmp_path / "dense.safetensors", tmp_path / "prepared.safetensors"
+    _write_checkpoint(p, dense_path)
+    _write_prepared(p, prepared_path, pretransposed=pre)
+    kw = dict(heads=MX_SPEC.heads, head_dim=MX_SPEC.head_dim, transformer_quantize=mode)
+    on_load = load_transformer(dense_path, device, **kw)
+    prepared = load_transformer(prepared_path, device, **kw)
+    layer = prepared.transformer_blocks[1].ff.project_out
+    assert isinstance(layer, quantized.PretransposedQuantizedLinear if pre else quantized.QuantizedLinear)
+    assert layer.mode == "mxfp8" and (layer.group_size, layer.bits) == (32, 8)
+    inputs = workloads.ltx_model_inputs(MX_SPEC, in_channels=CHANNELS)
+    a, b = _velocity(on_load, inputs, device), _velocity(prepared, inputs, device)
+    assert torch.isfinite(a.float()).all() and torch.equal(a, b)
+
+    # the model on the exact dequantization of every packed weight (oracle)
+    blocks = []
+    for block in p["blocks"]:
+        q = dict(block)
+        for name in workloads.QUANTIZED_LTX_LINEARS:
+            w = q[f"{name}.weight"].float().numpy()
+            if pre:
+                deq = oracle.dequantize_mxfp8(*oracle.quantize_mxfp8(np.ascontiguousarray(w.T))).T
+            else:
+                deq = oracle.dequantize_mxfp8(*oracle.quantize_mxfp8(w))
+            q[f"{name}.weight"] = torch.from_numpy(np.ascontiguousarray(deq)).to(torch.bfloat16)
+        blocks.append(q)
+    dense = workloads.build_ltx_model(MX_SPEC, dict(p, blocks=blocks), device, in_channels=CHANNELS, out_channels=CHANNELS)
+    c = _velocity(dense, inputs, device)
+    if pre:
+        assert torch.equal(a, c)
+    else:
+        a32, c32 = a.float().numpy(), c.float().numpy()
+        assert cosine(a32, c32) > 0.9999 and rel_l2(a32, c32) < 5e-3
+
+
+def test_prepared_quant_tensors_need_a_mode(device, tmp_path):
+    p = workloads.ltx_model_params(SPEC, 1, in_channels=CHANNELS, out_channels=CHANNELS)
+    path = tmp_path / "prepared.safetensors"
+    _write_prepared(p, path, pretransposed=False)
+    with pytest.raises(ValueError, match="Missing quantization mode"):
+        load_transformer(path, device, heads=SPEC.heads, head_dim=SPEC.head_dim)
