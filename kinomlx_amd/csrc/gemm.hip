@@ -14,10 +14,9 @@
 // accumulator's lane holds one output row m and runs of 4 consecutive columns n: the epilogue
 // stores 8-byte vectors along the output row.
 //
-// Quantized weights: the stage's packed words and per-group bf16 scale/bias are loaded into
-// registers instead, and dequantized (bf16(fp32(scale) * q + fp32(bias))) on their way into LDS,
-// inside the mainloop; the MFMA loop is shared with the dense path. mxfp8 weights (OCP MX: FP8
-// E4M3 elements, one E8M0 scale byte per 32 along K) take the same route: each element is
+// Quantized weights: the stage's packed words and per-group bf16 scale/bias are loaded instead,
+// and dequantized (bf16(fp32(scale) * q + fp32(bias))) inside the mainloop. mxfp8 weights (OCP
+// MX: FP8 E4M3 elements, one E8M0 scale byte per 32 along K) take the same route: each element is
 // converted to fp32 exactly (v_cvt_pk_f32_fp8) and multiplied by its power-of-two scale (exact),
 // so the bf16 operand equals the format's value.
 #include <stdlib.h>
@@ -431,6 +430,8 @@ constexpr int DCPR = DBK / 8;          // 16-byte chunks per row
 constexpr int DRPI = 64 / DCPR;        // rows one DMA instruction fills
 constexpr int DNS = 4;                 // stages in the ring
 __device__ __forceinline__ int dswz(int r) { return (r >> 2) & 3; }
+// 8-bit packed weight rows (32 bytes per stage): chunk swizzle of row r
+__device__ __forceinline__ int qswz(int r) { return (r >> 3) & 1; }
 #define KX_LDS(p) ((__attribute__((address_space(3))) void*)(p))
 // A workgroup barrier that the compiler may not move memory accesses across.
 #define KX_BARRIER() asm volatile("s_barrier" ::: "memory")
@@ -500,104 +501,6 @@ __device__ __forceinline__ void epilogue_store4(float v[4], int m, int n, int N,
   }
 }
 
-// Dequantization of one stage's packed rows into the bf16 tile the MFMA loop reads: thread t owns
-// weight row t of the tile (32 k values). The packed words and the scale / bias pairs are read
-// from LDS one k16 step before the arithmetic, so their latency hides under MFMAs. The weight is
-// bf16(fp32(scale) * q + fp32(bias)): scale * q is exact in fp32 (8-bit scale significand times
-// q < 256), so the fma rounds once, like the separate multiply and add.
-template <int QB>
-struct DqIn {
-  uint32_t words[DBK * qbits<QB>() / 32];
-  uint32_t sw, bw;  // scale and bias pairs of the stage's two-group window (mxfp8: four scale bytes)
-};
-// TL: scale / bias pairs interleaved per row (s0 s1 b0 b1, the tiled layout); otherwise the
-// scale pairs of all rows then the bias pairs.
-template <int QB, bool TL>
-__device__ __forceinline__ void dequant_load(const uint8_t* wq, const uint8_t* sb, int bn, int r, DqIn<QB>& in) {
-  constexpr int QROW = DBK * qbits<QB>() / 8;  // packed bytes per row per stage
-#pragma unroll
-  for (int c = 0; c < QROW / 16; ++c) {
-    const uint4 v = *reinterpret_cast<const uint4*>(wq + r * QROW + 16 * c);
-    in.words[4 * c] = v.x; in.words[4 * c + 1] = v.y; in.words[4 * c + 2] = v.z; in.words[4 * c + 3] = v.w;
-  }
-  if constexpr (QB == QMX8) {
-    in.sw = *reinterpret_cast<const uint32_t*>(sb + 4 * r);
-    in.bw = 0u;
-  } else if (TL) {
-    const uint2 p = *reinterpret_cast<const uint2*>(sb + 8 * r);
-    in.sw = p.x;
-    in.bw = p.y;
-  } else {
-    in.sw = *reinterpret_cast<const uint32_t*>(sb + 4 * r);
-    in.bw = *reinterpret_cast<const uint32_t*>(sb + 4 * bn + 4 * r);
-  }
-}
-// Half a 16-byte chunk of the dequantized row (h = 2c + half: k = 8c + 4 half .. +3); the caller
-// spreads the eight pieces between MFMAs. `out` collects the chunk; piece 2c+1 stores it.
-template <int QB>
-__device__ __forceinline__ void dequant_piece(const DqIn<QB>& in, int h, float sc, float bi, uint32_t (&out)[2],
-                                              int r, uint8_t* wd) {
-  const int c = h >> 1, hf = h & 1;
-  float v[4];
-  if constexpr (QB == QMX8) {
-    const uint2 q = mx8_quad(in.words[2 * c + hf], sc);
-    if (hf == 0) {
-      out[0] = q.x;
-      out[1] = q.y;
-    } else {
-      *reinterpret_cast<uint4*>(wd + r * DROW + ((c ^ dswz(r)) << 4)) = make_uint4(out[0], out[1], q.x, q.y);
-    }
-    return;
-  }
-  if (QB == 4) {
-    // nibbles 4hf .. 4hf+3 of word c: even ones in the low nibbles of bytes 2hf, 2hf+1
-    const uint32_t lo = in.words[c] & 0x0F0F0F0Fu, hi = (in.words[c] >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      v[2 * j] = fmaf(sc, (float)((lo >> (8 * (2 * hf + j))) & 255u), bi);
-      v[2 * j + 1] = fmaf(sc, (float)((hi >> (8 * (2 * hf + j))) & 255u), bi);
-    }
-  } else {
-    const uint32_t w = in.words[2 * c + hf];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = fmaf(sc, (float)((w >> (8 * j)) & 255u), bi);
-  }
-  const uint32_t p0 = pack2(v[0], v[1]), p1 = pack2(v[2], v[3]);
-  if (hf == 0) {
-    out[0] = p0;
-    out[1] = p1;
-  } else {
-    *reinterpret_cast<uint4*>(wd + r * DROW + ((c ^ dswz(r)) << 4)) = make_uint4(out[0], out[1], p0, p1);
-  }
-}
-// Scale and bias of K stage kt within the loaded window: affine, group kt / 2 of the pair
-// (64-wide groups); mxfp8, scale byte kt % 4 of the word (32-wide groups).
-template <int QB>
-__device__ __forceinline__ void dequant_scale(const DqIn<QB>& in, int kt, float& sc, float& bi) {
-  if constexpr (QB == QMX8) {
-    sc = e8m0_f32((in.sw >> (8 * (kt & 3))) & 255u);
-    bi = 0.0f;
-  } else {
-    const bool half = (kt >> 1) & 1;
-    sc = half ? hi_f(in.sw) : lo_f(in.sw);
-    bi = half ? hi_f(in.bw) : lo_f(in.bw);
-  }
-}
-template <int QB>
-__device__ __forceinline__ void dequant_store(const DqIn<QB>& in, int r, int kt, uint8_t* wd) {
-  float sc, bi;
-  dequant_scale<QB>(in, kt, sc, bi);
-  uint32_t out[2];
-#pragma unroll
-  for (int h = 0; h < 2 * DCPR; ++h) dequant_piece<QB>(in, h, sc, bi, out, r, wd);
-}
-
-// QB = 0: bf16 weights, DMA'd like the activations. QB = 4 / 8: affine quantized weights; each
-// stage DMAs the packed words and the scale / bias pairs of its 64-wide group (QMX8: the word of
-// four E8M0 scale bytes holding its 32-wide group), and the workgroup
-// dequantizes stage kt+1 into one of two bf16 tiles while the MFMAs consume stage kt. TL: the
-// weights are in the tiled layout (one contiguous block per 256-row tile and stage, see
-// kx_qweight_tile_affine), else in the reference layout (one 16- or 4-byte piece per row).
 // One full-tile epilogue row piece: bias + activation (+ gated residual), then the store of 4
 // consecutive columns. Values by value so that nothing of the caller's frame is addressed.
 template <int GMODE, bool OUTF32, typename ResidT>
@@ -630,6 +533,13 @@ __device__ __forceinline__ void epi_row4(float4 a4, ResidT res, float b0, float 
   }
 }
 
+// QB = 0: bf16 weights, DMA'd like the activations. QB = 4 / 8 (affine) and QMX8 (mxfp8): each
+// stage DMAs the packed weight bytes and the scale (/ bias) words of its group, and every wave
+// dequantizes its own weight fragments in registers (bit-exact, the arithmetic of dequant8)
+// between the MFMAs of the previous k16 step: the stage's weights cross LDS once, packed, and no
+// bf16 copy of them is written. TL: the affine weights are in the tiled layout (one contiguous
+// block per 256-row tile and stage, see kx_qweight_tile_affine), else in the reference layout
+// (one 16- or 32-byte piece per row).
 template <int BM, int BN, int QB, bool TL, int GMODE, bool OUTF32>
 __global__ __launch_bounds__(256) void gemm_lds_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ W, int64_t ldw,
@@ -643,17 +553,16 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
   constexpr int PER = A_INST + W_INST;  // DMA instructions per wave per stage
   constexpr int W_BYTES = QB ? BN * QROW + BN * SB_BYTES : BN * DROW;
   constexpr int STAGE = BM * DROW + W_BYTES;
-  constexpr int WD_OFF = DNS * STAGE;    // two dequantized bf16 weight tiles follow the ring
-  constexpr int RING = QB ? WD_OFF + 2 * BN * DROW : DNS * STAGE;
+  constexpr int RING = DNS * STAGE;
   constexpr int WT_M = BM / 2, WT_N = BN / 2;
   constexpr int MB = WT_M / 32, NB = WT_N / 32;
   constexpr int KS = DBK / 16;
+  static_assert(KS == 2, "two k16 steps per stage");
   constexpr int DPS = (PER + KS - 1) / KS;  // DMA instructions per k16 step
   // At the wait in the last k16 step, stages kt+2 .. kt+NS-2 and the DMA of this iteration's
-  // earlier steps may stay in flight: stage kt+1 is then complete. The quantized path dequantizes
-  // one stage ahead, so there stage kt+2 must be complete too.
+  // earlier steps may stay in flight: stage kt+1 is then complete.
   constexpr int NBEFORE = (KS - 1) * DPS < PER ? (KS - 1) * DPS : PER;
-  constexpr int WAITN = (DNS - (QB ? 4 : 3)) * PER + NBEFORE;
+  constexpr int WAITN = (DNS - 3) * PER + NBEFORE;
   constexpr int PITCH = WT_N / 2 + 4;  // staged epilogue row, floats
   constexpr int EP_BYTES = 4 * WT_M * PITCH * 4;
   constexpr int SMEM = RING > EP_BYTES ? RING : EP_BYTES;
@@ -709,21 +618,28 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
     w_base = reinterpret_cast<const char*>(W + (int64_t)n0 * ldw);
   } else if constexpr (TL) {
     // tiled: the stage's packed words (BN * QROW bytes) and scale / bias pairs (BN * 8 bytes of
-    // its 128-wide window) are contiguous blocks
+    // its 128-wide window) are contiguous blocks (8-bit rows: chunk swizzle as below)
 #pragma unroll
-    for (int i = 0; i < WQ_INST; ++i) vo[A_INST + i] = (uint32_t)((wave * WQ_INST + i) * 1024 + lane * 16);
+    for (int i = 0; i < WQ_INST; ++i) {
+      const int r = (wave * WQ_INST + i) * (1024 / QROW) + lane / (QROW / 16);
+      const int chunk = QROW == 32 ? (lane & 1) ^ qswz(r) : 0;
+      vo[A_INST + i] = (uint32_t)(r * QROW + chunk * 16);
+    }
 #pragma unroll
     for (int i = 0; i < SB_INST; ++i) vo[A_INST + WQ_INST + i] = (uint32_t)((wave * SB_INST + i) * 256 + lane * 4);
     const int64_t nb = n0 / BN;
     w_base = reinterpret_cast<const char*>(qw.words) + nb * (K / DBK) * (int64_t)(BN * QROW);
     s_base = reinterpret_cast<const char*>(qw.scales) + nb * (K / 128) * (int64_t)(BN * 8);
   } else {
-    // packed words: RPW rows per instruction, QROW / 16 chunks per row
+    // packed words: RPW rows per instruction, QROW / 16 chunks per row; an 8-bit row's two
+    // chunks trade places when (r >> 3) & 1, so that the 16-byte fragment reads of 16 rows
+    // cover every bank once
     constexpr int RPW = 1024 / QROW;
 #pragma unroll
     for (int i = 0; i < WQ_INST; ++i) {
       const int r = (wave * WQ_INST + i) * RPW + lane / (QROW / 16);
-      vo[A_INST + i] = (uint32_t)((int64_t)(min(n0 + r, N - 1) - n0) * qrow_bytes + (lane % (QROW / 16)) * 16);
+      const int chunk = QROW == 32 ? (lane & 1) ^ qswz(r) : 0;
+      vo[A_INST + i] = (uint32_t)((int64_t)(min(n0 + r, N - 1) - n0) * qrow_bytes + chunk * 16);
     }
     // scale / bias pairs (mxfp8: scale-byte quads): 64 rows x 4 bytes per instruction
     const int64_t sb_row = QB == QMX8 ? K / 32 : groups * 2;  // bytes per row of the scale array
@@ -771,12 +687,14 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
     }
   };
 
-  // fragment byte offsets, per k16 step (the MFMA A operand is the weight tile): activation rows
-  // within a stage; weight rows within the stage (bf16) or within a dequantized tile
+  // fragment byte offsets, per k16 step (the MFMA A operand is the weight tile). Dense: step s
+  // of lane half h covers k = 16 s + 8 h .. + 7 of the stage. Quantized: k = 16 h + 8 s .. + 7
+  // (the same permutation of the sum on both operands), so that a lane's packed weight bytes of
+  // both steps are contiguous and come in one read per stage.
   int a_off[KS][MB], w_off[KS][NB];
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
-    const int c = 2 * s + lhalf;
+    const int c = QB ? 2 * lhalf + s : 2 * s + lhalf;
 #pragma unroll
     for (int j = 0; j < MB; ++j) {
       const int r = wm * WT_M + j * 32 + lrow;
@@ -785,27 +703,16 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
       const int r = wn * WT_N + i * 32 + lrow;
-      w_off[s][i] = (QB ? 0 : BM * DROW) + r * DROW + ((c ^ dswz(r)) << 4);
+      w_off[s][i] = BM * DROW + r * DROW + ((c ^ dswz(r)) << 4);
     }
   }
-  auto load_frags = [&](const uint8_t* abuf, const uint8_t* wbuf, int s, bf16x8* af, bf16x8* wf) {
+  auto load_frags = [&](const uint8_t* buf, int s, bf16x8* af, bf16x8* wf) {
 #pragma unroll
-    for (int j = 0; j < MB; ++j) af[j] = *reinterpret_cast<const bf16x8*>(abuf + a_off[s][j]);
+    for (int j = 0; j < MB; ++j) af[j] = *reinterpret_cast<const bf16x8*>(buf + a_off[s][j]);
+    if constexpr (QB == 0) {
 #pragma unroll
-    for (int i = 0; i < NB; ++i) wf[i] = *reinterpret_cast<const bf16x8*>(wbuf + w_off[s][i]);
-  };
-  auto wtile = [&](const uint8_t* stage_buf, int kt) -> const uint8_t* {
-    return QB ? smem + WD_OFF + (kt & 1) * BN * DROW : stage_buf;
-  };
-  DqIn<QB ? QB : 4> dq;
-  auto dequant_in = [&](int stage_i) {  // packed inputs of a stage into registers
-    if constexpr (QB != 0) {
-      const uint8_t* buf = smem + stage_i * STAGE + BM * DROW;
-      dequant_load<QB, TL>(buf, buf + BN * QROW, BN, tid, dq);
+      for (int i = 0; i < NB; ++i) wf[i] = *reinterpret_cast<const bf16x8*>(buf + w_off[s][i]);
     }
-  };
-  auto dequant_out = [&](int kt) {  // stage kt's bf16 weights into its tile
-    if constexpr (QB != 0) dequant_store<QB>(dq, tid, kt, smem + WD_OFF + (kt & 1) * BN * DROW);
   };
 
   f32x16 acc[NB][MB];
@@ -821,110 +728,227 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
   for (int p = 0; p < DNS - 1; ++p)
 #pragma unroll
     for (int i = 0; i < PER; ++i) dma(i, smem + p * STAGE, min(p, stages - 1) * DBK);
-  if constexpr (QB == 0) {
-    wait_vmcnt<(DNS - 2) * PER>();
-    KX_BARRIER();
-  } else {
-    // stages 0 and 1 landed; stage 0 dequantized and visible
-    wait_vmcnt<(DNS - 3) * PER>();
-    KX_BARRIER();
-    dequant_in(0);
-    dequant_out(0);
-    dequant_in(1);
-    wait_lgkmcnt0();
-    KX_BARRIER();
-  }
+  wait_vmcnt<(DNS - 2) * PER>();
+  KX_BARRIER();
   bf16x8 fa[2][MB], fw[2][NB];
-  load_frags(smem, wtile(smem, 0), 0, fa[0], fw[0]);
   int cur_i = 0;
-  for (int kt = 0; kt < stages; ++kt) {
-    const uint8_t* cur = smem + cur_i * STAGE;
-    const int nxt_i = cur_i + 1 == DNS ? 0 : cur_i + 1;
-    // stage kt+NS-1 goes into the buffer stage kt-1 used; past the end the last stage is
-    // re-read into it, which keeps the loop free of branches and the vmcnt arithmetic uniform
-    uint8_t* iss = smem + (cur_i == 0 ? DNS - 1 : cur_i - 1) * STAGE;
-    const int k_iss = min(kt + DNS - 1, stages - 1) * DBK;
+  if constexpr (QB != 0) {
+    // ---- quantized mainloop: every wave dequantizes its own weight fragments in registers ----
+    // A lane's packed bytes of weight block i for the whole stage (both k16 steps of its row)
+    // and the row's scale (and bias) word; read once per stage, right after the stage's barrier.
+    using Raw = typename std::conditional<qbits<QB>() == 4, uint2, uint4>::type;
+    Raw raw[NB];
+    uint32_t rsw[NB], rbw[NB];
+    int wr_off[NB], ws_off[NB];
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const int b = s & 1;
+    for (int i = 0; i < NB; ++i) {
+      const int r = wn * WT_N + i * 32 + lrow;
+      wr_off[i] = BM * DROW + (QROW == 16 ? r * 16 + 8 * lhalf : r * 32 + ((lhalf ^ qswz(r)) << 4));
+      ws_off[i] = BM * DROW + BN * QROW + (TL && QB != QMX8 ? 8 * r : 4 * r);
+    }
+    // scale (and bias) of each block's rows for stage kt: affine, group kt / 2 of the pair (64-wide
+    // groups); mxfp8, scale byte kt % 4 of the word (32-wide groups)
+    float scl[NB], bia[NB];
+    auto stage_scales = [&](int kt) {
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        if constexpr (QB == QMX8) {
+          scl[i] = e8m0_f32((rsw[i] >> (8 * (kt & 3))) & 255u);
+          bia[i] = 0.0f;
+        } else {
+          const bool half = (kt >> 1) & 1;
+          scl[i] = half ? hi_f(rsw[i]) : lo_f(rsw[i]);
+          bia[i] = half ? hi_f(rbw[i]) : lo_f(rbw[i]);
+        }
+      }
+    };
+    // values 2p, 2p+1 of block i's fragment for k16 step s, as two bf16 (dequant8's arithmetic)
+    auto dq_pair = [&](int i, int s, int p) -> uint32_t {
+      if constexpr (QB == QMX8) {
+        const uint32_t w = (2 * s + (p >> 1)) == 0 ? raw[i].x : (2 * s + (p >> 1)) == 1 ? raw[i].y
+                           : (2 * s + (p >> 1)) == 2 ? raw[i].z : raw[i].w;
+        const f32x2 v = (p & 1) ? __builtin_amdgcn_cvt_pk_f32_fp8(w, true) : __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
+        return pack2(v.x * scl[i], v.y * scl[i]);
+      } else if constexpr (QB == 8) {
+        const uint32_t w = (2 * s + (p >> 1)) == 0 ? raw[i].x : (2 * s + (p >> 1)) == 1 ? raw[i].y
+                           : (2 * s + (p >> 1)) == 2 ? raw[i].z : raw[i].w;
+        const int b = 2 * (p & 1);
+        return pack2(fmaf(scl[i], (float)((w >> (8 * b)) & 255u), bia[i]),
+                     fmaf(scl[i], (float)((w >> (8 * b + 8)) & 255u), bia[i]));
+      } else {
+        // even nibbles in the low halves of the bytes of lo, odd ones in hi: each value is one
+        // byte conversion (v_cvt_f32_ubyte), the masks are shared by the word's four pairs
+        const uint32_t w = s ? raw[i].y : raw[i].x;
+        uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+        // the masked words opaque to the optimizer, which would otherwise fold the masks back
+        // into one bit-field extract per value
+        asm("" : "+v"(lo));
+        asm("" : "+v"(hi));
+        return pack2(fmaf(scl[i], (float)((lo >> (8 * p)) & 255u), bia[i]),
+                     fmaf(scl[i], (float)((hi >> (8 * p)) & 255u), bia[i]));
+      }
+    };
+    // the fragment under construction, four pairs
+    uint32_t part[NB][4];
+    auto dq_step = [&](int idx, int s) {  // pair idx of the step's NB * 4 pairs
+      const int i = idx >> 2, p = idx & 3;
+      part[i][p] = dq_pair(i, s, p);
+    };
+    auto dq_commit = [&](bf16x8* wf) {
+#pragma unroll
+      for (int i = 0; i < NB; ++i) wf[i] = __builtin_bit_cast(bf16x8, make_uint4(part[i][0], part[i][1], part[i][2], part[i][3]));
+    };
+    constexpr int NMF = NB * MB;
+    constexpr int NPAIR = NB * 4;
+    constexpr int SB_RD = QB == QMX8 || TL ? 1 : 2;  // scale (bias) reads per block
+    constexpr int NRD1 = MB + NB * (1 + SB_RD);      // LDS reads at a stage's start
+    constexpr int QSPLIT = 4;                         // MFMAs before the wait for those reads
+    static_assert(NMF > QSPLIT, "MFMAs per step");
+    // LDS read r of a stage's start: A fragments of its step 0, raw blocks, scale words
+    auto stage_read = [&](int r, const uint8_t* buf) {
+      if (r < MB) {
+        fa[0][r] = *reinterpret_cast<const bf16x8*>(buf + a_off[0][r]);
+      } else if (r < MB + NB) {
+        raw[r - MB] = *reinterpret_cast<const Raw*>(buf + wr_off[r - MB]);
+      } else {
+        const int q = r - MB - NB, i = q % NB;
+        if constexpr (QB == QMX8) {
+          rsw[i] = *reinterpret_cast<const uint32_t*>(buf + ws_off[i]);
+        } else if constexpr (TL) {
+          const uint2 pr = *reinterpret_cast<const uint2*>(buf + ws_off[i]);
+          rsw[i] = pr.x;
+          rbw[i] = pr.y;
+        } else if (q < NB) {
+          rsw[i] = *reinterpret_cast<const uint32_t*>(buf + ws_off[i]);
+        } else {
+          rbw[i] = *reinterpret_cast<const uint32_t*>(buf + ws_off[i] + 4 * BN);
+        }
+      }
+    };
+
+#pragma unroll
+    for (int r = 0; r < NRD1; ++r) stage_read(r, smem);
+    wait_lgkmcnt0();
+    stage_scales(0);
+#pragma unroll
+    for (int q = 0; q < NPAIR; ++q) dq_step(q, 0);
+    dq_commit(fw[0]);
+    for (int kt = 0; kt < stages; ++kt) {
+      const uint8_t* cur = smem + cur_i * STAGE;
+      const int nxt_i = cur_i + 1 == DNS ? 0 : cur_i + 1;
+      const uint8_t* nxt = smem + nxt_i * STAGE;
+      uint8_t* iss = smem + (cur_i == 0 ? DNS - 1 : cur_i - 1) * STAGE;
+      const int k_iss = min(kt + DNS - 1, stages - 1) * DBK;
+      // step 0, in a fixed order: each MFMA, then its share of the pairs of step 1's weight
+      // fragments (the arithmetic runs while the MFMA executes); the A fragments of step 1 and
+      // the first DMA issues ride along the first MFMAs
       __builtin_amdgcn_sched_barrier(0);
       wait_lgkmcnt0();
       __builtin_amdgcn_sched_barrier(0);
-      if (QB != 0 && s == 0) {
-        // quantized first step, in a fixed order: the next step's fragment reads and this step's
-        // DMA, then the MFMAs with one piece of the next stage's dequantization after every
-        // other MFMA (the pieces' arithmetic runs while the MFMAs execute)
-        load_frags(cur, wtile(cur, kt), 1, fa[1], fw[1]);
+#pragma unroll
+      for (int q = 0; q < NMF; ++q) {
+        const int i = q / MB, j = q % MB;
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fw[0][i], fa[0][j], acc[i][j], 0, 0, 0);
+        if (q < MB) fa[1][q] = *reinterpret_cast<const bf16x8*>(cur + a_off[1][q]);
+        if (q < DPS && q < PER) dma(q, iss, k_iss);
+#pragma unroll
+        for (int idx = q * NPAIR / NMF; idx < (q + 1) * NPAIR / NMF; ++idx) dq_step(idx, 1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      dq_commit(fw[1]);
+      // step 1: stage kt+1 has landed for this wave and its reads of stage kt-1's buffer ended
+      // one step ago; after the barrier this holds for every wave. The stage-start reads of stage
+      // kt+1 and the remaining DMA issues ride along the first QSPLIT MFMAs; after the wait for
+      // those reads, each further MFMA is followed by pairs of stage kt+1's step-0 fragments.
+      __builtin_amdgcn_sched_barrier(0);
+      wait_lgkmcnt0();
+      wait_vmcnt<WAITN>();
+      KX_BARRIER();
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int q = 0; q < QSPLIT; ++q) {
+        const int i = q / MB, j = q % MB;
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fw[1][i], fa[1][j], acc[i][j], 0, 0, 0);
+#pragma unroll
+        for (int r = q * NRD1 / QSPLIT; r < (q + 1) * NRD1 / QSPLIT; ++r) stage_read(r, nxt);
+#pragma unroll
+        for (int d = DPS + q * (PER - DPS) / QSPLIT; d < DPS + (q + 1) * (PER - DPS) / QSPLIT; ++d)
+          dma(d, iss, k_iss);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      wait_lgkmcnt0();
+      stage_scales(kt + 1);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int q = QSPLIT; q < NMF; ++q) {
+        const int i = q / MB, j = q % MB;
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fw[1][i], fa[1][j], acc[i][j], 0, 0, 0);
+#pragma unroll
+        for (int idx = (q - QSPLIT) * NPAIR / (NMF - QSPLIT); idx < (q - QSPLIT + 1) * NPAIR / (NMF - QSPLIT); ++idx)
+          dq_step(idx, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      dq_commit(fw[0]);
+      cur_i = nxt_i;
+    }
+  } else {
+    load_frags(smem, 0, fa[0], fw[0]);
+    for (int kt = 0; kt < stages; ++kt) {
+      const uint8_t* cur = smem + cur_i * STAGE;
+      const int nxt_i = cur_i + 1 == DNS ? 0 : cur_i + 1;
+      // stage kt+NS-1 goes into the buffer stage kt-1 used; past the end the last stage is
+      // re-read into it, which keeps the loop free of branches and the vmcnt arithmetic uniform
+      uint8_t* iss = smem + (cur_i == 0 ? DNS - 1 : cur_i - 1) * STAGE;
+      const int k_iss = min(kt + DNS - 1, stages - 1) * DBK;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const int b = s & 1;
+        __builtin_amdgcn_sched_barrier(0);
+        wait_lgkmcnt0();
+        __builtin_amdgcn_sched_barrier(0);
+        if (s + 1 < KS) {
+          load_frags(cur, s + 1, fa[b ^ 1], fw[b ^ 1]);
+        } else {
+          // stage kt+1 has landed for this wave and its reads of cur are done; after the barrier
+          // this holds for every wave, and nobody reads cur again before it is refilled
+          wait_vmcnt<WAITN>();
+          KX_BARRIER();
+          load_frags(smem + nxt_i * STAGE, 0, fa[b ^ 1], fw[b ^ 1]);
+        }
 #pragma unroll
         for (int d = 0; d < DPS; ++d)
-          if (d < PER) dma(d, iss, k_iss);
-        const int kq = kt + 1;
-        float sc, bi;
-        dequant_scale<QB ? QB : 4>(dq, kq, sc, bi);
-        uint8_t* wd = smem + WD_OFF + (kq & 1) * BN * DROW;
-        uint32_t piece[2];
-        __builtin_amdgcn_sched_barrier(0);
+          if (s * DPS + d < PER) dma(s * DPS + d, iss, k_iss);
 #pragma unroll
-        for (int q = 0; q < NB * MB; ++q) {
-          const int i = q / MB, j = q % MB;
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fw[0][i], fa[0][j], acc[i][j], 0, 0, 0);
-          if constexpr (QB != 0) {
-            // pieces [q P / Q, (q + 1) P / Q): all P = 2 * DCPR pieces over the Q MFMAs
-            constexpr int P = 2 * DCPR, Q = NB * MB;
+        for (int i = 0; i < NB; ++i)
 #pragma unroll
-            for (int h = q * P / Q; h < (q + 1) * P / Q; ++h) dequant_piece<QB>(dq, h, sc, bi, piece, tid, wd);
-          }
-          __builtin_amdgcn_sched_barrier(0);
+          for (int j = 0; j < MB; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fw[b][i], fa[b][j], acc[i][j], 0, 0, 0);
+        // the next step's fragment reads one per MFMA (a burst of them fills the LDS command
+        // queue and stalls the wave before its MFMAs), then the DMA issues between the
+        // remaining MFMAs
+        constexpr int NRD = MB + NB, NMF = NB * MB;
+        constexpr int PAIRS = NRD < NMF ? NRD : NMF;
+        constexpr int DMF = DPS < NMF - PAIRS ? DPS : NMF - PAIRS;
+#pragma unroll
+        for (int q = 0; q < PAIRS; ++q) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         }
-        continue;
-      }
-      if (s + 1 < KS) {
-        load_frags(cur, wtile(cur, kt), s + 1, fa[b ^ 1], fw[b ^ 1]);
-      } else {
-        // stage kt+1 (kt+2 when quantized) has landed for this wave and its reads of cur are
-        // done; after the barrier this holds for every wave, and nobody reads cur again before
-        // it is refilled
-        wait_vmcnt<WAITN>();
-        KX_BARRIER();
-        load_frags(smem + nxt_i * STAGE, wtile(smem + nxt_i * STAGE, kt + 1), 0, fa[b ^ 1], fw[b ^ 1]);
-        // packed inputs of stage kt+2 (landed before this barrier; its buffer is refilled only
-        // after stage kt+2 has been dequantized)
-        int i2 = nxt_i + 1;
-        i2 = i2 == DNS ? 0 : i2;
-        dequant_in(i2);
-      }
+        if constexpr (NRD > PAIRS) __builtin_amdgcn_sched_group_barrier(0x100, NRD - PAIRS, 0);
 #pragma unroll
-      for (int d = 0; d < DPS; ++d)
-        if (s * DPS + d < PER) dma(s * DPS + d, iss, k_iss);
-#pragma unroll
-      for (int i = 0; i < NB; ++i)
-#pragma unroll
-        for (int j = 0; j < MB; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fw[b][i], fa[b][j], acc[i][j], 0, 0, 0);
-      // the next step's fragment reads one per MFMA (a burst of them fills the LDS command queue
-      // and stalls the wave before its MFMAs), then the DMA issues between the remaining MFMAs
-      constexpr int NRD = MB + NB, NMF = NB * MB;
-      constexpr int PAIRS = NRD < NMF ? NRD : NMF;
-      constexpr int DMF = DPS < NMF - PAIRS ? DPS : NMF - PAIRS;
-#pragma unroll
-      for (int q = 0; q < PAIRS; ++q) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        for (int q = 0; q < DMF; ++q) {
+          __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+        if constexpr (DPS > DMF) {
+          __builtin_amdgcn_sched_group_barrier(0x002, DPS - DMF, 0);
+          __builtin_amdgcn_sched_group_barrier(0x020, DPS - DMF, 0);
+        }
+        if constexpr (NMF > PAIRS + DMF) __builtin_amdgcn_sched_group_barrier(0x008, NMF - PAIRS - DMF, 0);
       }
-      if constexpr (NRD > PAIRS) __builtin_amdgcn_sched_group_barrier(0x100, NRD - PAIRS, 0);
-#pragma unroll
-      for (int q = 0; q < DMF; ++q) {
-        __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      }
-      if constexpr (DPS > DMF) {
-        __builtin_amdgcn_sched_group_barrier(0x002, DPS - DMF, 0);
-        __builtin_amdgcn_sched_group_barrier(0x020, DPS - DMF, 0);
-      }
-      if constexpr (NMF > PAIRS + DMF) __builtin_amdgcn_sched_group_barrier(0x008, NMF - PAIRS - DMF, 0);
+      cur_i = nxt_i;
     }
-    cur_i = nxt_i;
   }
   wait_vmcnt<0>();
 

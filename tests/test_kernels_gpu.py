@@ -373,23 +373,27 @@ def test_linear_fp32_residual_stream(device, resid_dtype, out_dtype, bits):
     od = torch.float32 if out_dtype == "f32" else torch.bfloat16
     xd = _bf(x.reshape(2, 70, k), device)
     if bits is None:
-        out = mpp_linear.fused_linear(xd, _bf(w, device), _bf(b, device), residual=resid_d,
-                                      gate=_f32(gate, device), out_dtype=od)
+        outs = [mpp_linear.fused_linear(xd, _bf(w, device), _bf(b, device), residual=resid_d,
+                                        gate=_f32(gate, device), out_dtype=od)]
         weight = w
     else:
         words, scales, biases = oracle.quantize_affine(w, 64, bits)
         layer = quantized.QuantizedLinear(
             torch.from_numpy(words.view(np.int32)).to(device), _bf(scales, device), _bf(biases, device),
             _bf(b, device), group_size=64, bits=bits)
-        out = layer(xd, residual=resid_d, gate=_f32(gate, device), out_dtype=od)
+        # the layer (dequantize, dense GEMM) and the in-mainloop kernel
+        outs = [layer(xd, residual=resid_d, gate=_f32(gate, device), out_dtype=od),
+                quantized.quantized_matmul(xd, layer.weight, layer.scales, layer.biases, group_size=64, bits=bits,
+                                           bias=layer.bias, residual=resid_d, gate=_f32(gate, device), out_dtype=od)]
         weight = oracle.dequantize_affine(words, scales, biases, group_size=64, bits=bits)
-    assert out.dtype == od
-    got = _np(out)
     ref = oracle.gated_residual(resid, oracle.linear(x, weight, b).reshape(2, 70, n), gate)
-    if out_dtype == "f32":
-        assert np.all(np.abs(got - ref) <= 1e-5 * np.abs(ref) + 2e-5 * np.abs(ref).max())
-    else:
-        assert _gemm_close(got, ref)
+    for out in outs:
+        assert out.dtype == od
+        got = _np(out)
+        if out_dtype == "f32":
+            assert np.all(np.abs(got - ref) <= 1e-5 * np.abs(ref) + 2e-5 * np.abs(ref).max())
+        else:
+            assert _gemm_close(got, ref)
 
 
 @pytest.mark.parametrize("dim", [1024, 4096, 1000])
@@ -525,12 +529,14 @@ def test_quantized_linear_matches_oracle(device, monkeypatch, tile, bits, m, n, 
     words, scales, biases = oracle.quantize_affine(w, 64, bits)
     layer = quantized.QuantizedLinear(torch.from_numpy(words.view(np.int32)).to(device), _bf(scales, device),
                                       _bf(biases, device), _bf(b, device), group_size=64, bits=bits)
-    got = _np(layer(_bf(x, device)))
     ref = oracle.quantized_linear(x, words, scales, biases, b, group_size=64, bits=bits)
+    # the in-mainloop kernels (KX355_GEMM_TILE selects the register-staged kernel's tile)
+    got = _np(quantized.quantized_matmul(_bf(x, device), layer.weight, layer.scales, layer.biases, group_size=64,
+                                         bits=bits, bias=layer.bias))
     assert _gemm_close(got, ref)
-    # the dequantized weight through the dense kernel gives the same product
-    dense = _np(mpp_linear.linear(_bf(x, device), quantized.dequantize(layer.weight, layer.scales, layer.biases,
-                                                                       bits=bits), _bf(b, device), transposed=True))
+    # the layer: the exactly dequantized weight through the dense kernel
+    dense = _np(layer(_bf(x, device)))
+    assert _gemm_close(dense, ref)
     assert max_abs(got, dense) <= 2.0**-7 * np.abs(dense).max()
 
 
@@ -540,29 +546,36 @@ def test_quantized_linear_matches_oracle(device, monkeypatch, tile, bits, m, n, 
 @pytest.mark.parametrize("epilogue", ["bias", "gated_f32"])
 @pytest.mark.parametrize("layout", ["tiled", "reference"])
 def test_quantized_linear_dequantizes_in_lds(device, monkeypatch, tile, bits, m, n, k, epilogue, layout):
-    """The direct-to-LDS quantized kernel (packed words and scale / bias pairs DMA'd per stage,
-    dequantized once per stage into a bf16 tile) at both of its tiles (256x256, 192x256), on full
-    and ragged tiles: equal to the dense kernel on the exactly dequantized weight (the dequant is
-    bit-exact, so the two differ only in fp32 summation order)."""
+    """The direct-to-LDS quantized kernel (packed words and scale / bias words DMA'd per stage,
+    each wave dequantizing its own weight fragments in registers) at both of its tiles (256x256,
+    192x256), on full and ragged tiles, on the tiled and the reference layout: equal to the oracle
+    up to fp32 summation order (the dequantization is bit-exact)."""
     monkeypatch.setenv("KX355_GEMM_LDS_TILE", tile)
     r = _rng(m + n + k + bits)
     x = oracle.to_bf16((r.standard_normal((m, k)) * 0.5).astype(F32))
     w = oracle.to_bf16((r.standard_normal((n, k)) * 0.02).astype(F32))
     b = oracle.to_bf16((r.standard_normal(n) * 0.02).astype(F32))
     words, scales, biases = oracle.quantize_affine(w, 64, bits)
-    layer = quantized.QuantizedLinear(torch.from_numpy(words.view(np.int32)).to(device), _bf(scales, device),
-                                      _bf(biases, device), _bf(b, device), group_size=64, bits=bits)
-    assert layer._tiled is not None
-    if layout == "reference":  # the C ABI on the reference layout (packed rows read in place)
-        layer._tiled = None
+    wq, sd, bd, bias = torch.from_numpy(words.view(np.int32)).to(device), _bf(scales, device), _bf(biases, device), _bf(b, device)
+    tiled = quantized.tile_weights(wq, sd, bd, bits=bits) if layout == "tiled" else None
+
+    def call(**kw):
+        if tiled is None:  # the C ABI on the reference layout (packed rows read in place)
+            return quantized.quantized_matmul(_bf(x, device), wq, sd, bd, group_size=64, bits=bits, bias=bias, **kw)
+        out = torch.empty((m, n), device=device, dtype=kw.get("out_dtype") or torch.bfloat16)
+        flags = _lib.EPI_BIAS | (_lib.EPI_GATED_RESIDUAL if "residual" in kw else 0)  # dtype flags: the launcher
+        _lib.launch_qgemm_tiled(_bf(x, device), tiled[0], tiled[1], out, n=n, k=k, bits=bits, bias=bias, flags=flags,
+                                resid=kw.get("residual"), gate=kw.get("gate"))
+        return out
+
     ref = oracle.quantized_linear(x, words, scales, biases, b, group_size=64, bits=bits)
     if epilogue == "bias":
-        got = _np(layer(_bf(x, device)))
+        got = _np(call())
         assert _gemm_close(got, ref)
     else:
         resid = r.standard_normal((m, n)).astype(F32)
         gate = r.standard_normal(n).astype(F32)
-        got = _np(layer(_bf(x, device), residual=_f32(resid, device), gate=_f32(gate, device), out_dtype=torch.float32))
+        got = _np(call(residual=_f32(resid, device), gate=_f32(gate, device), out_dtype=torch.float32))
         full = resid + gate * ref
         assert np.all(np.abs(got - full) <= 1e-5 * np.abs(full) + 2e-5 * np.abs(full).max())
 
@@ -671,21 +684,26 @@ def test_mxfp8_linear_matches_oracle(device, monkeypatch, tile, m, n, k, epilogu
     layer = quantized.QuantizedLinear(torch.from_numpy(words.view(np.int32)).to(device), torch.from_numpy(scales).to(device),
                                       None, _bf(b, device), mode="mxfp8")
     assert (layer.group_size, layer.bits) == (32, 8)
-    if n <= 64:
-        layer._dense = None  # the skinny kernel itself, not the layer's dequantized copy
     ref = oracle.mxfp8_linear(x, words, scales, b)
+
+    def in_loop(**kw):  # the in-mainloop kernels, not the layer's dequantize-then-dense path
+        return quantized.quantized_matmul(_bf(x, device), layer.weight, layer.scales, None, group_size=32, bits=8,
+                                          mode="mxfp8", bias=layer.bias, **kw)
+
     if epilogue == "bias":
-        got = _np(layer(_bf(x, device)))
+        got = _np(in_loop())
         assert _gemm_close(got, ref)
-        dense = _np(mpp_linear.linear(_bf(x, device), quantized.dequantize_mxfp8(layer.weight, layer.scales),
-                                      _bf(b, device), transposed=True))
+        dense = _np(layer(_bf(x, device)))
+        assert _gemm_close(dense, ref)
         assert max_abs(got, dense) <= 2.0**-7 * np.abs(dense).max()
     else:
         resid = r.standard_normal((m, n)).astype(F32)
         gate = r.standard_normal(n).astype(F32)
-        got = _np(layer(_bf(x, device), residual=_f32(resid, device), gate=_f32(gate, device), out_dtype=torch.float32))
         full = resid + gate * ref
-        assert np.all(np.abs(got - full) <= 1e-5 * np.abs(full) + 2e-5 * np.abs(full).max())
+        for fn in (in_loop, layer):
+            kw = dict(residual=_f32(resid, device), gate=_f32(gate, device), out_dtype=torch.float32)
+            got = _np(fn(**kw) if fn is in_loop else fn(_bf(x, device), **kw))
+            assert np.all(np.abs(got - full) <= 1e-5 * np.abs(full) + 2e-5 * np.abs(full).max())
 
 
 def test_mxfp8_identity_linear_returns_its_input(device):
@@ -695,8 +713,8 @@ def test_mxfp8_identity_linear_returns_its_input(device):
     x = torch.ones((1, 32), dtype=torch.bfloat16, device=device)
     layer = quantized.QuantizedLinear.from_linear(eye.to(device), mode="mxfp8")
     assert torch.equal(layer(x), x)
-    layer._dense = None
-    assert torch.equal(layer(x), x)
+    in_loop = quantized.quantized_matmul(x, layer.weight, layer.scales, None, group_size=32, bits=8, mode="mxfp8")
+    assert torch.equal(in_loop, x)
     pre = quantized.PretransposedQuantizedLinear.from_linear(eye.to(device))
     assert torch.equal(pre(x), x)
     y = torch.randn((5, 32), device=device).to(torch.bfloat16)
