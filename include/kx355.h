@@ -47,7 +47,9 @@ enum {
   KX_EPI_ACT_SIGMOID = 4 << 4,  /* sigmoid(.) — Krea 2 output gate */
   KX_EPI_GATED_RESIDUAL = 1 << 8, /* c = resid + gate[col] * act(acc + bias) */
   KX_EPI_RESID_F32 = 1 << 9,      /* resid is fp32 (a residual stream carried in fp32) */
-  KX_EPI_OUT_F32 = 1 << 10        /* c is fp32 */
+  KX_EPI_OUT_F32 = 1 << 10,       /* c is fp32 */
+  KX_EPI_QK_NORM_ROPE = 1 << 11   /* per-head RMSNorm + pair RoPE on the Q and K columns
+                                     (kx_gemm_qknorm_rope_bf16 only) */
 };
 
 int kx_abi_version(void);
@@ -238,6 +240,27 @@ int kx_gemm_splitk_noalloc_bf16(const void* a, int64_t lda, const void* w, int64
                                 void* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int epilogue,
                                 const void* resid, int64_t ldr, const float* gate, int64_t gate_div,
                                 int64_t gate_stride, int splits, kx_stream_t stream);
+
+/*
+ * Projection with the attention's per-head Q/K RMSNorm and adjacent-pair RoPE in its epilogue:
+ * c = x w^T + bias (bf16 out), where columns [0, q_end) are query heads and [q_end, k_end) key
+ * heads of 128 (the rest, V and anything after, plain). For each row m and head: v = acc + bias
+ * rounded to bf16 (the value the plain projection would store), n = v * rsqrt(mean(v^2) + eps) *
+ * (w_norm[d] + weight_offset) in fp32, then
+ * out[2i] = n[2i] c[2i] - n[2i+1] s[2i], out[2i+1] = n[2i+1] c[2i+1] + n[2i] s[2i+1] (each product
+ * rounded in fp32 before the sum), one bf16 rounding. Tables: cos/sin + (m / table_rows) *
+ * table_bs + (m % table_rows) * table_ld + head * table_hs + d. Replaces the projection, QKNorm
+ * and rotate of FLUX.2 DoubleAttention / SingleAttention (kinomlx/models/flux2/transformer.py:68-75,
+ * 25-29, 88-164) and of Krea2Attention (kinomlx/models/krea2/transformer/model.py:29-46, 69-92,
+ * 134-185); the bf16 q/k round trip through HBM between the projection and the norm pass is
+ * removed. norm weights fp32 or bf16 (norm_dtype KX_F32 / KX_BF16);
+ * requires k % 32 == 0 and 16-byte aligned table rows.
+ */
+int kx_gemm_qknorm_rope_bf16(const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias, void* c,
+                             int64_t ldc, int64_t m, int64_t n, int64_t k, int64_t q_end, int64_t k_end,
+                             const void* norm_q, const void* norm_k, int norm_dtype, float eps, float weight_offset,
+                             const float* cos, const float* sin, int64_t table_ld, int64_t table_hs,
+                             int64_t table_rows, int64_t table_bs, kx_stream_t stream);
 
 /*
  * Group-wise affine int4/int8 weight-quantized linear, dequantized inside the MFMA mainloop:

@@ -92,6 +92,10 @@ SIGNATURES: dict[str, list] = {
         _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I, _P, _I64, _P, _I64, _I64, _P,
     ],
     "kx_table_add_f32": [_P, _I, _P, _I, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P],
+    "kx_gemm_qknorm_rope_bf16": [
+        _P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _I, _F, _F, _P, _P, _I64, _I64,
+        _I64, _I64, _P,
+    ],
     "kx_qgemm_mxfp8_bf16": [
         _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I, _P, _I64, _P, _I64, _I64, _P,
     ],
@@ -425,6 +429,32 @@ def launch_gemm(a, w, out, *, bias=None, flags: int = 0, resid=None, gate=None) 
     _call(
         "kx_gemm_bf16", _ptr(a), lda, _ptr(w), ldw, _ptr(bias), _ptr(out), ldc, m, n, k, flags,
         _ptr(resid), ldr, _ptr(gate), div, stride, _stream(),
+    )
+
+
+def launch_gemm_qknorm_rope(a, w, out, *, bias, q_end: int, k_end: int, norm_q, norm_k, eps: float,
+                            weight_offset: float, cos, sin, table_ld: int, table_hs: int, table_rows: int,
+                            table_bs: int) -> None:
+    """``out = a @ w.T + bias`` with per-head (128) RMSNorm + adjacent-pair RoPE applied to the
+    query columns ``[0, q_end)`` and key columns ``[q_end, k_end)`` in the GEMM epilogue."""
+    _check_gpu("gemm_qknorm_rope", a, w, out, bias, norm_q, norm_k, cos, sin)
+    m, k, lda = _rows(a, "qk-norm projection input")
+    n, kw, ldw = _rows(w, "qk-norm projection weight")
+    if kw != k:
+        raise ValueError(f"qk-norm projection: input width {k} does not match weight width {kw}")
+    _, nout, ldc = _rows(out, "qk-norm projection output")
+    if nout != n or out.dtype != torch.bfloat16:
+        raise ValueError("qk-norm projection: out must be bf16 rows of the weight's output width")
+    if norm_q.dtype != norm_k.dtype or norm_q.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("qk-norm projection: norm weights must both be fp32 or both bf16")
+    if norm_q.shape != (128,) or norm_k.shape != (128,) or not (norm_q.is_contiguous() and norm_k.is_contiguous()):
+        raise ValueError("qk-norm projection: norm weights must be contiguous (128,)")
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32:
+        raise ValueError("qk-norm projection: rotary tables must be fp32")
+    _call(
+        "kx_gemm_qknorm_rope_bf16", _ptr(a), lda, _ptr(w), ldw, _ptr(bias), _ptr(out), ldc, m, n, k, q_end, k_end,
+        _ptr(norm_q), _ptr(norm_k), KX_BF16 if norm_q.dtype == torch.bfloat16 else KX_F32, float(eps),
+        float(weight_offset), _ptr(cos), _ptr(sin), table_ld, table_hs, table_rows, table_bs, _stream(),
     )
 
 

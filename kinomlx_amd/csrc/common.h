@@ -79,6 +79,23 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Sum over the 16 lanes of a DPP row (lanes 16r .. 16r+15), the same in every lane of the row, by
+// VALU lane permutes instead of LDS round trips: swap neighbours, swap pairs (quad_perm [1,0,3,2]
+// and [2,3,0,1]), then the half-row mirror (lane i <- 7 - i) and the row mirror (i <- 15 - i), which
+// after the quad steps add the other quad and the other half-row. The adds are the ones of an
+// xor-1, 2, 4, 8 butterfly, in that order.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_mov<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp_mov<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v += dpp_mov<0x141>(v);  // row_half_mirror
+  v += dpp_mov<0x140>(v);  // row_mirror
+  return v;
+}
+
 // ---- host side ----------------------------------------------------------------------------------
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);

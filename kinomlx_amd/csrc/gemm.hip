@@ -21,6 +21,7 @@
 // so the bf16 operand equals the format's value.
 #include <stdlib.h>
 
+#include <algorithm>
 #include <mutex>
 #include <type_traits>
 
@@ -40,6 +41,20 @@ struct Epilogue {
   int64_t gate_div;
   int64_t gate_stride;
   int flags;
+  // KX_EPI_QK_NORM_ROPE: columns [0, q_end) are query heads and [q_end, k_end) key heads of 128;
+  // each row's head is RMS-normalized (weights nq / nk, fp32 or bf16, plus w_off; eps), then
+  // rotated in adjacent pairs by the row's cos / sin table row:
+  // tables + (m / t_rows) * t_bs + (m % t_rows) * t_ld + head * t_hs + d.
+  const void* nq;
+  const void* nk;
+  int n_bf16;
+  float n_eps, n_off;
+  int64_t q_end, k_end;
+  const float* cosp;
+  const float* sinp;
+  int64_t t_ld, t_hs, t_rows, t_bs;
+  uint32_t t_magic;  // m / t_rows = (umulhi(m, t_magic) + m) >> t_shift for m < 2^31
+  int t_shift;
 };
 
 struct QuantW {
@@ -540,7 +555,7 @@ __device__ __forceinline__ void epi_row4(float4 a4, ResidT res, float b0, float 
 // bf16 copy of them is written. TL: the affine weights are in the tiled layout (one contiguous
 // block per 256-row tile and stage, see kx_qweight_tile_affine), else in the reference layout
 // (one 16- or 32-byte piece per row).
-template <int BM, int BN, int QB, bool TL, int GMODE, bool OUTF32>
+template <int BM, int BN, int QB, bool TL, int GMODE, bool OUTF32, bool NR = false>
 __global__ __launch_bounds__(256) void gemm_lds_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ W, int64_t ldw,
     QuantW qw, void* __restrict__ C, int64_t ldc, int M, int N, int K, Epilogue epi) {
@@ -952,6 +967,27 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
   }
   wait_vmcnt<0>();
 
+  // ---- KX_EPI_QK_NORM_ROPE (NR): a wave's 128 columns are one head. A query or key head's wave
+  // stages its two halves twice: the first time its store-loop lanes sum the squares of bias +
+  // accumulator, rounded to bf16 as the projection's output would be, over their rows (each
+  // row's 128 columns spread over 16 lanes and both halves), the second time they apply the
+  // same rounded values' weighted RMSNorm and the adjacent-pair rotation in fp32
+  // (each product of the rotation rounded before the sum, as the standalone norm + RoPE kernel
+  // does) and store. Reading the accumulators only through the staging keeps them in place.
+  bool bias_done = false;  // a norm wave: its store loop adds the bias
+  int64_t nr_head = 0;
+  const void* nr_w = nullptr;
+  if constexpr (NR) {
+    static_assert(WT_N == 128 && GMODE == 0 && !OUTF32 && QB == 0, "one 128-wide head per wave");
+    const int64_t ncol0 = (int64_t)n0 + wn * WT_N;
+    if (ncol0 < epi.k_end) {
+      const bool isq = ncol0 < epi.q_end;
+      nr_w = isq ? epi.nq : epi.nk;
+      nr_head = isq ? ncol0 / 128 : (ncol0 - epi.q_end) / 128;
+      bias_done = true;
+    }
+  }
+
   // ---- epilogue: the accumulator lane holds row m = j*32 + lrow and columns 8g + 4 lhalf + e of
   // block i; staged per half of the wave's columns into a private LDS region.
   const bool vec_ok = (ldc % 4 == 0) && (!(epi.flags & KX_EPI_GATED_RESIDUAL) || epi.ldr % 4 == 0);
@@ -995,8 +1031,13 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
   _Pragma("unroll") for (int g = 0; g < 4; ++g)                                                   \
       *reinterpret_cast<float4*>(ep + (j * 32 + lrow) * PITCH + (ii) * 32 + 8 * g + 4 * lhalf) =  \
           make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+  float nr_ss[NR ? NROW : 1], nr_inv[NR ? NROW : 1];  // NR: per row of this lane
+#pragma unroll
+  for (int k = 0; k < (NR ? NROW : 1); ++k) nr_ss[k] = 0.0f;
+  const int passes = NR && bias_done ? 4 : 2;  // norm waves: two summing passes, then two storing
 #pragma unroll 1
-  for (int h = 0; h < 2; ++h) {
+  for (int hp = 0; hp < passes; ++hp) {
+    const int h = hp & 1;
     if constexpr (PREF) {
       if (h == 1 && full) { KX_PREFETCH_RESID(1, 0) }
     }
@@ -1010,7 +1051,111 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
 #undef KX_STAGE_BLOCK
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     const int n = n0 + wn * WT_N + h * HALF_N + 4 * q;
-    if (full) {
+    if (NR && bias_done && hp < 2) {
+      // summing pass: this lane's 4 columns of each of its rows
+      float b4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (has_bias) {
+        const uint2 bb = *reinterpret_cast<const uint2*>(epi.bias + n);
+        b4[0] = lo_f(bb.x); b4[1] = hi_f(bb.x); b4[2] = lo_f(bb.y); b4[3] = hi_f(bb.y);
+      }
+#pragma unroll
+      for (int k = 0; k < (NR ? NROW : 1); ++k) {
+        const float4 a4 = *reinterpret_cast<const float4*>(ep + (rr + k * RPI_EP) * PITCH + 4 * q);
+        const float v0 = bf2f(f2bf(a4.x + b4[0])), v1 = bf2f(f2bf(a4.y + b4[1]));
+        const float v2 = bf2f(f2bf(a4.z + b4[2])), v3 = bf2f(f2bf(a4.w + b4[3]));
+        nr_ss[k] = fmaf(v3, v3, fmaf(v2, v2, fmaf(v1, v1, fmaf(v0, v0, nr_ss[k]))));
+      }
+      if (hp == 1) {
+        // a row's 16 lanes (lane / LPR is the row slot) add their sums; then 1 / rms
+#pragma unroll
+        for (int k = 0; k < (NR ? NROW : 1); ++k) {
+          static_assert(!NR || LPR == 16, "a staged row's lanes are one DPP row");
+          nr_inv[k] = rsqrtf(row16_sum(nr_ss[k]) * (1.0f / 128.0f) + epi.n_eps);
+        }
+      }
+    } else if (NR && bias_done) {
+      // storing pass: bias, norm and rotation of 4 columns per lane of a query / key head (whole
+      // inside N)
+      const int d = h * HALF_N + 4 * q;  // column within the head; pairs (d, d+1), (d+2, d+3)
+      float b4[4] = {0.0f, 0.0f, 0.0f, 0.0f}, w4[4];
+      if (has_bias) {
+        const uint2 bb = *reinterpret_cast<const uint2*>(epi.bias + n);
+        b4[0] = lo_f(bb.x); b4[1] = hi_f(bb.x); b4[2] = lo_f(bb.y); b4[3] = hi_f(bb.y);
+      }
+      if (epi.n_bf16) {
+        const uint2 ww = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(nr_w) + d);
+        w4[0] = lo_f(ww.x); w4[1] = hi_f(ww.x); w4[2] = lo_f(ww.y); w4[3] = hi_f(ww.y);
+      } else {
+        const float4 ww = *reinterpret_cast<const float4*>(static_cast<const float*>(nr_w) + d);
+        w4[0] = ww.x; w4[1] = ww.y; w4[2] = ww.z; w4[3] = ww.w;
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w4[e] += epi.n_off;
+      // Rows go in groups of GR: the group's table rows (a row clamped to M - 1 past the end) are
+      // loaded together, so one memory latency covers GR rows. Table row of output row m: m / t_rows
+      // by the host's magic number (m < 2^31: umulhi(m, magic) + m fits 32 bits).
+      if constexpr (NR) {
+        constexpr int GR = 8, NG = NROW / GR;
+        static_assert(NROW % GR == 0, "NR row groups");
+        const float* ct = epi.cosp + nr_head * epi.t_hs + d;
+        const float* st = epi.sinp + nr_head * epi.t_hs + d;
+        const uint32_t t_rows = (uint32_t)epi.t_rows, t_bs = (uint32_t)epi.t_bs, t_ld = (uint32_t)epi.t_ld;
+        // the rows' offsets are the same in both storing passes: opaque here, so that they are
+        // computed per pass and group rather than held in registers across the epilogue
+        int mb = mrow0 + rr;
+        asm volatile("" : "+v"(mb));
+        uint16_t* crow = static_cast<uint16_t*>(C) + (int64_t)mb * ldc + n;
+        // two groups of table rows in flight: group g + 1's loads are issued before group g's math
+        float4 c4[2][GR], s4[2][GR];
+        auto load_group = [&](int g0, float4* cg, float4* sg) {
+#pragma unroll
+          for (int j = 0; j < GR; ++j) {
+            const uint32_t m = (uint32_t)min(mb + (g0 + j) * RPI_EP, M - 1);
+            const uint32_t seq = (__umulhi(m, epi.t_magic) + m) >> epi.t_shift;
+            const uint32_t trow = seq * t_bs + (m - seq * t_rows) * t_ld;  // < 2^31 (host check)
+            cg[j] = *reinterpret_cast<const float4*>(ct + trow);
+            sg[j] = *reinterpret_cast<const float4*>(st + trow);
+          }
+        };
+        load_group(0, c4[0], s4[0]);
+#pragma unroll
+        for (int gi = 0; gi < NG; ++gi) {
+          if (gi + 1 < NG) load_group((gi + 1) * GR, c4[(gi + 1) & 1], s4[(gi + 1) & 1]);
+          const float4* cg = c4[gi & 1];
+          const float4* sg = s4[gi & 1];
+#pragma unroll
+          for (int j = 0; j < GR; ++j) {
+            const int k = gi * GR + j;
+            const int r = rr + k * RPI_EP;
+            const int m = mb + k * RPI_EP;
+            const float4 a4 = *reinterpret_cast<const float4*>(ep + r * PITCH + 4 * q);
+            const float iv = nr_inv[k];
+            const float av[4] = {a4.x, a4.y, a4.z, a4.w};
+            const float c[4] = {cg[j].x, cg[j].y, cg[j].z, cg[j].w}, sn[4] = {sg[j].x, sg[j].y, sg[j].z, sg[j].w};
+            float nv[4], o[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) nv[e] = bf2f(f2bf(av[e] + b4[e])) * iv * w4[e];
+#pragma unroll
+            for (int e = 0; e < 4; e += 2) {
+#pragma clang fp contract(off)
+              const float a0 = nv[e] * c[e];
+              const float b0 = (-nv[e + 1]) * sn[e];
+              const float a1 = nv[e + 1] * c[e + 1];
+              const float b1 = nv[e] * sn[e + 1];
+              o[e] = a0 + b0;
+              o[e + 1] = a1 + b1;
+            }
+            uint2 sv;
+            sv.x = pack2(o[0], o[1]);
+            sv.y = pack2(o[2], o[3]);
+            if (m < M) *reinterpret_cast<uint2*>(crow + (int64_t)(k * RPI_EP) * ldc) = sv;
+          }
+          // keeps group g + 2's loads (and their address arithmetic) below this group's math
+          asm volatile("" ::: "memory");
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    } else if (full) {
       // column data is fixed per lane: bias, and the gate when one gate row covers the rows
       float b4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
       if (has_bias) {
@@ -1176,11 +1321,12 @@ int pick_cfg(int64_t m, int64_t n) {
   return T128x128;
 }
 
-template <int BM, int BN, int QB, bool TL, int GMODE, bool OUTF32>
+template <int BM, int BN, int QB, bool TL, int GMODE, bool OUTF32, bool NR = false>
 int launch_lds_t(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, QuantW qw, void* c,
                  int64_t ldc, int m, int n, int k, const Epilogue& epi, hipStream_t s) {
   const int tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
-  gemm_lds_kernel<BM, BN, QB, TL, GMODE, OUTF32><<<tiles, 256, 0, s>>>(a, lda, w, ldw, qw, c, ldc, m, n, k, epi);
+  gemm_lds_kernel<BM, BN, QB, TL, GMODE, OUTF32, NR><<<tiles, 256, 0, s>>>(a, lda, w, ldw, qw, c, ldc, m, n, k,
+                                                                           epi);
   return KX_OK;
 }
 
@@ -1403,6 +1549,71 @@ extern "C" int kx_gemm_bf16(const void* a, int64_t lda, const void* w, int64_t l
   dispatch<0>((const uint16_t*)a, lda, (const uint16_t*)w, ldw, QuantW{}, c, ldc, m, n, k, epi,
               (hipStream_t)stream);
   return check_launch("kx_gemm_bf16");
+}
+
+extern "C" int kx_gemm_qknorm_rope_bf16(const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias,
+                                        void* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int64_t q_end,
+                                        int64_t k_end, const void* norm_q, const void* norm_k, int norm_dtype,
+                                        float eps, float weight_offset, const float* cos, const float* sin,
+                                        int64_t table_ld, int64_t table_hs, int64_t table_rows, int64_t table_bs,
+                                        kx_stream_t stream) {
+  const char* what = "kx_gemm_qknorm_rope_bf16";
+  KX_REQUIRE(a && w && c && norm_q && norm_k && cos && sin, "%s: null tensor", what);
+  KX_REQUIRE(m >= 0 && n > 0 && k > 0 && m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 30) && k % 32 == 0,
+             "%s: bad shape (m=%lld n=%lld k=%lld; k %% 32 == 0)", what, (long long)m, (long long)n, (long long)k);
+  KX_REQUIRE(q_end >= 0 && q_end % 128 == 0 && k_end >= q_end && k_end % 128 == 0 && k_end <= n,
+             "%s: the query and key columns must be whole 128-wide heads inside n (q_end=%lld k_end=%lld)", what,
+             (long long)q_end, (long long)k_end);
+  KX_REQUIRE(lda % 8 == 0 && ldw % 8 == 0 && lda >= k && ldw >= k && ldc >= n && ldc % 4 == 0 && lda <= (1 << 22) &&
+                 ldw <= (1 << 22),
+             "%s: bad strides", what);
+  KX_REQUIRE(aligned16(a) && aligned16(w) && aligned8(c) && (!bias || aligned8(bias)), "%s: misaligned tensor", what);
+  KX_REQUIRE(norm_dtype == KX_F32 || norm_dtype == KX_BF16, "%s: norm weights must be KX_F32 or KX_BF16", what);
+  KX_REQUIRE(norm_dtype == KX_BF16 ? (aligned8(norm_q) && aligned8(norm_k)) : (aligned16(norm_q) && aligned16(norm_k)),
+             "%s: misaligned norm weights", what);
+  KX_REQUIRE(aligned16(cos) && aligned16(sin) && table_ld % 4 == 0 && table_hs % 4 == 0 && table_bs % 4 == 0 &&
+                 table_rows > 0 && table_rows < (1ll << 31),
+             "%s: tables need 16-byte aligned rows (table_ld, table_hs, table_bs multiples of 4)", what);
+  {
+    // the kernel indexes the tables with 32-bit offsets
+    const int64_t heads = std::max(q_end, k_end - q_end) / 128;
+    const int64_t last = (m > 0 ? (m - 1) / table_rows : 0) * table_bs + std::min(m, table_rows) * table_ld +
+                         std::max<int64_t>(heads - 1, 0) * table_hs + 128;
+    KX_REQUIRE(table_ld >= 0 && table_hs >= 0 && table_bs >= 0 && last < (1ll << 31),
+               "%s: table offsets must be non-negative and below 2^31 elements", what);
+  }
+  if (m == 0) return KX_OK;
+  Epilogue epi{(const uint16_t*)bias, nullptr, 0, nullptr, 1, 0, bias ? KX_EPI_BIAS : 0};
+  epi.nq = norm_q;
+  epi.nk = norm_k;
+  epi.n_bf16 = norm_dtype == KX_BF16;
+  epi.n_eps = eps;
+  epi.n_off = weight_offset;
+  epi.q_end = q_end;
+  epi.k_end = k_end;
+  epi.cosp = cos;
+  epi.sinp = sin;
+  epi.t_ld = table_ld;
+  epi.t_hs = table_hs;
+  epi.t_rows = table_rows;
+  epi.t_bs = table_bs;
+  // division by the invariant table_rows (round-up method): shift = ceil(log2 d),
+  // magic = floor(2^32 (2^shift - d) / d) + 1
+  int shift = 0;
+  while ((1ll << shift) < table_rows) ++shift;
+  epi.t_shift = shift;
+  epi.t_magic = (uint32_t)(((((unsigned __int128)1 << 32) * (uint64_t)((1ll << shift) - table_rows)) /
+                            (uint64_t)table_rows) + 1);
+  const int64_t t256 = ((m + 255) / 256) * ((n + 255) / 256), t192 = ((m + 191) / 192) * ((n + 255) / 256);
+  const bool tall = (t256 + 255) / 256 * 256 <= (t192 + 255) / 256 * 192;
+  hipStream_t s = (hipStream_t)stream;
+  if (tall)
+    launch_lds_t<256, 256, 0, false, 0, false, true>((const uint16_t*)a, lda, (const uint16_t*)w, ldw, QuantW{}, c,
+                                                     ldc, (int)m, (int)n, (int)k, epi, s);
+  else
+    launch_lds_t<192, 256, 0, false, 0, false, true>((const uint16_t*)a, lda, (const uint16_t*)w, ldw, QuantW{}, c,
+                                                     ldc, (int)m, (int)n, (int)k, epi, s);
+  return check_launch(what);
 }
 
 extern "C" int kx_qgemm_affine_bf16(const void* a, int64_t lda, const uint32_t* wq,

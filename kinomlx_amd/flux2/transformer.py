@@ -37,7 +37,7 @@ import torch
 from .. import _lib
 from ..kernels import fused_ops
 from ..ltx2 import dense_attention as _dense
-from ..ltx2.attention import Linear, _cat_layers
+from ..ltx2.attention import Linear, _cat_layers, qknorm_rope_projection
 from ..ltx2.transformer import layer_norm_modulate
 from .kv import attend
 
@@ -218,18 +218,39 @@ class DoubleAttention:
         tokens = t_text + t_image
         cos, sin = _tables(positions, batch, tokens, self.head_dim)
         qkv = torch.empty((batch, tokens, 3 * width), dtype=torch.bfloat16, device=image.device)
-        self._project(self._added_qkv, (self.add_q_proj, self.add_k_proj, self.add_v_proj), text, qkv[:, :t_text])
-        self._project(self._qkv, (self.to_q, self.to_k, self.to_v), image, qkv[:, t_text:])
-        q = torch.empty((batch, tokens, width), dtype=torch.bfloat16, device=image.device)
-        k = torch.empty_like(q)
-        for norm_q, norm_k, start, stop in ((self.norm_added_q, self.norm_added_k, 0, t_text),
-                                            (self.norm_q, self.norm_k, t_text, tokens)):
-            if stop > start:
-                _norm_rope_into(qkv[:, start:stop, :width], q[:, start:stop], norm_q, cos, sin, start, self.heads)
-                _norm_rope_into(qkv[:, start:stop, width:2 * width], k[:, start:stop], norm_k, cos, sin, start,
-                                self.heads)
-        return _dense.batched_attention(q, k, qkv[..., 2 * width:], heads=self.heads,
-                                            scale=self.head_dim ** -0.5)
+        self._stream_qkv(self._added_qkv, (self.add_q_proj, self.add_k_proj, self.add_v_proj), text,
+                         qkv[:, :t_text], self.norm_added_q, self.norm_added_k, cos, sin, 0)
+        self._stream_qkv(self._qkv, (self.to_q, self.to_k, self.to_v), image, qkv[:, t_text:], self.norm_q,
+                         self.norm_k, cos, sin, t_text)
+        return _dense.batched_attention(qkv[..., :width], qkv[..., width:2 * width], qkv[..., 2 * width:],
+                                        heads=self.heads, scale=self.head_dim ** -0.5)
+
+    def _stream_qkv(self, fused, layers, value: torch.Tensor, rows: torch.Tensor, norm_q: QKNorm, norm_k: QKNorm,
+                    cos: torch.Tensor, sin: torch.Tensor, row0: int) -> None:
+        """``rows`` ``(B, Ts, 3D)`` = one stream's Q/K/V projection with Q and K normalized per
+        head and rotated at joint positions ``row0 + t``. With the fused weight the norm and rotation
+        run in the projection's epilogue, one launch per batch entry; otherwise the projection, then
+        the norm + RoPE pass (into scratch rows, copied back over the raw Q/K columns)."""
+        width = self.heads * self.head_dim
+        count = rows.shape[1]
+        if count == 0:
+            return
+        for b in range(rows.shape[0]):
+            tb = b if cos.shape[0] > 1 else 0
+            if (fused is not None and norm_q.weight is not None and norm_k.weight is not None
+                    and qknorm_rope_projection(fused, value[b], rows[b], q_width=width, k_width=width,
+                                               norm_q=norm_q.weight, norm_k=norm_k.weight, eps=1e-6,
+                                               weight_offset=0.0, cos=cos[tb, row0:row0 + count, 0],
+                                               sin=sin[tb, row0:row0 + count, 0])):
+                continue
+            entry = rows[b:b + 1]
+            self._project(fused, layers, value[b:b + 1], entry)
+            normed = torch.empty((1, count, 2 * width), dtype=torch.bfloat16, device=rows.device)
+            _norm_rope_into(entry[..., :width], normed[..., :width], norm_q, cos[tb:tb + 1], sin[tb:tb + 1], row0,
+                            self.heads)
+            _norm_rope_into(entry[..., width:2 * width], normed[..., width:], norm_k, cos[tb:tb + 1],
+                            sin[tb:tb + 1], row0, self.heads)
+            entry[..., :2 * width].copy_(normed)
 
     def __call__(self, image: torch.Tensor, text: torch.Tensor, positions: tuple[torch.Tensor, torch.Tensor],
                  reference_kv=None, layer: int = 0, *, image_residual: torch.Tensor | None = None,
@@ -312,15 +333,24 @@ class SingleAttention:
             raise ValueError("SingleAttention takes (batch, tokens, width) values")
         width = self.heads * self.head_dim
         batch, tokens = value.shape[0], value.shape[1]
-        fused = self.to_qkv_mlp_proj(value)
-        mlp_width = fused.shape[-1] - 3 * width
+        total = int(self.to_qkv_mlp_proj.out_features)
+        mlp_width = total - 3 * width
         if mlp_width <= 0 or mlp_width % 2:
-            raise ValueError(f"to_qkv_mlp_proj width {fused.shape[-1]} does not split into [{width} x 3, 2F]")
+            raise ValueError(f"to_qkv_mlp_proj width {total} does not split into [{width} x 3, 2F]")
         cos, sin = _tables(positions, batch, tokens, self.head_dim)
-        q = torch.empty((batch, tokens, width), dtype=torch.bfloat16, device=value.device)
-        k = torch.empty_like(q)
-        _norm_rope_into(fused[..., :width], q, self.norm_q, cos, sin, 0, self.heads)
-        _norm_rope_into(fused[..., width:2 * width], k, self.norm_k, cos, sin, 0, self.heads)
+        fused = torch.empty((batch, tokens, total), dtype=torch.bfloat16, device=value.device)
+        if (self.norm_q.weight is not None and self.norm_k.weight is not None and value.is_contiguous()
+                and qknorm_rope_projection(self.to_qkv_mlp_proj, value.view(batch * tokens, -1),
+                                           fused.view(batch * tokens, total), q_width=width, k_width=width,
+                                           norm_q=self.norm_q.weight, norm_k=self.norm_k.weight, eps=1e-6,
+                                           weight_offset=0.0, cos=cos[:, :, 0], sin=sin[:, :, 0])):
+            q, k = fused[..., :width], fused[..., width:2 * width]
+        else:  # the projection, then the norm + RoPE pass
+            self.to_qkv_mlp_proj(value, out=fused)
+            q = torch.empty((batch, tokens, width), dtype=torch.bfloat16, device=value.device)
+            k = torch.empty_like(q)
+            _norm_rope_into(fused[..., :width], q, self.norm_q, cos, sin, 0, self.heads)
+            _norm_rope_into(fused[..., width:2 * width], k, self.norm_k, cos, sin, 0, self.heads)
         joined = torch.empty((batch, tokens, width + mlp_width // 2), dtype=torch.bfloat16, device=value.device)
         _dense.batched_attention(q, k, fused[..., 2 * width:3 * width], heads=self.heads,
                                      scale=self.head_dim ** -0.5, out=joined[..., :width])

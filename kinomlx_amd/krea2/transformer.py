@@ -32,7 +32,7 @@ import torch
 from .. import _lib
 from ..kernels import fused_ops
 from ..ltx2 import dense_attention as _dense
-from ..ltx2.attention import Linear, _cat_layers
+from ..ltx2.attention import Linear, _cat_layers, qknorm_rope_projection
 from ..ltx2.transformer import adaln
 
 __all__ = [
@@ -200,15 +200,29 @@ class Krea2Attention:
             raise ValueError("reference attention capture is not built for MI355X")
         q_width = self.num_heads * self.head_dim
         kv_width = self.num_kv_heads * self.head_dim
+        q = k = None
         if self._qkv is not None:
-            qkv = self._qkv(hidden_states)
+            qkv = torch.empty((batch, length, q_width + 2 * kv_width), dtype=torch.bfloat16,
+                              device=hidden_states.device)
+            if (rotary is not None and self.norm_q.weight is not None and self.norm_k.weight is not None
+                    and self.norm_q.eps == self.norm_k.eps and hidden_states.is_contiguous()):
+                cos, sin = _check_tables(*rotary, batch, length, self.head_dim)
+                if qknorm_rope_projection(self._qkv, hidden_states.view(batch * length, -1),
+                                          qkv.view(batch * length, -1), q_width=q_width, k_width=kv_width,
+                                          norm_q=self.norm_q.weight, norm_k=self.norm_k.weight, eps=self.norm_q.eps,
+                                          weight_offset=1.0, cos=cos, sin=sin):
+                    # zero-centred norms and the rotation ran in the projection's epilogue
+                    q, k = qkv[..., :q_width], qkv[..., q_width:q_width + kv_width]
+            if q is None:
+                self._qkv(hidden_states, out=qkv)
             q_raw, k_raw = qkv[..., :q_width], qkv[..., q_width:q_width + kv_width]
             v = qkv[..., q_width + kv_width:]
         else:
             q_raw, k_raw, v = self.to_q(hidden_states), self.to_k(hidden_states), self.to_v(hidden_states)
         sigmoid_gate = self.to_gate(hidden_states, activation="sigmoid", out_dtype=torch.float32)
-        q = _norm_rope_rows(q_raw, self.norm_q, rotary, self.num_heads)
-        k = _norm_rope_rows(k_raw, self.norm_k, rotary, self.num_kv_heads)
+        if q is None:
+            q = _norm_rope_rows(q_raw, self.norm_q, rotary, self.num_heads)
+            k = _norm_rope_rows(k_raw, self.norm_k, rotary, self.num_kv_heads)
         attended = _dense.batched_attention(q, k, v, heads=self.num_heads, kv_heads=self.num_kv_heads,
                                             scale=self.scale, mask=key_mask)
         if attention_mask is not None:

@@ -194,6 +194,54 @@ def _cat_layers(layers):
     return None
 
 
+def _dense_weight(layer):
+    """The bf16 ``(out, in)`` weight a layer multiplies by (a quantized layer's exact
+    dequantization), or None for a layer of another kind."""
+    if isinstance(layer, Linear):
+        return layer.weight
+    if isinstance(layer, PretransposedQuantizedLinear):
+        return layer._dense
+    if isinstance(layer, QuantizedLinear) and layer.weight.is_cuda:
+        return layer._dense if layer._dense is not None else layer.dequantized()
+    return None
+
+
+def qknorm_rope_projection(layer, value: torch.Tensor, out: torch.Tensor, *, q_width: int, k_width: int,
+                           norm_q: torch.Tensor, norm_k: torch.Tensor, eps: float, weight_offset: float,
+                           cos: torch.Tensor, sin: torch.Tensor) -> bool:
+    """``out = layer(value)`` with the query columns ``[0, q_width)`` and key columns
+    ``[q_width, q_width + k_width)`` normalized per 128-wide head (``(x * rsqrt(mean(x^2) + eps))
+    * (w + weight_offset)`` of the bf16 projection) and rotated in adjacent pairs, all in the GEMM's
+    epilogue (``kx_gemm_qknorm_rope_bf16``). ``value`` ``(R, in)`` and ``out`` ``(R, out)`` are the
+    rows of ``R / T`` sequences of ``T`` tokens; ``cos``/``sin`` are their fp32 tables, ``(T, 128)``
+    or ``(1 | R / T, T, 128)``, with unit-stride rows. Returns False (nothing written) when the layer
+    or the shapes do not take this path; the caller then runs the separate passes."""
+    weight = _dense_weight(layer)
+    if (weight is None or weight.dtype != torch.bfloat16 or value.dtype != torch.bfloat16 or value.dim() != 2
+            or out.dim() != 2 or cos.dim() not in (2, 3) or cos.shape != sin.shape or cos.stride() != sin.stride()):
+        return False
+    rows, k = int(value.shape[0]), int(value.shape[1])
+    n = int(weight.shape[0])
+    tokens = int(cos.shape[-2])
+    batches = 1 if cos.dim() == 2 else int(cos.shape[0])
+    if (rows == 0 or tokens == 0 or rows % tokens or batches not in (1, rows // tokens) or cos.shape[-1] != 128
+            or q_width % 128 or k_width % 128 or q_width + k_width > n or k % 32 or int(weight.shape[1]) != k
+            or norm_q.shape != (128,) or norm_k.shape != (128,) or norm_q.dtype != norm_k.dtype
+            or cos.dtype != torch.float32 or sin.dtype != torch.float32 or cos.stride(-1) != 1
+            or cos.stride(-2) % 4 or (batches > 1 and cos.stride(0) % 4) or cos.data_ptr() % 16
+            or sin.data_ptr() % 16 or tuple(out.shape) != (rows, n) or out.dtype != torch.bfloat16
+            or out.stride(-1) != 1 or out.stride(0) % 4 or out.data_ptr() % 8):
+        return False
+    a = value if value.stride(-1) == 1 and value.stride(0) % 8 == 0 and value.data_ptr() % 16 == 0 else value.contiguous()
+    bias = getattr(layer, "bias", None)
+    bias = None if bias is None else bias.to(torch.bfloat16).contiguous()
+    _lib.launch_gemm_qknorm_rope(a, weight, out, bias=bias, q_end=q_width, k_end=q_width + k_width,
+                                 norm_q=norm_q.contiguous(), norm_k=norm_k.contiguous(), eps=eps,
+                                 weight_offset=weight_offset, cos=cos, sin=sin, table_ld=int(cos.stride(-2)),
+                                 table_hs=0, table_rows=tokens, table_bs=int(cos.stride(0)) if batches > 1 else 0)
+    return True
+
+
 class Attention:
     """Multi-head attention with Q/K RMSNorm, split RoPE and per-head gates
     (``attention.py:249-371``). Weights are assigned after construction, as the reference's
@@ -297,6 +345,7 @@ __all__ = [
     "dense_kernel_attention",
     "norm_rope",
     "norm_rope_qk",
+    "qknorm_rope_projection",
     "rms_norm",
     "scaled_dot_product_attention",
 ]

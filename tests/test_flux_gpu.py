@@ -97,7 +97,10 @@ def test_double_block_unfused_and_batched_agree_with_fused(device):
     fi, ft = _run_double(spec, p, inputs, device)
     ui, ut = _run_double(spec, p, inputs, device, fuse=False)
     bi, bt = _run_double(spec, p, inputs, device, batch=2)
-    assert torch.equal(fi, ui) and torch.equal(ft, ut)
+    # the fused projections norm and rotate Q/K in their epilogue (the norm's sum of squares in
+    # another order than the standalone pass: a bf16 ulp in a few Q/K elements)
+    for f, u in ((fi, ui), (ft, ut)):
+        assert rel_l2(_np(f), _np(u)) < 1e-3 and max_abs(_np(f), _np(u)) < 2e-2
     assert torch.equal(bi[0], fi[0]) and torch.equal(bi[1], fi[0])
     assert torch.equal(bt[0], ft[0]) and torch.equal(bt[1], ft[0])
 

@@ -430,6 +430,177 @@ def test_linear_rows_adds_the_residual_after_the_product(device):
     assert _gemm_close(got, ref)
 
 
+# ---- projection with the per-head Q/K norm and pair RoPE in its epilogue ---------------------------
+
+
+def _qknorm_case(m, k, q_heads, k_heads, rest, tokens, table_batch, seed):
+    r = _rng(seed)
+    n = (q_heads + k_heads) * 128 + rest
+    x, w, b = _linear_case(m, n, k, seed, None, scale=2.0)
+    nq = (r.standard_normal(128) * 0.1 + 1).astype(F32)
+    nk = (r.standard_normal(128) * 0.1 + 1).astype(F32)
+    ang = np.repeat(r.uniform(-4, 4, (table_batch, tokens, 64)), 2, axis=-1).astype(F32)
+    return x, w, b, nq, nk, np.cos(ang).astype(F32), np.sin(ang).astype(F32)
+
+
+def _qknorm_reference(proj, q_end, k_end, nq, nk, eps, offset, cos_rows, sin_rows):
+    """The oracle's norm + rotation of each query / key head of ``proj`` (the bf16 projection)."""
+    out = np.array(proj, dtype=F32)
+    rows = proj.shape[0]
+    for lo, hi, weight in ((0, q_end, nq), (q_end, k_end, nk)):
+        if hi > lo:
+            heads = (hi - lo) // 128
+            normed = oracle.rms_norm(proj[:, lo:hi].reshape(rows, heads, 128), weight, eps, weight_offset=offset)
+            out[:, lo:hi] = oracle.pair_rope(normed, cos_rows[:, None], sin_rows[:, None]).reshape(rows, hi - lo)
+    return out
+
+
+def _pair_bound(ref, scale):
+    """``scale`` times the magnitude of each element's rotation pair (rotation mixes the pair)."""
+    pairs = np.abs(ref).reshape(*ref.shape[:-1], -1, 2).sum(axis=-1, keepdims=True)
+    return scale * np.broadcast_to(pairs, pairs.shape[:-1] + (2,)).reshape(ref.shape)
+
+
+QKNORM_CASES = [
+    # m, k, q heads, k heads, other columns, tokens per table row set, table sets, bias, norm dtype, offset, eps
+    (300, 512, 4, 4, 512, 300, 1, False, "bf16", 0.0, 1e-6),          # FLUX stream: ragged M, V after
+    (2 * 97, 256, 8, 4, 456, 97, 2, True, "f32", 1.0, 1e-5),          # Krea GQA, batched tables, ragged N
+    (512, 384, 4, 4, 512 + 2048, 512, 1, False, "bf16", 0.0, 1e-6),   # FLUX single: Q, K, V, then MLP
+    (500, 64, 88, 88, 0, 250, 1, True, "bf16", 0.0, 1e-6),            # every column a head, 256-row tiles
+    (9, 128, 1, 1, 128, 9, 1, True, "f32", 1.0, 1e-6),                # one partial tile
+    (130, 256, 1, 2, 384, 65, 2, True, "bf16", 0.0, 1e-6),            # a tile with a key head and V columns
+]
+
+
+@pytest.mark.parametrize(("m", "k", "q_heads", "k_heads", "rest", "tokens", "table_batch", "bias", "wdtype",
+                          "offset", "eps"), QKNORM_CASES,
+                         ids=["flux-stream", "krea-gqa-batched", "flux-single", "all-heads-256", "tiny",
+                              "mixed-tile"])
+def test_qknorm_rope_projection_matches_oracle(device, m, k, q_heads, k_heads, rest, tokens, table_batch, bias,
+                                               wdtype, offset, eps):
+    """kx_gemm_qknorm_rope_bf16 against the oracle's linear -> bf16 -> per-head RMSNorm -> pair RoPE
+    (FLUX.2 transformer.py:25-29, 68-75; Krea model.py:29-46, 69-92). Q/K columns: relative L2 and
+    cosine at the standalone norm + RoPE kernel's bar, and every element within 2^-6 of its
+    rotation pair's magnitude (one bf16 ulp of the projection, carried through the norm, plus the
+    output's rounding); the other columns at the plain GEMM's bar."""
+    x, w, b, nq, nk, cos, sin = _qknorm_case(m, k, q_heads, k_heads, rest, tokens, table_batch, m + k + rest)
+    n = w.shape[0]
+    q_end, k_end = 128 * q_heads, 128 * (q_heads + k_heads)
+    wt = torch.bfloat16 if wdtype == "bf16" else torch.float32
+    if wdtype == "bf16":
+        nq, nk = oracle.to_bf16(nq), oracle.to_bf16(nk)
+    out = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=device)
+    _lib.launch_gemm_qknorm_rope(
+        _bf(x, device), _bf(w, device), out, bias=_bf(b, device) if bias else None, q_end=q_end, k_end=k_end,
+        norm_q=torch.from_numpy(nq).to(device, wt), norm_k=torch.from_numpy(nk).to(device, wt), eps=eps,
+        weight_offset=offset, cos=_f32(cos, device), sin=_f32(sin, device), table_ld=128, table_hs=0,
+        table_rows=tokens, table_bs=tokens * 128 if table_batch > 1 else 0)
+    got = _np(out)
+    linear = oracle.linear(x, w, b if bias else None)
+    rows = np.arange(m)
+    tb = rows // tokens if table_batch > 1 else np.zeros(m, dtype=int)
+    cos_rows, sin_rows = cos[tb, rows % tokens], sin[tb, rows % tokens]
+    ref = _qknorm_reference(oracle.to_bf16(linear), q_end, k_end, nq, nk, eps, offset, cos_rows, sin_rows)
+    g, r = got[:, :k_end], ref[:, :k_end]
+    assert np.isfinite(got).all()
+    assert rel_l2(g, r) < 4e-3 and cosine(g, r) > 0.99999
+    assert np.all(np.abs(g - r) <= _pair_bound(r, 2.0**-6) + 1e-5)
+    if k_end < n:
+        assert _gemm_close(got[:, k_end:], linear[:, k_end:])
+
+
+@pytest.mark.parametrize("case", [0, 1, 2], ids=["flux-stream", "krea-gqa-batched", "flux-single"])
+def test_qknorm_rope_projection_agrees_with_the_two_pass_path(device, monkeypatch, case):
+    """Against the plain 256x256 projection then kx_rmsnorm_rope_bf16 on its bf16 output (the path
+    the epilogue replaces; Q and K widths that are multiples of 512, that kernel's one-pass
+    contract): the other columns bit-identical (same kernel family, same K order), the Q/K columns
+    within one bf16 ulp (the norm's sum of squares runs in another order)."""
+    m, k, q_heads, k_heads, rest, tokens, table_batch, bias, wdtype, offset, eps = QKNORM_CASES[case]
+    x, w, b, nq, nk, cos, sin = _qknorm_case(m, k, q_heads, k_heads, rest, tokens, table_batch, case)
+    n = w.shape[0]
+    q_end, k_end = 128 * q_heads, 128 * (q_heads + k_heads)
+    wt = torch.bfloat16 if wdtype == "bf16" else torch.float32
+    xd, wd, bd = _bf(x, device), _bf(w, device), _bf(b, device) if bias else None
+    nqd, nkd = torch.from_numpy(nq).to(device, wt), torch.from_numpy(nk).to(device, wt)
+    fused = torch.empty((m, n), dtype=torch.bfloat16, device=device)
+    _lib.launch_gemm_qknorm_rope(xd, wd, fused, bias=bd, q_end=q_end, k_end=k_end, norm_q=nqd, norm_k=nkd, eps=eps,
+                                 weight_offset=offset, cos=_f32(cos, device), sin=_f32(sin, device), table_ld=128,
+                                 table_hs=0, table_rows=tokens, table_bs=tokens * 128 if table_batch > 1 else 0)
+    monkeypatch.setenv("KX355_GEMM_LDS_TILE", "0")
+    proj = mpp_linear.fused_linear(xd, wd, bd)
+    rows = torch.arange(m)
+    tb = rows // tokens if table_batch > 1 else torch.zeros(m, dtype=torch.long)
+    cos_rows = _f32(cos, device)[tb, rows % tokens].contiguous()
+    sin_rows = _f32(sin, device)[tb, rows % tokens].contiguous()
+    two = proj.clone()
+    for lo, hi, weight in ((0, q_end, nqd), (q_end, k_end, nkd)):
+        _lib.launch_rmsnorm_rope(proj[:, lo:hi], two[:, lo:hi], weight, eps, offset, norm_width=128,
+                                 rope_kind=_lib.KX_ROPE_PAIR, cos=cos_rows, sin=sin_rows, table_ld=128, table_hs=0,
+                                 tokens=m, table_batched=True, head_dim=128)
+    assert torch.equal(fused[:, k_end:], two[:, k_end:])
+    g, r = _np(fused[:, :k_end]), _np(two[:, :k_end])
+    assert np.all(np.abs(g - r) <= np.abs(r) * 2.0**-7 + 1e-6)
+    assert np.mean(g != r) < 0.01
+
+
+def test_qknorm_rope_projection_per_head_tables(device):
+    """Tables with a row per head (table_hs): query head h and key head h read row block h."""
+    m, k, heads = 70, 128, 2
+    x, w, b, nq, nk, _, _ = _qknorm_case(m, k, heads, heads, 256, m, 1, 5)
+    ang = np.repeat(_rng(6).uniform(-4, 4, (m, heads, 64)), 2, axis=-1).astype(F32)
+    cos, sin = np.cos(ang).astype(F32), np.sin(ang).astype(F32)
+    out = torch.empty((m, w.shape[0]), dtype=torch.bfloat16, device=device)
+    _lib.launch_gemm_qknorm_rope(_bf(x, device), _bf(w, device), out, bias=_bf(b, device), q_end=256, k_end=512,
+                                 norm_q=_f32(nq, device), norm_k=_f32(nk, device), eps=1e-6, weight_offset=0.0,
+                                 cos=_f32(cos, device), sin=_f32(sin, device), table_ld=heads * 128, table_hs=128,
+                                 table_rows=m, table_bs=0)
+    proj = oracle.to_bf16(oracle.linear(x, w, b))
+    ref = proj.copy()
+    for lo, weight in ((0, nq), (256, nk)):
+        normed = oracle.rms_norm(proj[:, lo:lo + 256].reshape(m, heads, 128), weight, 1e-6)
+        ref[:, lo:lo + 256] = oracle.pair_rope(normed, cos, sin).reshape(m, 256)
+    got = _np(out)
+    assert rel_l2(got[:, :512], ref[:, :512]) < 4e-3
+    assert np.all(np.abs(got[:, :512] - ref[:, :512]) <= _pair_bound(ref[:, :512], 2.0**-6) + 1e-5)
+
+
+def test_qknorm_rope_projection_layer_helper_matches_the_launch(device):
+    """``qknorm_rope_projection`` on a Linear over two sequences with broadcast and per-sequence
+    tables reads the same table rows as the explicit launch."""
+    m, tokens = 2 * 64, 64
+    x, w, b, nq, nk, cos, sin = _qknorm_case(m, 256, 2, 2, 256, tokens, 2, 11)
+    layer = ltx_attention.Linear(_bf(w, device), _bf(b, device))
+    for table_batch in (1, 2):
+        c, s_ = _f32(cos[:table_batch], device), _f32(sin[:table_batch], device)
+        out = torch.empty((m, w.shape[0]), dtype=torch.bfloat16, device=device)
+        assert ltx_attention.qknorm_rope_projection(layer, _bf(x, device), out, q_width=256, k_width=256,
+                                                    norm_q=_f32(nq, device), norm_k=_f32(nk, device), eps=1e-6,
+                                                    weight_offset=0.0, cos=c, sin=s_)
+        ref = torch.empty_like(out)
+        _lib.launch_gemm_qknorm_rope(_bf(x, device), _bf(w, device), ref, bias=_bf(b, device), q_end=256,
+                                     k_end=512, norm_q=_f32(nq, device), norm_k=_f32(nk, device), eps=1e-6,
+                                     weight_offset=0.0, cos=c, sin=s_, table_ld=128, table_hs=0, table_rows=tokens,
+                                     table_bs=tokens * 128 if table_batch > 1 else 0)
+        assert torch.equal(out, ref)
+        if table_batch == 1:  # the second sequence reads the first table set
+            assert torch.equal(out[tokens:, :512], _qk_rows_with_tables(layer, x[tokens:], c, s_, nq, nk, device))
+    # outside the kernel's contract (head width 64): nothing written, the caller runs two passes
+    out = torch.zeros((m, w.shape[0]), dtype=torch.bfloat16, device=device)
+    assert not ltx_attention.qknorm_rope_projection(layer, _bf(x, device), out, q_width=256, k_width=256,
+                                                    norm_q=_f32(nq[:64], device), norm_k=_f32(nk[:64], device),
+                                                    eps=1e-6, weight_offset=0.0, cos=_f32(cos[0], device)[:, :64],
+                                                    sin=_f32(sin[0], device)[:, :64])
+    assert not out.any()
+
+
+def _qk_rows_with_tables(layer, x, cos, sin, nq, nk, device):
+    out = torch.empty((x.shape[0], layer.out_features), dtype=torch.bfloat16, device=device)
+    assert ltx_attention.qknorm_rope_projection(layer, _bf(x, device), out, q_width=256, k_width=256,
+                                                norm_q=_f32(nq, device), norm_k=_f32(nk, device), eps=1e-6,
+                                                weight_offset=0.0, cos=cos[0], sin=sin[0])
+    return out[:, :512]
+
+
 # ---- attention -----------------------------------------------------------------------------------
 
 

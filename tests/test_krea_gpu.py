@@ -53,7 +53,9 @@ def test_krea_block_unfused_and_batched_agree(device):
     kwargs = dict(time_modulation=tmod.to(device), rotary=tables, attention_mask=None)
     fused = build_krea_block(p, hidden, heads, kv_heads, device)(x.to(device), **kwargs)
     plain = build_krea_block(p, hidden, heads, kv_heads, device, fuse=False)(x.to(device), **kwargs)
-    assert torch.equal(fused, plain)
+    # the fused projection norms and rotates Q/K in its epilogue; the unfused path's two passes
+    # (the key width is not a multiple of 512) round the normalized keys once more
+    assert rel_l2(_np(fused), _np(plain)) < 2e-3 and max_abs(_np(fused), _np(plain)) < 2e-2
     one = build_krea_block(p, hidden, heads, kv_heads, device)(
         x[1:].to(device), time_modulation=tmod[1:].to(device), rotary=tuple(t[1:] for t in tables),
         attention_mask=None)
