@@ -1231,7 +1231,10 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
 // One workgroup per 32 rows x 32 columns; its NWK waves split K into NWK slices and read both
 // MFMA operands straight from global memory (the weight is a few hundred KB and stays in L2, each
 // activation row is read once), then add their partial tiles through LDS. (Splitting K over 8 or
-// 16 waves measured slower at 9216 x 32 x 4096: fewer workgroups fit a CU.)
+// 16 waves measured slower at 9216 x 32 x 4096: fewer workgroups fit a CU.) The products are
+// 16x16x32 MFMAs: a 16-byte operand load then spans 16 rows (four lanes of 64 contiguous bytes per
+// row) instead of the 32 rows of a 32x32x16 operand, which halves the cache lines each load
+// instruction touches, the limit of this kernel.
 // Quantized weights are dequantized in registers with the arithmetic of the other kernels.
 template <int QB, int NWK>
 __global__ __launch_bounds__(NWK * 64) void gemm_skinny_kernel(
@@ -1240,15 +1243,25 @@ __global__ __launch_bounds__(NWK * 64) void gemm_skinny_kernel(
   __shared__ __attribute__((aligned(16))) float part[NWK][16][64];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lrow = lane & 31, lhalf = lane >> 5;
+  const int l16 = lane & 15, lq = lane >> 4;
   const int m0 = blockIdx.x * 32, n0 = blockIdx.y * 32;
-  const int m = min(m0 + lrow, M - 1), n = min(n0 + lrow, N - 1);
-  const int kq = K / NWK, kbeg = wave * kq;
-  const uint16_t* arow = A + (int64_t)m * lda + 8 * lhalf;
-  f32x16 acc;
+  // operand rows of this lane: activation rows m0 + 16 rb + l16, weight rows n0 + 16 cb + l16
+  int arow_i[2], wrow_i[2];
 #pragma unroll
-  for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
-  auto wfrag = [&](int k) -> bf16x8 {  // k: this lane's 8 values start at k (k % 8 == 0)
+  for (int b = 0; b < 2; ++b) {
+    arow_i[b] = min(m0 + 16 * b + l16, M - 1);
+    wrow_i[b] = min(n0 + 16 * b + l16, N - 1);
+  }
+  const int kq = K / NWK, kbeg = wave * kq;
+  // accumulator (cb, rb): lane holds weight rows n0 + 16 cb + 4 lq + e, activation row m0 + 16 rb + l16
+  f32x4 acc[2][2];
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[cb][rb][e] = 0.0f;
+  auto wfrag = [&](int n, int k) -> bf16x8 {  // row n, this lane's 8 values start at k (k % 8 == 0)
     if constexpr (QB == 0) {
       return *reinterpret_cast<const bf16x8*>(W + (int64_t)n * ldw + k);
     } else if constexpr (QB == QMX8) {
@@ -1264,19 +1277,28 @@ __global__ __launch_bounds__(NWK * 64) void gemm_skinny_kernel(
       return __builtin_bit_cast(bf16x8, dequant8<QB>(tmp, sc, bi));
     }
   };
-#pragma unroll 8
-  for (int k = kbeg; k < kbeg + kq; k += 16) {
-    const bf16x8 wf = wfrag(k + 8 * lhalf);
-    const bf16x8 xf = *reinterpret_cast<const bf16x8*>(arow + k);
-    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, xf, acc, 0, 0, 0);
+  const uint16_t* arow0 = A + (int64_t)arow_i[0] * lda + 8 * lq;
+  const uint16_t* arow1 = A + (int64_t)arow_i[1] * lda + 8 * lq;
+#pragma unroll 4
+  for (int k = kbeg; k < kbeg + kq; k += 32) {
+    const bf16x8 w0 = wfrag(wrow_i[0], k + 8 * lq), w1 = wfrag(wrow_i[1], k + 8 * lq);
+    const bf16x8 x0 = *reinterpret_cast<const bf16x8*>(arow0 + k);
+    const bf16x8 x1 = *reinterpret_cast<const bf16x8*>(arow1 + k);
+    acc[0][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, x0, acc[0][0], 0, 0, 0);
+    acc[0][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, x1, acc[0][1], 0, 0, 0);
+    acc[1][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, x0, acc[1][0], 0, 0, 0);
+    acc[1][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, x1, acc[1][1], 0, 0, 0);
   }
 #pragma unroll
-  for (int e = 0; e < 16; ++e) part[wave][e][lane] = acc[e];
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) part[wave][4 * a + e][lane] = acc[a >> 1][a & 1][e];
   __syncthreads();
   if (wave >= 4) return;
-  // wave w < 4 finishes accumulator elements 4w .. 4w+3 (4 consecutive columns of one row)
-  const int row = m0 + lrow;
-  const int col = n0 + 8 * wave + 4 * lhalf;
+  // wave w < 4 finishes accumulator (cb, rb) = (w / 2, w % 2): 4 consecutive columns of one row
+  const int cb = wave >> 1, rb = wave & 1;
+  const int row = m0 + 16 * rb + l16;
+  const int col = n0 + 16 * cb + 4 * lq;
   float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int p = 0; p < NWK; ++p)
@@ -1380,7 +1402,7 @@ int dispatch(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, Qua
              hipStream_t s) {
   const char* legacy = getenv("KX355_GEMM_TILE");
   const bool use_legacy = legacy && *legacy;
-  if (n <= 64 && k % 64 == 0 && !use_legacy) {
+  if (n <= 64 && k % 128 == 0 && !use_legacy) {
     const dim3 grid((unsigned)((m + 31) / 32), (unsigned)((n + 31) / 32));
     gemm_skinny_kernel<QB, 4><<<grid, 256, 0, s>>>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi);
     return KX_OK;
