@@ -35,7 +35,7 @@ PEAK_HBM_GBS = 8000.0
 
 def _kernel_flops(name: str, args: tuple) -> float:
     """Algorithmic FLOPs of one launch from its C arguments (0 for memory-bound kernels)."""
-    if name == "kx_gemm_bf16":
+    if name in ("kx_gemm_bf16", "kx_gemm_splitk_bf16"):
         m, n, k = args[7], args[8], args[9]
         return 2.0 * m * n * k
     if name == "kx_qgemm_affine_bf16":
@@ -76,6 +76,8 @@ def _kernel_bytes(name: str, args: tuple) -> float:
 def _kernel_label(name: str, args: tuple) -> str:
     if name == "kx_gemm_bf16":
         return f"gemm m{args[7]} n{args[8]} k{args[9]}"
+    if name == "kx_gemm_splitk_bf16":
+        return f"gemm splitk{args[18]} m{args[7]} n{args[8]} k{args[9]}"
     if name == "kx_qgemm_affine_bf16":
         return f"qgemm{args[12]} m{args[8]} n{args[9]} k{args[10]}"
     if name == "kx_qgemm_affine_tiled_bf16":
@@ -250,7 +252,9 @@ def main() -> int:
 
     flops = workloads.flop_count(spec)
     attn_ms = sum(v for k, v in kernel_ms_per_step.items() if name_of[k] == "kx_attention_fwd_bf16")
-    gemm_ms = sum(v for k, v in kernel_ms_per_step.items() if name_of[k] in ("kx_gemm_bf16", "kx_qgemm_affine_bf16", "kx_qgemm_affine_tiled_bf16"))
+    gemm_ms = sum(v for k, v in kernel_ms_per_step.items()
+                  if name_of[k] in ("kx_gemm_bf16", "kx_gemm_splitk_bf16", "kx_qgemm_affine_bf16",
+                                    "kx_qgemm_affine_tiled_bf16"))
     other_ms = sum(kernel_ms_per_step.values()) - attn_ms - gemm_ms
     attn_tflops = flops["attention"] / (attn_ms * 1e-3) / 1e12
     gemm_tflops = flops["gemm"] / (gemm_ms * 1e-3) / 1e12

@@ -418,6 +418,25 @@ def launch_gemm(a, w, out, *, bias=None, flags: int = 0, resid=None, gate=None) 
     if resid is not None:
         _, _, ldr = _rows(resid, "linear residual")
         div, stride = _mod_rows(gate, m, n, "linear gate")
+    plan = tail_split(m, n, k)
+    # a gate that changes with the row block (stride != 0) keeps the plain tiling: the tail call
+    # would index its rows from zero
+    if plan is not None and (gate is None or stride == 0) and a.data_ptr() % 16 == 0 \
+            and w.data_ptr() % 16 == 0 and lda <= (1 << 22) and ldw <= (1 << 22):
+        # whole rounds of 256x256 tiles over the first rows, the tail rows as K slices filling one round
+        rows, tail_splits = plan
+        _call(
+            "kx_gemm_bf16", _ptr(a), lda, _ptr(w), ldw, _ptr(bias), _ptr(out), ldc, rows, n, k, flags,
+            _ptr(resid), ldr, _ptr(gate), div, stride, _stream(),
+        )
+        tail = m - rows
+        work = torch.empty(tail_splits * tail * n, dtype=torch.float32, device=a.device)
+        _call(
+            "kx_gemm_splitk_bf16", _ptr(a[rows:]), lda, _ptr(w), ldw, _ptr(bias), _ptr(out[rows:]), ldc, tail, n, k,
+            flags, _ptr(None if resid is None else resid[rows:]), ldr, _ptr(gate), div, stride, _ptr(work),
+            work.numel() * 4, tail_splits, _stream(),
+        )
+        return
     splits = splitk_splits(m, n, k)
     if splits > 1 and a.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0 and lda <= (1 << 22) and ldw <= (1 << 22):
         work = torch.empty(splits * m * n, dtype=torch.float32, device=a.device)
@@ -456,6 +475,33 @@ def launch_gemm_qknorm_rope(a, w, out, *, bias, q_end: int, k_end: int, norm_q, 
         _ptr(norm_q), _ptr(norm_k), KX_BF16 if norm_q.dtype == torch.bfloat16 else KX_F32, float(eps),
         float(weight_offset), _ptr(cos), _ptr(sin), table_ld, table_hs, table_rows, table_bs, _stream(),
     )
+
+
+def tail_split(m: int, n: int, k: int) -> tuple[int, int] | None:
+    """``(rows, splits)`` when a product's 256x256 tiles would end in a partial round of
+    workgroups (e.g. 9216 x 4096: 576 tiles, 2.25 rounds on 256 CUs): the first ``rows`` rows run as
+    whole rounds of 256x256 tiles, and the remaining rows as ``splits`` K slices of 256x256 tiles,
+    which fill one more round with a fraction of the work; the slices' fp32 partial products are
+    summed by the split-K reduction, which applies the epilogue. None when the product takes the
+    plain tiling."""
+    # the slices of the tail are a quarter of a tile's K or less: worth their partial products and
+    # reduction only for long K (the 9216 x 4096 x 16384 down projection: 1.33 -> 1.16 ms; at
+    # K = 4096 the tail costs more than the partial round it replaces)
+    if m < 2048 or n % 256 or n < 1024 or k < 8192:
+        return None
+    tiles_n = n // 256
+    rounds = (m // 256) * tiles_n // 256
+    if rounds < 1 or (rounds * 256) % tiles_n:
+        return None
+    rows = rounds * 256 // tiles_n * 256
+    tail_tiles = -(-(m - rows) // 256) * tiles_n
+    if tail_tiles == 0 or tail_tiles > 128:
+        return None
+    splits = 1
+    for cand in (2, 4, 8):
+        if tail_tiles * cand <= 256 and k % (32 * cand) == 0 and k // cand >= 512:
+            splits = cand
+    return (rows, splits) if splits > 1 else None
 
 
 def splitk_splits(m: int, n: int, k: int) -> int:

@@ -1810,7 +1810,12 @@ int run_splitk(const char* what, const void* a, int64_t lda, const void* w, int6
                void* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int epilogue, const void* resid,
                int64_t ldr, const float* gate, int64_t gate_div, int64_t gate_stride, float* parts, int splits,
                hipStream_t s) {
-  if (pick_lds_cfg(m, n) == 3)
+  // slices of 256x256 tiles for the tail rows of a large product (a few 256-row tiles across a wide
+  // N, each slice a quarter or less of K); up to 512 rows keep the 64x128 / 128x128 tiles
+  if (m > 512 && n >= 1024)
+    launch_splitk<256, 256>((const uint16_t*)a, lda, (const uint16_t*)w, ldw, parts, (int)m, (int)n, (int)k, splits,
+                            s);
+  else if (pick_lds_cfg(m, n) == 3)
     launch_splitk<64, 128>((const uint16_t*)a, lda, (const uint16_t*)w, ldw, parts, (int)m, (int)n, (int)k, splits, s);
   else
     launch_splitk<128, 128>((const uint16_t*)a, lda, (const uint16_t*)w, ldw, parts, (int)m, (int)n, (int)k, splits,

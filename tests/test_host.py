@@ -146,3 +146,24 @@ def test_workload_flops_match_baseline():
     f5 = workloads.flop_count(workloads.CONFIGS[5])
     assert f5["gemm"] / 1e9 == pytest.approx(12846.6, abs=0.2)
     assert workloads.CONFIGS[3].tokens == 9216 and workloads.CONFIGS[5].tokens == 27280
+
+
+def test_tail_split_rule():
+    from kinomlx_amd import _lib
+
+    # 9216 x 4096: 576 tiles of 256x256, 2.25 rounds on 256 CUs -> two whole rounds over 8192 rows,
+    # the 1024-row tail (64 tiles) as 4 K slices
+    assert _lib.tail_split(9216, 4096, 16384) == (8192, 4)
+    assert _lib.tail_split(4864, 4096, 8192) == (4096, 4)
+    assert _lib.tail_split(4352, 4096, 8192) == (4096, 8)
+    assert _lib.tail_split(9216, 4096, 4096) is None   # short K keeps the plain tiling
+    assert _lib.tail_split(8192, 4096, 16384) is None  # already whole rounds
+    assert _lib.tail_split(1024, 4096, 16384) is None  # under one round
+    assert _lib.tail_split(9216, 4000, 16384) is None  # N not a whole number of 256-wide tiles
+    for m, n, k in [(9216, 4096, 16384), (4864, 4096, 8192), (27280, 4096, 16384)]:
+        plan = _lib.tail_split(m, n, k)
+        if plan is None:
+            continue
+        rows, splits = plan
+        assert rows % 256 == 0 and (rows // 256) * (n // 256) % 256 == 0
+        assert k % (32 * splits) == 0 and -(-(m - rows) // 256) * (n // 256) * splits <= 256

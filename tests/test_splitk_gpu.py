@@ -47,3 +47,57 @@ def test_splitk_matches_oracle(device, m, n, k, epi):
     assert cosine(out, ref) > 0.99999
     bound = 2e-3 if got.dtype == torch.float32 else 2 ** -7 * max(1.0, np.abs(ref).max())
     assert max_abs(out, ref) <= bound, (max_abs(out, ref), bound)
+
+
+@pytest.mark.parametrize("m,n,k", [(4864, 4096, 8192), (4352, 4096, 8192)])
+@pytest.mark.parametrize("epi", ["plain", "gated_f32"])
+def test_tail_split_matches_oracle(device, m, n, k, epi):
+    """A long-K product split into whole rounds of 256x256 tiles plus K slices of the tail rows
+    (768 tail rows take the 256x256 slices, 256 tail rows the small-M slices): the head rows, the
+    rows either side of the split and every tail row against the FP32 oracle."""
+    rows, splits = _lib.tail_split(m, n, k)
+    x, w = _bf((m, k), 11), _bf((n, k), 12, 0.02)
+    sample = np.r_[0:64, rows - 64:m]
+    ref = oracle.linear(x[sample].float().numpy(), w.float().numpy())
+    kwargs = {}
+    if epi == "gated_f32":
+        resid = workloads.normal(13, "resid", (m, n))
+        gate = workloads.normal(14, "gate", (n,), 0.5)
+        kwargs = dict(residual=resid.to(device), gate=gate.to(device), out_dtype=torch.float32)
+        ref = resid[sample].numpy() + gate.numpy() * ref
+    timer = _lib.LaunchTimer()
+    _lib.set_timer(timer)
+    try:
+        got = fused_linear(x.to(device), w.to(device), None, **kwargs)
+    finally:
+        _lib.set_timer(None)
+    launches = [(name, args) for name, args, _ in timer.durations_ms()]
+    assert [name for name, _ in launches] == ["kx_gemm_bf16", "kx_gemm_splitk_bf16"]
+    assert launches[0][1][7] == rows and launches[1][1][7] == m - rows and launches[1][1][18] == splits
+    out = got.float().cpu().numpy()[sample]
+    assert cosine(out, ref) > 0.99999
+    bound = 2e-3 if got.dtype == torch.float32 else 2 ** -7 * max(1.0, np.abs(ref).max())
+    assert max_abs(out, ref) <= bound, (max_abs(out, ref), bound)
+
+
+def test_tail_split_keeps_plain_tiling_for_a_per_batch_gate(device):
+    """A gate that changes with the row block indexes rows from the product's first row: such a
+    product keeps the one plain launch."""
+    m, n, k = 4864, 4096, 8192
+    x, w = _bf((m, k), 15), _bf((n, k), 16, 0.02)
+    resid = workloads.normal(17, "resid", (2, m // 2, n)).to(device)
+    gate = workloads.normal(18, "gate", (2, 1, n), 0.5).to(device)
+    timer = _lib.LaunchTimer()
+    _lib.set_timer(timer)
+    try:
+        got = fused_linear(x.view(2, m // 2, k).to(device), w.to(device), None, residual=resid, gate=gate,
+                           out_dtype=torch.float32)
+    finally:
+        _lib.set_timer(None)
+    assert [name for name, _, _ in timer.durations_ms()] == ["kx_gemm_bf16"]
+    sample = np.r_[0:32, m // 2 - 32:m // 2 + 32, m - 32:m]
+    ref = oracle.linear(x[sample].float().numpy(), w.float().numpy())
+    g = gate.cpu().numpy()[np.where(sample < m // 2, 0, 1), 0]
+    ref = resid.view(m, n)[sample].cpu().numpy() + g * ref
+    out = got.view(m, n).float().cpu().numpy()[sample]
+    assert max_abs(out, ref) <= 2e-3, max_abs(out, ref)
