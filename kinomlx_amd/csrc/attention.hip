@@ -7,9 +7,12 @@
 // queries.
 //
 // K and V tiles of 64 keys go from global memory straight into LDS with global_load_lds_dwordx4
-// (no VGPR staging) through a ring of 4 stages: while tile i is consumed, tiles i+1 .. i+3 are in
-// flight. Waves 0-7 each issue 1/8 of a stage's DMA instructions; one workgroup barrier per tile
-// makes tile i visible and frees the buffer of tile i-1 for tile i+3.
+// (no VGPR staging) through a ring of 4 stages. Waves 0-7 each issue 1/8 of a stage's DMA
+// instructions; one workgroup barrier per tile makes a tile visible and frees an older buffer.
+// At D = 128 without a score bias the key loop is software-pipelined over 32-key blocks (the next
+// block's score MFMAs run beside this block's exps, the P V MFMAs beside the next block's max) and
+// tile i+1 becomes visible in the middle of tile i, with tile i+2 in flight; the other forms keep
+// one tile per iteration with tiles i+1 .. i+3 in flight.
 //
 // Scores are computed transposed, S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (A = 32 keys read from
 // LDS, B = the wave's 32 queries): the accumulator lane holds one query (lane % 32) and 16 of the
@@ -59,6 +62,17 @@ __device__ __forceinline__ void wait_vmcnt() {
 // transposing read hit distinct slots.
 template <int D> __device__ __forceinline__ int swz_k(int r) { return D == 128 ? (r & 15) : ((r >> 1) & 7); }
 template <int D> __device__ __forceinline__ int swz_v(int r) { return D == 128 ? 4 * (r & 3) : 4 * ((r >> 1) & 1); }
+
+// One 16-byte-per-lane global -> LDS copy (global_load_lds_dwordx4; M0 holds the wave's LDS
+// address). Written as inline assembly so that the compiler's wait-count pass does not see an LDS
+// write pending on vmcnt: as the builtin, every transposing LDS read after it got a vmcnt(0) wait
+// for the copies just issued (the pass cannot tell the ring's buffers apart), which stalled the
+// issuing waves for a whole memory round trip per tile. The kernel orders the copies itself:
+// wait_vmcnt for a tile's copies, then the workgroup barrier, before any wave reads the tile.
+__device__ __forceinline__ void dma16(const void* src, const void* lds) {
+  const uint32_t m0 = (uint32_t)(uintptr_t)KX_LDS(lds);
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+}
 
 __device__ __forceinline__ bf16x8 read_vt(const uint8_t* p, int second) {
   const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(p));
@@ -134,28 +148,35 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
     qf[s] = *reinterpret_cast<const bf16x8*>(Qb + (int64_t)qrow * ldq + (2 * s + lhalf) * 8);
 
   // DMA: instruction g = wave * PER + i of a stage fills RPI rows of the K tile (g < INST / 2) or
-  // the V tile; lane -> row lane / CPR, slot lane % CPR, which holds chunk slot ^ swz(row). Keys
-  // past the end re-read the last key (in bounds; masked below).
+  // the V tile, a wave's PER instructions all of one kind; lane -> row lane / CPR, slot
+  // lane % CPR, which holds chunk slot ^ swz(row). A lane's source is the tile's scalar base plus a
+  // 32-bit byte offset kept across the loop. Keys past the end re-read the last key (in bounds;
+  // masked below).
+  static_assert((INST / 2) % PER == 0, "a DMA wave fills one kind of tile");
   const int r_in = lane / CPR, slot = lane % CPR;
-  int dma_row[PER];
-  uint32_t dma_col[PER];
-  bool dma_isv[PER];
+  const bool wave_isv = wave * PER >= INST / 2;
+  const char* dma_base = wave_isv ? Vb : Kb;
+  const int64_t dma_ld = (wave_isv ? ldv : ldk) * 2;  // bytes per key (< 2^25, checked on the host)
+  const int row0 = (wave_isv ? wave * PER - INST / 2 : wave * PER) * RPI;
+  uint32_t dma_off[PER];
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
-    const int g = wave * PER + i;
-    const bool isv = g >= INST / 2;
-    const int r = (isv ? g - INST / 2 : g) * RPI + r_in;
-    dma_isv[i] = isv;
-    dma_row[i] = r;
-    dma_col[i] = (uint32_t)((slot ^ (isv ? swz_v<D>(r) : swz_k<D>(r))) * 16);
+    const int r = row0 + i * RPI + r_in;
+    dma_off[i] = (uint32_t)(r * dma_ld) + (uint32_t)((slot ^ (wave_isv ? swz_v<D>(r) : swz_k<D>(r))) * 16);
   }
   auto issue = [&](uint8_t* buf, int j0) {
     if (!dma_wave) return;
+    const char* base = dma_base + (int64_t)j0 * dma_ld;
+    if (j0 + BKV <= tk) {
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int key = min(j0 + dma_row[i], tk - 1);
-      const char* src = (dma_isv[i] ? Vb + (int64_t)key * ldv * 2 : Kb + (int64_t)key * ldk * 2) + dma_col[i];
-      __builtin_amdgcn_global_load_lds((const void*)src, KX_LDS(buf + (wave * PER + i) * 1024), 16, 0, 0);
+      for (int i = 0; i < PER; ++i)
+        dma16(base + dma_off[i], buf + (wave * PER + i) * 1024);
+    } else {
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int over = max(j0 + row0 + i * RPI + r_in - (tk - 1), 0);  // rows past the last key
+        dma16(base + dma_off[i] - (int64_t)over * dma_ld, buf + (wave * PER + i) * 1024);
+      }
     }
   };
 
@@ -184,118 +205,220 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
   float l_run = 0.0f;       // this lane's partial row sum
 
   const int ntiles = (tk + BKV - 1) / BKV;
+  if constexpr (D == 128 && !BIAS) {
+    // Software pipeline over blocks of 32 keys (block c = key half c % 2 of tile c / 2): the MFMAs
+    // of block c + 1's scores run between the exps of block c, and the P V MFMAs of block c between
+    // the max of block c + 1, so the matrix core and the VALU of a wave work side by side instead
+    // of in turns. Tile t becomes visible at a barrier before the scores of its first block (in
+    // the middle of tile t - 1); that barrier also frees the buffer of tile t - 2 (every wave has
+    // finished its P V products), which takes tile t + NSTAGE - 2.
+    auto buf = [&](int t) { return smem + (t % NSTAGE) * STAGE; };
 #pragma unroll
-  for (int p = 0; p < NSTAGE - 1; ++p) issue(smem + p * STAGE, min(p, ntiles - 1) * BKV);
-  int cur_i = 0;
-  for (int it = 0; it < ntiles; ++it) {
-    // tile it has landed for this wave; after the barrier for every wave, and every wave is done
-    // with tile it-1, whose buffer takes tile it+3 (past the end the last tile is re-read, which
-    // keeps the vmcnt arithmetic uniform)
-    wait_vmcnt<(NSTAGE - 2) * PER>();
-    KX_BARRIER();
-    const uint8_t* cur = smem + cur_i * STAGE;
-    issue(smem + (cur_i == 0 ? NSTAGE - 1 : cur_i - 1) * STAGE, min(it + NSTAGE - 1, ntiles - 1) * BKV);
-
-    // S^T = K Q^T for two 32-key blocks
-    f32x16 s[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int e = 0; e < 16; ++e) s[kb][e] = 0.0f;
-#pragma unroll
-      for (int st = 0; st < QS; ++st) {
-        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(cur + koff[st] + kb * 32 * ROWB);
-        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], s[kb], 0, 0, 0);
-      }
-    }
-    const int j0 = it * BKV;
-    if constexpr (BIAS) {
-      // lane: query qrow, keys j0 + 32 kb + 8 g + 4 lhalf + (0..3) = elements 4 g .. 4 g + 3
-      const uint16_t* brow =
-          bias.ptr + (int64_t)b * bias.bs + (int64_t)h * bias.hs + (int64_t)qrow * bias.qs + j_begin;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int key = j0 + kb * 32 + 8 * g + 4 * lhalf;
-          float bv[4];
-          if (key + 3 < tk) {
-            const uint2 w = *reinterpret_cast<const uint2*>(brow + key);
-            bv[0] = lo_f(w.x); bv[1] = hi_f(w.x); bv[2] = lo_f(w.y); bv[3] = hi_f(w.y);
-          } else {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) bv[i] = key + i < tk ? bf2f(brow[key + i]) : 0.0f;
-          }
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float add = bv[i] * bias.mul;
-            s[kb][4 * g + i] += add < -1e20f ? -1e30f : add;
-          }
-        }
-    }
-    if (j0 + BKV > tk) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int key = j0 + kb * 32 + 8 * (e >> 2) + 4 * lhalf + (e & 3);
-          if (key >= tk) s[kb][e] = -INFINITY;
-        }
-    }
-    float tmax = s[0][0];
-#pragma unroll
-    for (int e = 1; e < 16; ++e) tmax = fmaxf(tmax, s[0][e]);
-#pragma unroll
-    for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, s[1][e]);
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    if (__any(tmax * scale_log2 > m_run * scale_log2 + LAZY_TH || m_run == -INFINITY)) {
-      const float m_new = fmaxf(m_run, tmax);
-      const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
-      l_run *= alpha;
-#pragma unroll
-      for (int i = 0; i < DB; ++i)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) o[i][e] *= alpha;
-      m_run = m_new;
-    }
-
-    // P^T in bf16 as the B operand: elements 8hf .. 8hf+7 of block kb
-    const float mc = m_run * scale_log2;
-    const float removed_p = m_run == -1e30f ? 1.0f : 0.0f;  // p of a removed key (bias variant)
-    bf16x8 pb[2][2];
-    float psum = 0.0f;
-    auto pexp = [&](int kb, int hf, int e) {
-      float p = __builtin_amdgcn_exp2f(fmaf(s[kb][8 * hf + e], scale_log2, -mc));
-      if constexpr (BIAS) p = s[kb][8 * hf + e] == -1e30f ? removed_p : p;
-      psum += p;
-      pb[kb][hf][e] = (__bf16)p;
+    for (int p = 0; p < NSTAGE - 2; ++p) issue(buf(p), min(p, ntiles - 1) * BKV);
+    auto arrive = [&](int t) {
+      wait_vmcnt<(NSTAGE - 3) * PER>();  // tile t has landed (tile t + 1 may be in flight)
+      KX_BARRIER();
+      issue(buf(t + NSTAGE - 2), min(t + NSTAGE - 2, ntiles - 1) * BKV);
     };
-    if constexpr (D == 128 && !BIAS) {
-      // O^T += V^T P^T, 16 keys per step; step ts = 2 kb + hf uses P^T block pb[kb][hf]. The exps
-      // of keys 32..63 run between the MFMAs of keys 0..31 (the VALU beside the matrix core), and
-      // each step's V^T fragment is read one step ahead (1.40 -> 1.38 ms at 9216^2; the score-bias
-      // form keeps the plain order, whose live values already exceed the register budget)
+    // At D = 128 the K swizzle (row & 15) and the V swizzle (4 (row & 3)) flip chunk-index bits
+    // above the lane's own, so the offsets of steps st and dim blocks db are the first offset with
+    // st << 5, db << 6 XORed in: one VALU per read instead of 12 registers held across the loop
+    const int koff0 = koff[0], voff0 = voff[0];
+    auto kfrag = [&](const uint8_t* tile, int kb, int st) {
+      return *reinterpret_cast<const bf16x8*>(tile + (koff0 ^ (st << 5)) + kb * 32 * ROWB);
+    };
+    auto vfrag = [&](const uint8_t* tile, int db, int ts16) {
+      return read_vt(tile + (voff0 ^ (db << 6)) + ts16 * 16 * ROWB, 8 * ROWB);
+    };
+    // keys past the end of block c score -inf
+    auto mask = [&](f32x16& sc, int c) {
+      if (32 * (c + 1) > tk) {
 #pragma unroll
-      for (int hf = 0; hf < 2; ++hf)
+        for (int e = 0; e < 16; ++e)
+          if (32 * c + 8 * (e >> 2) + 4 * lhalf + (e & 3) >= tk) sc[e] = -INFINITY;
+      }
+    };
+
+    arrive(0);
+    f32x16 sc;  // the current block's scores
 #pragma unroll
-        for (int e = 0; e < 8; ++e) pexp(0, hf, e);
-      bf16x8 vf[2];
-      vf[0] = read_vt(cur + voff[0], 8 * ROWB);
+    for (int e = 0; e < 16; ++e) sc[e] = 0.0f;
+#pragma unroll
+    for (int st = 0; st < QS; ++st) sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfrag(buf(0), 0, st), qf[st], sc, 0, 0, 0);
+    mask(sc, 0);
+    {
+      float tmax = sc[0];
+#pragma unroll
+      for (int e = 1; e < 16; ++e) tmax = fmaxf(tmax, sc[e]);
+      m_run = fmaxf(tmax, __shfl_xor(tmax, 32, 64));  // finite: block 0 holds key 0
+    }
+
+    // block c (key half kb of tile `cur`) with the scores of block cn (key half nkb of tile `nxt`)
+    auto step = [&](const uint8_t* cur, int kb, const uint8_t* nxt, int nkb, int cn) {
+      const float mc = m_run * scale_log2;
+      bf16x8 pb[2];
+      float psum = 0.0f;
+      f32x16 sn;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sn[e] = 0.0f;
+      // each exp is pinned where it is placed (the empty asm takes its result): otherwise the
+      // compiler sinks the exps past the score MFMAs to their first use in the P V products
+      auto pexp = [&](int e) {
+        float p = __builtin_amdgcn_exp2f(fmaf(sc[e], scale_log2, -mc));
+        asm volatile("" : "+v"(p));
+        psum += p;
+        pb[e >> 3][e & 7] = (__bf16)p;
+      };
+      // VALU work is spread so that each MFMA has about its own duration of it beside it: the
+      // exps of elements 0..PA-1 between the 8 score MFMAs, the rest between the 4 P V MFMAs of
+      // the first 16 keys (which need only elements 0..7), the max of block cn between the last 4
+      constexpr int PA = 10;
+      bf16x8 kf[2];
+      kf[0] = kfrag(nxt, nkb, 0);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int q = 0; q < 4 * DB; ++q) {
-        const int ts = q / DB, db = q % DB;
-        if (q + 1 < 4 * DB)
-          vf[(q + 1) & 1] = read_vt(cur + voff[(q + 1) % DB] + 16 * ((q + 1) / DB) * ROWB, 8 * ROWB);
+      for (int st = 0; st < QS; ++st) {
+        if (st + 1 < QS) kf[(st + 1) & 1] = kfrag(nxt, nkb, st + 1);
         __builtin_amdgcn_sched_barrier(0);
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[q & 1], pb[ts >> 1][ts & 1], o[db], 0, 0, 0);
-        if (q < 2 * DB) {
-          pexp(1, (2 * q) / 8, (2 * q) % 8);
-          pexp(1, (2 * q + 1) / 8, (2 * q + 1) % 8);
+        sn = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[st & 1], qf[st], sn, 0, 0, 0);
+#pragma unroll
+        for (int e = st * PA / QS; e < (st + 1) * PA / QS; ++e) pexp(e);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      mask(sn, cn);
+      // O^T += V^T P^T over the block's two 16-key steps, V^T read one MFMA ahead
+      bf16x8 vf[2];
+      vf[0] = vfrag(cur, 0, 2 * kb);
+      float tmax = -INFINITY;
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int q = 0; q < 2 * DB; ++q) {
+        const int ts = q / DB, db = q % DB;
+        if (q + 1 < 2 * DB)
+          vf[(q + 1) & 1] = vfrag(cur, (q + 1) % DB, 2 * kb + (q + 1) / DB);
+        __builtin_amdgcn_sched_barrier(0);
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[q & 1], pb[ts], o[db], 0, 0, 0);
+        if (q < DB) {
+#pragma unroll
+          for (int e = PA + q * (16 - PA) / DB; e < PA + (q + 1) * (16 - PA) / DB; ++e) pexp(e);
+        } else {
+#pragma unroll
+          for (int e = (q - DB) * 16 / DB; e < (q - DB + 1) * 16 / DB; ++e) tmax = fmaxf(tmax, sn[e]);
+          asm volatile("" : "+v"(tmax));
         }
         __builtin_amdgcn_sched_barrier(0);
       }
-    } else {
+      l_run += psum;
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      if (__any(tmax * scale_log2 > m_run * scale_log2 + LAZY_TH)) {
+        const float m_new = fmaxf(m_run, tmax);
+        const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
+        l_run *= alpha;
+#pragma unroll
+        for (int i = 0; i < DB; ++i)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) o[i][e] *= alpha;
+        m_run = m_new;
+      }
+      sc = sn;
+    };
+
+    for (int t = 0; t < ntiles; ++t) {
+      const uint8_t* cur = buf(t);
+      step(cur, 0, cur, 1, 2 * t + 1);
+      // the last block recomputes the scores of block 2t, already seen (its max cannot move the
+      // running max); they are not used
+      const bool more = t + 1 < ntiles;
+      if (more) arrive(t + 1);
+      step(cur, 1, more ? buf(t + 1) : cur, 0, more ? 2 * t + 2 : 2 * t);
+    }
+  } else {
+#pragma unroll
+    for (int p = 0; p < NSTAGE - 1; ++p) issue(smem + p * STAGE, min(p, ntiles - 1) * BKV);
+    int cur_i = 0;
+    for (int it = 0; it < ntiles; ++it) {
+      // tile it has landed for this wave; after the barrier for every wave, and every wave is done
+      // with tile it-1, whose buffer takes tile it+3 (past the end the last tile is re-read, which
+      // keeps the vmcnt arithmetic uniform)
+      wait_vmcnt<(NSTAGE - 2) * PER>();
+      KX_BARRIER();
+      const uint8_t* cur = smem + cur_i * STAGE;
+      issue(smem + (cur_i == 0 ? NSTAGE - 1 : cur_i - 1) * STAGE, min(it + NSTAGE - 1, ntiles - 1) * BKV);
+
+      // S^T = K Q^T for two 32-key blocks
+      f32x16 s[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s[kb][e] = 0.0f;
+#pragma unroll
+        for (int st = 0; st < QS; ++st) {
+          const bf16x8 kf = *reinterpret_cast<const bf16x8*>(cur + koff[st] + kb * 32 * ROWB);
+          s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], s[kb], 0, 0, 0);
+        }
+      }
+      const int j0 = it * BKV;
+      if constexpr (BIAS) {
+        // lane: query qrow, keys j0 + 32 kb + 8 g + 4 lhalf + (0..3) = elements 4 g .. 4 g + 3
+        const uint16_t* brow =
+            bias.ptr + (int64_t)b * bias.bs + (int64_t)h * bias.hs + (int64_t)qrow * bias.qs + j_begin;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int key = j0 + kb * 32 + 8 * g + 4 * lhalf;
+            float bv[4];
+            if (key + 3 < tk) {
+              const uint2 w = *reinterpret_cast<const uint2*>(brow + key);
+              bv[0] = lo_f(w.x); bv[1] = hi_f(w.x); bv[2] = lo_f(w.y); bv[3] = hi_f(w.y);
+            } else {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) bv[i] = key + i < tk ? bf2f(brow[key + i]) : 0.0f;
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float add = bv[i] * bias.mul;
+              s[kb][4 * g + i] += add < -1e20f ? -1e30f : add;
+            }
+          }
+      }
+      if (j0 + BKV > tk) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int key = j0 + kb * 32 + 8 * (e >> 2) + 4 * lhalf + (e & 3);
+            if (key >= tk) s[kb][e] = -INFINITY;
+          }
+      }
+      float tmax = s[0][0];
+#pragma unroll
+      for (int e = 1; e < 16; ++e) tmax = fmaxf(tmax, s[0][e]);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) tmax = fmaxf(tmax, s[1][e]);
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      if (__any(tmax * scale_log2 > m_run * scale_log2 + LAZY_TH || m_run == -INFINITY)) {
+        const float m_new = fmaxf(m_run, tmax);
+        const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
+        l_run *= alpha;
+#pragma unroll
+        for (int i = 0; i < DB; ++i)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) o[i][e] *= alpha;
+        m_run = m_new;
+      }
+
+      // P^T in bf16 as the B operand: elements 8hf .. 8hf+7 of block kb
+      const float mc = m_run * scale_log2;
+      const float removed_p = m_run == -1e30f ? 1.0f : 0.0f;  // p of a removed key (bias variant)
+      bf16x8 pb[2][2];
+      float psum = 0.0f;
+      auto pexp = [&](int kb, int hf, int e) {
+        float p = __builtin_amdgcn_exp2f(fmaf(s[kb][8 * hf + e], scale_log2, -mc));
+        if constexpr (BIAS) p = s[kb][8 * hf + e] == -1e30f ? removed_p : p;
+        psum += p;
+        pb[kb][hf][e] = (__bf16)p;
+      };
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -310,9 +433,9 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
           const bf16x8 vf = read_vt(cur + voff[db] + 16 * ts * ROWB, 8 * ROWB);
           o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb[ts >> 1][ts & 1], o[db], 0, 0, 0);
         }
+      l_run += psum;
+      cur_i = cur_i + 1 == NSTAGE ? 0 : cur_i + 1;
     }
-    l_run += psum;
-    cur_i = cur_i + 1 == NSTAGE ? 0 : cur_i + 1;
   }
   wait_vmcnt<0>();  // the re-read tiles past the end have landed before the workgroup ends
 
@@ -446,6 +569,7 @@ int attention_entry(const char* name, const void* q, int64_t ldq, const void* k,
   const int64_t width = heads * head_dim, kv_width = kv_heads * head_dim;
   KX_REQUIRE(ldq >= width && ldk >= kv_width && ldv >= kv_width && ldo >= width,
              "%s: row strides must cover heads * head_dim", name);
+  KX_REQUIRE(ldk < (1ll << 24) && ldv < (1ll << 24), "%s: key/value row strides must be below 2^24", name);
   KX_REQUIRE(ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0 && ldo % 4 == 0 && aligned16(q) &&
                  aligned16(k) && aligned16(v) && aligned8(o),
              "%s: q/k/v rows must be 16-byte and o rows 8-byte aligned", name);

@@ -64,13 +64,21 @@ def test_fully_masked_row_averages_values(device):
     assert np.allclose(got[0, 3].float().cpu().numpy(), mean, atol=1e-2)
 
 
-def test_unmasked_bias_of_zero_is_bit_identical_to_no_mask(device):
-    heads, tq, tk, dim = 4, 300, 200, 128
+@pytest.mark.parametrize("dim", [64, 128])
+def test_unmasked_bias_of_zero_matches_no_mask(device, dim):
+    # D = 64 runs one key loop for both forms (bit-identical); at D = 128 the unbiased kernel is
+    # software-pipelined over 32-key blocks (its running max moves per block, its row sums add per
+    # 16 keys), so the two forms agree to the kernel's per-op bar rather than bit for bit
+    heads, tq, tk = 4, 300, 200
     q, k, v = _bf((1, tq, heads * dim), 10), _bf((1, tk, heads * dim), 11), _bf((1, tk, heads * dim), 12)
     plain = batched_attention(q.to(device), k.to(device), v.to(device), heads=heads)
     zero = batched_attention(q.to(device), k.to(device), v.to(device), heads=heads,
                              mask=torch.zeros((1, 1, 1, tk), dtype=torch.bfloat16, device=device))
-    assert torch.equal(plain, zero)
+    if dim == 64:
+        assert torch.equal(plain, zero)
+    else:
+        a, b = plain.float().cpu().numpy(), zero.float().cpu().numpy()
+        assert cosine(a, b) > 0.99999 and max_abs(a, b) < 2e-2, (cosine(a, b), max_abs(a, b))
 
 
 def test_preprocessor_mask_conversions(device):
