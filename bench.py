@@ -316,6 +316,10 @@ def main() -> int:
     return 0
 
 
+_DISPATCHES = {"kx_gemm_splitk_bf16": 2, "kx_gemm_splitk_noalloc_bf16": 2, "kx_attention_split_fwd_bf16": 2,
+               "kx_all_finite": 2}
+
+
 def profile_summary(root: str) -> int:
     """Markdown table of one block's kernels from rocprofv3 runs of this script: ``root/trace``
     (``--kernel-trace``), ``root/mfma`` (``--pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE``),
@@ -329,7 +333,13 @@ def profile_summary(root: str) -> int:
 
     with open(os.path.join(root, "launches.json")) as fh:
         launches = json.load(fh)
-    period = len(launches)
+    # kernel dispatches per launch: the split forms add their reduction / merge pass, the finite
+    # check its flag initialisation
+    groups, period = [], 0
+    for entry in launches:
+        count = _DISPATCHES.get(entry.get("entry", ""), 1)
+        groups.append(range(period, period + count))
+        period += count
 
     def kx_rows(sub, pattern):
         files = glob.glob(os.path.join(root, sub, "**", pattern), recursive=True)
@@ -392,18 +402,19 @@ def profile_summary(root: str) -> int:
     print("|---|---|---|---|---|---|---|---|---|---|---|")
     total_us = 0.0
     for i, entry in enumerate(launches):
-        avg = statistics.mean(dur[i])
+        g = groups[i]
+        avg = sum(statistics.mean(dur[j]) for j in g)
         total_us += avg
-        kernel = kname[i][0].replace("kx::(anonymous namespace)::", "").split("(")[0]
+        kernel = " + ".join(kname[j][0].replace("kx::(anonymous namespace)::", "").split("(")[0] for j in g)
         tf = entry["flops"] / (avg * 1e-6) / 1e12 if entry["flops"] else None
         gbs = entry["bytes"] / (avg * 1e-6) / 1e9 if entry["bytes"] else None
         b = None
         if busy:
             # SQ_VALU_MFMA_BUSY_CYCLES sums the 1024 SIMDs; GRBM_GUI_ACTIVE sums the 8 XCDs' cycles
-            cyc = statistics.mean(gui[i]) / 8
-            b = statistics.mean(busy[i]) / (1024 * cyc) if cyc else None
-        fm = statistics.mean(fpos[i]) * 1024 * fscale / 1e6 if fpos and fscale else None
-        wm = statistics.mean(wpos[i]) * 1024 * wscale / 1e6 if wpos and wscale else None
+            cyc = sum(statistics.mean(gui[j]) for j in g) / 8
+            b = sum(statistics.mean(busy[j]) for j in g) / (1024 * cyc) if cyc else None
+        fm = sum(statistics.mean(fpos[j]) for j in g) * 1024 * fscale / 1e6 if fpos and fscale else None
+        wm = sum(statistics.mean(wpos[j]) for j in g) * 1024 * wscale / 1e6 if wpos and wscale else None
 
         def f(x, fmt):
             return fmt.format(x) if x is not None else "-"
