@@ -64,8 +64,16 @@ __device__ __forceinline__ float fast_exp(float x) {
   return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
 }
 __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+// The same function with -2 log2(e) folded into the inner polynomial and the clamp (+-10 on the
+// inner argument is +-20 log2(e) on the exp2 argument): 7 VALU per value instead of 11. Its error
+// against the exact clamped tanh GELU is the same as the unfolded form's (both <= 2.5e-6 relative
+// over [-12, 12], set by the exp at large negative x).
 __device__ __forceinline__ float fast_gelu_tanh(float x) {
-  return x * fast_rcp(1.0f + fast_exp(-2.0f * gelu_inner(x)));
+  constexpr float A = -2.0f * 1.4426950408889634f * 0.7978845608028654f;
+  constexpr float B = A * 0.044715f;
+  constexpr float LIM = 20.0f * 1.4426950408889634f;
+  const float z = fminf(fmaxf(x * fmaf(B, x * x, A), -LIM), LIM);
+  return x * fast_rcp(1.0f + __builtin_amdgcn_exp2f(z));
 }
 __device__ __forceinline__ float fast_silu(float x) { return x * fast_rcp(1.0f + fast_exp(-x)); }
 __device__ __forceinline__ float fast_sigmoid2(float x) { return 2.0f * fast_rcp(1.0f + fast_exp(-x)); }
