@@ -516,15 +516,25 @@ __device__ __forceinline__ void epilogue_store4(float v[4], int m, int n, int N,
   }
 }
 
+// The activation as a compile-time choice (ACT = the epilogue's activation code; -1: chosen at
+// run time per value).
+template <int ACT>
+__device__ __forceinline__ float act_c(float v, int act) {
+  if constexpr (ACT == 1) return fast_gelu_tanh(v);
+  else if constexpr (ACT == 2) return fast_silu(v);
+  else if constexpr (ACT == 0) return v;
+  else return apply_act(v, act);
+}
+
 // One full-tile epilogue row piece: bias + activation (+ gated residual), then the store of 4
 // consecutive columns. Values by value so that nothing of the caller's frame is addressed.
-template <int GMODE, bool OUTF32, typename ResidT>
+template <int GMODE, bool OUTF32, int ACT, typename ResidT>
 __device__ __forceinline__ void epi_row4(float4 a4, ResidT res, float b0, float b1, float b2, float b3,
                                          int act, float4 gv, char* dst) {
   float v[4] = {a4.x + b0, a4.y + b1, a4.z + b2, a4.w + b3};
-  if (act) {
+  if (ACT != 0) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = apply_act(v[e], act);
+    for (int e = 0; e < 4; ++e) v[e] = act_c<ACT>(v[e], act);
   }
   if constexpr (GMODE != 0) {
     float rv[4];
@@ -1167,49 +1177,58 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
       float4 g4c = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       if (GMODE != 0 && gate_const) g4c = *reinterpret_cast<const float4*>(epi.gate + (mrow0 / gdiv) * gstride + n);
       char* cbase = reinterpret_cast<char*>(C) + ((int64_t)mrow0 * ldc + n) * (OUTF32 ? 4 : 2);
-      if constexpr (!PREF) {
+      // the rows with the activation fixed at compile time (a run-time choice per value put a
+      // chain of scalar branches around every value and serialised them)
+      auto full_rows = [&](auto act_tag) {
+        constexpr int ACT = decltype(act_tag)::value;
+        if constexpr (!PREF) {
 #pragma unroll 4
-        for (int r = rr; r < WT_M; r += RPI_EP) {
-          ResidT res{};
-          float4 gv = g4c;
-          if constexpr (GMODE != 0) {
-            res = *reinterpret_cast<const ResidT*>(rbase + ((int64_t)r * epi.ldr + h * HALF_N) * resid_es);
-            if (!gate_const) {
-              const int64_t grow = gdiv == 1 ? (int64_t)(mrow0 + r) : (int64_t)(mrow0 + r) / gdiv;
-              gv = *reinterpret_cast<const float4*>(epi.gate + grow * gstride + n);
-            }
-          }
-          epi_row4<GMODE, OUTF32>(*reinterpret_cast<const float4*>(ep + r * PITCH + 4 * q), res, b4[0], b4[1],
-                                  b4[2], b4[3], act, gv, cbase + (int64_t)r * ldc * (OUTF32 ? 4 : 2));
-        }
-      } else {
-        // groups of 4 rows: their staged reads together, then their stores (bounded registers:
-        // the prefetched residual stays live, the staged values of one group at a time)
-        constexpr int GR = 4;
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-          if (c > 0) { KX_PREFETCH_RESID(h, c) }
-#pragma unroll
-          for (int k0 = 0; k0 < PF; k0 += GR) {
-            float4 a4[GR];
-#pragma unroll
-            for (int k = 0; k < GR; ++k)
-              a4[k] = *reinterpret_cast<const float4*>(ep + (rr + (c * PF + k0 + k) * RPI_EP) * PITCH + 4 * q);
-#pragma unroll
-            for (int k = 0; k < GR; ++k) {
-              const int r = rr + (c * PF + k0 + k) * RPI_EP;
-              float4 gv = g4c;
+          for (int r = rr; r < WT_M; r += RPI_EP) {
+            ResidT res{};
+            float4 gv = g4c;
+            if constexpr (GMODE != 0) {
+              res = *reinterpret_cast<const ResidT*>(rbase + ((int64_t)r * epi.ldr + h * HALF_N) * resid_es);
               if (!gate_const) {
                 const int64_t grow = gdiv == 1 ? (int64_t)(mrow0 + r) : (int64_t)(mrow0 + r) / gdiv;
                 gv = *reinterpret_cast<const float4*>(epi.gate + grow * gstride + n);
               }
-              epi_row4<GMODE, OUTF32>(a4[k], rpre[k0 + k], b4[0], b4[1], b4[2], b4[3], act, gv,
-                                      cbase + (int64_t)r * ldc * (OUTF32 ? 4 : 2));
             }
-            __builtin_amdgcn_sched_barrier(0);
+            epi_row4<GMODE, OUTF32, ACT>(*reinterpret_cast<const float4*>(ep + r * PITCH + 4 * q), res, b4[0],
+                                         b4[1], b4[2], b4[3], act, gv, cbase + (int64_t)r * ldc * (OUTF32 ? 4 : 2));
+          }
+        } else {
+          // groups of 4 rows: their staged reads together, then their stores (bounded registers:
+          // the prefetched residual stays live, the staged values of one group at a time)
+          constexpr int GR = 4;
+#pragma unroll
+          for (int c = 0; c < NCH; ++c) {
+            if (c > 0) { KX_PREFETCH_RESID(h, c) }
+#pragma unroll
+            for (int k0 = 0; k0 < PF; k0 += GR) {
+              float4 a4[GR];
+#pragma unroll
+              for (int k = 0; k < GR; ++k)
+                a4[k] = *reinterpret_cast<const float4*>(ep + (rr + (c * PF + k0 + k) * RPI_EP) * PITCH + 4 * q);
+#pragma unroll
+              for (int k = 0; k < GR; ++k) {
+                const int r = rr + (c * PF + k0 + k) * RPI_EP;
+                float4 gv = g4c;
+                if (!gate_const) {
+                  const int64_t grow = gdiv == 1 ? (int64_t)(mrow0 + r) : (int64_t)(mrow0 + r) / gdiv;
+                  gv = *reinterpret_cast<const float4*>(epi.gate + grow * gstride + n);
+                }
+                epi_row4<GMODE, OUTF32, ACT>(a4[k], rpre[k0 + k], b4[0], b4[1], b4[2], b4[3], act, gv,
+                                             cbase + (int64_t)r * ldc * (OUTF32 ? 4 : 2));
+              }
+              __builtin_amdgcn_sched_barrier(0);
+            }
           }
         }
-      }
+      };
+      if (act == 0) full_rows(std::integral_constant<int, 0>{});
+      else if (GMODE == 0 && act == 1) full_rows(std::integral_constant<int, GMODE == 0 ? 1 : -1>{});
+      else if (GMODE == 0 && act == 2) full_rows(std::integral_constant<int, GMODE == 0 ? 2 : -1>{});
+      else full_rows(std::integral_constant<int, -1>{});
     } else {
 #pragma unroll 2
       for (int r = rr; r < WT_M; r += RPI_EP) {
