@@ -1179,8 +1179,9 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
       char* cbase = reinterpret_cast<char*>(C) + ((int64_t)mrow0 * ldc + n) * (OUTF32 ? 4 : 2);
       // the rows with the activation fixed at compile time (a run-time choice per value put a
       // chain of scalar branches around every value and serialised them)
-      auto full_rows = [&](auto act_tag) {
+      auto full_rows = [&](auto act_tag, auto gate_tag) {
         constexpr int ACT = decltype(act_tag)::value;
+        constexpr bool GC = decltype(gate_tag)::value;  // one gate row covers the wave's rows
         if constexpr (!PREF) {
 #pragma unroll 4
           for (int r = rr; r < WT_M; r += RPI_EP) {
@@ -1188,7 +1189,7 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
             float4 gv = g4c;
             if constexpr (GMODE != 0) {
               res = *reinterpret_cast<const ResidT*>(rbase + ((int64_t)r * epi.ldr + h * HALF_N) * resid_es);
-              if (!gate_const) {
+              if constexpr (!GC) {
                 const int64_t grow = gdiv == 1 ? (int64_t)(mrow0 + r) : (int64_t)(mrow0 + r) / gdiv;
                 gv = *reinterpret_cast<const float4*>(epi.gate + grow * gstride + n);
               }
@@ -1213,7 +1214,7 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
               for (int k = 0; k < GR; ++k) {
                 const int r = rr + (c * PF + k0 + k) * RPI_EP;
                 float4 gv = g4c;
-                if (!gate_const) {
+                if constexpr (!GC) {
                   const int64_t grow = gdiv == 1 ? (int64_t)(mrow0 + r) : (int64_t)(mrow0 + r) / gdiv;
                   gv = *reinterpret_cast<const float4*>(epi.gate + grow * gstride + n);
                 }
@@ -1225,10 +1226,13 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
           }
         }
       };
-      if (act == 0) full_rows(std::integral_constant<int, 0>{});
-      else if (GMODE == 0 && act == 1) full_rows(std::integral_constant<int, GMODE == 0 ? 1 : -1>{});
-      else if (GMODE == 0 && act == 2) full_rows(std::integral_constant<int, GMODE == 0 ? 2 : -1>{});
-      else full_rows(std::integral_constant<int, -1>{});
+      using Const = std::true_type;
+      using PerRow = std::integral_constant<bool, GMODE == 0>;  // GMODE 0 reads no gate
+      if (act == 0 && gate_const) full_rows(std::integral_constant<int, 0>{}, Const{});
+      else if (act == 0) full_rows(std::integral_constant<int, 0>{}, PerRow{});
+      else if (GMODE == 0 && act == 1) full_rows(std::integral_constant<int, GMODE == 0 ? 1 : -1>{}, Const{});
+      else if (GMODE == 0 && act == 2) full_rows(std::integral_constant<int, GMODE == 0 ? 2 : -1>{}, Const{});
+      else full_rows(std::integral_constant<int, -1>{}, PerRow{});
     } else {
 #pragma unroll 2
       for (int r = rr; r < WT_M; r += RPI_EP) {
