@@ -104,12 +104,17 @@ struct SplitOut {
   int chunk;  // keys per slice, a multiple of BKV
 };
 
-template <int D, bool BIAS, bool SPLIT>
+// RES (D = 128, no bias, no split, at most NSTAGE key tiles): every key tile is copied into LDS
+// once and stays there while the workgroup runs up to qpw consecutive query tiles of its head; the
+// waves need no barrier after the copy, so one wave's query load and output store overlap the
+// other waves' products.
+template <int D, bool BIAS, bool SPLIT, bool RES = false>
 __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
     const uint16_t* __restrict__ Q, int64_t ldq, const uint16_t* __restrict__ K, int64_t ldk,
     const uint16_t* __restrict__ V, int64_t ldv, uint16_t* __restrict__ O, int64_t ldo, int tq,
     int tk_all, int heads, int kv_group, float scale_log2, const uint16_t* __restrict__ gate,
-    int64_t ld_gate, int qtiles, ScoreBias bias, SplitOut split) {
+    int64_t ld_gate, int qtiles, int qpw, ScoreBias bias, SplitOut split) {
+  static_assert(!RES || (D == 128 && !BIAS && !SPLIT), "resident keys: the pipelined form only");
   constexpr int ROWB = D * 2;             // bytes per K / V row
   constexpr int CPR = ROWB / 16;          // 16-byte chunks per row
   constexpr int RPI = 64 / CPR;           // rows per DMA instruction
@@ -127,7 +132,8 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
   const int lrow = lane & 31, lhalf = lane >> 5;
   // work order: XCD-contiguous so the workgroups of one XCD share few heads' K/V in its L2
   const int t = xcd_remap(blockIdx.x, gridDim.x);
-  const int qt = t % qtiles, bh = t / qtiles;
+  const int wph = RES ? (qtiles + qpw - 1) / qpw : qtiles;  // workgroups per (batch, head)
+  const int qt = RES ? (t % wph) * qpw : t % qtiles, bh = t / wph;
   const int h = bh % heads, b = bh / heads;
   const uint16_t* Qb = Q + (int64_t)b * tq * ldq + (int64_t)h * D;
   const int hk = h / kv_group;  // grouped-query attention: kv_group query heads share a K/V head
@@ -140,8 +146,8 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
   const char* Kb = reinterpret_cast<const char*>(K + ((int64_t)b * tk_all + j_begin) * ldk + (int64_t)hk * D);
   const char* Vb = reinterpret_cast<const char*>(V + ((int64_t)b * tk_all + j_begin) * ldv + (int64_t)hk * D);
 
-  const int q0 = qt * BQ + wave * 32;
-  const int qrow = min(q0 + lrow, tq - 1);
+  int q0 = qt * BQ + wave * 32;
+  int qrow = min(q0 + lrow, tq - 1);
   bf16x8 qf[QS];
 #pragma unroll
   for (int s = 0; s < QS; ++s)
@@ -153,24 +159,36 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
   // 32-bit byte offset kept across the loop. Keys past the end re-read the last key (in bounds;
   // masked below).
   static_assert((INST / 2) % PER == 0, "a DMA wave fills one kind of tile");
-  const int r_in = lane / CPR, slot = lane % CPR;
   const bool wave_isv = wave * PER >= INST / 2;
   const char* dma_base = wave_isv ? Vb : Kb;
   const int64_t dma_ld = (wave_isv ? ldv : ldk) * 2;  // bytes per key (< 2^25, checked on the host)
   const int row0 = (wave_isv ? wave * PER - INST / 2 : wave * PER) * RPI;
-  uint32_t dma_off[PER];
+  // streaming form: the lane's byte offsets of its PER copies, kept across the key loop
+  const int r_in = lane / CPR, slot = lane % CPR;
+  uint32_t dma_off[RES ? 1 : PER];
+  if constexpr (!RES) {
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int r = row0 + i * RPI + r_in;
-    dma_off[i] = (uint32_t)(r * dma_ld) + (uint32_t)((slot ^ (wave_isv ? swz_v<D>(r) : swz_k<D>(r))) * 16);
+    for (int i = 0; i < PER; ++i) {
+      const int r = row0 + i * RPI + r_in;
+      dma_off[i] = (uint32_t)(r * dma_ld) + (uint32_t)((slot ^ (wave_isv ? swz_v<D>(r) : swz_k<D>(r))) * 16);
+    }
   }
   auto issue = [&](uint8_t* buf, int j0) {
     if (!dma_wave) return;
     const char* base = dma_base + (int64_t)j0 * dma_ld;
-    if (j0 + BKV <= tk) {
+    if constexpr (RES) {
+      // the resident form copies each tile once, before its loop: offsets computed here
 #pragma unroll
-      for (int i = 0; i < PER; ++i)
-        dma16(base + dma_off[i], buf + (wave * PER + i) * 1024);
+      for (int i = 0; i < PER; ++i) {
+        const int r = row0 + i * RPI + r_in;
+        const int key = min(j0 + r, tk - 1);  // keys past the end re-read the last key
+        const uint32_t off = (uint32_t)((key - j0) * dma_ld) +
+                             (uint32_t)((slot ^ (wave_isv ? swz_v<D>(r) : swz_k<D>(r))) * 16);
+        dma16(base + off, buf + (wave * PER + i) * 1024);
+      }
+    } else if (j0 + BKV <= tk) {
+#pragma unroll
+      for (int i = 0; i < PER; ++i) dma16(base + dma_off[i], buf + (wave * PER + i) * 1024);
     } else {
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
@@ -213,8 +231,10 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
     // the middle of tile t - 1); that barrier also frees the buffer of tile t - 2 (every wave has
     // finished its P V products), which takes tile t + NSTAGE - 2.
     auto buf = [&](int t) { return smem + (t % NSTAGE) * STAGE; };
+    if constexpr (!RES) {
 #pragma unroll
-    for (int p = 0; p < NSTAGE - 2; ++p) issue(buf(p), min(p, ntiles - 1) * BKV);
+      for (int p = 0; p < NSTAGE - 2; ++p) issue(buf(p), min(p, ntiles - 1) * BKV);
+    }
     auto arrive = [&](int t) {
       wait_vmcnt<(NSTAGE - 3) * PER>();  // tile t has landed (tile t + 1 may be in flight)
       KX_BARRIER();
@@ -239,22 +259,27 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
       }
     };
 
-    arrive(0);
     f32x16 sc;  // the current block's scores
+    // block 0's scores and the running max they start
+    auto first_block = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int e = 0; e < 16; ++e) sc[e] = 0.0f;
+      for (int e = 0; e < 16; ++e) sc[e] = 0.0f;
 #pragma unroll
-    for (int st = 0; st < QS; ++st) sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfrag(buf(0), 0, st), qf[st], sc, 0, 0, 0);
-    mask(sc, 0);
-    {
+      for (int st = 0; st < QS; ++st)
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfrag(buf(0), 0, st), qf[st], sc, 0, 0, 0);
+      mask(sc, 0);
       float tmax = sc[0];
 #pragma unroll
       for (int e = 1; e < 16; ++e) tmax = fmaxf(tmax, sc[e]);
       m_run = fmaxf(tmax, __shfl_xor(tmax, 32, 64));  // finite: block 0 holds key 0
+    };
+    if constexpr (!RES) {
+      arrive(0);
+      first_block();
     }
 
     // block c (key half kb of tile `cur`) with the scores of block cn (key half nkb of tile `nxt`)
-    auto step = [&](const uint8_t* cur, int kb, const uint8_t* nxt, int nkb, int cn) {
+    auto step = [&](const uint8_t* cur, int kb, const uint8_t* nxt, int nkb, int cn) __attribute__((always_inline)) {
       const float mc = m_run * scale_log2;
       bf16x8 pb[2];
       float psum = 0.0f;
@@ -323,6 +348,52 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
       sc = sn;
     };
 
+    if constexpr (RES) {
+      // every key tile, copied once (at most NSTAGE of them, checked on the host); then each query
+      // tile runs the same block sequence without barriers
+      for (int p = 0; p < ntiles; ++p) issue(buf(p), p * BKV);
+      wait_vmcnt<0>();
+      KX_BARRIER();
+      const int nq = min(qpw, qtiles - qt);
+      for (int qi = 0; qi < nq; ++qi) {
+        if (qi > 0) {
+          q0 += BQ;
+          qrow = min(q0 + lrow, tq - 1);
+#pragma unroll
+          for (int st = 0; st < QS; ++st)
+            qf[st] = *reinterpret_cast<const bf16x8*>(Qb + (int64_t)qrow * ldq + (2 * st + lhalf) * 8);
+#pragma unroll
+          for (int i = 0; i < DB; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) o[i][e] = 0.0f;
+          l_run = 0.0f;
+        }
+        first_block();
+        for (int t = 0; t < ntiles; ++t) {
+          const uint8_t* cur = buf(t);
+          step(cur, 0, cur, 1, 2 * t + 1);
+          const bool more = t + 1 < ntiles;
+          step(cur, 1, more ? buf(t + 1) : cur, 0, more ? 2 * t + 2 : 2 * t);
+        }
+        const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+        const int q = q0 + lrow;
+        if (q < tq) {
+          float scale_out = 1.0f / l_tot;
+          if (gate) scale_out *= bf2f(gate[((int64_t)b * tq + q) * ld_gate + h]);
+          uint16_t* orow = O + ((int64_t)b * tq + q) * ldo + (int64_t)h * D;
+#pragma unroll
+          for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              uint2 w;
+              w.x = pack2(o[db][4 * g + 0] * scale_out, o[db][4 * g + 1] * scale_out);
+              w.y = pack2(o[db][4 * g + 2] * scale_out, o[db][4 * g + 3] * scale_out);
+              *reinterpret_cast<uint2*>(orow + db * 32 + 8 * g + 4 * lhalf) = w;
+            }
+        }
+      }
+      return;
+    }
     for (int t = 0; t < ntiles; ++t) {
       const uint8_t* cur = buf(t);
       step(cur, 0, cur, 1, 2 * t + 1);
@@ -506,15 +577,32 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
   *reinterpret_cast<uint2*>(O + ((int64_t)b * tq + q) * ldo + (int64_t)h * D + d) = w2;
 }
 
-template <int D, bool BIAS, bool SPLIT>
+template <int D, bool BIAS, bool SPLIT, bool RES = false>
 void launch_attn_t(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv, void* o,
                    int64_t ldo, int64_t tq, int64_t tk, int64_t heads, int64_t kv_heads, float scale,
                    const void* gate, int64_t ld_gate, ScoreBias bias, SplitOut split, dim3 grid, int qtiles,
-                   hipStream_t s) {
-  attn_fwd_kernel<D, BIAS, SPLIT><<<grid, NWAVE * 64, 0, s>>>(
+                   hipStream_t s, int qpw = 1) {
+  attn_fwd_kernel<D, BIAS, SPLIT, RES><<<grid, NWAVE * 64, 0, s>>>(
       (const uint16_t*)q, ldq, (const uint16_t*)k, ldk, (const uint16_t*)v, ldv, (uint16_t*)o, ldo, (int)tq,
       (int)tk, (int)heads, (int)(heads / kv_heads), scale * 1.4426950408889634f, (const uint16_t*)gate, ld_gate,
-      qtiles, bias, split);
+      qtiles, qpw, bias, split);
+}
+
+// Query tiles per workgroup for the resident-key form: the fewest workgroup rounds on the 256 CUs
+// times the tiles each workgroup runs, ties to more tiles per workgroup (each keeps its keys).
+int resident_qpw(int64_t qtiles, int64_t heads_total) {
+  constexpr int64_t kCUs = 256;
+  int best = 1;
+  int64_t best_cost = -1;
+  for (int qpw = 1; qpw <= 8 && qpw <= qtiles; ++qpw) {
+    const int64_t groups = heads_total * ((qtiles + qpw - 1) / qpw);
+    const int64_t cost = (groups + kCUs - 1) / kCUs * qpw;
+    if (best_cost < 0 || cost <= best_cost) {
+      best = qpw;
+      best_cost = cost;
+    }
+  }
+  return best;
 }
 
 template <int D>
@@ -538,6 +626,12 @@ int launch_attn(const void* q, int64_t ldq, const void* k, int64_t ldk, const vo
   } else if (bias.ptr) {
     launch_attn_t<D, true, false>(q, ldq, k, ldk, v, ldv, o, ldo, tq, tk, heads, kv_heads, scale, gate, ld_gate,
                                   bias, split, grid, qtiles, s);
+  } else if (D == 128 && tk <= NSTAGE * BKV) {
+    // few keys (a text context): they stay in LDS while a workgroup runs several query tiles
+    const int qpw = resident_qpw(qtiles, heads * batch);
+    const dim3 rgrid((unsigned)((qtiles + qpw - 1) / qpw * heads * batch));
+    launch_attn_t<D, false, false, D == 128>(q, ldq, k, ldk, v, ldv, o, ldo, tq, tk, heads, kv_heads, scale, gate,
+                                             ld_gate, bias, split, rgrid, qtiles, s, qpw);
   } else {
     launch_attn_t<D, false, false>(q, ldq, k, ldk, v, ldv, o, ldo, tq, tk, heads, kv_heads, scale, gate, ld_gate,
                                    bias, split, grid, qtiles, s);

@@ -654,6 +654,20 @@ def test_attention_gate_batch_and_strided_inputs(device):
         assert rel_l2(_np(got[i]), ref) < 6e-3
 
 
+@pytest.mark.parametrize("tk", [256, 250, 64, 1])
+def test_attention_resident_keys_over_several_query_tiles(device, tk):
+    """At most 256 keys (a text context) stay in LDS while a workgroup runs several query tiles
+    of its head: 4000 queries x 32 heads is 11 tiles of 384 per head, two per workgroup (the last
+    one alone), with a per-(query, head) gate, against the FP32 oracle."""
+    tq, heads, dim = 4000, 32, 128
+    q, k, v = _attn_inputs(tq, tk, dim, heads, 40 + tk)
+    gate = oracle.to_bf16(_rng(41).uniform(0, 2, (tq, heads)).astype(F32))
+    got = dense_attention.batched_attention(_bf(q, device)[None], _bf(k, device)[None], _bf(v, device)[None],
+                                            heads=heads, gate=_bf(gate, device)[None])
+    ref = (oracle.attention(q, k, v, heads=heads).reshape(tq, heads, dim) * gate[:, :, None]).reshape(tq, -1)
+    assert rel_l2(_np(got[0]), ref) < 6e-3 and cosine(_np(got[0]), ref) > 0.9999
+
+
 def test_attention_self_attention_at_ltx_width(device):
     q, k, v = _attn_inputs(1100, 1100, 128, 32, 13)
     got = dense_attention.dense_attention(_bf(q, device), _bf(k, device), _bf(v, device), heads=32)
