@@ -279,7 +279,8 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
     }
 
     // block c (key half kb of tile `cur`) with the scores of block cn (key half nkb of tile `nxt`)
-    auto step = [&](const uint8_t* cur, int kb, const uint8_t* nxt, int nkb, int cn) __attribute__((always_inline)) {
+    auto step = [&](const uint8_t* cur, int kb, const uint8_t* nxt, int nkb,
+                    int cn) __attribute__((always_inline)) {
       const float mc = m_run * scale_log2;
       bf16x8 pb[2];
       float psum = 0.0f;
