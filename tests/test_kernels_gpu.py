@@ -668,6 +668,22 @@ def test_attention_resident_keys_over_several_query_tiles(device, tk):
     assert rel_l2(_np(got[0]), ref) < 6e-3 and cosine(_np(got[0]), ref) > 0.9999
 
 
+def test_attention_resident_keys_grouped_query_batched(device):
+    """The resident-key form with grouped-query heads (32 query heads over 8 key/value heads)
+    and a batch of two: each workgroup reads its own batch's and group's keys."""
+    b, tq, tk, heads, kv_heads, dim = 2, 900, 100, 32, 8, 128
+    r = _rng(42)
+    q = oracle.to_bf16(r.standard_normal((b, tq, heads * dim)).astype(F32))
+    k, v = (oracle.to_bf16(r.standard_normal((b, tk, kv_heads * dim)).astype(F32)) for _ in range(2))
+    got = dense_attention.batched_attention(_bf(q, device), _bf(k, device), _bf(v, device), heads=heads,
+                                            kv_heads=kv_heads)
+    group = heads // kv_heads
+    for i in range(b):
+        kx, vx = (np.repeat(t[i].reshape(tk, kv_heads, dim), group, axis=1).reshape(tk, heads * dim) for t in (k, v))
+        ref = oracle.attention(q[i], kx, vx, heads=heads)
+        assert rel_l2(_np(got[i]), ref) < 6e-3
+
+
 def test_attention_self_attention_at_ltx_width(device):
     q, k, v = _attn_inputs(1100, 1100, 128, 32, 13)
     got = dense_attention.dense_attention(_bf(q, device), _bf(k, device), _bf(v, device), heads=32)
