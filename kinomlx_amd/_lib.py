@@ -495,12 +495,22 @@ def tail_split(m: int, n: int, k: int) -> tuple[int, int] | None:
         return None
     rows = rounds * 256 // tiles_n * 256
     tail_tiles = -(-(m - rows) // 256) * tiles_n
-    if tail_tiles == 0 or tail_tiles > 128:
+    if tail_tiles == 0 or tail_tiles > 256:
         return None
     splits = 1
-    for cand in (2, 4, 8):
-        if tail_tiles * cand <= 256 and k % (32 * cand) == 0 and k // cand >= 512:
-            splits = cand
+    if tail_tiles <= 128:
+        # the most slices that still fit one round
+        for cand in (2, 4, 8):
+            if tail_tiles * cand <= 256 and k % (32 * cand) == 0 and k // cand >= 512:
+                splits = cand
+    else:
+        # a tail over half a round (27 280 rows: 176 tiles): the slice count with the fewest
+        # rounds of 1/splits tiles, under the one full round the tail takes unsplit
+        best = 1.0
+        for cand in (2, 4, 8):
+            cost = -(-tail_tiles * cand // 256) / cand
+            if cost < best - 1e-9 and k % (32 * cand) == 0 and k // cand >= 512:
+                splits, best = cand, cost
     return (rows, splits) if splits > 1 else None
 
 

@@ -160,10 +160,11 @@ def test_tail_split_rule():
     assert _lib.tail_split(8192, 4096, 16384) is None  # already whole rounds
     assert _lib.tail_split(1024, 4096, 16384) is None  # under one round
     assert _lib.tail_split(9216, 4000, 16384) is None  # N not a whole number of 256-wide tiles
-    for m, n, k in [(9216, 4096, 16384), (4864, 4096, 8192), (27280, 4096, 16384)]:
-        plan = _lib.tail_split(m, n, k)
-        if plan is None:
-            continue
-        rows, splits = plan
+    # 27 280 rows: a 176-tile tail; 4 slices take 3 rounds of quarter tiles (0.75 of a round)
+    assert _lib.tail_split(27280, 4096, 16384) == (24576, 4)
+    for m, n, k in [(9216, 4096, 16384), (4864, 4096, 8192), (27280, 4096, 16384), (5376, 4096, 16384)]:
+        rows, splits = _lib.tail_split(m, n, k)
+        tail_tiles = -(-(m - rows) // 256) * (n // 256)
         assert rows % 256 == 0 and (rows // 256) * (n // 256) % 256 == 0
-        assert k % (32 * splits) == 0 and -(-(m - rows) // 256) * (n // 256) * splits <= 256
+        assert k % (32 * splits) == 0 and k // splits >= 512
+        assert tail_tiles * splits <= 256 or -(-tail_tiles * splits // 256) / splits < 1.0

@@ -49,12 +49,13 @@ def test_splitk_matches_oracle(device, m, n, k, epi):
     assert max_abs(out, ref) <= bound, (max_abs(out, ref), bound)
 
 
-@pytest.mark.parametrize("m,n,k", [(4864, 4096, 8192), (4352, 4096, 8192)])
+@pytest.mark.parametrize("m,n,k", [(4864, 4096, 8192), (4352, 4096, 8192), (6400, 4096, 8192)])
 @pytest.mark.parametrize("epi", ["plain", "gated_f32"])
 def test_tail_split_matches_oracle(device, m, n, k, epi):
     """A long-K product split into whole rounds of 256x256 tiles plus K slices of the tail rows
-    (768 tail rows take the 256x256 slices, 256 tail rows the small-M slices): the head rows, the
-    rows either side of the split and every tail row against the FP32 oracle."""
+    (768 tail rows take the 256x256 slices, 256 tail rows the small-M slices, 2304 tail rows over
+    half a round take 8 slices in 5 rounds): the head rows, the rows either side of the split and
+    every tail row against the FP32 oracle."""
     rows, splits = _lib.tail_split(m, n, k)
     x, w = _bf((m, k), 11), _bf((n, k), 12, 0.02)
     sample = np.r_[0:64, rows - 64:m]
