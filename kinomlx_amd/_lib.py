@@ -481,9 +481,9 @@ def tail_split(m: int, n: int, k: int) -> tuple[int, int] | None:
     """``(rows, splits)`` when a product's 256x256 tiles would end in a partial round of
     workgroups (e.g. 9216 x 4096: 576 tiles, 2.25 rounds on 256 CUs): the first ``rows`` rows run as
     whole rounds of 256x256 tiles, and the remaining rows as ``splits`` K slices of 256x256 tiles,
-    which fill one more round with a fraction of the work; the slices' fp32 partial products are
-    summed by the split-K reduction, which applies the epilogue. None when the product takes the
-    plain tiling."""
+    which take one round (or, for a tail over half a round, a few rounds) of a fraction of a
+    tile's work each; the slices' fp32 partial products are summed by the split-K reduction, which
+    applies the epilogue. None when the product takes the plain tiling."""
     # the slices of the tail are a quarter of a tile's K or less: worth their partial products and
     # reduction only for long K (the 9216 x 4096 x 16384 down projection: 1.33 -> 1.16 ms; at
     # K = 4096 the tail costs more than the partial round it replaces)
