@@ -431,10 +431,14 @@ def launch_gemm(a, w, out, *, bias=None, flags: int = 0, resid=None, gate=None) 
         )
         tail = m - rows
         work = torch.empty(tail_splits * tail * n, dtype=torch.float32, device=a.device)
+        # row ``rows`` of each operand from its flattened row stride (the leading axes of an N-D
+        # tensor are not rows)
+        a_tail = a.data_ptr() + rows * lda * a.element_size()
+        out_tail = out.data_ptr() + rows * ldc * out.element_size()
+        resid_tail = None if resid is None else resid.data_ptr() + rows * ldr * resid.element_size()
         _call(
-            "kx_gemm_splitk_bf16", _ptr(a[rows:]), lda, _ptr(w), ldw, _ptr(bias), _ptr(out[rows:]), ldc, tail, n, k,
-            flags, _ptr(None if resid is None else resid[rows:]), ldr, _ptr(gate), div, stride, _ptr(work),
-            work.numel() * 4, tail_splits, _stream(),
+            "kx_gemm_splitk_bf16", a_tail, lda, _ptr(w), ldw, _ptr(bias), out_tail, ldc, tail, n, k,
+            flags, resid_tail, ldr, _ptr(gate), div, stride, _ptr(work), work.numel() * 4, tail_splits, _stream(),
         )
         return
     splits = splitk_splits(m, n, k)

@@ -304,6 +304,11 @@ class QuantizedLinear:
         _check_mode(mode, group_size, bits)
         if (biases is None) != (mode == "mxfp8"):
             raise ValueError("affine weights carry biases and mxfp8 weights none")
+        # the kernels reinterpret the scale bits: bf16 scale / bias pairs (affine), E8M0 bytes (mxfp8)
+        if mode == "mxfp8" and scales.dtype != torch.uint8:
+            raise ValueError(f"mxfp8 scales must be uint8 E8M0 exponents, got {scales.dtype}")
+        if mode == "affine" and (scales.dtype != torch.bfloat16 or biases.dtype != torch.bfloat16):
+            raise ValueError(f"affine scales and biases must be bfloat16, got {scales.dtype} and {biases.dtype}")
         self.weight = weight
         self.scales = scales
         self.biases = biases

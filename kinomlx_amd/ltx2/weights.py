@@ -219,6 +219,8 @@ def load_transformer(path: Path | str, device, *, heads: int = 32, head_dim: int
             biases = take(f"{quant}.biases") if f"{quant}.biases" in params else None
             if pretransposed and mode == "mxfp8":
                 return PretransposedQuantizedLinear(words, scales, bias, group_size=gs, bits=bits, mode=mode)
+            if mode == "affine":  # the affine kernels read bf16 scales and biases
+                scales = _bf16(scales)
             return QuantizedLinear(words, scales, None if biases is None else _bf16(biases), bias, group_size=gs,
                                    bits=bits, mode=mode)
         layout = f"{LAYOUT_KEY_PREFIX}{prefix}.weight_t"
@@ -252,9 +254,16 @@ def load_transformer(path: Path | str, device, *, heads: int = 32, head_dim: int
     dim = int(patchify.shape[0])
     if dim != heads * head_dim:
         raise ValueError(f"{path}: hidden size {dim} does not match {heads} heads x {head_dim}")
+    # a linear's weight may be stored plain, pretransposed (``__layout__.<name>.weight_t``, which
+    # the reference's preparation writes for every top-level AdaLN linear, layout.py:11-20) or
+    # packed (``__quant__.<name>.weight``)
+    def has_linear(prefix: str) -> bool:
+        return any(key in params for key in (f"{prefix}.weight", f"{LAYOUT_KEY_PREFIX}{prefix}.weight_t",
+                                             f"{QUANT_KEY_PREFIX}{prefix}.weight"))
+
     model = LTXAVModel(num_layers=len(layers), video_heads=heads, video_head_dim=head_dim,
                        video_in_channels=int(patchify.shape[1]), video_out_channels=int(proj_out.shape[0]),
-                       video_context_dim=dim, use_prompt_adaln_single="prompt_adaln_single.linear.weight" in params)
+                       video_context_dim=dim, use_prompt_adaln_single=has_linear("prompt_adaln_single.linear"))
     model.patchify_proj = linear("patchify_proj")
     model.proj_out = linear("proj_out")
     model.scale_shift_table = take("scale_shift_table")

@@ -108,9 +108,14 @@ os.environ.setdefault("PYTHONHASHSEED", "0")
 # 0.05-0.15 for any bf16 execution, the reference's own included; which elements carry them depends
 # on every rounding decision upstream, so no FP32 evaluation reproduces one bf16 execution there.
 # Those blocks are held to the north-star cosine, to the relative-L2 bound the reference sets for
-# its bf16 kernels (tests/models/ltx2/test_dense_attention.py:49-64: < 6e-3), and to the noise a
-# bf16 execution that stores bf16 exactly where this build does must carry: the RMS error against
-# FP32 at most 1.25x that of the FP32 evaluation rounded at this build's bf16 points.
+# its bf16 kernels (tests/models/ltx2/test_dense_attention.py:49-64: < 6e-3), to the noise a
+# bf16 execution that stores bf16 exactly where this build does must carry (the RMS error against
+# FP32 at most 1.25x that of the FP32 evaluation rounded at this build's bf16 points), and
+# elementwise to the reference's own arithmetic: no element may miss the FP32 evaluation by more
+# than the reference's bf16 graph (every array MLX materialises rounded to bf16,
+# kinomlx/models/ltx2/transformer/transformer.py:16-45) misses it on the same inputs, beyond the
+# output's own rounding. Each kernel stage at D = 4096 is held to the literal 2e-2 on its own in
+# tests/test_block_stages_gpu.py.
 BLOCK_REL_L2 = 6e-3
 KX_NOISE_FACTOR = 1.25
 
@@ -118,14 +123,17 @@ KX_NOISE_FACTOR = 1.25
 def assert_block_parity(got, ref, what: str, *, ref_kx=None, graph=None, fp32_out: bool = False,
                         small: bool = True) -> None:
     """Block parity against the FP32 evaluation ``ref``: the fixed block bar where bf16 storage
-    admits it (``small``: D <= 1024); otherwise the cosine, ``BLOCK_REL_L2`` and the storage-point
-    noise bound against ``ref_kx`` (the FP32 evaluation rounded where this build stores bf16).
-    ``graph``: the reference's own bf16 execution, printed for comparison only."""
+    admits it (``small``: D <= 1024); otherwise the cosine, ``BLOCK_REL_L2``, the storage-point
+    noise bound against ``ref_kx`` (the FP32 evaluation rounded where this build stores bf16), and,
+    with ``graph`` (the reference's own bf16 execution on the same inputs), the elementwise anchor:
+    the largest error beyond the bf16 output rounding is at most the graph's (an FP32 ``got`` gets
+    no rounding allowance: its max abs error is held to the graph's excess)."""
     if small:
         assert_block_bar(got, ref, what, fp32_out=fp32_out, context=graph)
         return
     e = block_errors(got, ref)
     note = ""
+    c = None
     if graph is not None:
         c = block_errors(graph, ref)
         note = f" | reference bf16 graph: rel_l2 {c['rel_l2']:.3g} max_abs {c['max_abs']:.4g} excess {c['excess']:.4g}"
@@ -137,3 +145,6 @@ def assert_block_parity(got, ref, what: str, *, ref_kx=None, graph=None, fp32_ou
     assert e["cosine"] >= BLOCK_COS_MIN, (what, e)
     assert e["rel_l2"] <= BLOCK_REL_L2, (what, e)
     assert e["rms"] <= KX_NOISE_FACTOR * k["rms"], (what, e["rms"], k["rms"])
+    if c is not None:
+        mine = e["max_abs"] if fp32_out else e["excess"]
+        assert mine <= c["excess"], (what, "elementwise error beyond the reference bf16 graph's", mine, c["excess"])

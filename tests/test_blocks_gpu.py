@@ -8,10 +8,15 @@ Bars (``tests.conftest.assert_block_parity``), against the FP32 evaluation:
   bf16 output's own rounding, |got - ref| <= 2e-2 + ulp_bf16(ref) / 2; with the block's output
   kept in FP32 (the block takes and returns the residual stream in its input's dtype) the literal
   max |got - ref| <= 2e-2.
-* D = 4096 (configs 3-5): cosine >= 0.9995, relative L2 <= 6e-3, and an RMS error at most 1.25x
+* D = 4096 (configs 3-5): cosine >= 0.9995, relative L2 <= 6e-3, an RMS error at most 1.25x
   the rounding noise of the FP32 evaluation rounded where this build stores bf16
-  (``rounding_mode="kx"``); the max abs error is printed beside the reference's own bf16 graph.
+  (``rounding_mode="kx"``), and elementwise no element further from the FP32 evaluation (beyond
+  the output's bf16 rounding) than the reference's own bf16 graph's worst element on the same
+  inputs. ``test_block_stages_gpu.py`` holds every kernel stage of the config-3/4 blocks to the
+  literal 2e-2 on its own.
 """
+
+import dataclasses
 
 import numpy as np
 import pytest
@@ -80,7 +85,7 @@ def test_ltx_block_matches_oracle(device, spec):
     small = spec.dim <= 1024
     assert_block_parity(got, ref, f"ltx {spec.dim} bits={spec.bits}", ref_kx=kx, graph=graph, small=small)
     got32 = _run_block(spec, p, inputs, pe, device, fp32=True)
-    assert_block_parity(got32, ref, "  fp32 out", ref_kx=kx, fp32_out=True, small=small)
+    assert_block_parity(got32, ref, "  fp32 out", ref_kx=kx, graph=graph, fp32_out=True, small=small)
 
 
 def test_ltx_block_unfused_projections_agree_with_fused(device):
@@ -93,11 +98,16 @@ def test_ltx_block_unfused_projections_agree_with_fused(device):
     assert torch.equal(fused.x, plain.x)
 
 
-@pytest.mark.parametrize("config", [3, 4])
+FULL_SIZE = {"3": workloads.CONFIGS[3], "4": workloads.CONFIGS[4],
+             "4-int8": dataclasses.replace(workloads.CONFIGS[4], bits=8)}
+
+
+@pytest.mark.parametrize("config", list(FULL_SIZE))
 def test_ltx_block_full_9216_tokens_matches_fp32_evaluation(device, config):
-    """Config 3 (bf16 weights) and config 4 (every linear int4, group 64) at full size: 9216
-    video tokens, 256 text tokens, D = 4096, 32 x 128; bf16 output and FP32 output."""
-    spec = workloads.CONFIGS[config]
+    """Config 3 (bf16 weights) and config 4 (every linear int4, and its int8 variant, group 64)
+    at full size: 9216 video tokens, 256 text tokens, D = 4096, 32 x 128; bf16 output and FP32
+    output."""
+    spec = FULL_SIZE[config]
     p, op, inputs, pe = ltx_case(spec)
     block = workloads.build_ltx_block(spec, p, device)
     got = _run_block(spec, p, inputs, pe, device, block=block)
@@ -105,7 +115,8 @@ def test_ltx_block_full_9216_tokens_matches_fp32_evaluation(device, config):
     del block
     ref, kx, graph = _torch_eval(spec, op, inputs, pe, device)
     assert_block_parity(got, ref, f"config{config} full block", ref_kx=kx, graph=graph, small=False)
-    assert_block_parity(got32, ref, f"config{config} full block, fp32 out", ref_kx=kx, fp32_out=True, small=False)
+    assert_block_parity(got32, ref, f"config{config} full block, fp32 out", ref_kx=kx, graph=graph, fp32_out=True,
+                        small=False)
 
 
 def _chunked_attention_fp32(q, k, v, heads):
@@ -146,5 +157,5 @@ def test_config5_int4_block_matches_fp32_evaluation(device):
     spec = workloads.CONFIGS[5]
     p, op, inputs, pe = ltx_case(spec)
     got = _run_block(spec, p, inputs, pe, device)
-    ref, kx, _ = _torch_eval(spec, op, inputs, pe, device, graph=False)
-    assert_block_parity(got, ref, "config5 int4 full block", ref_kx=kx, small=False)
+    ref, kx, graph = _torch_eval(spec, op, inputs, pe, device)
+    assert_block_parity(got, ref, "config5 int4 full block", ref_kx=kx, graph=graph, small=False)

@@ -69,8 +69,8 @@ def test_double_block_matches_oracle(device, spec):
     _check(_np(t_out[0]), rt, kt, gt, "text", fp32_bar=small)
     i32, t32 = _run_double(spec, p, inputs, device, fp32=True)
     assert i32.dtype == torch.float32
-    _check(_np(i32[0]), ri, ki, None, "  image fp32 out", fp32_out=True, fp32_bar=small)
-    _check(_np(t32[0]), rt, kt, None, "  text fp32 out", fp32_out=True, fp32_bar=small)
+    _check(_np(i32[0]), ri, ki, gi, "  image fp32 out", fp32_out=True, fp32_bar=small)
+    _check(_np(t32[0]), rt, kt, gt, "  text fp32 out", fp32_out=True, fp32_bar=small)
 
 
 def test_config1_block_full_size_matches_oracle(device):
@@ -122,7 +122,7 @@ def test_single_block_matches_oracle(device, dim, heads, hidden):
     _check(_np(got[0]), ref, kx, graph, "single", fp32_bar=small)
     got32 = block(x.to(device).float(), mod, tables)
     assert got32.dtype == torch.float32
-    _check(_np(got32[0]), ref, kx, None, "  single fp32 out", fp32_out=True, fp32_bar=small)
+    _check(_np(got32[0]), ref, kx, graph, "  single fp32 out", fp32_out=True, fp32_bar=small)
 
 
 def test_config2_double_then_single_full_size_matches_fp32_evaluation(device):
@@ -156,7 +156,7 @@ def test_config2_double_then_single_full_size_matches_fp32_evaluation(device):
             outs[mode] = _torch_ref.flux_single_block(sp, torch.cat([rt, ri]), tp["single_mod"], rope_d, spec.heads,
                                                       spec.dim, rounding_mode=mode).cpu().numpy()
     _check(got, outs[None], outs["kx"], outs["graph"], "config2 double+single", fp32_bar=False)
-    _check(got32, outs[None], outs["kx"], None, "config2 double+single fp32 out", fp32_out=True, fp32_bar=False)
+    _check(got32, outs[None], outs["kx"], outs["graph"], "config2 double+single fp32 out", fp32_out=True, fp32_bar=False)
 
 
 # ---- the standalone operator surface ---------------------------------------------------------

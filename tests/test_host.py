@@ -168,3 +168,16 @@ def test_tail_split_rule():
         assert rows % 256 == 0 and (rows // 256) * (n // 256) % 256 == 0
         assert k % (32 * splits) == 0 and k // splits >= 512
         assert tail_tiles * splits <= 256 or -(-tail_tiles * splits // 256) / splits < 1.0
+
+
+def test_quantized_layers_refuse_scales_the_kernels_would_misread():
+    """The kernels reinterpret the scale bits: affine layers take bf16 scales and biases, mxfp8
+    layers uint8 E8M0 exponents; any other dtype is refused instead of read as the wrong bits."""
+    words = torch.zeros((32, 8), dtype=torch.int32)
+    good = torch.zeros((32, 1), dtype=torch.bfloat16)
+    quantized.QuantizedLinear(words, good, good, group_size=64, bits=4)
+    for scales, biases in ((good.half(), good), (good.float(), good), (good, good.half())):
+        with pytest.raises(ValueError, match="bfloat16"):
+            quantized.QuantizedLinear(words, scales, biases, group_size=64, bits=4)
+    with pytest.raises(ValueError, match="uint8"):
+        quantized.QuantizedLinear(words, torch.zeros((32, 1), dtype=torch.bfloat16), None, mode="mxfp8")

@@ -102,3 +102,20 @@ def test_tail_split_keeps_plain_tiling_for_a_per_batch_gate(device):
     ref = resid.view(m, n)[sample].cpu().numpy() + g * ref
     out = got.view(m, n).float().cpu().numpy()[sample]
     assert max_abs(out, ref) <= 2e-3, max_abs(out, ref)
+
+
+def test_tail_split_of_a_batched_input_equals_the_flat_product(device):
+    """A 3-D ``(B, T, K)`` input whose flattened rows take the tail split: the tail's first row is
+    found from the flattened row stride, not the batch axis, so the result equals the 2-D product
+    bit for bit."""
+    m, n, k = 4864, 4096, 8192
+    assert _lib.tail_split(m, n, k) is not None
+    x, w = _bf((m, k), 19), _bf((n, k), 20, 0.02)
+    resid = workloads.normal(21, "resid", (m, n)).to(device)
+    gate = workloads.normal(22, "gate", (n,), 0.5).to(device)
+    xd, wd = x.to(device), w.to(device)
+    flat = fused_linear(xd, wd, None, residual=resid, gate=gate, out_dtype=torch.float32)
+    batched = fused_linear(xd.view(2, m // 2, k), wd, None, residual=resid.view(2, m // 2, n), gate=gate,
+                           out_dtype=torch.float32)
+    assert batched.shape == (2, m // 2, n)
+    assert torch.equal(batched.view(m, n), flat)

@@ -125,6 +125,34 @@ def test_model_from_checkpoint_matches_the_in_memory_model(device, tmp_path, bit
     assert torch.equal(a, b)
 
 
+def test_pretransposed_adaln_linears_bind_like_plain_ones(device, tmp_path):
+    """The reference's preparation may store every top-level AdaLN linear pretransposed, as
+    ``__layout__.<name>.weight_t`` only (``kinomlx/models/ltx2/weights/layout.py:11-20``): the
+    model must still be built with its prompt AdaLN, every tensor placed (strict), and give the
+    plain checkpoint's velocities bit for bit."""
+    p = workloads.ltx_model_params(SPEC, 1, in_channels=CHANNELS, out_channels=CHANNELS)
+    plain_path, layout_path = tmp_path / "plain.safetensors", tmp_path / "layout.safetensors"
+    _write_checkpoint(p, plain_path)
+    tensors = {}
+    for index, block in enumerate(p["blocks"]):
+        for name, value in block.items():
+            tensors[_source_name(f"transformer_blocks.{index}.{name}")] = value.contiguous()
+    for name, value in p.items():
+        if name == "blocks":
+            continue
+        if name in ("adaln_single.linear.weight", "prompt_adaln_single.linear.weight"):
+            tensors[f"__layout__.{name}_t"] = value.t().contiguous()
+        else:
+            tensors[_source_name(name)] = value.contiguous()
+    assert "__layout__.prompt_adaln_single.linear.weight_t" in tensors
+    save_file(tensors, str(layout_path))
+    plain = load_transformer(plain_path, device, heads=SPEC.heads, head_dim=SPEC.head_dim)
+    layout = load_transformer(layout_path, device, heads=SPEC.heads, head_dim=SPEC.head_dim, strict=True)
+    assert layout.prompt_adaln_single is not None and plain.prompt_adaln_single is not None
+    inputs = workloads.ltx_model_inputs(SPEC, in_channels=CHANNELS)
+    assert torch.equal(_velocity(layout, inputs, device), _velocity(plain, inputs, device))
+
+
 def test_strict_loading_rejects_unplaced_tensors(device, tmp_path):
     p = workloads.ltx_model_params(SPEC, 1, in_channels=CHANNELS, out_channels=CHANNELS)
     path = tmp_path / "extra.safetensors"

@@ -69,12 +69,18 @@ def test_noalloc_largest_product_size(device):
     _pair(device, m, n, k, False)
 
 
-def test_noalloc_refuses_more_than_the_scratch():
+def test_noalloc_refuses_more_than_the_scratch(device):
+    # real, correctly shaped operands: a product whose partial products (2 x 1024 x 4096 fp32 =
+    # 32 MiB) exceed the scratch is refused with an error, whatever order the checks run in
     lib = _lib.load()
-    fake = 1 << 20  # never dereferenced: the size check fails first
-    m, n, k, splits = 1024, 4096, 4096, 2  # 32 MiB of partial products
-    rc = lib.kx_gemm_splitk_noalloc_bf16(fake, k, fake, k, None, fake, n, m, n, k, 0, None, 0, None, 1, 0, splits,
-                                         None)
+    m, n, k, splits = 1024, 4096, 4096, 2
+    assert splits * m * n * 4 > SCRATCH_BYTES
+    x, w = _bf((m, k), 6).to(device), _bf((n, k), 7, 0.02).to(device)
+    out = torch.zeros((m, n), dtype=torch.bfloat16, device=device)
+    rc = lib.kx_gemm_splitk_noalloc_bf16(x.data_ptr(), k, w.data_ptr(), k, None, out.data_ptr(), n, m, n, k, 0, None,
+                                         0, None, 1, 0, splits, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
     assert rc == _lib.KX_ERR_INVALID
     assert "exceeds" in lib.kx_last_error().decode()
+    assert not out.any()  # nothing was launched
     assert ctypes.sizeof(ctypes.c_void_p) == 8
