@@ -2,9 +2,9 @@
  * kx355 — C ABI of the MI355X (gfx950) DiT-block kernels.
  *
  * Conventions shared by every entry point:
- *   - Pointers are device pointers. Activations are bf16 (raw 16-bit patterns), tables and
- *     modulation vectors fp32, packed weights uint32. "ld*" arguments are row strides in
- *     elements. Sizes are int64_t.
+ *   - Pointers are device pointers. Activations are bf16 (raw 16-bit patterns; fp16 for the
+ *     _f16 entry points at the end), tables and modulation vectors fp32, packed weights uint32.
+ *     "ld*" arguments are row strides in elements. Sizes are int64_t.
  *   - Work is enqueued asynchronously on `stream` (a hipStream_t; NULL = the null stream).
  *   - The library never allocates or frees device memory; the caller owns every buffer.
  *   - Return value: 0 on success, a negative KX_ERR_* code otherwise; kx_last_error() gives the
@@ -29,8 +29,8 @@ enum {
   KX_ERR_LAUNCH = -3       /* the HIP launch reported an error */
 };
 
-/* Element type of tensors that may be fp32 or bf16. */
-enum { KX_F32 = 0, KX_BF16 = 1 };
+/* Element type of tensors that may be fp32, bf16 or fp16 (where an entry point says so). */
+enum { KX_F32 = 0, KX_BF16 = 1, KX_F16 = 2 };
 
 /* Norm kinds for kx_adaln_norm_bf16; KX_NORM_IN_F32 may be or-ed in for an fp32 input. */
 enum { KX_NORM_RMS = 0, KX_NORM_LAYER = 1, KX_NORM_IN_F32 = 1 << 4 };
@@ -364,7 +364,7 @@ int kx_quantize_mxfp8_bf16(const void* w, int64_t ldw, uint32_t* wq, void* scale
                            int group_size, kx_stream_t stream);
 
 /* Modulation values: out[b, t, r, c] = fp32(table[r, c]) + fp32(ts[b, t, r, c]) for a (rows, dim)
- * table (KX_F32 or KX_BF16) and an optional timestep modulation ts (null: the table alone) with
+ * table (KX_F32, KX_BF16 or KX_F16) and an optional timestep modulation ts (null: the table alone) with
  * element strides ts_bs / ts_ts / ts_rs (dim contiguous); out is fp32 (batch, tokens, rows, dim)
  * contiguous. BasicAVTransformerBlock._ada_values and the prompt / A/V tables
  * (kinomlx/models/ltx2/transformer/transformer.py:179-199,209-219): scale_shift_table + timestep. */
@@ -444,6 +444,73 @@ int kx_mask_composite(const void* denoised, int denoised_dtype, const void* clea
  * on the stream; x may be NULL when n == 0): the per-step check mx.all(mx.isfinite(latent))
  * (kinomlx/models/ltx2/denoise.py:244-258). */
 int kx_all_finite(const void* x, int64_t n, int dtype, int* flag, kx_stream_t stream);
+
+/*
+ * ---- fp16 activations ----------------------------------------------------------------------
+ * The reference runs the LTX-2 transformer in FP16 by default (docs/PERFORMANCE.md:228-230,
+ * --transformer-dtype, kinomlx/models/ltx2/settings.py:233), and every hot-path operator takes
+ * float16 as well as bfloat16: dense_attention (kinomlx/models/ltx2/kernels/dense_attention.py:
+ * 47,112-116), split_rope.rotate (kinomlx/kernels/split_rope.py:32), the {half, bfloat} MPP GEMMs
+ * (kinomlx/kernels/mpp_linear.py:145-294), fused_ops.rms_norm / gelu_approx / silu
+ * (kinomlx/kernels/fused_ops.py:327-457). Each entry point below is its _bf16 namesake's contract
+ * with fp16 in place of bf16 for every 16-bit tensor (inputs, outputs, bias, gate, score bias,
+ * 16-bit residual): the same kernels, with v_mfma_f32_*_f16 products and fp16 roundings (round
+ * to nearest even; a value beyond 65504 becomes infinity, as an fp16 cast does). fp32 tables,
+ * modulation vectors, residual streams and workspaces are unchanged; norm weights may be
+ * KX_F32, KX_BF16 or KX_F16.
+ */
+int kx_adaln_norm_f16(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows, int64_t dim,
+                      const float* shift, const float* scale, int64_t mod_div, int64_t mod_stride, float eps,
+                      int kind, kx_stream_t stream);
+int kx_rmsnorm_rope_f16(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows, int64_t dim,
+                        int64_t norm_width, const void* w, int w_dtype, float eps, float weight_offset,
+                        int rope_kind, const float* cos, const float* sin, int64_t table_ld, int64_t table_hs,
+                        int64_t tokens, int table_batched, int64_t head_dim, kx_stream_t stream);
+int kx_qk_rmsnorm_rope_f16(const void* xq, int64_t ldq, const void* xk, int64_t ldk, void* yq, int64_t ldyq,
+                           void* yk, int64_t ldyk, int64_t rows, int64_t dim, const void* wq, const void* wk,
+                           int w_dtype, float eps, float weight_offset, const float* cos, const float* sin,
+                           int64_t table_ld, int64_t table_hs, int64_t tokens, int table_batched,
+                           kx_stream_t stream);
+int kx_rope_split_f16(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t batch, int64_t tokens,
+                      int64_t heads, int64_t half, const float* cos, const float* sin, int table_batched,
+                      kx_stream_t stream);
+int kx_rope_pair_f16(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows, int64_t heads,
+                     int64_t head_dim, const float* cos, const float* sin, int64_t table_ld, int64_t table_hs,
+                     int64_t tokens, int table_batched, kx_stream_t stream);
+int kx_attention_fwd_f16(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
+                         void* o, int64_t ldo, int64_t batch, int64_t tq, int64_t tk, int64_t heads,
+                         int64_t head_dim, float scale, const void* gate, int64_t ld_gate, kx_stream_t stream);
+int kx_attention_gqa_fwd_f16(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
+                             void* o, int64_t ldo, int64_t batch, int64_t tq, int64_t tk, int64_t heads,
+                             int64_t kv_heads, int64_t head_dim, float scale, const void* gate, int64_t ld_gate,
+                             kx_stream_t stream);
+int kx_attention_bias_fwd_f16(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v,
+                              int64_t ldv, void* o, int64_t ldo, int64_t batch, int64_t tq, int64_t tk,
+                              int64_t heads, int64_t kv_heads, int64_t head_dim, float scale, const void* gate,
+                              int64_t ld_gate, const void* bias, int64_t bias_bs, int64_t bias_hs,
+                              int64_t bias_qs, kx_stream_t stream);
+int kx_attention_split_fwd_f16(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v,
+                               int64_t ldv, void* o, int64_t ldo, int64_t batch, int64_t tq, int64_t tk,
+                               int64_t heads, int64_t kv_heads, int64_t head_dim, float scale, const void* gate,
+                               int64_t ld_gate, const void* bias, int64_t bias_bs, int64_t bias_hs,
+                               int64_t bias_qs, void* workspace, int64_t workspace_bytes, int splits,
+                               kx_stream_t stream);
+int kx_gemm_f16(const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias, void* c, int64_t ldc,
+                int64_t m, int64_t n, int64_t k, int epilogue, const void* resid, int64_t ldr, const float* gate,
+                int64_t gate_div, int64_t gate_stride, kx_stream_t stream);
+int kx_gemm_splitk_f16(const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias, void* c,
+                       int64_t ldc, int64_t m, int64_t n, int64_t k, int epilogue, const void* resid, int64_t ldr,
+                       const float* gate, int64_t gate_div, int64_t gate_stride, void* workspace,
+                       int64_t workspace_bytes, int splits, kx_stream_t stream);
+int kx_gelu_tanh_f16(const void* x, void* y, int64_t count, kx_stream_t stream);
+int kx_silu_f16(const void* x, void* y, int64_t count, kx_stream_t stream);
+int kx_swiglu_f16(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows, int64_t hidden,
+                  kx_stream_t stream);
+int kx_modulate_f16(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows, int64_t dim,
+                    const float* shift, const float* scale, int64_t mod_div, int64_t mod_stride, kx_stream_t stream);
+int kx_gated_residual_f16(const void* x, int64_t ldx, const void* r, int64_t ldr, void* y, int64_t ldy,
+                          int64_t rows, int64_t dim, const float* gate, int64_t gate_div, int64_t gate_stride,
+                          kx_stream_t stream);
 
 #ifdef __cplusplus
 }

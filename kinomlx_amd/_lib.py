@@ -25,6 +25,7 @@ KX_ERR_LAUNCH = -3
 
 KX_F32 = 0
 KX_BF16 = 1
+KX_F16 = 2
 KX_NORM_RMS = 0
 KX_NORM_LAYER = 1
 KX_NORM_IN_F32 = 1 << 4
@@ -114,6 +115,16 @@ SIGNATURES: dict[str, list] = {
     "kx_mask_composite": [_P, _I, _P, _I, _P, _P, _I64, _I64, _P],
     "kx_all_finite": [_P, _I64, _I, _P, _P],
 }
+
+# fp16 entry points: the bf16 namesake's arguments with fp16 16-bit tensors (include/kx355.h)
+F16_ENTRIES = (
+    "kx_adaln_norm", "kx_rmsnorm_rope", "kx_qk_rmsnorm_rope", "kx_rope_split", "kx_rope_pair",
+    "kx_attention_fwd", "kx_attention_gqa_fwd", "kx_attention_bias_fwd", "kx_attention_split_fwd", "kx_gemm",
+    "kx_gemm_splitk", "kx_gelu_tanh", "kx_silu", "kx_swiglu", "kx_modulate", "kx_gated_residual",
+)
+for _base in F16_ENTRIES:
+    SIGNATURES[f"{_base}_f16"] = SIGNATURES[f"{_base}_bf16"]
+del _base
 
 _lib: ctypes.CDLL | None = None
 
@@ -206,6 +217,31 @@ def _check_gpu(name: str, *tensors: torch.Tensor | None) -> None:
             raise ValueError(f"{name}: the MI355X kernels take GPU tensors, got one on {t.device}")
 
 
+HALF_DTYPES = (torch.bfloat16, torch.float16)
+
+
+def _suffix(t: torch.Tensor, name: str) -> str:
+    """The entry-point suffix for a 16-bit activation tensor: ``bf16`` or ``f16``."""
+    if t.dtype == torch.bfloat16:
+        return "bf16"
+    if t.dtype == torch.float16:
+        return "f16"
+    raise ValueError(f"{name}: needs float16 or bfloat16 activations, got {t.dtype}")
+
+
+def _same_dtype(name: str, dtype: torch.dtype, *tensors) -> None:
+    for t in tensors:
+        if t is not None and t.dtype != dtype:
+            raise ValueError(f"{name}: every 16-bit tensor must be {dtype}, got {t.dtype}")
+
+
+def _weight_code(w: torch.Tensor, name: str) -> int:
+    codes = {torch.float32: KX_F32, torch.bfloat16: KX_BF16, torch.float16: KX_F16}
+    if w.dtype not in codes:
+        raise ValueError(f"{name}: norm weight must be float32, bfloat16 or float16, got {w.dtype}")
+    return codes[w.dtype]
+
+
 def _rows(t: torch.Tensor, name: str) -> tuple[int, int, int]:
     """(rows, width, row stride) of a tensor whose last axis is contiguous and whose leading
     axes flatten into rows of one stride."""
@@ -254,21 +290,21 @@ def _shared_mod_rows(shift, scale, rows: int, width: int, name: str) -> tuple[in
 
 
 def launch_adaln_norm(x, out, shift, scale, eps: float, kind: int) -> None:
-    """``x`` is bf16 or fp32 (a residual stream carried in fp32); ``out`` is bf16."""
+    """``out`` is bf16 or fp16; ``x`` is of the same type or fp32 (a residual stream carried in
+    fp32)."""
     _check_gpu("adaln_norm", x, out, shift, scale)
+    suffix = _suffix(out, "adaln_norm out")
     if x.dtype == torch.float32:
         kind |= KX_NORM_IN_F32
-    elif x.dtype != torch.bfloat16:
-        raise ValueError(f"adaln_norm: x must be bfloat16 or float32, got {x.dtype}")
-    if out.dtype != torch.bfloat16:
-        raise ValueError("adaln_norm: the output is bfloat16")
+    elif x.dtype != out.dtype:
+        raise ValueError(f"adaln_norm: x must be {out.dtype} or float32, got {x.dtype}")
     rows, dim, ldx = _rows(x, "adaln_norm x")
     _, _, ldy = _rows(out, "adaln_norm out")
     div, stride = (1, 0)
     if shift is not None:
         div, stride = _shared_mod_rows(shift, scale, rows, dim, "adaln_norm")
     _call(
-        "kx_adaln_norm_bf16", _ptr(x), ldx, _ptr(out), ldy, rows, dim, _ptr(shift), _ptr(scale),
+        f"kx_adaln_norm_{suffix}", _ptr(x), ldx, _ptr(out), ldy, rows, dim, _ptr(shift), _ptr(scale),
         div, stride, eps, kind, _stream(),
     )
 
@@ -279,18 +315,15 @@ def launch_rmsnorm_rope(
     table_batched: bool = False, head_dim: int = 0,
 ) -> None:
     _check_gpu("rmsnorm_rope", x, out, weight, cos, sin)
+    suffix = _suffix(x, "rms_norm")
+    _same_dtype("rms_norm", x.dtype, out)
     rows, dim, ldx = _rows(x, "rmsnorm x")
     _, _, ldy = _rows(out, "rmsnorm out")
-    if weight.dtype == torch.bfloat16:
-        w_dtype = KX_BF16
-    elif weight.dtype == torch.float32:
-        w_dtype = KX_F32
-    else:
-        raise ValueError("rms_norm weight must be float32 or bfloat16")
+    w_dtype = _weight_code(weight, "rms_norm")
     if not weight.is_contiguous():
         raise ValueError("rms_norm weight must be contiguous")
     _call(
-        "kx_rmsnorm_rope_bf16", _ptr(x), ldx, _ptr(out), ldy, rows, dim, norm_width, _ptr(weight),
+        f"kx_rmsnorm_rope_{suffix}", _ptr(x), ldx, _ptr(out), ldy, rows, dim, norm_width, _ptr(weight),
         w_dtype, eps, weight_offset, rope_kind, _ptr(cos), _ptr(sin), table_ld, table_hs, tokens,
         int(table_batched), head_dim, _stream(),
     )
@@ -307,14 +340,11 @@ def launch_qk_rmsnorm_rope(xq, xk, yq, yk, wq, wk, eps: float, *, cos, sin, tabl
     _, _, ldyk = _rows(yk, "qk_rmsnorm_rope k out")
     if (rows_k, dim_k) != (rows, dim) or wq.dtype != wk.dtype:
         raise ValueError("qk_rmsnorm_rope: q and k must have one shape and one weight dtype")
-    if wq.dtype == torch.bfloat16:
-        w_dtype = KX_BF16
-    elif wq.dtype == torch.float32:
-        w_dtype = KX_F32
-    else:
-        raise ValueError("rms_norm weight must be float32 or bfloat16")
+    suffix = _suffix(xq, "qk_rmsnorm_rope")
+    _same_dtype("qk_rmsnorm_rope", xq.dtype, xk, yq, yk)
+    w_dtype = _weight_code(wq, "rms_norm")
     code = _call(
-        "kx_qk_rmsnorm_rope_bf16", _ptr(xq), ldq, _ptr(xk), ldk, _ptr(yq), ldyq, _ptr(yk), ldyk, rows, dim,
+        f"kx_qk_rmsnorm_rope_{suffix}", _ptr(xq), ldq, _ptr(xk), ldk, _ptr(yq), ldyq, _ptr(yk), ldyk, rows, dim,
         _ptr(wq), _ptr(wk), w_dtype, eps, 0.0, _ptr(cos), _ptr(sin), table_ld, table_hs, tokens,
         int(table_batched), _stream(), unsupported_ok=True,
     )
@@ -323,20 +353,24 @@ def launch_qk_rmsnorm_rope(xq, xk, yq, yk, wq, wk, eps: float, *, cos, sin, tabl
 
 def launch_rope_split(x, out, cos_tm, sin_tm, *, batch, tokens, heads, half, table_batched) -> None:
     _check_gpu("rope_split", x, out, cos_tm, sin_tm)
+    suffix = _suffix(x, "rope")
+    _same_dtype("rope", x.dtype, out)
     _, _, ldx = _rows(x, "rope x")
     _, _, ldy = _rows(out, "rope out")
     _call(
-        "kx_rope_split_bf16", _ptr(x), ldx, _ptr(out), ldy, batch, tokens, heads, half,
+        f"kx_rope_split_{suffix}", _ptr(x), ldx, _ptr(out), ldy, batch, tokens, heads, half,
         _ptr(cos_tm), _ptr(sin_tm), int(table_batched), _stream(),
     )
 
 
 def launch_rope_pair(x, out, cos, sin, *, heads, head_dim, table_ld, table_hs, tokens, table_batched) -> None:
     _check_gpu("rope_pair", x, out, cos, sin)
+    suffix = _suffix(x, "rope")
+    _same_dtype("rope", x.dtype, out)
     rows, _, ldx = _rows(x, "rope x")
     _, _, ldy = _rows(out, "rope out")
     _call(
-        "kx_rope_pair_bf16", _ptr(x), ldx, _ptr(out), ldy, rows, heads, head_dim, _ptr(cos),
+        f"kx_rope_pair_{suffix}", _ptr(x), ldx, _ptr(out), ldy, rows, heads, head_dim, _ptr(cos),
         _ptr(sin), table_ld, table_hs, tokens, int(table_batched), _stream(),
     )
 
@@ -344,38 +378,40 @@ def launch_rope_pair(x, out, cos, sin, *, heads, head_dim, table_ld, table_hs, t
 def launch_attention(q, k, v, out, *, batch, tq, tk, heads, head_dim, scale, gate=None, kv_heads=None,
                      bias=None, bias_strides=None) -> None:
     _check_gpu("attention", q, k, v, out, gate, bias)
+    sfx = _suffix(q, "attention")
+    _same_dtype("attention", q.dtype, k, v, out, gate)
     ld_gate = 0
     if gate is not None:
         _, _, ld_gate = _rows(gate, "attention gate")
-    if bias is not None and (bias.dtype != torch.bfloat16 or bias_strides is None):
-        raise ValueError("attention bias: bfloat16 values with (batch, head, query) strides")
+    if bias is not None and (bias.dtype != q.dtype or bias_strides is None):
+        raise ValueError(f"attention bias: {q.dtype} values with (batch, head, query) strides")
     splits = attention_splits(batch, tq, tk, heads)
     if splits > 1:
         chunk = -(-(-(-tk // splits)) // 64) * 64
         used = -(-tk // chunk)
         work = torch.empty(used * batch * heads * tq * (head_dim + 2), dtype=torch.float32, device=q.device)
         _call(
-            "kx_attention_split_fwd_bf16", _ptr(q), q.stride(-2), _ptr(k), k.stride(-2), _ptr(v), v.stride(-2),
+            f"kx_attention_split_fwd_{sfx}", _ptr(q), q.stride(-2), _ptr(k), k.stride(-2), _ptr(v), v.stride(-2),
             _ptr(out), out.stride(-2), batch, tq, tk, heads, kv_heads or heads, head_dim, scale, _ptr(gate), ld_gate,
             _ptr(bias), *(bias_strides or (0, 0, 0)), _ptr(work), work.numel() * 4, splits, _stream(),
         )
         return
     if bias is not None:
         _call(
-            "kx_attention_bias_fwd_bf16", _ptr(q), q.stride(-2), _ptr(k), k.stride(-2), _ptr(v), v.stride(-2),
+            f"kx_attention_bias_fwd_{sfx}", _ptr(q), q.stride(-2), _ptr(k), k.stride(-2), _ptr(v), v.stride(-2),
             _ptr(out), out.stride(-2), batch, tq, tk, heads, kv_heads or heads, head_dim, scale, _ptr(gate), ld_gate,
             _ptr(bias), *bias_strides, _stream(),
         )
         return
     if kv_heads is not None and kv_heads != heads:
         _call(
-            "kx_attention_gqa_fwd_bf16", _ptr(q), q.stride(-2), _ptr(k), k.stride(-2), _ptr(v),
+            f"kx_attention_gqa_fwd_{sfx}", _ptr(q), q.stride(-2), _ptr(k), k.stride(-2), _ptr(v),
             v.stride(-2), _ptr(out), out.stride(-2), batch, tq, tk, heads, kv_heads, head_dim, scale,
             _ptr(gate), ld_gate, _stream(),
         )
         return
     _call(
-        "kx_attention_fwd_bf16", _ptr(q), q.stride(-2), _ptr(k), k.stride(-2), _ptr(v),
+        f"kx_attention_fwd_{sfx}", _ptr(q), q.stride(-2), _ptr(k), k.stride(-2), _ptr(v),
         v.stride(-2), _ptr(out), out.stride(-2), batch, tq, tk, heads, head_dim, scale,
         _ptr(gate), ld_gate, _stream(),
     )
@@ -391,24 +427,27 @@ def attention_splits(batch: int, tq: int, tk: int, heads: int) -> int:
     return max(1, min(16, -(-512 // blocks), tk // 256))
 
 
-def _dtype_flags(out, resid, name: str) -> int:
-    """Epilogue flags for an fp32 output and an fp32 residual (bf16 otherwise)."""
+def _dtype_flags(out, resid, name: str, half: torch.dtype = torch.bfloat16) -> int:
+    """Epilogue flags for an fp32 output and an fp32 residual (``half``, the operands' 16-bit
+    type, otherwise)."""
     flags = 0
     if out.dtype == torch.float32:
         flags |= EPI_OUT_F32
-    elif out.dtype != torch.bfloat16:
-        raise ValueError(f"{name}: the output must be bfloat16 or float32, got {out.dtype}")
+    elif out.dtype != half:
+        raise ValueError(f"{name}: the output must be {half} or float32, got {out.dtype}")
     if resid is not None:
         if resid.dtype == torch.float32:
             flags |= EPI_RESID_F32
-        elif resid.dtype != torch.bfloat16:
-            raise ValueError(f"{name}: the residual must be bfloat16 or float32, got {resid.dtype}")
+        elif resid.dtype != half:
+            raise ValueError(f"{name}: the residual must be {half} or float32, got {resid.dtype}")
     return flags
 
 
 def launch_gemm(a, w, out, *, bias=None, flags: int = 0, resid=None, gate=None) -> None:
     _check_gpu("gemm", a, w, out, bias, resid, gate)
-    flags |= _dtype_flags(out, resid, "linear")
+    sfx = _suffix(a, "linear")
+    _same_dtype("linear", a.dtype, w, bias)
+    flags |= _dtype_flags(out, resid, "linear", a.dtype)
     m, k, lda = _rows(a, "linear input")
     n, kw, ldw = _rows(w, "linear weight")
     if kw != k:
@@ -426,7 +465,7 @@ def launch_gemm(a, w, out, *, bias=None, flags: int = 0, resid=None, gate=None) 
         # whole rounds of 256x256 tiles over the first rows, the tail rows as K slices filling one round
         rows, tail_splits = plan
         _call(
-            "kx_gemm_bf16", _ptr(a), lda, _ptr(w), ldw, _ptr(bias), _ptr(out), ldc, rows, n, k, flags,
+            f"kx_gemm_{sfx}", _ptr(a), lda, _ptr(w), ldw, _ptr(bias), _ptr(out), ldc, rows, n, k, flags,
             _ptr(resid), ldr, _ptr(gate), div, stride, _stream(),
         )
         tail = m - rows
@@ -437,7 +476,7 @@ def launch_gemm(a, w, out, *, bias=None, flags: int = 0, resid=None, gate=None) 
         out_tail = out.data_ptr() + rows * ldc * out.element_size()
         resid_tail = None if resid is None else resid.data_ptr() + rows * ldr * resid.element_size()
         _call(
-            "kx_gemm_splitk_bf16", a_tail, lda, _ptr(w), ldw, _ptr(bias), out_tail, ldc, tail, n, k,
+            f"kx_gemm_splitk_{sfx}", a_tail, lda, _ptr(w), ldw, _ptr(bias), out_tail, ldc, tail, n, k,
             flags, resid_tail, ldr, _ptr(gate), div, stride, _ptr(work), work.numel() * 4, tail_splits, _stream(),
         )
         return
@@ -445,12 +484,12 @@ def launch_gemm(a, w, out, *, bias=None, flags: int = 0, resid=None, gate=None) 
     if splits > 1 and a.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0 and lda <= (1 << 22) and ldw <= (1 << 22):
         work = torch.empty(splits * m * n, dtype=torch.float32, device=a.device)
         _call(
-            "kx_gemm_splitk_bf16", _ptr(a), lda, _ptr(w), ldw, _ptr(bias), _ptr(out), ldc, m, n, k, flags,
+            f"kx_gemm_splitk_{sfx}", _ptr(a), lda, _ptr(w), ldw, _ptr(bias), _ptr(out), ldc, m, n, k, flags,
             _ptr(resid), ldr, _ptr(gate), div, stride, _ptr(work), work.numel() * 4, splits, _stream(),
         )
         return
     _call(
-        "kx_gemm_bf16", _ptr(a), lda, _ptr(w), ldw, _ptr(bias), _ptr(out), ldc, m, n, k, flags,
+        f"kx_gemm_{sfx}", _ptr(a), lda, _ptr(w), ldw, _ptr(bias), _ptr(out), ldc, m, n, k, flags,
         _ptr(resid), ldr, _ptr(gate), div, stride, _stream(),
     )
 
@@ -634,33 +673,40 @@ def launch_dequant(words, scales, biases, out, *, n, k, group_size, bits) -> Non
 
 
 def launch_unary(name: str, x, out) -> None:
+    """``name``: the entry point without its type suffix (``kx_gelu_tanh``, ``kx_silu``)."""
     _check_gpu(name, x, out)
+    sfx = _suffix(x, name)
+    _same_dtype(name, x.dtype, out)
     if not (x.is_contiguous() and out.is_contiguous()):
         raise ValueError(f"{name}: contiguous tensors required")
-    _call(name, _ptr(x), _ptr(out), x.numel(), _stream())
+    _call(f"{name}_{sfx}", _ptr(x), _ptr(out), x.numel(), _stream())
 
 
 def launch_swiglu(x, out) -> None:
     _check_gpu("swiglu", x, out)
+    sfx = _suffix(x, "swiglu")
+    _same_dtype("swiglu", x.dtype, out)
     rows, width, ldx = _rows(x, "swiglu x")
     _, _, ldy = _rows(out, "swiglu out")
-    _call("kx_swiglu_bf16", _ptr(x), ldx, _ptr(out), ldy, rows, width // 2, _stream())
+    _call(f"kx_swiglu_{sfx}", _ptr(x), ldx, _ptr(out), ldy, rows, width // 2, _stream())
 
 
 def launch_modulate(x, out, shift, scale) -> None:
     _check_gpu("modulate", x, out, shift, scale)
+    sfx = _suffix(x, "modulate")
+    _same_dtype("modulate", x.dtype, out)
     rows, dim, ldx = _rows(x, "modulate x")
     _, _, ldy = _rows(out, "modulate out")
     div, stride = _shared_mod_rows(shift, scale, rows, dim, "modulate")
     _call(
-        "kx_modulate_bf16", _ptr(x), ldx, _ptr(out), ldy, rows, dim, _ptr(shift), _ptr(scale),
+        f"kx_modulate_{sfx}", _ptr(x), ldx, _ptr(out), ldy, rows, dim, _ptr(shift), _ptr(scale),
         div, stride, _stream(),
     )
 
 
 def table_add(table: torch.Tensor, ts: torch.Tensor | None) -> torch.Tensor:
     """``fp32(table) + fp32(ts)`` as a new contiguous fp32 ``(B, T, rows, D)`` tensor: ``table`` is
-    ``(rows, D)`` (fp32 or bf16), ``ts`` ``(B, T, rows, D)`` with a contiguous last axis, or ``None``
+    ``(rows, D)`` (fp32, bf16 or fp16), ``ts`` ``(B, T, rows, D)`` with a contiguous last axis, or ``None``
     (the table alone, as ``(1, 1, rows, D)``)."""
     _check_gpu("table_add", table, ts)
     if table.dim() != 2 or table.stride(-1) != 1 or (table.shape[0] > 1 and table.stride(0) != table.shape[1]):
@@ -673,15 +719,17 @@ def table_add(table: torch.Tensor, ts: torch.Tensor | None) -> torch.Tensor:
             raise ValueError(f"table_add: timestep modulation {tuple(ts.shape)} does not match table {(rows, dim)}")
         batch, tokens = ts.shape[:2]
         bs, tstride, rs = ts.stride(0), ts.stride(1), ts.stride(2)
-        ts_code = _dtype_code(ts, "table_add timestep")
+        ts_code = _weight_code(ts, "table_add timestep")
     out = torch.empty((batch, tokens, rows, dim), dtype=torch.float32, device=table.device)
-    _call("kx_table_add_f32", _ptr(table), _dtype_code(table, "table_add table"), _ptr(ts), ts_code, bs, tstride, rs,
+    _call("kx_table_add_f32", _ptr(table), _weight_code(table, "table_add table"), _ptr(ts), ts_code, bs, tstride, rs,
           _ptr(out), batch, tokens, rows, dim, _stream())
     return out
 
 
 def launch_gated_residual(x, r, out, gate) -> None:
     _check_gpu("gated_residual", x, r, out, gate)
+    sfx = _suffix(r, "gated_residual")
+    _same_dtype("gated_residual", r.dtype, x, out)
     rows, dim, ldr = _rows(r, "gated_residual residual")
     ldx = 0
     if x is not None:
@@ -689,7 +737,7 @@ def launch_gated_residual(x, r, out, gate) -> None:
     _, _, ldy = _rows(out, "gated_residual out")
     div, stride = _mod_rows(gate, rows, dim, "gated_residual gate")
     _call(
-        "kx_gated_residual_bf16", _ptr(x), ldx, _ptr(r), ldr, _ptr(out), ldy, rows, dim, _ptr(gate),
+        f"kx_gated_residual_{sfx}", _ptr(x), ldx, _ptr(r), ldr, _ptr(out), ldy, rows, dim, _ptr(gate),
         div, stride, _stream(),
     )
 

@@ -14,7 +14,8 @@
 // tile i+1 becomes visible in the middle of tile i, with tile i+2 in flight; the other forms keep
 // one tile per iteration with tiles i+1 .. i+3 in flight.
 //
-// Scores are computed transposed, S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (A = 32 keys read from
+// The 16-bit type is bf16 or fp16 (template H; v_mfma_f32_32x32x16_bf16 / _f16, P rounded to the
+// same type). Scores are computed transposed, S^T = K Q^T with one 32x32x16 MFMA (A = 32 keys read from
 // LDS, B = the wave's 32 queries): the accumulator lane holds one query (lane % 32) and 16 of the
 // 32 keys, so the row max is an in-lane reduction plus one exchange with lane ^ 32. The output
 // is accumulated transposed too, O^T += V^T P^T: P^T comes straight out of the S^T accumulator
@@ -108,7 +109,7 @@ struct SplitOut {
 // once and stays there while the workgroup runs up to qpw consecutive query tiles of its head; the
 // waves need no barrier after the copy, so one wave's query load and output store overlap the
 // other waves' products.
-template <int D, bool BIAS, bool SPLIT, bool RES = false>
+template <bool H, int D, bool BIAS, bool SPLIT, bool RES = false>
 __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
     const uint16_t* __restrict__ Q, int64_t ldq, const uint16_t* __restrict__ K, int64_t ldk,
     const uint16_t* __restrict__ V, int64_t ldv, uint16_t* __restrict__ O, int64_t ldo, int tq,
@@ -266,7 +267,7 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
       for (int e = 0; e < 16; ++e) sc[e] = 0.0f;
 #pragma unroll
       for (int st = 0; st < QS; ++st)
-        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfrag(buf(0), 0, st), qf[st], sc, 0, 0, 0);
+        sc = mfma32x32x16<H>(kfrag(buf(0), 0, st), qf[st], sc);
       mask(sc, 0);
       float tmax = sc[0];
 #pragma unroll
@@ -293,7 +294,7 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
         float p = __builtin_amdgcn_exp2f(fmaf(sc[e], scale_log2, -mc));
         asm volatile("" : "+v"(p));
         psum += p;
-        pb[e >> 3][e & 7] = (__bf16)p;
+        pb[e >> 3][e & 7] = e16<H>(p);
       };
       // VALU work is spread so that each MFMA has about its own duration of it beside it: the
       // exps of elements 0..PA-1 between the 8 score MFMAs, the rest between the 4 P V MFMAs of
@@ -306,7 +307,7 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
       for (int st = 0; st < QS; ++st) {
         if (st + 1 < QS) kf[(st + 1) & 1] = kfrag(nxt, nkb, st + 1);
         __builtin_amdgcn_sched_barrier(0);
-        sn = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[st & 1], qf[st], sn, 0, 0, 0);
+        sn = mfma32x32x16<H>(kf[st & 1], qf[st], sn);
 #pragma unroll
         for (int e = st * PA / QS; e < (st + 1) * PA / QS; ++e) pexp(e);
         __builtin_amdgcn_sched_barrier(0);
@@ -323,7 +324,7 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
         if (q + 1 < 2 * DB)
           vf[(q + 1) & 1] = vfrag(cur, (q + 1) % DB, 2 * kb + (q + 1) / DB);
         __builtin_amdgcn_sched_barrier(0);
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[q & 1], pb[ts], o[db], 0, 0, 0);
+        o[db] = mfma32x32x16<H>(vf[q & 1], pb[ts], o[db]);
         if (q < DB) {
 #pragma unroll
           for (int e = PA + q * (16 - PA) / DB; e < PA + (q + 1) * (16 - PA) / DB; ++e) pexp(e);
@@ -380,15 +381,15 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
         const int q = q0 + lrow;
         if (q < tq) {
           float scale_out = 1.0f / l_tot;
-          if (gate) scale_out *= bf2f(gate[((int64_t)b * tq + q) * ld_gate + h]);
+          if (gate) scale_out *= e2f<H>(gate[((int64_t)b * tq + q) * ld_gate + h]);
           uint16_t* orow = O + ((int64_t)b * tq + q) * ldo + (int64_t)h * D;
 #pragma unroll
           for (int db = 0; db < DB; ++db)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
               uint2 w;
-              w.x = pack2(o[db][4 * g + 0] * scale_out, o[db][4 * g + 1] * scale_out);
-              w.y = pack2(o[db][4 * g + 2] * scale_out, o[db][4 * g + 3] * scale_out);
+              w.x = e_pack2<H>(o[db][4 * g + 0] * scale_out, o[db][4 * g + 1] * scale_out);
+              w.y = e_pack2<H>(o[db][4 * g + 2] * scale_out, o[db][4 * g + 3] * scale_out);
               *reinterpret_cast<uint2*>(orow + db * 32 + 8 * g + 4 * lhalf) = w;
             }
         }
@@ -426,7 +427,7 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
 #pragma unroll
         for (int st = 0; st < QS; ++st) {
           const bf16x8 kf = *reinterpret_cast<const bf16x8*>(cur + koff[st] + kb * 32 * ROWB);
-          s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], s[kb], 0, 0, 0);
+          s[kb] = mfma32x32x16<H>(kf, qf[st], s[kb]);
         }
       }
       const int j0 = it * BKV;
@@ -442,10 +443,10 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
             float bv[4];
             if (key + 3 < tk) {
               const uint2 w = *reinterpret_cast<const uint2*>(brow + key);
-              bv[0] = lo_f(w.x); bv[1] = hi_f(w.x); bv[2] = lo_f(w.y); bv[3] = hi_f(w.y);
+              bv[0] = e_lo<H>(w.x); bv[1] = e_hi<H>(w.x); bv[2] = e_lo<H>(w.y); bv[3] = e_hi<H>(w.y);
             } else {
 #pragma unroll
-              for (int i = 0; i < 4; ++i) bv[i] = key + i < tk ? bf2f(brow[key + i]) : 0.0f;
+              for (int i = 0; i < 4; ++i) bv[i] = key + i < tk ? e2f<H>(brow[key + i]) : 0.0f;
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -489,7 +490,7 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
         float p = __builtin_amdgcn_exp2f(fmaf(s[kb][8 * hf + e], scale_log2, -mc));
         if constexpr (BIAS) p = s[kb][8 * hf + e] == -1e30f ? removed_p : p;
         psum += p;
-        pb[kb][hf][e] = (__bf16)p;
+        pb[kb][hf][e] = e16<H>(p);
       };
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
@@ -503,7 +504,7 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
           const bf16x8 vf = read_vt(cur + voff[db] + 16 * ts * ROWB, 8 * ROWB);
-          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb[ts >> 1][ts & 1], o[db], 0, 0, 0);
+          o[db] = mfma32x32x16<H>(vf, pb[ts >> 1][ts & 1], o[db]);
         }
       l_run += psum;
       cur_i = cur_i + 1 == NSTAGE ? 0 : cur_i + 1;
@@ -528,22 +529,22 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
     return;
   }
   float scale_out = 1.0f / l_tot;
-  if (gate) scale_out *= bf2f(gate[((int64_t)b * tq + q) * ld_gate + h]);
+  if (gate) scale_out *= e2f<H>(gate[((int64_t)b * tq + q) * ld_gate + h]);
   uint16_t* orow = O + ((int64_t)b * tq + q) * ldo + (int64_t)h * D;
 #pragma unroll
   for (int db = 0; db < DB; ++db)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       uint2 w;
-      w.x = pack2(o[db][4 * g + 0] * scale_out, o[db][4 * g + 1] * scale_out);
-      w.y = pack2(o[db][4 * g + 2] * scale_out, o[db][4 * g + 3] * scale_out);
+      w.x = e_pack2<H>(o[db][4 * g + 0] * scale_out, o[db][4 * g + 1] * scale_out);
+      w.y = e_pack2<H>(o[db][4 * g + 2] * scale_out, o[db][4 * g + 3] * scale_out);
       *reinterpret_cast<uint2*>(orow + db * 32 + 8 * g + 4 * lhalf) = w;
     }
 }
 
 // out = (sum_y 2^(m_y - M) O_y) / (sum_y 2^(m_y - M) l_y) * gate, M = max_y m_y: the slices of the
 // split form merged (4 dims of one row per thread).
-template <int D>
+template <bool H, int D>
 __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ part_o,
                                                            const float* __restrict__ part_ml, int splits,
                                                            int64_t rows, int tq, int heads,
@@ -571,19 +572,19 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
   const int64_t bh = row / tq;
   const int h = (int)(bh % heads), b = (int)(bh / heads);
   float scale_out = 1.0f / l;
-  if (gate) scale_out *= bf2f(gate[((int64_t)b * tq + q) * ld_gate + h]);
+  if (gate) scale_out *= e2f<H>(gate[((int64_t)b * tq + q) * ld_gate + h]);
   uint2 w2;
-  w2.x = pack2(acc.x * scale_out, acc.y * scale_out);
-  w2.y = pack2(acc.z * scale_out, acc.w * scale_out);
+  w2.x = e_pack2<H>(acc.x * scale_out, acc.y * scale_out);
+  w2.y = e_pack2<H>(acc.z * scale_out, acc.w * scale_out);
   *reinterpret_cast<uint2*>(O + ((int64_t)b * tq + q) * ldo + (int64_t)h * D + d) = w2;
 }
 
-template <int D, bool BIAS, bool SPLIT, bool RES = false>
+template <bool H, int D, bool BIAS, bool SPLIT, bool RES = false>
 void launch_attn_t(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv, void* o,
                    int64_t ldo, int64_t tq, int64_t tk, int64_t heads, int64_t kv_heads, float scale,
                    const void* gate, int64_t ld_gate, ScoreBias bias, SplitOut split, dim3 grid, int qtiles,
                    hipStream_t s, int qpw = 1) {
-  attn_fwd_kernel<D, BIAS, SPLIT, RES><<<grid, NWAVE * 64, 0, s>>>(
+  attn_fwd_kernel<H, D, BIAS, SPLIT, RES><<<grid, NWAVE * 64, 0, s>>>(
       (const uint16_t*)q, ldq, (const uint16_t*)k, ldk, (const uint16_t*)v, ldv, (uint16_t*)o, ldo, (int)tq,
       (int)tk, (int)heads, (int)(heads / kv_heads), scale * 1.4426950408889634f, (const uint16_t*)gate, ld_gate,
       qtiles, qpw, bias, split);
@@ -606,7 +607,7 @@ int resident_qpw(int64_t qtiles, int64_t heads_total) {
   return best;
 }
 
-template <int D>
+template <bool H, int D>
 int launch_attn(const void* q, int64_t ldq, const void* k, int64_t ldk, const void* v, int64_t ldv,
                 void* o, int64_t ldo, int64_t batch, int64_t tq, int64_t tk, int64_t heads,
                 int64_t kv_heads, float scale, const void* gate, int64_t ld_gate, ScoreBias bias,
@@ -616,28 +617,28 @@ int launch_attn(const void* q, int64_t ldq, const void* k, int64_t ldk, const vo
   const dim3 grid((unsigned)blocks, (unsigned)splits);
   if (splits > 1) {
     if (bias.ptr)
-      launch_attn_t<D, true, true>(q, ldq, k, ldk, v, ldv, o, ldo, tq, tk, heads, kv_heads, scale, gate, ld_gate,
+      launch_attn_t<H, D, true, true>(q, ldq, k, ldk, v, ldv, o, ldo, tq, tk, heads, kv_heads, scale, gate, ld_gate,
                                    bias, split, grid, qtiles, s);
     else
-      launch_attn_t<D, false, true>(q, ldq, k, ldk, v, ldv, o, ldo, tq, tk, heads, kv_heads, scale, gate, ld_gate,
+      launch_attn_t<H, D, false, true>(q, ldq, k, ldk, v, ldv, o, ldo, tq, tk, heads, kv_heads, scale, gate, ld_gate,
                                     bias, split, grid, qtiles, s);
     const int64_t rows = batch * heads * tq;
-    attn_combine_kernel<D><<<(unsigned)((rows * (D / 4) + 255) / 256), 256, 0, s>>>(
+    attn_combine_kernel<H, D><<<(unsigned)((rows * (D / 4) + 255) / 256), 256, 0, s>>>(
         split.o, split.ml, splits, rows, (int)tq, (int)heads, (uint16_t*)o, ldo, (const uint16_t*)gate, ld_gate);
   } else if (bias.ptr) {
-    launch_attn_t<D, true, false>(q, ldq, k, ldk, v, ldv, o, ldo, tq, tk, heads, kv_heads, scale, gate, ld_gate,
+    launch_attn_t<H, D, true, false>(q, ldq, k, ldk, v, ldv, o, ldo, tq, tk, heads, kv_heads, scale, gate, ld_gate,
                                   bias, split, grid, qtiles, s);
   } else if (D == 128 && tk <= NSTAGE * BKV) {
     // few keys (a text context): they stay in LDS while a workgroup runs several query tiles
     const int qpw = resident_qpw(qtiles, heads * batch);
     const dim3 rgrid((unsigned)((qtiles + qpw - 1) / qpw * heads * batch));
-    launch_attn_t<D, false, false, D == 128>(q, ldq, k, ldk, v, ldv, o, ldo, tq, tk, heads, kv_heads, scale, gate,
+    launch_attn_t<H, D, false, false, D == 128>(q, ldq, k, ldk, v, ldv, o, ldo, tq, tk, heads, kv_heads, scale, gate,
                                              ld_gate, bias, split, rgrid, qtiles, s, qpw);
   } else {
-    launch_attn_t<D, false, false>(q, ldq, k, ldk, v, ldv, o, ldo, tq, tk, heads, kv_heads, scale, gate, ld_gate,
+    launch_attn_t<H, D, false, false>(q, ldq, k, ldk, v, ldv, o, ldo, tq, tk, heads, kv_heads, scale, gate, ld_gate,
                                    bias, split, grid, qtiles, s);
   }
-  return check_launch("kx_attention_fwd_bf16");
+  return check_launch(ename<H>("kx_attention_fwd_bf16", "kx_attention_fwd_f16"));
 }
 
 }  // namespace
@@ -646,6 +647,7 @@ int launch_attn(const void* q, int64_t ldq, const void* k, int64_t ldk, const vo
 using namespace kx;
 
 namespace {
+template <bool H>
 int attention_entry(const char* name, const void* q, int64_t ldq, const void* k, int64_t ldk,
                     const void* v, int64_t ldv, void* o, int64_t ldo, int64_t batch, int64_t tq,
                     int64_t tk, int64_t heads, int64_t kv_heads, int64_t head_dim, float scale,
@@ -673,77 +675,81 @@ int attention_entry(const char* name, const void* q, int64_t ldq, const void* k,
              name);
   if (tq == 0 || batch == 0) return KX_OK;
   if (head_dim == 128)
-    return launch_attn<128>(q, ldq, k, ldk, v, ldv, o, ldo, batch, tq, tk, heads, kv_heads, scale,
+    return launch_attn<H, 128>(q, ldq, k, ldk, v, ldv, o, ldo, batch, tq, tk, heads, kv_heads, scale,
                             gate, ld_gate, bias, split, splits, (hipStream_t)stream);
-  return launch_attn<64>(q, ldq, k, ldk, v, ldv, o, ldo, batch, tq, tk, heads, kv_heads, scale,
+  return launch_attn<H, 64>(q, ldq, k, ldk, v, ldv, o, ldo, batch, tq, tk, heads, kv_heads, scale,
                          gate, ld_gate, bias, split, splits, (hipStream_t)stream);
 }
 }  // namespace
 
-extern "C" int kx_attention_gqa_fwd_bf16(const void* q, int64_t ldq, const void* k, int64_t ldk,
-                                         const void* v, int64_t ldv, void* o, int64_t ldo,
-                                         int64_t batch, int64_t tq, int64_t tk, int64_t heads,
-                                         int64_t kv_heads, int64_t head_dim, float scale,
-                                         const void* gate, int64_t ld_gate, kx_stream_t stream) {
-  return attention_entry("kx_attention_gqa_fwd_bf16", q, ldq, k, ldk, v, ldv, o, ldo, batch, tq,
-                         tk, heads, kv_heads, head_dim, scale, gate, ld_gate, stream);
-}
+#define KX_ATTN_ENTRY(SUFFIX, H)                                                                                \
+extern "C" int kx_attention_gqa_fwd_##SUFFIX(const void* q, int64_t ldq, const void* k, int64_t ldk,                   \
+                                         const void* v, int64_t ldv, void* o, int64_t ldo,                             \
+                                         int64_t batch, int64_t tq, int64_t tk, int64_t heads,                         \
+                                         int64_t kv_heads, int64_t head_dim, float scale,                              \
+                                         const void* gate, int64_t ld_gate, kx_stream_t stream) {                      \
+  return attention_entry<H>("kx_attention_gqa_fwd_" #SUFFIX, q, ldq, k, ldk, v, ldv, o, ldo, batch, tq,                \
+                         tk, heads, kv_heads, head_dim, scale, gate, ld_gate, stream);                                 \
+}                                                                                                                      \
+                                                                                                                       \
+extern "C" int kx_attention_fwd_##SUFFIX(const void* q, int64_t ldq, const void* k, int64_t ldk,                       \
+                                     const void* v, int64_t ldv, void* o, int64_t ldo,                                 \
+                                     int64_t batch, int64_t tq, int64_t tk, int64_t heads,                             \
+                                     int64_t head_dim, float scale, const void* gate,                                  \
+                                     int64_t ld_gate, kx_stream_t stream) {                                            \
+  return attention_entry<H>("kx_attention_fwd_" #SUFFIX, q, ldq, k, ldk, v, ldv, o, ldo, batch, tq, tk,                \
+                         heads, heads, head_dim, scale, gate, ld_gate, stream);                                        \
+}                                                                                                                      \
+                                                                                                                       \
+extern "C" int kx_attention_bias_fwd_##SUFFIX(const void* q, int64_t ldq, const void* k, int64_t ldk,                  \
+                                          const void* v, int64_t ldv, void* o, int64_t ldo,                            \
+                                          int64_t batch, int64_t tq, int64_t tk, int64_t heads,                        \
+                                          int64_t kv_heads, int64_t head_dim, float scale,                             \
+                                          const void* gate, int64_t ld_gate, const void* bias,                         \
+                                          int64_t bias_bs, int64_t bias_hs, int64_t bias_qs,                           \
+                                          kx_stream_t stream) {                                                        \
+  KX_REQUIRE(bias, "kx_attention_bias_fwd_" #SUFFIX ": null bias");                                                    \
+  KX_REQUIRE(aligned8(bias) && bias_bs >= 0 && bias_hs >= 0 && bias_qs >= 0 && bias_bs % 4 == 0 &&                     \
+                 bias_hs % 4 == 0 && bias_qs % 4 == 0,                                                                 \
+             "kx_attention_bias_fwd_" #SUFFIX ": bias must be 8-byte aligned with non-negative strides that "          \
+             "are multiples of 4 elements");                                                                           \
+  KX_REQUIRE(scale > 0.0f && isfinite(scale), "kx_attention_bias_fwd_" #SUFFIX ": scale must be positive");            \
+  return attention_entry<H>("kx_attention_bias_fwd_" #SUFFIX, q, ldq, k, ldk, v, ldv, o, ldo, batch, tq, tk,           \
+                         heads, kv_heads, head_dim, scale, gate, ld_gate, stream,                                      \
+                         ScoreBias{(const uint16_t*)bias, bias_bs, bias_hs, bias_qs, 1.0f / scale});                   \
+}                                                                                                                      \
+                                                                                                                       \
+extern "C" int kx_attention_split_fwd_##SUFFIX(const void* q, int64_t ldq, const void* k, int64_t ldk,                 \
+                                           const void* v, int64_t ldv, void* o, int64_t ldo, int64_t batch,            \
+                                           int64_t tq, int64_t tk, int64_t heads, int64_t kv_heads,                    \
+                                           int64_t head_dim, float scale, const void* gate, int64_t ld_gate,           \
+                                           const void* bias, int64_t bias_bs, int64_t bias_hs, int64_t bias_qs,        \
+                                           void* workspace, int64_t workspace_bytes, int splits,                       \
+                                           kx_stream_t stream) {                                                       \
+  const char* name = "kx_attention_split_fwd_" #SUFFIX;                                                                \
+  KX_REQUIRE(workspace && aligned16(workspace), "%s: workspace must be a 16-byte aligned buffer", name);               \
+  KX_REQUIRE(splits >= 2 && splits <= 256 && tk > 0, "%s: splits must be 2..256, got %d", name, splits);               \
+  KX_REQUIRE(ldo % 4 == 0 && aligned8(o), "%s: output rows must be 8-byte aligned", name);                             \
+  /* keys per slice: a whole number of 64-key tiles; the slices actually used cover tk exactly */                      \
+  const int64_t chunk = ((tk + splits - 1) / splits + BKV - 1) / BKV * BKV;                                            \
+  const int used = (int)((tk + chunk - 1) / chunk);                                                                    \
+  const int64_t rows = batch * heads * tq;                                                                             \
+  KX_REQUIRE(workspace_bytes >= (int64_t)used * rows * (head_dim + 2) * 4,                                             \
+             "%s: workspace of %lld bytes is below splits * batch * heads * tq * (head_dim + 2) * 4", name,            \
+             (long long)workspace_bytes);                                                                              \
+  ScoreBias sb{nullptr, 0, 0, 0, 0.0f};                                                                                \
+  if (bias) {                                                                                                          \
+    KX_REQUIRE(aligned8(bias) && bias_bs >= 0 && bias_hs >= 0 && bias_qs >= 0 && bias_bs % 4 == 0 &&                   \
+                   bias_hs % 4 == 0 && bias_qs % 4 == 0,                                                               \
+               "%s: bias must be 8-byte aligned with non-negative strides that are multiples of 4", name);             \
+    KX_REQUIRE(scale > 0.0f && isfinite(scale), "%s: scale must be positive", name);                                   \
+    sb = ScoreBias{(const uint16_t*)bias, bias_bs, bias_hs, bias_qs, 1.0f / scale};                                    \
+  }                                                                                                                    \
+  float* ws = static_cast<float*>(workspace);                                                                          \
+  const SplitOut split{ws, ws + (int64_t)used * rows * head_dim, (int)chunk};                                          \
+  return attention_entry<H>(name, q, ldq, k, ldk, v, ldv, o, ldo, batch, tq, tk, heads, kv_heads, head_dim, scale,     \
+                         gate, ld_gate, stream, sb, split, used);                                                      \
+}                                                                                                                      \
 
-extern "C" int kx_attention_fwd_bf16(const void* q, int64_t ldq, const void* k, int64_t ldk,
-                                     const void* v, int64_t ldv, void* o, int64_t ldo,
-                                     int64_t batch, int64_t tq, int64_t tk, int64_t heads,
-                                     int64_t head_dim, float scale, const void* gate,
-                                     int64_t ld_gate, kx_stream_t stream) {
-  return attention_entry("kx_attention_fwd_bf16", q, ldq, k, ldk, v, ldv, o, ldo, batch, tq, tk,
-                         heads, heads, head_dim, scale, gate, ld_gate, stream);
-}
-
-extern "C" int kx_attention_bias_fwd_bf16(const void* q, int64_t ldq, const void* k, int64_t ldk,
-                                          const void* v, int64_t ldv, void* o, int64_t ldo,
-                                          int64_t batch, int64_t tq, int64_t tk, int64_t heads,
-                                          int64_t kv_heads, int64_t head_dim, float scale,
-                                          const void* gate, int64_t ld_gate, const void* bias,
-                                          int64_t bias_bs, int64_t bias_hs, int64_t bias_qs,
-                                          kx_stream_t stream) {
-  KX_REQUIRE(bias, "kx_attention_bias_fwd_bf16: null bias");
-  KX_REQUIRE(aligned8(bias) && bias_bs >= 0 && bias_hs >= 0 && bias_qs >= 0 && bias_bs % 4 == 0 &&
-                 bias_hs % 4 == 0 && bias_qs % 4 == 0,
-             "kx_attention_bias_fwd_bf16: bias must be 8-byte aligned with non-negative strides that "
-             "are multiples of 4 elements");
-  KX_REQUIRE(scale > 0.0f && isfinite(scale), "kx_attention_bias_fwd_bf16: scale must be positive");
-  return attention_entry("kx_attention_bias_fwd_bf16", q, ldq, k, ldk, v, ldv, o, ldo, batch, tq, tk,
-                         heads, kv_heads, head_dim, scale, gate, ld_gate, stream,
-                         ScoreBias{(const uint16_t*)bias, bias_bs, bias_hs, bias_qs, 1.0f / scale});
-}
-
-extern "C" int kx_attention_split_fwd_bf16(const void* q, int64_t ldq, const void* k, int64_t ldk,
-                                           const void* v, int64_t ldv, void* o, int64_t ldo, int64_t batch,
-                                           int64_t tq, int64_t tk, int64_t heads, int64_t kv_heads,
-                                           int64_t head_dim, float scale, const void* gate, int64_t ld_gate,
-                                           const void* bias, int64_t bias_bs, int64_t bias_hs, int64_t bias_qs,
-                                           void* workspace, int64_t workspace_bytes, int splits,
-                                           kx_stream_t stream) {
-  const char* name = "kx_attention_split_fwd_bf16";
-  KX_REQUIRE(workspace && aligned16(workspace), "%s: workspace must be a 16-byte aligned buffer", name);
-  KX_REQUIRE(splits >= 2 && splits <= 256 && tk > 0, "%s: splits must be 2..256, got %d", name, splits);
-  KX_REQUIRE(ldo % 4 == 0 && aligned8(o), "%s: output rows must be 8-byte aligned", name);
-  // keys per slice: a whole number of 64-key tiles; the slices actually used cover tk exactly
-  const int64_t chunk = ((tk + splits - 1) / splits + BKV - 1) / BKV * BKV;
-  const int used = (int)((tk + chunk - 1) / chunk);
-  const int64_t rows = batch * heads * tq;
-  KX_REQUIRE(workspace_bytes >= (int64_t)used * rows * (head_dim + 2) * 4,
-             "%s: workspace of %lld bytes is below splits * batch * heads * tq * (head_dim + 2) * 4", name,
-             (long long)workspace_bytes);
-  ScoreBias sb{nullptr, 0, 0, 0, 0.0f};
-  if (bias) {
-    KX_REQUIRE(aligned8(bias) && bias_bs >= 0 && bias_hs >= 0 && bias_qs >= 0 && bias_bs % 4 == 0 &&
-                   bias_hs % 4 == 0 && bias_qs % 4 == 0,
-               "%s: bias must be 8-byte aligned with non-negative strides that are multiples of 4", name);
-    KX_REQUIRE(scale > 0.0f && isfinite(scale), "%s: scale must be positive", name);
-    sb = ScoreBias{(const uint16_t*)bias, bias_bs, bias_hs, bias_qs, 1.0f / scale};
-  }
-  float* ws = static_cast<float*>(workspace);
-  const SplitOut split{ws, ws + (int64_t)used * rows * head_dim, (int)chunk};
-  return attention_entry(name, q, ldq, k, ldk, v, ldv, o, ldo, batch, tq, tk, heads, kv_heads, head_dim, scale,
-                         gate, ld_gate, stream, sb, split, used);
-}
+KX_ATTN_ENTRY(bf16, false)
+KX_ATTN_ENTRY(f16, true)

@@ -42,6 +42,69 @@ __device__ __forceinline__ uint4 pack8(const float* v) {
   return w;
 }
 
+// ---- 16-bit activations: bf16 (H = false) or fp16 (H = true) ------------------------------------
+// Widening is exact for both. Narrowing rounds to nearest even (v_cvt_pk_bf16_f32 /
+// v_cvt_pk_f16_f32); an fp16 result beyond 65504 becomes infinity, as an fp16 cast does.
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
+template <bool H>
+__device__ __forceinline__ float e2f(uint16_t b) {
+  if constexpr (H) return (float)__builtin_bit_cast(_Float16, b);
+  else return bf2f(b);
+}
+template <bool H>
+__device__ __forceinline__ float e_lo(uint32_t w) { return e2f<H>((uint16_t)(w & 0xffffu)); }
+template <bool H>
+__device__ __forceinline__ float e_hi(uint32_t w) {
+  if constexpr (H) return e2f<H>((uint16_t)(w >> 16));
+  else return hi_f(w);
+}
+template <bool H>
+__device__ __forceinline__ uint16_t f2e(float f) {
+  if constexpr (H) return __builtin_bit_cast(uint16_t, (_Float16)f);
+  else return f2bf(f);
+}
+template <bool H>
+__device__ __forceinline__ uint32_t e_pack2(float lo, float hi) {
+  if constexpr (H) return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, f16x2));
+  else return pack2(lo, hi);
+}
+template <bool H>
+__device__ __forceinline__ void e_unpack8(const uint4& w, float* v) {
+  v[0] = e_lo<H>(w.x); v[1] = e_hi<H>(w.x);
+  v[2] = e_lo<H>(w.y); v[3] = e_hi<H>(w.y);
+  v[4] = e_lo<H>(w.z); v[5] = e_hi<H>(w.z);
+  v[6] = e_lo<H>(w.w); v[7] = e_hi<H>(w.w);
+}
+template <bool H>
+__device__ __forceinline__ uint4 e_pack8(const float* v) {
+  uint4 w;
+  w.x = e_pack2<H>(v[0], v[1]);
+  w.y = e_pack2<H>(v[2], v[3]);
+  w.z = e_pack2<H>(v[4], v[5]);
+  w.w = e_pack2<H>(v[6], v[7]);
+  return w;
+}
+// One 32x32x16 MFMA on 16-bit operands held as 8 x 16-bit lanes (the bits of bf16 or fp16).
+template <bool H>
+__device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
+  if constexpr (H)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// One fp32 value rounded to the 16-bit type, as the bits of a __bf16 vector lane.
+template <bool H>
+__device__ __forceinline__ __bf16 e16(float f) {
+  if constexpr (H) return __builtin_bit_cast(__bf16, (_Float16)f);
+  else return (__bf16)f;
+}
+
+// The entry point's name for a launch of element type H (names end in _bf16 / _f16).
+template <bool H>
+constexpr const char* ename(const char* bf16_name, const char* f16_name) { return H ? f16_name : bf16_name; }
+
 // ---- activations (fp32 opmath) -----------------------------------------------------------------
 // tanh GELU with the inner argument clamped to +-10 (kinomlx/kernels/fused_ops.py:27-35), through
 // the identity 0.5 x (1 + tanh(u)) = x * sigmoid(2u) = x / (1 + e^(-2u)). The tanh form cancels in

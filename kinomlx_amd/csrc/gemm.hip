@@ -1,7 +1,8 @@
 // Dense bf16 and affine int4/int8 weight-quantized linear layers on gfx950 MFMA.
 //
 // c[m, n] = epilogue(sum_k a[m, k] * w[n, k]) — both operands K-contiguous (the reference's
-// (out, in) weight layout), fp32 accumulation in v_mfma_f32_32x32x16_bf16, one bf16 rounding.
+// (out, in) weight layout), fp32 accumulation in v_mfma_f32_32x32x16_bf16 (or _f16: the dense
+// kernels take bf16 or fp16 operands, template H), one rounding to the 16-bit type.
 //
 // Tiling: a BM x BN output tile per workgroup of WM x WN waves; each wave owns a
 // (BM/WM) x (BN/WN) sub-tile as a grid of 32x32 MFMA blocks. K advances in stages of 64: the
@@ -117,7 +118,7 @@ __device__ __forceinline__ uint4 dequant8(const uint32_t* wd, float s, float b) 
 }
 
 // QB = 0: dense bf16 weights; QB = 4 / 8: affine quantized weights of that many bits; QMX8: mxfp8.
-template <int BM, int BN, int WM, int WN, int QB>
+template <int BM, int BN, int WM, int WN, int QB, bool H = false>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ W, int64_t ldw,
     QuantW qw, void* __restrict__ C, int64_t ldc, int M, int N, int K, Epilogue epi) {
@@ -250,7 +251,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(
       for (int i = 0; i < NB; ++i)
 #pragma unroll
         for (int j = 0; j < MB; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[i], af[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = mfma32x32x16<H>(wf[i], af[j], acc[i][j]);
     }
     if (more) store_stage(smem + ((kt + 1) & 1) * STAGE);
     __syncthreads();
@@ -287,7 +288,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(
     float bias4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (has_bias) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) bias4[e] = n + e < N ? bf2f(epi.bias[n + e]) : 0.0f;
+      for (int e = 0; e < 4; ++e) bias4[e] = n + e < N ? e2f<H>(epi.bias[n + e]) : 0.0f;
     }
 #pragma unroll 2
     for (int r = lane >> 3; r < WT_M; r += 8) {
@@ -309,7 +310,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(
             rv[0] = rr.x; rv[1] = rr.y; rv[2] = rr.z; rv[3] = rr.w;
           } else {
             const uint2 rr = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(epi.resid) + ro);
-            rv[0] = lo_f(rr.x); rv[1] = hi_f(rr.x); rv[2] = lo_f(rr.y); rv[3] = hi_f(rr.y);
+            rv[0] = e_lo<H>(rr.x); rv[1] = e_hi<H>(rr.x); rv[2] = e_lo<H>(rr.y); rv[3] = e_hi<H>(rr.y);
           }
           v[0] = rv[0] + gv.x * v[0];
           v[1] = rv[1] + gv.y * v[1];
@@ -320,8 +321,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(
           *reinterpret_cast<float4*>(static_cast<float*>(C) + co) = make_float4(v[0], v[1], v[2], v[3]);
         } else {
           uint2 o;
-          o.x = pack2(v[0], v[1]);
-          o.y = pack2(v[2], v[3]);
+          o.x = e_pack2<H>(v[0], v[1]);
+          o.y = e_pack2<H>(v[2], v[3]);
           *reinterpret_cast<uint2*>(static_cast<uint16_t*>(C) + co) = o;
         }
       } else {
@@ -329,13 +330,13 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(
           float x = v[e];
           if (gated) {
             const float rv = resid_f32 ? static_cast<const float*>(epi.resid)[ro + e]
-                                       : bf2f(static_cast<const uint16_t*>(epi.resid)[ro + e]);
+                                       : e2f<H>(static_cast<const uint16_t*>(epi.resid)[ro + e]);
             x = rv + epi.gate[(m / epi.gate_div) * epi.gate_stride + n + e] * x;
           }
           if (out_f32)
             static_cast<float*>(C)[co + e] = x;
           else
-            static_cast<uint16_t*>(C)[co + e] = f2bf(x);
+            static_cast<uint16_t*>(C)[co + e] = f2e<H>(x);
         }
       }
     }
@@ -458,8 +459,15 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+// gfx9 s_waitcnt immediate that waits for lgkmcnt <= N only (LDS reads complete in order).
+template <int N>
+__device__ __forceinline__ void wait_lgkmcnt() {
+  static_assert(N >= 0 && N < 16, "lgkmcnt");
+  __builtin_amdgcn_s_waitcnt(0xC07F | (N << 8));
+}
 
 // bias + activation + gated residual on 4 consecutive columns n..n+3 of row m, then the store.
+template <bool H>
 __device__ __forceinline__ void epilogue_store4(float v[4], int m, int n, int N, const Epilogue& epi,
                                                 void* __restrict__ C, int64_t ldc, bool vec_ok) {
   const int act = (epi.flags >> 4) & 15;
@@ -471,7 +479,7 @@ __device__ __forceinline__ void epilogue_store4(float v[4], int m, int n, int N,
   if (vec_ok && n + 3 < N) {
     if (epi.flags & KX_EPI_BIAS) {
       const uint2 bb = *reinterpret_cast<const uint2*>(epi.bias + n);
-      v[0] += lo_f(bb.x); v[1] += hi_f(bb.x); v[2] += lo_f(bb.y); v[3] += hi_f(bb.y);
+      v[0] += e_lo<H>(bb.x); v[1] += e_hi<H>(bb.x); v[2] += e_lo<H>(bb.y); v[3] += e_hi<H>(bb.y);
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) v[e] = apply_act(v[e], act);
@@ -483,7 +491,7 @@ __device__ __forceinline__ void epilogue_store4(float v[4], int m, int n, int N,
         rv[0] = rr.x; rv[1] = rr.y; rv[2] = rr.z; rv[3] = rr.w;
       } else {
         const uint2 rr = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(epi.resid) + ro);
-        rv[0] = lo_f(rr.x); rv[1] = hi_f(rr.x); rv[2] = lo_f(rr.y); rv[3] = hi_f(rr.y);
+        rv[0] = e_lo<H>(rr.x); rv[1] = e_hi<H>(rr.x); rv[2] = e_lo<H>(rr.y); rv[3] = e_hi<H>(rr.y);
       }
       v[0] = rv[0] + gv.x * v[0];
       v[1] = rv[1] + gv.y * v[1];
@@ -494,25 +502,25 @@ __device__ __forceinline__ void epilogue_store4(float v[4], int m, int n, int N,
       *reinterpret_cast<float4*>(static_cast<float*>(C) + co) = make_float4(v[0], v[1], v[2], v[3]);
     } else {
       uint2 o;
-      o.x = pack2(v[0], v[1]);
-      o.y = pack2(v[2], v[3]);
+      o.x = e_pack2<H>(v[0], v[1]);
+      o.y = e_pack2<H>(v[2], v[3]);
       *reinterpret_cast<uint2*>(static_cast<uint16_t*>(C) + co) = o;
     }
     return;
   }
   for (int e = 0; e < 4 && n + e < N; ++e) {
     float x = v[e];
-    if (epi.flags & KX_EPI_BIAS) x += bf2f(epi.bias[n + e]);
+    if (epi.flags & KX_EPI_BIAS) x += e2f<H>(epi.bias[n + e]);
     x = apply_act(x, act);
     if (gated) {
       const float rv = resid_f32 ? static_cast<const float*>(epi.resid)[ro + e]
-                                 : bf2f(static_cast<const uint16_t*>(epi.resid)[ro + e]);
+                                 : e2f<H>(static_cast<const uint16_t*>(epi.resid)[ro + e]);
       x = rv + epi.gate[(m / epi.gate_div) * epi.gate_stride + n + e] * x;
     }
     if (out_f32)
       static_cast<float*>(C)[co + e] = x;
     else
-      static_cast<uint16_t*>(C)[co + e] = f2bf(x);
+      static_cast<uint16_t*>(C)[co + e] = f2e<H>(x);
   }
 }
 
@@ -528,7 +536,7 @@ __device__ __forceinline__ float act_c(float v, int act) {
 
 // One full-tile epilogue row piece: bias + activation (+ gated residual), then the store of 4
 // consecutive columns. Values by value so that nothing of the caller's frame is addressed.
-template <int GMODE, bool OUTF32, int ACT, typename ResidT>
+template <bool H, int GMODE, bool OUTF32, int ACT, typename ResidT>
 __device__ __forceinline__ void epi_row4(float4 a4, ResidT res, float b0, float b1, float b2, float b3,
                                          int act, float4 gv, char* dst) {
   float v[4] = {a4.x + b0, a4.y + b1, a4.z + b2, a4.w + b3};
@@ -541,7 +549,7 @@ __device__ __forceinline__ void epi_row4(float4 a4, ResidT res, float b0, float 
     if constexpr (GMODE == 2) {
       rv[0] = res.x; rv[1] = res.y; rv[2] = res.z; rv[3] = res.w;
     } else {
-      rv[0] = lo_f(res.x); rv[1] = hi_f(res.x); rv[2] = lo_f(res.y); rv[3] = hi_f(res.y);
+      rv[0] = e_lo<H>(res.x); rv[1] = e_hi<H>(res.x); rv[2] = e_lo<H>(res.y); rv[3] = e_hi<H>(res.y);
     }
     v[0] = rv[0] + gv.x * v[0];
     v[1] = rv[1] + gv.y * v[1];
@@ -552,8 +560,8 @@ __device__ __forceinline__ void epi_row4(float4 a4, ResidT res, float b0, float 
     *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
   } else {
     uint2 o;
-    o.x = pack2(v[0], v[1]);
-    o.y = pack2(v[2], v[3]);
+    o.x = e_pack2<H>(v[0], v[1]);
+    o.y = e_pack2<H>(v[2], v[3]);
     *reinterpret_cast<uint2*>(dst) = o;
   }
 }
@@ -565,7 +573,7 @@ __device__ __forceinline__ void epi_row4(float4 a4, ResidT res, float b0, float 
 // bf16 copy of them is written. TL: the affine weights are in the tiled layout (one contiguous
 // block per 256-row tile and stage, see kx_qweight_tile_affine), else in the reference layout
 // (one 16- or 32-byte piece per row).
-template <int BM, int BN, int QB, bool TL, int GMODE, bool OUTF32, bool NR = false>
+template <int BM, int BN, int QB, bool TL, int GMODE, bool OUTF32, bool NR = false, bool H = false>
 __global__ __launch_bounds__(256) void gemm_lds_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ W, int64_t ldw,
     QuantW qw, void* __restrict__ C, int64_t ldc, int M, int N, int K, Epilogue epi) {
@@ -579,7 +587,11 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
   constexpr int W_BYTES = QB ? BN * QROW + BN * SB_BYTES : BN * DROW;
   constexpr int STAGE = BM * DROW + W_BYTES;
   constexpr int RING = DNS * STAGE;
-  constexpr int WT_M = BM / 2, WT_N = BN / 2;
+  // wave layout: dense products 2 x 2 waves of (BM / 2) x (BN / 2); quantized weights 1 x 4 waves
+  // of BM x (BN / 4), so that each weight column is dequantized by one wave only (a 2 x 2 layout
+  // dequantizes every column twice) for the same LDS fragment traffic per MFMA as the dense form
+  constexpr int WGM = QB ? 1 : 2, WGN = 4 / WGM;
+  constexpr int WT_M = BM / WGM, WT_N = BN / WGN;
   constexpr int MB = WT_M / 32, NB = WT_N / 32;
   constexpr int KS = DBK / 16;
   static_assert(KS == 2, "two k16 steps per stage");
@@ -595,11 +607,12 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
   static_assert(QB == 0 ? (BN / DRPI / 4) * DRPI * 4 == BN : (BN == 256 && WQ_INST >= 1), "weight tile");
   static_assert(MB + NB <= 15 && WAITN >= 0, "pipeline");
   static_assert(!(TL && QB == QMX8), "mxfp8 weights are read in the reference layout only");
+  static_assert(!H || (QB == 0 && !NR), "fp16 operands: the dense product without the norm epilogue");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave & 1, wn = wave >> 1;
+  const int wm = wave % WGM, wn = wave / WGM;
   const int lrow = lane & 31, lhalf = lane >> 5;
   if constexpr (QB == 0 && GMODE == 0 && OUTF32) {
     // split-K (grid.y > 1): workgroup row y multiplies K slice y (K is the slice length) and
@@ -827,16 +840,18 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
     constexpr int NPAIR = NB * 4;
     constexpr int SB_RD = QB == QMX8 || TL ? 1 : 2;  // scale (bias) reads per block
     constexpr int NRD1 = MB + NB * (1 + SB_RD);      // LDS reads at a stage's start
-    constexpr int QSPLIT = 4;                         // MFMAs before the wait for those reads
+    constexpr int NRQ = NB * (1 + SB_RD);             // of which the packed weights and scales
+    constexpr int QSPLIT = 4;                         // MFMAs before the wait for those
     static_assert(NMF > QSPLIT, "MFMAs per step");
-    // LDS read r of a stage's start: A fragments of its step 0, raw blocks, scale words
+    // LDS read r of a stage's start: the raw blocks and scale words (needed first, by the
+    // dequantization of the stage's step 0), then the A fragments of its step 0
     auto stage_read = [&](int r, const uint8_t* buf) {
-      if (r < MB) {
-        fa[0][r] = *reinterpret_cast<const bf16x8*>(buf + a_off[0][r]);
-      } else if (r < MB + NB) {
-        raw[r - MB] = *reinterpret_cast<const Raw*>(buf + wr_off[r - MB]);
+      if (r >= NRQ) {
+        fa[0][r - NRQ] = *reinterpret_cast<const bf16x8*>(buf + a_off[0][r - NRQ]);
+      } else if (r < NB) {
+        raw[r] = *reinterpret_cast<const Raw*>(buf + wr_off[r]);
       } else {
-        const int q = r - MB - NB, i = q % NB;
+        const int q = r - NB, i = q % NB;
         if constexpr (QB == QMX8) {
           rsw[i] = *reinterpret_cast<const uint32_t*>(buf + ws_off[i]);
         } else if constexpr (TL) {
@@ -873,7 +888,7 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
 #pragma unroll
       for (int q = 0; q < NMF; ++q) {
         const int i = q / MB, j = q % MB;
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fw[0][i], fa[0][j], acc[i][j], 0, 0, 0);
+        acc[i][j] = mfma32x32x16<H>(fw[0][i], fa[0][j], acc[i][j]);
         if (q < MB) fa[1][q] = *reinterpret_cast<const bf16x8*>(cur + a_off[1][q]);
         if (q < DPS && q < PER) dma(q, iss, k_iss);
 #pragma unroll
@@ -893,7 +908,7 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
 #pragma unroll
       for (int q = 0; q < QSPLIT; ++q) {
         const int i = q / MB, j = q % MB;
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fw[1][i], fa[1][j], acc[i][j], 0, 0, 0);
+        acc[i][j] = mfma32x32x16<H>(fw[1][i], fa[1][j], acc[i][j]);
 #pragma unroll
         for (int r = q * NRD1 / QSPLIT; r < (q + 1) * NRD1 / QSPLIT; ++r) stage_read(r, nxt);
 #pragma unroll
@@ -901,13 +916,13 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
           dma(d, iss, k_iss);
         __builtin_amdgcn_sched_barrier(0);
       }
-      wait_lgkmcnt0();
+      wait_lgkmcnt<MB>();
       stage_scales(kt + 1);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int q = QSPLIT; q < NMF; ++q) {
         const int i = q / MB, j = q % MB;
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fw[1][i], fa[1][j], acc[i][j], 0, 0, 0);
+        acc[i][j] = mfma32x32x16<H>(fw[1][i], fa[1][j], acc[i][j]);
 #pragma unroll
         for (int idx = (q - QSPLIT) * NPAIR / (NMF - QSPLIT); idx < (q - QSPLIT + 1) * NPAIR / (NMF - QSPLIT); ++idx)
           dq_step(idx, 0);
@@ -947,7 +962,7 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
         for (int i = 0; i < NB; ++i)
 #pragma unroll
           for (int j = 0; j < MB; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fw[b][i], fa[b][j], acc[i][j], 0, 0, 0);
+            acc[i][j] = mfma32x32x16<H>(fw[b][i], fa[b][j], acc[i][j]);
         // the next step's fragment reads one per MFMA (a burst of them fills the LDS command
         // queue and stalls the wave before its MFMAs), then the DMA issues between the
         // remaining MFMAs
@@ -1017,8 +1032,8 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
   static_assert(NROW * RPI_EP == WT_M, "epilogue rows");
   // residual rows are prefetched in chunks of PF rows. 256-row tiles hold all 256 accumulator
   // registers through the epilogue and have no room for the prefetch: they read the residual
-  // row by row (PREF false).
-  constexpr bool PREF = GMODE != 0 && BM <= 192;
+  // row by row (PREF false); so do the 1 x 4 quantized layouts, whose lanes hold 192 or 256 rows.
+  constexpr bool PREF = GMODE != 0 && BM <= 192 && WGM == 2;
   constexpr int PF = NROW > 24 ? NROW / 2 : NROW;
   constexpr int NCH = NROW / PF;
   static_assert(NCH * PF == NROW && PF % 4 == 0, "epilogue chunks");
@@ -1066,7 +1081,7 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
       float b4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
       if (has_bias) {
         const uint2 bb = *reinterpret_cast<const uint2*>(epi.bias + n);
-        b4[0] = lo_f(bb.x); b4[1] = hi_f(bb.x); b4[2] = lo_f(bb.y); b4[3] = hi_f(bb.y);
+        b4[0] = e_lo<H>(bb.x); b4[1] = e_hi<H>(bb.x); b4[2] = e_lo<H>(bb.y); b4[3] = e_hi<H>(bb.y);
       }
 #pragma unroll
       for (int k = 0; k < (NR ? NROW : 1); ++k) {
@@ -1090,7 +1105,7 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
       float b4[4] = {0.0f, 0.0f, 0.0f, 0.0f}, w4[4];
       if (has_bias) {
         const uint2 bb = *reinterpret_cast<const uint2*>(epi.bias + n);
-        b4[0] = lo_f(bb.x); b4[1] = hi_f(bb.x); b4[2] = lo_f(bb.y); b4[3] = hi_f(bb.y);
+        b4[0] = e_lo<H>(bb.x); b4[1] = e_hi<H>(bb.x); b4[2] = e_lo<H>(bb.y); b4[3] = e_hi<H>(bb.y);
       }
       if (epi.n_bf16) {
         const uint2 ww = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(nr_w) + d);
@@ -1170,7 +1185,7 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
       float b4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
       if (has_bias) {
         const uint2 bb = *reinterpret_cast<const uint2*>(epi.bias + n);
-        b4[0] = lo_f(bb.x); b4[1] = hi_f(bb.x); b4[2] = lo_f(bb.y); b4[3] = hi_f(bb.y);
+        b4[0] = e_lo<H>(bb.x); b4[1] = e_hi<H>(bb.x); b4[2] = e_lo<H>(bb.y); b4[3] = e_hi<H>(bb.y);
       }
       const int64_t gstride = epi.gate_stride, gdiv = epi.gate_div;
       const bool gate_const = GMODE == 0 || gstride == 0 || (mrow0 / gdiv) == ((mrow0 + WT_M - 1) / gdiv);
@@ -1194,7 +1209,7 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
                 gv = *reinterpret_cast<const float4*>(epi.gate + grow * gstride + n);
               }
             }
-            epi_row4<GMODE, OUTF32, ACT>(*reinterpret_cast<const float4*>(ep + r * PITCH + 4 * q), res, b4[0],
+            epi_row4<H, GMODE, OUTF32, ACT>(*reinterpret_cast<const float4*>(ep + r * PITCH + 4 * q), res, b4[0],
                                          b4[1], b4[2], b4[3], act, gv, cbase + (int64_t)r * ldc * (OUTF32 ? 4 : 2));
           }
         } else {
@@ -1218,7 +1233,7 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
                   const int64_t grow = gdiv == 1 ? (int64_t)(mrow0 + r) : (int64_t)(mrow0 + r) / gdiv;
                   gv = *reinterpret_cast<const float4*>(epi.gate + grow * gstride + n);
                 }
-                epi_row4<GMODE, OUTF32, ACT>(a4[k], rpre[k0 + k], b4[0], b4[1], b4[2], b4[3], act, gv,
+                epi_row4<H, GMODE, OUTF32, ACT>(a4[k], rpre[k0 + k], b4[0], b4[1], b4[2], b4[3], act, gv,
                                              cbase + (int64_t)r * ldc * (OUTF32 ? 4 : 2));
               }
               __builtin_amdgcn_sched_barrier(0);
@@ -1240,7 +1255,7 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
         const float4 a4 = *reinterpret_cast<const float4*>(ep + r * PITCH + 4 * q);
         if (m < M && n < N) {
           float v[4] = {a4.x, a4.y, a4.z, a4.w};
-          epilogue_store4(v, m, n, N, epi, C, ldc, vec_ok);
+          epilogue_store4<H>(v, m, n, N, epi, C, ldc, vec_ok);
         }
       }
     }
@@ -1259,7 +1274,16 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
 // row) instead of the 32 rows of a 32x32x16 operand, which halves the cache lines each load
 // instruction touches, the limit of this kernel.
 // Quantized weights are dequantized in registers with the arithmetic of the other kernels.
-template <int QB, int NWK>
+// One 16x16x32 MFMA on 16-bit operands (bf16, or fp16 with H).
+template <bool H>
+__device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
+  if constexpr (H)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+template <int QB, int NWK, bool H = false>
 __global__ __launch_bounds__(NWK * 64) void gemm_skinny_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ W, int64_t ldw,
     QuantW qw, void* __restrict__ C, int64_t ldc, int M, int N, int K, Epilogue epi) {
@@ -1307,10 +1331,10 @@ __global__ __launch_bounds__(NWK * 64) void gemm_skinny_kernel(
     const bf16x8 w0 = wfrag(wrow_i[0], k + 8 * lq), w1 = wfrag(wrow_i[1], k + 8 * lq);
     const bf16x8 x0 = *reinterpret_cast<const bf16x8*>(arow0 + k);
     const bf16x8 x1 = *reinterpret_cast<const bf16x8*>(arow1 + k);
-    acc[0][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, x0, acc[0][0], 0, 0, 0);
-    acc[0][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w0, x1, acc[0][1], 0, 0, 0);
-    acc[1][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, x0, acc[1][0], 0, 0, 0);
-    acc[1][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1, x1, acc[1][1], 0, 0, 0);
+    acc[0][0] = mfma16x16x32<H>(w0, x0, acc[0][0]);
+    acc[0][1] = mfma16x16x32<H>(w0, x1, acc[0][1]);
+    acc[1][0] = mfma16x16x32<H>(w1, x0, acc[1][0]);
+    acc[1][1] = mfma16x16x32<H>(w1, x1, acc[1][1]);
   }
 #pragma unroll
   for (int a = 0; a < 4; ++a)
@@ -1329,7 +1353,7 @@ __global__ __launch_bounds__(NWK * 64) void gemm_skinny_kernel(
     for (int e = 0; e < 4; ++e) v[e] += part[p][4 * wave + e][lane];
   if (row < M && col < N) {
     const bool vec_ok = (ldc % 4 == 0) && (!(epi.flags & KX_EPI_GATED_RESIDUAL) || epi.ldr % 4 == 0);
-    epilogue_store4(v, row, col, N, epi, C, ldc, vec_ok);
+    epilogue_store4<H>(v, row, col, N, epi, C, ldc, vec_ok);
   }
 }
 
@@ -1337,12 +1361,12 @@ __global__ __launch_bounds__(NWK * 64) void gemm_skinny_kernel(
 
 enum TileCfg { T256x256 = 0, T256x128 = 1, T128x128 = 2, T64x64 = 3, T128x64 = 4 };
 
-template <int BM, int BN, int WM, int WN, int QB>
+template <int BM, int BN, int WM, int WN, int QB, bool H = false>
 int launch_cfg(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, QuantW qw,
                void* c, int64_t ldc, int m, int n, int k, const Epilogue& epi,
                hipStream_t s) {
   const int tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
-  gemm_kernel<BM, BN, WM, WN, QB><<<tiles, WM * WN * 64, 0, s>>>(a, lda, w, ldw, qw, c, ldc, m, n,
+  gemm_kernel<BM, BN, WM, WN, QB, H><<<tiles, WM * WN * 64, 0, s>>>(a, lda, w, ldw, qw, c, ldc, m, n,
                                                                 k, epi);
   return KX_OK;
 }
@@ -1366,28 +1390,28 @@ int pick_cfg(int64_t m, int64_t n) {
   return T128x128;
 }
 
-template <int BM, int BN, int QB, bool TL, int GMODE, bool OUTF32, bool NR = false>
+template <int BM, int BN, int QB, bool TL, int GMODE, bool OUTF32, bool NR = false, bool H = false>
 int launch_lds_t(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, QuantW qw, void* c,
                  int64_t ldc, int m, int n, int k, const Epilogue& epi, hipStream_t s) {
   const int tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
-  gemm_lds_kernel<BM, BN, QB, TL, GMODE, OUTF32, NR><<<tiles, 256, 0, s>>>(a, lda, w, ldw, qw, c, ldc, m, n, k,
+  gemm_lds_kernel<BM, BN, QB, TL, GMODE, OUTF32, NR, H><<<tiles, 256, 0, s>>>(a, lda, w, ldw, qw, c, ldc, m, n, k,
                                                                            epi);
   return KX_OK;
 }
 
 // Residual mode (none / bf16 / fp32) and output type select the epilogue specialisation.
-template <int BM, int BN, int QB, bool TL = false>
+template <int BM, int BN, int QB, bool TL = false, bool H = false>
 int launch_lds(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, QuantW qw, void* c,
                int64_t ldc, int m, int n, int k, const Epilogue& epi, hipStream_t s) {
   const int gmode = (epi.flags & KX_EPI_GATED_RESIDUAL) ? ((epi.flags & KX_EPI_RESID_F32) ? 2 : 1) : 0;
   const bool out32 = epi.flags & KX_EPI_OUT_F32;
   switch (gmode * 2 + (out32 ? 1 : 0)) {
-    case 0: return launch_lds_t<BM, BN, QB, TL, 0, false>(a, lda, w, ldw, qw, c, ldc, m, n, k, epi, s);
-    case 1: return launch_lds_t<BM, BN, QB, TL, 0, true>(a, lda, w, ldw, qw, c, ldc, m, n, k, epi, s);
-    case 2: return launch_lds_t<BM, BN, QB, TL, 1, false>(a, lda, w, ldw, qw, c, ldc, m, n, k, epi, s);
-    case 3: return launch_lds_t<BM, BN, QB, TL, 1, true>(a, lda, w, ldw, qw, c, ldc, m, n, k, epi, s);
-    case 4: return launch_lds_t<BM, BN, QB, TL, 2, false>(a, lda, w, ldw, qw, c, ldc, m, n, k, epi, s);
-    default: return launch_lds_t<BM, BN, QB, TL, 2, true>(a, lda, w, ldw, qw, c, ldc, m, n, k, epi, s);
+    case 0: return launch_lds_t<BM, BN, QB, TL, 0, false, false, H>(a, lda, w, ldw, qw, c, ldc, m, n, k, epi, s);
+    case 1: return launch_lds_t<BM, BN, QB, TL, 0, true, false, H>(a, lda, w, ldw, qw, c, ldc, m, n, k, epi, s);
+    case 2: return launch_lds_t<BM, BN, QB, TL, 1, false, false, H>(a, lda, w, ldw, qw, c, ldc, m, n, k, epi, s);
+    case 3: return launch_lds_t<BM, BN, QB, TL, 1, true, false, H>(a, lda, w, ldw, qw, c, ldc, m, n, k, epi, s);
+    case 4: return launch_lds_t<BM, BN, QB, TL, 2, false, false, H>(a, lda, w, ldw, qw, c, ldc, m, n, k, epi, s);
+    default: return launch_lds_t<BM, BN, QB, TL, 2, true, false, H>(a, lda, w, ldw, qw, c, ldc, m, n, k, epi, s);
   }
 }
 
@@ -1419,7 +1443,7 @@ int pick_lds_cfg(int64_t m, int64_t n) {
   return best;
 }
 
-template <int QB>
+template <int QB, bool H = false>
 int dispatch(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, QuantW qw,
              void* c, int64_t ldc, int64_t m, int64_t n, int64_t k, const Epilogue& epi,
              hipStream_t s) {
@@ -1427,16 +1451,16 @@ int dispatch(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, Qua
   const bool use_legacy = legacy && *legacy;
   if (n <= 64 && k % 128 == 0 && !use_legacy) {
     const dim3 grid((unsigned)((m + 31) / 32), (unsigned)((n + 31) / 32));
-    gemm_skinny_kernel<QB, 4><<<grid, 256, 0, s>>>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi);
+    gemm_skinny_kernel<QB, 4, H><<<grid, 256, 0, s>>>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi);
     return KX_OK;
   }
   // the direct-to-LDS kernel keeps per-lane 32-bit byte offsets within a 256-row tile
   if (QB == 0 && k % DBK == 0 && lda <= (1 << 22) && ldw <= (1 << 22) && !use_legacy) {
     switch (pick_lds_cfg(m, n)) {
-      case 0: return launch_lds<256, 256, 0>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi, s);
-      case 1: return launch_lds<192, 256, 0>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi, s);
-      case 2: return launch_lds<128, 128, 0>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi, s);
-      default: return launch_lds<64, 128, 0>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi, s);
+      case 0: return launch_lds<256, 256, 0, false, H>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi, s);
+      case 1: return launch_lds<192, 256, 0, false, H>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi, s);
+      case 2: return launch_lds<128, 128, 0, false, H>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi, s);
+      default: return launch_lds<64, 128, 0, false, H>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi, s);
     }
   }
   // quantized weights: the direct-to-LDS kernel with in-LDS dequantization needs whole 128-wide
@@ -1459,25 +1483,26 @@ int dispatch(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, Qua
   }
   switch (pick_cfg(m, n)) {
     case T256x256:
-      return launch_cfg<256, 256, 2, 2, QB>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k,
+      return launch_cfg<256, 256, 2, 2, QB, H>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k,
                                             epi, s);
     case T256x128:
-      return launch_cfg<256, 128, 2, 2, QB>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k,
+      return launch_cfg<256, 128, 2, 2, QB, H>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k,
                                             epi, s);
     case T128x128:
-      return launch_cfg<128, 128, 2, 2, QB>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k,
+      return launch_cfg<128, 128, 2, 2, QB, H>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k,
                                             epi, s);
     case T128x64:
-      return launch_cfg<128, 64, 2, 2, QB>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k,
+      return launch_cfg<128, 64, 2, 2, QB, H>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k,
                                            epi, s);
     default:
-      return launch_cfg<64, 64, 2, 2, QB>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi,
+      return launch_cfg<64, 64, 2, 2, QB, H>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi,
                                           s);
   }
 }
 
 // Split-K reduction: c = epilogue(sum over the planes of the fp32 partial products), 4 columns
 // of one row per thread (the planes are (M, N) fp32, N a multiple of 4).
+template <bool H>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ parts, int splits,
                                                             int M, int N, void* __restrict__ C, int64_t ldc,
                                                             Epilogue epi, bool vec_ok) {
@@ -1495,15 +1520,15 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
     acc.w += p.w;
   }
   float v[4] = {acc.x, acc.y, acc.z, acc.w};
-  epilogue_store4(v, m, n, N, epi, C, ldc, vec_ok);
+  epilogue_store4<H>(v, m, n, N, epi, C, ldc, vec_ok);
 }
 
-template <int BM, int BN>
+template <int BM, int BN, bool H>
 int launch_splitk(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, float* parts, int m, int n,
                   int k, int splits, hipStream_t s) {
   const dim3 grid((unsigned)(((m + BM - 1) / BM) * ((n + BN - 1) / BN)), (unsigned)splits);
   const Epilogue plain{nullptr, nullptr, 0, nullptr, 1, 0, KX_EPI_OUT_F32};
-  gemm_lds_kernel<BM, BN, 0, false, 0, true><<<grid, 256, 0, s>>>(a, lda, w, ldw, QuantW{}, parts, n, m, n,
+  gemm_lds_kernel<BM, BN, 0, false, 0, true, false, H><<<grid, 256, 0, s>>>(a, lda, w, ldw, QuantW{}, parts, n, m, n,
                                                                    k / splits, plain);
   return KX_OK;
 }
@@ -1574,28 +1599,42 @@ int check_epilogue(const char* name, int epilogue, const void* bias, const void*
 
 using namespace kx;
 
-extern "C" int kx_gemm_bf16(const void* a, int64_t lda, const void* w, int64_t ldw,
-                            const void* bias, void* c, int64_t ldc, int64_t m, int64_t n,
-                            int64_t k, int epilogue, const void* resid, int64_t ldr,
-                            const float* gate, int64_t gate_div, int64_t gate_stride,
-                            kx_stream_t stream) {
-  KX_REQUIRE(a && w && c, "kx_gemm_bf16: null tensor");
+namespace {
+template <bool H>
+int gemm_entry(const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias, void* c, int64_t ldc,
+               int64_t m, int64_t n, int64_t k, int epilogue, const void* resid, int64_t ldr, const float* gate,
+               int64_t gate_div, int64_t gate_stride, hipStream_t s) {
+  const char* what = ename<H>("kx_gemm_bf16", "kx_gemm_f16");
+  KX_REQUIRE(a && w && c, "%s: null tensor", what);
   KX_REQUIRE(m >= 0 && n >= 0 && k > 0 && m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 30),
-             "kx_gemm_bf16: bad shape (%lld, %lld, %lld)", (long long)m, (long long)n,
-             (long long)k);
+             "%s: bad shape (%lld, %lld, %lld)", what, (long long)m, (long long)n, (long long)k);
   KX_REQUIRE(k % 8 == 0 && lda % 8 == 0 && ldw % 8 == 0 && lda >= k && ldw >= k && ldc >= n,
-             "kx_gemm_bf16: k, lda and ldw must be multiples of 8 (k=%lld lda=%lld ldw=%lld)",
-             (long long)k, (long long)lda, (long long)ldw);
-  KX_REQUIRE(aligned16(a) && aligned16(w) && aligned8(c), "kx_gemm_bf16: a/w must be 16-byte "
-             "and c 8-byte aligned");
-  const int rc = check_epilogue("kx_gemm_bf16", epilogue, bias, c, ldc, resid, ldr, n, gate,
-                                gate_div, gate_stride);
+             "%s: k, lda and ldw must be multiples of 8 (k=%lld lda=%lld ldw=%lld)", what, (long long)k,
+             (long long)lda, (long long)ldw);
+  KX_REQUIRE(aligned16(a) && aligned16(w) && aligned8(c), "%s: a/w must be 16-byte and c 8-byte aligned", what);
+  const int rc = check_epilogue(what, epilogue, bias, c, ldc, resid, ldr, n, gate, gate_div, gate_stride);
   if (rc) return rc;
   if (m == 0 || n == 0) return KX_OK;
   const Epilogue epi{(const uint16_t*)bias, resid, ldr, gate, gate_div, gate_stride, epilogue};
-  dispatch<0>((const uint16_t*)a, lda, (const uint16_t*)w, ldw, QuantW{}, c, ldc, m, n, k, epi,
-              (hipStream_t)stream);
-  return check_launch("kx_gemm_bf16");
+  dispatch<0, H>((const uint16_t*)a, lda, (const uint16_t*)w, ldw, QuantW{}, c, ldc, m, n, k, epi, s);
+  return check_launch(what);
+}
+}  // namespace
+
+extern "C" int kx_gemm_bf16(const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias, void* c,
+                            int64_t ldc, int64_t m, int64_t n, int64_t k, int epilogue, const void* resid,
+                            int64_t ldr, const float* gate, int64_t gate_div, int64_t gate_stride,
+                            kx_stream_t stream) {
+  return gemm_entry<false>(a, lda, w, ldw, bias, c, ldc, m, n, k, epilogue, resid, ldr, gate, gate_div, gate_stride,
+                           (hipStream_t)stream);
+}
+
+extern "C" int kx_gemm_f16(const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias, void* c,
+                           int64_t ldc, int64_t m, int64_t n, int64_t k, int epilogue, const void* resid,
+                           int64_t ldr, const float* gate, int64_t gate_div, int64_t gate_stride,
+                           kx_stream_t stream) {
+  return gemm_entry<true>(a, lda, w, ldw, bias, c, ldc, m, n, k, epilogue, resid, ldr, gate, gate_div, gate_stride,
+                          (hipStream_t)stream);
 }
 
 extern "C" int kx_gemm_qknorm_rope_bf16(const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias,
@@ -1829,6 +1868,7 @@ int check_splitk(const char* what, const void* a, int64_t lda, const void* w, in
 
 // Both passes of a split-K product on `parts` (splits * m * n floats): every slice writes all of its
 // (m, n) plane before the reduction reads it, so `parts` needs no clearing between calls.
+template <bool H>
 int run_splitk(const char* what, const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias,
                void* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int epilogue, const void* resid,
                int64_t ldr, const float* gate, int64_t gate_div, int64_t gate_stride, float* parts, int splits,
@@ -1836,17 +1876,17 @@ int run_splitk(const char* what, const void* a, int64_t lda, const void* w, int6
   // slices of 256x256 tiles for the tail rows of a large product (a few 256-row tiles across a wide
   // N, each slice a quarter or less of K); up to 512 rows keep the 64x128 / 128x128 tiles
   if (m > 512 && n >= 1024)
-    launch_splitk<256, 256>((const uint16_t*)a, lda, (const uint16_t*)w, ldw, parts, (int)m, (int)n, (int)k, splits,
+    launch_splitk<256, 256, H>((const uint16_t*)a, lda, (const uint16_t*)w, ldw, parts, (int)m, (int)n, (int)k, splits,
                             s);
   else if (pick_lds_cfg(m, n) == 3)
-    launch_splitk<64, 128>((const uint16_t*)a, lda, (const uint16_t*)w, ldw, parts, (int)m, (int)n, (int)k, splits, s);
+    launch_splitk<64, 128, H>((const uint16_t*)a, lda, (const uint16_t*)w, ldw, parts, (int)m, (int)n, (int)k, splits, s);
   else
-    launch_splitk<128, 128>((const uint16_t*)a, lda, (const uint16_t*)w, ldw, parts, (int)m, (int)n, (int)k, splits,
+    launch_splitk<128, 128, H>((const uint16_t*)a, lda, (const uint16_t*)w, ldw, parts, (int)m, (int)n, (int)k, splits,
                             s);
   const Epilogue epi{(const uint16_t*)bias, resid, ldr, gate, gate_div, gate_stride, epilogue};
   const bool vec_ok = (ldc % 4 == 0) && (!(epilogue & KX_EPI_GATED_RESIDUAL) || ldr % 4 == 0);
   const int64_t threads = m * (n / 4);
-  splitk_reduce_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, s>>>(parts, splits, (int)m, (int)n, c, ldc, epi,
+  splitk_reduce_kernel<H><<<(unsigned)((threads + 255) / 256), 256, 0, s>>>(parts, splits, (int)m, (int)n, c, ldc, epi,
                                                                          vec_ok);
   return check_launch(what);
 }
@@ -1883,12 +1923,13 @@ int scratch_address(const char* what, float** out) {
 
 }  // namespace
 
-extern "C" int kx_gemm_splitk_bf16(const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias,
-                                   void* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int epilogue,
-                                   const void* resid, int64_t ldr, const float* gate, int64_t gate_div,
-                                   int64_t gate_stride, void* workspace, int64_t workspace_bytes, int splits,
-                                   kx_stream_t stream) {
-  const char* what = "kx_gemm_splitk_bf16";
+namespace {
+template <bool H>
+int splitk_entry(const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias, void* c, int64_t ldc,
+                 int64_t m, int64_t n, int64_t k, int epilogue, const void* resid, int64_t ldr, const float* gate,
+                 int64_t gate_div, int64_t gate_stride, void* workspace, int64_t workspace_bytes, int splits,
+                 hipStream_t s) {
+  const char* what = ename<H>("kx_gemm_splitk_bf16", "kx_gemm_splitk_f16");
   KX_REQUIRE(workspace, "%s: null tensor", what);
   const int rc = check_splitk(what, a, lda, w, ldw, bias, c, ldc, m, n, k, epilogue, resid, ldr, gate, gate_div,
                               gate_stride, splits);
@@ -1897,9 +1938,23 @@ extern "C" int kx_gemm_splitk_bf16(const void* a, int64_t lda, const void* w, in
   KX_REQUIRE(workspace_bytes >= (int64_t)splits * m * n * 4,
              "%s: workspace of %lld bytes is below splits * m * n * 4 = %lld", what, (long long)workspace_bytes,
              (long long)splits * m * n * 4);
-  return run_splitk(what, a, lda, w, ldw, bias, c, ldc, m, n, k, epilogue, resid, ldr, gate, gate_div, gate_stride,
-                    static_cast<float*>(workspace), splits, (hipStream_t)stream);
+  return run_splitk<H>(what, a, lda, w, ldw, bias, c, ldc, m, n, k, epilogue, resid, ldr, gate, gate_div,
+                       gate_stride, static_cast<float*>(workspace), splits, s);
 }
+}  // namespace
+
+#define KX_SPLITK_ENTRY(SUFFIX, H)                                                                                \
+  extern "C" int kx_gemm_splitk_##SUFFIX(const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias, \
+                                         void* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int epilogue,     \
+                                         const void* resid, int64_t ldr, const float* gate, int64_t gate_div,     \
+                                         int64_t gate_stride, void* workspace, int64_t workspace_bytes,           \
+                                         int splits, kx_stream_t stream) {                                        \
+    return splitk_entry<H>(a, lda, w, ldw, bias, c, ldc, m, n, k, epilogue, resid, ldr, gate, gate_div,          \
+                           gate_stride, workspace, workspace_bytes, splits, (hipStream_t)stream);                \
+  }
+
+KX_SPLITK_ENTRY(bf16, false)
+KX_SPLITK_ENTRY(f16, true)
 
 extern "C" int kx_gemm_splitk_noalloc_bf16(const void* a, int64_t lda, const void* w, int64_t ldw,
                                            const void* bias, void* c, int64_t ldc, int64_t m, int64_t n, int64_t k,
@@ -1915,6 +1970,6 @@ extern "C" int kx_gemm_splitk_noalloc_bf16(const void* a, int64_t lda, const voi
   float* parts = nullptr;
   const int arc = scratch_address(what, &parts);
   if (arc) return arc;
-  return run_splitk(what, a, lda, w, ldw, bias, c, ldc, m, n, k, epilogue, resid, ldr, gate, gate_div, gate_stride,
-                    parts, splits, (hipStream_t)stream);
+  return run_splitk<false>(what, a, lda, w, ldw, bias, c, ldc, m, n, k, epilogue, resid, ldr, gate, gate_div,
+                           gate_stride, parts, splits, (hipStream_t)stream);
 }

@@ -12,6 +12,7 @@ namespace {
 
 // Vectorized split RoPE: each thread rotates 8 consecutive pairs (i .. i+7 of one head) of one
 // row; requires half % 8 == 0 and 16-byte aligned rows and tables.
+template <bool H>
 __global__ __launch_bounds__(256) void rope_split_vec(
     const uint16_t* __restrict__ x, int64_t ldx, uint16_t* __restrict__ y, int64_t ldy,
     int64_t tokens, int heads, int half, const float* __restrict__ cosp,
@@ -26,8 +27,8 @@ __global__ __launch_bounds__(256) void rope_split_vec(
   const int64_t entry = ((table_batched ? b : 0) * tokens + t) * (int64_t)(heads * half) + j8;
   const uint16_t* xr = x + row * ldx + (int64_t)h * 2 * half + i;
   float f[8], s2[8];
-  unpack8(*reinterpret_cast<const uint4*>(xr), f);
-  unpack8(*reinterpret_cast<const uint4*>(xr + half), s2);
+  e_unpack8<H>(*reinterpret_cast<const uint4*>(xr), f);
+  e_unpack8<H>(*reinterpret_cast<const uint4*>(xr + half), s2);
   const float4 c0 = *reinterpret_cast<const float4*>(cosp + entry);
   const float4 c1 = *reinterpret_cast<const float4*>(cosp + entry + 4);
   const float4 n0 = *reinterpret_cast<const float4*>(sinp + entry);
@@ -45,10 +46,11 @@ __global__ __launch_bounds__(256) void rope_split_vec(
     o2[k] = first_s + second_c;
   }
   uint16_t* yr = y + row * ldy + (int64_t)h * 2 * half + i;
-  *reinterpret_cast<uint4*>(yr) = pack8(o1);
-  *reinterpret_cast<uint4*>(yr + half) = pack8(o2);
+  *reinterpret_cast<uint4*>(yr) = e_pack8<H>(o1);
+  *reinterpret_cast<uint4*>(yr + half) = e_pack8<H>(o2);
 }
 
+template <bool H>
 __global__ __launch_bounds__(256) void rope_split_scalar(
     const uint16_t* __restrict__ x, int64_t ldx, uint16_t* __restrict__ y, int64_t ldy,
     int64_t tokens, int heads, int half, const float* __restrict__ cosp,
@@ -63,18 +65,19 @@ __global__ __launch_bounds__(256) void rope_split_scalar(
   const int64_t entry = ((table_batched ? b : 0) * tokens + t) * (int64_t)per_row + j;
   const int64_t off = (int64_t)h * 2 * half + i;
   const float c = cosp[entry], s = sinp[entry];
-  const float first = bf2f(x[row * ldx + off]);
-  const float second = bf2f(x[row * ldx + off + half]);
+  const float first = e2f<H>(x[row * ldx + off]);
+  const float second = e2f<H>(x[row * ldx + off + half]);
   const float first_c = first * c;
   const float second_s = second * s;
   const float rotated_first = first_c - second_s;
   const float first_s = first * s;
   const float second_c = second * c;
   const float rotated_second = first_s + second_c;
-  y[row * ldy + off] = f2bf(rotated_first);
-  y[row * ldy + off + half] = f2bf(rotated_second);
+  y[row * ldy + off] = f2e<H>(rotated_first);
+  y[row * ldy + off + half] = f2e<H>(rotated_second);
 }
 
+template <bool H>
 __global__ __launch_bounds__(256) void rope_pair_scalar(
     const uint16_t* __restrict__ x, int64_t ldx, uint16_t* __restrict__ y, int64_t ldy,
     int64_t rows, int heads, int head_dim, const float* __restrict__ cosp,
@@ -90,14 +93,14 @@ __global__ __launch_bounds__(256) void rope_pair_scalar(
   const float* ct = cosp + tok * table_ld + (int64_t)h * table_hs + d;
   const float* st = sinp + tok * table_ld + (int64_t)h * table_hs + d;
   const int64_t off = (int64_t)h * head_dim + d;
-  const float x0 = bf2f(x[row * ldx + off]);
-  const float x1 = bf2f(x[row * ldx + off + 1]);
+  const float x0 = e2f<H>(x[row * ldx + off]);
+  const float x1 = e2f<H>(x[row * ldx + off + 1]);
   const float a0 = x0 * ct[0];
   const float b0 = (-x1) * st[0];
   const float a1 = x1 * ct[1];
   const float b1 = x0 * st[1];
-  y[row * ldy + off] = f2bf(a0 + b0);
-  y[row * ldy + off + 1] = f2bf(a1 + b1);
+  y[row * ldy + off] = f2e<H>(a0 + b0);
+  y[row * ldy + off + 1] = f2e<H>(a1 + b1);
 }
 
 // LTX split-RoPE tables (kinomlx/models/ltx2/transformer/rope.py:95-176): for token t of batch b
@@ -134,48 +137,70 @@ __global__ __launch_bounds__(256) void ltx_rope_tables_kernel(
 
 using namespace kx;
 
-extern "C" int kx_rope_split_bf16(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t batch,
-                                  int64_t tokens, int64_t heads, int64_t half, const float* cos,
-                                  const float* sin, int table_batched, kx_stream_t stream) {
-  KX_REQUIRE(x && y && cos && sin, "kx_rope_split_bf16: null tensor");
-  KX_REQUIRE(batch >= 0 && tokens >= 0 && heads > 0 && half > 0, "kx_rope_split_bf16: bad shape");
-  KX_REQUIRE(ldx >= heads * 2 * half && ldy >= heads * 2 * half, "kx_rope_split_bf16: bad stride");
-  KX_REQUIRE(heads * half < (1ll << 30), "kx_rope_split_bf16: row too wide");
+namespace kx {
+namespace {
+
+template <bool H>
+int rope_split(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t batch, int64_t tokens, int64_t heads,
+               int64_t half, const float* cos, const float* sin, int table_batched, hipStream_t s) {
+  const char* name = ename<H>("kx_rope_split_bf16", "kx_rope_split_f16");
+  KX_REQUIRE(x && y && cos && sin, "%s: null tensor", name);
+  KX_REQUIRE(batch >= 0 && tokens >= 0 && heads > 0 && half > 0, "%s: bad shape", name);
+  KX_REQUIRE(ldx >= heads * 2 * half && ldy >= heads * 2 * half, "%s: bad stride", name);
+  KX_REQUIRE(heads * half < (1ll << 30), "%s: row too wide", name);
   const int64_t rows = batch * tokens;
   if (rows == 0) return KX_OK;
-  hipStream_t s = (hipStream_t)stream;
   const bool vec = half % 8 == 0 && ldx % 8 == 0 && ldy % 8 == 0 && aligned16(x) && aligned16(y) &&
                    aligned16(cos) && aligned16(sin);
   if (vec) {
     const int64_t total = rows * heads * half / 8;
-    rope_split_vec<<<(unsigned)((total + 255) / 256), 256, 0, s>>>(
-        (const uint16_t*)x, ldx, (uint16_t*)y, ldy, tokens, (int)heads, (int)half, cos, sin, rows,
-        table_batched);
+    rope_split_vec<H><<<(unsigned)((total + 255) / 256), 256, 0, s>>>(
+        (const uint16_t*)x, ldx, (uint16_t*)y, ldy, tokens, (int)heads, (int)half, cos, sin, rows, table_batched);
   } else {
     const int64_t total = rows * heads * half;
-    rope_split_scalar<<<(unsigned)((total + 255) / 256), 256, 0, s>>>(
-        (const uint16_t*)x, ldx, (uint16_t*)y, ldy, tokens, (int)heads, (int)half, cos, sin, rows,
-        table_batched);
+    rope_split_scalar<H><<<(unsigned)((total + 255) / 256), 256, 0, s>>>(
+        (const uint16_t*)x, ldx, (uint16_t*)y, ldy, tokens, (int)heads, (int)half, cos, sin, rows, table_batched);
   }
-  return check_launch("kx_rope_split_bf16");
+  return check_launch(name);
 }
 
-extern "C" int kx_rope_pair_bf16(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows,
-                                 int64_t heads, int64_t head_dim, const float* cos,
-                                 const float* sin, int64_t table_ld, int64_t table_hs,
-                                 int64_t tokens, int table_batched, kx_stream_t stream) {
-  KX_REQUIRE(x && y && cos && sin, "kx_rope_pair_bf16: null tensor");
-  KX_REQUIRE(rows >= 0 && heads > 0 && head_dim > 0 && head_dim % 2 == 0,
-             "kx_rope_pair_bf16: bad shape");
-  KX_REQUIRE(ldx >= heads * head_dim && ldy >= heads * head_dim, "kx_rope_pair_bf16: bad stride");
-  KX_REQUIRE(table_batched || tokens > 0, "kx_rope_pair_bf16: bad token count");
+template <bool H>
+int rope_pair(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows, int64_t heads, int64_t head_dim,
+              const float* cos, const float* sin, int64_t table_ld, int64_t table_hs, int64_t tokens,
+              int table_batched, hipStream_t s) {
+  const char* name = ename<H>("kx_rope_pair_bf16", "kx_rope_pair_f16");
+  KX_REQUIRE(x && y && cos && sin, "%s: null tensor", name);
+  KX_REQUIRE(rows >= 0 && heads > 0 && head_dim > 0 && head_dim % 2 == 0, "%s: bad shape", name);
+  KX_REQUIRE(ldx >= heads * head_dim && ldy >= heads * head_dim, "%s: bad stride", name);
+  KX_REQUIRE(table_batched || tokens > 0, "%s: bad token count", name);
   if (rows == 0) return KX_OK;
   const int64_t total = rows * heads * head_dim / 2;
-  rope_pair_scalar<<<(unsigned)((total + 255) / 256), 256, 0, (hipStream_t)stream>>>(
-      (const uint16_t*)x, ldx, (uint16_t*)y, ldy, rows, (int)heads, (int)head_dim, cos, sin,
-      table_ld, table_hs, tokens, table_batched);
-  return check_launch("kx_rope_pair_bf16");
+  rope_pair_scalar<H><<<(unsigned)((total + 255) / 256), 256, 0, s>>>(
+      (const uint16_t*)x, ldx, (uint16_t*)y, ldy, rows, (int)heads, (int)head_dim, cos, sin, table_ld, table_hs,
+      tokens, table_batched);
+  return check_launch(name);
 }
+
+}  // namespace
+}  // namespace kx
+
+#define KX_ROPE_ENTRY(SUFFIX, H)                                                                                 \
+  extern "C" int kx_rope_split_##SUFFIX(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t batch,         \
+                                        int64_t tokens, int64_t heads, int64_t half, const float* cos,            \
+                                        const float* sin, int table_batched, kx_stream_t stream) {                \
+    return rope_split<H>(x, ldx, y, ldy, batch, tokens, heads, half, cos, sin, table_batched,                    \
+                         (hipStream_t)stream);                                                                    \
+  }                                                                                                               \
+  extern "C" int kx_rope_pair_##SUFFIX(const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows,           \
+                                       int64_t heads, int64_t head_dim, const float* cos, const float* sin,       \
+                                       int64_t table_ld, int64_t table_hs, int64_t tokens, int table_batched,     \
+                                       kx_stream_t stream) {                                                      \
+    return rope_pair<H>(x, ldx, y, ldy, rows, heads, head_dim, cos, sin, table_ld, table_hs, tokens,             \
+                        table_batched, (hipStream_t)stream);                                                      \
+  }
+
+KX_ROPE_ENTRY(bf16, false)
+KX_ROPE_ENTRY(f16, true)
 
 extern "C" int kx_ltx_rope_tables(const float* positions, int64_t pos_stride, int middle,
                                   const float* max_pos, const float* grid, float* cos, float* sin,

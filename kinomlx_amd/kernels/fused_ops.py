@@ -2,8 +2,9 @@
 
 Mirror of ``kinomlx/kernels/fused_ops.py``: same names, arguments and dtype-preserving
 semantics, on torch tensors. Every function runs a hand-written gfx950 kernel from
-``libkx355.so``; there is no CPU or PyTorch fallback. Activations are bf16 (the dtype the MI355X
-path computes in); other dtypes raise ``ValueError``.
+``libkx355.so``; there is no CPU or PyTorch fallback. Activations are bf16 or fp16 (the
+reference's two transformer dtypes; the output keeps the input's); other dtypes raise
+``ValueError``.
 """
 
 from __future__ import annotations
@@ -12,12 +13,12 @@ import torch
 
 from .. import _lib
 
-_DTYPES = (torch.bfloat16,)
+_DTYPES = (torch.bfloat16, torch.float16)
 
 
 def _require(value: torch.Tensor, what: str) -> None:
     if value.dtype not in _DTYPES:
-        raise ValueError(f"{what} takes bfloat16 activations on MI355X, got {value.dtype}")
+        raise ValueError(f"{what} takes float16 or bfloat16 activations on MI355X, got {value.dtype}")
 
 
 def _empty(value: torch.Tensor) -> torch.Tensor:
@@ -66,7 +67,7 @@ def gelu_approx(value: torch.Tensor) -> torch.Tensor:
     src = value.contiguous()
     out = _empty(value)
     if value.numel():
-        _lib.launch_unary("kx_gelu_tanh_bf16", src, out)
+        _lib.launch_unary("kx_gelu_tanh", src, out)
     return out
 
 
@@ -76,7 +77,7 @@ def silu(value: torch.Tensor) -> torch.Tensor:
     src = value.contiguous()
     out = _empty(value)
     if value.numel():
-        _lib.launch_unary("kx_silu_bf16", src, out)
+        _lib.launch_unary("kx_silu", src, out)
     return out
 
 

@@ -1,9 +1,11 @@
-"""Dense bf16 linear products on gfx950 MFMA, behind the reference's ``mpp_linear`` surface.
+"""Dense bf16 / fp16 linear products on gfx950 MFMA, behind the reference's ``mpp_linear`` surface.
 
 Mirror of ``kinomlx/kernels/mpp_linear.py`` (``linear``, ``applies``, ``supports``,
 ``available``, ``prepare``, ``restore``, ``fp16_operand``, ``Operand``, ``set_enabled``,
 ``enabled``, ``linear_rows``), computing ``addmm(bias, x, W^T)``: FP32 accumulation in
-``v_mfma_f32_32x32x16_bf16``, bias added in FP32, one rounding (``mpp_linear.py:1-6``).
+``v_mfma_f32_32x32x16_bf16`` (``_f16`` for float16 operands, the reference's ``half`` MPP GEMMs,
+``mpp_linear.py:145-294``), bias added in FP32, one rounding to the input's type
+(``mpp_linear.py:1-6``).
 
 MI355X has native bf16 MFMA, so the M1's scaled-FP16 operand conversion has no counterpart:
 ``fp16_operand``/``prepare`` return the operand unchanged (``Operand(values, None)``) and
@@ -25,7 +27,7 @@ from .. import _lib
 
 MIN_ROWS = 1
 MIN_WIDTH = 8
-_DTYPES = (torch.bfloat16,)
+_DTYPES = (torch.bfloat16, torch.float16)
 _enabled = True
 
 ACTIVATIONS = {
@@ -57,8 +59,8 @@ def enabled() -> bool:
 
 
 def supports(rows: int, k: int, n: int, *, transposed: bool, dtype: torch.dtype) -> bool:
-    """Whether the kernel computes a ``rows x k`` by ``k x n`` product: bf16, ``k`` a multiple
-    of 8 (16-byte rows), 32-bit counts."""
+    """Whether the kernel computes a ``rows x k`` by ``k x n`` product: bf16 or fp16, ``k`` a
+    multiple of 8 (16-byte rows), 32-bit counts."""
     del transposed
     return (
         dtype in _DTYPES and rows >= MIN_ROWS and n >= 1 and k >= MIN_WIDTH and k % 8 == 0
@@ -98,7 +100,7 @@ def applies(value: torch.Tensor, weight: torch.Tensor | Operand, bias: torch.Ten
 
 
 def fp16_operand(value: torch.Tensor) -> Operand:
-    """The operand as the kernel multiplies it: unchanged (bf16 is native on MI355X)."""
+    """The operand as the kernel multiplies it: unchanged (bf16 and fp16 are native on MI355X)."""
     return Operand(value, None)
 
 
@@ -109,7 +111,7 @@ def prepare(weight: torch.Tensor, *, transposed: bool = True) -> Operand:
 
 
 def restore(prepared: Operand) -> torch.Tensor:
-    """The bf16 ``(out, in)`` weight a prepared operand holds."""
+    """The ``(out, in)`` weight a prepared operand holds."""
     return prepared.values
 
 
@@ -143,14 +145,16 @@ def fused_linear(
     """``residual + gate * act(value @ W^T + bias)`` in one MFMA pass (``(out, in)`` weight).
 
     ``gate`` is an fp32 row vector ``(n,)``, one per batch ``(B, 1, n)`` or per row; without
-    ``residual`` the epilogue stops after the activation. ``residual`` may be bf16 or fp32 and
-    the output (``out_dtype``, default the input dtype) bf16 or fp32: a residual stream can be
-    carried in fp32 between blocks' branches so that it is rounded once, not once per add.
+    ``residual`` the epilogue stops after the activation. ``residual`` may be of the input's
+    16-bit type or fp32 and the output (``out_dtype``, default the input dtype) likewise: a
+    residual stream can be carried in fp32 between blocks' branches so that it is rounded once, not
+    once per add.
     """
     w = _as_out_in(weight, True)
     dtype = value.dtype
     if dtype not in _DTYPES or w.dtype != dtype:
-        raise ValueError(f"the MFMA linear multiplies bf16 inputs by bf16 weights, got {dtype}, {w.dtype}")
+        raise ValueError(f"the MFMA linear multiplies float16 or bfloat16 inputs by weights of that dtype, "
+                         f"got {dtype}, {w.dtype}")
     n, k = (int(s) for s in w.shape)
     if int(value.shape[-1]) != k:
         raise ValueError(f"linear input width {value.shape[-1]} does not match weight width {k}")
@@ -162,7 +166,7 @@ def fused_linear(
     flags = ACTIVATIONS[activation]
     if bias is not None:
         if bias.dtype != dtype or bias.shape != (n,):
-            raise ValueError(f"bias must be bf16 of shape ({n},)")
+            raise ValueError(f"bias must be {dtype} of shape ({n},)")
         flags |= _lib.EPI_BIAS
         bias = bias.contiguous()
     resid2 = None

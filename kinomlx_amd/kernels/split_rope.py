@@ -17,7 +17,7 @@ import torch
 
 from .. import _lib
 
-_DTYPES = (torch.bfloat16,)
+_DTYPES = (torch.bfloat16, torch.float16)
 _enabled = True
 
 

@@ -3,12 +3,14 @@
 Mirror of ``kinomlx/models/ltx2/kernels/dense_attention.py`` (``HEAD_DIMS``, ``applies``,
 ``dense_attention``). Queries are token-major ``(query_tokens, heads * dim)`` and keys/values
 ``(key_tokens, heads * dim)`` — the layout of the projections, so neither side needs a head
-transpose and self- and cross-attention are the same call. Scores and accumulation are FP32
-(bf16 MFMA inputs); the output has the queries' shape and dtype.
+transpose and self- and cross-attention are the same call. q, k and v are float16 or bfloat16,
+multiplied on MFMA in that type (P rounded to it too); scores and accumulation are FP32, and the
+output has the queries' shape and dtype (``dense_attention.py:47,112-116``).
 
-Differences from the M1 kernel, by design: inputs stay bf16 (no FP16 saturation step: MI355X
-multiplies bf16 natively), and 64-wide heads take the kernel at any token count (the
-reference's 512-token floor was an M1 speed heuristic against MLX's SDPA).
+Differences from the M1 kernel, by design: bf16 inputs stay bf16 (no FP16 saturation step:
+MI355X multiplies bf16 natively, so values beyond the FP16 range stay finite without a clip), and
+64-wide heads take the kernel at any token count (the reference's 512-token floor was an M1 speed
+heuristic against MLX's SDPA).
 """
 
 from __future__ import annotations
@@ -18,7 +20,7 @@ import torch
 from .. import _lib
 
 HEAD_DIMS = (64, 128)
-_SUPPORTED_DTYPES = (torch.bfloat16,)
+_SUPPORTED_DTYPES = (torch.float16, torch.bfloat16)
 
 
 def applies(query: torch.Tensor, key: torch.Tensor, *, heads: int) -> bool:
@@ -40,13 +42,15 @@ def applies(query: torch.Tensor, key: torch.Tensor, *, heads: int) -> bool:
     )
 
 
-def score_bias(mask: torch.Tensor, *, batch: int, heads: int, tq: int, tk: int) -> tuple[torch.Tensor, tuple]:
-    """An SDPA mask as the kernel's additive bf16 bias and its (batch, head, query) strides.
+def score_bias(mask: torch.Tensor, *, batch: int, heads: int, tq: int, tk: int,
+               dtype: torch.dtype = torch.bfloat16) -> tuple[torch.Tensor, tuple]:
+    """An SDPA mask as the kernel's additive bias (in ``dtype``, the queries' type) and its
+    (batch, head, query) strides.
 
     Shapes follow ``_prepare_attention_mask`` (``attention.py:136-141``): ``(Tq, Tk)`` is shared
     by every batch and head, ``(B, Tq, Tk)`` by every head, ``(B | 1, H | 1, Tq | 1, Tk)`` as
-    given. A boolean mask keeps its True keys (False -> -inf); other dtypes are cast to bf16 and
-    added to the scaled scores. Broadcast axes get stride 0; rows are padded to a multiple of 4
+    given. A boolean mask keeps its True keys (False -> -inf); other dtypes are cast to ``dtype``
+    and added to the scaled scores. Broadcast axes get stride 0; rows are padded to a multiple of 4
     keys when the layout needs it."""
     if mask.dim() == 2:
         mask = mask[None, None]
@@ -59,10 +63,10 @@ def score_bias(mask: torch.Tensor, *, batch: int, heads: int, tq: int, tk: int) 
             raise ValueError(f"attention mask {tuple(mask.shape)} does not broadcast to ({batch}, {heads}, {tq}, {tk})")
     if mask.dtype == torch.bool:
         mask = torch.where(mask, 0.0, float("-inf"))
-    mask = mask.to(torch.bfloat16)
+    mask = mask.to(dtype)
     strides = [mask.stride(a) if mask.shape[a] != 1 else 0 for a in range(3)]
     if mask.stride(-1) != 1 or any(st % 4 for st in strides) or mask.data_ptr() % 8:
-        padded = torch.zeros((*mask.shape[:3], (tk + 3) // 4 * 4), dtype=torch.bfloat16, device=mask.device)
+        padded = torch.zeros((*mask.shape[:3], (tk + 3) // 4 * 4), dtype=dtype, device=mask.device)
         padded[..., :tk] = mask
         mask = padded
         strides = [mask.stride(a) if mask.shape[a] != 1 else 0 for a in range(3)]
@@ -79,12 +83,12 @@ def _attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, heads: int,
           or (batch > 1 and out.stride(0) != tq * out.stride(1))):
         raise ValueError(f"attention out must be {q.dtype} ({batch}, {tq}, {heads * dim}) with contiguous rows")
     if gate is not None:
-        if gate.dtype != torch.bfloat16 or tuple(gate.shape[-1:]) != (heads,):
-            raise ValueError(f"attention gate must be bf16 (..., {heads})")
+        if gate.dtype != q.dtype or tuple(gate.shape[-1:]) != (heads,):
+            raise ValueError(f"attention gate must be {q.dtype} (..., {heads})")
         gate = gate.reshape(batch * tq, heads)
     bias = strides = None
     if mask is not None:
-        bias, strides = score_bias(mask, batch=batch, heads=heads, tq=tq, tk=tk)
+        bias, strides = score_bias(mask, batch=batch, heads=heads, tq=tq, tk=tk, dtype=q.dtype)
     _lib.launch_attention(
         q, k, v, out, batch=batch, tq=tq, tk=tk, heads=heads, head_dim=dim,
         scale=dim ** -0.5 if scale is None else scale, gate=gate, kv_heads=kv_heads, bias=bias, bias_strides=strides,
@@ -97,8 +101,6 @@ def _check(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, heads: int, width:
         raise ValueError(
             f"dense attention needs float16 or bfloat16 q, k and v, got {q.dtype}, {k.dtype}, {v.dtype}"
         )
-    if q.dtype not in _SUPPORTED_DTYPES:
-        raise ValueError("dense attention on MI355X computes bfloat16 q, k and v, got float16")
     dim = width // heads if heads > 0 and width % heads == 0 else 0
     return dim
 
@@ -106,7 +108,7 @@ def _check(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, heads: int, width:
 def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, heads: int,
                     gate: torch.Tensor | None = None) -> torch.Tensor:
     """Dense attention of ``(query_tokens, heads * dim)`` queries over ``(key_tokens, ...)``
-    (``dense_attention.py:106-153``). ``dim`` is 64 or 128. ``gate`` (optional, bf16
+    (``dense_attention.py:106-153``). ``dim`` is 64 or 128. ``gate`` (optional, the queries' dtype,
     ``(query_tokens, heads)``) multiplies each head's output before the one rounding."""
     width = q.shape[1] if q.dim() == 2 else 0
     dim = _check(q, k, v, heads, width)

@@ -12,8 +12,9 @@ Kernel schedule of one block (B=1, T video tokens, Tc text tokens):
   -> attention -> out GEMM (+ x + g8 * .) ; AdaLN(x) -> up GEMM (GELU) -> down GEMM (+ x + g5 * .)
 Every residual add rides in a GEMM epilogue; every reduction and epilogue is FP32. Between the
 block's three branches the residual stream is carried in FP32 (written by the out-projection
-epilogues, read by the next AdaLN and epilogue) and rounded to bf16 once, by the last epilogue;
-every other intermediate is bf16. The reference rounds the stream after each branch
+epilogues, read by the next AdaLN and epilogue) and rounded to the block's 16-bit type (bf16 or
+fp16, the dtype of its weights) once, by the last epilogue; every other intermediate is of that
+type. The reference rounds the stream after each branch
 (``transformer.py:26-30`` casts to ``value.dtype``); carrying it costs 2 x T x D x 2 extra bytes
 per branch and removes two of the block's output roundings. The audio stream follows the same
 schedule at its own width, then the A/V cross-attention of each stream reads the other's
@@ -50,14 +51,28 @@ def _mod_pair(shift: torch.Tensor, scale: torch.Tensor) -> tuple[torch.Tensor, t
     return shift32, scale32
 
 
-def adaln(value: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor, eps: float) -> torch.Tensor:
+_HALF = (torch.bfloat16, torch.float16)
+
+
+def _norm_out_dtype(value: torch.Tensor, out_dtype: torch.dtype | None, what: str) -> torch.dtype:
+    if value.dtype not in (*_HALF, torch.float32):
+        raise ValueError(f"{what} takes float16 or bfloat16 (or an fp32 residual stream) on MI355X, got {value.dtype}")
+    dtype = out_dtype or (value.dtype if value.dtype in _HALF else torch.bfloat16)
+    if dtype not in _HALF:
+        raise ValueError(f"{what} writes float16 or bfloat16, not {dtype}")
+    if value.dtype in _HALF and value.dtype != dtype:
+        raise ValueError(f"{what}: a {value.dtype} input normalizes to {value.dtype}, not {dtype}")
+    return dtype
+
+
+def adaln(value: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor, eps: float,
+          out_dtype: torch.dtype | None = None) -> torch.Tensor:
     """``rms_norm(x) * (1 + scale) + shift`` in one FP32 pass (``transformer.py:16-23``).
-    ``scale``/``shift`` broadcast as ``(D,)``, ``(B, 1, D)`` or ``(B, T, D)``. ``value`` is bf16,
-    or an FP32 residual stream; the result is bf16, the dtype the next GEMM reads (the
-    reference returns ``value.dtype``)."""
-    if value.dtype not in (torch.bfloat16, torch.float32):
-        raise ValueError(f"adaln takes bfloat16 (or an fp32 residual stream) on MI355X, got {value.dtype}")
-    out = torch.empty(value.shape, dtype=torch.bfloat16, device=value.device)
+    ``scale``/``shift`` broadcast as ``(D,)``, ``(B, 1, D)`` or ``(B, T, D)``. ``value`` is bf16
+    or fp16, or an FP32 residual stream; the result is the 16-bit type the next GEMM reads:
+    ``value``'s own (as the reference returns ``value.dtype``), or ``out_dtype`` for a stream
+    (default bf16)."""
+    out = torch.empty(value.shape, dtype=_norm_out_dtype(value, out_dtype, "adaln"), device=value.device)
     if value.numel():
         shift32, scale32 = _mod_pair(shift, scale)
         _lib.launch_adaln_norm(value, out, shift32, scale32, eps, _lib.KX_NORM_RMS)
@@ -65,13 +80,12 @@ def adaln(value: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor, eps: fl
 
 
 def layer_norm_modulate(value: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor,
-                        eps: float = 1e-6) -> torch.Tensor:
+                        eps: float = 1e-6, out_dtype: torch.dtype | None = None) -> torch.Tensor:
     """``layer_norm(x) * (1 + scale) + shift`` in one FP32 pass (FLUX.2 ``normalized``,
-    ``kinomlx/models/flux2/transformer.py:56-57``). ``value`` is bf16 or an FP32 residual
-    stream; the result is bf16."""
-    if value.dtype not in (torch.bfloat16, torch.float32):
-        raise ValueError(f"layer_norm_modulate takes bfloat16 (or an fp32 residual stream) on MI355X, got {value.dtype}")
-    out = torch.empty(value.shape, dtype=torch.bfloat16, device=value.device)
+    ``kinomlx/models/flux2/transformer.py:56-57``). ``value`` is bf16 or fp16, or an FP32
+    residual stream; the result's type is chosen as ``adaln``'s."""
+    out = torch.empty(value.shape, dtype=_norm_out_dtype(value, out_dtype, "layer_norm_modulate"),
+                      device=value.device)
     if value.numel():
         shift32, scale32 = _mod_pair(shift, scale)
         _lib.launch_adaln_norm(value, out, shift32, scale32, eps, _lib.KX_NORM_LAYER)
@@ -101,6 +115,15 @@ def gate(value: torch.Tensor, gate_value: torch.Tensor) -> torch.Tensor:
     if value.numel():
         _lib.launch_gated_residual(None, value, out, _mod32(gate_value))
     return out
+
+
+def compute_dtype(attention: Attention) -> torch.dtype:
+    """The 16-bit type an attention's projections multiply in: its output projection's weight
+    dtype when that is float16 or bfloat16 (the transformer dtype), else bf16 (quantized layers
+    dequantize to bf16)."""
+    weight = getattr(attention.to_out, "weight", None)
+    dtype = getattr(weight, "dtype", None)
+    return dtype if dtype in _HALF else torch.bfloat16
 
 
 # The reference's private names and their compiled forms map to the same fused kernels.
@@ -224,7 +247,7 @@ class BasicAVTransformerBlock:
         attention = self.attn2 if attention is None else attention
         prompt_table = self.prompt_scale_shift_table if prompt_table is None else prompt_table
         prompt = _lib.table_add(prompt_table, args.prompt_timestep)
-        query = adaln(value, ada[:, :, 7], ada[:, :, 6], self.norm_eps)
+        query = adaln(value, ada[:, :, 7], ada[:, :, 6], self.norm_eps, compute_dtype(attention))
         context = modulate(args.context, prompt[:, :, 1], prompt[:, :, 0])
         return attention(query, context=context, mask=args.context_mask, residual=value, gate=ada[:, :, 8],
                          out_dtype=torch.float32)
@@ -235,7 +258,7 @@ class BasicAVTransformerBlock:
             raise ValueError("sparse (Sol-Attn) attention is not built for MI355X")
         x = args.x
         ada = _lib.table_add(table, args.timesteps)
-        normalized = adaln(x, ada[:, :, 1], ada[:, :, 0], self.norm_eps)
+        normalized = adaln(x, ada[:, :, 1], ada[:, :, 0], self.norm_eps, compute_dtype(attn1))
         x1 = attn1(normalized, pe=args.positional_embeddings, mask=args.self_attention_mask, residual=x,
                    gate=ada[:, :, 2], out_dtype=torch.float32)
         return self._text_cross_attention(x1, args, ada, attn2, prompt_table), ada
@@ -272,25 +295,29 @@ class BasicAVTransformerBlock:
             video_base, audio_base = video_value, audio_value
             # rms_norm(x) * (1 + scale) + shift is one AdaLN pass per (stream, direction)
             if run_a2v:
-                query = adaln(video_base, v_scale_a2v, v_shift_a2v, self.norm_eps)
-                context = adaln(audio_base, a_scale_a2v, a_shift_a2v, self.norm_eps)
+                cdt = compute_dtype(self.audio_to_video_attn)
+                query = adaln(video_base, v_scale_a2v, v_shift_a2v, self.norm_eps, cdt)
+                context = adaln(audio_base, a_scale_a2v, a_shift_a2v, self.norm_eps, cdt)
                 video_value = self.audio_to_video_attn(
                     query, context=context, pe=video.cross_positional_embeddings,
                     k_pe=audio.cross_positional_embeddings, residual=video_base, gate=gate_a2v,
                     out_dtype=torch.float32)
             if run_v2a:
-                query = adaln(audio_base, a_scale_v2a, a_shift_v2a, self.norm_eps)
-                context = adaln(video_base, v_scale_v2a, v_shift_v2a, self.norm_eps)
+                cdt = compute_dtype(self.video_to_audio_attn)
+                query = adaln(audio_base, a_scale_v2a, a_shift_v2a, self.norm_eps, cdt)
+                context = adaln(video_base, v_scale_v2a, v_shift_v2a, self.norm_eps, cdt)
                 audio_value = self.video_to_audio_attn(
                     query, context=context, pe=audio.cross_positional_embeddings,
                     k_pe=video.cross_positional_embeddings, residual=audio_base, gate=gate_v2a,
                     out_dtype=torch.float32)
         if run_video:
-            normalized = adaln(video_value, video_ada[:, :, 4], video_ada[:, :, 3], self.norm_eps)
+            normalized = adaln(video_value, video_ada[:, :, 4], video_ada[:, :, 3], self.norm_eps,
+                               compute_dtype(self.attn1))
             video = replace(video, x=self.ff(normalized, residual=video_value, gate=video_ada[:, :, 5],
                                              out_dtype=video.x.dtype))
         if run_audio:
-            normalized = adaln(audio_value, audio_ada[:, :, 4], audio_ada[:, :, 3], self.norm_eps)
+            normalized = adaln(audio_value, audio_ada[:, :, 4], audio_ada[:, :, 3], self.norm_eps,
+                               compute_dtype(self.audio_attn1))
             audio = replace(audio, x=self.audio_ff(normalized, residual=audio_value, gate=audio_ada[:, :, 5],
                                                    out_dtype=audio.x.dtype))
         return video, audio
@@ -299,6 +326,7 @@ class BasicAVTransformerBlock:
 __all__ = [
     "BasicAVTransformerBlock",
     "TransformerArgs",
+    "compute_dtype",
     "TransformerConfig",
     "adaln",
     "gate",

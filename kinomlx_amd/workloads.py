@@ -94,32 +94,34 @@ def ltx_positions(grid: tuple[int, int, int]) -> torch.Tensor:
     return torch.stack([start, start + 1.0], dim=-1)[None]
 
 
-def _ltx_attention_params(p: dict, seed: int, prefix: str, dim: int, heads: int) -> None:
+def _ltx_attention_params(p: dict, seed: int, prefix: str, dim: int, heads: int,
+                          dtype: torch.dtype = torch.bfloat16) -> None:
     for name in ("to_q", "to_k", "to_v", "to_out"):
-        p[f"{prefix}.{name}.weight"] = bf16(normal(seed, f"{prefix}.{name}.weight", (dim, dim), 0.02))
-        p[f"{prefix}.{name}.bias"] = bf16(normal(seed, f"{prefix}.{name}.bias", (dim,), 0.02))
-    p[f"{prefix}.to_gate_logits.weight"] = bf16(normal(seed, f"{prefix}.to_gate_logits.weight", (heads, dim), 0.02))
-    p[f"{prefix}.to_gate_logits.bias"] = bf16(normal(seed, f"{prefix}.to_gate_logits.bias", (heads,), 0.02))
+        p[f"{prefix}.{name}.weight"] = normal(seed, f"{prefix}.{name}.weight", (dim, dim), 0.02).to(dtype)
+        p[f"{prefix}.{name}.bias"] = normal(seed, f"{prefix}.{name}.bias", (dim,), 0.02).to(dtype)
+    p[f"{prefix}.to_gate_logits.weight"] = normal(seed, f"{prefix}.to_gate_logits.weight", (heads, dim), 0.02).to(dtype)
+    p[f"{prefix}.to_gate_logits.bias"] = normal(seed, f"{prefix}.to_gate_logits.bias", (heads,), 0.02).to(dtype)
     for name in ("q_norm", "k_norm"):
-        p[f"{prefix}.{name}.weight"] = bf16(normal(seed, f"{prefix}.{name}.weight", (dim,), 0.02, 1.0))
+        p[f"{prefix}.{name}.weight"] = normal(seed, f"{prefix}.{name}.weight", (dim,), 0.02, 1.0).to(dtype)
 
 
-def ltx_params(spec: LTXSpec, seed: int = 0) -> dict[str, torch.Tensor]:
-    """Dense bf16 parameters of one LTX video block plus its per-step modulation rows."""
+def ltx_params(spec: LTXSpec, seed: int = 0, dtype: torch.dtype = torch.bfloat16) -> dict[str, torch.Tensor]:
+    """Dense parameters of one LTX video block (``dtype``: bf16, or fp16 for the reference's
+    default FP16 transformer) plus its per-step modulation rows (fp32 tables, ``dtype`` rows)."""
     d = spec.dim
     p: dict[str, torch.Tensor] = {}
-    _ltx_attention_params(p, seed, "attn1", d, spec.heads)
-    _ltx_attention_params(p, seed, "attn2", d, spec.heads)
+    _ltx_attention_params(p, seed, "attn1", d, spec.heads, dtype)
+    _ltx_attention_params(p, seed, "attn2", d, spec.heads, dtype)
     f = d * spec.ff_mult
-    p["ff.proj_in.weight"] = bf16(normal(seed, "ff.proj_in.weight", (f, d), 0.02))
-    p["ff.proj_in.bias"] = bf16(normal(seed, "ff.proj_in.bias", (f,), 0.02))
-    p["ff.proj_out.weight"] = bf16(normal(seed, "ff.proj_out.weight", (d, f), 0.02))
-    p["ff.proj_out.bias"] = bf16(normal(seed, "ff.proj_out.bias", (d,), 0.02))
+    p["ff.proj_in.weight"] = normal(seed, "ff.proj_in.weight", (f, d), 0.02).to(dtype)
+    p["ff.proj_in.bias"] = normal(seed, "ff.proj_in.bias", (f,), 0.02).to(dtype)
+    p["ff.proj_out.weight"] = normal(seed, "ff.proj_out.weight", (d, f), 0.02).to(dtype)
+    p["ff.proj_out.bias"] = normal(seed, "ff.proj_out.bias", (d,), 0.02).to(dtype)
     p["scale_shift_table"] = normal(seed, "scale_shift_table", (9, d), 0.02)
     p["prompt_scale_shift_table"] = normal(seed, "prompt_scale_shift_table", (2, d), 0.02)
     cond = normal(seed, "cond", (1, COND_DIM))
     w_mod = bf16(normal(seed, "adaln.linear.weight", (9 * d, COND_DIM), 0.02)).float()
-    p["timesteps"] = bf16((cond @ w_mod.T).reshape(1, 1, 9, d))
+    p["timesteps"] = (cond @ w_mod.T).reshape(1, 1, 9, d).to(dtype)
     return p
 
 
@@ -143,11 +145,11 @@ def quantize_ltx_params(p: dict[str, torch.Tensor], bits: int, group_size: int =
     return q
 
 
-def ltx_inputs(spec: LTXSpec, seed: int = 0) -> dict[str, torch.Tensor]:
-    """Hidden states ``(1, T, D)``, context ``(1, Tc, D)`` (bf16) and RoPE positions."""
+def ltx_inputs(spec: LTXSpec, seed: int = 0, dtype: torch.dtype = torch.bfloat16) -> dict[str, torch.Tensor]:
+    """Hidden states ``(1, T, D)``, context ``(1, Tc, D)`` (bf16, or ``dtype``) and RoPE positions."""
     return {
-        "x": bf16(normal(seed, "x", (1, spec.tokens, spec.dim))),
-        "context": bf16(normal(seed, "context", (1, spec.text_tokens, spec.dim))),
+        "x": normal(seed, "x", (1, spec.tokens, spec.dim)).to(dtype),
+        "context": normal(seed, "context", (1, spec.text_tokens, spec.dim)).to(dtype),
         "positions": ltx_positions(spec.grid),
     }
 

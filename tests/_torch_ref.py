@@ -17,7 +17,12 @@ def bf16_store(x, site="graph"):
     return x.to(torch.bfloat16).float()
 
 
-# This build's bf16 storage points (the same names as ``oracle.blocks.KX_SITES``).
+def fp16_store(x, site="graph"):
+    """Round an FP32 tensor to fp16 values (kept in FP32): the reference's FP16 graph."""
+    return x.to(torch.float16).float()
+
+
+# This build's 16-bit storage points (the same names as ``oracle.blocks.KX_SITES``).
 KX_SITES = frozenset({"norm", "proj", "gate", "qk", "attn_gated", "ctx", "act"})
 
 
@@ -25,15 +30,20 @@ def _kx_store(x, site="graph"):
     return x.to(torch.bfloat16).float() if site in KX_SITES else x
 
 
-def rounding(mode):
-    """``None``/``False``: FP32; ``True``/``"graph"``: the reference's bf16 graph; ``"kx"``: only
-    where the MI355X path stores bf16 (as ``oracle.blocks.rounding``)."""
+def _kx_store16(x, site="graph"):
+    return x.to(torch.float16).float() if site in KX_SITES else x
+
+
+def rounding(mode, half=torch.bfloat16):
+    """``None``/``False``: FP32; ``True``/``"graph"``: the reference's graph in ``half`` (bf16 or
+    fp16: every materialised array rounded to it); ``"kx"``: only where the MI355X path stores its
+    16-bit type (as ``oracle.blocks.rounding``)."""
     if not mode:
         return _keep
     if mode is True or mode == "graph":
-        return bf16_store
+        return fp16_store if half == torch.float16 else bf16_store
     if mode == "kx":
-        return _kx_store
+        return _kx_store16 if half == torch.float16 else _kx_store
     raise ValueError(f"unknown rounding mode {mode!r}")
 
 
@@ -88,10 +98,10 @@ def _ltx_attention(p, prefix, x, heads, context=None, pe=None, st=_keep):
     return st(_lin(p, f"{prefix}.to_out", o), "out_proj")
 
 
-def ltx_video_block(p, x, context, pe, heads, bf16_graph=False, rounding_mode=None):
+def ltx_video_block(p, x, context, pe, heads, bf16_graph=False, rounding_mode=None, half=torch.bfloat16):
     """``p``: fp32 tensors named as in ``oracle.ltx_video_block`` (dense weights);
-    ``bf16_graph`` / ``rounding_mode`` round at the same sites as the oracle's modes."""
-    st = rounding(rounding_mode or bf16_graph)
+    ``bf16_graph`` / ``rounding_mode`` round at the same sites as the oracle's modes, to ``half``."""
+    st = rounding(rounding_mode or bf16_graph, half)
     ada, prompt = p["ada"], p["prompt"]
     n = st(st(_rms(x), "norm_raw") * (1 + ada[1]) + ada[0], "norm")
     x = st(x + _ltx_attention(p, "attn1", n, heads, pe=pe, st=st) * ada[2], "resid")

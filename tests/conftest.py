@@ -61,6 +61,24 @@ def half_ulp_bf16(x) -> np.ndarray:
     return np.exp2(e - 8.0)
 
 
+def half_ulp_fp16(x) -> np.ndarray:
+    """Half the fp16 spacing at |x|: 2^(floor(log2 |x|) - 11) for normal values (11 significant
+    bits), 2^-25 below the smallest normal 2^-14."""
+    a = np.abs(np.asarray(x, dtype=np.float64))
+    e = np.floor(np.log2(np.maximum(a, 2.0 ** -14)))
+    return np.exp2(e - 11.0)
+
+
+def half_ulp(x, half: str = "bf16") -> np.ndarray:
+    """Half the spacing of the output's 16-bit type (``"bf16"`` or ``"fp16"``) at |x|."""
+    return half_ulp_fp16(x) if half == "fp16" else half_ulp_bf16(x)
+
+
+def half_round_fp16(x) -> np.ndarray:
+    """``x`` rounded to the nearest fp16 value (round half to even), as float32."""
+    return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
 def half_round_bf16(x) -> np.ndarray:
     """``x`` rounded to the nearest bf16 value (round half to even), as float32."""
     import torch
@@ -68,28 +86,28 @@ def half_round_bf16(x) -> np.ndarray:
     return torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).to(torch.bfloat16).float().numpy()
 
 
-def block_errors(got, ref) -> dict:
-    """Cosine, max abs error, and the max error beyond the output's own bf16 rounding (with |ref|
-    at that element)."""
+def block_errors(got, ref, half: str = "bf16") -> dict:
+    """Cosine, max abs error, and the max error beyond the output's own rounding to its 16-bit
+    type ``half`` (with |ref| at that element)."""
     g = np.asarray(got, dtype=np.float64)
     r = np.asarray(ref, dtype=np.float64)
     diff = np.abs(g - r)
-    excess = diff - half_ulp_bf16(r)
+    excess = diff - half_ulp(r, half)
     i = int(np.argmax(excess))
     return {"cosine": cosine(g, r), "max_abs": float(diff.max()), "excess": float(excess.flat[i]),
             "ref_at_excess": float(np.abs(r.flat[i])), "max_ref": float(np.abs(r).max()),
             "rel_l2": rel_l2(g, r), "rms": float(np.sqrt(np.mean(diff * diff)))}
 
 
-def assert_block_bar(got, ref, what: str = "", *, fp32_out: bool = False, context=None) -> dict:
+def assert_block_bar(got, ref, what: str = "", *, fp32_out: bool = False, context=None, half: str = "bf16") -> dict:
     """Assert the block bar and print the errors (``context``: the reference's own bf16-graph
-    output on the same inputs, printed for comparison only)."""
+    output on the same inputs, printed for comparison only; ``half``: the output's 16-bit type)."""
     assert np.all(np.isfinite(got)), what
-    e = block_errors(got, ref)
+    e = block_errors(got, ref, half)
     note = ""
     if context is not None:
-        c = block_errors(context, ref)
-        note = f" | reference bf16 graph: max_abs {c['max_abs']:.4g} excess {c['excess']:.4g}"
+        c = block_errors(context, ref, half)
+        note = f" | reference {half} graph: max_abs {c['max_abs']:.4g} excess {c['excess']:.4g}"
     print(f"{what}: cosine {e['cosine']:.7f} rel_l2 {e['rel_l2']:.3g} max_abs {e['max_abs']:.4g} "
           f"excess {e['excess']:.4g} (|ref| {e['ref_at_excess']:.3g} there, max|ref| {e['max_ref']:.3g}){note}")
     assert e["cosine"] >= BLOCK_COS_MIN, (what, e)
@@ -121,24 +139,26 @@ KX_NOISE_FACTOR = 1.25
 
 
 def assert_block_parity(got, ref, what: str, *, ref_kx=None, graph=None, fp32_out: bool = False,
-                        small: bool = True) -> None:
+                        small: bool = True, half: str = "bf16") -> None:
     """Block parity against the FP32 evaluation ``ref``: the fixed block bar where bf16 storage
     admits it (``small``: D <= 1024); otherwise the cosine, ``BLOCK_REL_L2``, the storage-point
     noise bound against ``ref_kx`` (the FP32 evaluation rounded where this build stores bf16), and,
     with ``graph`` (the reference's own bf16 execution on the same inputs), the elementwise anchor:
     the largest error beyond the bf16 output rounding is at most the graph's (an FP32 ``got`` gets
-    no rounding allowance: its max abs error is held to the graph's excess)."""
+    no rounding allowance: its max abs error is held to the graph's excess). ``half``: the 16-bit
+    type (``"bf16"`` or ``"fp16"``) of the output, of ``ref_kx``'s storage points and of the graph."""
     if small:
-        assert_block_bar(got, ref, what, fp32_out=fp32_out, context=graph)
+        assert_block_bar(got, ref, what, fp32_out=fp32_out, context=graph, half=half)
         return
-    e = block_errors(got, ref)
+    e = block_errors(got, ref, half)
     note = ""
     c = None
     if graph is not None:
-        c = block_errors(graph, ref)
-        note = f" | reference bf16 graph: rel_l2 {c['rel_l2']:.3g} max_abs {c['max_abs']:.4g} excess {c['excess']:.4g}"
+        c = block_errors(graph, ref, half)
+        note = f" | reference {half} graph: rel_l2 {c['rel_l2']:.3g} max_abs {c['max_abs']:.4g} excess {c['excess']:.4g}"
     # the FP32 evaluation at this build's bf16 points, its output rounded as ``got`` is
-    k = block_errors(ref_kx if fp32_out else half_round_bf16(ref_kx), ref)
+    rounded = half_round_fp16(ref_kx) if half == "fp16" else half_round_bf16(ref_kx)
+    k = block_errors(ref_kx if fp32_out else rounded, ref, half)
     print(f"{what}: cosine {e['cosine']:.7f} rel_l2 {e['rel_l2']:.3g} rms {e['rms']:.3g} (kx-point noise "
           f"{k['rms']:.3g}) max_abs {e['max_abs']:.4g} excess {e['excess']:.4g} (max|ref| {e['max_ref']:.3g}){note}")
     assert np.all(np.isfinite(got)), what
