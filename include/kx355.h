@@ -363,6 +363,28 @@ int kx_dequant_mxfp8_bf16(const uint32_t* wq, const void* scales, void* out, int
 int kx_quantize_mxfp8_bf16(const void* w, int64_t ldw, uint32_t* wq, void* scales, int64_t n, int64_t k,
                            int group_size, kx_stream_t stream);
 
+/* FP4 weight formats: E2M1 elements, eight per little-endian uint32 (element j at bits [4j, 4j+4)),
+ * with one scale byte per group along K: KX_FP4_MX = mxfp4 (OCP MX, E8M0 scale 2^(S - 127), group
+ * 32), KX_FP4_NV = nvfp4 (E4M3 scale, group 16). The reference routes feed-forward layers to them
+ * through video_ff_quantize_specs (kinomlx/models/ltx2/settings.py:39,107,281; defaults
+ * kinomlx/models/ltx2/weights/tensors.py:190-195; packed by mx.quantize(w, group_size, 4, mode),
+ * kinomlx/models/ltx2/preparation.py:152). */
+enum { KX_FP4_MX = 0, KX_FP4_NV = 1 };
+
+/* (n, k) bf16 <- FP4 words (n, k / 8) and scale bytes (n, k / group_size), exactly:
+ * w = e2m1(q) * scale (the product has at most 6 significant bits). The dequantize -> dense GEMM
+ * route of the fp4 QuantizedLinear. */
+int kx_dequant_fp4_bf16(const uint32_t* wq, const void* scales, void* out, int64_t n, int64_t k, int group_size,
+                        int scale_kind, kx_stream_t stream);
+
+/* FP4 quantize-on-load of a bf16 (n, k) weight with 16-byte aligned rows at ldw: per group,
+ * mxfp4: X = floor(log2(max |w|)) - 2 clamped to [-127, 127] (-127 for zeros), scale byte X + 127,
+ * codes E2M1(w * 2^-X); nvfp4: s = E4M3(max |w| / 6), codes E2M1(fp32(w / s)) (zeros when s is 0);
+ * E2M1 rounds to nearest even and saturates at +-6. This build's quantizer: MLX's own scale choice
+ * is not reproduced. */
+int kx_quantize_fp4_bf16(const void* w, int64_t ldw, uint32_t* wq, void* scales, int64_t n, int64_t k,
+                         int group_size, int scale_kind, kx_stream_t stream);
+
 /* Modulation values: out[b, t, r, c] = fp32(table[r, c]) + fp32(ts[b, t, r, c]) for a (rows, dim)
  * table (KX_F32, KX_BF16 or KX_F16) and an optional timestep modulation ts (null: the table alone) with
  * element strides ts_bs / ts_ts / ts_rs (dim contiguous); out is fp32 (batch, tokens, rows, dim)

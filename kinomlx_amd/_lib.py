@@ -29,6 +29,8 @@ KX_F16 = 2
 KX_NORM_RMS = 0
 KX_NORM_LAYER = 1
 KX_NORM_IN_F32 = 1 << 4
+KX_FP4_MX = 0
+KX_FP4_NV = 1
 KX_ROPE_NONE = 0
 KX_ROPE_SPLIT = 1
 KX_ROPE_PAIR = 2
@@ -101,6 +103,8 @@ SIGNATURES: dict[str, list] = {
         _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I, _P, _I64, _P, _I64, _I64, _P,
     ],
     "kx_dequant_mxfp8_bf16": [_P, _P, _P, _I64, _I64, _I, _I, _P],
+    "kx_dequant_fp4_bf16": [_P, _P, _P, _I64, _I64, _I, _I, _P],
+    "kx_quantize_fp4_bf16": [_P, _I64, _P, _P, _I64, _I64, _I, _I, _P],
     "kx_quantize_mxfp8_bf16": [_P, _I64, _P, _P, _I64, _I64, _I, _P],
     "kx_gelu_tanh_bf16": [_P, _P, _I64, _P],
     "kx_silu_bf16": [_P, _P, _I64, _P],
@@ -624,6 +628,29 @@ def launch_dequant_mxfp8(words, scales, out, *, n, k, group_size=32, transposed:
     if out.shape != (n, k) or out.dtype != torch.bfloat16 or not out.is_contiguous():
         raise ValueError("dequant_mxfp8: out must be a contiguous bf16 (n, k) tensor")
     _call("kx_dequant_mxfp8_bf16", _ptr(words), _ptr(scales), _ptr(out), n, k, group_size, int(transposed),
+          _stream())
+
+
+def launch_dequant_fp4(words, scales, out, *, n, k, group_size, scale_kind) -> None:
+    """The bf16 (n, k) weight of FP4 ``words`` (n, k / 8) / ``scales`` (n, k / group_size) uint8."""
+    _check_gpu("dequant_fp4", words, scales, out)
+    if words.shape != (n, k // 8) or scales.shape != (n, k // group_size) or scales.dtype != torch.uint8:
+        raise ValueError("dequant_fp4: words must be (n, k / 8) and scales (n, k / group_size) uint8")
+    if out.shape != (n, k) or out.dtype != torch.bfloat16 or not out.is_contiguous():
+        raise ValueError("dequant_fp4: out must be a contiguous bf16 (n, k) tensor")
+    _call("kx_dequant_fp4_bf16", _ptr(words.contiguous()), _ptr(scales.contiguous()), _ptr(out), n, k, group_size,
+          scale_kind, _stream())
+
+
+def launch_quantize_fp4(w, words, scales, *, group_size: int, scale_kind: int) -> None:
+    """FP4 (words, scales) <- bf16 weight w (n, k) with contiguous rows."""
+    _check_gpu("quantize_fp4", w, words, scales)
+    n, k = (int(v) for v in w.shape)
+    if w.dtype != torch.bfloat16 or w.stride(-1) != 1:
+        raise ValueError("quantize_fp4: the weight must be bfloat16 with contiguous rows")
+    if words.shape != (n, k // 8) or scales.shape != (n, k // group_size) or scales.dtype != torch.uint8:
+        raise ValueError("quantize_fp4: output shapes do not match the weight")
+    _call("kx_quantize_fp4_bf16", _ptr(w), w.stride(0), _ptr(words), _ptr(scales), n, k, group_size, scale_kind,
           _stream())
 
 

@@ -376,6 +376,38 @@ __global__ __launch_bounds__(256) void dequant_mx8_kernel(const uint32_t* __rest
       dequant8<QMX8>(tmp, e8m0_f32(scales[r * (k / 32) + c / 4]), 0.0f);
 }
 
+// mxfp4 / nvfp4: (n, k / 8) words of eight E2M1 codes and (n, k / G) scale bytes (G = 32: E8M0,
+// G = 16: E4M3) -> (n, k) bf16, eight values (one word) per thread. Every value is exact: an E2M1
+// magnitude has at most 2 significant bits and the scale at most 4.
+__device__ __forceinline__ float e2m1_f32(uint32_t c) {
+  const uint32_t m3 = c & 7u;
+  // 0, 0.5, then 1, 1.5, 2, 3, 4, 6: from code 2 on, the fp32 bits step by 2^22 from 1.0
+  const float mag = m3 < 2u ? 0.5f * (float)m3 : __uint_as_float(0x3F800000u + ((m3 - 2u) << 22));
+  return __uint_as_float(__float_as_uint(mag) | ((c & 8u) << 28));
+}
+__device__ __forceinline__ float e4m3_f32(uint32_t b) {
+  const uint32_t e = (b >> 3) & 15u, m = b & 7u;
+  const float mag = e == 0 ? (float)m * 0.001953125f : ldexpf(1.0f + (float)m * 0.125f, (int)e - 7);
+  return (b & 0x80u) ? -mag : mag;
+}
+template <bool NV>
+__global__ __launch_bounds__(256) void dequant_fp4_kernel(const uint32_t* __restrict__ words,
+                                                          const uint8_t* __restrict__ scales,
+                                                          uint16_t* __restrict__ out, int64_t n, int64_t k) {
+  constexpr int G = NV ? 16 : 32;
+  const int64_t words_per_row = k / 8;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= n * words_per_row) return;
+  const int64_t r = idx / words_per_row, c = idx - r * words_per_row;
+  const uint32_t w = words[idx];
+  const uint32_t sb = scales[r * (k / G) + (8 * c) / G];
+  const float sc = NV ? e4m3_f32(sb) : e8m0_f32(sb);
+  float v[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = e2m1_f32((w >> (4 * j)) & 15u) * sc;
+  *reinterpret_cast<uint4*>(out + r * k + 8 * c) = pack8(v);
+}
+
 // mxfp8 in the pretransposed layout (quantized from weight.T: (k, n / 4) words and (k, n / 32)
 // scale bytes, groups along n) -> the (n, k) bf16 weight, through 64 x 64 LDS tiles: a thread
 // dequantizes 16 consecutive n of one k row and writes them transposed into the tile, then
@@ -1790,6 +1822,27 @@ extern "C" int kx_dequant_mxfp8_bf16(const uint32_t* wq, const void* scales, voi
     dequant_mx8_kernel<<<(unsigned)((total + 255) / 256), 256, 0, s>>>(wq, (const uint8_t*)scales, (uint16_t*)out,
                                                                        n, k);
   }
+  return check_launch(what);
+}
+
+extern "C" int kx_dequant_fp4_bf16(const uint32_t* wq, const void* scales, void* out, int64_t n, int64_t k,
+                                   int group_size, int scale_kind, kx_stream_t stream) {
+  const char* what = "kx_dequant_fp4_bf16";
+  KX_REQUIRE(wq && scales && out, "%s: null tensor", what);
+  KX_REQUIRE(scale_kind == KX_FP4_MX || scale_kind == KX_FP4_NV, "%s: bad scale kind %d", what, scale_kind);
+  const int gs = scale_kind == KX_FP4_NV ? 16 : 32;
+  KX_REQUIRE(group_size == gs, "%s: group_size must be %d for this scale kind, got %d", what, gs, group_size);
+  KX_REQUIRE(n >= 0 && k > 0 && k % gs == 0, "%s: k must be a multiple of the group size (n=%lld k=%lld)", what,
+             (long long)n, (long long)k);
+  KX_REQUIRE(aligned16(out), "%s: out must be 16-byte aligned", what);
+  const int64_t total = n * (k / 8);
+  KX_REQUIRE(total / 256 < (1ll << 31), "%s: too many elements", what);
+  if (total == 0) return KX_OK;
+  const unsigned grid = (unsigned)((total + 255) / 256);
+  if (scale_kind == KX_FP4_NV)
+    dequant_fp4_kernel<true><<<grid, 256, 0, (hipStream_t)stream>>>(wq, (const uint8_t*)scales, (uint16_t*)out, n, k);
+  else
+    dequant_fp4_kernel<false><<<grid, 256, 0, (hipStream_t)stream>>>(wq, (const uint8_t*)scales, (uint16_t*)out, n, k);
   return check_launch(what);
 }
 

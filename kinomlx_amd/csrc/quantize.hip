@@ -137,6 +137,85 @@ __global__ __launch_bounds__(256) void quantize_mx8_kernel(const uint16_t* __res
   if (sub == 0) scales[g] = (uint8_t)(x + 127);
 }
 
+// ---- mxfp4 / nvfp4 (FP4 E2M1 elements) ---------------------------------------------------------
+//
+// E2M1 (OCP MX v1.0): sign in bit 3, exponent bits 2-1 (bias 1), mantissa bit 0: magnitudes 0, 0.5,
+// 1, 1.5, 2, 3, 4, 6; eight codes per little-endian uint32 (element j at bits [4j, 4j + 4)).
+// mxfp4: one E8M0 scale per 32 along K, X = floor(log2(max |w|)) - 2 (2: the exponent of E2M1's
+// largest normal, 6 = 1.5 * 2^2), clamped to [-127, 127] (-127 for an all-zero group); element =
+// E2M1 of w * 2^-X (an exact scaling). nvfp4: one E4M3 scale per 16, s = E4M3(max |w| / 6) (IEEE
+// fp32 division, round to nearest even, saturating at 448); element = E2M1 of fp32(w / s); a
+// group whose s is zero stores zero codes. E2M1 rounds to nearest even and saturates at +-6.
+
+// |v| -> E2M1 code (sign from v's sign bit): the round-to-nearest-even decision boundaries of the
+// grid 0, 0.5, 1, 1.5, 2, 3, 4, 6 (a tie goes to the even mantissa: 0.25 -> 0, 0.75 -> 1, 1.25 -> 1,
+// 1.75 -> 2, 2.5 -> 2, 3.5 -> 4, 5 -> 4); NaN gives zero.
+__device__ __forceinline__ uint32_t e2m1_rne(float v) {
+  if (v != v) return 0u;
+  const uint32_t sign = (__float_as_uint(v) >> 28) & 8u;
+  const float a = fabsf(v);
+  uint32_t code;
+  if (a <= 0.25f) code = 0;
+  else if (a < 0.75f) code = 1;
+  else if (a <= 1.25f) code = 2;
+  else if (a < 1.75f) code = 3;
+  else if (a <= 2.5f) code = 4;
+  else if (a < 3.5f) code = 5;
+  else if (a <= 5.0f) code = 6;
+  else code = 7;
+  return sign | code;
+}
+
+// An E4M3 byte (OCP, no infinities) as fp32, exactly.
+__device__ __forceinline__ float e4m3_value(uint32_t b) {
+  const uint32_t e = (b >> 3) & 15u, m = b & 7u;
+  const float mag = e == 0 ? (float)m * 0.001953125f : ldexpf(1.0f + (float)m * 0.125f, (int)e - 7);
+  return (b & 0x80u) ? -mag : mag;
+}
+
+// G / 8 lanes per group (mxfp4: G = 32, nvfp4: G = 16): lane `sub` holds values 8 sub .. 8 sub + 7
+// (one 16-byte load) and writes their packed word; the group maximum is reduced over the lanes.
+template <bool NV>
+__global__ __launch_bounds__(256) void quantize_fp4_kernel(const uint16_t* __restrict__ w, int64_t ldw,
+                                                           uint32_t* __restrict__ words, uint8_t* __restrict__ scales,
+                                                           int64_t groups, int64_t groups_per_row) {
+  constexpr int G = NV ? 16 : 32, LPG = G / 8;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t g = t / LPG;
+  const int sub = (int)(t % LPG);
+  // whole groups of lanes are in or out of range together, so the shuffles stay in a group
+  if (g >= groups) return;
+  const int64_t row = g / groups_per_row, col = g - row * groups_per_row;
+  float v[8];
+  unpack8(*reinterpret_cast<const uint4*>(w + row * ldw + col * G + sub * 8), v);
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+#pragma unroll
+  for (int o = 1; o < LPG; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, LPG));
+  uint32_t word = 0, sbyte;
+  if constexpr (NV) {
+    sbyte = e4m3_rne(amax / 6.0f) & 0x7Fu;
+    const float sc = e4m3_value(sbyte);
+    if (sc > 0.0f) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) word |= e2m1_rne(v[i] / sc) << (4 * i);
+    }
+  } else {
+    int x = -127;
+    if (amax > 0.0f) {
+      int e;
+      frexpf(amax, &e);
+      x = min(max(e - 1 - 2, -127), 127);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) word |= e2m1_rne(ldexpf(v[i], -x)) << (4 * i);
+    sbyte = (uint32_t)(x + 127);
+  }
+  words[g * LPG + sub] = word;
+  if (sub == 0) scales[g] = (uint8_t)sbyte;
+}
+
 }  // namespace
 }  // namespace kx
 
@@ -180,4 +259,27 @@ extern "C" int kx_quantize_affine_bf16(const void* w, int64_t ldw, uint32_t* wq,
     quantize_affine_kernel<8><<<grid, 256, 0, s>>>((const uint16_t*)w, ldw, wq, (uint16_t*)scales,
                                                    (uint16_t*)biases, groups, k / QGROUP);
   return check_launch("kx_quantize_affine_bf16");
+}
+
+extern "C" int kx_quantize_fp4_bf16(const void* w, int64_t ldw, uint32_t* wq, void* scales, int64_t n, int64_t k,
+                                    int group_size, int scale_kind, kx_stream_t stream) {
+  const char* what = "kx_quantize_fp4_bf16";
+  KX_REQUIRE(w && wq && scales, "%s: null tensor", what);
+  KX_REQUIRE(scale_kind == KX_FP4_MX || scale_kind == KX_FP4_NV, "%s: bad scale kind %d", what, scale_kind);
+  const int gs = scale_kind == KX_FP4_NV ? 16 : 32;
+  KX_REQUIRE(group_size == gs, "%s: group_size must be %d for this scale kind, got %d", what, gs, group_size);
+  KX_REQUIRE(n >= 0 && k > 0 && k % gs == 0 && ldw >= k && ldw % 8 == 0 && aligned16(w),
+             "%s: bad shape (n=%lld k=%lld ldw=%lld; k %% %d == 0, 16-byte rows)", what, (long long)n, (long long)k,
+             (long long)ldw, gs);
+  KX_REQUIRE(aligned8(wq), "%s: wq must be 8-byte aligned", what);
+  const int64_t groups = n * (k / gs);
+  KX_REQUIRE(groups * (gs / 8) / 256 < (1ll << 31), "%s: too many groups", what);
+  if (groups == 0) return KX_OK;
+  const unsigned grid = (unsigned)((groups * (gs / 8) + 255) / 256);
+  hipStream_t s = (hipStream_t)stream;
+  if (scale_kind == KX_FP4_NV)
+    quantize_fp4_kernel<true><<<grid, 256, 0, s>>>((const uint16_t*)w, ldw, wq, (uint8_t*)scales, groups, k / gs);
+  else
+    quantize_fp4_kernel<false><<<grid, 256, 0, s>>>((const uint16_t*)w, ldw, wq, (uint8_t*)scales, groups, k / gs);
+  return check_launch(what);
 }

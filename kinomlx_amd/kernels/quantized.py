@@ -33,8 +33,14 @@ once, exactly, to the bf16 ``(out, in)`` weight and runs the dense GEMM. ``quant
 the OCP MX conversion (shared exponent ``floor(log2(max |w|)) - 8``, elements rounded to nearest
 even and saturated at 448); MLX's own exponent choice is not reproduced.
 
-``quant_defaults`` knows the reference's four modes; mxfp4 and nvfp4 layers raise
-``NotImplementedError`` on MI355X.
+mxfp4 / nvfp4 (the reference's feed-forward modes, ``video_ff_quantize_specs``,
+``kinomlx/models/ltx2/settings.py:39``): ``weight`` uint32 words ``(out, in / 8)`` of eight FP4 E2M1
+codes (element ``j`` at bits ``[4j, 4j + 4)``), ``scales`` uint8 ``(out, in / 32)`` E8M0 exponents
+(mxfp4) or ``(out, in / 16)`` E4M3 values (nvfp4), no biases; ``w = e2m1(q) * scale``, exact in bf16.
+Each GPU call dequantizes (``kx_dequant_fp4_bf16``) and runs the dense GEMM. ``quantize_fp4`` is this
+build's conversion (mxfp4: OCP MX shared exponent ``floor(log2(max |w|)) - 2``; nvfp4: E4M3 scale of
+``max |w| / 6``; E2M1 round to nearest even, saturated at 6); MLX's own scale choice is not
+reproduced.
 """
 
 from __future__ import annotations
@@ -48,7 +54,10 @@ DEFAULT_GROUP_SIZE = 64
 DEFAULT_BITS = 4
 # (group_size, bits) per mode (``weights/tensors.py:185-203``)
 _DEFAULTS = {"affine": (64, 4), "mxfp4": (32, 4), "mxfp8": (32, 8), "nvfp4": (16, 4)}
-KERNEL_MODES = ("affine", "mxfp8")
+KERNEL_MODES = ("affine", "mxfp8", "mxfp4", "nvfp4")
+# modes whose scales are uint8 exponent / E4M3 bytes and that carry no biases
+SCALED_MODES = ("mxfp8", "mxfp4", "nvfp4")
+FP4_MODES = ("mxfp4", "nvfp4")
 
 
 def quant_defaults(mode: str, group_size: int | None, bits: int | None) -> tuple[int, int]:
@@ -67,10 +76,11 @@ def _check_mode(mode: str, group_size: int, bits: int) -> None:
     """A mode, group size and width this build has kernels for."""
     quant_defaults(mode, group_size, bits)
     if mode not in KERNEL_MODES:
-        raise NotImplementedError(f"{mode} quantized linears have no MI355X kernel (affine and mxfp8 do)")
-    if mode == "mxfp8":
-        if (group_size, bits) != (32, 8):
-            raise ValueError(f"mxfp8 takes group size 32 and 8 bits, got {group_size} and {bits}")
+        raise NotImplementedError(f"{mode} quantized linears have no MI355X kernel")
+    if mode in SCALED_MODES:
+        if (group_size, bits) != _DEFAULTS[mode]:
+            want = _DEFAULTS[mode]
+            raise ValueError(f"{mode} takes group size {want[0]} and {want[1]} bits, got {group_size} and {bits}")
     else:
         _check_format(group_size, bits)
 
@@ -193,6 +203,63 @@ def dequantize_mxfp8(words: torch.Tensor, scales: torch.Tensor, *, transposed: b
     return out
 
 
+def _e2m1_codes(x: torch.Tensor) -> torch.Tensor:
+    """float32 -> E2M1 codes (int64): the round-to-nearest-even decision boundaries of the grid
+    0, 0.5, 1, 1.5, 2, 3, 4, 6 (ties to the even mantissa), saturated at 6, sign in bit 3; NaN -> 0."""
+    a = torch.nan_to_num(x.abs(), nan=0.0)
+    code = ((a > 0.25).long() + (a >= 0.75).long() + (a > 1.25).long() + (a >= 1.75).long() + (a > 2.5).long()
+            + (a >= 3.5).long() + (a > 5.0).long())
+    return code | ((torch.signbit(x) & ~torch.isnan(x)).long() << 3)
+
+
+def quantize_fp4(weight: torch.Tensor, mode: str = "mxfp4") -> tuple[torch.Tensor, torch.Tensor]:
+    """``(out, in)`` weight -> FP4 ``(words (out, in / 8) int32, scales (out, in / G) uint8)``:
+    ``mode`` ``"mxfp4"`` (G = 32, E8M0 scales) or ``"nvfp4"`` (G = 16, E4M3 scales). On the GPU:
+    the quantize-on-load kernel (``kx_quantize_fp4_bf16``) on the bf16 weight; a host weight is
+    converted by the same arithmetic in torch (bit-identical on bf16 weights, tested)."""
+    if mode not in FP4_MODES:
+        raise ValueError(f"quantize_fp4 takes mode mxfp4 or nvfp4, got {mode}")
+    group = _DEFAULTS[mode][0]
+    n, k = (int(v) for v in weight.shape)
+    if k % group:
+        raise ValueError(f"{mode} groups the last axis by {group}: cannot quantize a {n} x {k} matrix")
+    kind = _lib.KX_FP4_NV if mode == "nvfp4" else _lib.KX_FP4_MX
+    if weight.is_cuda:
+        w = weight.to(torch.bfloat16)
+        if w.stride(-1) != 1 or w.stride(0) % 8 or w.data_ptr() % 16:
+            w = w.contiguous()
+        words = torch.empty((n, k // 8), dtype=torch.int32, device=w.device)
+        scales = torch.empty((n, k // group), dtype=torch.uint8, device=w.device)
+        if n:
+            _lib.launch_quantize_fp4(w, words, scales, group_size=group, scale_kind=kind)
+        return words, scales
+    w = weight.to(torch.bfloat16).float().reshape(n, k // group, group)
+    amax = w.abs().amax(dim=-1)
+    if mode == "nvfp4":
+        sc = (amax / 6.0).clamp(max=448.0).to(torch.float8_e4m3fn)
+        sbytes = sc.view(torch.uint8) & 0x7F
+        s = sc.float().abs()
+        codes = torch.where(s[..., None] > 0, _e2m1_codes(w / s[..., None]), torch.zeros_like(w, dtype=torch.int64))
+    else:
+        _, e = torch.frexp(amax)
+        x = torch.where(amax > 0, (e.to(torch.int64) - 3).clamp(-127, 127), torch.full_like(e, -127, dtype=torch.int64))
+        codes = _e2m1_codes(torch.ldexp(w, (-x)[..., None].to(torch.float32)))
+        sbytes = (x + 127).to(torch.uint8)
+    return pack(codes.reshape(n, k), 4), sbytes.contiguous()
+
+
+def dequantize_fp4(words: torch.Tensor, scales: torch.Tensor, mode: str = "mxfp4") -> torch.Tensor:
+    """FP4 weight -> bf16 ``(out, in)``, exactly (``kx_dequant_fp4_bf16``)."""
+    if mode not in FP4_MODES:
+        raise ValueError(f"dequantize_fp4 takes mode mxfp4 or nvfp4, got {mode}")
+    group = _DEFAULTS[mode][0]
+    n, k = int(words.shape[0]), int(words.shape[1]) * 8
+    out = torch.empty((n, k), dtype=torch.bfloat16, device=words.device)
+    _lib.launch_dequant_fp4(words.contiguous(), scales.contiguous(), out, n=n, k=k, group_size=group,
+                            scale_kind=_lib.KX_FP4_NV if mode == "nvfp4" else _lib.KX_FP4_MX)
+    return out
+
+
 def tile_weights(words: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, *,
                  bits: int = DEFAULT_BITS, group_size: int = DEFAULT_GROUP_SIZE) -> tuple[torch.Tensor, torch.Tensor]:
     """Packed affine weights -> the kernel's tiled layout ``(wt, sbt)`` (uint8 tensors)."""
@@ -258,6 +325,15 @@ def quantized_matmul(
     ``mode="mxfp8"`` takes ``biases=None``; with ``transpose=False`` (mxfp8 only: the packing of
     ``weight.T``) the weight is dequantized for the call and multiplied by the dense GEMM."""
     _check_mode(mode, group_size, bits)
+    if mode in FP4_MODES:
+        # no in-mainloop FP4 product: the exact dequantization, then the dense GEMM
+        from .mpp_linear import fused_linear
+
+        if biases is not None or not transpose:
+            raise ValueError(f"{mode} weights carry no biases and take the (out, in) packing")
+        dense = dequantize_fp4(weight, scales, mode)
+        return fused_linear(value, dense, None if bias is None else bias.to(torch.bfloat16), activation=activation,
+                            residual=residual, gate=gate, out=out, out_dtype=out_dtype)
     if mode == "mxfp8":
         if biases is not None:
             raise ValueError("mxfp8 weights carry no biases")
@@ -302,11 +378,12 @@ class QuantizedLinear:
                  bits: int | None = None, mode: str = "affine") -> None:
         group_size, bits = quant_defaults(mode, group_size, bits)
         _check_mode(mode, group_size, bits)
-        if (biases is None) != (mode == "mxfp8"):
-            raise ValueError("affine weights carry biases and mxfp8 weights none")
-        # the kernels reinterpret the scale bits: bf16 scale / bias pairs (affine), E8M0 bytes (mxfp8)
-        if mode == "mxfp8" and scales.dtype != torch.uint8:
-            raise ValueError(f"mxfp8 scales must be uint8 E8M0 exponents, got {scales.dtype}")
+        if (biases is None) != (mode in SCALED_MODES):
+            raise ValueError("affine weights carry biases and mxfp8 / mxfp4 / nvfp4 weights none")
+        # the kernels reinterpret the scale bits: bf16 scale / bias pairs (affine), scale bytes
+        # (mxfp8 / mxfp4: E8M0, nvfp4: E4M3)
+        if mode in SCALED_MODES and scales.dtype != torch.uint8:
+            raise ValueError(f"{mode} scales must be uint8 bytes, got {scales.dtype}")
         if mode == "affine" and (scales.dtype != torch.bfloat16 or biases.dtype != torch.bfloat16):
             raise ValueError(f"affine scales and biases must be bfloat16, got {scales.dtype} and {biases.dtype}")
         self.weight = weight
@@ -327,6 +404,8 @@ class QuantizedLinear:
         """The bf16 ``(out, in)`` weight, exactly (a new buffer)."""
         if self.mode == "mxfp8":
             return dequantize_mxfp8(self.weight, self.scales)
+        if self.mode in FP4_MODES:
+            return dequantize_fp4(self.weight, self.scales, self.mode)
         return dequantize(self.weight, self.scales, self.biases, group_size=self.group_size, bits=self.bits)
 
     @classmethod
@@ -337,6 +416,10 @@ class QuantizedLinear:
         if mode == "mxfp8":
             _check_mode(mode, group_size, bits)
             words, scales = quantize_mxfp8(weight, group_size)
+            return cls(words, scales, None, bias, group_size=group_size, bits=bits, mode=mode)
+        if mode in FP4_MODES:
+            _check_mode(mode, group_size, bits)
+            words, scales = quantize_fp4(weight, mode)
             return cls(words, scales, None, bias, group_size=group_size, bits=bits, mode=mode)
         words, scales, biases = quantize(weight, group_size, bits)
         return cls(words, scales, biases, bias, group_size=group_size, bits=bits)
@@ -417,14 +500,17 @@ class PretransposedQuantizedLinear:
 
 
 __all__ = [
+    "FP4_MODES",
     "KERNEL_MODES",
     "PretransposedQuantizedLinear",
     "QuantizedLinear",
     "dequantize",
+    "dequantize_fp4",
     "dequantize_mxfp8",
     "pack",
     "quant_defaults",
     "quantize",
+    "quantize_fp4",
     "quantize_mxfp8",
     "quantized_matmul",
     "tile_weights",

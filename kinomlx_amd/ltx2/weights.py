@@ -9,7 +9,8 @@ binding of prepared checkpoints (``kinomlx/models/ltx2/weights/loading.py:82-110
 ``__quant__.`` are packed linears whose mode comes from the settings, ``quantization.py:199-274``;
 keys under ``__layout__.`` are ``weight_t``, the transposed dense weight). The tensors move from the
 file to HBM through ``kinomlx_amd.io.load_to_device``; on-load quantization runs the
-``kx_quantize_affine_bf16`` / ``kx_quantize_mxfp8_bf16`` kernels on the resident bf16 weight.
+``kx_quantize_affine_bf16`` / ``kx_quantize_mxfp8_bf16`` / ``kx_quantize_fp4_bf16`` (mxfp4 and nvfp4
+feed-forward layers, ``video_ff_quantize_specs``) kernels on the resident bf16 weight.
 """
 
 from __future__ import annotations

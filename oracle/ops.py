@@ -50,6 +50,15 @@ __all__ = [
     "swiglu",
     "to_bf16",
     "unpack_affine",
+    "E2M1_MAX",
+    "dequantize_fp4",
+    "e2m1_decode",
+    "e2m1_encode",
+    "fp4_linear",
+    "pack_nibbles",
+    "quantize_mxfp4",
+    "quantize_nvfp4",
+    "unpack_nibbles",
 ]
 
 
@@ -536,6 +545,107 @@ def dequantize_mxfp8(words, scales, *, group_size: int = 32) -> np.ndarray:
     vals = e4m3_decode(codes).astype(np.float64)
     s = np.repeat(e8m0_scale(scales).astype(np.float64), group_size, axis=1)[:, : codes.shape[1]]
     return to_bf16((vals * s).astype(F32))
+
+
+# ---------------------------------------------------------------------------------------------
+# FP4 weights: mxfp4 (OCP MX v1.0) and nvfp4, the modes the reference routes feed-forward layers to
+# (``kinomlx/models/ltx2/settings.py:39``, defaults ``kinomlx/models/ltx2/weights/tensors.py:190-195``:
+# mxfp4 (32, 4), nvfp4 (16, 4); packed by ``mx.quantize(w, group_size, 4, mode)``,
+# ``kinomlx/models/ltx2/preparation.py:152``). The arithmetic lives in MLX (not vendored): the
+# formats are the published ones. E2M1 elements: sign bit 3, exponent bits 2-1 (bias 1), mantissa
+# bit 0 -> magnitudes 0, 0.5, 1, 1.5, 2, 3, 4, 6; eight per little-endian uint32 (element j at bits
+# [4j, 4j + 4)). mxfp4 scales are E8M0 bytes (2^(S - 127)) per 32; nvfp4 scales are E4M3 bytes per 16.
+
+E2M1_MAX = 6.0
+_E2M1_GRID = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0])
+
+
+def e2m1_decode(codes) -> np.ndarray:
+    """FP4 E2M1 codes (0..15) -> float32, from the field definition (exponent e, mantissa m:
+    subnormal ``m / 2`` for e = 0, else ``(1 + m / 2) * 2^(e - 1)``)."""
+    c = np.asarray(codes, dtype=np.uint32)
+    e = ((c >> 1) & 3).astype(np.float64)
+    m = (c & 1).astype(np.float64)
+    mag = np.where(e == 0, m * 0.5, (1.0 + m * 0.5) * np.exp2(e - 1.0))
+    return np.where((c >> 3) & 1, -mag, mag).astype(F32)
+
+
+def e2m1_encode(value) -> np.ndarray:
+    """float -> E2M1 codes: round to nearest even on the E2M1 grid (the quantum is 0.5 below 2, 1 in
+    [2, 4) and 2 from 4 on; a tie keeps the even mantissa), saturating at +-6; the sign survives
+    (negative zero is code 8); NaN gives 0."""
+    v = np.asarray(value, dtype=np.float64)
+    a = np.nan_to_num(np.abs(v), nan=0.0, posinf=E2M1_MAX)
+    e = np.clip(np.floor(np.log2(np.maximum(a, 2.0 ** -30))), 0.0, 2.0)
+    quantum = np.exp2(e - 1.0)
+    q = np.minimum(np.rint(a / quantum) * quantum, E2M1_MAX)
+    code = np.searchsorted(_E2M1_GRID, q).astype(np.uint32)
+    sign = np.where(np.signbit(v) & ~np.isnan(v), 8, 0).astype(np.uint32)
+    return (code | sign).astype(np.uint8)
+
+
+def pack_nibbles(codes: np.ndarray) -> np.ndarray:
+    """``(R, C)`` 4-bit codes -> ``(R, C / 8)`` little-endian uint32 words."""
+    return pack_affine(np.asarray(codes, dtype=np.int64), 4)
+
+
+def unpack_nibbles(words: np.ndarray) -> np.ndarray:
+    """``(R, W)`` uint32 words -> ``(R, 8 W)`` 4-bit codes."""
+    return unpack_affine(words, 4)
+
+
+def quantize_mxfp4(weight, group_size: int = 32):
+    """``(R, C)`` -> ``(words (R, C/8) uint32, scales (R, C/32) uint8)`` by the OCP MX conversion:
+    shared exponent ``floor(log2(amax)) - 2`` (2: the exponent of E2M1's largest normal, 6 = 1.5 *
+    2^2), clamped to the E8M0 range (-127 for an all-zero group), elements E2M1 of ``w * 2^-X``. This
+    build's quantizer (MLX's own scale choice: parity unpinned)."""
+    w = np.asarray(weight, dtype=np.float64)
+    r, c = w.shape
+    if c % group_size:
+        raise ValueError("mxfp4 quantization needs the last axis a multiple of the group size")
+    g = w.reshape(r, c // group_size, group_size)
+    amax = np.abs(g).max(axis=-1)
+    exp = np.clip(np.floor(np.log2(np.maximum(amax, 2.0 ** -200))) - 2.0, -127.0, 127.0)
+    exp = np.where(amax == 0, -127.0, exp)
+    codes = e2m1_encode(g / np.exp2(exp)[..., None]).reshape(r, c)
+    return pack_nibbles(codes), (exp + 127.0).astype(np.uint8)
+
+
+def quantize_nvfp4(weight, group_size: int = 16):
+    """``(R, C)`` -> ``(words (R, C/8) uint32, scales (R, C/16) uint8)``: per group the E4M3 scale
+    ``s = E4M3(fp32(amax / 6))`` (RNE, saturating at 448) and elements E2M1 of ``fp32(w / s)`` (IEEE
+    fp32 division; zero codes when s is 0). This build's quantizer (NVIDIA's two-level form with a
+    per-tensor scale, and MLX's own choice: parity unpinned)."""
+    w = np.asarray(weight, dtype=F32)
+    r, c = w.shape
+    if c % group_size:
+        raise ValueError("nvfp4 quantization needs the last axis a multiple of the group size")
+    g = w.reshape(r, c // group_size, group_size)
+    amax = np.abs(g).max(axis=-1).astype(F32)
+    sbytes = e4m3_encode((amax / F32(6.0)).astype(F32)) & 0x7F
+    s = e4m3_decode(sbytes)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        scaled = (g / s[..., None]).astype(F32)
+    codes = np.where(s[..., None] > 0, e2m1_encode(scaled), 0).reshape(r, c)
+    return pack_nibbles(codes), sbytes.astype(np.uint8)
+
+
+def dequantize_fp4(words, scales, *, mode: str) -> np.ndarray:
+    """Bit-exact dequantisation along the last axis: ``bf16(e2m1(q) * scale)`` -> float32 ``(R, 8 W)``
+    (``mode`` ``"mxfp4"``: E8M0 scales per 32; ``"nvfp4"``: E4M3 scales per 16). The product has at
+    most 6 significant bits, so the bf16 rounding is the identity in the normal range."""
+    codes = unpack_nibbles(words)
+    vals = e2m1_decode(codes).astype(np.float64)
+    group = 16 if mode == "nvfp4" else 32
+    sv = e4m3_decode(scales) if mode == "nvfp4" else e8m0_scale(scales)
+    s = np.repeat(sv.astype(np.float64), group, axis=1)[:, : codes.shape[1]]
+    return to_bf16((vals * s).astype(F32))
+
+
+def fp4_linear(value, words, scales, bias=None, *, mode: str):
+    """``quantized_matmul(x, w, scales, transpose=True, group_size, bits=4, mode) + bias`` for an
+    mxfp4 / nvfp4 ``(out, in / 8)`` packed weight."""
+    return linear(value, dequantize_fp4(words, scales, mode=mode), bias)
 
 
 def mxfp8_linear(value, words, scales, bias=None, *, group_size: int = 32, transposed: bool = True):

@@ -84,10 +84,12 @@ def test_quant_defaults_follow_the_reference():
         quantized.quant_defaults("affine", 64, 0)
     with pytest.raises(ValueError, match="Unsupported FF quantization mode"):
         quantized.quant_defaults("int3", None, None)
-    # modes without an MI355X kernel are refused by the layer, not by the defaults
-    with pytest.raises(NotImplementedError, match="nvfp4"):
+    # the FP4 modes take their own group size and width only
+    quantized.QuantizedLinear(torch.zeros((32, 8), dtype=torch.int32), torch.zeros((32, 4), dtype=torch.uint8),
+                              None, mode="nvfp4")
+    with pytest.raises(ValueError, match="nvfp4 takes group size 16 and 4 bits"):
         quantized.QuantizedLinear(torch.zeros((32, 8), dtype=torch.int32), torch.zeros((32, 2), dtype=torch.uint8),
-                                  None, mode="nvfp4")
+                                  None, group_size=32, mode="nvfp4")
 
 
 def test_quant_routing_covers_whole_block_and_targeted_ff_modes():
@@ -181,3 +183,21 @@ def test_quantized_layers_refuse_scales_the_kernels_would_misread():
             quantized.QuantizedLinear(words, scales, biases, group_size=64, bits=4)
     with pytest.raises(ValueError, match="uint8"):
         quantized.QuantizedLinear(words, torch.zeros((32, 1), dtype=torch.bfloat16), None, mode="mxfp8")
+
+
+@pytest.mark.parametrize("mode", ["mxfp4", "nvfp4"])
+def test_host_fp4_quantizer_is_bit_identical_to_the_oracle(mode):
+    """The torch host packing of ``quantize_fp4`` (used for weights still in host memory) against
+    the oracle's quantizer, on bf16 weights over a range of magnitudes with zero and constant groups."""
+    import oracle
+
+    r = np.random.default_rng(9)
+    w = (r.standard_normal((48, 256)) * np.exp2(r.integers(-12, 6, (48, 1)))).astype(np.float32)
+    w[0, :32] = 0.0
+    w[1, :32] = 0.75
+    w[2, 7] = 1e4
+    w = oracle.to_bf16(w)
+    words, scales = quantized.quantize_fp4(torch.from_numpy(w).to(torch.bfloat16), mode)
+    o_words, o_scales = (oracle.quantize_mxfp4 if mode == "mxfp4" else oracle.quantize_nvfp4)(w)
+    assert np.array_equal(words.numpy().view(np.uint32), o_words)
+    assert np.array_equal(scales.numpy(), o_scales)

@@ -558,3 +558,76 @@ def test_krea_block_gates_and_modulation_order():
     full = oracle.krea_block(p_out, x, only_attn, None, heads=heads, kv_heads=kv_heads) - x
     assert max_abs(2 * half, full) < 1e-5
     assert max_abs(half, 0) > 1e-3
+
+
+# ---- FP4 (mxfp4 / nvfp4) -------------------------------------------------------------------------
+
+
+def test_e2m1_decode_is_the_published_table():
+    """OCP MX v1.0 E2M1: codes 0..7 are 0, 0.5, 1, 1.5, 2, 3, 4, 6 (the standard's table, typed
+    here, not derived from the oracle's field formula); bit 3 is the sign."""
+    table = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0]
+    got = oracle.e2m1_decode(np.arange(16))
+    assert got[:8].tolist() == table
+    assert (-got[8:]).tolist() == table and np.all(np.signbit(got[8:]))
+
+
+def test_e2m1_encode_rounds_to_nearest_even_and_saturates():
+    codes = np.arange(16)
+    assert np.array_equal(oracle.e2m1_encode(oracle.e2m1_decode(codes)), codes)
+    grid = oracle.e2m1_decode(np.arange(8)).astype(np.float64)
+    # brute force: the nearest grid value, ties to the even code (codes 0, 2, 4, 6 have mantissa 0)
+    r = np.random.default_rng(3)
+    x = np.concatenate([r.uniform(-7, 7, 20000), (grid[:-1] + grid[1:]) / 2, -(grid[:-1] + grid[1:]) / 2])
+    a = np.minimum(np.abs(x), 6.0)
+    dist = np.abs(a[:, None] - grid[None, :])
+    best = dist.min(axis=1, keepdims=True)
+    cand = np.where(dist == best, np.arange(8)[None, :], 99)
+    even = np.where(cand % 2 == 0, cand, 99).min(axis=1)
+    expect = np.where(even < 99, even, cand.min(axis=1)) | np.where(np.signbit(x), 8, 0)
+    assert np.array_equal(oracle.e2m1_encode(x), expect)
+    assert oracle.e2m1_encode(np.array([7.0, 1e30, -6.5]))[:].tolist() == [7, 7, 15]
+    assert oracle.e2m1_encode(np.array([np.nan]))[0] == 0
+
+
+@pytest.mark.parametrize("mode,group", [("mxfp4", 32), ("nvfp4", 16)])
+def test_fp4_identity_round_trips(mode, group):
+    """The reference's binding test packs an identity and gets its input back
+    (``tests/models/ltx2/weights/test_family.py:262-283``, mxfp8). mxfp4 represents 0 and 1 exactly
+    (scale 2^-2, code 4); nvfp4's scale is E4M3(amax / 6), exact for amax = 6 (scale 1, code 6),
+    so ``6 * eye`` round-trips there (1 / 6 has no E4M3 form: an nvfp4 identity does not)."""
+    eye = np.eye(2 * group, dtype=np.float32) * (6.0 if mode == "nvfp4" else 1.0)
+    q = oracle.quantize_mxfp4(eye) if mode == "mxfp4" else oracle.quantize_nvfp4(eye)
+    assert np.array_equal(oracle.dequantize_fp4(*q, mode=mode), eye)
+    x = np.random.default_rng(1).standard_normal((3, 2 * group)).astype(np.float32)
+    assert np.array_equal(oracle.fp4_linear(x, *q, mode=mode), oracle.linear(x, eye))
+
+
+def test_mxfp4_scale_is_the_ocp_shared_exponent_and_error_within_half_a_step():
+    r = np.random.default_rng(2)
+    w = (r.standard_normal((64, 128)) * np.exp2(r.integers(-8, 8, (64, 1)))).astype(np.float32)
+    words, scales = oracle.quantize_mxfp4(w)
+    g = w.reshape(64, 4, 32).astype(np.float64)
+    amax = np.abs(g).max(-1)
+    assert np.array_equal(scales.astype(np.int64) - 127, np.floor(np.log2(amax)).astype(np.int64) - 2)
+    deq = oracle.dequantize_fp4(words, scales, mode="mxfp4").reshape(64, 4, 32).astype(np.float64)
+    unit = np.exp2(scales.astype(np.float64) - 127)[..., None]  # 2^X: the element grid's unit
+    # below 2 units the grid step is 0.5 unit, then 1, then 2 (saturation above 6 units cannot
+    # happen: amax < 8 units)
+    step = np.where(np.abs(g) < 2 * unit, 0.5 * unit, np.where(np.abs(g) < 4 * unit, unit, 2 * unit))
+    assert np.all(np.abs(deq - g) <= step / 2 + np.maximum(0, np.abs(g) - 6 * unit))
+
+
+def test_nvfp4_scale_is_the_e4m3_of_amax_over_6():
+    r = np.random.default_rng(4)
+    w = (r.standard_normal((16, 64)) * 0.05).astype(np.float32)
+    words, scales = oracle.quantize_nvfp4(w)
+    amax = np.abs(w.reshape(16, 4, 16)).max(-1)
+    # torch's E4M3 (RNE) cast of amax / 6 is the scale byte
+    import torch
+
+    expect = torch.from_numpy((amax / np.float32(6.0)).astype(np.float32)).to(torch.float8_e4m3fn).view(torch.uint8)
+    assert np.array_equal(scales, expect.numpy())
+    deq = oracle.dequantize_fp4(words, scales, mode="nvfp4")
+    s = np.repeat(oracle.e4m3_decode(scales).astype(np.float64), 16, axis=1)
+    assert np.all(np.abs(deq - w) <= s * 1.0 + 1e-12)  # at most half the largest E2M1 step (2) per unit
