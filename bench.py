@@ -143,6 +143,9 @@ def main() -> int:
                         help="write one block's launch sequence (labels, FLOPs, bytes) as JSON to this path")
     parser.add_argument("--profile-summary", type=str, default="", metavar="DIR",
                         help="only summarize the rocprofv3 runs under DIR (see profiles/) as a markdown table")
+    parser.add_argument("--compare-rope-fold", action="store_true",
+                        help="only time LTX's Q/K norm + RoPE folded into the QKV GEMM epilogue against the "
+                             "separate pass, and exit")
     parser.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                         help="only run 5 device-to-device copies of MIB MiB (the known-size kernel that "
                              "scales the FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -162,6 +165,8 @@ def main() -> int:
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
         return 2
+    if args.compare_rope_fold:
+        return rope_fold_main(args)
     if args.denoise_step:
         return denoise_main(args)
     if args.load_checkpoint:
@@ -521,6 +526,75 @@ def load_main(args) -> int:
                             "hbm_gbs": round(q_bytes / (q_ms * 1e-3) / 1e9, 1) if q_ms else None},
     }
     print(json.dumps(result))
+    return 0
+
+
+def rope_fold_main(args) -> int:
+    """The config-3 self-attention Q/K/V projection (9216 x 12288 x 4096, bias) three ways: plain;
+    with the per-head RMSNorm + RoPE epilogue of the fused QKV GEMM (``kx_gemm_qknorm_rope_bf16``,
+    cos/sin tables of LTX's size: 64 fp32 per head and token); and the separate
+    ``kx_qk_rmsnorm_rope_bf16`` pass over its Q and K columns that LTX runs. LTX's Q/K norms span
+    the whole 4096-wide row, so a folded LTX epilogue would cost at least the per-head epilogue plus
+    a cross-tile reduction: the fold pays only if ``epilogue_extra_us`` stays below
+    ``separate_pass_us``. Timing only (the inputs are random)."""
+    import torch
+
+    from kinomlx_amd import _lib, workloads
+    from kinomlx_amd.kernels import mpp_linear
+
+    _lib.load()
+    device = torch.device("cuda:0")
+    spec = workloads.CONFIGS[3]
+    m, d, half = spec.tokens, spec.dim, spec.head_dim // 2
+    g = torch.Generator(device=device).manual_seed(0)
+    a = torch.randn(m, d, device=device, generator=g).to(torch.bfloat16)
+    w = (torch.randn(3 * d, d, device=device, generator=g) * 0.02).to(torch.bfloat16)
+    b = (torch.randn(3 * d, device=device, generator=g) * 0.02).to(torch.bfloat16)
+    norm_w = torch.ones(d, device=device, dtype=torch.bfloat16)
+    qkv = torch.empty(m, 3 * d, dtype=torch.bfloat16, device=device)
+    # the epilogue reads 128 table entries per head from head * table_hs: 64 more per row than LTX's
+    # (tokens, heads * 64) tables hold, so the fold's table is padded by one half head
+    fold_ld = spec.heads * half + half
+    cos_f, sin_f = (torch.rand(m, fold_ld, device=device, generator=g) for _ in range(2))
+    cos, sin = (t[:, : spec.heads * half].contiguous() for t in (cos_f, sin_f))
+    q_out, k_out = torch.empty(m, d, dtype=torch.bfloat16, device=device), torch.empty(m, d, dtype=torch.bfloat16,
+                                                                                       device=device)
+
+    def timed(fn, iters=max(args.steps, 10)):
+        for _ in range(max(args.warmup, 2)):
+            fn()
+        begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        begin.record()
+        for _ in range(iters):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        return begin.elapsed_time(end) / iters * 1e3
+
+    plain = timed(lambda: mpp_linear.fused_linear(a, w, b, out=qkv))
+    folded = timed(lambda: _lib.launch_gemm_qknorm_rope(
+        a, w, qkv, bias=b, q_end=d, k_end=2 * d, norm_q=norm_w[:128], norm_k=norm_w[:128], eps=1e-6,
+        weight_offset=0.0, cos=cos_f, sin=sin_f, table_ld=fold_ld, table_hs=half, table_rows=m, table_bs=0))
+
+    def separate():
+        if not _lib.launch_qk_rmsnorm_rope(qkv[:, :d], qkv[:, d:2 * d], q_out, k_out, norm_w, norm_w, 1e-6, cos=cos,
+                                           sin=sin, table_ld=spec.heads * half, table_hs=half, tokens=m,
+                                           table_batched=False):
+            raise RuntimeError("kx_qk_rmsnorm_rope_bf16 refused the config-3 shape")
+
+    pass_us = timed(separate)
+    extra = folded - plain
+    print(json.dumps({
+        "compare": "LTX Q/K norm + RoPE: folded into the QKV GEMM epilogue vs the separate pass",
+        "workload": f"config 3: {m} tokens, QKV {m}x{3 * d}x{d} bf16 + bias, {spec.heads} heads x {spec.head_dim}",
+        "qkv_plain_us": round(plain, 1),
+        "qkv_per_head_norm_rope_epilogue_us": round(folded, 1),
+        "epilogue_extra_us": round(extra, 1),
+        "separate_pass_us": round(pass_us, 1),
+        "fold_saves_at_most_us": round(pass_us - extra, 1),
+        "note": "a full-row (4096-wide) norm adds a cross-tile reduction to the per-head epilogue's cost",
+    }))
     return 0
 
 

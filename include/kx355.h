@@ -216,7 +216,7 @@ int kx_gemm_bf16(const void* a, int64_t lda, const void* w, int64_t ldw, const v
  * applies the epilogue (bias, activation, gated residual, output type) as kx_gemm_bf16 does.
  * Same products as the reference call of kx_gemm_bf16 (mpp_linear.linear / mx.addmm,
  * kinomlx/kernels/mpp_linear.py:469-506); the sum order over K differs (fp32 throughout).
- * Requires n % 4 == 0, k % (32 * splits) == 0, 2 <= splits <= 64.
+ * Requires n % 4 == 0, k % (64 * splits) == 0, 2 <= splits <= 64.
  */
 int kx_gemm_splitk_bf16(const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias, void* c,
                         int64_t ldc, int64_t m, int64_t n, int64_t k, int epilogue, const void* resid,
@@ -254,7 +254,7 @@ int kx_gemm_splitk_noalloc_bf16(const void* a, int64_t lda, const void* w, int64
  * 25-29, 88-164) and of Krea2Attention (kinomlx/models/krea2/transformer/model.py:29-46, 69-92,
  * 134-185); the bf16 q/k round trip through HBM between the projection and the norm pass is
  * removed. norm weights fp32 or bf16 (norm_dtype KX_F32 / KX_BF16);
- * requires k % 32 == 0 and 16-byte aligned table rows.
+ * requires k % 64 == 0 and 16-byte aligned table rows.
  */
 int kx_gemm_qknorm_rope_bf16(const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias, void* c,
                              int64_t ldc, int64_t m, int64_t n, int64_t k, int64_t q_end, int64_t k_end,

@@ -548,7 +548,7 @@ def tail_split(m: int, n: int, k: int) -> tuple[int, int] | None:
     if tail_tiles <= 128:
         # the most slices that still fit one round
         for cand in (2, 4, 8):
-            if tail_tiles * cand <= 256 and k % (32 * cand) == 0 and k // cand >= 512:
+            if tail_tiles * cand <= 256 and k % (64 * cand) == 0 and k // cand >= 512:
                 splits = cand
     else:
         # a tail over half a round (27 280 rows: 176 tiles): the slice count with the fewest
@@ -556,7 +556,7 @@ def tail_split(m: int, n: int, k: int) -> tuple[int, int] | None:
         best = 1.0
         for cand in (2, 4, 8):
             cost = -(-tail_tiles * cand // 256) / cand
-            if cost < best - 1e-9 and k % (32 * cand) == 0 and k // cand >= 512:
+            if cost < best - 1e-9 and k % (64 * cand) == 0 and k // cand >= 512:
                 splits, best = cand, cost
     return (rows, splits) if splits > 1 else None
 
@@ -564,7 +564,7 @@ def tail_split(m: int, n: int, k: int) -> tuple[int, int] | None:
 def splitk_splits(m: int, n: int, k: int) -> int:
     """K slices for a product whose output tiles (64 x 128) leave most of the 256 CUs idle:
     the most slices (up to 16) that keep at most 512 workgroups, a slice of at least 256 and a
-    whole number of 32-wide stages per slice; 1 means no split."""
+    whole number of 64-wide stages per slice; 1 means no split."""
     if m > 512 or n <= 64 or n % 4 or k < 1024:
         return 1
     tiles = -(-m // 64) * -(-n // 128)
@@ -572,7 +572,7 @@ def splitk_splits(m: int, n: int, k: int) -> int:
         return 1
     best = 1
     for splits in (2, 4, 8, 16):
-        if tiles * splits <= 512 and k % (32 * splits) == 0 and k // splits >= 256:
+        if tiles * splits <= 512 and k % (64 * splits) == 0 and k // splits >= 256:
             best = splits
     return best
 

@@ -454,33 +454,60 @@ __global__ __launch_bounds__(256) void dequant_mx8_t_kernel(const uint32_t* __re
   }
 }
 
-// ---- direct-to-LDS pipelined kernel (K % 32 == 0) -----------------------------------------------
+// ---- direct-to-LDS pipelined kernel (dense: K % 64 == 0; quantized: K % 128 == 0) ------------
 //
 // Operand tiles go from global memory straight into LDS with global_load_lds_dwordx4 (no VGPR
-// staging): one wave instruction fills 64 lanes x 16 B = RPI rows of BKT bf16. NS LDS stages of
-// BKT = 32 along K form a ring: while stage kt is consumed, stages kt+1 .. kt+NS-1 are in flight.
-// Each wave issues its DMA instructions for stage kt+NS-1 between the MFMAs of the first k16
-// steps, from a scalar tile base plus a loop-invariant 32-bit lane offset. Every k16 step is
-// one scheduling region: wait for this step's fragments (read one step earlier), issue the
-// fragment reads of the next step, then the step's MFMAs — so LDS latency hides under a full
-// step of MFMAs and never more than MB + NB reads are outstanding (lgkmcnt counts to 15). The
-// last step of a stage holds the stage's only workgroup barrier. The 16-byte slot of a row is
-// XOR-swizzled so that both the DMA writes and the 32-row fragment reads are bank-conflict free.
+// staging): one wave instruction fills 64 lanes x 16 B = DRPI rows of DBK bf16, from a scalar tile
+// base plus a loop-invariant 32-bit lane offset. Dense products use stages of DBK = 64 along K in
+// a ring of two: a row's 128 bytes of a stage are one full cache line, so each row makes one
+// 128-byte L1 -> L2 request. The per-CU operand stream is bounded by the requests it keeps in
+// flight times their latency, so 128-byte requests carry twice the bytes of the 64-byte ones
+// that 32-wide stages make. Stage kt+2 goes into stage kt's buffer, half of its DMA instructions
+// right after the barrier of stage kt's last k16 step and half during stage kt+1's first step.
+// Quantized products keep 32-wide stages in a ring of four, their DMA for stage kt+3 between
+// the MFMAs of stage kt. Every k16 step is one scheduling region: wait for this step's
+// fragments (read one step earlier), issue the fragment reads of the next step, then the step's
+// MFMAs, so LDS latency hides under a full step of MFMAs and never more than MB + NB reads are
+// outstanding (lgkmcnt counts to 15). The last step of a stage holds the stage's only workgroup
+// barrier. The 16-byte slots of a row are XOR-swizzled so that both the DMA writes and the
+// 32-row fragment reads are bank-conflict free.
 //
 // Epilogue: each wave stages half of its fp32 tile in LDS at a time and writes it back in rows,
 // 4 columns per lane, so bias / gate / residual loads and the stores are contiguous runs. Full,
 // aligned tiles take a compile-time specialisation per residual mode (GMODE 0: none, 1: bf16
 // residual, 2: fp32 residual) and output type; edge tiles take the generic masked path.
 
-constexpr int DBK = 32;                // K per LDS stage
-constexpr int DROW = DBK * 2;          // bytes per LDS row
-constexpr int DCPR = DBK / 8;          // 16-byte chunks per row
-constexpr int DRPI = 64 / DCPR;        // rows one DMA instruction fills
-constexpr int DNS = 4;                 // stages in the ring
-__device__ __forceinline__ int dswz(int r) { return (r >> 2) & 3; }
+// K per LDS stage of a dense product: a row's 128 bytes per stage are one full cache line, so
+// every DMA lane group of a row makes one 128-byte request (32-wide stages made two 64-byte
+// requests per line, twice the L1 -> L2 requests for the same bytes)
+constexpr int DENSE_BK = 64;
 // 8-bit packed weight rows (32 bytes per stage): chunk swizzle of row r
 __device__ __forceinline__ int qswz(int r) { return (r >> 3) & 1; }
 #define KX_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+// One k16 step's order: each of the next step's NRD fragment reads before an MFMA, then ND DMA
+// issues (address VALU + VMEM) each before an MFMA, then the remaining MFMAs.
+template <int NRD, int NMF, int ND>
+__device__ __forceinline__ void step_schedule() {
+  constexpr int PAIRS = NRD < NMF ? NRD : NMF;
+  constexpr int DMF = ND < NMF - PAIRS ? ND : NMF - PAIRS;
+#pragma unroll
+  for (int q = 0; q < PAIRS; ++q) {
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+  }
+  if constexpr (NRD > PAIRS) __builtin_amdgcn_sched_group_barrier(0x100, NRD - PAIRS, 0);
+#pragma unroll
+  for (int q = 0; q < DMF; ++q) {
+    __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+  }
+  if constexpr (ND > DMF) {
+    __builtin_amdgcn_sched_group_barrier(0x002, ND - DMF, 0);
+    __builtin_amdgcn_sched_group_barrier(0x020, ND - DMF, 0);
+  }
+  if constexpr (NMF > PAIRS + DMF) __builtin_amdgcn_sched_group_barrier(0x008, NMF - PAIRS - DMF, 0);
+}
 // A workgroup barrier that the compiler may not move memory accesses across.
 #define KX_BARRIER() asm volatile("s_barrier" ::: "memory")
 
@@ -609,6 +636,16 @@ template <int BM, int BN, int QB, bool TL, int GMODE, bool OUTF32, bool NR = fal
 __global__ __launch_bounds__(256) void gemm_lds_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ W, int64_t ldw,
     QuantW qw, void* __restrict__ C, int64_t ldc, int M, int N, int K, Epilogue epi) {
+  // stage geometry: dense, 64-wide stages in a 2-stage ring; quantized, 32-wide stages in a
+  // 4-stage ring. A row's 16-byte slots are XOR-swizzled (by (r >> 1) & 7, resp. (r >> 2) & 3) so
+  // that the DMA writes and the 32-row fragment reads are bank-conflict free.
+  constexpr bool D64 = QB == 0;
+  constexpr int DBK = D64 ? DENSE_BK : 32;  // K per LDS stage
+  constexpr int DROW = DBK * 2;             // bytes per LDS row
+  constexpr int DCPR = DBK / 8;             // 16-byte chunks per row
+  constexpr int DRPI = 64 / DCPR;           // rows one DMA instruction fills
+  constexpr int DNS = D64 ? 2 : 4;          // stages in the ring
+  const auto dswz = [](int r) { return D64 ? (r >> 1) & 7 : (r >> 2) & 3; };
   constexpr int A_INST = BM / DRPI / 4;
   constexpr int QROW = DBK * qbits<QB>() / 8;                         // packed bytes per row
   constexpr int WQ_INST = QB ? BN * QROW / 1024 / 4 : 0;              // packed words, per wave
@@ -626,12 +663,12 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
   constexpr int WT_M = BM / WGM, WT_N = BN / WGN;
   constexpr int MB = WT_M / 32, NB = WT_N / 32;
   constexpr int KS = DBK / 16;
-  static_assert(KS == 2, "two k16 steps per stage");
+  static_assert(KS == (D64 ? 4 : 2), "k16 steps per stage");
   constexpr int DPS = (PER + KS - 1) / KS;  // DMA instructions per k16 step
   // At the wait in the last k16 step, stages kt+2 .. kt+NS-2 and the DMA of this iteration's
   // earlier steps may stay in flight: stage kt+1 is then complete.
   constexpr int NBEFORE = (KS - 1) * DPS < PER ? (KS - 1) * DPS : PER;
-  constexpr int WAITN = (DNS - 3) * PER + NBEFORE;
+  constexpr int WAITN = D64 ? 0 : (DNS - 3) * PER + NBEFORE;
   constexpr int PITCH = WT_N / 2 + 4;  // staged epilogue row, floats
   constexpr int EP_BYTES = 4 * WT_M * PITCH * 4;
   constexpr int SMEM = RING > EP_BYTES ? RING : EP_BYTES;
@@ -794,11 +831,22 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
   const int stages = K / DBK;
+  // dense: stage 0, and the first DH1 DMA instructions of stage 1 (the rest go out in stage 0's
+  // first step); quantized: stages 0 .. NS-2
+  constexpr int DH1 = (PER + 1) / 2;
+  if constexpr (D64) {
 #pragma unroll
-  for (int p = 0; p < DNS - 1; ++p)
+    for (int i = 0; i < PER; ++i) dma(i, smem, 0);
 #pragma unroll
-    for (int i = 0; i < PER; ++i) dma(i, smem + p * STAGE, min(p, stages - 1) * DBK);
-  wait_vmcnt<(DNS - 2) * PER>();
+    for (int i = 0; i < DH1; ++i) dma(i, smem + STAGE, min(1, stages - 1) * DBK);
+    wait_vmcnt<DH1>();
+  } else {
+#pragma unroll
+    for (int p = 0; p < DNS - 1; ++p)
+#pragma unroll
+      for (int i = 0; i < PER; ++i) dma(i, smem + p * STAGE, min(p, stages - 1) * DBK);
+    wait_vmcnt<(DNS - 2) * PER>();
+  }
   KX_BARRIER();
   bf16x8 fa[2][MB], fw[2][NB];
   int cur_i = 0;
@@ -964,14 +1012,17 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
       cur_i = nxt_i;
     }
   } else {
+    // Two 64-wide stages. Stage kt+2 goes into stage kt's buffer: its first DH1 DMA instructions
+    // right after the barrier of stage kt's last k16 step (every wave has read that buffer's
+    // last fragments by then), the rest during step 0 of stage kt+1; the barrier of stage
+    // kt+1's last step waits for all of them. Past the end the last stage is re-read, which
+    // keeps the loop free of branches and the vmcnt arithmetic uniform.
     load_frags(smem, 0, fa[0], fw[0]);
     for (int kt = 0; kt < stages; ++kt) {
-      const uint8_t* cur = smem + cur_i * STAGE;
-      const int nxt_i = cur_i + 1 == DNS ? 0 : cur_i + 1;
-      // stage kt+NS-1 goes into the buffer stage kt-1 used; past the end the last stage is
-      // re-read into it, which keeps the loop free of branches and the vmcnt arithmetic uniform
-      uint8_t* iss = smem + (cur_i == 0 ? DNS - 1 : cur_i - 1) * STAGE;
-      const int k_iss = min(kt + DNS - 1, stages - 1) * DBK;
+      uint8_t* cur = smem + (kt & 1) * STAGE;
+      uint8_t* oth = smem + ((kt & 1) ^ 1) * STAGE;
+      const int k1 = min(kt + 1, stages - 1) * DBK;
+      const int k2 = min(kt + 2, stages - 1) * DBK;
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
         const int b = s & 1;
@@ -981,45 +1032,31 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
         if (s + 1 < KS) {
           load_frags(cur, s + 1, fa[b ^ 1], fw[b ^ 1]);
         } else {
-          // stage kt+1 has landed for this wave and its reads of cur are done; after the barrier
-          // this holds for every wave, and nobody reads cur again before it is refilled
-          wait_vmcnt<WAITN>();
+          wait_vmcnt<0>();
           KX_BARRIER();
-          load_frags(smem + nxt_i * STAGE, 0, fa[b ^ 1], fw[b ^ 1]);
+          load_frags(oth, 0, fa[b ^ 1], fw[b ^ 1]);
         }
+        constexpr int ND0 = PER - DH1;
+        if (s == 0) {
 #pragma unroll
-        for (int d = 0; d < DPS; ++d)
-          if (s * DPS + d < PER) dma(s * DPS + d, iss, k_iss);
+          for (int d = DH1; d < PER; ++d) dma(d, oth, k1);
+        } else if (s + 1 == KS) {
+#pragma unroll
+          for (int d = 0; d < DH1; ++d) dma(d, cur, k2);
+        }
 #pragma unroll
         for (int i = 0; i < NB; ++i)
 #pragma unroll
           for (int j = 0; j < MB; ++j)
             acc[i][j] = mfma32x32x16<H>(fw[b][i], fa[b][j], acc[i][j]);
-        // the next step's fragment reads one per MFMA (a burst of them fills the LDS command
-        // queue and stalls the wave before its MFMAs), then the DMA issues between the
-        // remaining MFMAs
-        constexpr int NRD = MB + NB, NMF = NB * MB;
-        constexpr int PAIRS = NRD < NMF ? NRD : NMF;
-        constexpr int DMF = DPS < NMF - PAIRS ? DPS : NMF - PAIRS;
-#pragma unroll
-        for (int q = 0; q < PAIRS; ++q) {
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (s == 0) {
+          step_schedule<MB + NB, NB * MB, ND0>();
+        } else if (s + 1 == KS) {
+          step_schedule<MB + NB, NB * MB, DH1>();
+        } else {
+          step_schedule<MB + NB, NB * MB, 0>();
         }
-        if constexpr (NRD > PAIRS) __builtin_amdgcn_sched_group_barrier(0x100, NRD - PAIRS, 0);
-#pragma unroll
-        for (int q = 0; q < DMF; ++q) {
-          __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        }
-        if constexpr (DPS > DMF) {
-          __builtin_amdgcn_sched_group_barrier(0x002, DPS - DMF, 0);
-          __builtin_amdgcn_sched_group_barrier(0x020, DPS - DMF, 0);
-        }
-        if constexpr (NMF > PAIRS + DMF) __builtin_amdgcn_sched_group_barrier(0x008, NMF - PAIRS - DMF, 0);
       }
-      cur_i = nxt_i;
     }
   }
   wait_vmcnt<0>();
@@ -1487,7 +1524,7 @@ int dispatch(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, Qua
     return KX_OK;
   }
   // the direct-to-LDS kernel keeps per-lane 32-bit byte offsets within a 256-row tile
-  if (QB == 0 && k % DBK == 0 && lda <= (1 << 22) && ldw <= (1 << 22) && !use_legacy) {
+  if (QB == 0 && k % DENSE_BK == 0 && lda <= (1 << 22) && ldw <= (1 << 22) && !use_legacy) {
     switch (pick_lds_cfg(m, n)) {
       case 0: return launch_lds<256, 256, 0, false, H>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi, s);
       case 1: return launch_lds<192, 256, 0, false, H>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi, s);
@@ -1677,8 +1714,9 @@ extern "C" int kx_gemm_qknorm_rope_bf16(const void* a, int64_t lda, const void* 
                                         kx_stream_t stream) {
   const char* what = "kx_gemm_qknorm_rope_bf16";
   KX_REQUIRE(a && w && c && norm_q && norm_k && cos && sin, "%s: null tensor", what);
-  KX_REQUIRE(m >= 0 && n > 0 && k > 0 && m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 30) && k % 32 == 0,
-             "%s: bad shape (m=%lld n=%lld k=%lld; k %% 32 == 0)", what, (long long)m, (long long)n, (long long)k);
+  KX_REQUIRE(m >= 0 && n > 0 && k > 0 && m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 30) &&
+                 k % DENSE_BK == 0,
+             "%s: bad shape (m=%lld n=%lld k=%lld; k %% 64 == 0)", what, (long long)m, (long long)n, (long long)k);
   KX_REQUIRE(q_end >= 0 && q_end % 128 == 0 && k_end >= q_end && k_end % 128 == 0 && k_end <= n,
              "%s: the query and key columns must be whole 128-wide heads inside n (q_end=%lld k_end=%lld)", what,
              (long long)q_end, (long long)k_end);
@@ -1909,8 +1947,8 @@ int check_splitk(const char* what, const void* a, int64_t lda, const void* w, in
   KX_REQUIRE(a && w && c, "%s: null tensor", what);
   KX_REQUIRE(splits >= 2 && splits <= 64, "%s: splits must be 2..64, got %d", what, splits);
   KX_REQUIRE(m > 0 && n > 0 && k > 0 && m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 30) && n % 4 == 0 &&
-                 k % (splits * DBK) == 0,
-             "%s: bad shape (m=%lld n=%lld k=%lld; n %% 4 == 0, k %% (32 splits) == 0)", what, (long long)m,
+                 k % (splits * DENSE_BK) == 0,
+             "%s: bad shape (m=%lld n=%lld k=%lld; n %% 4 == 0, k %% (64 splits) == 0)", what, (long long)m,
              (long long)n, (long long)k);
   KX_REQUIRE(lda % 8 == 0 && ldw % 8 == 0 && lda >= k && ldw >= k && ldc >= n && lda <= (1 << 22) &&
                  ldw <= (1 << 22),

@@ -225,7 +225,7 @@ def qknorm_rope_projection(layer, value: torch.Tensor, out: torch.Tensor, *, q_w
     tokens = int(cos.shape[-2])
     batches = 1 if cos.dim() == 2 else int(cos.shape[0])
     if (rows == 0 or tokens == 0 or rows % tokens or batches not in (1, rows // tokens) or cos.shape[-1] != 128
-            or q_width % 128 or k_width % 128 or q_width + k_width > n or k % 32 or int(weight.shape[1]) != k
+            or q_width % 128 or k_width % 128 or q_width + k_width > n or k % 64 or int(weight.shape[1]) != k
             or norm_q.shape != (128,) or norm_k.shape != (128,) or norm_q.dtype != norm_k.dtype
             or cos.dtype != torch.float32 or sin.dtype != torch.float32 or cos.stride(-1) != 1
             or cos.stride(-2) % 4 or (batches > 1 and cos.stride(0) % 4) or cos.data_ptr() % 16

@@ -78,7 +78,7 @@ def test_shape_and_format_checks():
     assert "bias" in lib.kx_last_error().decode()
     # unknown epilogue bits
     assert lib.kx_gemm_bf16(fake, 16, fake, 16, None, fake, 8, 4, 8, 16, 1 << 12, None, 0, None, 1, 0, None) == -1
-    # Q/K norm projection: heads must be whole 128-wide column blocks inside n, k a multiple of 32
+    # Q/K norm projection: heads must be whole 128-wide column blocks inside n, k a multiple of 64
     qk = lib.kx_gemm_qknorm_rope_bf16
     assert qk(fake, 64, fake, 64, None, fake, 512, 4, 512, 64, 192, 384, fake, fake, 0, 1e-6, 0.0, fake, fake, 128, 0,
               4, 0, None) == -1
@@ -87,6 +87,9 @@ def test_shape_and_format_checks():
               4, 0, None) == -1
     assert qk(fake, 48, fake, 48, None, fake, 512, 4, 512, 48, 256, 512, fake, fake, 0, 1e-6, 0.0, fake, fake, 128, 0,
               4, 0, None) == -1
+    assert qk(fake, 96, fake, 96, None, fake, 512, 4, 512, 96, 256, 512, fake, fake, 0, 1e-6, 0.0, fake, fake, 128, 0,
+              4, 0, None) == -1
+    assert "k % 64" in lib.kx_last_error().decode()
     assert qk(fake, 64, fake, 64, None, fake, 512, 4, 512, 64, 256, 512, fake, fake, 0, 1e-6, 0.0, fake, fake, 130, 0,
               4, 0, None) == -1
     # fused RoPE on a width the fused kernel does not take is refused, not silently changed

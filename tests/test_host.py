@@ -168,7 +168,7 @@ def test_tail_split_rule():
         rows, splits = _lib.tail_split(m, n, k)
         tail_tiles = -(-(m - rows) // 256) * (n // 256)
         assert rows % 256 == 0 and (rows // 256) * (n // 256) % 256 == 0
-        assert k % (32 * splits) == 0 and k // splits >= 512
+        assert k % (64 * splits) == 0 and k // splits >= 512
         assert tail_tiles * splits <= 256 or -(-tail_tiles * splits // 256) / splits < 1.0
 
 
