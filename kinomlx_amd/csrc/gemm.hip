@@ -458,14 +458,14 @@ __global__ __launch_bounds__(256) void dequant_mx8_t_kernel(const uint32_t* __re
 //
 // Operand tiles go from global memory straight into LDS with global_load_lds_dwordx4 (no VGPR
 // staging): one wave instruction fills 64 lanes x 16 B = DRPI rows of DBK bf16, from a scalar tile
-// base plus a loop-invariant 32-bit lane offset. Dense products use stages of DBK = 64 along K in
-// a ring of two: a row's 128 bytes of a stage are one full cache line, so each row makes one
+// base plus a loop-invariant 32-bit lane offset. Dense products use stages of DBK = 64 along K: a row's 128 bytes of a stage are one full cache line, so each row makes one
 // 128-byte L1 -> L2 request. The per-CU operand stream is bounded by the requests it keeps in
 // flight times their latency, so 128-byte requests carry twice the bytes of the 64-byte ones
-// that 32-wide stages make. Stage kt+2 goes into stage kt's buffer, half of its DMA instructions
-// right after the barrier of stage kt's last k16 step and half during stage kt+1's first step.
-// Quantized products keep 32-wide stages in a ring of four, their DMA for stage kt+3 between
-// the MFMAs of stage kt. Every k16 step is one scheduling region: wait for this step's
+// that 32-wide stages make. The 256 x 256 and 192 x 256 tiles keep two stages in LDS: stage kt+2
+// goes into stage kt's buffer, half of its DMA instructions right after the barrier of stage
+// kt's last k16 step and half during stage kt+1's first step. The small tiles (whose few MFMAs
+// per stage cannot hide a one-stage prefetch) keep a ring of four, and so do the quantized
+// products with 32-wide stages: their DMA for stage kt+3 goes out between the MFMAs of stage kt. Every k16 step is one scheduling region: wait for this step's
 // fragments (read one step earlier), issue the fragment reads of the next step, then the step's
 // MFMAs, so LDS latency hides under a full step of MFMAs and never more than MB + NB reads are
 // outstanding (lgkmcnt counts to 15). The last step of a stage holds the stage's only workgroup
@@ -636,15 +636,18 @@ template <int BM, int BN, int QB, bool TL, int GMODE, bool OUTF32, bool NR = fal
 __global__ __launch_bounds__(256) void gemm_lds_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ W, int64_t ldw,
     QuantW qw, void* __restrict__ C, int64_t ldc, int M, int N, int K, Epilogue epi) {
-  // stage geometry: dense, 64-wide stages in a 2-stage ring; quantized, 32-wide stages in a
-  // 4-stage ring. A row's 16-byte slots are XOR-swizzled (by (r >> 1) & 7, resp. (r >> 2) & 3) so
-  // that the DMA writes and the 32-row fragment reads are bank-conflict free.
+  // stage geometry: dense products, 64-wide stages, in a 2-stage ring for the 256 x 256 and
+  // 192 x 256 tiles and a 4-stage ring for the small tiles (whose few MFMAs per stage cannot
+  // cover a one-stage prefetch); quantized products, 32-wide stages in a 4-stage ring. A row's
+  // 16-byte slots are XOR-swizzled (by (r >> 1) & 7, resp. (r >> 2) & 3) so that the DMA writes
+  // and the 32-row fragment reads are bank-conflict free.
   constexpr bool D64 = QB == 0;
+  constexpr bool RING2 = D64 && BM * BN >= 192 * 256;
   constexpr int DBK = D64 ? DENSE_BK : 32;  // K per LDS stage
   constexpr int DROW = DBK * 2;             // bytes per LDS row
   constexpr int DCPR = DBK / 8;             // 16-byte chunks per row
   constexpr int DRPI = 64 / DCPR;           // rows one DMA instruction fills
-  constexpr int DNS = D64 ? 2 : 4;          // stages in the ring
+  constexpr int DNS = RING2 ? 2 : 4;        // stages in the ring
   const auto dswz = [](int r) { return D64 ? (r >> 1) & 7 : (r >> 2) & 3; };
   constexpr int A_INST = BM / DRPI / 4;
   constexpr int QROW = DBK * qbits<QB>() / 8;                         // packed bytes per row
@@ -668,7 +671,7 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
   // At the wait in the last k16 step, stages kt+2 .. kt+NS-2 and the DMA of this iteration's
   // earlier steps may stay in flight: stage kt+1 is then complete.
   constexpr int NBEFORE = (KS - 1) * DPS < PER ? (KS - 1) * DPS : PER;
-  constexpr int WAITN = D64 ? 0 : (DNS - 3) * PER + NBEFORE;
+  constexpr int WAITN = RING2 ? 0 : (DNS - 3) * PER + NBEFORE;
   constexpr int PITCH = WT_N / 2 + 4;  // staged epilogue row, floats
   constexpr int EP_BYTES = 4 * WT_M * PITCH * 4;
   constexpr int SMEM = RING > EP_BYTES ? RING : EP_BYTES;
@@ -834,7 +837,7 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
   // dense: stage 0, and the first DH1 DMA instructions of stage 1 (the rest go out in stage 0's
   // first step); quantized: stages 0 .. NS-2
   constexpr int DH1 = (PER + 1) / 2;
-  if constexpr (D64) {
+  if constexpr (RING2) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) dma(i, smem, 0);
 #pragma unroll
@@ -1009,6 +1012,64 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
         __builtin_amdgcn_sched_barrier(0);
       }
       dq_commit(fw[0]);
+      cur_i = nxt_i;
+    }
+  } else if constexpr (!RING2) {
+    load_frags(smem, 0, fa[0], fw[0]);
+    for (int kt = 0; kt < stages; ++kt) {
+      const uint8_t* cur = smem + cur_i * STAGE;
+      const int nxt_i = cur_i + 1 == DNS ? 0 : cur_i + 1;
+      // stage kt+NS-1 goes into the buffer stage kt-1 used; past the end the last stage is
+      // re-read into it, which keeps the loop free of branches and the vmcnt arithmetic uniform
+      uint8_t* iss = smem + (cur_i == 0 ? DNS - 1 : cur_i - 1) * STAGE;
+      const int k_iss = min(kt + DNS - 1, stages - 1) * DBK;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const int b = s & 1;
+        __builtin_amdgcn_sched_barrier(0);
+        wait_lgkmcnt0();
+        __builtin_amdgcn_sched_barrier(0);
+        if (s + 1 < KS) {
+          load_frags(cur, s + 1, fa[b ^ 1], fw[b ^ 1]);
+        } else {
+          // stage kt+1 has landed for this wave and its reads of cur are done; after the barrier
+          // this holds for every wave, and nobody reads cur again before it is refilled
+          wait_vmcnt<WAITN>();
+          KX_BARRIER();
+          load_frags(smem + nxt_i * STAGE, 0, fa[b ^ 1], fw[b ^ 1]);
+        }
+#pragma unroll
+        for (int d = 0; d < DPS; ++d)
+          if (s * DPS + d < PER) dma(s * DPS + d, iss, k_iss);
+#pragma unroll
+        for (int i = 0; i < NB; ++i)
+#pragma unroll
+          for (int j = 0; j < MB; ++j)
+            acc[i][j] = mfma32x32x16<H>(fw[b][i], fa[b][j], acc[i][j]);
+        // the next step's fragment reads one per MFMA (a burst of them fills the LDS command
+        // queue and stalls the wave before its MFMAs), then the DMA issues between the
+        // remaining MFMAs
+        constexpr int NRD = MB + NB, NMF = NB * MB;
+        constexpr int PAIRS = NRD < NMF ? NRD : NMF;
+        constexpr int DMF = DPS < NMF - PAIRS ? DPS : NMF - PAIRS;
+#pragma unroll
+        for (int q = 0; q < PAIRS; ++q) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+        if constexpr (NRD > PAIRS) __builtin_amdgcn_sched_group_barrier(0x100, NRD - PAIRS, 0);
+#pragma unroll
+        for (int q = 0; q < DMF; ++q) {
+          __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+        if constexpr (DPS > DMF) {
+          __builtin_amdgcn_sched_group_barrier(0x002, DPS - DMF, 0);
+          __builtin_amdgcn_sched_group_barrier(0x020, DPS - DMF, 0);
+        }
+        if constexpr (NMF > PAIRS + DMF) __builtin_amdgcn_sched_group_barrier(0x008, NMF - PAIRS - DMF, 0);
+      }
       cur_i = nxt_i;
     }
   } else {
@@ -1335,10 +1396,13 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
 
 // ---- skinny kernel (N <= 64: the gate-logit projections) ------------------------------------
 //
-// One workgroup per 32 rows x 32 columns; its NWK waves split K into NWK slices and read both
-// MFMA operands straight from global memory (the weight is a few hundred KB and stays in L2, each
-// activation row is read once), then add their partial tiles through LDS. (Splitting K over 8 or
-// 16 waves measured slower at 9216 x 32 x 4096: fewer workgroups fit a CU.) The products are
+// One workgroup per R rows x 32 columns, R = ceil(M / 256) (at least 16, at most 128), so that the
+// rows spread evenly over the 256 CUs: the kernel is bound by each CU's operand stream, and 32-row
+// workgroups (288 of them at 9216 rows) left 32 CUs with twice the rows of the others. The R rows
+// are RB = ceil(R / 16) MFMA row blocks; rows past R or M re-read the last valid row (the same
+// cache lines as its own lanes) and are not stored. The NWK waves split K into NWK slices and
+// read both MFMA operands straight from global memory (the weight is a few hundred KB and stays
+// in L2, each activation row is read once), then add their partial tiles through LDS. The products are
 // 16x16x32 MFMAs: a 16-byte operand load then spans 16 rows (four lanes of 64 contiguous bytes per
 // row) instead of the 32 rows of a 32x32x16 operand, which halves the cache lines each load
 // instruction touches, the limit of this kernel.
@@ -1352,29 +1416,31 @@ __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-template <int QB, int NWK, bool H = false>
+template <int QB, int NWK, int RB, bool H = false>
 __global__ __launch_bounds__(NWK * 64) void gemm_skinny_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ W, int64_t ldw,
-    QuantW qw, void* __restrict__ C, int64_t ldc, int M, int N, int K, Epilogue epi) {
-  __shared__ __attribute__((aligned(16))) float part[NWK][16][64];
+    QuantW qw, void* __restrict__ C, int64_t ldc, int M, int N, int K, int R, Epilogue epi) {
+  __shared__ __attribute__((aligned(16))) float part[NWK][2 * RB * 4][64];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l16 = lane & 15, lq = lane >> 4;
-  const int m0 = blockIdx.x * 32, n0 = blockIdx.y * 32;
-  // operand rows of this lane: activation rows m0 + 16 rb + l16, weight rows n0 + 16 cb + l16
-  int arow_i[2], wrow_i[2];
+  const int m0 = blockIdx.x * R, n0 = blockIdx.y * 32;
+  const int mend = min(m0 + R, M);
+  // operand rows of this lane: activation rows m0 + 16 rb + l16 (clamped to the last valid row),
+  // weight rows n0 + 16 cb + l16
+  int wrow_i[2];
 #pragma unroll
-  for (int b = 0; b < 2; ++b) {
-    arow_i[b] = min(m0 + 16 * b + l16, M - 1);
-    wrow_i[b] = min(n0 + 16 * b + l16, N - 1);
-  }
+  for (int b = 0; b < 2; ++b) wrow_i[b] = min(n0 + 16 * b + l16, N - 1);
+  const uint16_t* arow[RB];
+#pragma unroll
+  for (int b = 0; b < RB; ++b) arow[b] = A + (int64_t)min(m0 + 16 * b + l16, mend - 1) * lda + 8 * lq;
   const int kq = K / NWK, kbeg = wave * kq;
   // accumulator (cb, rb): lane holds weight rows n0 + 16 cb + 4 lq + e, activation row m0 + 16 rb + l16
-  f32x4 acc[2][2];
+  f32x4 acc[2][RB];
 #pragma unroll
   for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc[cb][rb][e] = 0.0f;
   auto wfrag = [&](int n, int k) -> bf16x8 {  // row n, this lane's 8 values start at k (k % 8 == 0)
@@ -1393,36 +1459,59 @@ __global__ __launch_bounds__(NWK * 64) void gemm_skinny_kernel(
       return __builtin_bit_cast(bf16x8, dequant8<QB>(tmp, sc, bi));
     }
   };
-  const uint16_t* arow0 = A + (int64_t)arow_i[0] * lda + 8 * lq;
-  const uint16_t* arow1 = A + (int64_t)arow_i[1] * lda + 8 * lq;
-#pragma unroll 4
+#pragma unroll 2
   for (int k = kbeg; k < kbeg + kq; k += 32) {
     const bf16x8 w0 = wfrag(wrow_i[0], k + 8 * lq), w1 = wfrag(wrow_i[1], k + 8 * lq);
-    const bf16x8 x0 = *reinterpret_cast<const bf16x8*>(arow0 + k);
-    const bf16x8 x1 = *reinterpret_cast<const bf16x8*>(arow1 + k);
-    acc[0][0] = mfma16x16x32<H>(w0, x0, acc[0][0]);
-    acc[0][1] = mfma16x16x32<H>(w0, x1, acc[0][1]);
-    acc[1][0] = mfma16x16x32<H>(w1, x0, acc[1][0]);
-    acc[1][1] = mfma16x16x32<H>(w1, x1, acc[1][1]);
+    bf16x8 x[RB];
+#pragma unroll
+    for (int b = 0; b < RB; ++b) x[b] = *reinterpret_cast<const bf16x8*>(arow[b] + k);
+#pragma unroll
+    for (int b = 0; b < RB; ++b) {
+      acc[0][b] = mfma16x16x32<H>(w0, x[b], acc[0][b]);
+      acc[1][b] = mfma16x16x32<H>(w1, x[b], acc[1][b]);
+    }
   }
 #pragma unroll
-  for (int a = 0; a < 4; ++a)
+  for (int a = 0; a < 2 * RB; ++a)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) part[wave][4 * a + e][lane] = acc[a >> 1][a & 1][e];
+    for (int e = 0; e < 4; ++e) part[wave][4 * a + e][lane] = acc[a / RB][a % RB][e];
   __syncthreads();
-  if (wave >= 4) return;
-  // wave w < 4 finishes accumulator (cb, rb) = (w / 2, w % 2): 4 consecutive columns of one row
-  const int cb = wave >> 1, rb = wave & 1;
-  const int row = m0 + 16 * rb + l16;
-  const int col = n0 + 16 * cb + 4 * lq;
-  float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  // wave w finishes accumulators a = w, w + NWK, ...: (cb, rb) = (a / RB, a % RB), 4 consecutive
+  // columns of one row per lane
+  const bool vec_ok = (ldc % 4 == 0) && (!(epi.flags & KX_EPI_GATED_RESIDUAL) || epi.ldr % 4 == 0);
+  for (int a = wave; a < 2 * RB; a += NWK) {
+    const int cb = a / RB, rb = a % RB;
+    const int row = m0 + 16 * rb + l16;
+    const int col = n0 + 16 * cb + 4 * lq;
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-  for (int p = 0; p < NWK; ++p)
+    for (int p = 0; p < NWK; ++p)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] += part[p][4 * wave + e][lane];
-  if (row < M && col < N) {
-    const bool vec_ok = (ldc % 4 == 0) && (!(epi.flags & KX_EPI_GATED_RESIDUAL) || epi.ldr % 4 == 0);
-    epilogue_store4<H>(v, row, col, N, epi, C, ldc, vec_ok);
+      for (int e = 0; e < 4; ++e) v[e] += part[p][4 * a + e][lane];
+    if (row < mend && col < N) epilogue_store4<H>(v, row, col, N, epi, C, ldc, vec_ok);
+  }
+}
+
+// Rows per skinny workgroup (see above) and its launch.
+template <int QB, bool H, int RB>
+void launch_skinny_rb(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, QuantW qw, void* c,
+                      int64_t ldc, int m, int n, int k, int r, const Epilogue& epi, hipStream_t s) {
+  const dim3 grid((unsigned)((m + r - 1) / r), (unsigned)((n + 31) / 32));
+  gemm_skinny_kernel<QB, 4, RB, H><<<grid, 256, 0, s>>>(a, lda, w, ldw, qw, c, ldc, m, n, k, r, epi);
+}
+
+template <int QB, bool H>
+void launch_skinny(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, QuantW qw, void* c,
+                   int64_t ldc, int m, int n, int k, const Epilogue& epi, hipStream_t s) {
+  const int r = std::min(std::max((m + 255) / 256, 16), 128);
+  switch ((r + 15) / 16) {
+    case 1: return launch_skinny_rb<QB, H, 1>(a, lda, w, ldw, qw, c, ldc, m, n, k, r, epi, s);
+    case 2: return launch_skinny_rb<QB, H, 2>(a, lda, w, ldw, qw, c, ldc, m, n, k, r, epi, s);
+    case 3: return launch_skinny_rb<QB, H, 3>(a, lda, w, ldw, qw, c, ldc, m, n, k, r, epi, s);
+    case 4: return launch_skinny_rb<QB, H, 4>(a, lda, w, ldw, qw, c, ldc, m, n, k, r, epi, s);
+    case 5:
+    case 6: return launch_skinny_rb<QB, H, 6>(a, lda, w, ldw, qw, c, ldc, m, n, k, r, epi, s);
+    default: return launch_skinny_rb<QB, H, 8>(a, lda, w, ldw, qw, c, ldc, m, n, k, r, epi, s);
   }
 }
 
@@ -1519,8 +1608,7 @@ int dispatch(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, Qua
   const char* legacy = getenv("KX355_GEMM_TILE");
   const bool use_legacy = legacy && *legacy;
   if (n <= 64 && k % 128 == 0 && !use_legacy) {
-    const dim3 grid((unsigned)((m + 31) / 32), (unsigned)((n + 31) / 32));
-    gemm_skinny_kernel<QB, 4, H><<<grid, 256, 0, s>>>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi);
+    launch_skinny<QB, H>(a, lda, w, ldw, qw, c, ldc, (int)m, (int)n, (int)k, epi, s);
     return KX_OK;
   }
   // the direct-to-LDS kernel keeps per-lane 32-bit byte offsets within a 256-row tile
