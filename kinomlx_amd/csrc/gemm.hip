@@ -484,30 +484,25 @@ constexpr int DENSE_BK = 64;
 // 8-bit packed weight rows (32 bytes per stage): chunk swizzle of row r
 __device__ __forceinline__ int qswz(int r) { return (r >> 3) & 1; }
 #define KX_LDS(p) ((__attribute__((address_space(3))) void*)(p))
-// One k16 step's order: each of the next step's NRD fragment reads before an MFMA, then ND DMA
-// issues (address VALU + VMEM) each before an MFMA, then the remaining MFMAs.
-template <int NRD, int NMF, int ND>
-__device__ __forceinline__ void step_schedule() {
-  constexpr int PAIRS = NRD < NMF ? NRD : NMF;
-  constexpr int DMF = ND < NMF - PAIRS ? ND : NMF - PAIRS;
-#pragma unroll
-  for (int q = 0; q < PAIRS; ++q) {
-    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-  }
-  if constexpr (NRD > PAIRS) __builtin_amdgcn_sched_group_barrier(0x100, NRD - PAIRS, 0);
-#pragma unroll
-  for (int q = 0; q < DMF; ++q) {
-    __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-  }
-  if constexpr (ND > DMF) {
-    __builtin_amdgcn_sched_group_barrier(0x002, ND - DMF, 0);
-    __builtin_amdgcn_sched_group_barrier(0x020, ND - DMF, 0);
-  }
-  if constexpr (NMF > PAIRS + DMF) __builtin_amdgcn_sched_group_barrier(0x008, NMF - PAIRS - DMF, 0);
+// Raw buffer resource over `base` (stride 0, 4 GiB range; dword 3 as for every gfx9 raw buffer)
+// and a 16-byte-per-lane buffer load into LDS (M0 + lane * 16) from base + voff + soff: the
+// offsets are one loop-invariant 32-bit lane offset and a scalar K offset, so a DMA issue needs
+// no 64-bit address arithmetic (3 % on the block GEMMs against global_load_lds with per-issue
+// 64-bit VALU adds). The host compilation pass has no buffer builtins; kernels only run on the
+// device.
+#if defined(__HIP_DEVICE_COMPILE__)
+using rsrc_t = __amdgpu_buffer_rsrc_t;
+__device__ __forceinline__ rsrc_t raw_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, -1, 0x00020000);
 }
+__device__ __forceinline__ void buffer_lds16(rsrc_t r, void* lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, KX_LDS(lds), 16, voff, soff, 0, 0);
+}
+#else
+struct rsrc_t {};
+__device__ inline rsrc_t raw_rsrc(const void*) { return {}; }
+__device__ inline void buffer_lds16(rsrc_t, void*, uint32_t, uint32_t) {}
+#endif
 // A workgroup barrier that the compiler may not move memory accesses across.
 #define KX_BARRIER() asm volatile("s_barrier" ::: "memory")
 
@@ -767,13 +762,14 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
       b_base = reinterpret_cast<const char*>(qw.biases) + (int64_t)n0 * sb_row;
     }
   }
+  // dense operands: buffer loads (the tile bases as resources; lane offsets < 2^31, K offsets
+  // < 2^23 by the dispatch's stride limits)
+  const rsrc_t a_rsrc = raw_rsrc(a_base), w_rsrc = raw_rsrc(w_base);
   auto dma = [&](int i, uint8_t* buf, int k0) {
     if (i < A_INST) {
-      __builtin_amdgcn_global_load_lds((const void*)(a_base + (int64_t)k0 * 2 + vo[i]),
-                                       KX_LDS(buf + (wave * A_INST + i) * DRPI * DROW), 16, 0, 0);
+      buffer_lds16(a_rsrc, buf + (wave * A_INST + i) * DRPI * DROW, vo[i], (uint32_t)k0 * 2);
     } else if constexpr (QB == 0) {
-      __builtin_amdgcn_global_load_lds((const void*)(w_base + (int64_t)k0 * 2 + vo[i]),
-                                       KX_LDS(buf + (BM + (wave * W_INST + i - A_INST) * DRPI) * DROW), 16, 0, 0);
+      buffer_lds16(w_rsrc, buf + (BM + (wave * W_INST + i - A_INST) * DRPI) * DROW, vo[i], (uint32_t)k0 * 2);
     } else if (TL && i < A_INST + WQ_INST) {
       __builtin_amdgcn_global_load_lds((const void*)(w_base + (int64_t)(k0 / DBK) * (BN * QROW) + vo[i]),
                                        KX_LDS(buf + BM * DROW + (wave * WQ_INST + i - A_INST) * 1024), 16, 0, 0);
@@ -1028,47 +1024,35 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
         const int b = s & 1;
         __builtin_amdgcn_sched_barrier(0);
         wait_lgkmcnt0();
-        __builtin_amdgcn_sched_barrier(0);
-        if (s + 1 < KS) {
-          load_frags(cur, s + 1, fa[b ^ 1], fw[b ^ 1]);
-        } else {
+        if (s + 1 == KS) {
           // stage kt+1 has landed for this wave and its reads of cur are done; after the barrier
           // this holds for every wave, and nobody reads cur again before it is refilled
           wait_vmcnt<WAITN>();
           KX_BARRIER();
-          load_frags(smem + nxt_i * STAGE, 0, fa[b ^ 1], fw[b ^ 1]);
         }
-#pragma unroll
-        for (int d = 0; d < DPS; ++d)
-          if (s * DPS + d < PER) dma(s * DPS + d, iss, k_iss);
-#pragma unroll
-        for (int i = 0; i < NB; ++i)
-#pragma unroll
-          for (int j = 0; j < MB; ++j)
-            acc[i][j] = mfma32x32x16<H>(fw[b][i], fa[b][j], acc[i][j]);
-        // the next step's fragment reads one per MFMA (a burst of them fills the LDS command
-        // queue and stalls the wave before its MFMAs), then the DMA issues between the
-        // remaining MFMAs
+        __builtin_amdgcn_sched_barrier(0);
+        // after each MFMA, its share of the next step's fragment reads (after the last step:
+        // stage kt+1's first) and of this step's DMA issues, in source order
+        const uint8_t* rbuf = s + 1 < KS ? cur : smem + nxt_i * STAGE;
+        const int rs = s + 1 < KS ? s + 1 : 0;
         constexpr int NRD = MB + NB, NMF = NB * MB;
-        constexpr int PAIRS = NRD < NMF ? NRD : NMF;
-        constexpr int DMF = DPS < NMF - PAIRS ? DPS : NMF - PAIRS;
+        const int d0 = s * DPS, nd = PER - d0 < DPS ? (PER - d0 > 0 ? PER - d0 : 0) : DPS;
 #pragma unroll
-        for (int q = 0; q < PAIRS; ++q) {
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        }
-        if constexpr (NRD > PAIRS) __builtin_amdgcn_sched_group_barrier(0x100, NRD - PAIRS, 0);
+        for (int q = 0; q < NMF; ++q) {
+          const int i = q / MB, j = q % MB;
+          acc[i][j] = mfma32x32x16<H>(fw[b][i], fa[b][j], acc[i][j]);
 #pragma unroll
-        for (int q = 0; q < DMF; ++q) {
-          __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          for (int r = q * NRD / NMF; r < (q + 1) * NRD / NMF; ++r) {
+            if (r < MB) {
+              fa[b ^ 1][r] = *reinterpret_cast<const bf16x8*>(rbuf + a_off[rs][r]);
+            } else {
+              fw[b ^ 1][r - MB] = *reinterpret_cast<const bf16x8*>(rbuf + w_off[rs][r - MB]);
+            }
+          }
+#pragma unroll
+          for (int d = q * nd / NMF; d < (q + 1) * nd / NMF; ++d) dma(d0 + d, iss, k_iss);
+          __builtin_amdgcn_sched_barrier(0);
         }
-        if constexpr (DPS > DMF) {
-          __builtin_amdgcn_sched_group_barrier(0x002, DPS - DMF, 0);
-          __builtin_amdgcn_sched_group_barrier(0x020, DPS - DMF, 0);
-        }
-        if constexpr (NMF > PAIRS + DMF) __builtin_amdgcn_sched_group_barrier(0x008, NMF - PAIRS - DMF, 0);
       }
       cur_i = nxt_i;
     }
@@ -1077,7 +1061,10 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
     // right after the barrier of stage kt's last k16 step (every wave has read that buffer's
     // last fragments by then), the rest during step 0 of stage kt+1; the barrier of stage
     // kt+1's last step waits for all of them. Past the end the last stage is re-read, which
-    // keeps the loop free of branches and the vmcnt arithmetic uniform.
+    // keeps the loop free of branches and the vmcnt arithmetic uniform. Each MFMA is followed by
+    // its share of the fragment reads and DMA issues, in source order (the compiler's own
+    // placement bunched the DMA issues, ~10 VALU / SALU / VMEM instructions each, between two
+    // MFMAs and left the matrix core idle: 5 % on every block shape).
     load_frags(smem, 0, fa[0], fw[0]);
     for (int kt = 0; kt < stages; ++kt) {
       uint8_t* cur = smem + (kt & 1) * STAGE;
@@ -1089,33 +1076,32 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
         const int b = s & 1;
         __builtin_amdgcn_sched_barrier(0);
         wait_lgkmcnt0();
-        __builtin_amdgcn_sched_barrier(0);
-        if (s + 1 < KS) {
-          load_frags(cur, s + 1, fa[b ^ 1], fw[b ^ 1]);
-        } else {
+        if (s + 1 == KS) {
           wait_vmcnt<0>();
           KX_BARRIER();
-          load_frags(oth, 0, fa[b ^ 1], fw[b ^ 1]);
         }
-        constexpr int ND0 = PER - DH1;
-        if (s == 0) {
+        __builtin_amdgcn_sched_barrier(0);
+        // the next step's fragments (after the last step: stage kt+1's first) and this step's
+        // DMA issues, one group after each MFMA, in a fixed order
+        const uint8_t* rbuf = s + 1 < KS ? cur : oth;
+        const int rs = s + 1 < KS ? s + 1 : 0;
+        constexpr int NRD = MB + NB, NMF = NB * MB;
+        const int nd = s == 0 ? PER - DH1 : s + 1 == KS ? DH1 : 0;
+        const int d0 = s == 0 ? DH1 : 0;
+        uint8_t* dbuf = s == 0 ? oth : cur;
+        const int dk = s == 0 ? k1 : k2;
 #pragma unroll
-          for (int d = DH1; d < PER; ++d) dma(d, oth, k1);
-        } else if (s + 1 == KS) {
+        for (int q = 0; q < NMF; ++q) {
+          const int i = q / MB, j = q % MB;
+          acc[i][j] = mfma32x32x16<H>(fw[b][i], fa[b][j], acc[i][j]);
+          if (q < MB) {
+            fa[b ^ 1][q] = *reinterpret_cast<const bf16x8*>(rbuf + a_off[rs][q]);
+          } else if (q < NRD) {
+            fw[b ^ 1][q - MB] = *reinterpret_cast<const bf16x8*>(rbuf + w_off[rs][q - MB]);
+          }
 #pragma unroll
-          for (int d = 0; d < DH1; ++d) dma(d, cur, k2);
-        }
-#pragma unroll
-        for (int i = 0; i < NB; ++i)
-#pragma unroll
-          for (int j = 0; j < MB; ++j)
-            acc[i][j] = mfma32x32x16<H>(fw[b][i], fa[b][j], acc[i][j]);
-        if (s == 0) {
-          step_schedule<MB + NB, NB * MB, ND0>();
-        } else if (s + 1 == KS) {
-          step_schedule<MB + NB, NB * MB, DH1>();
-        } else {
-          step_schedule<MB + NB, NB * MB, 0>();
+          for (int d = q * nd / NMF; d < (q + 1) * nd / NMF; ++d) dma(d0 + d, dbuf, dk);
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
     }
