@@ -1478,6 +1478,124 @@ __global__ __launch_bounds__(NWK * 64) void gemm_skinny_kernel(
   }
 }
 
+// LDS-staged form for bf16 / fp16 weights and K % 256 == 0. The register form's 16-byte operand
+// loads cover four lanes (64 bytes) of a row: every L1 -> L2 request is half a cache line, and the
+// per-CU stream (requests in flight x latency) holds the activation read to ~2.4 TB/s. Here each
+// wave streams its K quarter through a private ring of SKS stages in LDS: per stage its R
+// activation rows and 32 weight rows x 64 K, DMA'd by buffer loads of 8 rows x 128 bytes (one
+// full-line request per row), slots XOR-swizzled by (row >> 1) & 7 so that the 16-row fragment
+// reads are conflict free. A wave only reads stages it copied itself, so the ring needs its own
+// vmcnt waits and no barrier.
+template <int A_I, bool H>
+__global__ __launch_bounds__(256) void gemm_skinny_lds_kernel(
+    const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ W, int64_t ldw,
+    void* __restrict__ C, int64_t ldc, int M, int N, int K, int R, Epilogue epi) {
+  constexpr int SKS = 3;                          // stages per wave ring
+  constexpr int AROWS = A_I * 8;                  // activation rows per stage (R <= AROWS)
+  constexpr int RB = (AROWS + 15) / 16;           // MFMA row blocks; rows past AROWS read the
+                                                  // weight rows that follow (never stored)
+  constexpr int W_I = 4;                          // weight DMA instructions per stage
+  constexpr int STG = (AROWS + 32) * 128;         // bytes per stage
+  constexpr int RING_W = SKS * STG;               // bytes per wave
+  constexpr int PART = 4 * 2 * RB * 4 * 64 * 4;   // partial tiles of the 4 waves
+  constexpr int SMEM = 4 * RING_W > PART ? 4 * RING_W : PART;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l16 = lane & 15, lq = lane >> 4;
+  const int m0 = blockIdx.x * R, n0 = blockIdx.y * 32;
+  const int mend = min(m0 + R, M);
+  uint8_t* ring = smem + wave * RING_W;
+  // DMA lanes: row lane / 8 of the instruction's 8, 16-byte slot lane % 8 (global chunk slot ^ swz)
+  const int r8 = lane >> 3, slot = lane & 7;
+  const int kq = K / 4, kbeg = wave * kq, nst = kq / 64;
+  uint32_t av[A_I], wv[W_I];
+#pragma unroll
+  for (int i = 0; i < A_I; ++i) {
+    const int r = 8 * i + r8;
+    av[i] = (uint32_t)(((int64_t)(min(m0 + r, mend - 1) - m0) * lda + kbeg + 8 * (slot ^ ((r >> 1) & 7))) * 2);
+  }
+#pragma unroll
+  for (int i = 0; i < W_I; ++i) {
+    const int r = 8 * i + r8;
+    wv[i] = (uint32_t)(((int64_t)(min(n0 + r, N - 1) - n0) * ldw + kbeg + 8 * (slot ^ ((r >> 1) & 7))) * 2);
+  }
+  const rsrc_t a_rsrc = raw_rsrc(A + (int64_t)m0 * lda), w_rsrc = raw_rsrc(W + (int64_t)n0 * ldw);
+  auto issue = [&](int st) {  // stage st of this wave's K quarter (clamped: re-reads the last)
+    uint8_t* buf = ring + (st % SKS) * STG;
+    const uint32_t ko = (uint32_t)(min(st, nst - 1) * 64 * 2);
+#pragma unroll
+    for (int i = 0; i < A_I; ++i) buffer_lds16(a_rsrc, buf + i * 1024, av[i], ko);
+#pragma unroll
+    for (int i = 0; i < W_I; ++i) buffer_lds16(w_rsrc, buf + AROWS * 128 + i * 1024, wv[i], ko);
+  };
+  // fragment offsets: row r, 16-byte chunk c = 4 h + lq of k32 half h
+  int fo[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) fo[h] = l16 * 128 + (((4 * h + lq) ^ ((l16 >> 1) & 7)) << 4);
+  f32x4 acc[2][RB];
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[cb][rb][e] = 0.0f;
+#pragma unroll
+  for (int st = 0; st < SKS - 1; ++st) issue(st);
+  for (int st = 0; st < nst; ++st) {
+    // stage st landed (stage st + 1 may still be in flight)
+    wait_vmcnt<(SKS - 2) * (A_I + W_I)>();
+    const uint8_t* buf = ring + (st % SKS) * STG;
+    bf16x8 wf[2][2], xf[2][RB];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      // 16-row blocks are 2 KB apart; the swizzle depends on the row within its block only
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb)
+        wf[h][cb] = *reinterpret_cast<const bf16x8*>(buf + AROWS * 128 + cb * 2048 + fo[h]);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) xf[h][rb] = *reinterpret_cast<const bf16x8*>(buf + rb * 2048 + fo[h]);
+    }
+    wait_lgkmcnt0();
+    // the slot of stage st + SKS - 1 is stage st - 1's: read out one iteration ago
+    issue(st + SKS - 1);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        acc[0][rb] = mfma16x16x32<H>(wf[h][0], xf[h][rb], acc[0][rb]);
+        acc[1][rb] = mfma16x16x32<H>(wf[h][1], xf[h][rb], acc[1][rb]);
+      }
+  }
+  wait_vmcnt<0>();
+  __syncthreads();
+  float* part = reinterpret_cast<float*>(smem);  // [wave][2 RB * 4][64]
+#pragma unroll
+  for (int a = 0; a < 2 * RB; ++a)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) part[(wave * 2 * RB * 4 + 4 * a + e) * 64 + lane] = acc[a / RB][a % RB][e];
+  __syncthreads();
+  const bool vec_ok = (ldc % 4 == 0) && (!(epi.flags & KX_EPI_GATED_RESIDUAL) || epi.ldr % 4 == 0);
+  for (int a = wave; a < 2 * RB; a += 4) {
+    const int cb = a / RB, rb = a % RB;
+    const int row = m0 + 16 * rb + l16;
+    const int col = n0 + 16 * cb + 4 * lq;
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] += part[(p * 2 * RB * 4 + 4 * a + e) * 64 + lane];
+    if (row < mend && col < N) epilogue_store4<H>(v, row, col, N, epi, C, ldc, vec_ok);
+  }
+}
+
+template <bool H, int AI>
+void launch_skinny_lds_ai(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, void* c, int64_t ldc,
+                          int m, int n, int k, int r, const Epilogue& epi, hipStream_t s) {
+  const dim3 grid((unsigned)((m + r - 1) / r), (unsigned)((n + 31) / 32));
+  gemm_skinny_lds_kernel<AI, H><<<grid, 256, 0, s>>>(a, lda, w, ldw, c, ldc, m, n, k, r, epi);
+}
+
 // Rows per skinny workgroup (see above) and its launch.
 template <int QB, bool H, int RB>
 void launch_skinny_rb(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, QuantW qw, void* c,
@@ -1489,6 +1607,21 @@ void launch_skinny_rb(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t
 template <int QB, bool H>
 void launch_skinny(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, QuantW qw, void* c,
                    int64_t ldc, int m, int n, int k, const Epilogue& epi, hipStream_t s) {
+  if (QB == 0 && k % 256 == 0 && lda <= (1 << 22) && ldw <= (1 << 22)) {
+    // rows per workgroup: the rows spread over the 256 CUs in the fewest rounds of at most 64
+    // rows (at least 16)
+    const int per_cu = (m + 255) / 256, rounds = (per_cu + 63) / 64;
+    const int r = std::max((m + 256 * rounds - 1) / (256 * rounds), 16);
+    switch ((r + 7) / 8) {
+      case 2: return launch_skinny_lds_ai<H, 2>(a, lda, w, ldw, c, ldc, m, n, k, r, epi, s);
+      case 3: return launch_skinny_lds_ai<H, 3>(a, lda, w, ldw, c, ldc, m, n, k, r, epi, s);
+      case 4: return launch_skinny_lds_ai<H, 4>(a, lda, w, ldw, c, ldc, m, n, k, r, epi, s);
+      case 5: return launch_skinny_lds_ai<H, 5>(a, lda, w, ldw, c, ldc, m, n, k, r, epi, s);
+      case 6: return launch_skinny_lds_ai<H, 6>(a, lda, w, ldw, c, ldc, m, n, k, r, epi, s);
+      case 7: return launch_skinny_lds_ai<H, 7>(a, lda, w, ldw, c, ldc, m, n, k, r, epi, s);
+      default: return launch_skinny_lds_ai<H, 8>(a, lda, w, ldw, c, ldc, m, n, k, r, epi, s);
+    }
+  }
   const int r = std::min(std::max((m + 255) / 256, 16), 128);
   switch ((r + 15) / 16) {
     case 1: return launch_skinny_rb<QB, H, 1>(a, lda, w, ldw, qw, c, ldc, m, n, k, r, epi, s);

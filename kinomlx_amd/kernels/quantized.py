@@ -151,13 +151,23 @@ def quantize(weight: torch.Tensor, group_size: int = DEFAULT_GROUP_SIZE, bits: i
     return pack(codes, bits), scale_bf.contiguous(), bias_bf.contiguous()
 
 
+def _out_buffer(out: torch.Tensor | None, n: int, k: int, device) -> torch.Tensor:
+    if out is None:
+        return torch.empty((n, k), dtype=torch.bfloat16, device=device)
+    if out.shape != (n, k) or out.dtype != torch.bfloat16 or not out.is_contiguous():
+        raise ValueError(f"dequantize: out must be a contiguous bf16 ({n}, {k}) tensor")
+    return out
+
+
 def dequantize(words: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, *,
-               group_size: int = DEFAULT_GROUP_SIZE, bits: int = DEFAULT_BITS) -> torch.Tensor:
-    """Packed affine weight -> bf16 ``(out, in)`` through the kernel's own dequantization."""
+               group_size: int = DEFAULT_GROUP_SIZE, bits: int = DEFAULT_BITS,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """Packed affine weight -> bf16 ``(out, in)`` through the kernel's own dequantization (into
+    ``out`` when given)."""
     _check_format(group_size, bits)
     n = int(words.shape[0])
     k = int(words.shape[1]) * 32 // bits
-    out = torch.empty((n, k), dtype=torch.bfloat16, device=words.device)
+    out = _out_buffer(out, n, k, words.device)
     _lib.launch_dequant(words.contiguous(), scales.contiguous(), biases.contiguous(), out, n=n, k=k,
                         group_size=group_size, bits=bits)
     return out
@@ -193,12 +203,13 @@ def quantize_mxfp8(weight: torch.Tensor, group_size: int = 32) -> tuple[torch.Te
     return codes.contiguous().view(torch.int32), (x + 127).to(torch.uint8).contiguous()
 
 
-def dequantize_mxfp8(words: torch.Tensor, scales: torch.Tensor, *, transposed: bool = False) -> torch.Tensor:
+def dequantize_mxfp8(words: torch.Tensor, scales: torch.Tensor, *, transposed: bool = False,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
     """mxfp8 weight -> bf16 ``(out, in)``, exactly: ``words`` ``(out, in / 4)``, or with
     ``transposed`` the pretransposed ``(in, out / 4)`` packing of ``weight.T``."""
     rows, cols = int(words.shape[0]), int(words.shape[1]) * 4
     n, k = (cols, rows) if transposed else (rows, cols)
-    out = torch.empty((n, k), dtype=torch.bfloat16, device=words.device)
+    out = _out_buffer(out, n, k, words.device)
     _lib.launch_dequant_mxfp8(words.contiguous(), scales.contiguous(), out, n=n, k=k, transposed=transposed)
     return out
 
@@ -248,13 +259,14 @@ def quantize_fp4(weight: torch.Tensor, mode: str = "mxfp4") -> tuple[torch.Tenso
     return pack(codes.reshape(n, k), 4), sbytes.contiguous()
 
 
-def dequantize_fp4(words: torch.Tensor, scales: torch.Tensor, mode: str = "mxfp4") -> torch.Tensor:
+def dequantize_fp4(words: torch.Tensor, scales: torch.Tensor, mode: str = "mxfp4", *,
+                   out: torch.Tensor | None = None) -> torch.Tensor:
     """FP4 weight -> bf16 ``(out, in)``, exactly (``kx_dequant_fp4_bf16``)."""
     if mode not in FP4_MODES:
         raise ValueError(f"dequantize_fp4 takes mode mxfp4 or nvfp4, got {mode}")
     group = _DEFAULTS[mode][0]
     n, k = int(words.shape[0]), int(words.shape[1]) * 8
-    out = torch.empty((n, k), dtype=torch.bfloat16, device=words.device)
+    out = _out_buffer(out, n, k, words.device)
     _lib.launch_dequant_fp4(words.contiguous(), scales.contiguous(), out, n=n, k=k, group_size=group,
                             scale_kind=_lib.KX_FP4_NV if mode == "nvfp4" else _lib.KX_FP4_MX)
     return out
@@ -331,7 +343,8 @@ def quantized_matmul(
 
         if biases is not None or not transpose:
             raise ValueError(f"{mode} weights carry no biases and take the (out, in) packing")
-        dense = dequantize_fp4(weight, scales, mode)
+        n, k = int(weight.shape[0]), int(weight.shape[1]) * 8
+        dense = dequantize_fp4(weight, scales, mode, out=dequant_workspace(n, k, value.device))
         return fused_linear(value, dense, None if bias is None else bias.to(torch.bfloat16), activation=activation,
                             residual=residual, gate=gate, out=out, out_dtype=out_dtype)
     if mode == "mxfp8":
@@ -340,7 +353,8 @@ def quantized_matmul(
         if not transpose:
             from .mpp_linear import fused_linear
 
-            dense = dequantize_mxfp8(weight, scales, transposed=True)
+            n, k = int(weight.shape[1]) * 4, int(weight.shape[0])
+            dense = dequantize_mxfp8(weight, scales, transposed=True, out=dequant_workspace(n, k, value.device))
             return fused_linear(value, dense, None if bias is None else bias.to(torch.bfloat16), activation=activation,
                                 residual=residual, gate=gate, out=out, out_dtype=out_dtype)
         n = int(weight.shape[0])
@@ -366,6 +380,26 @@ def quantized_matmul(
         bias=bias, flags=flags, resid=resid2, gate=gate32,
     )
     return out
+
+
+# One dequantization buffer per (device, stream), grown to the largest quantized weight called on
+# it and kept: each GPU call of a quantized layer writes its bf16 weight there and the dense GEMM
+# reads it, so a block's calls reuse one allocation (134 MB for the LTX-2 feed-forward weights)
+# instead of taking a new one from the caching allocator per call. Calls on one stream run in
+# order, so a call's dequantization never overwrites a weight that an earlier GEMM still reads.
+_WORKSPACE: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def dequant_workspace(n: int, k: int, device: torch.device) -> torch.Tensor:
+    """A bf16 ``(n, k)`` view of the current stream's dequantization buffer on ``device``."""
+    device = torch.device(device)
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    key = (index, torch.cuda.current_stream(index).cuda_stream)
+    buf = _WORKSPACE.get(key)
+    if buf is None or buf.numel() < n * k:
+        buf = torch.empty(n * k, dtype=torch.bfloat16, device=torch.device("cuda", index))
+        _WORKSPACE[key] = buf
+    return buf[: n * k].view(n, k)
 
 
 class QuantizedLinear:
@@ -400,13 +434,14 @@ class QuantizedLinear:
         if weight.is_cuda and int(weight.shape[0]) <= 64:
             self._dense = self.dequantized()
 
-    def dequantized(self) -> torch.Tensor:
-        """The bf16 ``(out, in)`` weight, exactly (a new buffer)."""
+    def dequantized(self, out: torch.Tensor | None = None) -> torch.Tensor:
+        """The bf16 ``(out, in)`` weight, exactly (a new buffer, or ``out``)."""
         if self.mode == "mxfp8":
-            return dequantize_mxfp8(self.weight, self.scales)
+            return dequantize_mxfp8(self.weight, self.scales, out=out)
         if self.mode in FP4_MODES:
-            return dequantize_fp4(self.weight, self.scales, self.mode)
-        return dequantize(self.weight, self.scales, self.biases, group_size=self.group_size, bits=self.bits)
+            return dequantize_fp4(self.weight, self.scales, self.mode, out=out)
+        return dequantize(self.weight, self.scales, self.biases, group_size=self.group_size, bits=self.bits,
+                          out=out)
 
     @classmethod
     def from_linear(cls, weight: torch.Tensor, bias: torch.Tensor | None = None, *,
@@ -440,7 +475,9 @@ class QuantizedLinear:
 
             if int(value.shape[-1]) != self.in_features:
                 raise ValueError(f"input width {value.shape[-1]} does not match the packed width {self.in_features}")
-            weight = self._dense if self._dense is not None else self.dequantized()
+            weight = self._dense
+            if weight is None:
+                weight = self.dequantized(dequant_workspace(self.out_features, self.in_features, value.device))
             bias = None if self.bias is None else self.bias.to(torch.bfloat16)
             return fused_linear(value, weight, bias, activation=activation, residual=residual, gate=gate,
                                 out=out, out_dtype=out_dtype)
@@ -504,6 +541,7 @@ __all__ = [
     "KERNEL_MODES",
     "PretransposedQuantizedLinear",
     "QuantizedLinear",
+    "dequant_workspace",
     "dequantize",
     "dequantize_fp4",
     "dequantize_mxfp8",

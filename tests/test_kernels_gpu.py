@@ -741,6 +741,32 @@ def test_quantized_linear_matches_oracle(device, monkeypatch, tile, bits, m, n, 
     assert max_abs(got, dense) <= 2.0**-7 * np.abs(dense).max()
 
 
+def test_quantized_layers_share_one_dequantization_buffer(device):
+    """Consecutive quantized layers on one stream dequantize into one buffer (grown to the largest
+    weight, then reused), and each call equals the dense kernel on that layer's own dequantized
+    weight, also after a larger layer overwrote the buffer."""
+    r = _rng(77)
+    layers, xs = [], []
+    for n, k in ((256, 512), (640, 1024), (128, 256)):
+        w = oracle.to_bf16((r.standard_normal((n, k)) * 0.02).astype(F32))
+        words, scales, biases = oracle.quantize_affine(w, 64, 4)
+        layers.append(quantized.QuantizedLinear(torch.from_numpy(words.view(np.int32)).to(device), _bf(scales, device),
+                                                _bf(biases, device), group_size=64, bits=4))
+        xs.append(_bf(oracle.to_bf16(r.standard_normal((96, k)).astype(F32)), device))
+    quantized._WORKSPACE.clear()
+    outs = [layer(x) for layer, x in zip(layers, xs)]
+    torch.cuda.synchronize()
+    assert len(quantized._WORKSPACE) == 1
+    buf = next(iter(quantized._WORKSPACE.values()))
+    assert buf.numel() == 640 * 1024  # grown once, to the largest weight
+    ptr = buf.data_ptr()
+    again = layers[0](xs[0])
+    assert next(iter(quantized._WORKSPACE.values())).data_ptr() == ptr
+    for layer, x, got in zip(layers, xs, outs):
+        assert torch.equal(got, mpp_linear.fused_linear(x, layer.dequantized(), None))
+    assert torch.equal(again, outs[0])
+
+
 @pytest.mark.parametrize("tile", ["0", "1"])
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize(("m", "n", "k"), [(512, 512, 512), (300, 520, 1024), (200, 256, 128), (1000, 132, 384)])
@@ -781,11 +807,15 @@ def test_quantized_linear_dequantizes_in_lds(device, monkeypatch, tile, bits, m,
         assert np.all(np.abs(got - full) <= 1e-5 * np.abs(full) + 2e-5 * np.abs(full).max())
 
 
-@pytest.mark.parametrize(("m", "n", "k"), [(1000, 32, 1024), (37, 64, 256), (300, 40, 512)])
+@pytest.mark.parametrize(("m", "n", "k"), [(1000, 32, 1024), (37, 64, 256), (300, 40, 512), (9216, 32, 4096),
+                                           (20000, 64, 768), (70000, 32, 256), (500, 32, 640)])
 @pytest.mark.parametrize("bits", [None, 4, 8])
 @pytest.mark.parametrize("epilogue", ["sigmoid2", "gated_f32"])
 def test_skinny_linear_matches_oracle(device, m, n, k, bits, epilogue):
-    """N <= 64 (the gate-logit projections) takes the split-K skinny kernel, dense and quantized."""
+    """N <= 64 (the gate-logit projections) takes the skinny kernels, dense and quantized: the
+    LDS-staged one for K % 256 == 0 at every rows-per-workgroup form (16 rows; 36 rows = five 8-row
+    DMA groups at the block's 9216 rows; 40 and 55 rows in two and five rounds), the register one
+    for K % 256 != 0 (640)."""
     r = _rng(m + n + k)
     x = oracle.to_bf16((r.standard_normal((m, k)) * 0.5).astype(F32))
     w = oracle.to_bf16((r.standard_normal((n, k)) * k ** -0.5).astype(F32))
