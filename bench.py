@@ -429,6 +429,45 @@ def profile_summary(root: str) -> int:
               f"{f(gbs, '{:.0f}')} | {f(gbs / PEAK_HBM_GBS if gbs else None, '{:.2f}')} | "
               f"{f(fm, '{:.1f}')} | {f(wm, '{:.1f}')} |")
     print(f"\nSum of the block's kernels: {total_us / 1e3:.3f} ms ({len(dur[0])} blocks traced).")
+
+    # further counter passes (root/ctr_<name>, each a --pmc run of the same command): the mean per
+    # launch of each counter, for the launches that carry FLOPs (GEMMs and attention); busy and
+    # stall counters that sum the CUs' cycles are also given per CU-cycle (GRBM_GUI_ACTIVE / 8 XCDs
+    # x 256 CUs), SQ_VALU_MFMA_BUSY_CYCLES per SIMD-cycle, and TCP_TCC_READ_REQ_LATENCY per request
+    per_cu = {"TA_TA_BUSY", "TD_TD_BUSY", "TD_TC_STALL", "TA_ADDR_STALLED_BY_TC_CYCLES", "TCP_PENDING_STALL_CYCLES",
+              "TCP_UTCL1_STALL_INFLIGHT_MAX", "SQ_LDS_BANK_CONFLICT"}
+    for sub in sorted(d for d in os.listdir(root) if d.startswith("ctr_")):
+        names: list[str] = []
+        rows = kx_rows(sub, "*counter_collection.csv") or []
+        for r in rows:
+            if r["Counter_Name"] not in names:
+                names.append(r["Counter_Name"])
+        vals = counters(sub, names)
+        if not vals or not vals.get(names[0]):
+            continue
+        pos = {c: per_position(v) for c, v in vals.items()}
+        shown = [c for c in names if c != "GRBM_GUI_ACTIVE"]
+        print(f"\nCounter pass `{sub[4:]}` (mean per launch):\n")
+        print("| # | launch | " + " | ".join(shown) + " |")
+        print("|---|---|" + "---|" * len(shown))
+        for i, entry in enumerate(launches):
+            if not entry["flops"]:
+                continue
+            g = groups[i]
+            gui = sum(statistics.mean(pos["GRBM_GUI_ACTIVE"][j]) for j in g) / 8 if "GRBM_GUI_ACTIVE" in pos else 0
+            cells = []
+            for c in shown:
+                v = sum(statistics.mean(pos[c][j]) for j in g)
+                if c in per_cu and gui:
+                    cells.append(f"{v / (256 * gui):.3f}/CU-cyc")
+                elif c == "SQ_VALU_MFMA_BUSY_CYCLES" and gui:
+                    cells.append(f"{v / (1024 * gui):.3f}/SIMD-cyc")
+                elif c == "TCP_TCC_READ_REQ_LATENCY" and "TCP_TCC_READ_REQ" in pos:
+                    req = sum(statistics.mean(pos["TCP_TCC_READ_REQ"][j]) for j in g)
+                    cells.append(f"{v / req:.0f} cyc/req" if req else "-")
+                else:
+                    cells.append(f"{v:.4g}")
+            print(f"| {i} | {entry['label']} | " + " | ".join(cells) + " |")
     return 0
 
 
