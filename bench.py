@@ -143,6 +143,9 @@ def main() -> int:
                         help="write one block's launch sequence (labels, FLOPs, bytes) as JSON to this path")
     parser.add_argument("--profile-summary", type=str, default="", metavar="DIR",
                         help="only summarize the rocprofv3 runs under DIR (see profiles/) as a markdown table")
+    parser.add_argument("--kernel-table", type=str, default="", metavar="DIR",
+                        help="only print, from the rocprofv3 --kernel-trace run under DIR (of --steps S timed "
+                             "steps after --warmup W), this library's kernels per instantiation as a markdown table")
     parser.add_argument("--compare-rope-fold", action="store_true",
                         help="only time LTX's Q/K norm + RoPE folded into the QKV GEMM epilogue against the "
                              "separate pass, and exit")
@@ -152,6 +155,8 @@ def main() -> int:
     args = parser.parse_args()
     if args.profile_summary:
         return profile_summary(args.profile_summary)
+    if args.kernel_table:
+        return kernel_table(args.kernel_table, args.steps + args.warmup)
     if args.calibrate_copy:
         import torch
 
@@ -468,6 +473,39 @@ def profile_summary(root: str) -> int:
                 else:
                     cells.append(f"{v:.4g}")
             print(f"| {i} | {entry['label']} | " + " | ".join(cells) + " |")
+    return 0
+
+
+def kernel_table(root: str, steps: int) -> int:
+    """Per kernel instantiation (name with template arguments, workgroups over both grid axes):
+    calls, calls per step, mean / min / max duration and ms per step over the ``steps`` steps of a
+    rocprofv3 kernel trace; this library's kernels only."""
+    import csv
+    import glob
+    import re
+
+    files = glob.glob(os.path.join(root, "**", "*kernel_trace.csv"), recursive=True)
+    if not files:
+        print(f"no kernel trace under {root}", file=sys.stderr)
+        return 1
+    agg: dict[tuple[str, int], list[float]] = defaultdict(list)
+    with open(files[0]) as fh:
+        for r in csv.DictReader(fh):
+            name = r["Kernel_Name"]
+            if "kx::" not in name:
+                continue
+            name = name.replace("kx::(anonymous namespace)::", "")
+            m = re.match(r"void ([\w:]+(<[^()]*>)?)\(", name)
+            short = m.group(1) if m else name[:70]
+            wg = (int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"])) // (int(r["Workgroup_Size_X"]) * int(r["Workgroup_Size_Y"]))
+            agg[(short, wg)].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    total = sum(sum(v) for v in agg.values())
+    print("| kernel | workgroups | calls | calls/step | avg us | min us | max us | ms/step | share |")
+    print("|---|---|---|---|---|---|---|---|---|")
+    for (k, wg), v in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
+        print(f"| `{k}` | {wg} | {len(v)} | {len(v) // steps} | {sum(v) / len(v):.1f} | {min(v):.1f} | {max(v):.1f} | "
+              f"{sum(v) / steps / 1e3:.3f} | {100 * sum(v) / total:.1f}% |")
+    print(f"\nSum of this library's kernels: {total / steps / 1e3:.1f} ms per step.")
     return 0
 
 
