@@ -454,6 +454,32 @@ __global__ __launch_bounds__(256) void dequant_mx8_t_kernel(const uint32_t* __re
   }
 }
 
+// Tile of workgroup `bid` for the direct-to-LDS kernel, as (tile row, tile column). The 256
+// workgroups of a round run at once, 32 per XCD, and the XCDs' L2s are separate. When the tile
+// columns divide a round (8, 16, 32 or 64 of them) and the rows fill whole rounds, each round
+// covers R = 256 / tiles_n whole tile rows, and each XCD an a x b block of them with the fewest
+// operand panels (a + b = 12 for 32 tiles): every activation panel is then read in one round
+// only, so a product whose operands exceed the last-level cache re-reads them from HBM once per
+// round rather than once per round and XCD pair (the 9216 x 4096 x 16384 down projection: mean
+// L1 -> L2 request latency 688 -> 505 cycles, 2.5 % faster). Otherwise: XCD-contiguous tiles,
+// grouped by 8 tile rows.
+__device__ __forceinline__ int2 lds_tile_of(int bid, int tiles_m, int tiles_n) {
+  const int rows = 256 / tiles_n;
+  if ((tiles_n == 8 || tiles_n == 16 || tiles_n == 32 || tiles_n == 64) && tiles_m % rows == 0) {
+    // XCD x: block (x % ra, x / ra) of an ra x cb grid over the round, ra * cb = 8
+    const int ra = tiles_n >= 32 ? 1 : tiles_n == 16 ? 2 : 8, cb = 8 / ra;
+    const int a = rows / ra, b = tiles_n / cb;  // block rows x columns, a * b = 32
+    const int x = bid % 8, i = bid / 8, r = i / 32, j = i % 32;
+    return make_int2(r * rows + (x % ra) * a + j % a, (x / ra) * b + j / a);
+  }
+  const int t = xcd_remap(bid, tiles_m * tiles_n);
+  constexpr int GM = 8;
+  const int group_width = GM * tiles_n;
+  const int first_m = (t / group_width) * GM;
+  const int gsz = min(tiles_m - first_m, GM);
+  return make_int2(first_m + (t % group_width) % gsz, (t % group_width) / gsz);
+}
+
 // ---- direct-to-LDS pipelined kernel (dense: K % 64 == 0; quantized: K % 128 == 0) ------------
 //
 // Operand tiles go from global memory straight into LDS with global_load_lds_dwordx4 (no VGPR
@@ -690,15 +716,10 @@ __global__ __launch_bounds__(256) void gemm_lds_kernel(
     C = static_cast<float*>(C) + y * (int64_t)M * ldc;
   }
 
-  // tile coordinates: XCD-contiguous, then grouped by 8 tile rows for L2 reuse
+  // tile coordinates (see lds_tile_of)
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-  const int t = xcd_remap(blockIdx.x, tiles_m * tiles_n);
-  constexpr int GM = 8;
-  const int group_width = GM * tiles_n;
-  const int first_m = (t / group_width) * GM;
-  const int gsz = min(tiles_m - first_m, GM);
-  const int m0 = (first_m + (t % group_width) % gsz) * BM;
-  const int n0 = ((t % group_width) / gsz) * BN;
+  const int2 tile = lds_tile_of(blockIdx.x, tiles_m, tiles_n);
+  const int m0 = tile.x * BM, n0 = tile.y * BN;
 
   // per-lane DMA sources: lane -> row lane / DCPR of the instruction's rows, slot lane % DCPR;
   // rows past the end re-read the last row (in bounds; their results are never stored)

@@ -279,9 +279,11 @@ def _gemm_close(got, ref):
 
 
 @pytest.mark.parametrize("tile", ["auto", "0", "1", "2", "3", "4"])
-@pytest.mark.parametrize(("m", "n", "k"), [(1056, 1040, 1024), (300, 96, 64), (7, 32, 200)])
+@pytest.mark.parametrize(("m", "n", "k"), [(1056, 1040, 1024), (300, 96, 64), (7, 32, 200), (600, 520, 96)])
 def test_linear_matches_oracle_for_every_tile(device, monkeypatch, tile, m, n, k):
-    """Ragged against every tile shape (tests/kernels/test_mpp_linear.py:8-43 shape)."""
+    """Ragged against every tile shape (tests/kernels/test_mpp_linear.py:8-43 shape); K = 96 (a
+    multiple of 32 but not of the direct-to-LDS kernel's 64-wide stages) takes the register-staged
+    kernel on the auto path too."""
     if tile != "auto":
         monkeypatch.setenv("KX355_GEMM_TILE", tile)
     x, w, b = _linear_case(m, n, k, m + n + k, device)
