@@ -466,12 +466,11 @@ def launch_gemm(a, w, out, *, bias=None, flags: int = 0, resid=None, gate=None) 
     # would index its rows from zero
     if plan is not None and (gate is None or stride == 0) and a.data_ptr() % 16 == 0 \
             and w.data_ptr() % 16 == 0 and lda <= (1 << 22) and ldw <= (1 << 22):
-        # whole rounds of 256x256 tiles over the first rows, the tail rows as K slices filling one round
+        # whole rounds of 256x256 tiles over the first rows, the tail rows as K slices filling one
+        # round. The tail goes first: its rows are the input's last, the ones its producer wrote
+        # most recently (the likeliest to be in the memory-side cache), and its pass leaves the
+        # weight in that cache for the head (the down projection's head 923 -> 907 us).
         rows, tail_splits = plan
-        _call(
-            f"kx_gemm_{sfx}", _ptr(a), lda, _ptr(w), ldw, _ptr(bias), _ptr(out), ldc, rows, n, k, flags,
-            _ptr(resid), ldr, _ptr(gate), div, stride, _stream(),
-        )
         tail = m - rows
         work = torch.empty(tail_splits * tail * n, dtype=torch.float32, device=a.device)
         # row ``rows`` of each operand from its flattened row stride (the leading axes of an N-D
@@ -482,6 +481,10 @@ def launch_gemm(a, w, out, *, bias=None, flags: int = 0, resid=None, gate=None) 
         _call(
             f"kx_gemm_splitk_{sfx}", a_tail, lda, _ptr(w), ldw, _ptr(bias), out_tail, ldc, tail, n, k,
             flags, resid_tail, ldr, _ptr(gate), div, stride, _ptr(work), work.numel() * 4, tail_splits, _stream(),
+        )
+        _call(
+            f"kx_gemm_{sfx}", _ptr(a), lda, _ptr(w), ldw, _ptr(bias), _ptr(out), ldc, rows, n, k, flags,
+            _ptr(resid), ldr, _ptr(gate), div, stride, _stream(),
         )
         return
     splits = splitk_splits(m, n, k)

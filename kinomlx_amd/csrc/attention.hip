@@ -6,7 +6,7 @@
 // waves the 1152 workgroups took 4.5 rounds: 1.59 -> 1.44 ms), and each LDS K/V tile serves 384
 // queries.
 //
-// K and V tiles of 64 keys go from global memory straight into LDS with global_load_lds_dwordx4
+// K and V tiles of 64 keys go from global memory straight into LDS with buffer_load_dwordx4 ... lds
 // (no VGPR staging) through a ring of 4 stages. Waves 0-7 each issue 1/8 of a stage's DMA
 // instructions; one workgroup barrier per tile makes a tile visible and frees an older buffer.
 // At D = 128 without a score bias the key loop is software-pipelined over 32-key blocks (the next
@@ -28,7 +28,9 @@
 // fragment reads hit distinct banks, for V so that each transposing read (4 keys x 4 chunks) does.
 //
 // Softmax: fp32, in the exp2 domain with the scale * log2 e folded into one FMA per score. The
-// running max is lazy: it moves (and O, l are rescaled) only when a score exceeds it by more than
+// row sum adds the rounded P pairwise (v_dot2 with (1, 1)), the values the P V product uses; in
+// the pipelined form the two lane halves exchange their max by v_permlane32_swap. The running max
+// is lazy: it moves (and O, l are rescaled) only when a score exceeds it by more than
 // 2^8 in the exp2 domain, so p stays below 256 (exact in fp32 and bf16) and rescales are rare.
 // Keys past the end are masked to -inf; queries past the end run on a clamped row and are not
 // stored. An optional per-(query, head) gate multiplies the output before the single bf16 rounding.
@@ -64,15 +66,26 @@ __device__ __forceinline__ void wait_vmcnt() {
 template <int D> __device__ __forceinline__ int swz_k(int r) { return D == 128 ? (r & 15) : ((r >> 1) & 7); }
 template <int D> __device__ __forceinline__ int swz_v(int r) { return D == 128 ? 4 * (r & 3) : 4 * ((r >> 1) & 1); }
 
-// One 16-byte-per-lane global -> LDS copy (global_load_lds_dwordx4; M0 holds the wave's LDS
+// A raw buffer resource over 4 GiB from a 64-bit base: the copies below address their source as
+// this scalar base plus a 32-bit lane offset plus a 32-bit scalar offset, so a wave's copies of a
+// tile need one vector register and no address arithmetic.
+typedef __attribute__((ext_vector_type(4))) int i32x4;
+__device__ __forceinline__ i32x4 dma_rsrc(const void* base) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  return (i32x4){(int)(uint32_t)a, (int)(uint32_t)(a >> 32), -1, 0x00020000};
+}
+
+// One 16-byte-per-lane buffer -> LDS copy (buffer_load_dwordx4 ... lds; M0 holds the wave's LDS
 // address). Written as inline assembly so that the compiler's wait-count pass does not see an LDS
-// write pending on vmcnt: as the builtin, every transposing LDS read after it got a vmcnt(0) wait
+// write pending on vmcnt: as a builtin, every transposing LDS read after it got a vmcnt(0) wait
 // for the copies just issued (the pass cannot tell the ring's buffers apart), which stalled the
 // issuing waves for a whole memory round trip per tile. The kernel orders the copies itself:
 // wait_vmcnt for a tile's copies, then the workgroup barrier, before any wave reads the tile.
-__device__ __forceinline__ void dma16(const void* src, const void* lds) {
+__device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t voff, uint32_t soff, const void* lds) {
   const uint32_t m0 = (uint32_t)(uintptr_t)KX_LDS(lds);
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc), "s"(soff),
+               "{m0}"(m0)
+               : "memory");
 }
 
 __device__ __forceinline__ bf16x8 read_vt(const uint8_t* p, int second) {
@@ -81,6 +94,27 @@ __device__ __forceinline__ bf16x8 read_vt(const uint8_t* p, int second) {
   // whole-word casts: the operand is the two 8-byte results back to back
   const uint2 lo2 = __builtin_bit_cast(uint2, lo), hi2 = __builtin_bit_cast(uint2, hi);
   return __builtin_bit_cast(bf16x8, make_uint4(lo2.x, lo2.y, hi2.x, hi2.y));
+}
+
+// The larger of the values a lane and lane ^ 32 hold, by one v_permlane32_swap (no LDS round
+// trip). The scores are finite or -inf, so the max needs no NaN canonicalization.
+__device__ __forceinline__ float half_max(float x) {
+  const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(__uint_as_float(sw[0])), "v"(__uint_as_float(sw[1])));
+  return r;
+}
+
+// acc + the two 16-bit values of element pair j of v (v_dot2 with (1, 1)): the row sum of P taken
+// from the rounded values the P V product uses.
+template <bool H>
+__device__ __forceinline__ float add_pair(bf16x8 v, int j, float acc) {
+  const uint32_t w = __builtin_bit_cast(uint4, v)[j];
+  if constexpr (H)
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), __builtin_bit_cast(f16x2, 0x3C003C00u), acc, false);
+  else
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), __builtin_bit_cast(bf16x2, 0x3F803F80u),
+                                           acc, false);
 }
 
 // Optional additive score bias (the reference's SDPA mask): bias[b * bs + h * hs + q * qs + key]
@@ -126,6 +160,7 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
   static_assert(PER * NDMA == INST, "DMA split");
   const bool dma_wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) < NDMA;
   constexpr int QS = D / 16, DB = D / 32;
+  constexpr bool PIPE = D == 128 && !BIAS;  // the software-pipelined key loop
   __shared__ __attribute__((aligned(1024))) uint8_t smem[NSTAGE * STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -154,47 +189,40 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
   for (int s = 0; s < QS; ++s)
     qf[s] = *reinterpret_cast<const bf16x8*>(Qb + (int64_t)qrow * ldq + (2 * s + lhalf) * 8);
 
-  // DMA: instruction g = wave * PER + i of a stage fills RPI rows of the K tile (g < INST / 2) or
-  // the V tile, a wave's PER instructions all of one kind; lane -> row lane / CPR, slot
-  // lane % CPR, which holds chunk slot ^ swz(row). A lane's source is the tile's scalar base plus a
-  // 32-bit byte offset kept across the loop. Keys past the end re-read the last key (in bounds;
-  // masked below).
-  static_assert((INST / 2) % PER == 0, "a DMA wave fills one kind of tile");
-  const bool wave_isv = wave * PER >= INST / 2;
+  // DMA: waves [0, NDMA / 2) fill the K tile, the others the V tile; instruction i of the wave with
+  // index wk among its kind fills rows RPI (wk + NK i) .. + RPI - 1, lane -> row lane / CPR, slot
+  // lane % CPR, which holds chunk slot ^ swz(row). The row step between a wave's instructions is a
+  // multiple of the swizzle period, so every copy of the wave takes the same lane offset; the row
+  // step is a scalar offset and the tile's first key the resource's base. Keys past the end
+  // re-read the last key (in bounds; masked below).
+  constexpr int NK = NDMA / 2;
+  static_assert(PER * NK == INST / 2 && (RPI * NK) % 16 == 0, "DMA row interleave");
+  const bool wave_isv = wave >= NK;
+  const int wk = wave_isv ? wave - NK : wave;
   const char* dma_base = wave_isv ? Vb : Kb;
-  const int64_t dma_ld = (wave_isv ? ldv : ldk) * 2;  // bytes per key (< 2^25, checked on the host)
-  const int row0 = (wave_isv ? wave * PER - INST / 2 : wave * PER) * RPI;
-  // streaming form: the lane's byte offsets of its PER copies, kept across the key loop
-  const int r_in = lane / CPR, slot = lane % CPR;
-  uint32_t dma_off[RES ? 1 : PER];
-  if constexpr (!RES) {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int r = row0 + i * RPI + r_in;
-      dma_off[i] = (uint32_t)(r * dma_ld) + (uint32_t)((slot ^ (wave_isv ? swz_v<D>(r) : swz_k<D>(r))) * 16);
-    }
-  }
+  const uint32_t dma_ld = (uint32_t)((wave_isv ? ldv : ldk) * 2);  // bytes per key (< 2^25, checked on the host)
+  const int dma_lds = (wave_isv ? TILE : 0) + RPI * wk * ROWB;  // the wave's first copy in a stage
   auto issue = [&](uint8_t* buf, int j0) {
     if (!dma_wave) return;
-    const char* base = dma_base + (int64_t)j0 * dma_ld;
-    if constexpr (RES) {
-      // the resident form copies each tile once, before its loop: offsets computed here
+    // the lane offsets, recomputed from the lane id at each issue (a few VALU on the DMA waves):
+    // held across the key loop they would take registers the loop needs, and a spilled copy
+    // reloaded here would wait for every copy in flight
+    uint32_t ln;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
+    const int r_in = (int)ln / CPR, slot = (int)ln % CPR;
+    const int lrow_dma = RPI * wk + r_in;  // the lane's row in the wave's first copy
+    const uint32_t chunk_off = (uint32_t)((slot ^ (wave_isv ? swz_v<D>(lrow_dma) : swz_k<D>(lrow_dma))) * 16);
+    const uint32_t dma_voff = (uint32_t)lrow_dma * dma_ld + chunk_off;
+    const i32x4 rsrc = dma_rsrc(dma_base + (int64_t)j0 * dma_ld);
+    if (j0 + BKV <= tk) {
 #pragma unroll
-      for (int i = 0; i < PER; ++i) {
-        const int r = row0 + i * RPI + r_in;
-        const int key = min(j0 + r, tk - 1);  // keys past the end re-read the last key
-        const uint32_t off = (uint32_t)((key - j0) * dma_ld) +
-                             (uint32_t)((slot ^ (wave_isv ? swz_v<D>(r) : swz_k<D>(r))) * 16);
-        dma16(base + off, buf + (wave * PER + i) * 1024);
-      }
-    } else if (j0 + BKV <= tk) {
-#pragma unroll
-      for (int i = 0; i < PER; ++i) dma16(base + dma_off[i], buf + (wave * PER + i) * 1024);
+      for (int i = 0; i < PER; ++i)
+        dma16(rsrc, dma_voff, (uint32_t)(RPI * NK * i) * dma_ld, buf + dma_lds + RPI * NK * i * ROWB);
     } else {
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
-        const int over = max(j0 + row0 + i * RPI + r_in - (tk - 1), 0);  // rows past the last key
-        dma16(base + dma_off[i] - (int64_t)over * dma_ld, buf + (wave * PER + i) * 1024);
+        const int r = min(lrow_dma + RPI * NK * i, tk - 1 - j0);  // rows past the last key re-read it
+        dma16(rsrc, (uint32_t)r * dma_ld + chunk_off, 0u, buf + dma_lds + RPI * NK * i * ROWB);
       }
     }
   };
@@ -224,13 +252,14 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
   float l_run = 0.0f;       // this lane's partial row sum
 
   const int ntiles = (tk + BKV - 1) / BKV;
-  if constexpr (D == 128 && !BIAS) {
+  if constexpr (PIPE) {
     // Software pipeline over blocks of 32 keys (block c = key half c % 2 of tile c / 2): the MFMAs
     // of block c + 1's scores run between the exps of block c, and the P V MFMAs of block c between
     // the max of block c + 1, so the matrix core and the VALU of a wave work side by side instead
     // of in turns. Tile t becomes visible at a barrier before the scores of its first block (in
     // the middle of tile t - 1); that barrier also frees the buffer of tile t - 2 (every wave has
-    // finished its P V products), which takes tile t + NSTAGE - 2.
+    // finished its P V products), which takes tile t + NSTAGE - 2. (A ring of 5 with a barrier per
+    // two tiles measured 2-3 % slower.)
     auto buf = [&](int t) { return smem + (t % NSTAGE) * STAGE; };
     if constexpr (!RES) {
 #pragma unroll
@@ -261,6 +290,7 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
     };
 
     f32x16 sc;  // the current block's scores
+    float mc;   // the running max in the exp2 domain
     // block 0's scores and the running max they start
     auto first_block = [&]() __attribute__((always_inline)) {
 #pragma unroll
@@ -272,7 +302,8 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
       float tmax = sc[0];
 #pragma unroll
       for (int e = 1; e < 16; ++e) tmax = fmaxf(tmax, sc[e]);
-      m_run = fmaxf(tmax, __shfl_xor(tmax, 32, 64));  // finite: block 0 holds key 0
+      m_run = half_max(tmax);  // finite: block 0 holds key 0
+      mc = m_run * scale_log2;
     };
     if constexpr (!RES) {
       arrive(0);
@@ -282,9 +313,7 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
     // block c (key half kb of tile `cur`) with the scores of block cn (key half nkb of tile `nxt`)
     auto step = [&](const uint8_t* cur, int kb, const uint8_t* nxt, int nkb,
                     int cn) __attribute__((always_inline)) {
-      const float mc = m_run * scale_log2;
       bf16x8 pb[2];
-      float psum = 0.0f;
       f32x16 sn;
 #pragma unroll
       for (int e = 0; e < 16; ++e) sn[e] = 0.0f;
@@ -293,38 +322,41 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
       auto pexp = [&](int e) {
         float p = __builtin_amdgcn_exp2f(fmaf(sc[e], scale_log2, -mc));
         asm volatile("" : "+v"(p));
-        psum += p;
         pb[e >> 3][e & 7] = e16<H>(p);
+        if (e & 1) l_run = add_pair<H>(pb[e >> 3], (e & 7) >> 1, l_run);
       };
       // VALU work is spread so that each MFMA has about its own duration of it beside it: the
       // exps of elements 0..PA-1 between the 8 score MFMAs, the rest between the 4 P V MFMAs of
       // the first 16 keys (which need only elements 0..7), the max of block cn between the last 4
       constexpr int PA = 10;
-      bf16x8 kf[2];
-      kf[0] = kfrag(nxt, nkb, 0);
+      // K fragments are read KFD MFMAs ahead, V fragments VFD ahead (the first ones during the last
+      // score MFMAs)
+      constexpr int KFD = 1, VFD = 1;
+      bf16x8 kf[KFD + 1], vf[VFD + 1];
+#pragma unroll
+      for (int i = 0; i < KFD; ++i) kf[i] = kfrag(nxt, nkb, i);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int st = 0; st < QS; ++st) {
-        if (st + 1 < QS) kf[(st + 1) & 1] = kfrag(nxt, nkb, st + 1);
+        if (st + KFD < QS) kf[(st + KFD) % (KFD + 1)] = kfrag(nxt, nkb, st + KFD);
+        if (st + VFD >= QS) vf[st + VFD - QS] = vfrag(cur, (st + VFD - QS) % DB, 2 * kb + (st + VFD - QS) / DB);
         __builtin_amdgcn_sched_barrier(0);
-        sn = mfma32x32x16<H>(kf[st & 1], qf[st], sn);
+        sn = mfma32x32x16<H>(kf[st % (KFD + 1)], qf[st], sn);
 #pragma unroll
         for (int e = st * PA / QS; e < (st + 1) * PA / QS; ++e) pexp(e);
         __builtin_amdgcn_sched_barrier(0);
       }
       mask(sn, cn);
-      // O^T += V^T P^T over the block's two 16-key steps, V^T read one MFMA ahead
-      bf16x8 vf[2];
-      vf[0] = vfrag(cur, 0, 2 * kb);
+      // O^T += V^T P^T over the block's two 16-key steps
       float tmax = -INFINITY;
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int q = 0; q < 2 * DB; ++q) {
         const int ts = q / DB, db = q % DB;
-        if (q + 1 < 2 * DB)
-          vf[(q + 1) & 1] = vfrag(cur, (q + 1) % DB, 2 * kb + (q + 1) / DB);
+        if (q + VFD < 2 * DB)
+          vf[(q + VFD) % (VFD + 1)] = vfrag(cur, (q + VFD) % DB, 2 * kb + (q + VFD) / DB);
         __builtin_amdgcn_sched_barrier(0);
-        o[db] = mfma32x32x16<H>(vf[q & 1], pb[ts], o[db]);
+        o[db] = mfma32x32x16<H>(vf[q % (VFD + 1)], pb[ts], o[db]);
         if (q < DB) {
 #pragma unroll
           for (int e = PA + q * (16 - PA) / DB; e < PA + (q + 1) * (16 - PA) / DB; ++e) pexp(e);
@@ -335,9 +367,8 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
         }
         __builtin_amdgcn_sched_barrier(0);
       }
-      l_run += psum;
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-      if (__any(tmax * scale_log2 > m_run * scale_log2 + LAZY_TH)) {
+      tmax = half_max(tmax);
+      if (__any(tmax * scale_log2 > mc + LAZY_TH)) {
         const float m_new = fmaxf(m_run, tmax);
         const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
         l_run *= alpha;
@@ -346,6 +377,7 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
 #pragma unroll
           for (int e = 0; e < 16; ++e) o[i][e] *= alpha;
         m_run = m_new;
+        mc = m_run * scale_log2;
       }
       sc = sn;
     };
@@ -485,11 +517,9 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
       const float mc = m_run * scale_log2;
       const float removed_p = m_run == -1e30f ? 1.0f : 0.0f;  // p of a removed key (bias variant)
       bf16x8 pb[2][2];
-      float psum = 0.0f;
       auto pexp = [&](int kb, int hf, int e) {
         float p = __builtin_amdgcn_exp2f(fmaf(s[kb][8 * hf + e], scale_log2, -mc));
         if constexpr (BIAS) p = s[kb][8 * hf + e] == -1e30f ? removed_p : p;
-        psum += p;
         pb[kb][hf][e] = e16<H>(p);
       };
 #pragma unroll
@@ -498,6 +528,13 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
         for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
           for (int e = 0; e < 8; ++e) pexp(kb, hf, e);
+      // the row sum of the rounded P, as in the pipelined form
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) l_run = add_pair<H>(pb[kb][hf], j, l_run);
       // O^T += V^T P^T, 16 keys per step; step ts = 2 kb + hf uses P^T block pb[kb][hf]
 #pragma unroll
       for (int ts = 0; ts < 4; ++ts)
@@ -506,7 +543,6 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
           const bf16x8 vf = read_vt(cur + voff[db] + 16 * ts * ROWB, 8 * ROWB);
           o[db] = mfma32x32x16<H>(vf, pb[ts >> 1][ts & 1], o[db]);
         }
-      l_run += psum;
       cur_i = cur_i + 1 == NSTAGE ? 0 : cur_i + 1;
     }
   }

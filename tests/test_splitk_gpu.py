@@ -73,8 +73,9 @@ def test_tail_split_matches_oracle(device, m, n, k, epi):
     finally:
         _lib.set_timer(None)
     launches = [(name, args) for name, args, _ in timer.durations_ms()]
-    assert [name for name, _ in launches] == ["kx_gemm_bf16", "kx_gemm_splitk_bf16"]
-    assert launches[0][1][7] == rows and launches[1][1][7] == m - rows and launches[1][1][18] == splits
+    # the tail's K slices first (its rows are the input's most recently written), then the head
+    assert [name for name, _ in launches] == ["kx_gemm_splitk_bf16", "kx_gemm_bf16"]
+    assert launches[1][1][7] == rows and launches[0][1][7] == m - rows and launches[0][1][18] == splits
     out = got.float().cpu().numpy()[sample]
     assert cosine(out, ref) > 0.99999
     bound = 2e-3 if got.dtype == torch.float32 else 2 ** -7 * max(1.0, np.abs(ref).max())
