@@ -289,8 +289,12 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
       }
     };
 
-    f32x16 sc;  // the current block's scores
-    float mc;   // the running max in the exp2 domain
+    f32x16 sc;    // the current block's scores
+    float mc;     // the running max in the exp2 domain
+    bf16x8 kpre;  // the next step's first K fragment, read ahead where no barrier comes between
+    // the read-ahead of kpre: bf16 streaming form only (the resident form, and the fp16 form with
+    // its wider conversions, have no registers to spare for it)
+    constexpr bool PRE = !RES && !H;
     // block 0's scores and the running max they start
     auto first_block = [&]() __attribute__((always_inline)) {
 #pragma unroll
@@ -304,6 +308,7 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
       for (int e = 1; e < 16; ++e) tmax = fmaxf(tmax, sc[e]);
       m_run = half_max(tmax);  // finite: block 0 holds key 0
       mc = m_run * scale_log2;
+      if constexpr (PRE) kpre = kfrag(buf(0), 1, 0);  // the first K fragment of block 1
     };
     if constexpr (!RES) {
       arrive(0);
@@ -311,8 +316,10 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
     }
 
     // block c (key half kb of tile `cur`) with the scores of block cn (key half nkb of tile `nxt`)
-    auto step = [&](const uint8_t* cur, int kb, const uint8_t* nxt, int nkb,
-                    int cn) __attribute__((always_inline)) {
+    // use_pre: the first K fragment is kpre; pnxt (if not null): read block 1's first K fragment
+    // of tile pnxt into kpre during the last P V MFMAs, for the step after this one
+    auto step = [&](const uint8_t* cur, int kb, const uint8_t* nxt, int nkb, int cn, bool use_pre,
+                    const uint8_t* pnxt) __attribute__((always_inline)) {
       bf16x8 pb[2];
       f32x16 sn;
 #pragma unroll
@@ -334,7 +341,7 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
       constexpr int KFD = 1, VFD = 1;
       bf16x8 kf[KFD + 1], vf[VFD + 1];
 #pragma unroll
-      for (int i = 0; i < KFD; ++i) kf[i] = kfrag(nxt, nkb, i);
+      for (int i = 0; i < KFD; ++i) kf[i] = i == 0 && use_pre ? kpre : kfrag(nxt, nkb, i);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int st = 0; st < QS; ++st) {
@@ -355,6 +362,8 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
         const int ts = q / DB, db = q % DB;
         if (q + VFD < 2 * DB)
           vf[(q + VFD) % (VFD + 1)] = vfrag(cur, (q + VFD) % DB, 2 * kb + (q + VFD) / DB);
+        else if (pnxt)
+          kpre = kfrag(pnxt, 1, 0);
         __builtin_amdgcn_sched_barrier(0);
         o[db] = mfma32x32x16<H>(vf[q % (VFD + 1)], pb[ts], o[db]);
         if (q < DB) {
@@ -405,9 +414,9 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
         first_block();
         for (int t = 0; t < ntiles; ++t) {
           const uint8_t* cur = buf(t);
-          step(cur, 0, cur, 1, 2 * t + 1);
+          step(cur, 0, cur, 1, 2 * t + 1, false, nullptr);
           const bool more = t + 1 < ntiles;
-          step(cur, 1, more ? buf(t + 1) : cur, 0, more ? 2 * t + 2 : 2 * t);
+          step(cur, 1, more ? buf(t + 1) : cur, 0, more ? 2 * t + 2 : 2 * t, false, nullptr);
         }
         const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
         const int q = q0 + lrow;
@@ -430,12 +439,15 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
     }
     for (int t = 0; t < ntiles; ++t) {
       const uint8_t* cur = buf(t);
-      step(cur, 0, cur, 1, 2 * t + 1);
+      step(cur, 0, cur, 1, 2 * t + 1, PRE, nullptr);
       // the last block recomputes the scores of block 2t, already seen (its max cannot move the
       // running max); they are not used
       const bool more = t + 1 < ntiles;
       if (more) arrive(t + 1);
-      step(cur, 1, more ? buf(t + 1) : cur, 0, more ? 2 * t + 2 : 2 * t);
+      // block 1's first K fragment of tile t + 1 (visible since the barrier above) is read during
+      // this step's last P V MFMAs; after the last tile the read takes a buffer the loop no longer
+      // uses and its value is dropped
+      step(cur, 1, more ? buf(t + 1) : cur, 0, more ? 2 * t + 2 : 2 * t, false, PRE ? buf(t + 1) : nullptr);
     }
   } else {
 #pragma unroll
