@@ -335,6 +335,8 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
       // VALU work is spread so that each MFMA has about its own duration of it beside it: the
       // exps of elements 0..PA-1 between the 8 score MFMAs, the rest between the 4 P V MFMAs of
       // the first 16 keys (which need only elements 0..7), the max of block cn between the last 4
+      // (8, 9, 12 or 14 here leave a query fragment spilled and reloaded in the loop, whose wait
+      // on vmcnt also waits for the K/V copies in flight: 10 % slower; 10 and 11 fit)
       constexpr int PA = 10;
       // K fragments are read KFD MFMAs ahead, V fragments VFD ahead (the first ones during the last
       // score MFMAs)
