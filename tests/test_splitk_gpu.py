@@ -120,3 +120,21 @@ def test_tail_split_of_a_batched_input_equals_the_flat_product(device):
                            out_dtype=torch.float32)
     assert batched.shape == (2, m // 2, n)
     assert torch.equal(batched.view(m, n), flat)
+
+
+def test_input_above_the_cache_size_is_tiled_newest_rows_first(device):
+    """An input over 128 MiB (here 9216 x 8192 bf16, 151 MB) makes the kernel visit its tile rows
+    last to first; the tile order changes no result: the first, middle and last rows against the
+    FP32 oracle, and the whole product bit-equal to the same rows computed in two halves (each
+    under the size, so in the ascending order)."""
+    m, n, k = 9216, 512, 8192
+    assert m * k * 2 > 128 << 20 and (m // 2) * k * 2 <= 128 << 20
+    x, w = _bf((m, k), 21), _bf((n, k), 22, 0.02)
+    xd, wd = x.to(device), w.to(device)
+    got = fused_linear(xd, wd, None)
+    halves = torch.cat([fused_linear(xd[: m // 2], wd, None), fused_linear(xd[m // 2:], wd, None)])
+    assert torch.equal(got, halves)
+    sample = np.r_[0:64, m // 2 - 32:m // 2 + 32, m - 64:m]
+    ref = oracle.linear(x[sample].float().numpy(), w.float().numpy())
+    out = got.float().cpu().numpy()[sample]
+    assert cosine(out, ref) > 0.99999 and max_abs(out, ref) <= 2 ** -7 * max(1.0, np.abs(ref).max())
