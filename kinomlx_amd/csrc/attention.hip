@@ -108,13 +108,16 @@ __device__ __forceinline__ float half_max(float x) {
 // acc + the two 16-bit values of element pair j of v (v_dot2 with (1, 1)): the row sum of P taken
 // from the rounded values the P V product uses.
 template <bool H>
-__device__ __forceinline__ float add_pair(bf16x8 v, int j, float acc) {
-  const uint32_t w = __builtin_bit_cast(uint4, v)[j];
+__device__ __forceinline__ float add_word(uint32_t w, float acc) {
   if constexpr (H)
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), __builtin_bit_cast(f16x2, 0x3C003C00u), acc, false);
   else
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), __builtin_bit_cast(bf16x2, 0x3F803F80u),
                                            acc, false);
+}
+template <bool H>
+__device__ __forceinline__ float add_pair(bf16x8 v, int j, float acc) {
+  return add_word<H>(__builtin_bit_cast(uint4, v)[j], acc);
 }
 
 // Optional additive score bias (the reference's SDPA mask): bias[b * bs + h * hs + q * qs + key]
@@ -292,9 +295,8 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
     f32x16 sc;    // the current block's scores
     float mc;     // the running max in the exp2 domain
     bf16x8 kpre;  // the next step's first K fragment, read ahead where no barrier comes between
-    // the read-ahead of kpre: bf16 streaming form only (the resident form, and the fp16 form with
-    // its wider conversions, have no registers to spare for it)
-    constexpr bool PRE = !RES && !H;
+    // the read-ahead of kpre: the streaming forms (the resident form has no registers to spare)
+    constexpr bool PRE = !RES;
     // block 0's scores and the running max they start
     auto first_block = [&]() __attribute__((always_inline)) {
 #pragma unroll
@@ -320,7 +322,8 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
     // of tile pnxt into kpre during the last P V MFMAs, for the step after this one
     auto step = [&](const uint8_t* cur, int kb, const uint8_t* nxt, int nkb, int cn, bool use_pre,
                     const uint8_t* pnxt) __attribute__((always_inline)) {
-      bf16x8 pb[2];
+      uint32_t pw[2][4];  // P^T as packed pairs (one v_cvt_pk per pair in both types)
+      float pe;           // the even element's p, until its odd partner is computed
       f32x16 sn;
 #pragma unroll
       for (int e = 0; e < 16; ++e) sn[e] = 0.0f;
@@ -329,8 +332,12 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
       auto pexp = [&](int e) {
         float p = __builtin_amdgcn_exp2f(fmaf(sc[e], scale_log2, -mc));
         asm volatile("" : "+v"(p));
-        pb[e >> 3][e & 7] = e16<H>(p);
-        if (e & 1) l_run = add_pair<H>(pb[e >> 3], (e & 7) >> 1, l_run);
+        if ((e & 1) == 0) {
+          pe = p;
+        } else {
+          pw[e >> 3][(e & 7) >> 1] = e_pack2<H>(pe, p);
+          l_run = add_word<H>(pw[e >> 3][(e & 7) >> 1], l_run);
+        }
       };
       // VALU work is spread so that each MFMA has about its own duration of it beside it: the
       // exps of elements 0..PA-1 between the 8 score MFMAs, the rest between the 4 P V MFMAs of
@@ -367,7 +374,8 @@ __global__ __launch_bounds__(NWAVE * 64) void attn_fwd_kernel(
         else if (pnxt)
           kpre = kfrag(pnxt, 1, 0);
         __builtin_amdgcn_sched_barrier(0);
-        o[db] = mfma32x32x16<H>(vf[q % (VFD + 1)], pb[ts], o[db]);
+        const bf16x8 pb = __builtin_bit_cast(bf16x8, make_uint4(pw[ts][0], pw[ts][1], pw[ts][2], pw[ts][3]));
+        o[db] = mfma32x32x16<H>(vf[q % (VFD + 1)], pb, o[db]);
         if (q < DB) {
 #pragma unroll
           for (int e = PA + q * (16 - PA) / DB; e < PA + (q + 1) * (16 - PA) / DB; ++e) pexp(e);
