@@ -387,12 +387,15 @@ int kx_quantize_fp4_bf16(const void* w, int64_t ldw, uint32_t* wq, void* scales,
 
 /* Modulation values: out[b, t, r, c] = fp32(table[r, c]) + fp32(ts[b, t, r, c]) for a (rows, dim)
  * table (KX_F32, KX_BF16 or KX_F16) and an optional timestep modulation ts (null: the table alone) with
- * element strides ts_bs / ts_ts / ts_rs (dim contiguous); out is fp32 (batch, tokens, rows, dim)
+ * element strides ts_bs / ts_ts / ts_rs (dim contiguous; 0 broadcasts); with round_dtype KX_BF16 or
+ * KX_F16 each sum is rounded to that type (KX_F32: kept); out is fp32 (batch, tokens, rows, dim)
  * contiguous. BasicAVTransformerBlock._ada_values and the prompt / A/V tables
- * (kinomlx/models/ltx2/transformer/transformer.py:179-199,209-219): scale_shift_table + timestep. */
+ * (kinomlx/models/ltx2/transformer/transformer.py:179-199,209-219): scale_shift_table + timestep;
+ * LTXAVModel._output (kinomlx/models/ltx2/transformer/model.py:577-593): the output head's
+ * (shift, scale), rounded to the hidden state's type. */
 int kx_table_add_f32(const void* table, int table_dtype, const void* ts, int ts_dtype, int64_t ts_bs,
                      int64_t ts_ts, int64_t ts_rs, float* out, int64_t batch, int64_t tokens, int64_t rows,
-                     int64_t dim, kx_stream_t stream);
+                     int64_t dim, int round_dtype, kx_stream_t stream);
 
 /* tanh GELU in fp32, inner argument clamped to +-10: fused_ops.gelu_approx
  * (kinomlx/kernels/fused_ops.py:27-35,327-350). */

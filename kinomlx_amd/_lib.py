@@ -94,7 +94,7 @@ SIGNATURES: dict[str, list] = {
     "kx_qgemm_affine_tiled_bf16": [
         _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _I, _P, _I64, _P, _I64, _I64, _P,
     ],
-    "kx_table_add_f32": [_P, _I, _P, _I, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P],
+    "kx_table_add_f32": [_P, _I, _P, _I, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I, _P],
     "kx_gemm_qknorm_rope_bf16": [
         _P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _I, _F, _F, _P, _P, _I64, _I64,
         _I64, _I64, _P,
@@ -734,10 +734,11 @@ def launch_modulate(x, out, shift, scale) -> None:
     )
 
 
-def table_add(table: torch.Tensor, ts: torch.Tensor | None) -> torch.Tensor:
+def table_add(table: torch.Tensor, ts: torch.Tensor | None, round_to: torch.dtype = torch.float32) -> torch.Tensor:
     """``fp32(table) + fp32(ts)`` as a new contiguous fp32 ``(B, T, rows, D)`` tensor: ``table`` is
-    ``(rows, D)`` (fp32, bf16 or fp16), ``ts`` ``(B, T, rows, D)`` with a contiguous last axis, or ``None``
-    (the table alone, as ``(1, 1, rows, D)``)."""
+    ``(rows, D)`` (fp32, bf16 or fp16), ``ts`` ``(B, T, rows, D)`` with a contiguous last axis (other
+    strides may be 0 to broadcast), or ``None`` (the table alone, as ``(1, 1, rows, D)``). With
+    ``round_to`` bf16 or fp16 every sum is rounded to that type (and kept as fp32)."""
     _check_gpu("table_add", table, ts)
     if table.dim() != 2 or table.stride(-1) != 1 or (table.shape[0] > 1 and table.stride(0) != table.shape[1]):
         raise ValueError("table_add: table must be a contiguous (rows, dim) tensor")
@@ -750,9 +751,12 @@ def table_add(table: torch.Tensor, ts: torch.Tensor | None) -> torch.Tensor:
         batch, tokens = ts.shape[:2]
         bs, tstride, rs = ts.stride(0), ts.stride(1), ts.stride(2)
         ts_code = _weight_code(ts, "table_add timestep")
+    round_code = {torch.float32: KX_F32, torch.bfloat16: KX_BF16, torch.float16: KX_F16}.get(round_to)
+    if round_code is None:
+        raise ValueError(f"table_add: round_to must be float32, bfloat16 or float16, got {round_to}")
     out = torch.empty((batch, tokens, rows, dim), dtype=torch.float32, device=table.device)
     _call("kx_table_add_f32", _ptr(table), _weight_code(table, "table_add table"), _ptr(ts), ts_code, bs, tstride, rs,
-          _ptr(out), batch, tokens, rows, dim, _stream())
+          _ptr(out), batch, tokens, rows, dim, round_code, _stream())
     return out
 
 

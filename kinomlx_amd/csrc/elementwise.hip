@@ -49,8 +49,9 @@ __device__ __forceinline__ float load_any(const void* p, int64_t i) {
   else return e2f<DT == KX_F16>(static_cast<const uint16_t*>(p)[i]);
 }
 
-// out[(b * tokens + t) * rows + r][c] = fp32(table[r][c]) + fp32(ts[b, t, r, c]) (ts optional).
-template <int TAB, int TS>
+// out[(b * tokens + t) * rows + r][c] = fp32(table[r][c]) + fp32(ts[b, t, r, c]) (ts optional),
+// then rounded to bf16 / fp16 (RND = KX_BF16 / KX_F16; KX_F32: kept) and stored as fp32.
+template <int TAB, int TS, int RND>
 __global__ __launch_bounds__(256) void table_add_kernel(const void* __restrict__ table, const void* __restrict__ ts,
                                                         int64_t ts_bs, int64_t ts_ts, int64_t ts_rs,
                                                         float* __restrict__ out, int64_t tokens, int64_t rows,
@@ -61,6 +62,7 @@ __global__ __launch_bounds__(256) void table_add_kernel(const void* __restrict__
   const int64_t t = bt % tokens, b = bt / tokens;
   float v = load_any<TAB>(table, r * dim + c);
   if (ts) v += load_any<TS>(ts, b * ts_bs + t * ts_ts + r * ts_rs + c);
+  if constexpr (RND != KX_F32) v = e2f<RND == KX_F16>(f2e<RND == KX_F16>(v));
   out[i] = v;
 }
 
@@ -110,22 +112,29 @@ KX_UNARY_ENTRY(f16, true)
 
 extern "C" int kx_table_add_f32(const void* table, int table_dtype, const void* ts, int ts_dtype, int64_t ts_bs,
                                 int64_t ts_ts, int64_t ts_rs, float* out, int64_t batch, int64_t tokens,
-                                int64_t rows, int64_t dim, kx_stream_t stream) {
+                                int64_t rows, int64_t dim, int round_dtype, kx_stream_t stream) {
   KX_REQUIRE(table && out && batch >= 0 && tokens > 0 && rows > 0 && dim > 0,
              "kx_table_add_f32: bad argument");
-  KX_REQUIRE(table_dtype >= KX_F32 && table_dtype <= KX_F16 && ts_dtype >= KX_F32 && ts_dtype <= KX_F16,
+  KX_REQUIRE(table_dtype >= KX_F32 && table_dtype <= KX_F16 && ts_dtype >= KX_F32 && ts_dtype <= KX_F16 &&
+                 round_dtype >= KX_F32 && round_dtype <= KX_F16,
              "kx_table_add_f32: dtypes must be KX_F32, KX_BF16 or KX_F16");
   const int64_t total = batch * tokens * rows * dim;
   if (total == 0) return KX_OK;
   const unsigned blocks = (unsigned)((total + 255) / 256);
   hipStream_t s = (hipStream_t)stream;
-#define KX_TABLE_ADD(TB, SB) \
-  table_add_kernel<TB, SB><<<blocks, 256, 0, s>>>(table, ts, ts_bs, ts_ts, ts_rs, out, tokens, rows, dim, total)
-#define KX_TABLE_TS(TB)                                   \
-  switch (ts_dtype) {                                     \
-    case KX_BF16: KX_TABLE_ADD(TB, KX_BF16); break;       \
-    case KX_F16: KX_TABLE_ADD(TB, KX_F16); break;         \
-    default: KX_TABLE_ADD(TB, KX_F32);                    \
+#define KX_TABLE_ADD(TB, SB, RB) \
+  table_add_kernel<TB, SB, RB><<<blocks, 256, 0, s>>>(table, ts, ts_bs, ts_ts, ts_rs, out, tokens, rows, dim, total)
+#define KX_TABLE_RND(TB, SB)                                \
+  switch (round_dtype) {                                    \
+    case KX_BF16: KX_TABLE_ADD(TB, SB, KX_BF16); break;     \
+    case KX_F16: KX_TABLE_ADD(TB, SB, KX_F16); break;       \
+    default: KX_TABLE_ADD(TB, SB, KX_F32);                  \
+  }
+#define KX_TABLE_TS(TB)                                     \
+  switch (ts_dtype) {                                       \
+    case KX_BF16: KX_TABLE_RND(TB, KX_BF16) break;          \
+    case KX_F16: KX_TABLE_RND(TB, KX_F16) break;            \
+    default: KX_TABLE_RND(TB, KX_F32)                       \
   }
   switch (table_dtype) {
     case KX_BF16: KX_TABLE_TS(KX_BF16) break;
@@ -133,6 +142,7 @@ extern "C" int kx_table_add_f32(const void* table, int table_dtype, const void* 
     default: KX_TABLE_TS(KX_F32)
   }
 #undef KX_TABLE_TS
+#undef KX_TABLE_RND
 #undef KX_TABLE_ADD
   return check_launch("kx_table_add_f32");
 }

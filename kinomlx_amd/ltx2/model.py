@@ -23,6 +23,7 @@ from dataclasses import replace
 
 import torch
 
+from .. import _lib
 from .attention import Linear
 from .rope import precompute_freqs_cis
 from .timestep import AdaLayerNormSingle
@@ -274,9 +275,10 @@ class LTXAVModel:
         ``(table + embedded_timestep)`` rounded to the value dtype (``model.py:577-593``)."""
         if embedded_timestep is None:
             raise ValueError("transformer output requires an embedded timestep")
-        modulation = (table[None, None].float() + embedded_timestep[:, :, None, :].float()).to(value.dtype).float()
-        shift = modulation[:, :, 0].contiguous()
-        scale = modulation[:, :, 1].contiguous()
+        rows = table.shape[0]
+        modulation = _lib.table_add(table, embedded_timestep[:, :, None, :].expand(-1, -1, rows, -1),
+                                    round_to=value.dtype)
+        shift, scale = modulation[:, :, 0], modulation[:, :, 1]
         normalized = layer_norm_modulate(value, shift, scale, self.norm_eps)
         return projection(normalized)
 

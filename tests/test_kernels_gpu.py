@@ -992,3 +992,18 @@ def test_table_add_is_bit_exact(device, table_dtype, ts_dtype):
     assert torch.equal(got, table[None, None].float() + ts.float())
     part = _lib.table_add(table[3:6], ts[:, :, 3:6, :])
     assert torch.equal(part, table[3:6][None, None].float() + ts[:, :, 3:6, :].float())
+
+
+@pytest.mark.parametrize("round_to", [torch.bfloat16, torch.float16])
+def test_table_add_rounds_and_broadcasts(device, round_to):
+    """The output head's ``(shift, scale)`` (``model.py:577-593``): the table plus the embedded
+    timestep broadcast over the table's rows by a zero stride, each sum rounded to the hidden
+    state's type, bit for bit as torch rounds the FP32 sum."""
+    g = torch.Generator().manual_seed(12)
+    table = torch.randn((2, 640), generator=g).to(torch.bfloat16).to(device)
+    emb = (torch.randn((2, 3, 640), generator=g) * 3.0).to(device)
+    got = _lib.table_add(table, emb[:, :, None, :].expand(-1, -1, 2, -1), round_to=round_to)
+    want = (table[None, None].float() + emb[:, :, None, :]).to(round_to).float()
+    assert got.shape == (2, 3, 2, 640)
+    assert torch.equal(got, want)
+    assert not torch.equal(got, table[None, None].float() + emb[:, :, None, :])
