@@ -1,6 +1,6 @@
 """Benchmark of the MI355X DiT-block hot path.
 
-One step = one forward pass of the LTX-2-like video DiT block (9216 video
+One step = one forward pass of the LTX-2-like video DiT block (benchmark config 3: 9216 video
 tokens with 3D RoPE + 256 text tokens by cross-attention, D = 4096, 32 heads x 128, GELU MLP x4)
 over synthetic seeded inputs already resident in HBM. Prints ONE JSON line:
 

@@ -121,7 +121,7 @@ def assert_block_bar(got, ref, what: str = "", *, fp32_out: bool = False, contex
 os.environ.setdefault("PYTHONHASHSEED", "0")
 
 
-# At D = 4096 the synthetic N(0, 1) modulation gates amplify the bf16
+# At D = 4096 (benchmark configs 2-5) the synthetic N(0, 1) modulation gates amplify the bf16
 # rounding of the GEMM operands (normalized input, attention output, FF hidden) to output errors of
 # 0.05-0.15 for any bf16 execution, the reference's own included; which elements carry them depends
 # on every rounding decision upstream, so no FP32 evaluation reproduces one bf16 execution there.

@@ -1,4 +1,4 @@
-"""Stage-by-stage parity of the full-size LTX-2 block (BASELINE configs 3 and 4, int4 and int8).
+"""Stage-by-stage parity of the full-size LTX-2 block (benchmark configs 3 and 4, int4 and int8).
 
 The block is run one kernel stage at a time, through the same calls the block makes, and the
 chained stages are first checked bit-identical to the block's own output. Each stage's output is

@@ -1,7 +1,8 @@
 """Block parity on the GPU: the MI355X LTX-2 video block against the FP32 oracle on the same
-seeded inputs, and at the full BASELINE shapes (configs 3, 4 and 5) against the FP32 torch
-evaluation of the same block (pinned to the oracle in ``test_blocks_cpu.py``; quantized blocks are
-evaluated on the oracle's dequantized weights, the operand the quantized GEMM multiplies).
+seeded inputs, and at the full benchmark shapes (configs 3, 4 and 5 of ``workloads.CONFIGS``)
+against the FP32 torch evaluation of the same block (pinned to the oracle in
+``test_blocks_cpu.py``; quantized blocks are evaluated on the oracle's dequantized weights, the
+operand the quantized GEMM multiplies).
 
 Bars (``tests.conftest.assert_block_parity``), against the FP32 evaluation:
 * D = 1024: the north star: cosine similarity >= 0.9995, and every element within 2e-2 beyond the
