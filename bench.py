@@ -88,36 +88,46 @@ def _kernel_label(name: str, args: tuple) -> str:
 
 
 def cpu_baseline(budget_s: float = 12.0) -> dict:
-    """Config-1 block (1024 + 128 tokens, D = 1024) through the FP32 numpy restatement on the
-    host cores: median of repeated runs within ``budget_s`` seconds."""
-    import numpy as np
+    """Config-1 block (1024 + 128 tokens, D = 1024) through the FP32 torch-CPU restatement
+    (``oracle/torch_cpu.py``, pinned to the numpy oracle) on the host cores, with
+    ``torch.set_num_threads`` at the cores this process may use: median of repeated runs within
+    ``budget_s`` seconds."""
+    import torch
 
-    import oracle
     from kinomlx_amd import workloads
+    from oracle import torch_cpu
 
     spec = workloads.CONFIGS[1]
     p = workloads.flux_params(spec, 0)
     inputs = workloads.flux_inputs(spec, 0)
-    op = {k: v.float().numpy() for k, v in p.items()}
-    image = inputs["image"][0].float().numpy()
-    text = inputs["text"][0].float().numpy()
-    cos, sin = (t.numpy() for t in workloads.flux_rope(spec))
+    tp = torch_cpu.to_torch({k: v.float().numpy() for k, v in p.items()})
+    image = inputs["image"][0].float().contiguous()
+    text = inputs["text"][0].float().contiguous()
+    rope = tuple(t.float().contiguous() for t in workloads.flux_rope(spec))
     flops = workloads.flop_count(spec)["total"]
+    cores = len(os.sched_getaffinity(0))
+    threads_before = torch.get_num_threads()
+    torch.set_num_threads(cores)
     times = []
-    start = time.perf_counter()
-    while len(times) < 3 or (time.perf_counter() - start < budget_s and len(times) < 50):
-        t0 = time.perf_counter()
-        oracle.config1_double_block(op, image, text, op["image_mod"], op["text_mod"], (cos, sin), heads=spec.heads)
-        times.append(time.perf_counter() - t0)
+    try:
+        with torch.no_grad():
+            start = time.perf_counter()
+            while len(times) < 3 or (time.perf_counter() - start < budget_s and len(times) < 50):
+                t0 = time.perf_counter()
+                torch_cpu.config1_double_block(tp, image, text, tp["image_mod"], tp["text_mod"], rope,
+                                               heads=spec.heads)
+                times.append(time.perf_counter() - t0)
+    finally:
+        torch.set_num_threads(threads_before)
     med = statistics.median(times)
     return {
         "value": round(flops / med / 1e12, 4),
         "unit": "TFLOP/s",
-        "cores": len(os.sched_getaffinity(0)),
+        "cores": cores,
         "kind": "port",
-        "sample": f"config-1 block (1024 image + 128 text tokens, D=1024, 16x64, GELU MLP), FP32 numpy "
-                  f"restatement, median of {len(times)} runs ({med * 1e3:.1f} ms/block); "
-                  f"CPU restatement (fp32), not reference code",
+        "sample": f"config-1 block (1024 image + 128 text tokens, D=1024, 16x64, GELU MLP), FP32 torch-CPU "
+                  f"restatement, torch.set_num_threads({cores}), median of {len(times)} runs "
+                  f"({med * 1e3:.1f} ms/block); CPU restatement (fp32), not reference code",
         "ms_per_block": round(med * 1e3, 2),
     }
 

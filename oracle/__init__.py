@@ -7,6 +7,9 @@ modulation producers, the output head, the transformer forward, the X0 conversio
 conditioning composite, the Euler updates and the finite check, ``oracle/denoise.py``). Every function cites the reference file:line it follows (paths are
 relative to the reference checkout).
 
+``oracle/torch_cpu.py`` restates the config-1 block once more in FP32 on torch's CPU kernels: the
+timed CPU baseline, pinned to the numpy restatement.
+
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import
 this package, and only as the checker or the timed CPU baseline. The product package
 ``kinomlx_amd`` never imports it: there is no CPU fallback on the product path.

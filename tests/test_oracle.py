@@ -631,3 +631,29 @@ def test_nvfp4_scale_is_the_e4m3_of_amax_over_6():
     deq = oracle.dequantize_fp4(words, scales, mode="nvfp4")
     s = np.repeat(oracle.e4m3_decode(scales).astype(np.float64), 16, axis=1)
     assert np.all(np.abs(deq - w) <= s * 1.0 + 1e-12)  # at most half the largest E2M1 step (2) per unit
+
+
+def test_torch_cpu_config1_block_matches_the_numpy_restatement():
+    """The CPU baseline's torch restatement (``oracle/torch_cpu.py``: torch's layer norm, linear
+    and SDPA kernels) against the numpy oracle on the full config-1 block, both FP32: they agree
+    to FP32 reassociation. A dropped term, a swapped gate or a transposed operand in either moves
+    the relative L2 error to order 1."""
+    from kinomlx_amd import workloads
+    from oracle import torch_cpu
+
+    spec = workloads.CONFIGS[1]
+    p = workloads.flux_params(spec, 0)
+    inputs = workloads.flux_inputs(spec, 0)
+    op = {k: v.float().numpy() for k, v in p.items()}
+    image, text = inputs["image"][0].float().numpy(), inputs["text"][0].float().numpy()
+    cos, sin = (t.numpy() for t in workloads.flux_rope(spec))
+    ri, rt = oracle.config1_double_block(op, image, text, op["image_mod"], op["text_mod"], (cos, sin),
+                                         heads=spec.heads)
+    tp = torch_cpu.to_torch(op)
+    gi, gt = torch_cpu.config1_double_block(tp, torch.from_numpy(image), torch.from_numpy(text), tp["image_mod"],
+                                            tp["text_mod"], (torch.from_numpy(cos), torch.from_numpy(sin)),
+                                            heads=spec.heads)
+    for got, ref in ((gi.numpy(), ri), (gt.numpy(), rt)):
+        assert got.shape == ref.shape
+        assert rel_l2(got, ref) < 1e-5
+        assert max_abs(got, ref) <= 1e-4 * float(np.abs(ref).max())
