@@ -157,8 +157,9 @@ def main() -> int:
     parser.add_argument("--profile-summary", type=str, default="", metavar="DIR",
                         help="only summarize the rocprofv3 runs under DIR (see profiles/) as a markdown table")
     parser.add_argument("--kernel-table", type=str, default="", metavar="DIR",
-                        help="only print, from the rocprofv3 --kernel-trace run under DIR (of --steps S timed "
-                             "steps after --warmup W), this library's kernels per instantiation as a markdown table")
+                        help="only print, from the rocprofv3 --kernel-trace run under DIR of a --denoise-step run "
+                             "with --warmup W and --steps S (W warm-up steps, then S timed steps twice: without and "
+                             "with per-launch events), this library's kernels per instantiation as a markdown table")
     parser.add_argument("--compare-rope-fold", action="store_true",
                         help="only time LTX's Q/K norm + RoPE folded into the QKV GEMM epilogue against the "
                              "separate pass, and exit")
@@ -169,7 +170,7 @@ def main() -> int:
     if args.profile_summary:
         return profile_summary(args.profile_summary)
     if args.kernel_table:
-        return kernel_table(args.kernel_table, args.steps + args.warmup)
+        return kernel_table(args.kernel_table, args.warmup + 2 * args.steps)
     if args.calibrate_copy:
         import torch
 
@@ -738,16 +739,23 @@ def denoise_main(args) -> int:
 
     for _ in range(args.warmup):
         step(state)
-    timer = _lib.LaunchTimer()
-    _lib.set_timer(timer)
+    # headline: the steps alone, no per-launch events
     torch.cuda.synchronize()
     wall0 = time.perf_counter()
     for _ in range(args.steps):
         out = step(state)
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
-    _lib.set_timer(None)
     ms_per_step = wall * 1e3 / args.steps
+    # breakdown: the same steps again with HIP events around every launch (on its stream)
+    timer = _lib.LaunchTimer()
+    _lib.set_timer(timer)
+    wall1 = time.perf_counter()
+    for _ in range(args.steps):
+        out = step(state)
+    torch.cuda.synchronize()
+    instrumented_ms = (time.perf_counter() - wall1) * 1e3 / args.steps
+    _lib.set_timer(None)
 
     per_kernel: dict[str, list[float]] = defaultdict(list)
     name_of: dict[str, str] = {}
@@ -797,6 +805,7 @@ def denoise_main(args) -> int:
         "gemm_ms": round(gemm_ms, 2),
         "outside_block_kernels_ms": round(sum(v for k, v in kernel_ms.items() if name_of[k] in outside), 3),
         "kernel_sum_ms": round(sum(kernel_ms.values()), 2),
+        "instrumented_ms_per_step": round(instrumented_ms, 2),
         "build_s": round(build_s, 1),
         "finite": bool(torch.isfinite(out.latent.float()).all()),
     }
