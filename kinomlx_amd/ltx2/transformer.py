@@ -53,6 +53,18 @@ def _mod_pair(shift: torch.Tensor, scale: torch.Tensor) -> tuple[torch.Tensor, t
 
 _HALF = (torch.bfloat16, torch.float16)
 
+_SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
+
+
+def _side_stream(device: torch.device) -> torch.cuda.Stream:
+    """The stream a joint block runs its audio stream on: one per device, default priority."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    stream = _SIDE_STREAMS.get(index)
+    if stream is None:
+        stream = torch.cuda.Stream(device=index)
+        _SIDE_STREAMS[index] = stream
+    return stream
+
 
 def _norm_out_dtype(value: torch.Tensor, out_dtype: torch.dtype | None, what: str) -> torch.dtype:
     if value.dtype not in (*_HALF, torch.float32):
@@ -184,6 +196,9 @@ class BasicAVTransformerBlock:
         self.norm_eps = norm_eps
         self.video_config = video_config
         self.audio_config = audio_config
+        # with both streams present, run the audio stream's launches on a second HIP stream beside
+        # the video stream's (the same kernels on the same values; False keeps one stream)
+        self.audio_side_stream = True
         v_backend = {"compile_attention": video_config.compile_attention,
                      "dense_kernel": video_config.dense_attention_kernel}
         self.attn1 = Attention(video_config.dim, heads=video_config.heads, dim_head=video_config.head_dim,
@@ -277,12 +292,23 @@ class BasicAVTransformerBlock:
 
         video_value = video.x if video_present else None
         audio_value = audio.x if audio_present else None
+        # With both streams running, the audio stream's work (a few hundred tokens: small launches
+        # that leave most CUs idle) goes to a second HIP stream beside the video stream's. The
+        # streams join before the A/V attention (each reads the other's value) and at the end of
+        # the block; every tensor one stream hands the other stays referenced until that final
+        # join, so the caching allocator cannot reuse its memory while the other stream reads it.
+        main = side = None
+        if run_video and run_audio and self.audio_side_stream and video.x.is_cuda:
+            main = torch.cuda.current_stream(video.x.device)
+            side = _side_stream(video.x.device)
+            side.wait_stream(main)
+        if run_audio:
+            with torch.cuda.stream(side):
+                audio_value, audio_ada = self._first_branches(audio, self.audio_scale_shift_table, self.audio_attn1,
+                                                              self.audio_attn2, self.audio_prompt_scale_shift_table)
         if run_video:
             video_value, video_ada = self._first_branches(video, self.scale_shift_table, self.attn1, self.attn2,
                                                           self.prompt_scale_shift_table)
-        if run_audio:
-            audio_value, audio_ada = self._first_branches(audio, self.audio_scale_shift_table, self.audio_attn1,
-                                                          self.audio_attn2, self.audio_prompt_scale_shift_table)
         if run_a2v or run_v2a:
             for args in (video, audio):
                 if (args.cross_scale_shift_timestep is None or args.cross_gate_timestep is None
@@ -293,6 +319,9 @@ class BasicAVTransformerBlock:
             v_scale_a2v, v_shift_a2v, v_scale_v2a, v_shift_v2a, gate_a2v = self._av_ada_values(
                 self.scale_shift_table_a2v_ca_video, video.cross_scale_shift_timestep, video.cross_gate_timestep)
             video_base, audio_base = video_value, audio_value
+            if side is not None:
+                main.wait_stream(side)
+                side.wait_stream(main)
             # rms_norm(x) * (1 + scale) + shift is one AdaLN pass per (stream, direction)
             if run_a2v:
                 cdt = compute_dtype(self.audio_to_video_attn)
@@ -303,23 +332,27 @@ class BasicAVTransformerBlock:
                     k_pe=audio.cross_positional_embeddings, residual=video_base, gate=gate_a2v,
                     out_dtype=torch.float32)
             if run_v2a:
-                cdt = compute_dtype(self.video_to_audio_attn)
-                query = adaln(audio_base, a_scale_v2a, a_shift_v2a, self.norm_eps, cdt)
-                context = adaln(video_base, v_scale_v2a, v_shift_v2a, self.norm_eps, cdt)
-                audio_value = self.video_to_audio_attn(
-                    query, context=context, pe=audio.cross_positional_embeddings,
-                    k_pe=video.cross_positional_embeddings, residual=audio_base, gate=gate_v2a,
-                    out_dtype=torch.float32)
+                with torch.cuda.stream(side):
+                    cdt = compute_dtype(self.video_to_audio_attn)
+                    query = adaln(audio_base, a_scale_v2a, a_shift_v2a, self.norm_eps, cdt)
+                    context = adaln(video_base, v_scale_v2a, v_shift_v2a, self.norm_eps, cdt)
+                    audio_value = self.video_to_audio_attn(
+                        query, context=context, pe=audio.cross_positional_embeddings,
+                        k_pe=video.cross_positional_embeddings, residual=audio_base, gate=gate_v2a,
+                        out_dtype=torch.float32)
+        if run_audio:
+            with torch.cuda.stream(side):
+                normalized = adaln(audio_value, audio_ada[:, :, 4], audio_ada[:, :, 3], self.norm_eps,
+                                   compute_dtype(self.audio_attn1))
+                audio = replace(audio, x=self.audio_ff(normalized, residual=audio_value, gate=audio_ada[:, :, 5],
+                                                       out_dtype=audio.x.dtype))
         if run_video:
             normalized = adaln(video_value, video_ada[:, :, 4], video_ada[:, :, 3], self.norm_eps,
                                compute_dtype(self.attn1))
             video = replace(video, x=self.ff(normalized, residual=video_value, gate=video_ada[:, :, 5],
                                              out_dtype=video.x.dtype))
-        if run_audio:
-            normalized = adaln(audio_value, audio_ada[:, :, 4], audio_ada[:, :, 3], self.norm_eps,
-                               compute_dtype(self.audio_attn1))
-            audio = replace(audio, x=self.audio_ff(normalized, residual=audio_value, gate=audio_ada[:, :, 5],
-                                                   out_dtype=audio.x.dtype))
+        if side is not None:
+            main.wait_stream(side)
         return video, audio
 
 

@@ -56,6 +56,29 @@ def test_av_block_matches_oracle(device, fuse):
     _check(out_a.x[0].float().cpu().numpy(), ref_a, graph_a)
 
 
+def test_av_block_side_stream_matches_one_stream(device):
+    """With both streams present the block runs the audio stream on a second HIP stream beside
+    the video stream's; three chained blocks give the one-stream schedule's outputs bit for bit."""
+    from kinomlx_amd.ltx2 import transformer as ltx_transformer
+
+    p = workloads.ltx_av_params(SPEC, AUDIO)
+    inputs = workloads.ltx_av_inputs(SPEC, AUDIO)
+    block = workloads.build_ltx_av_block(SPEC, AUDIO, p, device)
+    outs = {}
+    for two in (True, False):
+        block.audio_side_stream = two
+        video, audio = _args(p, inputs, device)
+        seq = []
+        for _ in range(3):
+            video, audio = block(video, audio)
+            seq.append((video.x.clone(), audio.x.clone()))
+        torch.cuda.synchronize()
+        outs[two] = seq
+    assert ltx_transformer._SIDE_STREAMS
+    for (v2, a2), (v1, a1) in zip(outs[True], outs[False]):
+        assert torch.equal(v2, v1) and torch.equal(a2, a1)
+
+
 def test_disabled_audio_still_feeds_video(device):
     """A present but disabled audio stream is left as it is and still supplies the audio ->
     video K/V; the video output then differs from a block run without audio."""
