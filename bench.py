@@ -136,7 +136,9 @@ def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
-    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--warmup", type=int, default=20,
+                        help="untimed steps first (the first ~10 blocks after launch run up to 25 %% slower while "
+                             "the clock settles)")
     parser.add_argument("--config", type=int, default=3, choices=(3, 4, 5))
     parser.add_argument("--dtype", default="bf16", choices=("bf16", "fp16"),
                         help="activation and weight type of the block (fp16: the reference's default LTX-2 "
@@ -168,7 +170,7 @@ def main() -> int:
                              "scales the FETCH_SIZE / WRITE_SIZE counters) and exit")
     args = parser.parse_args()
     if args.profile_summary:
-        return profile_summary(args.profile_summary)
+        return profile_summary(args.profile_summary, args.warmup)
     if args.kernel_table:
         return kernel_table(args.kernel_table, args.warmup + 2 * args.steps)
     if args.calibrate_copy:
@@ -349,14 +351,15 @@ _DISPATCHES = {"kx_gemm_splitk_bf16": 2, "kx_gemm_splitk_noalloc_bf16": 2, "kx_a
                "kx_all_finite": 2}
 
 
-def profile_summary(root: str) -> int:
+def profile_summary(root: str, warmup: int = 0) -> int:
     """Markdown table of one block's kernels from rocprofv3 runs of this script: ``root/trace``
     (``--kernel-trace``), ``root/mfma`` (``--pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE``),
     ``root/fetch`` / ``root/write`` (``FETCH_SIZE`` / ``WRITE_SIZE``), ``root/copy_fetch`` /
     ``root/copy_write`` (the same counters over ``--calibrate-copy 1024``) and ``root/launches.json``
     (``--launch-log``). Dispatches of the kx kernels are matched to the block's launch sequence by
     position (every block launches the same sequence), so launches of one kernel with different
-    shapes (self- and cross-attention) get their own rows."""
+    shapes (self- and cross-attention) get their own rows. The first ``warmup`` blocks of each run
+    (its untimed warm-up) are left out of the means."""
     import csv
     import glob
 
@@ -384,7 +387,7 @@ def profile_summary(root: str) -> int:
         out = [[] for _ in range(period)]
         for i, v in enumerate(vals):
             out[i % period].append(v)
-        return out
+        return [lst[warmup:] if len(lst) > warmup else lst for lst in out]
 
     trace = sorted(kx_rows("trace", "*kernel_trace.csv"), key=lambda r: int(r["Dispatch_Id"]))
     durations, names = [], []
@@ -452,7 +455,8 @@ def profile_summary(root: str) -> int:
               f"{f(tf / PEAK_BF16_TFLOPS if tf else None, '{:.3f}')} | {f(b if tf else None, '{:.2f}')} | "
               f"{f(gbs, '{:.0f}')} | {f(gbs / PEAK_HBM_GBS if gbs else None, '{:.2f}')} | "
               f"{f(fm, '{:.1f}')} | {f(wm, '{:.1f}')} |")
-    print(f"\nSum of the block's kernels: {total_us / 1e3:.3f} ms ({len(dur[0])} blocks traced).")
+    print(f"\nSum of the block's kernels: {total_us / 1e3:.3f} ms (means over the {len(dur[0])} timed blocks, "
+          f"after {warmup} warm-up blocks).")
 
     # further counter passes (root/ctr_<name>, each a --pmc run of the same command): the mean per
     # launch of each counter, for the launches that carry FLOPs (GEMMs and attention); busy and
