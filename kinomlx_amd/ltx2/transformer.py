@@ -29,6 +29,7 @@ from dataclasses import dataclass, replace
 import torch
 
 from .. import _lib
+from ..streams import side_stream
 from .attention import Attention, rms_norm
 from .feed_forward import FeedForward
 from .rope import LTXRopeType
@@ -53,17 +54,6 @@ def _mod_pair(shift: torch.Tensor, scale: torch.Tensor) -> tuple[torch.Tensor, t
 
 _HALF = (torch.bfloat16, torch.float16)
 
-_SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
-
-
-def _side_stream(device: torch.device) -> torch.cuda.Stream:
-    """The stream a joint block runs its audio stream on: one per device, default priority."""
-    index = device.index if device.index is not None else torch.cuda.current_device()
-    stream = _SIDE_STREAMS.get(index)
-    if stream is None:
-        stream = torch.cuda.Stream(device=index)
-        _SIDE_STREAMS[index] = stream
-    return stream
 
 
 def _norm_out_dtype(value: torch.Tensor, out_dtype: torch.dtype | None, what: str) -> torch.dtype:
@@ -300,7 +290,7 @@ class BasicAVTransformerBlock:
         main = side = None
         if run_video and run_audio and self.audio_side_stream and video.x.is_cuda:
             main = torch.cuda.current_stream(video.x.device)
-            side = _side_stream(video.x.device)
+            side = side_stream(video.x.device)
             side.wait_stream(main)
         if run_audio:
             with torch.cuda.stream(side):

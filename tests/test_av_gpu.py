@@ -59,7 +59,7 @@ def test_av_block_matches_oracle(device, fuse):
 def test_av_block_side_stream_matches_one_stream(device):
     """With both streams present the block runs the audio stream on a second HIP stream beside
     the video stream's; three chained blocks give the one-stream schedule's outputs bit for bit."""
-    from kinomlx_amd.ltx2 import transformer as ltx_transformer
+    from kinomlx_amd import streams
 
     p = workloads.ltx_av_params(SPEC, AUDIO)
     inputs = workloads.ltx_av_inputs(SPEC, AUDIO)
@@ -74,7 +74,7 @@ def test_av_block_side_stream_matches_one_stream(device):
             seq.append((video.x.clone(), audio.x.clone()))
         torch.cuda.synchronize()
         outs[two] = seq
-    assert ltx_transformer._SIDE_STREAMS
+    assert streams._SIDE_STREAMS
     for (v2, a2), (v1, a1) in zip(outs[True], outs[False]):
         assert torch.equal(v2, v1) and torch.equal(a2, a1)
 
