@@ -1,5 +1,5 @@
-"""The second HIP stream the two-stream blocks (LTX-2's joint audio/video block, FLUX.2's
-double-stream block) run their small stream on: one per device, default priority."""
+"""The second HIP stream LTX-2's joint audio/video block runs its audio stream on: one per device,
+default priority."""
 
 from __future__ import annotations
 
