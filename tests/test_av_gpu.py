@@ -56,12 +56,28 @@ def test_av_block_matches_oracle(device, fuse):
     _check(out_a.x[0].float().cpu().numpy(), ref_a, graph_a)
 
 
-def test_av_block_side_stream_matches_one_stream(device):
+def _quantized(p, bits):
+    """Every 2-D linear weight of ``p`` in the packed affine form (group 64)."""
+    from kinomlx_amd.kernels.quantized import quantize
+
+    q = dict(p)
+    for key in [k for k, v in p.items() if k.endswith(".weight") and v.dim() == 2 and v.shape[1] % 64 == 0]:
+        name = key[: -len(".weight")]
+        q[f"{name}.wq"], q[f"{name}.scales"], q[f"{name}.biases"] = quantize(q.pop(key), 64, bits)
+        q[f"{name}.group_size"], q[f"{name}.bits"] = torch.tensor(64), torch.tensor(bits)
+    return q
+
+
+@pytest.mark.parametrize("bits", [None, 4], ids=["bf16", "int4"])
+def test_av_block_side_stream_matches_one_stream(device, bits):
     """With both streams present the block runs the audio stream on a second HIP stream beside
-    the video stream's; three chained blocks give the one-stream schedule's outputs bit for bit."""
+    the video stream's; three chained blocks give the one-stream schedule's outputs bit for bit
+    (with int4 layers each stream dequantizes into its own workspace)."""
     from kinomlx_amd import streams
 
     p = workloads.ltx_av_params(SPEC, AUDIO)
+    if bits:
+        p = _quantized(p, bits)
     inputs = workloads.ltx_av_inputs(SPEC, AUDIO)
     block = workloads.build_ltx_av_block(SPEC, AUDIO, p, device)
     outs = {}
